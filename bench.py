@@ -1,0 +1,167 @@
+"""Benchmark of the SVDQuant W4A4 linear hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+
+A step is one pass of the hot path over one batch of synthetic input: the
+config-1 SVDQuant W4A4 linear (M = 4096 image + 512 text tokens = 4608,
+K = N = 3072, rank 32, group 64, bf16 in/out): kernel 1 (smoothing + int4
+act-quant + x @ proj_down) then kernel 2 (W4A4 GEMM + low-rank/bias
+epilogue). Inputs are resident in HBM before the timed region. ``value`` is
+the linear's throughput in int-TOPS (2*M*N*K per step). The ``roofline``
+object covers the dominant kernel (the GEMM), timed with HIP events on the
+stream it runs on; ``cpu_baseline`` times the reference's CPU serving lane
+(dense fold + one bf16 Linear) on a bounded sample of the same workload.
+Prints ONE JSON line on stdout; progress goes to stderr.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "python-gen-worker_amd"))
+sys.path.insert(0, str(ROOT))
+
+METRIC = "W4A4 linear TOPS (% int8 MFMA peak) at M=4608 K=N=3072; DiT step ms"
+INT8_PEAK_TOPS = 5000.0      # MI355X dense int8 MFMA, 5.0 POP/s
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, 8 TB/s
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-rows", type=int, default=512, help="rows of the bounded CPU sample")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}): this build's path is a single-GPU "
+              f"kernel pair; multi-GPU sharding is design-only.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    import gen_worker_amd  # noqa: F401
+    from gen_worker_amd import _native, synthetic
+    from gen_worker_amd.svdq import act_quant_bytes, build_svdq_w4a4_linear, w4a4_int_ops
+
+    _native.load()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    cfg = synthetic.C1
+    m, n, k, r = cfg["m"], cfg["n"], cfg["k"], cfg["rank"]
+    log(f"bench: building config-1 layer M={m} N={n} K={k} r={r}")
+    L = synthetic.w4a4_layer(n, k, r)
+    x_cpu = synthetic.activation(m, k, outlier_frac=cfg["outlier_frac"], outlier_scale=cfg["outlier_scale"])
+    mod = build_svdq_w4a4_linear(qweight=L.qweight, wscales=L.wscales, smooth=L.smooth, proj_down=L.proj_down,
+                                 proj_up=L.proj_up, bias=L.bias, device=dev)
+    x = x_cpu.to(dev)
+    ops = torch.ops.cozy_gen_worker
+
+    def step(evs=None):
+        if evs is not None:
+            evs[0].record()
+        qa, sa, la = ops.svdq_quant_lora(x, mod.smooth_factor, None, mod.proj_down_t)
+        if evs is not None:
+            evs[1].record()
+        y = ops.svdq_w4a4_linear(qa, sa, mod.weight, mod.weight_scale, None, mod.second, la, mod.proj_up,
+                                 mod.bias, torch.bfloat16, False)
+        if evs is not None:
+            evs[2].record()
+        return y
+
+    log(f"bench: warmup {args.warmup}")
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    log(f"bench: timing {args.steps} steps")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(evs[i])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    q_ms = [e[0].elapsed_time(e[1]) for e in evs]
+    g_ms = [e[1].elapsed_time(e[2]) for e in evs]
+    ms_per_step = wall * 1e3 / args.steps
+
+    int_ops = w4a4_int_ops(m, n, k)
+    value_tops = int_ops / (ms_per_step * 1e-3) / 1e12
+    gemm_ms = statistics.mean(g_ms)
+    quant_ms = statistics.mean(q_ms)
+    gemm_tops = int_ops / (gemm_ms * 1e-3) / 1e12
+    qbytes = act_quant_bytes(m, k, r)
+    quant_gbs = qbytes / (quant_ms * 1e-3) / 1e9
+    log(f"bench: step {ms_per_step * 1e3:.1f} us  quant {quant_ms * 1e3:.1f} us ({quant_gbs:.0f} GB/s)  "
+        f"gemm {gemm_ms * 1e3:.1f} us ({gemm_tops:.0f} TOPS, {100 * gemm_tops / INT8_PEAK_TOPS:.1f}% int8 peak)")
+
+    traffic = None
+    tpath = ROOT / "profiles" / "w4a4_gemm_c1_traffic.json"
+    if tpath.exists():
+        try:
+            traffic = json.loads(tpath.read_text()).get("hbm_bytes_per_launch")
+        except Exception:  # noqa: BLE001
+            traffic = None
+
+    cpu = None
+    if not args.no_cpu:
+        import numpy as np
+
+        from oracle import cpu_baseline
+
+        rows = max(1, min(args.cpu_rows, m))
+        b = lambda t: t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)  # noqa: E731
+        log(f"bench: cpu baseline on {rows} rows")
+        res = cpu_baseline.time_w4a4_linear_cpu(b(x_cpu[:rows]), b(L.smooth), L.qweight.numpy(), L.wscales.numpy(),
+                                                b(L.proj_down), b(L.proj_up), b(L.bias))
+        cpu_tops = w4a4_int_ops(rows, n, k) / res["fallback_s"] / 1e12
+        cpu = {"value": round(cpu_tops, 4), "unit": "TOPS", "cores": res["threads"], "kind": "port",
+               "sample": (f"reference CPU fallback lane (fold_to_dense + one bf16 nn.Linear, "
+                          f"svdq_native.py:200-221) on {rows} of {m} config-1 rows, K=N={k}: median of 10 = "
+                          f"{res['fallback_s'] * 1e3:.2f} ms; oracle chain (int4 act-quant -> dequant -> fp32 "
+                          f"matmul) {res['chain_s'] * 1e3:.1f} ms; torch threads={res['threads']}")}
+
+    out = {
+        "metric": METRIC,
+        "value": round(value_tops, 2),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int4",
+        "data": "synthetic",
+        "config": {"workload": "svdq_w4a4_linear_c1", "M": m, "N": n, "K": k, "rank": r, "group": 64,
+                   "in_dtype": "bf16", "out_dtype": "bf16", "parallelism": "none"},
+        "roofline": {"bound": "mfma", "achieved": round(gemm_tops, 2), "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
+                     "frac": round(gemm_tops / INT8_PEAK_TOPS, 4), "traffic": traffic,
+                     "kernel": "w4a4_gemm_kernel", "algorithmic_ops_per_launch": int_ops,
+                     "avg_launch_us": round(gemm_ms * 1e3, 2)},
+        "pct_int8_peak": round(100 * value_tops / INT8_PEAK_TOPS, 2),
+        "act_quant": {"avg_launch_us": round(quant_ms * 1e3, 2), "algorithmic_bytes": qbytes,
+                      "achieved_GBps": round(quant_gbs, 1), "frac_hbm_peak": round(quant_gbs / HBM_PEAK_GBS, 4)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,136 @@
+/*
+ * gen_worker_amd — C ABI of the MI355X (gfx950) SVDQuant quantized-linear path.
+ *
+ * Plain pointers and sizes only; no torch types. Every entry point returns 0
+ * on success or a GWA_ERR_* code, and leaves a message for gwa_last_error()
+ * (thread-local). Device pointers are HIP device memory; `stream` is a
+ * hipStream_t (NULL = the default stream). Nothing synchronizes the host:
+ * kernels are enqueued on `stream`, as the reference's Triton launches and
+ * torch._scaled_mm run on the current stream.
+ *
+ * Formats (the int4-g64 / int8 variants of the reference's nvfp4/fp8 path):
+ *   bf16/fp16 tensors     : raw 16-bit patterns
+ *   int4 packed codes     : uint8 [rows, K/2], two's-complement nibbles,
+ *                           element 2j in the LOW nibble (the byte order of
+ *                           pack_e2m1, src/gen_worker/models/nvfp4_quant.py:54-56)
+ *   int4 group scales     : fp16 [rows, K/64], one per group of 64 along K
+ *   int8 codes            : int8 [rows, K]; per-row fp32 scales [rows]
+ */
+#ifndef GEN_WORKER_AMD_H
+#define GEN_WORKER_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  GWA_OK = 0,
+  GWA_ERR_INVALID = 1,   /* bad argument / unsupported shape */
+  GWA_ERR_HIP = 2,       /* HIP runtime or launch failure */
+};
+
+enum { GWA_DT_BF16 = 0, GWA_DT_F16 = 1, GWA_DT_F32 = 2 };
+
+/* GEMM epilogue flags */
+enum { GWA_EPI_GELU_TANH = 1 };
+
+/* Library version and build description ("archs=gfx950 hip=..."). Mirrors
+ * cozy_kernels::build_info, csrc/cozy_kernels/ops.cpp:23-27. */
+int gwa_version(void);
+const char* gwa_build_info(void);
+
+/* Message for the last failed call on this thread ("" if none). Replaces the
+ * TORCH_CHECK / C10_CUDA_KERNEL_LAUNCH_CHECK error surface of
+ * csrc/cozy_kernels/probe.cu:15-16,25. */
+const char* gwa_last_error(void);
+
+/* out[i] = in[i] + 1 for float32 [n]. The extension probe
+ * cozy_kernels::probe_add_one, csrc/cozy_kernels/probe.cu:9-27; used by the
+ * load-and-probe gate of models/native_kernels.py:120-143. */
+int gwa_probe_add_one(const float* in, float* out, int64_t n, void* stream);
+
+/* Kernel 1 — fused activation quantization (+ low-rank down-projection).
+ * Replaces cozy_gen_worker::svdq_quant (models/svdq_fused.py:254-306,
+ * Triton _quant_smooth_kernel :70-114) plus the separate
+ * `la = x2 @ self.proj_down` of models/svdq_fused.py:524.
+ *   x          bf16 [M, K] rows with stride ldx (elements), K % 64 == 0
+ *   smooth     bf16 [K] or NULL (per-input-channel divisor, 4-bit branch only)
+ *   s2         fp32 device scalar or NULL (= 1.0): second-level scale; the
+ *              group scale is fp16(amax / (7 * s2)) and codes divide by
+ *              (scale * s2), as models/nvfp4_quant.py:98-101 do for nvfp4
+ *   proj_down_t bf16 [rank, K] (proj_down transposed) or NULL; rank % 16 == 0, rank <= 128
+ *   q          uint8 [M, K/2] packed codes (out)
+ *   scales     fp16 [M, K/64] (out)
+ *   la         bf16 [M, rank] = x @ proj_down on RAW x (out; NULL iff proj_down_t is NULL) */
+int gwa_svdq_quant_int4(const void* x, int64_t ldx, const void* smooth, const float* s2,
+                        const void* proj_down_t, int64_t rank,
+                        uint8_t* q, void* scales, void* la,
+                        int64_t M, int64_t K, void* stream);
+
+/* Kernel 2 — W4A4 GEMM with the fused SVDQuant epilogue.
+ * Replaces _gemm_w4a4 (torch._scaled_mm, models/w4a4.py:173-180) followed by
+ * cozy_gen_worker::svdq_epilogue_lora (models/svdq_fused.py:315-377); same
+ * math as the registered cozy_gen_worker::svdq_gemm_w4a4_lora
+ * (models/svdq_fused.py:180-238, :379-389):
+ *   y[m,n] = (sum_g acc_g[m,n] * sa[m,g] * sw[n,g]) * s2 * second[n]
+ *            + la[m,:] . up[n,:] + bias[n]          (then optional GELU-tanh)
+ *   qa     uint8 [M, K/2]   sa fp16 [M, K/64]
+ *   qw     uint8 [N, K/2]   sw fp16 [N, K/64]   (weight [out, in/2] layout)
+ *   s2     fp32 device scalar or NULL (= 1.0)
+ *   second fp32 [second_numel] (1 or N) or NULL (= 1.0)
+ *   la     bf16 [M, rank] or NULL;  up bf16 [N, rank] or NULL; rank % 16 == 0, <= 128
+ *   bias   bf16 [N] or NULL
+ *   out    [M, N] of out_dtype (GWA_DT_BF16 or GWA_DT_F16)
+ * K % 128 == 0, N % 16 == 0. */
+int gwa_svdq_gemm_w4a4(const uint8_t* qa, const void* sa, const uint8_t* qw, const void* sw,
+                       const float* s2, const float* second, int64_t second_numel,
+                       const void* la, const void* up, int64_t rank, const void* bias,
+                       void* out, int out_dtype, int epilogue_flags,
+                       int64_t M, int64_t N, int64_t K, void* stream);
+
+/* Debug: exact int32 per-group partial sums out[m, n, g] = sum_{k in g} qx[m,k] qw[n,k]
+ * computed by the same MFMA and unpack code as gwa_svdq_gemm_w4a4. No
+ * reference counterpart (the reference has no int4 arithmetic); it pins the
+ * integer core of kernel 2 bit-exactly. */
+int gwa_svdq_group_psums(const uint8_t* qa, const uint8_t* qw, int32_t* out,
+                         int64_t M, int64_t N, int64_t K, void* stream);
+
+/* Standalone epilogue: out = y0 * (s2 * second) + la @ up^T + bias (bf16 out).
+ * cozy_gen_worker::svdq_epilogue_lora, models/svdq_fused.py:315-377.
+ *   y0 bf16 [M, N]; la bf16 [M, rank]; up bf16 [N, rank]; bias bf16 [N] or NULL */
+int gwa_svdq_epilogue_lora(const void* y0, const void* la, const void* up, int64_t rank,
+                           const float* s2, const float* second, int64_t second_numel,
+                           const void* bias, void* out, int64_t M, int64_t N, void* stream);
+
+/* W8A8 per-token int8 activation quantization.
+ * Replaces the quantizer of _Fp8ScaledLinear.forward (models/w8a8.py:259-297,
+ * :363) with the reference's int8 formula (models/svdq_layout.py:261-275,
+ * block = one row): sa = max(amax/127, 1e-12); q = clamp(rne(x/sa), -127, 127).
+ *   x bf16 [M, K] (row stride ldx) -> q int8 [M, K], sa fp32 [M] */
+int gwa_w8a8_quant_int8(const void* x, int64_t ldx, int8_t* q, float* sa,
+                        int64_t M, int64_t K, void* stream);
+
+/* Kernel 3 — W8A8 GEMM with per-token x per-channel scales.
+ * Replaces torch._scaled_mm(xq, W.t(), scale_a=sa, scale_b=weight_scale.t(),
+ * bias, out_dtype) of models/w8a8.py:374-378:
+ *   y[m,n] = (sum_k qa[m,k] qw[n,k]) * sa[m] * sw[n] + bias[n]
+ *   qa int8 [M, K]; qw int8 [N, K]; sa fp32 [M]; sw fp32 [N]
+ *   bias of bias_dtype [N] or NULL; out [M, N] of out_dtype (bf16/f16)
+ * K % 64 == 0, N % 16 == 0. */
+int gwa_w8a8_gemm(const int8_t* qa, const int8_t* qw, const float* sa, const float* sw,
+                  const void* bias, int bias_dtype, void* out, int out_dtype,
+                  int64_t M, int64_t N, int64_t K, void* stream);
+
+/* Row-major 2-D transpose of 1/2/4-byte elements: dst[c, r] = src[r, c].
+ * Layout plumbing for the reference's K-major operands (wq_kn [K/2, N] of
+ * models/svdq_fused.py:214, proj_down [in, rank] of :506-507). */
+int gwa_transpose_2d(const void* src, void* dst, int64_t rows, int64_t cols,
+                     int64_t elem_size, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GEN_WORKER_AMD_H */

@@ -1,0 +1,79 @@
+// Shared device/host helpers for the gen_worker_amd C-ABI library (gfx950).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/gen_worker_amd.h"
+
+// ---------------------------------------------------------------------------
+// vector types used as MFMA operands
+// ---------------------------------------------------------------------------
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+
+// ---------------------------------------------------------------------------
+// host-side error state (defined in gwa_runtime.hip)
+// ---------------------------------------------------------------------------
+int gwa_set_error(int code, const char* fmt, ...);
+int gwa_check_launch(const char* what);
+
+#define GWA_ALIGNED(p, n) ((((uintptr_t)(p)) & ((n) - 1)) == 0)
+
+#define GWA_REQUIRE(cond, ...)                                   \
+  do {                                                           \
+    if (!(cond)) return gwa_set_error(GWA_ERR_INVALID, __VA_ARGS__); \
+  } while (0)
+
+// ---------------------------------------------------------------------------
+// scalar conversions (exact, RNE where rounding happens)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float(((uint32_t)b) << 16); }
+
+// float -> bf16 bits, round to nearest even; NaN stays NaN (quiet bit set).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+  _Float16 h = (_Float16)f;
+  return __builtin_bit_cast(uint16_t, h);
+}
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t b) {
+  return (float)__builtin_bit_cast(_Float16, b);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  return (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
+}
+__device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
+  return (uint32_t)f32_to_f16_bits(a) | ((uint32_t)f32_to_f16_bits(b) << 16);
+}
+
+// GELU, tanh approximation, fp32.
+__device__ __forceinline__ float gelu_tanh_f32(float y) {
+  const float c = 0.7978845608028654f;  // sqrt(2/pi)
+  float t = tanhf(c * (y + 0.044715f * y * y * y));
+  return 0.5f * y * (1.0f + t);
+}
+
+// ---------------------------------------------------------------------------
+// int4 helpers
+// ---------------------------------------------------------------------------
+// Two's-complement nibbles, element 2j in the low nibble of byte j.
+// To int8 operand bytes holding 16*q (the nibble in the high half of the
+// byte): a signed int8 MFMA on these computes 256 * sum(qx * qw), exactly.
+__device__ __forceinline__ uint32_t int4_lo_x16(uint32_t w) { return (w << 4) & 0xF0F0F0F0u; }
+__device__ __forceinline__ uint32_t int4_hi_x16(uint32_t w) { return w & 0xF0F0F0F0u; }
+
+__device__ __forceinline__ int ceil_div(int a, int b) { return (a + b - 1) / b; }

@@ -1,0 +1,79 @@
+"""Build the C-ABI library ``libgen_worker_amd.so`` for gfx950 with hipcc.
+
+The library is built in-tree (next to this file) so that it travels with the
+source tree; nothing is installed. ``python -m gen_worker_amd.build`` or
+``__graft_entry__.build()`` runs it.
+"""
+
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent
+CSRC = PKG_DIR.parent / "csrc"
+INCLUDE = PKG_DIR.parent.parent / "include"
+BUILD_DIR = PKG_DIR.parent / "_build"
+LIB_NAME = "libgen_worker_amd.so"
+LIB_PATH = PKG_DIR / LIB_NAME
+ARCH = "gfx950"
+
+SOURCES = ("gwa_runtime.hip", "act_quant.hip", "w4a4_gemm.hip", "w8a8_gemm.hip")
+
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    # hipcc -O3 otherwise forms v_pk_{add,mul,fma}_f32 from scalar fp32 code;
+    # this build never emits packed-fp32 arithmetic.
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wno-unused-command-line-argument",
+]
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found (set HIPCC or install ROCm)")
+
+
+def _compile(src: Path, obj: Path, extra: list[str]) -> None:
+    cmd = [hipcc(), *HIPCC_FLAGS, *extra, f"-I{INCLUDE}", "-c", str(src), "-o", str(obj)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stderr[-6000:]}")
+
+
+def build(verbose: bool = False, jobs: int | None = None) -> Path:
+    """Compile every HIP source for gfx950 and link the shared library; returns its path."""
+    BUILD_DIR.mkdir(parents=True, exist_ok=True)
+    desc = f'-DGWA_BUILD_DESC="archs={ARCH}"'
+    objs = []
+    jobs = jobs or min(len(SOURCES), max(1, (os.cpu_count() or 2) // 2))
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        futs = []
+        for s in SOURCES:
+            obj = BUILD_DIR / (Path(s).stem + ".o")
+            objs.append(obj)
+            futs.append(ex.submit(_compile, CSRC / s, obj, [desc]))
+        for f in futs:
+            f.result()
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed:\n{res.stderr[-4000:]}")
+    os.replace(tmp, LIB_PATH)
+    if verbose:
+        print(f"built {LIB_PATH}", file=sys.stderr)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    build(verbose=True)

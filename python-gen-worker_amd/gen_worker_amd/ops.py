@@ -1,0 +1,350 @@
+"""``torch.library`` operators of the int4-g64 SVDQuant / W8A8 path.
+
+The reference registers its fused lane as ``cozy_gen_worker::*`` custom ops
+(``src/gen_worker/models/svdq_fused.py:17-19``, ``:293-389``) and its native
+probe as ``cozy_kernels::probe_add_one`` (``csrc/cozy_kernels/ops.cpp:29-36``).
+The same names and schemas are registered here, backed by the HIP kernels of
+``libgen_worker_amd.so``, with int4 group-64 semantics in place of nvfp4:
+
+* ``svdq_quant(x2, smooth, s2, blocked) -> (q, s)``: q uint8 [M, K/2],
+  s fp16 [M, K/64]. int4 scales are flat; ``blocked=True`` (the nvfp4 cuBLAS
+  tile swizzle) is refused.
+* ``svdq_gemm_w4a4_lora(qa, sa, wq_kn, ws, s2, second, lora_act, up, bias)``:
+  ``wq_kn`` is the reference's K-major packed weight [K/2, N].
+* ``svdq_epilogue_lora(y0, la, up, s2, second, bias)``.
+
+Additions (no reference counterpart; the fused forms the reference keeps as
+separate steps):
+
+* ``svdq_quant_lora(x2, smooth, s2, proj_down_t) -> (q, s, la)``: kernel 1
+  with ``la = x2 @ proj_down`` fused (``proj_down_t`` = proj_down^T, [rank, K]).
+* ``svdq_w4a4_linear(qa, sa, weight, wscales, s2, second, la, up, bias,
+  out_dtype, gelu)``: kernel 2 on the resident ``weight`` [N, K/2] layout.
+* ``svdq_group_psums(qa, qw)``: exact int32 per-group partial sums (debug).
+* ``w8a8_quant(x2) -> (q, sa)`` and ``w8a8_scaled_mm(qa, weight, sa,
+  weight_scale, bias, out_dtype)``: the int8 lane.
+
+Every op runs on the current HIP stream and allocates its outputs with
+``torch.empty`` on the input's device, as the reference launchers do
+(``models/svdq_fused.py:260-266``). Inputs must be contiguous CUDA tensors;
+CPU tensors are refused (there is no CPU implementation).
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+from torch import Tensor
+
+from . import _native as nat
+
+GROUP = 64
+
+
+class SvdqOpError(ValueError):
+    """Typed contract violation at the op boundary (never a silent fallback)."""
+
+
+def _check_cuda(name: str, **tensors: Optional[Tensor]) -> None:
+    for k, t in tensors.items():
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise SvdqOpError(f"{name}: {k} is on {t.device}; the int4/int8 path runs on the GPU only")
+        if not t.is_contiguous():
+            raise SvdqOpError(f"{name}: {k} must be contiguous")
+
+
+def _check_dtype(name: str, t: Optional[Tensor], *dtypes: torch.dtype, what: str) -> None:
+    if t is not None and t.dtype not in dtypes:
+        raise SvdqOpError(f"{name}: {what} has dtype {t.dtype}, expected one of {dtypes}")
+
+
+def _scalar_f32(name: str, s2: Optional[Tensor]) -> Optional[Tensor]:
+    if s2 is None:
+        return None
+    if s2.numel() != 1:
+        raise SvdqOpError(f"{name}: s2 must hold one value, got {s2.numel()}")
+    if s2.dtype != torch.float32:
+        s2 = s2.float()
+    return s2.reshape(()).contiguous()
+
+
+def _dt_code(dtype: torch.dtype) -> int:
+    if dtype == torch.bfloat16:
+        return nat.DT_BF16
+    if dtype == torch.float16:
+        return nat.DT_F16
+    if dtype == torch.float32:
+        return nat.DT_F32
+    raise SvdqOpError(f"unsupported dtype {dtype}")
+
+
+# ---------------------------------------------------------------------------
+# kernel 1
+# ---------------------------------------------------------------------------
+
+def _quant_impl(x2: Tensor, smooth: Optional[Tensor], s2: Optional[Tensor],
+                proj_down_t: Optional[Tensor]) -> tuple[Tensor, Tensor, Optional[Tensor]]:
+    name = "svdq_quant"
+    if x2.dim() != 2:
+        raise SvdqOpError(f"{name}: x2 must be 2-D, got {tuple(x2.shape)}")
+    _check_dtype(name, x2, torch.bfloat16, what="x2")
+    _check_dtype(name, smooth, torch.bfloat16, what="smooth")
+    _check_dtype(name, proj_down_t, torch.bfloat16, what="proj_down_t")
+    s2 = _scalar_f32(name, s2)
+    _check_cuda(name, x2=x2, smooth=smooth, s2=s2, proj_down_t=proj_down_t)
+    m, k = int(x2.shape[0]), int(x2.shape[1])
+    if k % GROUP:
+        raise SvdqOpError(f"{name}: K={k} is not a multiple of {GROUP}")
+    if smooth is not None and smooth.numel() != k:
+        raise SvdqOpError(f"{name}: smooth has {smooth.numel()} values for K={k}")
+    rank = 0
+    if proj_down_t is not None:
+        if proj_down_t.dim() != 2 or int(proj_down_t.shape[1]) != k:
+            raise SvdqOpError(f"{name}: proj_down_t must be [rank, K={k}], got {tuple(proj_down_t.shape)}")
+        rank = int(proj_down_t.shape[0])
+    q = torch.empty(m, k // 2, dtype=torch.uint8, device=x2.device)
+    s = torch.empty(m, k // GROUP, dtype=torch.float16, device=x2.device)
+    la = torch.empty(m, rank, dtype=torch.bfloat16, device=x2.device) if proj_down_t is not None else None
+    nat.call("gwa_svdq_quant_int4", nat.ptr(x2), k, nat.ptr(smooth), nat.ptr(s2), nat.ptr(proj_down_t),
+             rank, nat.ptr(q), nat.ptr(s), nat.ptr(la), m, k, nat.stream_of(x2))
+    return q, s, la
+
+
+@torch.library.custom_op("cozy_gen_worker::svdq_quant", mutates_args=())
+def svdq_quant(x2: Tensor, smooth: Optional[Tensor], s2: Tensor, blocked: bool) -> tuple[Tensor, Tensor]:
+    """int4 group-64 activation quant: (packed codes uint8 [M, K/2], fp16 scales [M, K/64])."""
+    if blocked:
+        raise SvdqOpError("svdq_quant: int4 group scales are flat [M, K/64]; the blocked (cuBLAS 128x4 "
+                          "tile) layout is an nvfp4 format and is not produced")
+    q, s, _ = _quant_impl(x2, smooth, s2, None)
+    return q, s
+
+
+@svdq_quant.register_fake
+def _(x2: Tensor, smooth: Optional[Tensor], s2: Tensor, blocked: bool) -> tuple[Tensor, Tensor]:
+    m, k = int(x2.shape[0]), int(x2.shape[1])
+    return (x2.new_empty(m, k // 2, dtype=torch.uint8), x2.new_empty(m, k // GROUP, dtype=torch.float16))
+
+
+@torch.library.custom_op("cozy_gen_worker::svdq_quant_lora", mutates_args=())
+def svdq_quant_lora(x2: Tensor, smooth: Optional[Tensor], s2: Optional[Tensor],
+                    proj_down_t: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+    """Kernel 1 with the low-rank down-projection fused: (q, s, la = x2 @ proj_down)."""
+    q, s, la = _quant_impl(x2, smooth, s2, proj_down_t)
+    assert la is not None
+    return q, s, la
+
+
+@svdq_quant_lora.register_fake
+def _(x2, smooth, s2, proj_down_t):
+    m, k = int(x2.shape[0]), int(x2.shape[1])
+    r = int(proj_down_t.shape[0])
+    return (x2.new_empty(m, k // 2, dtype=torch.uint8), x2.new_empty(m, k // GROUP, dtype=torch.float16),
+            x2.new_empty(m, r, dtype=torch.bfloat16))
+
+
+# ---------------------------------------------------------------------------
+# kernel 2
+# ---------------------------------------------------------------------------
+
+def _gemm_impl(qa: Tensor, sa: Tensor, weight: Tensor, wscales: Tensor, s2: Optional[Tensor],
+               second: Optional[Tensor], la: Optional[Tensor], up: Optional[Tensor], bias: Optional[Tensor],
+               out_dtype: torch.dtype, gelu: bool) -> Tensor:
+    name = "svdq_w4a4_linear"
+    s2 = _scalar_f32(name, s2)
+    if second is not None and second.dtype != torch.float32:
+        second = second.float().contiguous()
+    _check_dtype(name, qa, torch.uint8, what="qa")
+    _check_dtype(name, weight, torch.uint8, what="weight")
+    _check_dtype(name, sa, torch.float16, what="sa")
+    _check_dtype(name, wscales, torch.float16, what="weight scales")
+    _check_dtype(name, la, torch.bfloat16, what="la")
+    _check_dtype(name, up, torch.bfloat16, what="up")
+    _check_dtype(name, bias, torch.bfloat16, what="bias")
+    _check_cuda(name, qa=qa, sa=sa, weight=weight, wscales=wscales, s2=s2, second=second, la=la, up=up, bias=bias)
+    if out_dtype not in (torch.bfloat16, torch.float16):
+        raise SvdqOpError(f"{name}: out_dtype {out_dtype} not bf16/fp16")
+    m, kh = int(qa.shape[0]), int(qa.shape[1])
+    k = 2 * kh
+    n = int(weight.shape[0])
+    if tuple(weight.shape) != (n, kh):
+        raise SvdqOpError(f"{name}: weight {tuple(weight.shape)} != [N, K/2={kh}]")
+    if tuple(sa.shape) != (m, k // GROUP) or tuple(wscales.shape) != (n, k // GROUP):
+        raise SvdqOpError(f"{name}: scales {tuple(sa.shape)} / {tuple(wscales.shape)} do not match "
+                          f"[M, K/64] / [N, K/64] for M={m} N={n} K={k}")
+    if (la is None) != (up is None):
+        raise SvdqOpError(f"{name}: la and up must both be given or both be None")
+    rank = 0
+    if la is not None:
+        rank = int(up.shape[1])
+        if tuple(la.shape) != (m, rank) or tuple(up.shape) != (n, rank):
+            raise SvdqOpError(f"{name}: la {tuple(la.shape)} / up {tuple(up.shape)} do not match rank {rank}")
+    if bias is not None and bias.numel() != n:
+        raise SvdqOpError(f"{name}: bias has {bias.numel()} values for N={n}")
+    sec_n = 0 if second is None else int(second.numel())
+    out = torch.empty(m, n, dtype=out_dtype, device=qa.device)
+    nat.call("gwa_svdq_gemm_w4a4", nat.ptr(qa), nat.ptr(sa), nat.ptr(weight), nat.ptr(wscales), nat.ptr(s2),
+             nat.ptr(second), sec_n, nat.ptr(la), nat.ptr(up), rank, nat.ptr(bias), nat.ptr(out),
+             _dt_code(out_dtype), nat.EPI_GELU_TANH if gelu else 0, m, n, k, nat.stream_of(qa))
+    return out
+
+
+@torch.library.custom_op("cozy_gen_worker::svdq_w4a4_linear", mutates_args=())
+def svdq_w4a4_linear(qa: Tensor, sa: Tensor, weight: Tensor, wscales: Tensor, s2: Optional[Tensor],
+                     second: Optional[Tensor], la: Optional[Tensor], up: Optional[Tensor],
+                     bias: Optional[Tensor], out_dtype: torch.dtype, gelu: bool) -> Tensor:
+    """W4A4 GEMM + fused epilogue on the resident [N, K/2] weight layout."""
+    return _gemm_impl(qa, sa, weight, wscales, s2, second, la, up, bias, out_dtype, gelu)
+
+
+@svdq_w4a4_linear.register_fake
+def _(qa, sa, weight, wscales, s2, second, la, up, bias, out_dtype, gelu):
+    return qa.new_empty(int(qa.shape[0]), int(weight.shape[0]), dtype=out_dtype)
+
+
+@torch.library.custom_op("cozy_gen_worker::svdq_gemm_w4a4_lora", mutates_args=())
+def svdq_gemm_w4a4_lora(qa: Tensor, sa: Tensor, wq_kn: Tensor, ws: Tensor, s2: Tensor, second: Tensor,
+                        lora_act: Tensor, up: Tensor, bias: Optional[Tensor]) -> Tensor:
+    """The reference schema (``models/svdq_fused.py:379-389``): K-major weight ``wq_kn`` [K/2, N], bf16 out."""
+    _check_cuda("svdq_gemm_w4a4_lora", wq_kn=wq_kn)
+    _check_dtype("svdq_gemm_w4a4_lora", wq_kn, torch.uint8, what="wq_kn")
+    kh, n = int(wq_kn.shape[0]), int(wq_kn.shape[1])
+    w_nk = torch.empty(n, kh, dtype=torch.uint8, device=wq_kn.device)
+    nat.call("gwa_transpose_2d", nat.ptr(wq_kn), nat.ptr(w_nk), kh, n, 1, nat.stream_of(wq_kn))
+    return _gemm_impl(qa, sa, w_nk, ws, s2, second, lora_act, up, bias, torch.bfloat16, False)
+
+
+@svdq_gemm_w4a4_lora.register_fake
+def _(qa, sa, wq_kn, ws, s2, second, lora_act, up, bias):
+    return qa.new_empty(int(qa.shape[0]), int(wq_kn.shape[1]), dtype=torch.bfloat16)
+
+
+@torch.library.custom_op("cozy_gen_worker::svdq_epilogue_lora", mutates_args=())
+def svdq_epilogue_lora(y0: Tensor, la: Tensor, up: Tensor, s2: Tensor, second: Tensor,
+                       bias: Optional[Tensor]) -> Tensor:
+    """``y0 * (s2 * second) + la @ up^T + bias`` -> bf16 (``models/svdq_fused.py:315-377``)."""
+    name = "svdq_epilogue_lora"
+    s2 = _scalar_f32(name, s2)
+    if second.dtype != torch.float32:
+        second = second.float().contiguous()
+    _check_dtype(name, y0, torch.bfloat16, what="y0")
+    _check_dtype(name, la, torch.bfloat16, what="la")
+    _check_dtype(name, up, torch.bfloat16, what="up")
+    _check_dtype(name, bias, torch.bfloat16, what="bias")
+    _check_cuda(name, y0=y0, la=la, up=up, s2=s2, second=second, bias=bias)
+    m, n = int(y0.shape[0]), int(y0.shape[1])
+    r = int(up.shape[1])
+    if tuple(la.shape) != (m, r) or int(up.shape[0]) != n:
+        raise SvdqOpError(f"{name}: la {tuple(la.shape)} / up {tuple(up.shape)} do not match y0 {tuple(y0.shape)}")
+    out = torch.empty(m, n, dtype=torch.bfloat16, device=y0.device)
+    nat.call("gwa_svdq_epilogue_lora", nat.ptr(y0), nat.ptr(la), nat.ptr(up), r, nat.ptr(s2), nat.ptr(second),
+             int(second.numel()), nat.ptr(bias), nat.ptr(out), m, n, nat.stream_of(y0))
+    return out
+
+
+@svdq_epilogue_lora.register_fake
+def _(y0, la, up, s2, second, bias):
+    return y0.new_empty(int(y0.shape[0]), int(y0.shape[1]), dtype=torch.bfloat16)
+
+
+@torch.library.custom_op("cozy_gen_worker::svdq_group_psums", mutates_args=())
+def svdq_group_psums(qa: Tensor, qw: Tensor) -> Tensor:
+    """Exact int32 [M, N, K/64] per-group partial sums (debug/parity entry)."""
+    name = "svdq_group_psums"
+    _check_dtype(name, qa, torch.uint8, what="qa")
+    _check_dtype(name, qw, torch.uint8, what="qw")
+    _check_cuda(name, qa=qa, qw=qw)
+    m, kh = int(qa.shape[0]), int(qa.shape[1])
+    n = int(qw.shape[0])
+    if int(qw.shape[1]) != kh:
+        raise SvdqOpError(f"{name}: qa {tuple(qa.shape)} and qw {tuple(qw.shape)} disagree on K/2")
+    out = torch.empty(m, n, (2 * kh) // GROUP, dtype=torch.int32, device=qa.device)
+    nat.call("gwa_svdq_group_psums", nat.ptr(qa), nat.ptr(qw), nat.ptr(out), m, n, 2 * kh, nat.stream_of(qa))
+    return out
+
+
+@svdq_group_psums.register_fake
+def _(qa, qw):
+    return qa.new_empty(int(qa.shape[0]), int(qw.shape[0]), (2 * int(qa.shape[1])) // GROUP, dtype=torch.int32)
+
+
+# ---------------------------------------------------------------------------
+# W8A8
+# ---------------------------------------------------------------------------
+
+@torch.library.custom_op("cozy_gen_worker::w8a8_quant", mutates_args=())
+def w8a8_quant(x2: Tensor) -> tuple[Tensor, Tensor]:
+    """Per-token int8: (q int8 [M, K], sa fp32 [M, 1])."""
+    name = "w8a8_quant"
+    _check_dtype(name, x2, torch.bfloat16, what="x2")
+    _check_cuda(name, x2=x2)
+    m, k = int(x2.shape[0]), int(x2.shape[1])
+    q = torch.empty(m, k, dtype=torch.int8, device=x2.device)
+    sa = torch.empty(m, 1, dtype=torch.float32, device=x2.device)
+    nat.call("gwa_w8a8_quant_int8", nat.ptr(x2), k, nat.ptr(q), nat.ptr(sa), m, k, nat.stream_of(x2))
+    return q, sa
+
+
+@w8a8_quant.register_fake
+def _(x2):
+    m, k = int(x2.shape[0]), int(x2.shape[1])
+    return x2.new_empty(m, k, dtype=torch.int8), x2.new_empty(m, 1, dtype=torch.float32)
+
+
+@torch.library.custom_op("cozy_gen_worker::w8a8_scaled_mm", mutates_args=())
+def w8a8_scaled_mm(qa: Tensor, weight: Tensor, sa: Tensor, weight_scale: Tensor, bias: Optional[Tensor],
+                   out_dtype: torch.dtype) -> Tensor:
+    """``_scaled_mm(qa, weight.t(), scale_a=sa, scale_b=weight_scale.t(), bias, out_dtype)`` on int8 codes."""
+    name = "w8a8_scaled_mm"
+    _check_dtype(name, qa, torch.int8, what="qa")
+    _check_dtype(name, weight, torch.int8, what="weight")
+    _check_dtype(name, sa, torch.float32, what="sa")
+    _check_dtype(name, weight_scale, torch.float32, what="weight_scale")
+    _check_dtype(name, bias, torch.float32, torch.bfloat16, torch.float16, what="bias")
+    _check_cuda(name, qa=qa, weight=weight, sa=sa, weight_scale=weight_scale, bias=bias)
+    if out_dtype not in (torch.bfloat16, torch.float16):
+        raise SvdqOpError(f"{name}: out_dtype {out_dtype} not bf16/fp16")
+    m, k = int(qa.shape[0]), int(qa.shape[1])
+    n = int(weight.shape[0])
+    if int(weight.shape[1]) != k or sa.numel() != m or weight_scale.numel() != n:
+        raise SvdqOpError(f"{name}: shapes qa {tuple(qa.shape)} weight {tuple(weight.shape)} sa {tuple(sa.shape)} "
+                          f"weight_scale {tuple(weight_scale.shape)} disagree")
+    if bias is not None and bias.numel() != n:
+        raise SvdqOpError(f"{name}: bias has {bias.numel()} values for N={n}")
+    out = torch.empty(m, n, dtype=out_dtype, device=qa.device)
+    nat.call("gwa_w8a8_gemm", nat.ptr(qa), nat.ptr(weight), nat.ptr(sa), nat.ptr(weight_scale), nat.ptr(bias),
+             _dt_code(bias.dtype) if bias is not None else 0, nat.ptr(out), _dt_code(out_dtype), m, n, k,
+             nat.stream_of(qa))
+    return out
+
+
+@w8a8_scaled_mm.register_fake
+def _(qa, weight, sa, weight_scale, bias, out_dtype):
+    return qa.new_empty(int(qa.shape[0]), int(weight.shape[0]), dtype=out_dtype)
+
+
+# ---------------------------------------------------------------------------
+# cozy_kernels probe (csrc/cozy_kernels/ops.cpp:29-36)
+# ---------------------------------------------------------------------------
+
+@torch.library.custom_op("cozy_kernels::probe_add_one", mutates_args=())
+def probe_add_one(x: Tensor) -> Tensor:
+    if not (x.is_cuda and x.dtype == torch.float32):
+        raise SvdqOpError("probe_add_one expects a float32 CUDA tensor")
+    xin = x.contiguous()
+    out = torch.empty_like(xin)
+    nat.call("gwa_probe_add_one", nat.ptr(xin), nat.ptr(out), xin.numel(), nat.stream_of(xin))
+    return out
+
+
+@probe_add_one.register_fake
+def _(x):
+    return torch.empty_like(x)
+
+
+def build_info() -> str:
+    """Library build description (``cozy_kernels::build_info``, ``csrc/cozy_kernels/ops.cpp:23-27``)."""
+    return f"torch={torch.__version__} {nat.build_info()}"

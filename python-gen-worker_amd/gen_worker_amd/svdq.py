@@ -1,0 +1,274 @@
+"""SVDQuant W4A4 (int4, group 64) linear layer and its offline producers.
+
+``SvdqW4A4Linear`` is the int4-g64 counterpart of the reference's fused lane
+module ``_SvdqFusedLinear`` (``src/gen_worker/models/svdq_fused.py:471-534``):
+same buffer names (``weight``, ``weight_scale``, ``second``,
+``smooth_factor``, ``proj_down``, ``proj_up``, ``bias``), same forward
+structure (``:516-527``: quantize -> W4A4 GEMM -> low-rank + bias epilogue),
+but two launches instead of four: kernel 1 fuses the smoothing, the act-quant
+and ``x2 @ proj_down``; kernel 2 fuses the GEMM with the whole epilogue.
+
+Buffer formats (the int4 lane's own layout):
+  weight        uint8 [out, in/2]   two's-complement int4 codes, low nibble = even k
+  weight_scale  fp16  [out, in/64]  one scale per group of 64 along in_features
+  second        fp32  [out] or [1]  per-channel / per-tensor output multiplier
+  smooth_factor bf16  [in]          divides the activation of the 4-bit branch only
+  proj_down     bf16  [in, rank]    low-rank down factor (applied to RAW x)
+  proj_up       bf16  [out, rank]   low-rank up factor
+  bias          bf16  [out]
+"""
+
+from __future__ import annotations
+
+from typing import Any, Optional
+
+import torch
+import torch.nn as nn
+from torch import Tensor
+
+from . import ops
+
+GROUP = 64
+_N_ALIGN = 16
+SUPPORTED_RANKS = (0, 16, 32, 64, 128)
+
+
+class SvdqFusedError(RuntimeError):
+    """Typed contract failure of the int4 fused lane (``models/svdq_fused.py:34-35``)."""
+
+
+def fused_shape_supported(out_features: int, in_features: int, rank: int) -> bool:
+    """Shape contract of the kernels (reference: ``models/svdq_fused.py:38-41``)."""
+    return (in_features % GROUP == 0 and out_features % _N_ALIGN == 0 and rank in SUPPORTED_RANKS)
+
+
+# ---------------------------------------------------------------------------
+# int4 format helpers (torch; offline/CPU or GPU)
+# ---------------------------------------------------------------------------
+
+def pack_int4(codes: Tensor) -> Tensor:
+    """int codes [..., K] in [-8, 7] -> uint8 [..., K/2], element 2j in the LOW nibble (``pack_e2m1``, ``models/nvfp4_quant.py:54-56``)."""
+    c = (codes.to(torch.int16) & 0xF).to(torch.uint8)
+    return (c[..., 0::2] | (c[..., 1::2] << 4)).contiguous()
+
+
+def unpack_int4(packed: Tensor) -> Tensor:
+    """uint8 [..., K/2] -> int8 codes [..., K]."""
+    p = packed.to(torch.int16)
+    lo, hi = p & 0xF, (p >> 4) & 0xF
+    out = torch.stack((lo, hi), dim=-1).reshape(*packed.shape[:-1], packed.shape[-1] * 2)
+    out = torch.where(out >= 8, out - 16, out)
+    return out.to(torch.int8)
+
+
+def quantize_weight_int4(w: Tensor) -> tuple[Tensor, Tensor]:
+    """fp weight [N, K] -> (packed uint8 [N, K/2], fp16 scales [N, K/64]).
+
+    Offline producer, structured as ``quantize_nvfp4_tensor``
+    (``models/w4a4.py:140-154``): per-block absmax, zero blocks get scale 1,
+    clamp, cast the scale to its stored dtype, divide by the stored scale,
+    round (RNE) and clamp the codes. Single-level: no second scale.
+    """
+    wf = w.detach().float().cpu()
+    n, k = wf.shape
+    if k % GROUP:
+        raise SvdqFusedError(f"in_features {k} is not a multiple of {GROUP}")
+    blocks = wf.reshape(n, k // GROUP, GROUP)
+    bs = blocks.abs().amax(dim=-1) / 7.0
+    bs[bs == 0] = 1.0
+    bs = bs.clamp(min=2.0 ** -24, max=65504.0).to(torch.float16)
+    q = (blocks / bs.float().unsqueeze(-1)).round().clamp(-8, 7).to(torch.int8)
+    return pack_int4(q.reshape(n, k)), bs
+
+
+def dequantize_weight_int4(packed: Tensor, scales: Tensor) -> Tensor:
+    """(packed, fp16 scales) -> float32 [N, K] (``dequantize_decoded``, ``models/svdq_layout.py:492-504``)."""
+    q = unpack_int4(packed).float()
+    n, k = q.shape
+    return (q.reshape(n, k // GROUP, GROUP) * scales.float().reshape(n, k // GROUP, 1)).reshape(n, k)
+
+
+def svdquant_decompose(w: Tensor, smooth: Optional[Tensor], rank: int) -> tuple[Tensor, Tensor, Tensor]:
+    """SVDQuant split of a dense weight: W = W_res / smooth + up @ down^T.
+
+    The smoothed weight ``W * smooth`` (smoothing migrates activation
+    outliers into the weight) is split by an SVD into a rank-``rank``
+    component, kept in 16-bit as ``proj_up @ proj_down^T`` on the RAW
+    activations (so ``proj_down`` is pre-divided by ``smooth``, as the
+    reference notes in ``models/svdq_layout.py:1``), and a residual that is
+    quantized to int4. Returns (w_res [N, K] fp32, proj_down [K, r], proj_up [N, r]).
+    """
+    wf = w.detach().float().cpu()
+    sm = smooth.detach().float().cpu().reshape(1, -1) if smooth is not None else None
+    ws = wf * sm if sm is not None else wf
+    if rank == 0:
+        return ws, wf.new_zeros(wf.shape[1], 0), wf.new_zeros(wf.shape[0], 0)
+    u, s, vh = torch.linalg.svd(ws, full_matrices=False)
+    up = u[:, :rank] * s[:rank]                # [N, r]
+    down_s = vh[:rank].t()                      # [K, r] acting on smoothed x
+    res = ws - up @ down_s.t()
+    down = down_s / sm.reshape(-1, 1) if sm is not None else down_s
+    return res, down, up
+
+
+# ---------------------------------------------------------------------------
+# the module
+# ---------------------------------------------------------------------------
+
+class SvdqW4A4Linear(nn.Module):
+    """int4-g64 SVDQuant linear on the HIP kernels (the fused lane)."""
+
+    _cozy_svdq_linear = True
+    _cozy_svdq_fused = True
+
+    def __init__(self, in_features: int, out_features: int, *, rank: int, bias: bool,
+                 compute_dtype: Any = torch.bfloat16, per_channel_scale: bool = False,
+                 smooth: bool = True, activation: Optional[str] = None,
+                 out_dtype: Optional[torch.dtype] = None, device: Any = None) -> None:
+        super().__init__()
+        if not fused_shape_supported(out_features, in_features, rank):
+            raise SvdqFusedError(
+                f"SvdqW4A4Linear [{out_features}, {in_features}] r{rank} breaks the kernel contract "
+                f"(in%{GROUP}, out%{_N_ALIGN}, rank in {SUPPORTED_RANKS})")
+        if compute_dtype != torch.bfloat16:
+            raise SvdqFusedError(f"compute_dtype {compute_dtype}: the int4 lane quantizes bf16 activations")
+        if activation not in (None, "gelu_tanh"):
+            raise SvdqFusedError(f"activation {activation!r} not in (None, 'gelu_tanh')")
+        self.in_features = int(in_features)
+        self.out_features = int(out_features)
+        self.rank = int(rank)
+        self.compute_dtype = compute_dtype
+        self.per_channel_scale = bool(per_channel_scale)
+        self.activation = activation
+        self.out_dtype = out_dtype
+        dev = torch.device(device) if device is not None else torch.device("meta")
+        self.register_buffer("weight", torch.empty(out_features, in_features // 2, dtype=torch.uint8, device=dev))
+        self.register_buffer("weight_scale", torch.empty(out_features, in_features // GROUP,
+                                                         dtype=torch.float16, device=dev))
+        self.register_buffer("second", torch.ones(out_features if per_channel_scale else 1,
+                                                  dtype=torch.float32, device=dev))
+        if smooth:
+            self.register_buffer("smooth_factor", torch.empty(in_features, dtype=compute_dtype, device=dev))
+        else:
+            self.smooth_factor = None
+        if self.rank:
+            self.register_buffer("proj_down", torch.empty(in_features, self.rank, dtype=compute_dtype, device=dev))
+            self.register_buffer("proj_up", torch.empty(out_features, self.rank, dtype=compute_dtype, device=dev))
+            self.register_buffer("proj_down_t", torch.empty(self.rank, in_features, dtype=compute_dtype,
+                                                            device=dev), persistent=False)
+        else:
+            self.proj_down = self.proj_up = self.proj_down_t = None
+        if bias:
+            self.bias: Optional[nn.Parameter] = nn.Parameter(
+                torch.empty(out_features, dtype=compute_dtype, device=dev), requires_grad=False)
+        else:
+            self.bias = None
+        self.register_buffer("_one", torch.ones((), dtype=torch.float32, device=dev), persistent=False)
+
+    def refresh_derived(self) -> None:
+        """Recompute derived buffers after ``proj_down`` changes (the transposed copy kernel 1 reads)."""
+        if self.rank:
+            self.proj_down_t = self.proj_down.t().contiguous()
+
+    def _load_from_state_dict(self, *args: Any, **kwargs: Any) -> None:  # noqa: D401
+        super()._load_from_state_dict(*args, **kwargs)
+        if self.rank and self.proj_down is not None and self.proj_down.device.type != "meta":
+            self.refresh_derived()
+
+    def forward(self, x: Tensor) -> Tensor:
+        shape = x.shape
+        x2 = x.reshape(-1, self.in_features)
+        if x2.dtype != torch.bfloat16:
+            raise SvdqFusedError(f"SvdqW4A4Linear expects bf16 activations, got {x2.dtype}")
+        x2 = x2.contiguous()
+        out_dtype = self.out_dtype or torch.bfloat16
+        if self.rank:
+            qa, sa, la = torch.ops.cozy_gen_worker.svdq_quant_lora(x2, self.smooth_factor, None, self.proj_down_t)
+        else:
+            qa, sa = torch.ops.cozy_gen_worker.svdq_quant(x2, self.smooth_factor, self._one, False)
+            la = None
+        y = torch.ops.cozy_gen_worker.svdq_w4a4_linear(
+            qa, sa, self.weight, self.weight_scale, None, self.second, la, self.proj_up,
+            self.bias, out_dtype, self.activation == "gelu_tanh")
+        return y.reshape(*shape[:-1], self.out_features)
+
+    def extra_repr(self) -> str:
+        return (f"in_features={self.in_features}, out_features={self.out_features}, rank={self.rank}, "
+                f"bias={self.bias is not None}, per_channel_scale={self.per_channel_scale}, "
+                f"smooth={self.smooth_factor is not None}, activation={self.activation}, lane=int4-g64")
+
+
+def build_svdq_w4a4_linear(*, qweight: Tensor, wscales: Tensor, smooth: Optional[Tensor],
+                           proj_down: Optional[Tensor], proj_up: Optional[Tensor], bias: Optional[Tensor],
+                           second: Optional[Tensor] = None, activation: Optional[str] = None,
+                           out_dtype: Optional[torch.dtype] = None, device: Any = "cuda") -> SvdqW4A4Linear:
+    """A device-resident module from logical int4 buffers (``build_svdq_fused_linear``, ``models/svdq_fused.py:544-573``)."""
+    n, kh = int(qweight.shape[0]), int(qweight.shape[1])
+    rank = 0 if proj_down is None else int(proj_down.shape[1])
+    per_channel = second is not None and second.numel() > 1
+    mod = SvdqW4A4Linear(2 * kh, n, rank=rank, bias=bias is not None, per_channel_scale=per_channel,
+                         smooth=smooth is not None, activation=activation, out_dtype=out_dtype, device=device)
+    with torch.no_grad():
+        mod.weight.copy_(qweight.to(torch.uint8))
+        mod.weight_scale.copy_(wscales.to(torch.float16))
+        if second is not None:
+            mod.second.copy_(second.float().reshape(-1))
+        if smooth is not None:
+            mod.smooth_factor.copy_(smooth.to(torch.bfloat16).reshape(-1))
+        if rank:
+            mod.proj_down.copy_(proj_down.to(torch.bfloat16))
+            mod.proj_up.copy_(proj_up.to(torch.bfloat16))
+        if bias is not None:
+            mod.bias.copy_(bias.to(torch.bfloat16).reshape(-1))
+    mod.refresh_derived()
+    return mod
+
+
+def quantize_linear_w4a4(linear: nn.Linear, *, rank: int, smooth: Optional[Tensor] = None,
+                         activation: Optional[str] = None, device: Any = "cuda") -> SvdqW4A4Linear:
+    """Producer: dense ``nn.Linear`` -> SVDQuant int4 module (smoothing, SVD low-rank, int4 residual)."""
+    res, down, up = svdquant_decompose(linear.weight, smooth, rank)
+    qw, ws = quantize_weight_int4(res)
+    return build_svdq_w4a4_linear(qweight=qw, wscales=ws, smooth=smooth, proj_down=down if rank else None,
+                                  proj_up=up if rank else None,
+                                  bias=linear.bias.detach() if linear.bias is not None else None,
+                                  activation=activation, device=device)
+
+
+def fold_to_dense(mod: SvdqW4A4Linear, *, compute_dtype: Any = torch.bfloat16) -> nn.Linear:
+    """The any-hardware fallback lane: ONE dense ``nn.Linear`` equal to the whole int4 linear
+    (``fold_to_dense``, ``models/svdq_native.py:200-221``): ``W_eff = deq(W)*second / smooth + up @ down^T``.
+    Activation quantization is not part of this lane."""
+    w = dequantize_weight_int4(mod.weight.cpu(), mod.weight_scale.cpu())
+    w = w * mod.second.float().cpu().reshape(-1, 1)
+    if mod.smooth_factor is not None:
+        w = w / mod.smooth_factor.float().cpu().reshape(1, -1)
+    if mod.rank:
+        w = w + mod.proj_up.float().cpu() @ mod.proj_down.float().cpu().t()
+    lin = nn.Linear(mod.in_features, mod.out_features, bias=mod.bias is not None, dtype=compute_dtype)
+    with torch.no_grad():
+        lin.weight.copy_(w.to(compute_dtype))
+        if mod.bias is not None:
+            lin.bias.copy_(mod.bias.detach().cpu().to(compute_dtype))
+    lin.weight.requires_grad_(False)
+    if lin.bias is not None:
+        lin.bias.requires_grad_(False)
+    return lin
+
+
+def w4a4_int_ops(m: int, n: int, k: int) -> int:
+    """Algorithmic integer ops of the GEMM, 2*M*N*K."""
+    return 2 * m * n * k
+
+
+def act_quant_bytes(m: int, k: int, rank: int, smooth: bool = True) -> int:
+    """Minimal HBM bytes of kernel 1: x, smooth, L1, q, scales, la."""
+    return (m * k * 2 + (k * 2 if smooth else 0) + k * rank * 2 + m * k // 2 + m * (k // GROUP) * 2
+            + m * rank * 2)
+
+
+__all__ = [
+    "SvdqFusedError", "SvdqW4A4Linear", "build_svdq_w4a4_linear", "dequantize_weight_int4",
+    "fold_to_dense", "fused_shape_supported", "pack_int4", "quantize_linear_w4a4", "quantize_weight_int4",
+    "svdquant_decompose", "unpack_int4", "w4a4_int_ops", "act_quant_bytes",
+]

@@ -1,0 +1,106 @@
+"""W8A8 int8 linear layer and its offline producer.
+
+``Int8ScaledLinear`` is the int8 counterpart of the reference's
+``_Fp8ScaledLinear`` (``src/gen_worker/models/w8a8.py:319-388``): buffers
+``weight`` [out, in], ``weight_scale`` [out, 1] fp32, optional ``bias``,
+optional ``lora_a`` / ``lora_b``; forward = per-token activation quant
+(``:363``) -> scaled int8 GEMM with per-token x per-channel scales and the
+bias in the epilogue (``:374-378``) -> optional LoRA addend (``:379-380``).
+The quantizer is the reference's int8 formula (``models/svdq_layout.py:261-275``)
+with one block per row.
+"""
+
+from __future__ import annotations
+
+from typing import Any, Optional
+
+import torch
+import torch.nn as nn
+from torch import Tensor
+
+from . import ops  # noqa: F401  (registers the ops)
+
+_DIM_ALIGN = 16
+
+
+class W8a8Error(RuntimeError):
+    """Typed W8A8 contract failure."""
+
+
+def quantize_weight_int8(w: Tensor) -> tuple[Tensor, Tensor]:
+    """fp weight [N, K] -> (int8 [N, K], fp32 weight_scale [N, 1]): ``scale = max(amax/127, 1e-12)``,
+    ``q = clamp(round(w / scale), -127, 127)`` (``models/svdq_layout.py:267-272``, row blocks)."""
+    wf = w.detach().float().cpu()
+    scale = (wf.abs().amax(dim=-1, keepdim=True) / 127.0).clamp(min=1e-12)
+    q = (wf / scale).round().clamp(-127, 127).to(torch.int8)
+    return q, scale.float()
+
+
+class Int8ScaledLinear(nn.Module):
+    """Per-token x per-channel W8A8 linear on the HIP int8 GEMM."""
+
+    _cozy_w8a8_linear = True
+
+    def __init__(self, in_features: int, out_features: int, *, bias: bool, compute_dtype: Any = torch.bfloat16,
+                 bias_dtype: Optional[torch.dtype] = None, device: Any = None) -> None:
+        super().__init__()
+        if in_features % 64 or out_features % _DIM_ALIGN:
+            raise W8a8Error(f"Int8ScaledLinear [{out_features}, {in_features}] breaks the kernel contract "
+                            f"(in%64, out%{_DIM_ALIGN})")
+        self.in_features = int(in_features)
+        self.out_features = int(out_features)
+        self.compute_dtype = compute_dtype
+        dev = torch.device(device) if device is not None else torch.device("meta")
+        self.register_buffer("weight", torch.empty(out_features, in_features, dtype=torch.int8, device=dev))
+        self.register_buffer("weight_scale", torch.empty(out_features, 1, dtype=torch.float32, device=dev))
+        if bias:
+            self.bias: Optional[nn.Parameter] = nn.Parameter(
+                torch.empty(out_features, dtype=bias_dtype or compute_dtype, device=dev), requires_grad=False)
+        else:
+            self.bias = None
+        self.register_buffer("lora_a", None, persistent=False)
+        self.register_buffer("lora_b", None, persistent=False)
+
+    def _lora_addend(self, x2: Tensor) -> Tensor:
+        return (x2 @ self.lora_a.t()) @ self.lora_b.t()
+
+    def forward(self, x: Tensor) -> Tensor:
+        shape = x.shape
+        x2 = x.reshape(-1, self.in_features)
+        if x2.dtype != torch.bfloat16:
+            raise W8a8Error(f"Int8ScaledLinear expects bf16 activations, got {x2.dtype}")
+        x2 = x2.contiguous()
+        xq, sa = torch.ops.cozy_gen_worker.w8a8_quant(x2)
+        y = torch.ops.cozy_gen_worker.w8a8_scaled_mm(xq, self.weight, sa, self.weight_scale, self.bias,
+                                                     self.compute_dtype)
+        if self.lora_a is not None:
+            y = y + self._lora_addend(x2)
+        return y.reshape(*shape[:-1], self.out_features)
+
+    def extra_repr(self) -> str:
+        return (f"in_features={self.in_features}, out_features={self.out_features}, "
+                f"bias={self.bias is not None}, lane=int8-rowwise")
+
+
+def build_int8_linear(*, qweight: Tensor, weight_scale: Tensor, bias: Optional[Tensor],
+                      compute_dtype: Any = torch.bfloat16, device: Any = "cuda") -> Int8ScaledLinear:
+    n, k = int(qweight.shape[0]), int(qweight.shape[1])
+    mod = Int8ScaledLinear(k, n, bias=bias is not None, compute_dtype=compute_dtype,
+                           bias_dtype=bias.dtype if bias is not None else None, device=device)
+    with torch.no_grad():
+        mod.weight.copy_(qweight.to(torch.int8))
+        mod.weight_scale.copy_(weight_scale.float().reshape(n, 1))
+        if bias is not None:
+            mod.bias.copy_(bias.reshape(-1))
+    return mod
+
+
+def quantize_linear_w8a8(linear: nn.Linear, *, compute_dtype: Any = torch.bfloat16,
+                         device: Any = "cuda") -> Int8ScaledLinear:
+    """Producer (``quantize_tree_w8a8``, ``models/w8a8.py:738-792``, int8 form)."""
+    q, s = quantize_weight_int8(linear.weight)
+    b = linear.bias.detach().to(compute_dtype) if linear.bias is not None else None
+    return build_int8_linear(qweight=q, weight_scale=s, bias=b, compute_dtype=compute_dtype, device=device)
+
+
+__all__ = ["Int8ScaledLinear", "W8a8Error", "build_int8_linear", "quantize_linear_w8a8", "quantize_weight_int8"]

@@ -1,0 +1,363 @@
+"""GPU parity tests: every HIP kernel through the C-ABI against the CPU oracle.
+
+Integer outputs (int4/int8 codes, fp16/fp32 scales, int32 group partial sums)
+must be bit-exact; floating outputs meet the tolerance in tests/helpers.py.
+"""
+
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import bits16, check_output, from_bits
+from oracle import svdq_oracle as O
+
+pytestmark = pytest.mark.gpu
+GOLDEN = Path(__file__).resolve().parent / "golden"
+DEV = "cuda"
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _lib():
+    import gen_worker_amd  # noqa: F401
+    from gen_worker_amd import _native
+
+    _native.load()
+    assert torch.cuda.is_available()
+    yield
+
+
+def _rand_act(m, k, seed, frac=0.01, scale=20.0):
+    g = np.random.default_rng(seed)
+    x = g.standard_normal((m, k)).astype(np.float32)
+    n = int(frac * k)
+    if n:
+        x[:, g.permutation(k)[:n]] *= scale
+    return O.f32_to_bf16_bits(x)
+
+
+def _dev16(a, dtype=torch.bfloat16):
+    return from_bits(a, dtype, DEV)
+
+
+# ---------------------------------------------------------------------------
+# probe / transpose
+# ---------------------------------------------------------------------------
+
+def test_probe_add_one():
+    x = torch.arange(1000, device=DEV, dtype=torch.float32)
+    assert torch.equal(torch.ops.cozy_kernels.probe_add_one(x), x + 1)
+
+
+@pytest.mark.parametrize("rows,cols,dt", [(33, 70, torch.uint8), (384, 32, torch.bfloat16), (1, 5, torch.int32)])
+def test_transpose(rows, cols, dt):
+    from gen_worker_amd import _native as nat
+
+    src = torch.randint(0, 100, (rows, cols), device=DEV).to(dt)
+    dst = torch.empty(cols, rows, dtype=dt, device=DEV)
+    nat.call("gwa_transpose_2d", src.data_ptr(), dst.data_ptr(), rows, cols, src.element_size(),
+             nat.stream_of(src))
+    assert torch.equal(dst, src.t().contiguous())
+
+
+# ---------------------------------------------------------------------------
+# kernel 1: int4 activation quant (+ low-rank)
+# ---------------------------------------------------------------------------
+
+def _run_quant(x_bits, smooth_bits, down_bits, s2=None):
+    x = _dev16(x_bits)
+    sm = _dev16(smooth_bits) if smooth_bits is not None else None
+    s2t = torch.tensor(s2, dtype=torch.float32, device=DEV) if s2 is not None else None
+    if down_bits is not None:
+        pdt = _dev16(down_bits).t().contiguous()
+        q, s, la = torch.ops.cozy_gen_worker.svdq_quant_lora(x, sm, s2t, pdt)
+    else:
+        q, s = torch.ops.cozy_gen_worker.svdq_quant(x, sm, s2t if s2t is not None else
+                                                    torch.ones((), device=DEV), False)
+        la = None
+    torch.cuda.synchronize()
+    return q.cpu().numpy(), bits16(s), la
+
+
+def _check_la(la, x_bits, down_bits):
+    ref = O.lowrank_down(x_bits, down_bits)
+    got = la.float().cpu().numpy().astype(np.float64)
+    tol = 2.0 ** -8 * np.abs(ref) + 1e-3 * max(1.0, float(np.abs(ref).max()))
+    assert np.all(np.abs(got - ref) <= tol), float(np.max(np.abs(got - ref)))
+
+
+def test_quant_golden_smooth_lowrank():
+    f = np.load(GOLDEN / "act_quant_m77_k384_r32.npz")
+    q, s, la = _run_quant(f["x"], f["smooth"], f["proj_down"])
+    assert np.array_equal(q, f["q"])
+    assert np.array_equal(s, f["scales"])
+    ref = f["la"]
+    got = la.float().cpu().numpy().astype(np.float64)
+    assert np.all(np.abs(got - ref) <= 2.0 ** -8 * np.abs(ref) + 1e-3 * max(1.0, float(np.abs(ref).max())))
+
+
+def test_quant_golden_second_level_scale():
+    f = np.load(GOLDEN / "act_quant_m33_k256_s2.npz")
+    q, s, _ = _run_quant(f["x"], None, None, s2=float(f["s2"]))
+    assert np.array_equal(q, f["q"]) and np.array_equal(s, f["scales"])
+
+
+@pytest.mark.parametrize("m,k,rank,smooth", [
+    (1, 64, 0, False), (16, 128, 16, True), (77, 3072, 32, True), (333, 3072, 128, True),
+    (128, 512, 64, False), (1024, 12288, 32, True), (200, 15360, 32, True),
+])
+def test_quant_seeded_bit_exact(m, k, rank, smooth):
+    x = _rand_act(m, k, seed=m * 7 + k)
+    g = np.random.default_rng(k)
+    sm = O.f32_to_bf16_bits(np.exp(g.uniform(np.log(0.25), np.log(4), k)).astype(np.float32)) if smooth else None
+    down = O.f32_to_bf16_bits((g.standard_normal((k, rank)) * 0.02).astype(np.float32)) if rank else None
+    q, s, la = _run_quant(x, sm, down)
+    wq, ws = O.quantize_act_int4(x, sm)
+    assert np.array_equal(q, wq)
+    assert np.array_equal(s, ws.view(np.uint16))
+    if rank:
+        _check_la(la, x, down)
+
+
+def test_quant_edge_values():
+    """Zero rows, exact ties, saturation, tiny and huge magnitudes, subnormal-scale groups."""
+    k = 256
+    rows = []
+    rows.append(np.zeros(k, np.float32))                                  # zero group -> scale 2^-24
+    t = np.zeros(k, np.float32); t[:8] = [7, -7, 2.5, -2.5, 1.5, 0.5, -3.5, 6.5]; rows.append(t)  # ties
+    rows.append(np.full(k, 1e-30, np.float32))                            # tiny -> clamped scale
+    rows.append(np.linspace(-3e4, 3e4, k).astype(np.float32))             # large magnitudes
+    t = np.zeros(k, np.float32); t[::2] = 1e-6; t[1::2] = -3e-7; rows.append(t)  # subnormal fp16 scale
+    t = np.zeros(k, np.float32); t[5] = -100.0; t[70] = 65504.0 * 7; rows.append(t)  # clamp at fp16 max
+    x = O.f32_to_bf16_bits(np.stack(rows))
+    sm = O.f32_to_bf16_bits(np.concatenate([np.full(k // 2, 1.0), np.full(k // 2, 0.3)]).astype(np.float32))
+    for smooth in (None, sm):
+        q, s, _ = _run_quant(x, smooth, None)
+        wq, ws = O.quantize_act_int4(x, smooth)
+        assert np.array_equal(q, wq)
+        assert np.array_equal(s, ws.view(np.uint16))
+
+
+def test_quant_row_stride():
+    """x2 may be a row-strided view (ldx > K): same codes as the contiguous copy."""
+    from gen_worker_amd import _native as nat
+
+    m, k = 40, 256
+    big = _dev16(_rand_act(m, k + 64, seed=3))
+    x = big[:, :k]
+    q = torch.empty(m, k // 2, dtype=torch.uint8, device=DEV)
+    s = torch.empty(m, k // 64, dtype=torch.float16, device=DEV)
+    nat.call("gwa_svdq_quant_int4", x.data_ptr(), k + 64, None, None, None, 0, q.data_ptr(), s.data_ptr(), None,
+             m, k, nat.stream_of(x))
+    q2, s2 = torch.ops.cozy_gen_worker.svdq_quant(x.contiguous(), None, torch.ones((), device=DEV), False)
+    assert torch.equal(q, q2) and torch.equal(s.view(torch.int16), s2.view(torch.int16))
+
+
+def test_quant_config1_full_size():
+    """Config 1 activations (M=4608, K=3072, 0.5% outliers x30, log-uniform smoothing), bit-exact."""
+    from gen_worker_amd import synthetic
+
+    x = synthetic.activation(4608, 3072, outlier_frac=0.005, outlier_scale=30.0)
+    sm = synthetic.smooth_factor(3072)
+    down = synthetic.normal((3072, 32), 0.02, synthetic.SEED_L1, torch.bfloat16)
+    q, s, la = _run_quant(bits16(x), bits16(sm), bits16(down))
+    wq, ws = O.quantize_act_int4(bits16(x), bits16(sm))
+    assert np.array_equal(q, wq)
+    assert np.array_equal(s, ws.view(np.uint16))
+    _check_la(la, bits16(x), bits16(down))
+
+
+# ---------------------------------------------------------------------------
+# kernel 2: group partial sums (bit-exact) and the fused W4A4 linear
+# ---------------------------------------------------------------------------
+
+def test_psums_golden():
+    f = np.load(GOLDEN / "psums_m40_n48_k192.npz")
+    ps = torch.ops.cozy_gen_worker.svdq_group_psums(torch.from_numpy(f["qa"]).to(DEV),
+                                                    torch.from_numpy(f["qw"]).to(DEV))
+    assert np.array_equal(ps.cpu().numpy(), f["psums"])
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 16, 64), (77, 48, 192), (64, 160, 3072), (129, 96, 640)])
+def test_psums_seeded_extremes(m, n, k):
+    g = np.random.default_rng(m + n + k)
+    qa = g.integers(0, 256, size=(m, k // 2), dtype=np.uint8)
+    qw = g.integers(0, 256, size=(n, k // 2), dtype=np.uint8)
+    qa[0] = 0x88  # all -8: the extreme products
+    qw[0] = 0x88
+    ps = torch.ops.cozy_gen_worker.svdq_group_psums(torch.from_numpy(qa).to(DEV), torch.from_numpy(qw).to(DEV))
+    assert np.array_equal(ps.cpu().numpy(), O.group_psums(qa, qw))
+    assert int(ps[0, 0, 0]) == 64 * 64
+
+
+def _w4a4_case(m, n, k, rank, seed, smooth=True, bias=True, second=None, gelu=False, out_dtype=torch.bfloat16,
+               s2=None):
+    g = np.random.default_rng(seed)
+    x = _rand_act(m, k, seed=seed)
+    sm = O.f32_to_bf16_bits(np.exp(g.uniform(np.log(0.25), np.log(4), k)).astype(np.float32)) if smooth else None
+    qw, sw = O.quantize_weight_int4((g.standard_normal((n, k)) * 0.02).astype(np.float32))
+    down = O.f32_to_bf16_bits((g.standard_normal((k, rank)) * 0.02).astype(np.float32)) if rank else None
+    up = O.f32_to_bf16_bits((g.standard_normal((n, rank)) * 0.02).astype(np.float32)) if rank else None
+    b = O.f32_to_bf16_bits((g.standard_normal(n) * 0.02).astype(np.float32)) if bias else None
+    ref = O.w4a4_linear(x, sm, qw, sw, down, up, b, second=second, s2=1.0 if s2 is None else s2, gelu=gelu)
+    xd = _dev16(x)
+    smd = _dev16(sm) if sm is not None else None
+    s2t = torch.tensor(s2, dtype=torch.float32, device=DEV) if s2 is not None else None
+    if rank:
+        qa, sa, la = torch.ops.cozy_gen_worker.svdq_quant_lora(xd, smd, s2t, _dev16(down).t().contiguous())
+        upd = _dev16(up)
+    else:
+        qa, sa = torch.ops.cozy_gen_worker.svdq_quant(xd, smd, s2t if s2t is not None else
+                                                      torch.ones((), device=DEV), False)
+        la = upd = None
+    sec = torch.from_numpy(np.asarray(second, np.float32)).to(DEV) if second is not None else None
+    y = torch.ops.cozy_gen_worker.svdq_w4a4_linear(
+        qa, sa, torch.from_numpy(qw).to(DEV), from_bits(sw.view(np.uint16), torch.float16, DEV), s2t, sec, la,
+        upd, _dev16(b) if b is not None else None, out_dtype, gelu)
+    torch.cuda.synchronize()
+    return y, ref
+
+
+def test_w4a4_golden():
+    f = np.load(GOLDEN / "w4a4_m64_n128_k256_r16.npz")
+    xd = _dev16(f["x"])
+    qa, sa, la = torch.ops.cozy_gen_worker.svdq_quant_lora(xd, _dev16(f["smooth"]), None,
+                                                           _dev16(f["proj_down"]).t().contiguous())
+    assert np.array_equal(qa.cpu().numpy(), f["qa"]) and np.array_equal(bits16(sa), f["sa"])
+    y = torch.ops.cozy_gen_worker.svdq_w4a4_linear(
+        qa, sa, torch.from_numpy(f["qweight"]).to(DEV), from_bits(f["wscales"], torch.float16, DEV), None, None, la,
+        _dev16(f["proj_up"]), _dev16(f["bias"]), torch.bfloat16, False)
+    check_output(y, f["y"], what="golden w4a4")
+
+
+@pytest.mark.parametrize("m,n,k,rank", [
+    (1, 16, 64, 0), (77, 128, 384, 32), (256, 3072, 3072, 32), (333, 272, 512, 128), (130, 144, 192, 16),
+    (64, 256, 12288, 64), (96, 128, 15360, 32),
+])
+def test_w4a4_seeded(m, n, k, rank):
+    y, ref = _w4a4_case(m, n, k, rank, seed=m * 31 + n + k)
+    check_output(y, ref, what=f"w4a4 {m}x{n}x{k} r{rank}")
+
+
+def test_w4a4_epilogue_variants():
+    n = 256
+    sec = np.linspace(0.5, 2.0, n).astype(np.float32)
+    y, ref = _w4a4_case(96, n, 512, 32, seed=1, second=sec)
+    check_output(y, ref, what="per-channel second")
+    y, ref = _w4a4_case(96, n, 512, 32, seed=2, gelu=True)
+    check_output(y, ref, what="gelu")
+    y, ref = _w4a4_case(96, n, 512, 32, seed=3, out_dtype=torch.float16)
+    assert y.dtype == torch.float16
+    check_output(y, ref, what="fp16 out")
+    y, ref = _w4a4_case(96, n, 512, 0, seed=4, smooth=False, bias=False)
+    check_output(y, ref, what="no smooth / lowrank / bias")
+    y, ref = _w4a4_case(50, n, 512, 16, seed=5, s2=0.5)
+    check_output(y, ref, what="s2")
+
+
+def test_w4a4_module_config1_full_size():
+    """Config 1 end to end through the module (M=4608, K=N=3072, r=32) vs the dequant-then-matmul oracle."""
+    from gen_worker_amd import synthetic
+    from gen_worker_amd.svdq import build_svdq_w4a4_linear
+
+    L = synthetic.w4a4_layer(3072, 3072, 32)
+    x = synthetic.activation(4608, 3072, outlier_frac=0.005, outlier_scale=30.0)
+    mod = build_svdq_w4a4_linear(qweight=L.qweight, wscales=L.wscales, smooth=L.smooth, proj_down=L.proj_down,
+                                 proj_up=L.proj_up, bias=L.bias, device=DEV)
+    y = mod(x.to(DEV).reshape(1, 4608, 3072))
+    assert y.shape == (1, 4608, 3072)
+    ref = O.w4a4_linear(bits16(x), bits16(L.smooth), L.qweight.numpy(), L.wscales.numpy(), bits16(L.proj_down),
+                        bits16(L.proj_up), bits16(L.bias))
+    stats = check_output(y.reshape(4608, 3072), ref, what="config 1")
+    print("config1", stats)
+
+
+def test_reference_schema_ops():
+    """cozy_gen_worker::svdq_gemm_w4a4_lora (K-major wq_kn) and svdq_epilogue_lora keep the reference schemas."""
+    g = np.random.default_rng(8)
+    m, n, k, r = 70, 128, 256, 32
+    x = _rand_act(m, k, seed=8)
+    qw, sw = O.quantize_weight_int4((g.standard_normal((n, k)) * 0.02).astype(np.float32))
+    up = O.f32_to_bf16_bits((g.standard_normal((n, r)) * 0.02).astype(np.float32))
+    la = O.f32_to_bf16_bits(g.standard_normal((m, r)).astype(np.float32))
+    b = O.f32_to_bf16_bits((g.standard_normal(n) * 0.02).astype(np.float32))
+    second = (g.random(n) + 0.5).astype(np.float32)
+    qa, sa = torch.ops.cozy_gen_worker.svdq_quant(_dev16(x), None, torch.ones((), device=DEV), False)
+    wq_kn = torch.from_numpy(np.ascontiguousarray(qw.T)).to(DEV)
+    s2 = torch.tensor(1.0, device=DEV)
+    y = torch.ops.cozy_gen_worker.svdq_gemm_w4a4_lora(
+        qa, sa, wq_kn, from_bits(sw.view(np.uint16), torch.float16, DEV), s2, torch.from_numpy(second).to(DEV),
+        _dev16(la), _dev16(up), _dev16(b))
+    wqa, wsa = O.quantize_act_int4(x)
+    ref = (O.dequantize_int4(wqa, wsa) @ O.dequantize_int4(qw, sw).T) * second.astype(np.float64)
+    ref += O.bf16_bits_to_f32(la).astype(np.float64) @ O.bf16_bits_to_f32(up).astype(np.float64).T
+    ref += O.bf16_bits_to_f32(b).astype(np.float64)
+    check_output(y, ref, what="svdq_gemm_w4a4_lora")
+
+    y0 = O.f32_to_bf16_bits(g.standard_normal((m, n)).astype(np.float32))
+    out = torch.ops.cozy_gen_worker.svdq_epilogue_lora(_dev16(y0), _dev16(la), _dev16(up), s2,
+                                                       torch.from_numpy(second).to(DEV), _dev16(b))
+    ref = (O.bf16_bits_to_f32(y0).astype(np.float64) * second
+           + O.bf16_bits_to_f32(la).astype(np.float64) @ O.bf16_bits_to_f32(up).astype(np.float64).T
+           + O.bf16_bits_to_f32(b).astype(np.float64))
+    check_output(out, ref, what="svdq_epilogue_lora")
+
+
+# ---------------------------------------------------------------------------
+# W8A8
+# ---------------------------------------------------------------------------
+
+def test_w8a8_golden():
+    f = np.load(GOLDEN / "w8a8_m33_n64_k256.npz")
+    q, sa = torch.ops.cozy_gen_worker.w8a8_quant(_dev16(f["x"]))
+    assert np.array_equal(q.cpu().numpy(), f["qa"]) and np.array_equal(sa.cpu().numpy(), f["sa"])
+    y = torch.ops.cozy_gen_worker.w8a8_scaled_mm(q, torch.from_numpy(f["qweight"]).to(DEV), sa,
+                                                 torch.from_numpy(f["weight_scale"]).to(DEV),
+                                                 torch.from_numpy(f["bias"]).to(DEV), torch.bfloat16)
+    check_output(y, f["y"], what="golden w8a8")
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 16, 64), (256, 3072, 3072), (77, 160, 448), (300, 9216, 3072)])
+def test_w8a8_seeded(m, n, k):
+    g = np.random.default_rng(m + n)
+    x = _rand_act(m, k, seed=m + k)
+    x[min(3, m - 1)] = 0  # a zero row -> scale clamp 1e-12
+    qw, sw = O.quantize_weight_int8((g.standard_normal((n, k)) * 0.02).astype(np.float32))
+    b = (g.standard_normal(n) * 0.02).astype(np.float32)
+    q, sa = torch.ops.cozy_gen_worker.w8a8_quant(_dev16(x))
+    wq, wsa = O.quantize_act_int8(x)
+    assert np.array_equal(q.cpu().numpy(), wq) and np.array_equal(sa.cpu().numpy(), wsa)
+    qwd = torch.from_numpy(qw).to(DEV)
+    for bias, odt in ((torch.from_numpy(b).to(DEV), torch.bfloat16), (None, torch.float16)):
+        y = torch.ops.cozy_gen_worker.w8a8_scaled_mm(q, qwd, sa, torch.from_numpy(sw).to(DEV), bias, odt)
+        ref = O.w8a8_linear(x, qw, sw, b if bias is not None else None)
+        check_output(y, ref, what=f"w8a8 {m}x{n}x{k}")
+
+
+def test_w8a8_int32_core_exact():
+    """With unit scales and no bias the output is the exact int32 GEMM (values < 2^8 stay exact in bf16)."""
+    g = np.random.default_rng(0)
+    m, n, k = 64, 64, 128
+    qa = g.integers(-2, 3, size=(m, k), dtype=np.int8)
+    qw = g.integers(-1, 2, size=(n, k), dtype=np.int8)
+    ones_m = torch.ones(m, 1, device=DEV)
+    ones_n = torch.ones(n, 1, device=DEV)
+    y = torch.ops.cozy_gen_worker.w8a8_scaled_mm(torch.from_numpy(qa).to(DEV), torch.from_numpy(qw).to(DEV),
+                                                 ones_m, ones_n, None, torch.bfloat16)
+    want = O.int8_gemm(qa, qw)
+    assert np.array_equal(y.float().cpu().numpy().astype(np.int64), want)
+
+
+def test_w8a8_module_config0():
+    from gen_worker_amd import synthetic
+    from gen_worker_amd.w8a8 import build_int8_linear
+
+    L = synthetic.w8a8_layer(3072, 3072)
+    x = synthetic.activation(256, 3072, outlier_frac=0.01, outlier_scale=20.0)
+    mod = build_int8_linear(qweight=L.qweight, weight_scale=L.weight_scale, bias=L.bias, device=DEV)
+    y = mod(x.to(DEV))
+    ref = O.w8a8_linear(bits16(x), L.qweight.numpy(), L.weight_scale.numpy(), L.bias.numpy())
+    check_output(y, ref, what="config 0")

@@ -1,0 +1,171 @@
+"""CPU-side tests: the C-ABI library loads and exports its header, the golden
+fixtures reproduce, and the host boundary refuses what it must (no GPU needed)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import svdq_oracle as O
+
+ROOT = Path(__file__).resolve().parent.parent
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def _header_symbols() -> list[str]:
+    text = (ROOT / "include" / "gen_worker_amd.h").read_text()
+    return sorted(set(re.findall(r"\b(gwa_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_header_symbol():
+    from gen_worker_amd import _native
+
+    lib = _native.load()
+    syms = _header_symbols()
+    assert syms, "no symbols parsed from the header"
+    for s in syms:
+        assert hasattr(lib, s), s
+    assert set(syms) == set(_native.EXPORTED_SYMBOLS)
+    assert lib.gwa_version() == 1
+    assert "gfx950" in _native.build_info()
+
+
+def test_library_is_a_gfx950_code_object():
+    from gen_worker_amd import _native
+
+    data = _native.library_path().read_bytes()
+    assert b"amdgcn-amd-amdhsa--gfx950" in data
+
+
+def test_invalid_arguments_are_refused_before_any_launch():
+    from gen_worker_amd import _native
+
+    lib = _native.load()
+    # K not a multiple of 64: validated on the host, no device touched
+    rc = lib.gwa_svdq_quant_int4(None, 100, None, None, None, 0, None, None, None, 4, 100, None)
+    assert rc == 1 and "multiple of 64" in lib.gwa_last_error().decode()
+    rc = lib.gwa_svdq_gemm_w4a4(None, None, None, None, None, None, 0, None, None, 0, None, None, 0, 0,
+                                8, 24, 128, None)
+    assert rc == 1 and "multiple of 16" in lib.gwa_last_error().decode()
+    rc = lib.gwa_w8a8_gemm(None, None, None, None, None, 0, None, 7, 8, 64, 64, None)
+    assert rc == 1 and "out_dtype" in lib.gwa_last_error().decode()
+    rc = lib.gwa_transpose_2d(None, None, 4, 4, 3, None)
+    assert rc == 1
+    # empty problems are no-ops
+    assert lib.gwa_svdq_quant_int4(None, 64, None, None, None, 0, None, None, None, 0, 64, None) == 0
+    assert lib.gwa_probe_add_one(None, None, 0, None) == 0
+
+
+def test_native_error_is_raised_with_message():
+    from gen_worker_amd import _native
+
+    with pytest.raises(_native.NativeError, match="multiple of 64"):
+        _native.call("gwa_w8a8_gemm", None, None, None, None, None, 0, None, 0, 8, 64, 100, None)
+
+
+def test_ops_refuse_cpu_tensors():
+    import gen_worker_amd  # noqa: F401
+    from gen_worker_amd.ops import SvdqOpError
+
+    x = torch.zeros(4, 128, dtype=torch.bfloat16)
+    with pytest.raises(SvdqOpError, match="GPU only"):
+        torch.ops.cozy_gen_worker.svdq_quant(x, None, torch.ones(()), False)
+    with pytest.raises(SvdqOpError, match="blocked"):
+        torch.ops.cozy_gen_worker.svdq_quant(x, None, torch.ones(()), True)
+    with pytest.raises(SvdqOpError, match="GPU only"):
+        torch.ops.cozy_gen_worker.w8a8_quant(x)
+
+
+def test_fake_impls_trace_shapes():
+    import gen_worker_amd  # noqa: F401
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    with FakeTensorMode():
+        x = torch.empty(77, 384, dtype=torch.bfloat16)
+        pdt = torch.empty(32, 384, dtype=torch.bfloat16)
+        q, s, la = torch.ops.cozy_gen_worker.svdq_quant_lora(x, None, None, pdt)
+        assert q.shape == (77, 192) and s.shape == (77, 6) and la.shape == (77, 32)
+        w = torch.empty(128, 192, dtype=torch.uint8)
+        ws = torch.empty(128, 6, dtype=torch.float16)
+        y = torch.ops.cozy_gen_worker.svdq_w4a4_linear(q, s, w, ws, None, None, la, torch.empty(128, 32,
+                                                       dtype=torch.bfloat16), None, torch.float16, False)
+        assert y.shape == (77, 128) and y.dtype == torch.float16
+
+
+def test_module_contract_refusals():
+    from gen_worker_amd import SvdqFusedError, SvdqW4A4Linear, W8a8Error, Int8ScaledLinear
+
+    with pytest.raises(SvdqFusedError):
+        SvdqW4A4Linear(100, 128, rank=32, bias=True)
+    with pytest.raises(SvdqFusedError):
+        SvdqW4A4Linear(128, 120, rank=32, bias=True)
+    with pytest.raises(SvdqFusedError):
+        SvdqW4A4Linear(128, 128, rank=24, bias=True)
+    with pytest.raises(W8a8Error):
+        Int8ScaledLinear(100, 128, bias=False)
+    m = SvdqW4A4Linear(3072, 3072, rank=32, bias=True)
+    assert m.weight.shape == (3072, 1536) and m.weight.dtype == torch.uint8
+    assert m.weight_scale.shape == (3072, 48) and m.weight_scale.dtype == torch.float16
+    assert m.proj_down.shape == (3072, 32) and m.proj_up.shape == (3072, 32)
+    names = set(dict(m.named_buffers()))
+    assert {"weight", "weight_scale", "second", "smooth_factor", "proj_down", "proj_up"} <= names
+
+
+def test_fold_to_dense_module_matches_oracle():
+    """The any-hardware fallback lane of the module equals the oracle's folded weight."""
+    from gen_worker_amd import synthetic
+    from gen_worker_amd.svdq import build_svdq_w4a4_linear, fold_to_dense
+
+    L = synthetic.w4a4_layer(128, 256, 16)
+    mod = build_svdq_w4a4_linear(qweight=L.qweight, wscales=L.wscales, smooth=L.smooth, proj_down=L.proj_down,
+                                 proj_up=L.proj_up, bias=L.bias, device="cpu")
+    lin = fold_to_dense(mod, compute_dtype=torch.float32)
+    b = lambda t: t.view(torch.int16).numpy().view(np.uint16)  # noqa: E731
+    want = O.fold_to_dense(L.qweight.numpy(), L.wscales.numpy(), b(L.smooth), b(L.proj_down), b(L.proj_up))
+    assert np.allclose(lin.weight.detach().numpy(), want, rtol=1e-6, atol=1e-7)
+
+
+def test_svdquant_decompose_reconstructs():
+    from gen_worker_amd.svdq import svdquant_decompose
+
+    g = torch.Generator().manual_seed(0)
+    w = torch.randn(64, 128, generator=g)
+    sm = torch.rand(128, generator=g) + 0.5
+    res, down, up = svdquant_decompose(w, sm, 16)
+    back = res / sm.reshape(1, -1) + up @ down.t()
+    assert torch.allclose(back, w, atol=1e-4)
+
+
+@pytest.mark.parametrize("name", sorted(p.name for p in GOLDEN.glob("*.npz")))
+def test_golden_fixtures_reproduce(name):
+    """The pinned oracle regenerates every committed fixture bit for bit."""
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location("make_golden", GOLDEN / "make_golden.py")
+    mg = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mg)
+    import tempfile
+
+    with tempfile.TemporaryDirectory() as d:
+        mg.make(Path(d))
+        a = np.load(GOLDEN / name)
+        b = np.load(Path(d) / name)
+        assert set(a.files) == set(b.files)
+        for f in a.files:
+            assert np.array_equal(a[f], b[f]), f
+
+
+def test_synthetic_inputs_are_deterministic():
+    from gen_worker_amd import synthetic
+
+    a = synthetic.activation(8, 3072, outlier_frac=0.005, outlier_scale=30.0)
+    b = synthetic.activation(8, 3072, outlier_frac=0.005, outlier_scale=30.0)
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    assert int((a.float().abs().amax(dim=0) > 20).sum()) > 0
+    s = synthetic.smooth_factor(3072)
+    assert float(s.float().min()) >= 0.25 and float(s.float().max()) <= 4.0
