@@ -68,6 +68,7 @@ def main() -> int:
     mod = build_svdq_w4a4_linear(qweight=L.qweight, wscales=L.wscales, smooth=L.smooth, proj_down=L.proj_down,
                                  proj_up=L.proj_up, bias=L.bias, device=dev)
     x = x_cpu.to(dev)
+    assert mod.lane == "packed", "synthetic int4 weights are in [-7, 7]: the fast lane must be armed"
     ops = torch.ops.cozy_gen_worker
 
     def step(evs=None):
@@ -76,8 +77,8 @@ def main() -> int:
         qa, sa, la = ops.svdq_quant_lora(x, mod.smooth_factor, None, mod.proj_down_t)
         if evs is not None:
             evs[1].record()
-        y = ops.svdq_w4a4_linear(qa, sa, mod.weight, mod.weight_scale, None, mod.second, la, mod.proj_up,
-                                 mod.bias, torch.bfloat16, False)
+        y = ops.svdq_w4a4_linear_packed(qa, sa, mod.weight_packed, mod.weight_scale, mod.weight_sums, None,
+                                        mod.second, la, mod.proj_up, mod.bias, torch.bfloat16, False)
         if evs is not None:
             evs[2].record()
         return y
@@ -152,7 +153,7 @@ def main() -> int:
                    "in_dtype": "bf16", "out_dtype": "bf16", "parallelism": "none"},
         "roofline": {"bound": "mfma", "achieved": round(gemm_tops, 2), "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
                      "frac": round(gemm_tops / INT8_PEAK_TOPS, 4), "traffic": traffic,
-                     "kernel": "w4a4_gemm_kernel", "algorithmic_ops_per_launch": int_ops,
+                     "kernel": "w4a4_gemm_fp8_kernel", "algorithmic_ops_per_launch": int_ops,
                      "avg_launch_us": round(gemm_ms * 1e3, 2)},
         "pct_int8_peak": round(100 * value_tops / INT8_PEAK_TOPS, 2),
         "act_quant": {"avg_launch_us": round(quant_ms * 1e3, 2), "algorithmic_bytes": qbytes,

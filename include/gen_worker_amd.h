@@ -60,7 +60,7 @@ int gwa_probe_add_one(const float* in, float* out, int64_t n, void* stream);
  *   s2         fp32 device scalar or NULL (= 1.0): second-level scale; the
  *              group scale is fp16(amax / (7 * s2)) and codes divide by
  *              (scale * s2), as models/nvfp4_quant.py:98-101 do for nvfp4
- *   proj_down_t bf16 [rank, K] (proj_down transposed) or NULL; rank % 16 == 0, rank <= 128
+ *   proj_down_t bf16 [rank, K] (proj_down transposed) or NULL; rank in {0, 16, 32, 64, 128}
  *   q          uint8 [M, K/2] packed codes (out)
  *   scales     fp16 [M, K/64] (out)
  *   la         bf16 [M, rank] = x @ proj_down on RAW x (out; NULL iff proj_down_t is NULL) */
@@ -80,15 +80,47 @@ int gwa_svdq_quant_int4(const void* x, int64_t ldx, const void* smooth, const fl
  *   qw     uint8 [N, K/2]   sw fp16 [N, K/64]   (weight [out, in/2] layout)
  *   s2     fp32 device scalar or NULL (= 1.0)
  *   second fp32 [second_numel] (1 or N) or NULL (= 1.0)
- *   la     bf16 [M, rank] or NULL;  up bf16 [N, rank] or NULL; rank % 16 == 0, <= 128
+ *   la     bf16 [M, rank] or NULL;  up bf16 [N, rank] or NULL; rank in {0, 16, 32, 64, 128}
  *   bias   bf16 [N] or NULL
  *   out    [M, N] of out_dtype (GWA_DT_BF16 or GWA_DT_F16)
- * K % 128 == 0, N % 16 == 0. */
+ * K % 64 == 0, N % 16 == 0. This is the general path (int8 MFMA on the logical
+ * two's-complement weights, any code in [-8, 7]); gwa_svdq_gemm_w4a4_packed
+ * is the fast path for prepacked weights. */
 int gwa_svdq_gemm_w4a4(const uint8_t* qa, const void* sa, const uint8_t* qw, const void* sw,
                        const float* s2, const float* second, int64_t second_numel,
                        const void* la, const void* up, int64_t rank, const void* bias,
                        void* out, int out_dtype, int epilogue_flags,
                        int64_t M, int64_t N, int64_t K, void* stream);
+
+/* Prepack int4 weights for gwa_svdq_gemm_w4a4_packed (done once per weight).
+ * No reference counterpart beyond the layout conversions of
+ * models/svdq_layout.py:165-221 (pack_qweight & co.): converts the logical
+ * [N, K/2] two's-complement codes into this library's resident fp8-ready
+ * layout and computes the per-(row, group) code sums the GEMM's exact offset
+ * correction needs.
+ *   qw        uint8 [N, K/2] logical codes (in)
+ *   qw_packed uint8 [N, K/2] (out)     wsum int16 [N, K/64] (out)
+ *   n_neg8    int32 device counter, must hold 0; receives the number of -8
+ *             codes (the packed layout holds [-7, 7]; any -8 means the
+ *             weights must use gwa_svdq_gemm_w4a4 instead) */
+int gwa_svdq_pack_weight_int4(const uint8_t* qw, uint8_t* qw_packed, int16_t* wsum, int* n_neg8,
+                              int64_t N, int64_t K, void* stream);
+
+/* Kernel 2, fast path: the same contract as gwa_svdq_gemm_w4a4 (replacing
+ * _gemm_w4a4 + svdq_epilogue_lora, models/w4a4.py:173-180 and
+ * models/svdq_fused.py:315-377) on prepacked weights: one exact fp8 MFMA per
+ * K-group. qw_packed/wsum from gwa_svdq_pack_weight_int4. K % 128 == 0,
+ * N % 16 == 0. */
+int gwa_svdq_gemm_w4a4_packed(const uint8_t* qa, const void* sa, const uint8_t* qw_packed, const void* sw,
+                              const int16_t* wsum, const float* s2, const float* second, int64_t second_numel,
+                              const void* la, const void* up, int64_t rank, const void* bias,
+                              void* out, int out_dtype, int epilogue_flags,
+                              int64_t M, int64_t N, int64_t K, void* stream);
+
+/* Debug: exact per-group partial sums through the fast path's fp8 MFMA
+ * arithmetic (same layout as gwa_svdq_group_psums). No reference counterpart. */
+int gwa_svdq_group_psums_packed(const uint8_t* qa, const uint8_t* qw_packed, const int16_t* wsum,
+                                int32_t* out, int64_t M, int64_t N, int64_t K, void* stream);
 
 /* Debug: exact int32 per-group partial sums out[m, n, g] = sum_{k in g} qx[m,k] qw[n,k]
  * computed by the same MFMA and unpack code as gwa_svdq_gemm_w4a4. No

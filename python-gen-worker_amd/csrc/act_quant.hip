@@ -7,21 +7,46 @@
 // packed two per byte; plus la = x @ proj_down on the RAW activations via
 // bf16 MFMA 16x16x32.
 //
-// One wave owns 16 rows. Lane (i = lane % 16, kq = lane / 16) holds, per
-// group of 64, the 16 elements of row i at K offsets kq*8 + [0,8) and
-// 32 + kq*8 + [0,8): each is one 16-byte load, and the same registers are
-// the MFMA A operand for the two 32-wide K halves of the group. The row's
-// group absmax is a max over the 4 lanes {i, i+16, i+32, i+48}.
+// Work split: a workgroup owns 16 rows; its NW waves split the K groups of
+// those rows evenly, and their partial la blocks are summed through LDS. Lane
+// (i = lane % 16, kq = lane / 16) holds, per group of 64, the 16 elements of
+// row i at K offsets kq*8 + [0,8) and 32 + kq*8 + [0,8): each is one 16-byte
+// load, and the same registers are the MFMA A operand of the group's two
+// 32-wide K halves. The row's group absmax is a max over lanes {i, i+16,
+// i+32, i+48}.
 //
-// Arithmetic follows the reference order (models/svdq_fused.py:88-103,
-// models/nvfp4_quant.py:96-102): xs = bf16(x / smooth) (IEEE fp32 divide,
-// RNE); scale = fp16(clamp(amax / (7 * s2), 2^-24, 65504)); codes =
-// clamp(rne(xs / (float(scale) * s2)), -8, 7).
+// Arithmetic = the reference order (models/svdq_fused.py:88-103,
+// models/nvfp4_quant.py:96-102): xs = RN_bf16(RN_f32(x / smooth));
+// scale = fp16(clamp(RN_f32(amax / (7 * s2)), 2^-24, 65504));
+// code = clamp(rne(RN_f32(xs / (float(scale) * s2))), -8, 7).
+//
+// Fast path (bit-identical, no per-element division):
+//  * smoothing: xs = RN_bf16(x * r), r = RN_f32(1 / smooth). For bf16 x and a
+//    normal bf16 smooth, x/s lies at least 2^-17 (relative) from any bf16
+//    rounding tie unless it is exact, and |x*r - x/s| <= 2^-23 |x/s|, so both
+//    round to the same bf16.
+//  * codes (s2 == 1, scale a normal fp16 below the clamp): q = xs / d with an
+//    8-bit-significand xs and an 11-bit d is either an exact half-integer or
+//    more than 2^-12 from one; p = xs * rcp(d) is within 2^-19 of q. Adding
+//    3072 rounds p onto a 2^-12 grid, which lands exact ties exactly on k+1/2
+//    and leaves every other value on its own side; adding (1.5*2^23 - 3072)
+//    then rounds that grid value to an integer with ties-to-even, exactly the
+//    RNE of q. |q| <= 7*(1 + 2^-11) < 7.5 here, so no clamp is needed, and
+//    the code is the low nibble of the float's bits.
+//  Anything else (s2 != 1, non-normal smooth, clamped or subnormal scales)
+//  takes the IEEE-division path.
 // ---------------------------------------------------------------------------
 namespace {
 
 constexpr float kScaleMin = 5.9604644775390625e-08f;  // 2^-24, smallest positive fp16
 constexpr float kFp16Max = 65504.0f;
+constexpr float kFp16MinNormal = 6.103515625e-05f;     // 2^-14
+constexpr float kSnap = 3072.0f;                       // 1.5 * 2^11: spacing 2^-12 on [2048, 4096)
+constexpr float kRound = 12582912.0f - 3072.0f;        // 1.5 * 2^23 - 3072
+
+typedef float v2f __attribute__((ext_vector_type(2)));
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ void unpack8_bf16(v4i w, float* v) {
 #pragma unroll
@@ -32,94 +57,215 @@ __device__ __forceinline__ void unpack8_bf16(v4i w, float* v) {
   }
 }
 
-__device__ __forceinline__ float bf16_round(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+// RN_bf16 of two floats (v_cvt_pk_bf16_f32), returned as floats.
+__device__ __forceinline__ void round_bf16x2(float& a, float& b) {
+  v2bf r = __builtin_convertvector((v2f){a, b}, v2bf);
+  uint32_t u = __builtin_bit_cast(uint32_t, r);
+  a = bf16_lo(u);
+  b = bf16_hi(u);
+}
 
-__device__ __forceinline__ uint32_t int4_code(float v, float d) {
+__device__ __forceinline__ uint32_t int4_code_exact(float v, float d) {
   float q = __builtin_rintf(v / d);
   q = fminf(fmaxf(q, -8.0f), 7.0f);
   return (uint32_t)((int)q) & 0xFu;
 }
 
-template <int RB>
-__global__ __launch_bounds__(64) void svdq_quant_int4_kernel(
+// Pack 8 codes held as the low nibbles of h[0..7] (element 2j in the low nibble).
+__device__ __forceinline__ uint32_t pack_nibbles(const uint32_t* h) {
+  uint32_t w = 0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) w |= (h[j] & 0xFu) << (4 * j);
+  return w;
+}
+
+template <int RB, int NW>
+__global__ __launch_bounds__(NW * 64) void svdq_quant_int4_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, const uint16_t* __restrict__ smooth,
     const float* __restrict__ s2p, const uint16_t* __restrict__ pdt, uint8_t* __restrict__ q,
     uint16_t* __restrict__ sc, uint16_t* __restrict__ la, int M, int K) {
-  const int lane = threadIdx.x;
+  extern __shared__ float lds[];  // [K] smoothing reciprocals (if smooth), then [NW][RB][64][4] la partials
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int i = lane & 15, kq = lane >> 4;
   const int row0 = blockIdx.x * 16;
   const int row = row0 + i;
-  const bool valid = row < M;
-  const float s2 = s2p ? *s2p : 1.0f;
-  const float den7 = 7.0f * s2;
   const int G = K >> 6;
-  const uint16_t* xr = x + (int64_t)(valid ? row : 0) * ldx;
-  uint8_t* qr = q + (int64_t)(valid ? row : 0) * (K >> 1);
+  float* rs = lds;
+  float* lap = lds + (smooth ? K : 0);
+
+  // buffers: every access is unconditional; rows >= M read 0 / store nothing
+  const rsrc_t xbuf = make_rsrc(x, (uint32_t)(((int64_t)(M - 1) * ldx + K) * 2));
+  const rsrc_t qbuf = make_rsrc(q, (uint32_t)((int64_t)M * (K >> 1)));
+  const rsrc_t sbuf = make_rsrc(sc, (uint32_t)((int64_t)M * G * 2));
+  const rsrc_t pbuf = make_rsrc(pdt, (uint32_t)(RB * 16 * K * 2));
+  const uint32_t xrow = (uint32_t)((int64_t)row * ldx * 2);
+  const uint32_t qrow = (uint32_t)((int64_t)row * (K >> 1));
+  const uint32_t srow = kq == 0 ? (uint32_t)((int64_t)row * G * 2) : kOOB;
+  const uint32_t prow = (uint32_t)(i * K * 2);
+
+  bool smooth_fast = true;
+  if (smooth) {
+    int bad = 0;
+    for (int k = tid; k < K; k += NW * 64) {
+      const float sv = bf16_to_f32(smooth[k]);
+      const float a = fabsf(sv);
+      bad |= !(a >= 1.1754943508222875e-38f && a <= 3.4028234663852886e38f);
+      rs[k] = 1.0f / sv;
+    }
+    smooth_fast = !__syncthreads_or(bad);
+  }
+  const float s2 = s2p ? *s2p : 1.0f;
+  const bool s2_one = (s2 == 1.0f);
+  const float den7 = 7.0f * s2;
+
+  const int gpw = (G + NW - 1) / NW;
+  const int g0 = wave * gpw;
+  const int g1 = min(G, g0 + gpw);
 
   v4f acc[RB > 0 ? RB : 1];
 #pragma unroll
   for (int rb = 0; rb < (RB > 0 ? RB : 1); ++rb) acc[rb] = (v4f){0.f, 0.f, 0.f, 0.f};
 
-  for (int g = 0; g < G; ++g) {
-    const int k0 = g * 64 + kq * 8;
-    v4i xa = {0, 0, 0, 0}, xb = {0, 0, 0, 0};
-    if (valid) {
-      xa = *(const v4i*)(xr + k0);
-      xb = *(const v4i*)(xr + k0 + 32);
-    }
+  // One prefetch ring of depth PF for both the activations and the low-rank
+  // operands: every group's loads are issued PF groups before it is used, so
+  // a wave's chain of groups pays the memory latency once, not per group.
+  constexpr int PF = 4;
+  constexpr int RBX = RB > 0 ? RB : 1;
+  v4i xa[PF], xb[PF], ba[PF][RBX], bb[PF][RBX];
+#pragma unroll
+  for (int j = 0; j < PF; ++j) {
+    const uint32_t off = xrow + (uint32_t)((g0 + j) * 128 + kq * 16);
+    xa[j] = buf_load16(xbuf, off);
+    xb[j] = buf_load16(xbuf, off + 64);
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
-      const uint16_t* pr = pdt + (int64_t)(rb * 16 + i) * K;
-      v4i ba = *(const v4i*)(pr + k0);
-      v4i bb = *(const v4i*)(pr + k0 + 32);
-      acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, xa),
-                                                        __builtin_bit_cast(v8bf, ba), acc[rb], 0, 0, 0);
-      acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, xb),
-                                                        __builtin_bit_cast(v8bf, bb), acc[rb], 0, 0, 0);
+      const uint32_t po = prow + (uint32_t)(rb * 16 * K * 2 + (g0 + j) * 128 + kq * 16);
+      ba[j][rb] = buf_load16(pbuf, po);
+      bb[j][rb] = buf_load16(pbuf, po + 64);
     }
+  }
 
-    float v[16];
-    unpack8_bf16(xa, v);
-    unpack8_bf16(xb, v + 8);
-    if (smooth) {
-      float sm[16];
-      unpack8_bf16(*(const v4i*)(smooth + k0), sm);
-      unpack8_bf16(*(const v4i*)(smooth + k0 + 32), sm + 8);
+  for (int gb = g0; gb < g1; gb += PF) {
 #pragma unroll
-      for (int j = 0; j < 16; ++j) v[j] = bf16_round(v[j] / sm[j]);
-    }
-    float amax = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) amax = fmaxf(amax, fabsf(v[j]));
-    amax = fmaxf(amax, __shfl_xor(amax, 16));
-    amax = fmaxf(amax, __shfl_xor(amax, 32));
+    for (int j = 0; j < PF; ++j) {
+      const int g = gb + j;
+      if (g >= g1) break;
+      const int k0 = g * 64 + kq * 8;
+      const v4i ca = xa[j], cb = xb[j];
 
-    float scl = amax / den7;
-    scl = fminf(fmaxf(scl, kScaleMin), kFp16Max);
-    const uint16_t sh = f32_to_f16_bits(scl);
-    const float d = f16_bits_to_f32(sh) * s2;
-
-    uint32_t w0 = 0, w1 = 0;
+      // xs as packed bf16 words (8 per lane) and as floats
+      uint32_t w[8];
+      if (smooth) {
+        float v[16];
+        unpack8_bf16(ca, v);
+        unpack8_bf16(cb, v + 8);
+        if (smooth_fast) {
+          float r[16];
+          *(v4f*)(r) = *(const v4f*)(rs + k0);
+          *(v4f*)(r + 4) = *(const v4f*)(rs + k0 + 4);
+          *(v4f*)(r + 8) = *(const v4f*)(rs + k0 + 32);
+          *(v4f*)(r + 12) = *(const v4f*)(rs + k0 + 36);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      w0 |= int4_code(v[j], d) << (4 * j);
-      w1 |= int4_code(v[8 + j], d) << (4 * j);
-    }
-    if (valid) {
-      *(uint32_t*)(qr + (k0 >> 1)) = w0;
-      *(uint32_t*)(qr + ((k0 + 32) >> 1)) = w1;
-      if (kq == 0) sc[(int64_t)row * G + g] = sh;
+          for (int t = 0; t < 16; ++t) v[t] *= r[t];
+        } else {
+          float sm[16];
+          unpack8_bf16(*(const v4i*)(smooth + k0), sm);
+          unpack8_bf16(*(const v4i*)(smooth + k0 + 32), sm + 8);
+#pragma unroll
+          for (int t = 0; t < 16; ++t) v[t] /= sm[t];
+        }
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+          w[t] = __builtin_bit_cast(uint32_t, __builtin_convertvector((v2f){v[2 * t], v[2 * t + 1]}, v2bf));
+      } else {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          w[t] = (uint32_t)ca[t];
+          w[4 + t] = (uint32_t)cb[t];
+        }
+      }
+      // group absmax on the bf16 bit patterns (|x| orders like its bits)
+      v2u16 mx = {0, 0};
+#pragma unroll
+      for (int t = 0; t < 8; ++t)
+        mx = __builtin_elementwise_max(mx, __builtin_bit_cast(v2u16, w[t] & 0x7fff7fffu));
+      uint32_t mb = mx[0] > mx[1] ? mx[0] : mx[1];
+      mb = max(mb, (uint32_t)__shfl_xor((int)mb, 16));
+      mb = max(mb, (uint32_t)__shfl_xor((int)mb, 32));
+      const float amax = __uint_as_float(mb << 16);
+
+      float scl = amax / den7;
+      const bool fast = s2_one && scl >= kFp16MinNormal && scl < kFp16Max;
+      scl = fminf(fmaxf(scl, kScaleMin), kFp16Max);
+      const uint16_t sh = f32_to_f16_bits(scl);
+      const float d = f16_bits_to_f32(sh) * s2;
+
+      float v[16];
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        v[2 * t] = bf16_lo(w[t]);
+        v[2 * t + 1] = bf16_hi(w[t]);
+      }
+      uint32_t w0, w1;
+      if (fast) {
+        const float rd = __builtin_amdgcn_rcpf(d);
+        uint32_t h[16];
+#pragma unroll
+        for (int t = 0; t < 16; ++t) h[t] = __float_as_uint(((v[t] * rd) + kSnap) + kRound);
+        w0 = pack_nibbles(h);
+        w1 = pack_nibbles(h + 8);
+      } else {
+        w0 = w1 = 0;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          w0 |= int4_code_exact(v[t], d) << (4 * t);
+          w1 |= int4_code_exact(v[8 + t], d) << (4 * t);
+        }
+      }
+      buf_store4(w0, qbuf, qrow + (uint32_t)(k0 >> 1));
+      buf_store4(w1, qbuf, qrow + (uint32_t)((k0 + 32) >> 1));
+      buf_store2(sh, sbuf, srow + (uint32_t)(g * 2));
+
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, ca),
+                                                          __builtin_bit_cast(v8bf, ba[j][rb]), acc[rb], 0, 0, 0);
+        acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, cb),
+                                                          __builtin_bit_cast(v8bf, bb[j][rb]), acc[rb], 0, 0, 0);
+      }
+      {  // refill this ring slot with group g + PF
+        const uint32_t off = xrow + (uint32_t)((g + PF) * 128 + kq * 16);
+        xa[j] = buf_load16(xbuf, off);
+        xb[j] = buf_load16(xbuf, off + 64);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+          const uint32_t po = prow + (uint32_t)(rb * 16 * K * 2 + (g + PF) * 128 + kq * 16);
+          ba[j][rb] = buf_load16(pbuf, po);
+          bb[j][rb] = buf_load16(pbuf, po + 64);
+        }
+      }
     }
   }
 
   if (RB > 0) {
-    const int R = RB * 16;
+    // sum the NW partial la blocks through LDS; wave 0 writes bf16
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
+    for (int rb = 0; rb < RB; ++rb) *(v4f*)(lap + ((wave * RB + rb) * 64 + lane) * 4) = acc[rb];
+    __syncthreads();
+    if (wave == 0) {
+      const int R = RB * 16;
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int r = row0 + 4 * kq + t;
-        if (r < M) la[(int64_t)r * R + rb * 16 + i] = f32_to_bf16(acc[rb][t]);
+      for (int rb = 0; rb < RB; ++rb) {
+        v4f s = acc[rb];
+        for (int w = 1; w < NW; ++w) {
+          const v4f o = *(const v4f*)(lap + ((w * RB + rb) * 64 + lane) * 4);
+          s += o;
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int r = row0 + 4 * kq + t;
+          if (r < M) la[(int64_t)r * R + rb * 16 + i] = f32_to_bf16(s[t]);
+        }
       }
     }
   }
@@ -199,15 +345,15 @@ extern "C" int gwa_svdq_quant_int4(const void* x, int64_t ldx, const void* smoot
   GWA_REQUIRE((proj_down_t == nullptr) == (la == nullptr),
               "svdq_quant_int4: proj_down_t and la must both be given or both be NULL");
   const int64_t R = proj_down_t ? rank : 0;
-  GWA_REQUIRE(R % 16 == 0 && R <= 128, "svdq_quant_int4: rank %lld must be a multiple of 16 and <= 128",
-              (long long)R);
-  GWA_REQUIRE(M < (1ll << 31) && K < (1ll << 30), "svdq_quant_int4: shape too large");
+  GWA_REQUIRE(R == 0 || R == 16 || R == 32 || R == 64 || R == 128,
+              "svdq_quant_int4: rank %lld not in {0,16,32,64,128}", (long long)R);
+  GWA_REQUIRE(M < (1ll << 31) && K < (1ll << 24) && (M * ldx * 2) < (1ll << 31),
+              "svdq_quant_int4: x must stay below 2 GiB (buffer addressing)");
   if (M == 0) return GWA_OK;
   GWA_REQUIRE(x && q && scales, "svdq_quant_int4: null pointer");
   GWA_REQUIRE(GWA_ALIGNED(x, 16) && GWA_ALIGNED(q, 16) && GWA_ALIGNED(scales, 2) &&
                   GWA_ALIGNED(smooth, 16) && GWA_ALIGNED(proj_down_t, 16) && GWA_ALIGNED(la, 2),
               "svdq_quant_int4: x, q, smooth and proj_down_t must be 16-byte aligned");
-  const dim3 grid((unsigned)((M + 15) / 16)), block(64);
   hipStream_t s = (hipStream_t)stream;
   const uint16_t* xp = (const uint16_t*)x;
   const uint16_t* sm = (const uint16_t*)smooth;
@@ -215,23 +361,43 @@ extern "C" int gwa_svdq_quant_int4(const void* x, int64_t ldx, const void* smoot
   uint16_t* sc = (uint16_t*)scales;
   uint16_t* lp = (uint16_t*)la;
   const int m = (int)M, k = (int)K;
-#define GWA_QUANT_CASE(RBV)                                                                              \
-  case RBV:                                                                                              \
-    hipLaunchKernelGGL(svdq_quant_int4_kernel<RBV>, grid, block, 0, s, xp, ldx, sm, s2, pd, q, sc, lp, m, k); \
+  const int rb = (int)(R / 16);
+  // K is split over NW waves per 16-row block: wide splits when there are few
+  // row blocks, so that small-M calls still put enough waves on the GPU.
+  const int64_t blocks = (M + 15) / 16;
+  int nw = blocks >= 512 ? 4 : (blocks >= 128 ? 8 : 16);
+  // 16-wave blocks cap VGPRs at 128 and 8-wave blocks at 256: the low-rank
+  // operand rings of the larger ranks need the narrower splits
+  if (rb >= 2 && nw > 8) nw = 8;
+  if (rb >= 8) nw = 4;
+  const size_t lds = (sm ? (size_t)K * 4 : 0) + (size_t)nw * rb * 1024;
+  GWA_REQUIRE(lds <= 160 * 1024, "svdq_quant_int4: K=%lld needs too much LDS", (long long)K);
+  const dim3 grid((unsigned)blocks);
+#define GWA_QUANT_LAUNCH(RBV, NWV)                                                                  \
+  hipLaunchKernelGGL((svdq_quant_int4_kernel<RBV, NWV>), grid, dim3(NWV * 64), lds, s, xp, ldx, sm, s2, pd, q, \
+                     sc, lp, m, k)
+#define GWA_QUANT_RB(RBV)                      \
+  case RBV:                                    \
+    if (nw == 16) GWA_QUANT_LAUNCH(RBV, 16);   \
+    else if (nw == 8) GWA_QUANT_LAUNCH(RBV, 8); \
+    else GWA_QUANT_LAUNCH(RBV, 4);             \
     break;
-  switch (R / 16) {
-    GWA_QUANT_CASE(0)
-    GWA_QUANT_CASE(1)
-    GWA_QUANT_CASE(2)
-    GWA_QUANT_CASE(3)
-    GWA_QUANT_CASE(4)
-    GWA_QUANT_CASE(5)
-    GWA_QUANT_CASE(6)
-    GWA_QUANT_CASE(7)
-    GWA_QUANT_CASE(8)
-    default: return gwa_set_error(GWA_ERR_INVALID, "svdq_quant_int4: unsupported rank %lld", (long long)R);
+#define GWA_QUANT_RB_WIDE(RBV)                 \
+  case RBV:                                    \
+    if (nw == 8) GWA_QUANT_LAUNCH(RBV, 8);     \
+    else GWA_QUANT_LAUNCH(RBV, 4);             \
+    break;
+  switch (rb) {
+    GWA_QUANT_RB(0)
+    GWA_QUANT_RB(1)
+    GWA_QUANT_RB_WIDE(2)
+    GWA_QUANT_RB_WIDE(4)
+    case 8: GWA_QUANT_LAUNCH(8, 4); break;
+    default: return gwa_set_error(GWA_ERR_INVALID, "svdq_quant_int4: rank %lld not in {0,16,32,64,128}", (long long)R);
   }
-#undef GWA_QUANT_CASE
+#undef GWA_QUANT_RB
+#undef GWA_QUANT_RB_WIDE
+#undef GWA_QUANT_LAUNCH
   return gwa_check_launch("svdq_quant_int4");
 }
 

@@ -168,6 +168,7 @@ __global__ __launch_bounds__(256) void w4a4_gemm_kernel(
   }
 
   // ---------------- epilogue ----------------
+  const rsrc_t obuf = make_rsrc(out, (uint32_t)((int64_t)M * N * 2));
   const float s2 = s2p ? *s2p : 1.0f;
   const float base_mult = s2 * (1.0f / 256.0f);
 #pragma unroll
@@ -197,29 +198,28 @@ __global__ __launch_bounds__(256) void w4a4_gemm_kernel(
                                                       y, 0, 0, 0);
         }
       }
-      if (m < M) {
 #pragma unroll
-        for (int qd = 0; qd < 4; ++qd) {
-          const int n = nb + 8 * qd + 4 * h;
-          if (n >= N) continue;
-          float o[4];
+      for (int qd = 0; qd < 4; ++qd) {
+        const int n = nb + 8 * qd + 4 * h;
+        float o[4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            float t = y[4 * qd + e];
-            if (bias) t += bf16_to_f32(bias[n + e]);
-            if (GELU) t = gelu_tanh_f32(t);
-            o[e] = t;
-          }
-          uint2 pk;
-          if (OUT_F16) {
-            pk.x = pack_f16x2(o[0], o[1]);
-            pk.y = pack_f16x2(o[2], o[3]);
-          } else {
-            pk.x = pack_bf16x2(o[0], o[1]);
-            pk.y = pack_bf16x2(o[2], o[3]);
-          }
-          *(uint2*)(out + (int64_t)m * N + n) = pk;
+        for (int e = 0; e < 4; ++e) {
+          float t = y[4 * qd + e];
+          if (bias) t += bf16_to_f32(bias[n + e < N ? n + e : 0]);
+          if (GELU) t = gelu_tanh_f32(t);
+          o[e] = t;
         }
+        uint2 pk;
+        if (OUT_F16) {
+          pk.x = pack_f16x2(o[0], o[1]);
+          pk.y = pack_f16x2(o[2], o[3]);
+        } else {
+          pk.x = pack_bf16x2(o[0], o[1]);
+          pk.y = pack_bf16x2(o[2], o[3]);
+        }
+        // branch-free store after the MFMAs: rows >= M / columns >= N fall outside the buffer
+        const uint32_t off = (m < M && n < N) ? (uint32_t)(((int64_t)m * N + n) * 2) : kOOB;
+        buf_store8(pk, obuf, off);
       }
     }
   }
@@ -233,16 +233,17 @@ __global__ __launch_bounds__(64) void w4a4_psums_kernel(const uint8_t* __restric
   const int m0 = blockIdx.x * 32, n0 = blockIdx.y * 32;
   const int kbytes = K >> 1, G = K >> 6;
   const int m = m0 + r32, nr = n0 + r32;
+  const rsrc_t obuf = make_rsrc(out, (uint32_t)((int64_t)M * N * G * 4));
   for (int g = 0; g < G; ++g) {
     v4i a = nr < N ? *(const v4i*)(qw + (int64_t)nr * kbytes + g * 32 + 16 * h) : (v4i){0, 0, 0, 0};
     v4i b = m < M ? *(const v4i*)(qa + (int64_t)m * kbytes + g * 32 + 16 * h) : (v4i){0, 0, 0, 0};
     const v16i p = group_mfma_i8(a, b);
-    if (m < M) {
+    // branch-free stores (see the fp8 path): the buffer bounds drop the tails
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int n = n0 + 8 * (v >> 2) + 4 * h + (v & 3);
-        if (n < N) out[((int64_t)m * N + n) * G + g] = p[v] >> 8;
-      }
+    for (int v = 0; v < 16; ++v) {
+      const int n = n0 + 8 * (v >> 2) + 4 * h + (v & 3);
+      const uint32_t off = (m < M && n < N) ? (uint32_t)((((int64_t)m * N + n) * G + g) * 4) : kOOB;
+      buf_store4((uint32_t)(p[v] >> 8), obuf, off);
     }
   }
 }
@@ -261,13 +262,14 @@ extern "C" int gwa_svdq_gemm_w4a4(const uint8_t* qa, const void* sa, const uint8
               out_dtype);
   GWA_REQUIRE((la == nullptr) == (up == nullptr), "svdq_gemm_w4a4: la and up must both be given or both NULL");
   const int64_t R = la ? rank : 0;
-  GWA_REQUIRE(R % 16 == 0 && R <= 128, "svdq_gemm_w4a4: rank %lld must be a multiple of 16 and <= 128",
-              (long long)R);
+  GWA_REQUIRE(R == 0 || R == 16 || R == 32 || R == 64 || R == 128,
+              "svdq_gemm_w4a4: rank %lld not in {0,16,32,64,128}", (long long)R);
   GWA_REQUIRE(second == nullptr || second_numel == 1 || second_numel == N,
               "svdq_gemm_w4a4: second has %lld values for N=%lld", (long long)second_numel, (long long)N);
   GWA_REQUIRE((epilogue_flags & ~GWA_EPI_GELU_TANH) == 0, "svdq_gemm_w4a4: unknown epilogue flags 0x%x",
               epilogue_flags);
-  GWA_REQUIRE(M < (1ll << 31) && N < (1ll << 30) && K < (1ll << 30), "svdq_gemm_w4a4: shape too large");
+  GWA_REQUIRE(M < (1ll << 31) && N < (1ll << 30) && K < (1ll << 30) && M * N * 2 < (1ll << 31),
+              "svdq_gemm_w4a4: shape too large (the output must stay below 2 GiB)");
   if (M == 0) return GWA_OK;
   GWA_REQUIRE(qa && sa && qw && sw && out, "svdq_gemm_w4a4: null pointer");
   GWA_REQUIRE(GWA_ALIGNED(qa, 16) && GWA_ALIGNED(qw, 16) && GWA_ALIGNED(la, 16) && GWA_ALIGNED(up, 16) &&
@@ -318,7 +320,8 @@ extern "C" int gwa_svdq_gemm_w4a4(const uint8_t* qa, const void* sa, const uint8
 extern "C" int gwa_svdq_group_psums(const uint8_t* qa, const uint8_t* qw, int32_t* out, int64_t M, int64_t N,
                                     int64_t K, void* stream) {
   GWA_REQUIRE(M >= 0 && N >= 0 && K > 0 && K % 64 == 0, "svdq_group_psums: bad shape (K %% 64 == 0)");
-  GWA_REQUIRE(M < (1ll << 31) && N < (1ll << 30) && K < (1ll << 30), "svdq_group_psums: shape too large");
+  GWA_REQUIRE(M < (1ll << 31) && N < (1ll << 30) && K < (1ll << 30) && M * N * (K / 64) * 4 < (1ll << 31),
+              "svdq_group_psums: shape too large (the output must stay below 2 GiB)");
   GWA_REQUIRE((N + 31) / 32 < 65536, "svdq_group_psums: N too large");
   if (M == 0 || N == 0) return GWA_OK;
   GWA_REQUIRE(qa && qw && out, "svdq_group_psums: null pointer");

@@ -164,16 +164,31 @@ class SvdqW4A4Linear(nn.Module):
         else:
             self.bias = None
         self.register_buffer("_one", torch.ones((), dtype=torch.float32, device=dev), persistent=False)
+        # resident fast-path layout (derived from ``weight`` by refresh_derived)
+        self.register_buffer("weight_packed", None, persistent=False)
+        self.register_buffer("weight_sums", None, persistent=False)
 
     def refresh_derived(self) -> None:
-        """Recompute derived buffers after ``proj_down`` changes (the transposed copy kernel 1 reads)."""
+        """Recompute the derived buffers after ``weight`` / ``proj_down`` change: the transposed
+        ``proj_down`` kernel 1 reads, and (on the GPU) the prepacked fast-path weights. Weights holding a
+        -8 code keep the general int8 path."""
         if self.rank:
             self.proj_down_t = self.proj_down.t().contiguous()
+        self.weight_packed = self.weight_sums = None
+        if (self.weight.is_cuda and self.in_features % 128 == 0):
+            packed, sums, n_neg8 = torch.ops.cozy_gen_worker.svdq_pack_weight(self.weight)
+            if int(n_neg8.item()) == 0:
+                self.weight_packed, self.weight_sums = packed, sums
 
     def _load_from_state_dict(self, *args: Any, **kwargs: Any) -> None:  # noqa: D401
         super()._load_from_state_dict(*args, **kwargs)
-        if self.rank and self.proj_down is not None and self.proj_down.device.type != "meta":
+        if self.weight.device.type != "meta":
             self.refresh_derived()
+
+    @property
+    def lane(self) -> str:
+        """``"packed"`` (fast fp8-MFMA GEMM) or ``"general"`` (int8-MFMA GEMM on the logical weights)."""
+        return "packed" if self.weight_packed is not None else "general"
 
     def forward(self, x: Tensor) -> Tensor:
         shape = x.shape
@@ -187,9 +202,15 @@ class SvdqW4A4Linear(nn.Module):
         else:
             qa, sa = torch.ops.cozy_gen_worker.svdq_quant(x2, self.smooth_factor, self._one, False)
             la = None
-        y = torch.ops.cozy_gen_worker.svdq_w4a4_linear(
-            qa, sa, self.weight, self.weight_scale, None, self.second, la, self.proj_up,
-            self.bias, out_dtype, self.activation == "gelu_tanh")
+        gelu = self.activation == "gelu_tanh"
+        if self.weight_packed is not None:
+            y = torch.ops.cozy_gen_worker.svdq_w4a4_linear_packed(
+                qa, sa, self.weight_packed, self.weight_scale, self.weight_sums, None, self.second, la,
+                self.proj_up, self.bias, out_dtype, gelu)
+        else:
+            y = torch.ops.cozy_gen_worker.svdq_w4a4_linear(
+                qa, sa, self.weight, self.weight_scale, None, self.second, la, self.proj_up,
+                self.bias, out_dtype, gelu)
         return y.reshape(*shape[:-1], self.out_features)
 
     def extra_repr(self) -> str:

@@ -194,7 +194,7 @@ def test_psums_seeded_extremes(m, n, k):
 
 
 def _w4a4_case(m, n, k, rank, seed, smooth=True, bias=True, second=None, gelu=False, out_dtype=torch.bfloat16,
-               s2=None):
+               s2=None, packed=False):
     g = np.random.default_rng(seed)
     x = _rand_act(m, k, seed=seed)
     sm = O.f32_to_bf16_bits(np.exp(g.uniform(np.log(0.25), np.log(4), k)).astype(np.float32)) if smooth else None
@@ -214,9 +214,16 @@ def _w4a4_case(m, n, k, rank, seed, smooth=True, bias=True, second=None, gelu=Fa
                                                       torch.ones((), device=DEV), False)
         la = upd = None
     sec = torch.from_numpy(np.asarray(second, np.float32)).to(DEV) if second is not None else None
-    y = torch.ops.cozy_gen_worker.svdq_w4a4_linear(
-        qa, sa, torch.from_numpy(qw).to(DEV), from_bits(sw.view(np.uint16), torch.float16, DEV), s2t, sec, la,
-        upd, _dev16(b) if b is not None else None, out_dtype, gelu)
+    wd = torch.from_numpy(qw).to(DEV)
+    swd = from_bits(sw.view(np.uint16), torch.float16, DEV)
+    bd = _dev16(b) if b is not None else None
+    if packed:
+        wp, ws, n8 = torch.ops.cozy_gen_worker.svdq_pack_weight(wd)
+        assert int(n8.item()) == 0
+        y = torch.ops.cozy_gen_worker.svdq_w4a4_linear_packed(qa, sa, wp, swd, ws, s2t, sec, la, upd, bd,
+                                                              out_dtype, gelu)
+    else:
+        y = torch.ops.cozy_gen_worker.svdq_w4a4_linear(qa, sa, wd, swd, s2t, sec, la, upd, bd, out_dtype, gelu)
     torch.cuda.synchronize()
     return y, ref
 
@@ -258,6 +265,82 @@ def test_w4a4_epilogue_variants():
     check_output(y, ref, what="s2")
 
 
+# ---------------------------------------------------------------------------
+# kernel 2, fast path (prepacked weights, fp8 MFMA)
+# ---------------------------------------------------------------------------
+
+def _codes_no_neg8(g, shape):
+    q = g.integers(-7, 8, size=shape).astype(np.int8)
+    return O.pack_int4(q)
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 16, 128), (77, 48, 256), (64, 160, 3072), (129, 96, 640)])
+def test_psums_packed_bit_exact(m, n, k):
+    """The fast path's fp8 arithmetic reproduces every int32 group partial sum exactly,
+    for activations spanning all of [-8, 7] and weights spanning [-7, 7]."""
+    g = np.random.default_rng(m * 3 + n + k)
+    qa = g.integers(0, 256, size=(m, k // 2), dtype=np.uint8)
+    qa[0] = 0x88                                  # all -8 activations
+    qw = _codes_no_neg8(g, (n, k))
+    qw[0] = O.pack_int4(np.full((1, k), -7, np.int8))[0]   # extreme weights
+    wp, ws, n8 = torch.ops.cozy_gen_worker.svdq_pack_weight(torch.from_numpy(qw).to(DEV))
+    assert int(n8.item()) == 0
+    assert np.array_equal(ws.cpu().numpy().astype(np.int64),
+                          O.unpack_int4(qw).astype(np.int64).reshape(n, k // 64, 64).sum(-1))
+    ps = torch.ops.cozy_gen_worker.svdq_group_psums_packed(torch.from_numpy(qa).to(DEV), wp, ws)
+    assert np.array_equal(ps.cpu().numpy(), O.group_psums(qa, qw))
+    assert int(ps[0, 0, 0]) == 64 * 56
+
+
+def test_pack_counts_neg8():
+    g = np.random.default_rng(3)
+    codes = g.integers(-7, 8, size=(32, 256)).astype(np.int8)
+    codes[3, 5] = -8
+    codes[17, 200] = -8
+    _, _, n8 = torch.ops.cozy_gen_worker.svdq_pack_weight(torch.from_numpy(O.pack_int4(codes)).to(DEV))
+    assert int(n8.item()) == 2
+
+
+@pytest.mark.parametrize("m,n,k,rank", [
+    (1, 16, 128, 0), (77, 128, 384, 32), (256, 3072, 3072, 32), (333, 272, 512, 128), (130, 144, 256, 16),
+    (64, 256, 12288, 64), (300, 128, 15360, 32), (513, 400, 1024, 32),
+])
+def test_w4a4_packed_seeded(m, n, k, rank):
+    y, ref = _w4a4_case(m, n, k, rank, seed=m * 17 + n + k, packed=True)
+    check_output(y, ref, what=f"packed w4a4 {m}x{n}x{k} r{rank}")
+
+
+def test_w4a4_packed_epilogue_variants():
+    n = 256
+    sec = np.linspace(0.5, 2.0, n).astype(np.float32)
+    for kw, what in ((dict(second=sec), "second"), (dict(gelu=True), "gelu"), (dict(out_dtype=torch.float16), "f16"),
+                     (dict(smooth=False, bias=False), "bare"), (dict(s2=0.5), "s2")):
+        y, ref = _w4a4_case(96, n, 512, 32 if what != "bare" else 0, seed=11, packed=True, **kw)
+        check_output(y, ref, what=f"packed {what}")
+
+
+def test_module_lanes_agree():
+    """Weights without -8 take the packed lane, weights with a -8 code the general lane; both match the oracle."""
+    from gen_worker_amd import synthetic
+    from gen_worker_amd.svdq import build_svdq_w4a4_linear
+
+    L = synthetic.w4a4_layer(256, 512, 32)
+    x = synthetic.activation(100, 512, outlier_frac=0.01, outlier_scale=20.0)
+    mod = build_svdq_w4a4_linear(qweight=L.qweight, wscales=L.wscales, smooth=L.smooth, proj_down=L.proj_down,
+                                 proj_up=L.proj_up, bias=L.bias, device=DEV)
+    assert mod.lane == "packed"
+    qw = L.qweight.clone()
+    qw[0, 0] = (qw[0, 0] & 0xF0) | 0x8     # one -8 code
+    mod2 = build_svdq_w4a4_linear(qweight=qw, wscales=L.wscales, smooth=L.smooth, proj_down=L.proj_down,
+                                  proj_up=L.proj_up, bias=L.bias, device=DEV)
+    assert mod2.lane == "general"
+    for mdl, w in ((mod, L.qweight), (mod2, qw)):
+        y = mdl(x.to(DEV))
+        ref = O.w4a4_linear(bits16(x), bits16(L.smooth), w.numpy(), L.wscales.numpy(), bits16(L.proj_down),
+                            bits16(L.proj_up), bits16(L.bias))
+        check_output(y, ref, what=mdl.lane)
+
+
 def test_w4a4_module_config1_full_size():
     """Config 1 end to end through the module (M=4608, K=N=3072, r=32) vs the dequant-then-matmul oracle."""
     from gen_worker_amd import synthetic
@@ -267,6 +350,7 @@ def test_w4a4_module_config1_full_size():
     x = synthetic.activation(4608, 3072, outlier_frac=0.005, outlier_scale=30.0)
     mod = build_svdq_w4a4_linear(qweight=L.qweight, wscales=L.wscales, smooth=L.smooth, proj_down=L.proj_down,
                                  proj_up=L.proj_up, bias=L.bias, device=DEV)
+    assert mod.lane == "packed"
     y = mod(x.to(DEV).reshape(1, 4608, 3072))
     assert y.shape == (1, 4608, 3072)
     ref = O.w4a4_linear(bits16(x), bits16(L.smooth), L.qweight.numpy(), L.wscales.numpy(), bits16(L.proj_down),
