@@ -77,8 +77,8 @@ def main() -> int:
         qa, sa, la = ops.svdq_quant_lora(x, mod.smooth_factor, None, mod.proj_down_t)
         if evs is not None:
             evs[1].record()
-        y = ops.svdq_w4a4_linear_packed(qa, sa, mod.weight_packed, mod.weight_scale, mod.weight_sums, None,
-                                        mod.second, la, mod.proj_up, mod.bias, torch.bfloat16, False)
+        y = ops.svdq_w4a4_linear_packed(qa, sa, *mod.packed_weight(), None, mod.second, la, mod.proj_up, mod.bias,
+                                        torch.bfloat16, False)
         if evs is not None:
             evs[2].record()
         return y

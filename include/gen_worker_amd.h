@@ -96,23 +96,31 @@ int gwa_svdq_gemm_w4a4(const uint8_t* qa, const void* sa, const uint8_t* qw, con
  * No reference counterpart beyond the layout conversions of
  * models/svdq_layout.py:165-221 (pack_qweight & co.): converts the logical
  * [N, K/2] two's-complement codes into this library's resident fp8-ready
- * layout and computes the per-(row, group) code sums the GEMM's exact offset
- * correction needs.
+ * layout, rescales each row's group scales by a power of two, and prepacks
+ * the terms of the GEMM's activation-offset correction.
  *   qw        uint8 [N, K/2] logical codes (in)
- *   qw_packed uint8 [N, K/2] (out)     wsum int16 [N, K/64] (out)
+ *   sw        fp16 [N, K/64] group scales (in)
+ *   qw_packed uint8 [N, K/2] (out)
+ *   wsum      int16 [N, K/64] per-group code sums (out)
+ *   sw_packed fp16 [N, K/64] = sw * 2^-e[n] (out)
+ *   wcorr     fp16 [N, ceil(K/256), 8] correction pairs (out, 16-byte aligned)
+ *   escale    fp32 [N] = 2^e[n] (out)
  *   n_neg8    int32 device counter, must hold 0; receives the number of -8
  *             codes (the packed layout holds [-7, 7]; any -8 means the
  *             weights must use gwa_svdq_gemm_w4a4 instead) */
-int gwa_svdq_pack_weight_int4(const uint8_t* qw, uint8_t* qw_packed, int16_t* wsum, int* n_neg8,
+int gwa_svdq_pack_weight_int4(const uint8_t* qw, const void* sw, uint8_t* qw_packed, int16_t* wsum,
+                              void* sw_packed, void* wcorr, float* escale, int* n_neg8,
                               int64_t N, int64_t K, void* stream);
 
 /* Kernel 2, fast path: the same contract as gwa_svdq_gemm_w4a4 (replacing
  * _gemm_w4a4 + svdq_epilogue_lora, models/w4a4.py:173-180 and
  * models/svdq_fused.py:315-377) on prepacked weights: one exact fp8 MFMA per
- * K-group. qw_packed/wsum from gwa_svdq_pack_weight_int4. K % 128 == 0,
- * N % 16 == 0. */
-int gwa_svdq_gemm_w4a4_packed(const uint8_t* qa, const void* sa, const uint8_t* qw_packed, const void* sw,
-                              const int16_t* wsum, const float* s2, const float* second, int64_t second_numel,
+ * K-group. qw_packed / sw_packed / wcorr / escale from
+ * gwa_svdq_pack_weight_int4 (sa is the activation scale array as produced by
+ * gwa_svdq_quant_int4). K % 256 == 0, N % 16 == 0. */
+int gwa_svdq_gemm_w4a4_packed(const uint8_t* qa, const void* sa, const uint8_t* qw_packed,
+                              const void* sw_packed, const void* wcorr, const float* escale,
+                              const float* s2, const float* second, int64_t second_numel,
                               const void* la, const void* up, int64_t rank, const void* bias,
                               void* out, int out_dtype, int epilogue_flags,
                               int64_t M, int64_t N, int64_t K, void* stream);

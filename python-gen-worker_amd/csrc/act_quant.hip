@@ -57,14 +57,6 @@ __device__ __forceinline__ void unpack8_bf16(v4i w, float* v) {
   }
 }
 
-// RN_bf16 of two floats (v_cvt_pk_bf16_f32), returned as floats.
-__device__ __forceinline__ void round_bf16x2(float& a, float& b) {
-  v2bf r = __builtin_convertvector((v2f){a, b}, v2bf);
-  uint32_t u = __builtin_bit_cast(uint32_t, r);
-  a = bf16_lo(u);
-  b = bf16_hi(u);
-}
-
 __device__ __forceinline__ uint32_t int4_code_exact(float v, float d) {
   float q = __builtin_rintf(v / d);
   q = fminf(fmaxf(q, -8.0f), 7.0f);
@@ -72,117 +64,194 @@ __device__ __forceinline__ uint32_t int4_code_exact(float v, float d) {
 }
 
 // Pack 8 codes held as the low nibbles of h[0..7] (element 2j in the low nibble).
+// Each pair becomes one byte (bits 8+ of the pair word are don't-care), and
+// two byte permutes gather the four bytes.
 __device__ __forceinline__ uint32_t pack_nibbles(const uint32_t* h) {
-  uint32_t w = 0;
+  uint32_t p[4];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) w |= (h[j] & 0xFu) << (4 * j);
-  return w;
+  for (int j = 0; j < 4; ++j) p[j] = (h[2 * j] & 0xFu) | (h[2 * j + 1] << 4);
+  const uint32_t lo = __builtin_amdgcn_perm(p[1], p[0], 0x0c0c0400u);  // bytes 0,1: p0.b0, p1.b0
+  const uint32_t hi = __builtin_amdgcn_perm(p[3], p[2], 0x04000c0cu);  // bytes 2,3: p2.b0, p3.b0
+  return lo | hi;
 }
 
+// smoothing factor usable by the multiply path: 1/s is a normal float
+__device__ __forceinline__ bool smooth_ok(float s) {
+  const float a = fabsf(s);
+  return a >= 1.1754943508222875e-38f && a < 8.507059173023462e37f;
+}
+
+// ---------------------------------------------------------------------------
+// Kernel 1. A workgroup owns 16 rows and walks K in rounds of NW groups:
+// in round r wave w quantizes group r * NW + w. Each round's low-rank operand
+// slice (proj_down^T, NW * 64 columns) and smoothing factors are staged
+// once per workgroup into a double-buffered LDS area by all threads, so the
+// waves' registers only hold their own activation prefetch ring (PF rounds
+// deep). Staging loads for round r+2 are issued in round r, into the second
+// of two register sets, and written to LDS at the end of round r+1; they are
+// issued before the activation loads of round r+PF, and vector memory
+// operations complete in order, so waiting for the staging never waits for
+// activations still in flight.
+//
+// LDS per buffer: [NW][RB][2][64 lanes][8 bf16] operand slice, then
+// [NW * 64] reciprocals and [NW * 64] factors (fp32), then one flag word
+// holding the last round whose factors the multiply path cannot use.
+// ---------------------------------------------------------------------------
 template <int RB, int NW>
+struct QuantLds {
+  static constexpr int kOpBytes = NW * RB * 2 * 64 * 16;
+  static constexpr int kBufBytes = kOpBytes + NW * 64 * 4 * 2 + 16;
+  static constexpr int kChunks = (NW * RB * 2 * 64) / (NW * 64);  // 16-byte operand loads per thread per round
+};
+
+template <int RB, int NW, int PF>
 __global__ __launch_bounds__(NW * 64) void svdq_quant_int4_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, const uint16_t* __restrict__ smooth,
     const float* __restrict__ s2p, const uint16_t* __restrict__ pdt, uint8_t* __restrict__ q,
     uint16_t* __restrict__ sc, uint16_t* __restrict__ la, int M, int K) {
-  extern __shared__ float lds[];  // [K] smoothing reciprocals (if smooth), then [NW][RB][64][4] la partials
+  using L = QuantLds<RB, NW>;
+  constexpr int NCH = RB > 0 ? L::kChunks : 1;
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int i = lane & 15, kq = lane >> 4;
   const int row0 = blockIdx.x * 16;
   const int row = row0 + i;
   const int G = K >> 6;
-  float* rs = lds;
-  float* lap = lds + (smooth ? K : 0);
+  const int rounds = (G + NW - 1) / NW;
 
-  // buffers: every access is unconditional; rows >= M read 0 / store nothing
+  // buffers: every access is unconditional; rows >= M and groups >= G read 0 / store nothing
   const rsrc_t xbuf = make_rsrc(x, (uint32_t)(((int64_t)(M - 1) * ldx + K) * 2));
   const rsrc_t qbuf = make_rsrc(q, (uint32_t)((int64_t)M * (K >> 1)));
   const rsrc_t sbuf = make_rsrc(sc, (uint32_t)((int64_t)M * G * 2));
   const rsrc_t pbuf = make_rsrc(pdt, (uint32_t)(RB * 16 * K * 2));
-  const uint32_t xrow = (uint32_t)((int64_t)row * ldx * 2);
-  const uint32_t qrow = (uint32_t)((int64_t)row * (K >> 1));
+  const rsrc_t smbuf = make_rsrc(smooth, smooth ? (uint32_t)(K * 2) : 0u);
+  const uint32_t xrow = (uint32_t)((int64_t)row * ldx * 2) + (uint32_t)(kq * 16);
+  const uint32_t qrow = (uint32_t)((int64_t)row * (K >> 1)) + (uint32_t)(kq * 4);
   const uint32_t srow = kq == 0 ? (uint32_t)((int64_t)row * G * 2) : kOOB;
-  const uint32_t prow = (uint32_t)(i * K * 2);
 
-  bool smooth_fast = true;
-  if (smooth) {
-    int bad = 0;
-    for (int k = tid; k < K; k += NW * 64) {
-      const float sv = bf16_to_f32(smooth[k]);
-      const float a = fabsf(sv);
-      bad |= !(a >= 1.1754943508222875e-38f && a <= 3.4028234663852886e38f);
-      rs[k] = 1.0f / sv;
-    }
-    smooth_fast = !__syncthreads_or(bad);
+  // staging roles: operand chunk c = tid + j * NW * 64 -> (slot, rb, half, lane c % 64)
+  uint32_t poff[NCH];
+  int pslot[NCH];
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) {
+    const int c = tid + j * NW * 64;
+    const int cl = c & 63, half = (c >> 6) & 1, rb = (c >> 7) % (RB > 0 ? RB : 1);
+    pslot[j] = (c >> 7) / (RB > 0 ? RB : 1);
+    poff[j] = (uint32_t)(((rb * 16 + (cl & 15)) * K + half * 32 + (cl >> 4) * 8) * 2);
   }
+  // smoothing: threads 0 .. NW*32-1 stage two factors each
+  const bool sm_role = smooth && tid < NW * 32;
+
+  auto stage_load = [&](v4i* pv, uint32_t& sv, int r) {
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const int g = r * NW + pslot[j];
+      pv[j] = RB > 0 ? buf_load16(pbuf, g < G ? poff[j] + (uint32_t)(g * 128) : kOOB) : (v4i){0, 0, 0, 0};
+    }
+    const int k = r * NW * 64 + tid * 2;
+    sv = sm_role ? buf_load4(smbuf, k < K ? (uint32_t)(k * 2) : kOOB) : 0u;
+  };
+  // writes the staged round r into LDS buffer b; a factor the multiply path
+  // cannot use marks the buffer's flag word with r (stale marks hold older
+  // rounds, so the flag never needs clearing)
+  auto stage_store = [&](const v4i* pv, uint32_t sv, int r, int b) {
+    uint8_t* base = lds + b * L::kBufBytes;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j)
+      if (RB > 0) *(v4i*)(base + (tid + j * NW * 64) * 16) = pv[j];
+    if (sm_role) {
+      const float s0 = bf16_lo(sv), s1 = bf16_hi(sv);
+      const int k = tid * 2;
+      float* rs = (float*)(base + L::kOpBytes);
+      float* fs = rs + NW * 64;
+      rs[k] = 1.0f / s0;
+      rs[k + 1] = 1.0f / s1;
+      fs[k] = s0;
+      fs[k + 1] = s1;
+      const bool live = (r * NW * 64 + k < K);  // factors past K are padding
+      if (live && (!smooth_ok(s0) || !smooth_ok(s1))) *(int*)(fs + NW * 64) = r;
+    }
+  };
+  auto round_bad = [&](int r, int b) -> bool {
+    return *(const int*)(lds + b * L::kBufBytes + L::kOpBytes + NW * 64 * 8) == r;
+  };
+
   const float s2 = s2p ? *s2p : 1.0f;
   const bool s2_one = (s2 == 1.0f);
   const float den7 = 7.0f * s2;
 
-  const int gpw = (G + NW - 1) / NW;
-  const int g0 = wave * gpw;
-  const int g1 = min(G, g0 + gpw);
+  // prologue: stage round 0 (and issue round 1), prime the activation ring with rounds 0 .. PF-1
+  v4i pv[2][NCH];
+  uint32_t sv[2];
+  stage_load(pv[0], sv[0], 0);
+  stage_load(pv[1], sv[1], 1);
+  v4i xa[PF], xb[PF];
+#pragma unroll
+  for (int j = 0; j < PF; ++j) {
+    const int g = j * NW + wave;
+    const uint32_t off = g < G ? xrow + (uint32_t)(g * 128) : kOOB;
+    xa[j] = buf_load16(xbuf, off);
+    xb[j] = buf_load16(xbuf, g < G ? off + 64 : kOOB);
+  }
+  if (tid < 2) *(int*)(lds + tid * L::kBufBytes + L::kOpBytes + NW * 64 * 8) = -1;
+  __syncthreads();
+  stage_store(pv[0], sv[0], 0, 0);
+  __syncthreads();
 
   v4f acc[RB > 0 ? RB : 1];
 #pragma unroll
   for (int rb = 0; rb < (RB > 0 ? RB : 1); ++rb) acc[rb] = (v4f){0.f, 0.f, 0.f, 0.f};
 
-  // One prefetch ring of depth PF for both the activations and the low-rank
-  // operands: every group's loads are issued PF groups before it is used, so
-  // a wave's chain of groups pays the memory latency once, not per group.
-  constexpr int PF = 4;
-  constexpr int RBX = RB > 0 ? RB : 1;
-  v4i xa[PF], xb[PF], ba[PF][RBX], bb[PF][RBX];
-#pragma unroll
-  for (int j = 0; j < PF; ++j) {
-    const uint32_t off = xrow + (uint32_t)((g0 + j) * 128 + kq * 16);
-    xa[j] = buf_load16(xbuf, off);
-    xb[j] = buf_load16(xbuf, off + 64);
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
-      const uint32_t po = prow + (uint32_t)(rb * 16 * K * 2 + (g0 + j) * 128 + kq * 16);
-      ba[j][rb] = buf_load16(pbuf, po);
-      bb[j][rb] = buf_load16(pbuf, po + 64);
-    }
-  }
-
-  for (int gb = g0; gb < g1; gb += PF) {
+  static_assert(PF % 2 == 0, "the staging register set alternates with the round");
+  for (int rr = 0; rr < rounds; rr += PF) {
 #pragma unroll
     for (int j = 0; j < PF; ++j) {
-      const int g = gb + j;
-      if (g >= g1) break;
-      const int k0 = g * 64 + kq * 8;
+      const int r = rr + j;
+      const int b = r & 1;
+      // staging loads for round r+2 (set r & 1 was published at the end of
+      // round r-1), then the activation loads for round r+PF
+      stage_load(pv[j & 1], sv[j & 1], r + 2);
       const v4i ca = xa[j], cb = xb[j];
+      {
+        const int gn = (r + PF) * NW + wave;
+        const uint32_t off = gn < G ? xrow + (uint32_t)(gn * 128) : kOOB;
+        xa[j] = buf_load16(xbuf, off);
+        xb[j] = buf_load16(xbuf, gn < G ? off + 64 : kOOB);
+      }
+      const int g = r * NW + wave;
+      const bool valid = g < G;
+      const uint8_t* base = lds + b * L::kBufBytes;
+      const bool bad = smooth && round_bad(r, b);
 
-      // xs as packed bf16 words (8 per lane) and as floats
+      // xs as packed bf16 words (8 per lane)
       uint32_t w[8];
-      if (smooth) {
-        float v[16];
-        unpack8_bf16(ca, v);
-        unpack8_bf16(cb, v + 8);
-        if (smooth_fast) {
-          float r[16];
-          *(v4f*)(r) = *(const v4f*)(rs + k0);
-          *(v4f*)(r + 4) = *(const v4f*)(rs + k0 + 4);
-          *(v4f*)(r + 8) = *(const v4f*)(rs + k0 + 32);
-          *(v4f*)(r + 12) = *(const v4f*)(rs + k0 + 36);
-#pragma unroll
-          for (int t = 0; t < 16; ++t) v[t] *= r[t];
-        } else {
-          float sm[16];
-          unpack8_bf16(*(const v4i*)(smooth + k0), sm);
-          unpack8_bf16(*(const v4i*)(smooth + k0 + 32), sm + 8);
-#pragma unroll
-          for (int t = 0; t < 16; ++t) v[t] /= sm[t];
-        }
-#pragma unroll
-        for (int t = 0; t < 8; ++t)
-          w[t] = __builtin_bit_cast(uint32_t, __builtin_convertvector((v2f){v[2 * t], v[2 * t + 1]}, v2bf));
-      } else {
+      if (!smooth) {
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
           w[t] = (uint32_t)ca[t];
           w[4 + t] = (uint32_t)cb[t];
         }
+      } else {
+        float v[16], f[16];
+        unpack8_bf16(ca, v);
+        unpack8_bf16(cb, v + 8);
+        // bad == 0: multiply by RN(1/s), bit-identical to dividing (|x*r - x/s| <= 2^-23 |x/s|,
+        // while x/s is 2^-18 or more (relative) from every bf16 rounding tie); else divide.
+        const float* src = (const float*)(base + L::kOpBytes) + (bad ? NW * 64 : 0) + wave * 64 + kq * 8;
+        *(v4f*)(f) = *(const v4f*)(src);
+        *(v4f*)(f + 4) = *(const v4f*)(src + 4);
+        *(v4f*)(f + 8) = *(const v4f*)(src + 32);
+        *(v4f*)(f + 12) = *(const v4f*)(src + 36);
+        if (!bad) {
+#pragma unroll
+          for (int t = 0; t < 16; ++t) v[t] *= f[t];
+        } else {
+#pragma unroll
+          for (int t = 0; t < 16; ++t) v[t] /= f[t];
+        }
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+          w[t] = __builtin_bit_cast(uint32_t, __builtin_convertvector((v2f){v[2 * t], v[2 * t + 1]}, v2bf));
       }
       // group absmax on the bf16 bit patterns (|x| orders like its bits)
       v2u16 mx = {0, 0};
@@ -195,7 +264,7 @@ __global__ __launch_bounds__(NW * 64) void svdq_quant_int4_kernel(
       const float amax = __uint_as_float(mb << 16);
 
       float scl = amax / den7;
-      const bool fast = s2_one && scl >= kFp16MinNormal && scl < kFp16Max;
+      const bool fast = !valid || (s2_one && scl >= kFp16MinNormal && scl < kFp16Max);
       scl = fminf(fmaxf(scl, kScaleMin), kFp16Max);
       const uint16_t sh = f32_to_f16_bits(scl);
       const float d = f16_bits_to_f32(sh) * s2;
@@ -207,7 +276,8 @@ __global__ __launch_bounds__(NW * 64) void svdq_quant_int4_kernel(
         v[2 * t + 1] = bf16_hi(w[t]);
       }
       uint32_t w0, w1;
-      if (fast) {
+      // wave-uniform choice; neither side touches memory
+      if (__builtin_amdgcn_ballot_w64(!fast) == 0) {
         const float rd = __builtin_amdgcn_rcpf(d);
         uint32_t h[16];
 #pragma unroll
@@ -222,33 +292,31 @@ __global__ __launch_bounds__(NW * 64) void svdq_quant_int4_kernel(
           w1 |= int4_code_exact(v[8 + t], d) << (4 * t);
         }
       }
-      buf_store4(w0, qbuf, qrow + (uint32_t)(k0 >> 1));
-      buf_store4(w1, qbuf, qrow + (uint32_t)((k0 + 32) >> 1));
-      buf_store2(sh, sbuf, srow + (uint32_t)(g * 2));
+      const uint32_t qo = valid ? qrow + (uint32_t)(g * 32) : kOOB;
+      buf_store4(w0, qbuf, qo);
+      buf_store4(w1, qbuf, valid ? qo + 16 : kOOB);
+      buf_store2(sh, sbuf, valid ? srow + (uint32_t)(g * 2) : kOOB);
 
+      // la += x[:, group] @ proj_down[group, :] (raw activations)
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
-        acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, ca),
-                                                          __builtin_bit_cast(v8bf, ba[j][rb]), acc[rb], 0, 0, 0);
-        acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, cb),
-                                                          __builtin_bit_cast(v8bf, bb[j][rb]), acc[rb], 0, 0, 0);
+        const uint8_t* op = base + ((wave * RB + rb) * 2) * 1024 + lane * 16;
+        const v4i b0 = *(const v4i*)(op);
+        const v4i b1 = *(const v4i*)(op + 1024);
+        acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, ca), __builtin_bit_cast(v8bf, b0),
+                                                          acc[rb], 0, 0, 0);
+        acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, cb), __builtin_bit_cast(v8bf, b1),
+                                                          acc[rb], 0, 0, 0);
       }
-      {  // refill this ring slot with group g + PF
-        const uint32_t off = xrow + (uint32_t)((g + PF) * 128 + kq * 16);
-        xa[j] = buf_load16(xbuf, off);
-        xb[j] = buf_load16(xbuf, off + 64);
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb) {
-          const uint32_t po = prow + (uint32_t)(rb * 16 * K * 2 + (g + PF) * 128 + kq * 16);
-          ba[j][rb] = buf_load16(pbuf, po);
-          bb[j][rb] = buf_load16(pbuf, po + 64);
-        }
-      }
+      // publish round r+1 (its buffer was last read in round r-1, before the previous barrier)
+      stage_store(pv[(j + 1) & 1], sv[(j + 1) & 1], r + 1, b ^ 1);
+      __syncthreads();
     }
   }
 
   if (RB > 0) {
-    // sum the NW partial la blocks through LDS; wave 0 writes bf16
+    // sum the NW partial la blocks through LDS (buffer 0 is free after the last barrier); wave 0 writes bf16
+    float* lap = (float*)lds;
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) *(v4f*)(lap + ((wave * RB + rb) * 64 + lane) * 4) = acc[rb];
     __syncthreads();
@@ -362,41 +430,44 @@ extern "C" int gwa_svdq_quant_int4(const void* x, int64_t ldx, const void* smoot
   uint16_t* lp = (uint16_t*)la;
   const int m = (int)M, k = (int)K;
   const int rb = (int)(R / 16);
-  // K is split over NW waves per 16-row block: wide splits when there are few
-  // row blocks, so that small-M calls still put enough waves on the GPU.
+  // K is walked in rounds of NW groups per 16-row block: more waves when
+  // there are few row blocks, so that small-M calls still fill the GPU, as
+  // long as the double-buffered operand staging fits in LDS.
   const int64_t blocks = (M + 15) / 16;
   int nw = blocks >= 512 ? 4 : (blocks >= 128 ? 8 : 16);
-  // 16-wave blocks cap VGPRs at 128 and 8-wave blocks at 256: the low-rank
-  // operand rings of the larger ranks need the narrower splits
-  if (rb >= 2 && nw > 8) nw = 8;
-  if (rb >= 8) nw = 4;
-  const size_t lds = (sm ? (size_t)K * 4 : 0) + (size_t)nw * rb * 1024;
-  GWA_REQUIRE(lds <= 160 * 1024, "svdq_quant_int4: K=%lld needs too much LDS", (long long)K);
+  auto lds_bytes = [&](int w) { return (size_t)2 * ((size_t)w * rb * 2048 + (size_t)w * 512); };
+  while (nw > 4 && lds_bytes(nw) > 160 * 1024) nw >>= 1;
+  const size_t lds = lds_bytes(nw);
+  GWA_REQUIRE(lds <= 160 * 1024, "svdq_quant_int4: rank %lld needs too much LDS", (long long)R);
+  // activation prefetch depth (even: the staging registers alternate by round)
+  const int64_t rounds = (K / 64 + nw - 1) / nw;
+  const int pf = (rounds % 4 == 0) ? 4 : 2;
   const dim3 grid((unsigned)blocks);
-#define GWA_QUANT_LAUNCH(RBV, NWV)                                                                  \
-  hipLaunchKernelGGL((svdq_quant_int4_kernel<RBV, NWV>), grid, dim3(NWV * 64), lds, s, xp, ldx, sm, s2, pd, q, \
-                     sc, lp, m, k)
-#define GWA_QUANT_RB(RBV)                      \
-  case RBV:                                    \
-    if (nw == 16) GWA_QUANT_LAUNCH(RBV, 16);   \
-    else if (nw == 8) GWA_QUANT_LAUNCH(RBV, 8); \
-    else GWA_QUANT_LAUNCH(RBV, 4);             \
-    break;
-#define GWA_QUANT_RB_WIDE(RBV)                 \
-  case RBV:                                    \
-    if (nw == 8) GWA_QUANT_LAUNCH(RBV, 8);     \
-    else GWA_QUANT_LAUNCH(RBV, 4);             \
+#define GWA_QUANT_LAUNCH(RBV, NWV, PFV)                                                                  \
+  hipLaunchKernelGGL((svdq_quant_int4_kernel<RBV, NWV, PFV>), grid, dim3(NWV * 64), lds, s, xp, ldx, sm, s2, pd, \
+                     q, sc, lp, m, k)
+#define GWA_QUANT_NW(RBV, NWV)                                   \
+  if (pf == 4) GWA_QUANT_LAUNCH(RBV, NWV, 4);                    \
+  else GWA_QUANT_LAUNCH(RBV, NWV, 2);
+#define GWA_QUANT_RB(RBV)                    \
+  case RBV:                                  \
+    if (nw == 16) { GWA_QUANT_NW(RBV, 16) }  \
+    else if (nw == 8) { GWA_QUANT_NW(RBV, 8) } \
+    else { GWA_QUANT_NW(RBV, 4) }            \
     break;
   switch (rb) {
     GWA_QUANT_RB(0)
     GWA_QUANT_RB(1)
-    GWA_QUANT_RB_WIDE(2)
-    GWA_QUANT_RB_WIDE(4)
-    case 8: GWA_QUANT_LAUNCH(8, 4); break;
+    GWA_QUANT_RB(2)
+    case 4:
+      if (nw == 8) { GWA_QUANT_NW(4, 8) }
+      else { GWA_QUANT_NW(4, 4) }
+      break;
+    case 8: GWA_QUANT_NW(8, 4) break;
     default: return gwa_set_error(GWA_ERR_INVALID, "svdq_quant_int4: rank %lld not in {0,16,32,64,128}", (long long)R);
   }
+#undef GWA_QUANT_NW
 #undef GWA_QUANT_RB
-#undef GWA_QUANT_RB_WIDE
 #undef GWA_QUANT_LAUNCH
   return gwa_check_launch("svdq_quant_int4");
 }

@@ -4,7 +4,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include "../../include/gen_worker_amd.h"
+#include "gen_worker_amd.h"
 
 // ---------------------------------------------------------------------------
 // vector types used as MFMA operands

@@ -45,9 +45,9 @@ _SIGNATURES: dict[str, tuple] = {
     "gwa_svdq_gemm_w4a4": (_vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _int, _int,
                            _i64, _i64, _i64, _vp),
     "gwa_svdq_group_psums": (_vp, _vp, _vp, _i64, _i64, _i64, _vp),
-    "gwa_svdq_pack_weight_int4": (_vp, _vp, _vp, _vp, _i64, _i64, _vp),
-    "gwa_svdq_gemm_w4a4_packed": (_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _int, _int,
-                                  _i64, _i64, _i64, _vp),
+    "gwa_svdq_pack_weight_int4": (_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp),
+    "gwa_svdq_gemm_w4a4_packed": (_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _int,
+                                  _int, _i64, _i64, _i64, _vp),
     "gwa_svdq_group_psums_packed": (_vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp),
     "gwa_svdq_epilogue_lora": (_vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _i64, _i64, _vp),
     "gwa_w8a8_quant_int8": (_vp, _i64, _vp, _vp, _i64, _i64, _vp),

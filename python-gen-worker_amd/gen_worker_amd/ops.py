@@ -205,33 +205,39 @@ def _(qa, sa, weight, wscales, s2, second, la, up, bias, out_dtype, gelu):
     return qa.new_empty(int(qa.shape[0]), int(weight.shape[0]), dtype=out_dtype)
 
 
-def _packed_impl(qa: Tensor, sa: Tensor, weight_packed: Tensor, wscales: Tensor, wsum: Tensor,
-                 s2: Optional[Tensor], second: Optional[Tensor], la: Optional[Tensor], up: Optional[Tensor],
-                 bias: Optional[Tensor], out_dtype: torch.dtype, gelu: bool) -> Tensor:
+def _packed_impl(qa: Tensor, sa: Tensor, weight_packed: Tensor, wscales_packed: Tensor, wcorr: Tensor,
+                 escale: Tensor, s2: Optional[Tensor], second: Optional[Tensor], la: Optional[Tensor],
+                 up: Optional[Tensor], bias: Optional[Tensor], out_dtype: torch.dtype, gelu: bool) -> Tensor:
     name = "svdq_w4a4_linear_packed"
     s2 = _scalar_f32(name, s2)
     if second is not None and second.dtype != torch.float32:
         second = second.float().contiguous()
     _check_dtype(name, qa, torch.uint8, what="qa")
     _check_dtype(name, weight_packed, torch.uint8, what="weight_packed")
-    _check_dtype(name, wsum, torch.int16, what="weight sums")
     _check_dtype(name, sa, torch.float16, what="sa")
-    _check_dtype(name, wscales, torch.float16, what="weight scales")
+    _check_dtype(name, wscales_packed, torch.float16, what="packed weight scales")
+    _check_dtype(name, wcorr, torch.float16, what="weight correction pairs")
+    _check_dtype(name, escale, torch.float32, what="row exponent scales")
     _check_dtype(name, la, torch.bfloat16, what="la")
     _check_dtype(name, up, torch.bfloat16, what="up")
     _check_dtype(name, bias, torch.bfloat16, what="bias")
-    _check_cuda(name, qa=qa, sa=sa, weight_packed=weight_packed, wscales=wscales, wsum=wsum, s2=s2, second=second,
-                la=la, up=up, bias=bias)
+    _check_cuda(name, qa=qa, sa=sa, weight_packed=weight_packed, wscales_packed=wscales_packed, wcorr=wcorr,
+                escale=escale, s2=s2, second=second, la=la, up=up, bias=bias)
     if out_dtype not in (torch.bfloat16, torch.float16):
         raise SvdqOpError(f"{name}: out_dtype {out_dtype} not bf16/fp16")
     m, kh = int(qa.shape[0]), int(qa.shape[1])
     k = 2 * kh
     n = int(weight_packed.shape[0])
-    if tuple(weight_packed.shape) != (n, kh) or tuple(wsum.shape) != (n, k // GROUP):
-        raise SvdqOpError(f"{name}: packed weight {tuple(weight_packed.shape)} / sums {tuple(wsum.shape)} do not "
-                          f"match [N, K/2={kh}] / [N, K/64]")
-    if tuple(sa.shape) != (m, k // GROUP) or tuple(wscales.shape) != (n, k // GROUP):
-        raise SvdqOpError(f"{name}: scales {tuple(sa.shape)} / {tuple(wscales.shape)} do not match")
+    g = k // GROUP
+    if k % 256:
+        raise SvdqOpError(f"{name}: K={k} is not a multiple of 256 (use svdq_w4a4_linear)")
+    if (tuple(weight_packed.shape) != (n, kh) or tuple(wscales_packed.shape) != (n, g)
+            or tuple(wcorr.shape) != (n, g // 4, 8) or tuple(escale.shape) != (n,)):
+        raise SvdqOpError(f"{name}: prepacked weight {tuple(weight_packed.shape)} / scales "
+                          f"{tuple(wscales_packed.shape)} / corr {tuple(wcorr.shape)} / escale {tuple(escale.shape)} "
+                          f"do not match N={n}, K={k}")
+    if tuple(sa.shape) != (m, g):
+        raise SvdqOpError(f"{name}: activation scales {tuple(sa.shape)} do not match [M={m}, K/64={g}]")
     if (la is None) != (up is None):
         raise SvdqOpError(f"{name}: la and up must both be given or both be None")
     rank = 0
@@ -243,49 +249,65 @@ def _packed_impl(qa: Tensor, sa: Tensor, weight_packed: Tensor, wscales: Tensor,
         raise SvdqOpError(f"{name}: bias has {bias.numel()} values for N={n}")
     sec_n = 0 if second is None else int(second.numel())
     out = torch.empty(m, n, dtype=out_dtype, device=qa.device)
-    nat.call("gwa_svdq_gemm_w4a4_packed", nat.ptr(qa), nat.ptr(sa), nat.ptr(weight_packed), nat.ptr(wscales),
-             nat.ptr(wsum), nat.ptr(s2), nat.ptr(second), sec_n, nat.ptr(la), nat.ptr(up), rank, nat.ptr(bias),
-             nat.ptr(out), _dt_code(out_dtype), nat.EPI_GELU_TANH if gelu else 0, m, n, k, nat.stream_of(qa))
+    nat.call("gwa_svdq_gemm_w4a4_packed", nat.ptr(qa), nat.ptr(sa), nat.ptr(weight_packed), nat.ptr(wscales_packed),
+             nat.ptr(wcorr), nat.ptr(escale), nat.ptr(s2), nat.ptr(second), sec_n, nat.ptr(la), nat.ptr(up), rank,
+             nat.ptr(bias), nat.ptr(out), _dt_code(out_dtype), nat.EPI_GELU_TANH if gelu else 0, m, n, k,
+             nat.stream_of(qa))
     return out
 
 
 @torch.library.custom_op("cozy_gen_worker::svdq_w4a4_linear_packed", mutates_args=())
-def svdq_w4a4_linear_packed(qa: Tensor, sa: Tensor, weight_packed: Tensor, wscales: Tensor, wsum: Tensor,
-                            s2: Optional[Tensor], second: Optional[Tensor], la: Optional[Tensor],
+def svdq_w4a4_linear_packed(qa: Tensor, sa: Tensor, weight_packed: Tensor, wscales_packed: Tensor, wcorr: Tensor,
+                            escale: Tensor, s2: Optional[Tensor], second: Optional[Tensor], la: Optional[Tensor],
                             up: Optional[Tensor], bias: Optional[Tensor], out_dtype: torch.dtype,
                             gelu: bool) -> Tensor:
-    """Fast W4A4 GEMM + fused epilogue on prepacked weights (``svdq_pack_weight``)."""
-    return _packed_impl(qa, sa, weight_packed, wscales, wsum, s2, second, la, up, bias, out_dtype, gelu)
+    """Fast W4A4 GEMM + fused epilogue on prepacked weights (the outputs of ``svdq_pack_weight``)."""
+    return _packed_impl(qa, sa, weight_packed, wscales_packed, wcorr, escale, s2, second, la, up, bias, out_dtype,
+                        gelu)
 
 
 @svdq_w4a4_linear_packed.register_fake
-def _(qa, sa, weight_packed, wscales, wsum, s2, second, la, up, bias, out_dtype, gelu):
+def _(qa, sa, weight_packed, wscales_packed, wcorr, escale, s2, second, la, up, bias, out_dtype, gelu):
     return qa.new_empty(int(qa.shape[0]), int(weight_packed.shape[0]), dtype=out_dtype)
 
 
 @torch.library.custom_op("cozy_gen_worker::svdq_pack_weight", mutates_args=())
-def svdq_pack_weight(weight: Tensor) -> tuple[Tensor, Tensor, Tensor]:
-    """Prepack logical int4 weights [N, K/2] -> (packed [N, K/2], int16 sums [N, K/64], int32 count of -8 codes)."""
+def svdq_pack_weight(weight: Tensor, wscales: Tensor) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """Prepack logical int4 weights [N, K/2] with their fp16 group scales [N, K/64] for the fast GEMM.
+
+    Returns ``(packed [N, K/2] uint8, sums [N, K/64] int16, count [1] int32 of -8 codes,
+    wscales_packed [N, K/64] fp16, wcorr [N, ceil(K/256), 8] fp16, escale [N] fp32)``."""
     name = "svdq_pack_weight"
     _check_dtype(name, weight, torch.uint8, what="weight")
-    _check_cuda(name, weight=weight)
+    _check_dtype(name, wscales, torch.float16, what="wscales")
+    _check_cuda(name, weight=weight, wscales=wscales)
     n, kh = int(weight.shape[0]), int(weight.shape[1])
     k = 2 * kh
     if k % GROUP:
         raise SvdqOpError(f"{name}: K={k} is not a multiple of {GROUP}")
+    g = k // GROUP
+    if tuple(wscales.shape) != (n, g):
+        raise SvdqOpError(f"{name}: wscales {tuple(wscales.shape)} do not match [N={n}, K/64={g}]")
+    weight = weight.contiguous()
+    wscales = wscales.contiguous()
     packed = torch.empty_like(weight)
-    wsum = torch.empty(n, k // GROUP, dtype=torch.int16, device=weight.device)
+    wsum = torch.empty(n, g, dtype=torch.int16, device=weight.device)
     count = torch.zeros(1, dtype=torch.int32, device=weight.device)
-    nat.call("gwa_svdq_pack_weight_int4", nat.ptr(weight), nat.ptr(packed), nat.ptr(wsum), nat.ptr(count), n, k,
-             nat.stream_of(weight))
-    return packed, wsum, count
+    swp = torch.empty(n, g, dtype=torch.float16, device=weight.device)
+    wcorr = torch.empty(n, (g + 3) // 4, 8, dtype=torch.float16, device=weight.device)
+    escale = torch.empty(n, dtype=torch.float32, device=weight.device)
+    nat.call("gwa_svdq_pack_weight_int4", nat.ptr(weight), nat.ptr(wscales), nat.ptr(packed), nat.ptr(wsum),
+             nat.ptr(swp), nat.ptr(wcorr), nat.ptr(escale), nat.ptr(count), n, k, nat.stream_of(weight))
+    return packed, wsum, count, swp, wcorr, escale
 
 
 @svdq_pack_weight.register_fake
-def _(weight):
+def _(weight, wscales):
     n, kh = int(weight.shape[0]), int(weight.shape[1])
-    return (torch.empty_like(weight), weight.new_empty(n, (2 * kh) // GROUP, dtype=torch.int16),
-            weight.new_empty(1, dtype=torch.int32))
+    g = (2 * kh) // GROUP
+    return (torch.empty_like(weight), weight.new_empty(n, g, dtype=torch.int16),
+            weight.new_empty(1, dtype=torch.int32), weight.new_empty(n, g, dtype=torch.float16),
+            weight.new_empty(n, (g + 3) // 4, 8, dtype=torch.float16), weight.new_empty(n, dtype=torch.float32))
 
 
 @torch.library.custom_op("cozy_gen_worker::svdq_group_psums_packed", mutates_args=())

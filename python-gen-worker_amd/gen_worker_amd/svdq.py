@@ -167,6 +167,9 @@ class SvdqW4A4Linear(nn.Module):
         # resident fast-path layout (derived from ``weight`` by refresh_derived)
         self.register_buffer("weight_packed", None, persistent=False)
         self.register_buffer("weight_sums", None, persistent=False)
+        self.register_buffer("weight_scale_packed", None, persistent=False)
+        self.register_buffer("weight_corr", None, persistent=False)
+        self.register_buffer("weight_escale", None, persistent=False)
 
     def refresh_derived(self) -> None:
         """Recompute the derived buffers after ``weight`` / ``proj_down`` change: the transposed
@@ -175,15 +178,24 @@ class SvdqW4A4Linear(nn.Module):
         if self.rank:
             self.proj_down_t = self.proj_down.t().contiguous()
         self.weight_packed = self.weight_sums = None
-        if (self.weight.is_cuda and self.in_features % 128 == 0):
-            packed, sums, n_neg8 = torch.ops.cozy_gen_worker.svdq_pack_weight(self.weight)
+        self.weight_scale_packed = self.weight_corr = self.weight_escale = None
+        if self.weight.is_cuda and self.in_features % 256 == 0:
+            packed, sums, n_neg8, swp, corr, esc = torch.ops.cozy_gen_worker.svdq_pack_weight(
+                self.weight, self.weight_scale)
             if int(n_neg8.item()) == 0:
                 self.weight_packed, self.weight_sums = packed, sums
+                self.weight_scale_packed, self.weight_corr, self.weight_escale = swp, corr, esc
 
     def _load_from_state_dict(self, *args: Any, **kwargs: Any) -> None:  # noqa: D401
         super()._load_from_state_dict(*args, **kwargs)
         if self.weight.device.type != "meta":
             self.refresh_derived()
+
+    def packed_weight(self) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+        """The prepacked fast-lane weight: ``(weight_packed, weight_scale_packed, weight_corr, weight_escale)``."""
+        if self.weight_packed is None:
+            raise SvdqFusedError("this layer has no prepacked weight (lane is 'general')")
+        return self.weight_packed, self.weight_scale_packed, self.weight_corr, self.weight_escale
 
     @property
     def lane(self) -> str:
@@ -205,8 +217,7 @@ class SvdqW4A4Linear(nn.Module):
         gelu = self.activation == "gelu_tanh"
         if self.weight_packed is not None:
             y = torch.ops.cozy_gen_worker.svdq_w4a4_linear_packed(
-                qa, sa, self.weight_packed, self.weight_scale, self.weight_sums, None, self.second, la,
-                self.proj_up, self.bias, out_dtype, gelu)
+                qa, sa, *self.packed_weight(), None, self.second, la, self.proj_up, self.bias, out_dtype, gelu)
         else:
             y = torch.ops.cozy_gen_worker.svdq_w4a4_linear(
                 qa, sa, self.weight, self.weight_scale, None, self.second, la, self.proj_up,

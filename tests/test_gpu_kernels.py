@@ -194,11 +194,14 @@ def test_psums_seeded_extremes(m, n, k):
 
 
 def _w4a4_case(m, n, k, rank, seed, smooth=True, bias=True, second=None, gelu=False, out_dtype=torch.bfloat16,
-               s2=None, packed=False):
+               s2=None, packed=False, row_spread=False):
     g = np.random.default_rng(seed)
     x = _rand_act(m, k, seed=seed)
     sm = O.f32_to_bf16_bits(np.exp(g.uniform(np.log(0.25), np.log(4), k)).astype(np.float32)) if smooth else None
-    qw, sw = O.quantize_weight_int4((g.standard_normal((n, k)) * 0.02).astype(np.float32))
+    w = (g.standard_normal((n, k)) * 0.02).astype(np.float32)
+    if row_spread:   # weight rows (and so their group scales) spanning six orders of magnitude
+        w *= np.exp(g.uniform(np.log(1e-4), np.log(1e2), (n, 1))).astype(np.float32)
+    qw, sw = O.quantize_weight_int4(w)
     down = O.f32_to_bf16_bits((g.standard_normal((k, rank)) * 0.02).astype(np.float32)) if rank else None
     up = O.f32_to_bf16_bits((g.standard_normal((n, rank)) * 0.02).astype(np.float32)) if rank else None
     b = O.f32_to_bf16_bits((g.standard_normal(n) * 0.02).astype(np.float32)) if bias else None
@@ -218,9 +221,9 @@ def _w4a4_case(m, n, k, rank, seed, smooth=True, bias=True, second=None, gelu=Fa
     swd = from_bits(sw.view(np.uint16), torch.float16, DEV)
     bd = _dev16(b) if b is not None else None
     if packed:
-        wp, ws, n8 = torch.ops.cozy_gen_worker.svdq_pack_weight(wd)
+        wp, _, n8, swp, wc, esc = torch.ops.cozy_gen_worker.svdq_pack_weight(wd, swd)
         assert int(n8.item()) == 0
-        y = torch.ops.cozy_gen_worker.svdq_w4a4_linear_packed(qa, sa, wp, swd, ws, s2t, sec, la, upd, bd,
+        y = torch.ops.cozy_gen_worker.svdq_w4a4_linear_packed(qa, sa, wp, swp, wc, esc, s2t, sec, la, upd, bd,
                                                               out_dtype, gelu)
     else:
         y = torch.ops.cozy_gen_worker.svdq_w4a4_linear(qa, sa, wd, swd, s2t, sec, la, upd, bd, out_dtype, gelu)
@@ -283,7 +286,8 @@ def test_psums_packed_bit_exact(m, n, k):
     qa[0] = 0x88                                  # all -8 activations
     qw = _codes_no_neg8(g, (n, k))
     qw[0] = O.pack_int4(np.full((1, k), -7, np.int8))[0]   # extreme weights
-    wp, ws, n8 = torch.ops.cozy_gen_worker.svdq_pack_weight(torch.from_numpy(qw).to(DEV))
+    ones = torch.ones(n, k // 64, dtype=torch.float16, device=DEV)
+    wp, ws, n8, _, _, _ = torch.ops.cozy_gen_worker.svdq_pack_weight(torch.from_numpy(qw).to(DEV), ones)
     assert int(n8.item()) == 0
     assert np.array_equal(ws.cpu().numpy().astype(np.int64),
                           O.unpack_int4(qw).astype(np.int64).reshape(n, k // 64, 64).sum(-1))
@@ -297,13 +301,40 @@ def test_pack_counts_neg8():
     codes = g.integers(-7, 8, size=(32, 256)).astype(np.int8)
     codes[3, 5] = -8
     codes[17, 200] = -8
-    _, _, n8 = torch.ops.cozy_gen_worker.svdq_pack_weight(torch.from_numpy(O.pack_int4(codes)).to(DEV))
+    ones = torch.ones(32, 4, dtype=torch.float16, device=DEV)
+    n8 = torch.ops.cozy_gen_worker.svdq_pack_weight(torch.from_numpy(O.pack_int4(codes)).to(DEV), ones)[2]
     assert int(n8.item()) == 2
 
 
+def test_pack_scales_and_correction():
+    """sw' * escale reproduces sw exactly, escale is a power of two per row, and the correction
+    pairs hold -cw * sw' * 2^-9 to about 2^-22 (rows of very different scale magnitude)."""
+    g = np.random.default_rng(11)
+    n, k = 48, 1344                                          # 21 groups: padded to 24 in wcorr
+    codes = g.integers(-7, 8, size=(n, k)).astype(np.int8)
+    mag = np.exp(g.uniform(np.log(1e-4), np.log(1e2), (n, 1)))
+    sw = (mag * g.uniform(0.1, 1.0, (n, k // 64))).astype(np.float16)
+    sw[5, :] = np.float16(0)                                 # an all-zero row
+    wd = torch.from_numpy(O.pack_int4(codes)).to(DEV)
+    wp, ws, n8, swp, wc, esc = torch.ops.cozy_gen_worker.svdq_pack_weight(wd, torch.from_numpy(sw).to(DEV))
+    swp, wc, esc = swp.cpu().numpy(), wc.cpu().numpy().astype(np.float64), esc.cpu().numpy()
+    e = np.log2(esc)
+    assert np.array_equal(e, np.round(e)), "escale must be a power of two"
+    assert np.array_equal(swp.astype(np.float64) * esc[:, None], sw.astype(np.float64))
+    nz = sw.max(1) > 0
+    assert np.all(swp[nz].max(1) >= 2.0 ** 14) and np.all(swp[nz].max(1) < 2.0 ** 15)
+    cw = codes.astype(np.int64).reshape(n, k // 64, 64).sum(-1)
+    want = -(cw * swp.astype(np.float64)) / 512.0
+    got = np.zeros((n, 24))
+    got[:, :] = (wc[:, :, :4] + wc[:, :, 4:]).reshape(n, 24)
+    assert np.all(got[:, 21:] == 0)
+    err = np.abs(got[:, :21] - want)
+    assert np.all(err <= 2.0 ** -21 * np.abs(want).max(1, keepdims=True) + 1e-30)
+
+
 @pytest.mark.parametrize("m,n,k,rank", [
-    (1, 16, 128, 0), (77, 128, 384, 32), (256, 3072, 3072, 32), (333, 272, 512, 128), (130, 144, 256, 16),
-    (64, 256, 12288, 64), (300, 128, 15360, 32), (513, 400, 1024, 32),
+    (1, 16, 256, 0), (77, 128, 512, 32), (256, 3072, 3072, 32), (333, 272, 512, 128), (130, 144, 256, 16),
+    (64, 256, 12288, 64), (300, 128, 15360, 32), (513, 400, 1024, 32), (4097, 48, 768, 16),
 ])
 def test_w4a4_packed_seeded(m, n, k, rank):
     y, ref = _w4a4_case(m, n, k, rank, seed=m * 17 + n + k, packed=True)
@@ -314,7 +345,8 @@ def test_w4a4_packed_epilogue_variants():
     n = 256
     sec = np.linspace(0.5, 2.0, n).astype(np.float32)
     for kw, what in ((dict(second=sec), "second"), (dict(gelu=True), "gelu"), (dict(out_dtype=torch.float16), "f16"),
-                     (dict(smooth=False, bias=False), "bare"), (dict(s2=0.5), "s2")):
+                     (dict(smooth=False, bias=False), "bare"), (dict(s2=0.5), "s2"),
+                     (dict(row_spread=True, bias=False), "row scale spread")):
         y, ref = _w4a4_case(96, n, 512, 32 if what != "bare" else 0, seed=11, packed=True, **kw)
         check_output(y, ref, what=f"packed {what}")
 
