@@ -1,25 +1,36 @@
 """Benchmark of the SVDQuant W4A4 linear hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+    python bench.py --only {step,gemm,quant,copy} [--iters N]     (profiling driver)
 
 A step is one pass of the hot path over one batch of synthetic input: the
 config-1 SVDQuant W4A4 linear (M = 4096 image + 512 text tokens = 4608,
 K = N = 3072, rank 32, group 64, bf16 in/out): kernel 1 (smoothing + int4
 act-quant + x @ proj_down) then kernel 2 (W4A4 GEMM + low-rank/bias
-epilogue). Inputs are resident in HBM before the timed region. ``value`` is
-the linear's throughput in int-TOPS (2*M*N*K per step). The ``roofline``
-object covers the dominant kernel (the GEMM), timed with HIP events on the
-stream it runs on; ``cpu_baseline`` times the reference's CPU serving lane
-(dense fold + one bf16 Linear) on a bounded sample of the same workload.
-Prints ONE JSON line on stdout; progress goes to stderr.
+epilogue). Inputs are resident in HBM before the timed region. The K timed
+steps are captured once into a HIP graph and replayed, so host launch cost
+is not part of the figure; the eager (per-op Python dispatch) rate is
+reported beside it. ``value`` is the linear's throughput in int-TOPS
+(2*M*N*K per step).
+
+The ``roofline`` object covers the dominant kernel (the GEMM): its average
+launch duration comes from HIP events around a graph of K back-to-back GEMM
+launches on the stream they run on; ``traffic`` is the HBM bytes per launch
+measured with rocprofv3 FETCH_SIZE / WRITE_SIZE, scaled by the same
+counters' reading for a copy of known size (profiles/w4a4_gemm_c1_traffic.json).
+``cpu_baseline`` times the reference's CPU serving lane (dense fold + one
+bf16 Linear) on a bounded sample of the same workload. Prints ONE JSON line
+on stdout; progress goes to stderr.
+
+``--only`` runs one piece eagerly ``--iters`` times (after 3 warmups) and
+prints nothing on stdout: it is the command the committed rocprofv3
+summaries under profiles/ were taken with.
 """
 
 from __future__ import annotations
 
 import argparse
 import json
-import os
-import statistics
 import sys
 import time
 from pathlib import Path
@@ -31,10 +42,34 @@ sys.path.insert(0, str(ROOT))
 METRIC = "W4A4 linear TOPS (% int8 MFMA peak) at M=4608 K=N=3072; DiT step ms"
 INT8_PEAK_TOPS = 5000.0      # MI355X dense int8 MFMA, 5.0 POP/s
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, 8 TB/s
+COPY_BYTES = 64 << 20        # calibration copy for the traffic counters
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
+
+
+def graph_time_ms(torch, fn, reps: int) -> float:
+    """Average ms of ``fn`` from one replay of a HIP graph holding ``reps`` back-to-back calls,
+    timed with events on the stream the graph runs on."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            for _ in range(reps):
+                fn()
+    torch.cuda.synchronize()
+    g.replay()                                   # first replay: page-in, not timed
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    cur = torch.cuda.current_stream()
+    e0.record(cur)
+    g.replay()
+    e1.record(cur)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
 
 
 def main() -> int:
@@ -44,6 +79,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-rows", type=int, default=512, help="rows of the bounded CPU sample")
+    ap.add_argument("--only", choices=("step", "gemm", "quant", "copy"), default=None)
+    ap.add_argument("--iters", type=int, default=5)
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -70,52 +107,66 @@ def main() -> int:
     x = x_cpu.to(dev)
     assert mod.lane == "packed", "synthetic int4 weights are in [-7, 7]: the fast lane must be armed"
     ops = torch.ops.cozy_gen_worker
+    packed = mod.packed_weight()
 
-    def step(evs=None):
-        if evs is not None:
-            evs[0].record()
-        qa, sa, la = ops.svdq_quant_lora(x, mod.smooth_factor, None, mod.proj_down_t)
-        if evs is not None:
-            evs[1].record()
-        y = ops.svdq_w4a4_linear_packed(qa, sa, *mod.packed_weight(), None, mod.second, la, mod.proj_up, mod.bias,
-                                        torch.bfloat16, False)
-        if evs is not None:
-            evs[2].record()
-        return y
+    def quant():
+        return ops.svdq_quant_lora(x, mod.smooth_factor, None, mod.proj_down_t)
+
+    qa, sa, la = quant()
+
+    def gemm(qa=qa, sa=sa, la=la):
+        return ops.svdq_w4a4_linear_packed(qa, sa, *packed, None, mod.second, la, mod.proj_up, mod.bias,
+                                           torch.bfloat16, False)
+
+    def step():
+        q, s, l = quant()
+        return gemm(q, s, l)
+
+    if args.only is not None:
+        src = torch.empty(COPY_BYTES // 2, dtype=torch.bfloat16, device=dev) if args.only == "copy" else None
+        dst = torch.empty_like(src) if src is not None else None
+        fn = {"step": step, "gemm": gemm, "quant": quant, "copy": lambda: dst.copy_(src)}[args.only]
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        for _ in range(args.iters):
+            fn()
+        torch.cuda.synchronize()
+        log(f"bench: ran {args.only} x{args.iters}")
+        return 0
 
     log(f"bench: warmup {args.warmup}")
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
 
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
-    log(f"bench: timing {args.steps} steps")
+    # timed region: K steps captured in one graph, one replay, synchronize on both sides
+    log(f"bench: timing {args.steps} steps (graph)")
+    step_ms = graph_time_ms(torch, step, args.steps)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(args.steps):
-        step(evs[i])
+    for _ in range(args.steps):
+        step()
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    q_ms = [e[0].elapsed_time(e[1]) for e in evs]
-    g_ms = [e[1].elapsed_time(e[2]) for e in evs]
-    ms_per_step = wall * 1e3 / args.steps
+    eager_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    gemm_ms = graph_time_ms(torch, gemm, args.steps)
+    quant_ms = graph_time_ms(torch, quant, args.steps)
 
     int_ops = w4a4_int_ops(m, n, k)
-    value_tops = int_ops / (ms_per_step * 1e-3) / 1e12
-    gemm_ms = statistics.mean(g_ms)
-    quant_ms = statistics.mean(q_ms)
+    value_tops = int_ops / (step_ms * 1e-3) / 1e12
     gemm_tops = int_ops / (gemm_ms * 1e-3) / 1e12
     qbytes = act_quant_bytes(m, k, r)
     quant_gbs = qbytes / (quant_ms * 1e-3) / 1e9
-    log(f"bench: step {ms_per_step * 1e3:.1f} us  quant {quant_ms * 1e3:.1f} us ({quant_gbs:.0f} GB/s)  "
-        f"gemm {gemm_ms * 1e3:.1f} us ({gemm_tops:.0f} TOPS, {100 * gemm_tops / INT8_PEAK_TOPS:.1f}% int8 peak)")
+    log(f"bench: step {step_ms * 1e3:.1f} us (eager {eager_ms * 1e3:.1f} us)  quant {quant_ms * 1e3:.1f} us "
+        f"({quant_gbs:.0f} GB/s)  gemm {gemm_ms * 1e3:.1f} us ({gemm_tops:.0f} TOPS, "
+        f"{100 * gemm_tops / INT8_PEAK_TOPS:.1f}% int8 peak)")
 
     traffic = None
     tpath = ROOT / "profiles" / "w4a4_gemm_c1_traffic.json"
     if tpath.exists():
         try:
             traffic = json.loads(tpath.read_text()).get("hbm_bytes_per_launch")
-        except Exception:  # noqa: BLE001
+        except (OSError, ValueError):
             traffic = None
 
     cpu = None
@@ -143,21 +194,24 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 5),
+        "ms_per_step": round(step_ms, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int4",
         "data": "synthetic",
         "config": {"workload": "svdq_w4a4_linear_c1", "M": m, "N": n, "K": k, "rank": r, "group": 64,
-                   "in_dtype": "bf16", "out_dtype": "bf16", "parallelism": "none"},
+                   "in_dtype": "bf16", "out_dtype": "bf16", "parallelism": "none",
+                   "timing": "K steps in one HIP graph replay"},
         "roofline": {"bound": "mfma", "achieved": round(gemm_tops, 2), "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
                      "frac": round(gemm_tops / INT8_PEAK_TOPS, 4), "traffic": traffic,
                      "kernel": "w4a4_gemm_fp8_kernel", "algorithmic_ops_per_launch": int_ops,
                      "avg_launch_us": round(gemm_ms * 1e3, 2)},
         "pct_int8_peak": round(100 * value_tops / INT8_PEAK_TOPS, 2),
-        "act_quant": {"avg_launch_us": round(quant_ms * 1e3, 2), "algorithmic_bytes": qbytes,
-                      "achieved_GBps": round(quant_gbs, 1), "frac_hbm_peak": round(quant_gbs / HBM_PEAK_GBS, 4)},
+        "eager_ms_per_step": round(eager_ms, 5),
+        "act_quant": {"kernel": "svdq_quant_int4_kernel", "avg_launch_us": round(quant_ms * 1e3, 2),
+                      "algorithmic_bytes": qbytes, "achieved_GBps": round(quant_gbs, 1),
+                      "frac_hbm_peak": round(quant_gbs / HBM_PEAK_GBS, 4)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

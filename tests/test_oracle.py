@@ -314,3 +314,89 @@ def test_producers_match_oracle():
     oq8, os8 = O.quantize_weight_int8(w.numpy())
     assert np.array_equal(q8.numpy(), oq8) and np.array_equal(s8.numpy(), os8)
     assert np.array_equal(svdq.unpack_int4(qw).numpy(), O.unpack_int4(oq))
+
+
+# ---------------------------------------------------------------------------
+# the float pieces: library routines and losslessly quantizable inputs
+# ---------------------------------------------------------------------------
+
+def _nibbles(packed: np.ndarray) -> np.ndarray:
+    """Independent unpack: element 2j = low nibble of byte j, two's complement."""
+    p = np.asarray(packed, np.int64)
+    lo, hi = p & 0xF, p >> 4
+    out = np.empty(p.shape[:-1] + (2 * p.shape[-1],), np.int64)
+    out[..., 0::2], out[..., 1::2] = lo, hi
+    return np.where(out >= 8, out - 16, out)
+
+
+def test_gelu_tanh_matches_torch():
+    y = np.linspace(-12.0, 12.0, 4001)
+    want = torch.nn.functional.gelu(torch.from_numpy(y), approximate="tanh").numpy()
+    assert np.allclose(O.gelu_tanh(y), want, rtol=1e-13, atol=1e-15)
+
+
+def test_lowrank_down_matches_torch():
+    g = np.random.default_rng(21)
+    x = O.f32_to_bf16_bits(g.standard_normal((33, 320)).astype(np.float32))
+    d = O.f32_to_bf16_bits((g.standard_normal((320, 16)) * 0.02).astype(np.float32))
+    xt = torch.from_numpy(x.astype(np.int16)).view(torch.bfloat16).double()
+    dt = torch.from_numpy(d.astype(np.int16)).view(torch.bfloat16).double()
+    assert np.allclose(O.lowrank_down(x, d), (xt @ dt).numpy(), rtol=1e-12, atol=1e-14)
+
+
+def test_int8_gemm_matches_torch():
+    g = np.random.default_rng(22)
+    qa = g.integers(-127, 128, size=(19, 257), dtype=np.int8)
+    qw = g.integers(-127, 128, size=(23, 257), dtype=np.int8)
+    want = (torch.from_numpy(qa).long() @ torch.from_numpy(qw).long().t()).numpy()
+    assert np.array_equal(O.int8_gemm(qa, qw).astype(np.int64), want)
+    assert int(O.int8_gemm(np.full((1, 64), -127, np.int8), np.full((1, 64), 127, np.int8))[0, 0]) == -64 * 127 * 127
+
+
+def test_w8a8_linear_lossless_inputs():
+    """Rows built as q * 2^-e with max |q| = 127 quantize losslessly (scale = 2^-e exactly), so the
+    W8A8 linear must equal a plain float64 matmul of the inputs with the dequantized weights."""
+    g = np.random.default_rng(23)
+    m, n, k = 12, 40, 192
+    q = g.integers(-127, 128, size=(m, k))
+    q[:, 5] = 127
+    e = g.integers(-3, 9, size=(m, 1))
+    x = (q * np.exp2(-e.astype(np.float64))).astype(np.float32)
+    xb = O.f32_to_bf16_bits(x)
+    assert np.array_equal(O.bf16_bits_to_f32(xb), x)
+    w = (g.standard_normal((n, k)) * 0.02).astype(np.float32)
+    qw, sw = O.quantize_weight_int8(w)
+    bias = (g.standard_normal(n) * 0.1).astype(np.float32)
+    want = x.astype(np.float64) @ (qw.astype(np.float64) * sw.astype(np.float64)).T + bias.astype(np.float64)
+    assert np.allclose(O.w8a8_linear(xb, qw, sw, bias), want, rtol=1e-12, atol=1e-12)
+
+
+def test_w4a4_linear_lossless_inputs():
+    """Groups built as q * 2^-e with max |q| = 7 quantize losslessly (fp16(amax/7) = 2^-e), and a
+    power-of-two smoothing keeps that true, so the full linear (smoothing, quant, GEMM, second,
+    low-rank, bias, GELU) must equal a plain float64 assembly from the inputs: x/smooth @ deq(W)^T.
+    (s2 is pinned by the exact-rational scale and code tests.)"""
+    g = np.random.default_rng(24)
+    m, n, k, r = 10, 48, 256, 16
+    grp = k // 64
+    q = g.integers(-7, 8, size=(m, grp, 64))
+    q[:, :, 3] = -7
+    e = g.integers(-2, 6, size=(m, grp, 1))
+    xs = (q * np.exp2(-e.astype(np.float64))).reshape(m, k)           # the smoothed activations
+    sm = np.exp2(g.integers(-2, 3, size=k).astype(np.float64))         # power-of-two smoothing
+    x = (xs * sm).astype(np.float32)
+    xb, smb = O.f32_to_bf16_bits(x), O.f32_to_bf16_bits(sm.astype(np.float32))
+    assert np.array_equal(O.bf16_bits_to_f32(xb).astype(np.float64), xs * sm)
+    qw, sw = O.quantize_weight_int4((g.standard_normal((n, k)) * 0.02).astype(np.float32))
+    wd = _nibbles(qw).astype(np.float64) * np.repeat(sw.astype(np.float64), 64, axis=1)
+    down = O.f32_to_bf16_bits((g.standard_normal((k, r)) * 0.05).astype(np.float32))
+    up = O.f32_to_bf16_bits((g.standard_normal((n, r)) * 0.05).astype(np.float32))
+    b = O.f32_to_bf16_bits((g.standard_normal(n) * 0.1).astype(np.float32))
+    second = (g.random(n) + 0.5).astype(np.float32)
+    y = O.w4a4_linear(xb, smb, qw, sw, down, up, b, second=second, gelu=True)
+    la = torch.from_numpy((x.astype(np.float64) @ O.bf16_bits_to_f32(down).astype(np.float64)).astype(np.float32))
+    la = la.to(torch.bfloat16).double().numpy()
+    pre = (xs @ wd.T) * second.astype(np.float64) + la @ O.bf16_bits_to_f32(up).astype(np.float64).T \
+        + O.bf16_bits_to_f32(b).astype(np.float64)
+    want = torch.nn.functional.gelu(torch.from_numpy(pre), approximate="tanh").numpy()
+    assert np.allclose(y, want, rtol=1e-12, atol=1e-12)
