@@ -110,7 +110,7 @@ def main() -> int:
     packed = mod.packed_weight()
 
     def quant():
-        return ops.svdq_quant_lora(x, mod.smooth_factor, None, mod.proj_down_t)
+        return ops.svdq_quant_lora(x, mod.smooth_factor, None, mod.proj_down_op)
 
     qa, sa, la = quant()
 

@@ -36,6 +36,12 @@ enum { GWA_DT_BF16 = 0, GWA_DT_F16 = 1, GWA_DT_F32 = 2 };
 /* GEMM epilogue flags */
 enum { GWA_EPI_GELU_TANH = 1 };
 
+/* activation code formats written by gwa_svdq_quant_int4 */
+enum {
+  GWA_QFMT_INT4 = 0, /* uint8 [M, K/2]: two's-complement nibbles, element 2j in the low nibble (the reference contract) */
+  GWA_QFMT_FP6 = 1   /* uint8 [M, 3K/4]: the same codes as e3m2 fp6, element t of a group at bits [6t, 6t+6) of its 48 bytes */
+};
+
 /* Library version and build description ("archs=gfx950 hip=..."). Mirrors
  * cozy_kernels::build_info, csrc/cozy_kernels/ops.cpp:23-27. */
 int gwa_version(void);
@@ -60,14 +66,21 @@ int gwa_probe_add_one(const float* in, float* out, int64_t n, void* stream);
  *   s2         fp32 device scalar or NULL (= 1.0): second-level scale; the
  *              group scale is fp16(amax / (7 * s2)) and codes divide by
  *              (scale * s2), as models/nvfp4_quant.py:98-101 do for nvfp4
- *   proj_down_t bf16 [rank, K] (proj_down transposed) or NULL; rank in {0, 16, 32, 64, 128}
- *   q          uint8 [M, K/2] packed codes (out)
+ *   proj_down_op  proj_down in MFMA operand order (gwa_svdq_prep_proj_down)
+ *              or NULL; rank in {0, 16, 32, 64, 128}
+ *   out_format GWA_QFMT_INT4 (q uint8 [M, K/2]) or GWA_QFMT_FP6 (q uint8 [M, 3K/4])
  *   scales     fp16 [M, K/64] (out)
- *   la         bf16 [M, rank] = x @ proj_down on RAW x (out; NULL iff proj_down_t is NULL) */
+ *   la         bf16 [M, rank] = x @ proj_down on RAW x (out; NULL iff proj_down_op is NULL) */
 int gwa_svdq_quant_int4(const void* x, int64_t ldx, const void* smooth, const float* s2,
-                        const void* proj_down_t, int64_t rank,
+                        const void* proj_down_op, int64_t rank, int out_format,
                         uint8_t* q, void* scales, void* la,
                         int64_t M, int64_t K, void* stream);
+
+/* proj_down bf16 [K, rank] -> the operand order kernel 1 reads (done once
+ * per weight; no reference counterpart: the reference runs x2 @ proj_down
+ * as a separate bf16 GEMM, models/svdq_fused.py:524).
+ *   out  bf16 [ceil(K/256)*256 * rank] (16-byte aligned), zero padded */
+int gwa_svdq_prep_proj_down(const void* proj_down, void* out, int64_t K, int64_t rank, void* stream);
 
 /* Kernel 2 — W4A4 GEMM with the fused SVDQuant epilogue.
  * Replaces _gemm_w4a4 (torch._scaled_mm, models/w4a4.py:173-180) followed by

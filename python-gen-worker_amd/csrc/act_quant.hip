@@ -3,17 +3,28 @@
 #include "gwa_common.h"
 
 // ---------------------------------------------------------------------------
-// Kernel 1: smoothing divide -> group-64 absmax -> fp16 scale -> int4 codes,
-// packed two per byte; plus la = x @ proj_down on the RAW activations via
-// bf16 MFMA 16x16x32.
+// Kernel 1: smoothing divide -> group-64 absmax -> fp16 scale -> int4 codes;
+// plus la = x @ proj_down on the RAW activations via bf16 MFMA 16x16x32.
 //
-// Work split: a workgroup owns 16 rows; its NW waves split the K groups of
-// those rows evenly, and their partial la blocks are summed through LDS. Lane
-// (i = lane % 16, kq = lane / 16) holds, per group of 64, the 16 elements of
-// row i at K offsets kq*8 + [0,8) and 32 + kq*8 + [0,8): each is one 16-byte
-// load, and the same registers are the MFMA A operand of the group's two
-// 32-wide K halves. The row's group absmax is a max over lanes {i, i+16,
-// i+32, i+48}.
+// Work split: a 512-thread workgroup owns 16 rows and walks K in rounds of
+// 256 columns (4 groups). Each round's 16 x 256 bf16 tile is loaded with
+// row-contiguous 16-byte loads (512 bytes of a row per 32 lanes: whole cache
+// lines) into double-buffered LDS together with the round's smoothing
+// factors, PF rounds ahead of use; then
+//  * each wave quantizes 2 rows of the tile, a lane holding 8 consecutive
+//    elements, the group absmax a max over the group's 8 lanes (three DPP
+//    steps), the scale RN(amax / 7) by one fma-corrected multiply (exact for
+//    every finite bf16 amax, checked exhaustively with rational arithmetic);
+//  * each wave adds one 32-column slice of x @ proj_down with MFMA, the A
+//    operand read from the tile in MFMA order and the B operand loaded from
+//    proj_down pre-arranged in MFMA operand order (1 KB contiguous per load;
+//    gwa_svdq_prep_proj_down), so no transpose touches global memory.
+// The eight waves' la partials are summed through LDS at the end.
+//
+// Output formats: GWA_QFMT_INT4 is the reference contract (two's-complement
+// nibbles, element 2j in the low nibble of byte j); GWA_QFMT_FP6 writes the
+// same codes as e3m2 fp6 (6 bits each, element t of a group at bits
+// [6t, 6t+6) of the group's 48 bytes), the operand format of the fp6 GEMM.
 //
 // Arithmetic = the reference order (models/svdq_fused.py:88-103,
 // models/nvfp4_quant.py:96-102): xs = RN_bf16(RN_f32(x / smooth));
@@ -22,7 +33,7 @@
 //
 // Fast path (bit-identical, no per-element division):
 //  * smoothing: xs = RN_bf16(x * r), r = RN_f32(1 / smooth). For bf16 x and a
-//    normal bf16 smooth, x/s lies at least 2^-17 (relative) from any bf16
+//    normal bf16 smooth, x/s lies at least 2^-18 (relative) from any bf16
 //    rounding tie unless it is exact, and |x*r - x/s| <= 2^-23 |x/s|, so both
 //    round to the same bf16.
 //  * codes (s2 == 1, scale a normal fp16 below the clamp): q = xs / d with an
@@ -34,7 +45,7 @@
 //    RNE of q. |q| <= 7*(1 + 2^-11) < 7.5 here, so no clamp is needed, and
 //    the code is the low nibble of the float's bits.
 //  Anything else (s2 != 1, non-normal smooth, clamped or subnormal scales)
-//  takes the IEEE-division path.
+//  takes the IEEE-division path (a wave-uniform branch).
 // ---------------------------------------------------------------------------
 namespace {
 
@@ -44,9 +55,15 @@ constexpr float kFp16MinNormal = 6.103515625e-05f;     // 2^-14
 constexpr float kSnap = 3072.0f;                       // 1.5 * 2^11: spacing 2^-12 on [2048, 4096)
 constexpr float kRound = 12582912.0f - 3072.0f;        // 1.5 * 2^23 - 3072
 
+constexpr int KT = 256;                 // columns per round
+constexpr int XT_STR = KT * 2 + 16;     // LDS row stride of the x tile (bytes)
+constexpr int XT_BYTES = 16 * XT_STR;   // 8448
+constexpr int QBUF = XT_BYTES + KT * 4 * 2 + 16;  // tile + reciprocals + factors + flag word
+
 typedef float v2f __attribute__((ext_vector_type(2)));
 typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
 typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
+typedef unsigned int v3u __attribute__((ext_vector_type(3)));
 
 __device__ __forceinline__ void unpack8_bf16(v4i w, float* v) {
 #pragma unroll
@@ -63,259 +80,240 @@ __device__ __forceinline__ uint32_t int4_code_exact(float v, float d) {
   return (uint32_t)((int)q) & 0xFu;
 }
 
-// Pack 8 codes held as the low nibbles of h[0..7] (element 2j in the low nibble).
-// Each pair becomes one byte (bits 8+ of the pair word are don't-care), and
-// two byte permutes gather the four bytes.
-__device__ __forceinline__ uint32_t pack_nibbles(const uint32_t* h) {
-  uint32_t p[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) p[j] = (h[2 * j] & 0xFu) | (h[2 * j + 1] << 4);
-  const uint32_t lo = __builtin_amdgcn_perm(p[1], p[0], 0x0c0c0400u);  // bytes 0,1: p0.b0, p1.b0
-  const uint32_t hi = __builtin_amdgcn_perm(p[3], p[2], 0x04000c0cu);  // bytes 2,3: p2.b0, p3.b0
-  return lo | hi;
-}
-
 // smoothing factor usable by the multiply path: 1/s is a normal float
 __device__ __forceinline__ bool smooth_ok(float s) {
   const float a = fabsf(s);
   return a >= 1.1754943508222875e-38f && a < 8.507059173023462e37f;
 }
 
-// ---------------------------------------------------------------------------
-// Kernel 1. A workgroup owns 16 rows and walks K in rounds of NW groups:
-// in round r wave w quantizes group r * NW + w. Each round's low-rank operand
-// slice (proj_down^T, NW * 64 columns) and smoothing factors are staged
-// once per workgroup into a double-buffered LDS area by all threads, so the
-// waves' registers only hold their own activation prefetch ring (PF rounds
-// deep). Staging loads for round r+2 are issued in round r, into the second
-// of two register sets, and written to LDS at the end of round r+1; they are
-// issued before the activation loads of round r+PF, and vector memory
-// operations complete in order, so waiting for the staging never waits for
-// activations still in flight.
-//
-// LDS per buffer: [NW][RB][2][64 lanes][8 bf16] operand slice, then
-// [NW * 64] reciprocals and [NW * 64] factors (fp32), then one flag word
-// holding the last round whose factors the multiply path cannot use.
-// ---------------------------------------------------------------------------
-template <int RB, int NW>
-struct QuantLds {
-  static constexpr int kOpBytes = NW * RB * 2 * 64 * 16;
-  static constexpr int kBufBytes = kOpBytes + NW * 64 * 4 * 2 + 16;
-  static constexpr int kChunks = (NW * RB * 2 * 64) / (NW * 64);  // 16-byte operand loads per thread per round
-};
+// four nibble codes held as bytes (two's-complement nibble in the low 4 bits) -> four e3m2 bytes
+__device__ __forceinline__ uint32_t e3m2_x4(uint32_t nib) {
+  // q = 0..7 and q = -8..-1 (nibble 8..15) tables, byte j = code of nibble j / j + 8
+  const uint32_t sel = nib & 0x07070707u;
+  const uint32_t pos = __builtin_amdgcn_perm(0x17161514u, 0x12100C00u, sel);
+  const uint32_t neg = __builtin_amdgcn_perm(0x2C303234u, 0x35363738u, sel);
+  const uint32_t m = ((nib >> 3) & 0x01010101u) * 0xFFu;
+  return (neg & m) | (pos & ~m);
+}
 
-template <int RB, int NW, int PF>
-__global__ __launch_bounds__(NW * 64) void svdq_quant_int4_kernel(
+// four 6-bit codes in the low bits of four bytes -> 24 contiguous bits
+__device__ __forceinline__ uint32_t pack6_x4(uint32_t b) {
+  return (b & 0x3Fu) | ((b >> 2) & 0xFC0u) | ((b >> 4) & 0x3F000u) | ((b >> 6) & 0xFC0000u);
+}
+
+// max over the 8-lane group (lanes 8j .. 8j+7) of a 32-bit value
+__device__ __forceinline__ uint32_t oct_max(uint32_t v) {
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));   // quad_perm 2,3,0,1
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));  // row_half_mirror
+  return v;
+}
+
+template <int RB, int FMT, int PF>
+__global__ __launch_bounds__(512) void svdq_quant_int4_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, const uint16_t* __restrict__ smooth,
-    const float* __restrict__ s2p, const uint16_t* __restrict__ pdt, uint8_t* __restrict__ q,
+    const float* __restrict__ s2p, const uint16_t* __restrict__ pdo, uint8_t* __restrict__ q,
     uint16_t* __restrict__ sc, uint16_t* __restrict__ la, int M, int K) {
-  using L = QuantLds<RB, NW>;
-  constexpr int NCH = RB > 0 ? L::kChunks : 1;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int i = lane & 15, kq = lane >> 4;
+  constexpr int RBX = RB > 0 ? RB : 1;
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int row0 = blockIdx.x * 16;
-  const int row = row0 + i;
   const int G = K >> 6;
-  const int rounds = (G + NW - 1) / NW;
+  const int rounds = (K + KT - 1) / KT;
 
-  // buffers: every access is unconditional; rows >= M and groups >= G read 0 / store nothing
+  // buffers: every access is unconditional; rows >= M, columns >= K read 0 / store nothing
   const rsrc_t xbuf = make_rsrc(x, (uint32_t)(((int64_t)(M - 1) * ldx + K) * 2));
-  const rsrc_t qbuf = make_rsrc(q, (uint32_t)((int64_t)M * (K >> 1)));
+  const int64_t qrow_bytes = FMT == GWA_QFMT_FP6 ? (int64_t)K * 3 / 4 : (int64_t)K / 2;
+  const rsrc_t qbuf = make_rsrc(q, (uint32_t)((int64_t)M * qrow_bytes));
   const rsrc_t sbuf = make_rsrc(sc, (uint32_t)((int64_t)M * G * 2));
-  const rsrc_t pbuf = make_rsrc(pdt, (uint32_t)(RB * 16 * K * 2));
+  const rsrc_t pbuf = make_rsrc(pdo, (uint32_t)((int64_t)rounds * KT * RB * 32));
   const rsrc_t smbuf = make_rsrc(smooth, smooth ? (uint32_t)(K * 2) : 0u);
-  const uint32_t xrow = (uint32_t)((int64_t)row * ldx * 2) + (uint32_t)(kq * 16);
-  const uint32_t qrow = (uint32_t)((int64_t)row * (K >> 1)) + (uint32_t)(kq * 4);
-  const uint32_t srow = kq == 0 ? (uint32_t)((int64_t)row * G * 2) : kOOB;
 
-  // staging roles: operand chunk c = tid + j * NW * 64 -> (slot, rb, half, lane c % 64)
-  uint32_t poff[NCH];
-  int pslot[NCH];
-#pragma unroll
-  for (int j = 0; j < NCH; ++j) {
-    const int c = tid + j * NW * 64;
-    const int cl = c & 63, half = (c >> 6) & 1, rb = (c >> 7) % (RB > 0 ? RB : 1);
-    pslot[j] = (c >> 7) / (RB > 0 ? RB : 1);
-    poff[j] = (uint32_t)(((rb * 16 + (cl & 15)) * K + half * 32 + (cl >> 4) * 8) * 2);
-  }
-  // smoothing: threads 0 .. NW*32-1 stage two factors each
-  const bool sm_role = smooth && tid < NW * 32;
+  // tile loader: thread t -> row t >> 5, 16 bytes at column 8 (t & 31)
+  const int xcol = (tid & 31) * 8;
+  const uint32_t xoff = (uint32_t)(((int64_t)(row0 + (tid >> 5)) * ldx + xcol) * 2);
+  const bool sm_role = smooth && tid < KT / 2;
 
-  auto stage_load = [&](v4i* pv, uint32_t& sv, int r) {
-#pragma unroll
-    for (int j = 0; j < NCH; ++j) {
-      const int g = r * NW + pslot[j];
-      pv[j] = RB > 0 ? buf_load16(pbuf, g < G ? poff[j] + (uint32_t)(g * 128) : kOOB) : (v4i){0, 0, 0, 0};
-    }
-    const int k = r * NW * 64 + tid * 2;
-    sv = sm_role ? buf_load4(smbuf, k < K ? (uint32_t)(k * 2) : kOOB) : 0u;
+  struct Slot {
+    v4i xv;
+    uint32_t sv;
+    v4i lo[RBX];
   };
-  // writes the staged round r into LDS buffer b; a factor the multiply path
-  // cannot use marks the buffer's flag word with r (stale marks hold older
-  // rounds, so the flag never needs clearing)
-  auto stage_store = [&](const v4i* pv, uint32_t sv, int r, int b) {
-    uint8_t* base = lds + b * L::kBufBytes;
+  auto load_tile = [&](Slot& s, int r) {
+    const int kb = r * KT;
+    s.xv = buf_load16(xbuf, kb + xcol < K ? xoff + (uint32_t)(kb * 2) : kOOB);
+    const int k = kb + 2 * tid;
+    s.sv = sm_role ? buf_load4(smbuf, k < K ? (uint32_t)(k * 2) : kOOB) : 0u;
+  };
+  auto load_lowrank = [&](Slot& s, int r) {
 #pragma unroll
-    for (int j = 0; j < NCH; ++j)
-      if (RB > 0) *(v4i*)(base + (tid + j * NW * 64) * 16) = pv[j];
+    for (int rb = 0; rb < RB; ++rb)
+      s.lo[rb] = buf_load16(pbuf, (uint32_t)((((int64_t)(r * (KT / 32) + wave) * RB + rb) * 64 + lane) * 16));
+  };
+  // round r's tile + factors into LDS buffer b; a factor the multiply path
+  // cannot use marks the buffer's flag word with r
+  auto store_tile = [&](const Slot& s, int r, int b) {
+    uint8_t* base = lds + b * QBUF;
+    *(v4i*)(base + (tid >> 5) * XT_STR + (tid & 31) * 16) = s.xv;
     if (sm_role) {
-      const float s0 = bf16_lo(sv), s1 = bf16_hi(sv);
-      const int k = tid * 2;
-      float* rs = (float*)(base + L::kOpBytes);
-      float* fs = rs + NW * 64;
-      rs[k] = 1.0f / s0;
-      rs[k + 1] = 1.0f / s1;
-      fs[k] = s0;
-      fs[k + 1] = s1;
-      const bool live = (r * NW * 64 + k < K);  // factors past K are padding
-      if (live && (!smooth_ok(s0) || !smooth_ok(s1))) *(int*)(fs + NW * 64) = r;
+      const float s0 = bf16_lo(s.sv), s1 = bf16_hi(s.sv);
+      float* rs = (float*)(base + XT_BYTES);
+      float* fs = rs + KT;
+      rs[2 * tid] = 1.0f / s0;
+      rs[2 * tid + 1] = 1.0f / s1;
+      fs[2 * tid] = s0;
+      fs[2 * tid + 1] = s1;
+      if (r * KT + 2 * tid < K && (!smooth_ok(s0) || !smooth_ok(s1))) *(int*)(fs + KT) = r;
     }
-  };
-  auto round_bad = [&](int r, int b) -> bool {
-    return *(const int*)(lds + b * L::kBufBytes + L::kOpBytes + NW * 64 * 8) == r;
   };
 
   const float s2 = s2p ? *s2p : 1.0f;
   const bool s2_one = (s2 == 1.0f);
   const float den7 = 7.0f * s2;
+  const float r7 = 1.0f / 7.0f;
 
-  // prologue: stage round 0 (and issue round 1), prime the activation ring with rounds 0 .. PF-1
-  v4i pv[2][NCH];
-  uint32_t sv[2];
-  stage_load(pv[0], sv[0], 0);
-  stage_load(pv[1], sv[1], 1);
-  v4i xa[PF], xb[PF];
+  // quantization roles: wave w rows 2w, 2w+1; lane -> row 2w + (lane >> 5), 8 columns at 8 (lane & 31)
+  const int qr = 2 * wave + (lane >> 5), qc = (lane & 31) * 8;
+  const int grow = row0 + qr;
+  const uint32_t q_row_off = (uint32_t)((int64_t)grow * qrow_bytes);
+  const uint32_t s_row_off = (lane & 7) == 0 ? (uint32_t)((int64_t)grow * G * 2) : kOOB;
+
+  if (tid < 2) *(int*)(lds + tid * QBUF + XT_BYTES + KT * 8) = -1;
+  Slot slot[PF];
 #pragma unroll
   for (int j = 0; j < PF; ++j) {
-    const int g = j * NW + wave;
-    const uint32_t off = g < G ? xrow + (uint32_t)(g * 128) : kOOB;
-    xa[j] = buf_load16(xbuf, off);
-    xb[j] = buf_load16(xbuf, g < G ? off + 64 : kOOB);
+    load_tile(slot[j], j);
+    if (RB > 0) load_lowrank(slot[j], j);
   }
-  if (tid < 2) *(int*)(lds + tid * L::kBufBytes + L::kOpBytes + NW * 64 * 8) = -1;
-  __syncthreads();
-  stage_store(pv[0], sv[0], 0, 0);
   __syncthreads();
 
-  v4f acc[RB > 0 ? RB : 1];
+  v4f acc[RBX];
 #pragma unroll
-  for (int rb = 0; rb < (RB > 0 ? RB : 1); ++rb) acc[rb] = (v4f){0.f, 0.f, 0.f, 0.f};
+  for (int rb = 0; rb < RBX; ++rb) acc[rb] = (v4f){0.f, 0.f, 0.f, 0.f};
 
-  static_assert(PF % 2 == 0, "the staging register set alternates with the round");
   for (int rr = 0; rr < rounds; rr += PF) {
 #pragma unroll
     for (int j = 0; j < PF; ++j) {
       const int r = rr + j;
       const int b = r & 1;
-      // staging loads for round r+2 (set r & 1 was published at the end of
-      // round r-1), then the activation loads for round r+PF
-      stage_load(pv[j & 1], sv[j & 1], r + 2);
-      const v4i ca = xa[j], cb = xb[j];
-      {
-        const int gn = (r + PF) * NW + wave;
-        const uint32_t off = gn < G ? xrow + (uint32_t)(gn * 128) : kOOB;
-        xa[j] = buf_load16(xbuf, off);
-        xb[j] = buf_load16(xbuf, gn < G ? off + 64 : kOOB);
-      }
-      const int g = r * NW + wave;
-      const bool valid = g < G;
-      const uint8_t* base = lds + b * L::kBufBytes;
-      const bool bad = smooth && round_bad(r, b);
+      store_tile(slot[j], r, b);
+      load_tile(slot[j], r + PF);
+      __syncthreads();
+      const uint8_t* base = lds + b * QBUF;
 
-      // xs as packed bf16 words (8 per lane)
-      uint32_t w[8];
-      if (!smooth) {
+      // ---- quantize 8 columns of one row per lane (a group = 8 lanes)
+      {
+        const int kg = r * KT + qc;       // first column
+        const int g = kg >> 6;            // group
+        const bool valid = kg < K;
+        const v4i c0 = *(const v4i*)(base + qr * XT_STR + qc * 2);
+        uint32_t w[4];
+        if (!smooth) {
+#pragma unroll
+          for (int t = 0; t < 4; ++t) w[t] = (uint32_t)c0[t];
+        } else {
+          const bool bad = *(const int*)(base + XT_BYTES + KT * 8) == r;
+          float v[8], f[8];
+          unpack8_bf16(c0, v);
+          const float* src = (const float*)(base + XT_BYTES) + (bad ? KT : 0) + qc;
+          *(v4f*)(f) = *(const v4f*)(src);
+          *(v4f*)(f + 4) = *(const v4f*)(src + 4);
+          if (!bad) {
+#pragma unroll
+            for (int t = 0; t < 8; ++t) v[t] *= f[t];
+          } else {
+#pragma unroll
+            for (int t = 0; t < 8; ++t) v[t] /= f[t];
+          }
+#pragma unroll
+          for (int t = 0; t < 4; ++t)
+            w[t] = __builtin_bit_cast(uint32_t, __builtin_convertvector((v2f){v[2 * t], v[2 * t + 1]}, v2bf));
+        }
+        // group absmax on the bf16 bit patterns (|x| orders like its bits), over the 8 lanes of the group
+        v2u16 mx = {0, 0};
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          mx = __builtin_elementwise_max(mx, __builtin_bit_cast(v2u16, w[t] & 0x7fff7fffu));
+        const uint32_t mb = oct_max(mx[0] > mx[1] ? mx[0] : mx[1]);
+        const float amax = __uint_as_float(mb << 16);
+
+        // RN(amax / 7): for a finite bf16 amax, one fma correction of amax * RN(1/7) is the correctly
+        // rounded quotient wherever it is >= 2^-24 (below that the scale clamps anyway); otherwise
+        // (s2 != 1, inf/NaN) the IEEE division (wave-uniform branch)
+        float scl;
+        const bool easy = s2_one && (mb & 0x7F80u) != 0x7F80u;
+        if (__builtin_amdgcn_ballot_w64(!easy) == 0) {
+          const float q1 = amax * r7;
+          scl = fmaf(fmaf(-7.0f, q1, amax), r7, q1);
+        } else {
+          scl = amax / den7;
+        }
+        const bool fast = !valid || (s2_one && scl >= kFp16MinNormal && scl < kFp16Max);
+        scl = fminf(fmaxf(scl, kScaleMin), kFp16Max);
+        const uint16_t sh = f32_to_f16_bits(scl);
+        const float d = f16_bits_to_f32(sh) * s2;
+
+        float v[8];
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-          w[t] = (uint32_t)ca[t];
-          w[4 + t] = (uint32_t)cb[t];
+          v[2 * t] = bf16_lo(w[t]);
+          v[2 * t + 1] = bf16_hi(w[t]);
         }
-      } else {
-        float v[16], f[16];
-        unpack8_bf16(ca, v);
-        unpack8_bf16(cb, v + 8);
-        // bad == 0: multiply by RN(1/s), bit-identical to dividing (|x*r - x/s| <= 2^-23 |x/s|,
-        // while x/s is 2^-18 or more (relative) from every bf16 rounding tie); else divide.
-        const float* src = (const float*)(base + L::kOpBytes) + (bad ? NW * 64 : 0) + wave * 64 + kq * 8;
-        *(v4f*)(f) = *(const v4f*)(src);
-        *(v4f*)(f + 4) = *(const v4f*)(src + 4);
-        *(v4f*)(f + 8) = *(const v4f*)(src + 32);
-        *(v4f*)(f + 12) = *(const v4f*)(src + 36);
-        if (!bad) {
+        // codes as bytes: nb[j] holds elements 4j .. 4j+3, one nibble per byte
+        uint32_t nb[2];
+        if (__builtin_amdgcn_ballot_w64(!fast) == 0) {  // wave-uniform; neither side touches memory
+          const float rd = __builtin_amdgcn_rcpf(d);
 #pragma unroll
-          for (int t = 0; t < 16; ++t) v[t] *= f[t];
+          for (int j4 = 0; j4 < 2; ++j4) {
+            uint32_t hb[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) hb[e] = __float_as_uint(((v[4 * j4 + e] * rd) + kSnap) + kRound);
+            nb[j4] = __builtin_amdgcn_perm(__builtin_amdgcn_perm(hb[3], hb[2], 0x0c0c0400u),
+                                           __builtin_amdgcn_perm(hb[1], hb[0], 0x0c0c0400u), 0x05040100u) &
+                     0x0F0F0F0Fu;
+          }
         } else {
 #pragma unroll
-          for (int t = 0; t < 16; ++t) v[t] /= f[t];
+          for (int j4 = 0; j4 < 2; ++j4) {
+            nb[j4] = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) nb[j4] |= int4_code_exact(v[4 * j4 + e], d) << (8 * e);
+          }
         }
-#pragma unroll
-        for (int t = 0; t < 8; ++t)
-          w[t] = __builtin_bit_cast(uint32_t, __builtin_convertvector((v2f){v[2 * t], v[2 * t + 1]}, v2bf));
-      }
-      // group absmax on the bf16 bit patterns (|x| orders like its bits)
-      v2u16 mx = {0, 0};
-#pragma unroll
-      for (int t = 0; t < 8; ++t)
-        mx = __builtin_elementwise_max(mx, __builtin_bit_cast(v2u16, w[t] & 0x7fff7fffu));
-      uint32_t mb = mx[0] > mx[1] ? mx[0] : mx[1];
-      mb = max(mb, (uint32_t)__shfl_xor((int)mb, 16));
-      mb = max(mb, (uint32_t)__shfl_xor((int)mb, 32));
-      const float amax = __uint_as_float(mb << 16);
-
-      float scl = amax / den7;
-      const bool fast = !valid || (s2_one && scl >= kFp16MinNormal && scl < kFp16Max);
-      scl = fminf(fmaxf(scl, kScaleMin), kFp16Max);
-      const uint16_t sh = f32_to_f16_bits(scl);
-      const float d = f16_bits_to_f32(sh) * s2;
-
-      float v[16];
-#pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        v[2 * t] = bf16_lo(w[t]);
-        v[2 * t + 1] = bf16_hi(w[t]);
-      }
-      uint32_t w0, w1;
-      // wave-uniform choice; neither side touches memory
-      if (__builtin_amdgcn_ballot_w64(!fast) == 0) {
-        const float rd = __builtin_amdgcn_rcpf(d);
-        uint32_t h[16];
-#pragma unroll
-        for (int t = 0; t < 16; ++t) h[t] = __float_as_uint(((v[t] * rd) + kSnap) + kRound);
-        w0 = pack_nibbles(h);
-        w1 = pack_nibbles(h + 8);
-      } else {
-        w0 = w1 = 0;
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-          w0 |= int4_code_exact(v[t], d) << (4 * t);
-          w1 |= int4_code_exact(v[8 + t], d) << (4 * t);
+        if (FMT == GWA_QFMT_FP6) {
+          // 8 codes = 48 bits per lane; lane pairs share three dwords (the even lane stores the first two)
+          const uint32_t t0 = pack6_x4(e3m2_x4(nb[0])), t1 = pack6_x4(e3m2_x4(nb[1]));
+          const uint32_t lo32 = t0 | (t1 << 24), hi16 = t1 >> 8;          // this lane's 48 bits
+          const uint32_t nlo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)lo32, 0xB1, 0xF, 0xF, false);
+          const bool even = (lane & 1) == 0;
+          const uint32_t base6 = valid ? q_row_off + (uint32_t)((kg - (lane & 1) * 8) * 3 / 4) : kOOB;
+          // branch-free: each lane issues both stores, the one that is not its own goes out of range
+          buf_store8(make_uint2(lo32, hi16 | (nlo << 16)), qbuf, even ? base6 : kOOB);
+          buf_store4((lo32 >> 16) | (hi16 << 16), qbuf, (!even && valid) ? base6 + 8 : kOOB);
+        } else {
+          const uint32_t a = nb[0], bb = nb[1];
+          const uint32_t pa = (a & 0xFu) | ((a >> 4) & 0xF0u) | ((a >> 8) & 0xF00u) | ((a >> 12) & 0xF000u);
+          const uint32_t pb = (bb & 0xFu) | ((bb >> 4) & 0xF0u) | ((bb >> 8) & 0xF00u) | ((bb >> 12) & 0xF000u);
+          buf_store4(pa | (pb << 16), qbuf, valid ? q_row_off + (uint32_t)(kg / 2) : kOOB);
         }
+        buf_store2(sh, sbuf, valid ? s_row_off + (uint32_t)(g * 2) : kOOB);
       }
-      const uint32_t qo = valid ? qrow + (uint32_t)(g * 32) : kOOB;
-      buf_store4(w0, qbuf, qo);
-      buf_store4(w1, qbuf, valid ? qo + 16 : kOOB);
-      buf_store2(sh, sbuf, valid ? srow + (uint32_t)(g * 2) : kOOB);
 
-      // la += x[:, group] @ proj_down[group, :] (raw activations)
+      // ---- la += x[:, slice] @ proj_down[slice, :] for this wave's 32-column slice
+      if (RB > 0) {
+        const v4i a = *(const v4i*)(base + (lane & 15) * XT_STR + wave * 64 + (lane >> 4) * 16);
 #pragma unroll
-      for (int rb = 0; rb < RB; ++rb) {
-        const uint8_t* op = base + ((wave * RB + rb) * 2) * 1024 + lane * 16;
-        const v4i b0 = *(const v4i*)(op);
-        const v4i b1 = *(const v4i*)(op + 1024);
-        acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, ca), __builtin_bit_cast(v8bf, b0),
-                                                          acc[rb], 0, 0, 0);
-        acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, cb), __builtin_bit_cast(v8bf, b1),
-                                                          acc[rb], 0, 0, 0);
+        for (int rb = 0; rb < RB; ++rb)
+          acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, a),
+                                                            __builtin_bit_cast(v8bf, slot[j].lo[rb]), acc[rb], 0, 0, 0);
+        load_lowrank(slot[j], r + PF);
       }
-      // publish round r+1 (its buffer was last read in round r-1, before the previous barrier)
-      stage_store(pv[(j + 1) & 1], sv[(j + 1) & 1], r + 1, b ^ 1);
-      __syncthreads();
     }
   }
 
   if (RB > 0) {
-    // sum the NW partial la blocks through LDS (buffer 0 is free after the last barrier); wave 0 writes bf16
+    // sum the 8 waves' partial la blocks through LDS; wave 0 writes bf16
+    __syncthreads();
     float* lap = (float*)lds;
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) *(v4f*)(lap + ((wave * RB + rb) * 64 + lane) * 4) = acc[rb];
@@ -325,18 +323,40 @@ __global__ __launch_bounds__(NW * 64) void svdq_quant_int4_kernel(
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
         v4f s = acc[rb];
-        for (int w = 1; w < NW; ++w) {
-          const v4f o = *(const v4f*)(lap + ((w * RB + rb) * 64 + lane) * 4);
-          s += o;
-        }
+#pragma unroll
+        for (int w2 = 1; w2 < 8; ++w2) s += *(const v4f*)(lap + ((w2 * RB + rb) * 64 + lane) * 4);
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-          const int r = row0 + 4 * kq + t;
-          if (r < M) la[(int64_t)r * R + rb * 16 + i] = f32_to_bf16(s[t]);
+          const int r = row0 + 4 * (lane >> 4) + t;
+          if (r < M) la[(int64_t)r * R + rb * 16 + (lane & 15)] = f32_to_bf16(s[t]);
         }
       }
     }
   }
+}
+
+// proj_down [K, R] bf16 -> MFMA B-operand order for kernel 1, zero padded to
+// a multiple of 256 rows: out[((kc * RB + rb) * 64 + lane) * 8 + e] =
+// proj_down[32 kc + 8 (lane / 16) + e][16 rb + lane % 16].
+__global__ __launch_bounds__(256) void prep_proj_down_kernel(const uint16_t* __restrict__ pd,
+                                                             uint16_t* __restrict__ out, int K, int Kp, int R) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int RB = R / 16;
+  if (idx >= (int64_t)(Kp / 32) * RB * 64) return;
+  const int lane = (int)(idx % 64);
+  const int rb = (int)((idx / 64) % RB);
+  const int kc = (int)(idx / (64 * RB));
+  const int r = rb * 16 + (lane & 15);
+  const int k0 = kc * 32 + (lane >> 4) * 8;
+  uint16_t v[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = (k0 + e < K) ? pd[(int64_t)(k0 + e) * R + r] : (uint16_t)0;
+  uint4 o;
+  o.x = (uint32_t)v[0] | ((uint32_t)v[1] << 16);
+  o.y = (uint32_t)v[2] | ((uint32_t)v[3] << 16);
+  o.z = (uint32_t)v[4] | ((uint32_t)v[5] << 16);
+  o.w = (uint32_t)v[6] | ((uint32_t)v[7] << 16);
+  *(uint4*)(out + idx * 8) = o;
 }
 
 // ---------------------------------------------------------------------------
@@ -403,71 +423,66 @@ __global__ __launch_bounds__(256) void svdq_epilogue_kernel(const uint16_t* __re
 
 }  // namespace
 
+extern "C" int gwa_svdq_prep_proj_down(const void* proj_down, void* out, int64_t K, int64_t rank, void* stream) {
+  GWA_REQUIRE(K > 0 && K % 64 == 0 && K < (1ll << 24), "svdq_prep_proj_down: bad K=%lld", (long long)K);
+  GWA_REQUIRE(rank == 16 || rank == 32 || rank == 64 || rank == 128, "svdq_prep_proj_down: rank %lld not in {16,32,64,128}",
+              (long long)rank);
+  GWA_REQUIRE(proj_down && out, "svdq_prep_proj_down: null pointer");
+  GWA_REQUIRE(GWA_ALIGNED(proj_down, 2) && GWA_ALIGNED(out, 16), "svdq_prep_proj_down: out must be 16-byte aligned");
+  const int64_t kp = (K + 255) / 256 * 256;
+  const int64_t total = (kp / 32) * (rank / 16) * 64;
+  hipLaunchKernelGGL(prep_proj_down_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t*)proj_down, (uint16_t*)out, (int)K, (int)kp, (int)rank);
+  return gwa_check_launch("svdq_prep_proj_down");
+}
+
 extern "C" int gwa_svdq_quant_int4(const void* x, int64_t ldx, const void* smooth, const float* s2,
-                                   const void* proj_down_t, int64_t rank, uint8_t* q, void* scales,
-                                   void* la, int64_t M, int64_t K, void* stream) {
+                                   const void* proj_down_op, int64_t rank, int out_format, uint8_t* q,
+                                   void* scales, void* la, int64_t M, int64_t K, void* stream) {
   GWA_REQUIRE(M >= 0 && K > 0, "svdq_quant_int4: bad shape M=%lld K=%lld", (long long)M, (long long)K);
   GWA_REQUIRE(K % 64 == 0, "svdq_quant_int4: K=%lld is not a multiple of 64", (long long)K);
   GWA_REQUIRE(ldx >= K && ldx % 8 == 0, "svdq_quant_int4: row stride %lld must be >= K and a multiple of 8",
               (long long)ldx);
-  GWA_REQUIRE((proj_down_t == nullptr) == (la == nullptr),
-              "svdq_quant_int4: proj_down_t and la must both be given or both be NULL");
-  const int64_t R = proj_down_t ? rank : 0;
+  GWA_REQUIRE(out_format == GWA_QFMT_INT4 || out_format == GWA_QFMT_FP6, "svdq_quant_int4: out_format %d",
+              out_format);
+  GWA_REQUIRE((proj_down_op == nullptr) == (la == nullptr),
+              "svdq_quant_int4: proj_down_op and la must both be given or both be NULL");
+  const int64_t R = proj_down_op ? rank : 0;
   GWA_REQUIRE(R == 0 || R == 16 || R == 32 || R == 64 || R == 128,
               "svdq_quant_int4: rank %lld not in {0,16,32,64,128}", (long long)R);
   GWA_REQUIRE(M < (1ll << 31) && K < (1ll << 24) && (M * ldx * 2) < (1ll << 31),
               "svdq_quant_int4: x must stay below 2 GiB (buffer addressing)");
   if (M == 0) return GWA_OK;
   GWA_REQUIRE(x && q && scales, "svdq_quant_int4: null pointer");
-  GWA_REQUIRE(GWA_ALIGNED(x, 16) && GWA_ALIGNED(q, 16) && GWA_ALIGNED(scales, 2) &&
-                  GWA_ALIGNED(smooth, 16) && GWA_ALIGNED(proj_down_t, 16) && GWA_ALIGNED(la, 2),
-              "svdq_quant_int4: x, q, smooth and proj_down_t must be 16-byte aligned");
+  GWA_REQUIRE(GWA_ALIGNED(x, 16) && GWA_ALIGNED(q, 16) && GWA_ALIGNED(scales, 2) && GWA_ALIGNED(smooth, 4) &&
+                  GWA_ALIGNED(proj_down_op, 16) && GWA_ALIGNED(la, 2),
+              "svdq_quant_int4: x, q and proj_down_op must be 16-byte aligned");
   hipStream_t s = (hipStream_t)stream;
   const uint16_t* xp = (const uint16_t*)x;
   const uint16_t* sm = (const uint16_t*)smooth;
-  const uint16_t* pd = (const uint16_t*)proj_down_t;
+  const uint16_t* pd = (const uint16_t*)proj_down_op;
   uint16_t* sc = (uint16_t*)scales;
   uint16_t* lp = (uint16_t*)la;
   const int m = (int)M, k = (int)K;
   const int rb = (int)(R / 16);
-  // K is walked in rounds of NW groups per 16-row block: more waves when
-  // there are few row blocks, so that small-M calls still fill the GPU, as
-  // long as the double-buffered operand staging fits in LDS.
-  const int64_t blocks = (M + 15) / 16;
-  int nw = blocks >= 512 ? 4 : (blocks >= 128 ? 8 : 16);
-  auto lds_bytes = [&](int w) { return (size_t)2 * ((size_t)w * rb * 2048 + (size_t)w * 512); };
-  while (nw > 4 && lds_bytes(nw) > 160 * 1024) nw >>= 1;
-  const size_t lds = lds_bytes(nw);
-  GWA_REQUIRE(lds <= 160 * 1024, "svdq_quant_int4: rank %lld needs too much LDS", (long long)R);
-  // activation prefetch depth (even: the staging registers alternate by round)
-  const int64_t rounds = (K / 64 + nw - 1) / nw;
-  const int pf = (rounds % 4 == 0) ? 4 : 2;
-  const dim3 grid((unsigned)blocks);
-#define GWA_QUANT_LAUNCH(RBV, NWV, PFV)                                                                  \
-  hipLaunchKernelGGL((svdq_quant_int4_kernel<RBV, NWV, PFV>), grid, dim3(NWV * 64), lds, s, xp, ldx, sm, s2, pd, \
-                     q, sc, lp, m, k)
-#define GWA_QUANT_NW(RBV, NWV)                                   \
-  if (pf == 4) GWA_QUANT_LAUNCH(RBV, NWV, 4);                    \
-  else GWA_QUANT_LAUNCH(RBV, NWV, 2);
-#define GWA_QUANT_RB(RBV)                    \
-  case RBV:                                  \
-    if (nw == 16) { GWA_QUANT_NW(RBV, 16) }  \
-    else if (nw == 8) { GWA_QUANT_NW(RBV, 8) } \
-    else { GWA_QUANT_NW(RBV, 4) }            \
-    break;
+  const size_t lds = 2 * (size_t)QBUF > (size_t)rb * 8192 ? 2 * (size_t)QBUF : (size_t)rb * 8192;
+  const dim3 grid((unsigned)((M + 15) / 16)), block(512);
+  const bool fp6 = out_format == GWA_QFMT_FP6;
+#define GWA_QUANT_LAUNCH(RBV, PFV)                                                                               \
+  if (fp6)                                                                                                       \
+    hipLaunchKernelGGL((svdq_quant_int4_kernel<RBV, GWA_QFMT_FP6, PFV>), grid, block, lds, s, xp, ldx, sm, s2, pd, \
+                       q, sc, lp, m, k);                                                                          \
+  else                                                                                                           \
+    hipLaunchKernelGGL((svdq_quant_int4_kernel<RBV, GWA_QFMT_INT4, PFV>), grid, block, lds, s, xp, ldx, sm, s2,   \
+                       pd, q, sc, lp, m, k);
   switch (rb) {
-    GWA_QUANT_RB(0)
-    GWA_QUANT_RB(1)
-    GWA_QUANT_RB(2)
-    case 4:
-      if (nw == 8) { GWA_QUANT_NW(4, 8) }
-      else { GWA_QUANT_NW(4, 4) }
-      break;
-    case 8: GWA_QUANT_NW(8, 4) break;
+    case 0: GWA_QUANT_LAUNCH(0, 4) break;
+    case 1: GWA_QUANT_LAUNCH(1, 4) break;
+    case 2: GWA_QUANT_LAUNCH(2, 4) break;
+    case 4: GWA_QUANT_LAUNCH(4, 3) break;
+    case 8: GWA_QUANT_LAUNCH(8, 2) break;
     default: return gwa_set_error(GWA_ERR_INVALID, "svdq_quant_int4: rank %lld not in {0,16,32,64,128}", (long long)R);
   }
-#undef GWA_QUANT_NW
-#undef GWA_QUANT_RB
 #undef GWA_QUANT_LAUNCH
   return gwa_check_launch("svdq_quant_int4");
 }

@@ -56,6 +56,12 @@ __device__ __forceinline__ float f16_bits_to_f32(uint16_t b) {
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   return (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
 }
+// RN-even bf16 pair with the hardware conversion (v_cvt_pk_bf16_f32); a NaN stays a NaN.
+__device__ __forceinline__ uint32_t pack_bf16x2_rn(float a, float b) {
+  typedef float v2f_ __attribute__((ext_vector_type(2)));
+  typedef __bf16 v2bf_ __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((v2f_){a, b}, v2bf_));
+}
 __device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
   return (uint32_t)f32_to_f16_bits(a) | ((uint32_t)f32_to_f16_bits(b) << 16);
 }

@@ -56,6 +56,8 @@ constexpr int LDS_SW = TN * GS * 2;                // [TN][GS] f16
 constexpr int LDS_CW = TN * 16;                    // [TN][hi0..3, lo0..3] f16
 constexpr int OFF_W = LDS_X, OFF_SX = OFF_W + LDS_W, OFF_SW = OFF_SX + LDS_SX, OFF_CW = OFF_SW + LDS_SW;
 constexpr int LDS_STAGE = OFF_CW + LDS_CW;         // 76800
+constexpr int OFF_EPI = 2 * LDS_STAGE;             // [TN] column multipliers, [TN] bias (fp32)
+constexpr int LDS_TOTAL = OFF_EPI + 2 * TN * 4;
 static_assert(TM * KTB / 16 == 4 * NTHREADS && TN * KTB / 16 == 2 * NTHREADS, "loader split");
 constexpr int kWScaleE8M0 = 127 + 6;               // 2^6 on the weight operand
 constexpr float kUnscale = 4096.0f;                // 2^12
@@ -206,6 +208,19 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp8_kernel(
 
   Stage regs;
   load(regs, 0);
+  // the tile's per-column epilogue constants, staged once: 2^12 * s2 * 2^e[n] * second[n] and bias[n]
+  if (tid < TN) {
+    const int n = n0 + tid;
+    float mult = 0.0f, bv = 0.0f;
+    if (n < N) {
+      mult = (s2p ? *s2p : 1.0f) * kUnscale * escale[n];
+      if (second) mult *= second[second_per_channel ? n : 0];
+      if (bias) bv = bf16_to_f32(bias[n]);
+    }
+    float* epi = (float*)(lds + OFF_EPI);
+    epi[tid] = mult;
+    epi[TN + tid] = bv;
+  }
   store(regs, 0);
   __syncthreads();
 
@@ -281,44 +296,67 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp8_kernel(
   }
 
   // ---------------- epilogue ----------------
-  const rsrc_t obuf = make_rsrc(out, (uint32_t)((int64_t)M * N * 2));
-  const float s2 = s2p ? *s2p : 1.0f;
-  const float base_mult = s2 * kUnscale;
+  // acc = acc * colmul[n]; acc += la @ up^T (the low-rank operands loaded in
+  // chunks of up to 2 rank-16 slices, every load of a chunk in flight
+  // together); then + bias[n] (+ GELU) and packed stores.
+  const float* epi = (const float*)(lds + OFF_EPI);
 #pragma unroll
   for (int bn = 0; bn < WBN; ++bn) {
-    const int nb = n0 + 32 * (WBN * wn + bn);
+    const int nl = 32 * (WBN * wn + bn);  // block's first column within the tile
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd) {
+      const v4f cm = *(const v4f*)(epi + nl + 8 * qd + 4 * h);
+#pragma unroll
+      for (int bm = 0; bm < WBM; ++bm)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[bn][bm][4 * qd + e] *= cm[e];
+    }
+  }
+  if (RB > 0) {
+    constexpr int RC = RB < 2 ? RB : 2;
+    const rsrc_t ubuf = make_rsrc(up, (uint32_t)((int64_t)N * RB * 32));
+    const rsrc_t lbuf = make_rsrc(la, (uint32_t)((int64_t)M * RB * 32));
+#pragma unroll
+    for (int k0 = 0; k0 < RB; k0 += RC) {
+      v4i ua[WBN][RC > 0 ? RC : 1], lb[WBM][RC > 0 ? RC : 1];
+#pragma unroll
+      for (int bn = 0; bn < WBN; ++bn)
+#pragma unroll
+        for (int kk = 0; kk < RC; ++kk)
+          ua[bn][kk] = buf_load16(
+              ubuf, (uint32_t)((int64_t)(n0 + 32 * (WBN * wn + bn) + r32) * (RB * 32) + (k0 + kk) * 32 + 16 * h));
+#pragma unroll
+      for (int bm = 0; bm < WBM; ++bm)
+#pragma unroll
+        for (int kk = 0; kk < RC; ++kk)
+          lb[bm][kk] = buf_load16(
+              lbuf, (uint32_t)((int64_t)(m0 + 32 * (WBM * wm + bm) + r32) * (RB * 32) + (k0 + kk) * 32 + 16 * h));
+#pragma unroll
+      for (int bn = 0; bn < WBN; ++bn)
+#pragma unroll
+        for (int bm = 0; bm < WBM; ++bm)
+#pragma unroll
+          for (int kk = 0; kk < RC; ++kk)
+            acc[bn][bm] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, ua[bn][kk]),
+                                                                  __builtin_bit_cast(v8bf, lb[bm][kk]), acc[bn][bm],
+                                                                  0, 0, 0);
+    }
+  }
+  const rsrc_t obuf = make_rsrc(out, (uint32_t)((int64_t)M * N * 2));
+#pragma unroll
+  for (int bn = 0; bn < WBN; ++bn) {
+    const int nl = 32 * (WBN * wn + bn);
 #pragma unroll
     for (int bm = 0; bm < WBM; ++bm) {
       const int m = m0 + 32 * (WBM * wm + bm) + r32;
-      v16f y = acc[bn][bm];
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int n = nb + 8 * (v >> 2) + 4 * h + (v & 3);
-        const int nc = n < N ? n : 0;
-        float mult = base_mult * escale[nc];
-        if (second) mult *= second[second_per_channel ? nc : 0];
-        y[v] *= mult;
-      }
-      if (RB > 0) {
-        const int nrow = nb + r32;
-        const bool nin = nrow < N, min_ = m < M;
-#pragma unroll
-        for (int kk = 0; kk < RB; ++kk) {
-          const int r0 = kk * 16 + 8 * h;
-          v4i ua = nin ? *(const v4i*)(up + (int64_t)nrow * (RB * 16) + r0) : (v4i){0, 0, 0, 0};
-          v4i lb = min_ ? *(const v4i*)(la + (int64_t)m * (RB * 16) + r0) : (v4i){0, 0, 0, 0};
-          y = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, ua), __builtin_bit_cast(v8bf, lb),
-                                                      y, 0, 0, 0);
-        }
-      }
 #pragma unroll
       for (int qd = 0; qd < 4; ++qd) {
-        const int n = nb + 8 * qd + 4 * h;
+        const int n = n0 + nl + 8 * qd + 4 * h;
+        const v4f cb = *(const v4f*)(epi + TN + nl + 8 * qd + 4 * h);
         float o[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          float t = y[4 * qd + e];
-          if (bias) t += bf16_to_f32(bias[n + e < N ? n + e : 0]);
+          float t = acc[bn][bm][4 * qd + e] + cb[e];
           if (GELU) t = gelu_tanh_f32(t);
           o[e] = t;
         }
@@ -327,8 +365,8 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp8_kernel(
           pk.x = pack_f16x2(o[0], o[1]);
           pk.y = pack_f16x2(o[2], o[3]);
         } else {
-          pk.x = pack_bf16x2(o[0], o[1]);
-          pk.y = pack_bf16x2(o[2], o[3]);
+          pk.x = pack_bf16x2_rn(o[0], o[1]);
+          pk.y = pack_bf16x2_rn(o[2], o[3]);
         }
         // branch-free store after the MFMAs: rows >= M / columns >= N fall outside the buffer
         const uint32_t off = (m < M && n < N) ? (uint32_t)(((int64_t)m * N + n) * 2) : kOOB;
@@ -490,7 +528,7 @@ extern "C" int gwa_svdq_gemm_w4a4_packed(const uint8_t* qa, const void* sa, cons
   hipStream_t s = (hipStream_t)stream;
   const int64_t per_xcd = (tiles + kXcds - 1) / kXcds;
   const dim3 grid((unsigned)(per_xcd * kXcds)), block(NTHREADS);
-  const size_t lds = 2 * (size_t)LDS_STAGE;
+  const size_t lds = (size_t)LDS_TOTAL;
   const int pc = second_numel > 1;
   const uint16_t* sap = (const uint16_t*)sa;
   const uint16_t* swp = (const uint16_t*)sw_packed;

@@ -21,6 +21,7 @@ LIB_NAME = "libgen_worker_amd.so"
 
 DT_BF16, DT_F16, DT_F32 = 0, 1, 2
 EPI_GELU_TANH = 1
+QFMT_INT4, QFMT_FP6 = 0, 1
 
 
 class NativeUnavailable(RuntimeError):
@@ -41,7 +42,8 @@ _SIGNATURES: dict[str, tuple] = {
     "gwa_build_info": (),
     "gwa_last_error": (),
     "gwa_probe_add_one": (_vp, _vp, _i64, _vp),
-    "gwa_svdq_quant_int4": (_vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _vp),
+    "gwa_svdq_quant_int4": (_vp, _i64, _vp, _vp, _vp, _i64, _int, _vp, _vp, _vp, _i64, _i64, _vp),
+    "gwa_svdq_prep_proj_down": (_vp, _vp, _i64, _i64, _vp),
     "gwa_svdq_gemm_w4a4": (_vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _int, _int,
                            _i64, _i64, _i64, _vp),
     "gwa_svdq_group_psums": (_vp, _vp, _vp, _i64, _i64, _i64, _vp),

@@ -16,8 +16,13 @@ The same names and schemas are registered here, backed by the HIP kernels of
 Additions (no reference counterpart; the fused forms the reference keeps as
 separate steps):
 
-* ``svdq_quant_lora(x2, smooth, s2, proj_down_t) -> (q, s, la)``: kernel 1
-  with ``la = x2 @ proj_down`` fused (``proj_down_t`` = proj_down^T, [rank, K]).
+* ``svdq_prep_proj_down(proj_down) -> proj_down_op``: proj_down [K, rank] in
+  the operand order kernel 1 reads ([ceil(K/256)*256, rank], done once).
+* ``svdq_quant_lora(x2, smooth, s2, proj_down_op) -> (q, s, la)``: kernel 1
+  with ``la = x2 @ proj_down`` fused.
+* ``svdq_quant_fp6(x2, smooth, s2, proj_down_op) -> (q6, s, la)``: the same
+  codes as e3m2 fp6 [M, 3K/4] for the fp6 GEMM (``la`` empty when
+  ``proj_down_op`` is None).
 * ``svdq_w4a4_linear(qa, sa, weight, wscales, s2, second, la, up, bias,
   out_dtype, gelu)``: kernel 2 on the resident ``weight`` [N, K/2] layout.
 * ``svdq_group_psums(qa, qw)``: exact int32 per-group partial sums (debug).
@@ -85,31 +90,34 @@ def _dt_code(dtype: torch.dtype) -> int:
 # kernel 1
 # ---------------------------------------------------------------------------
 
-def _quant_impl(x2: Tensor, smooth: Optional[Tensor], s2: Optional[Tensor],
-                proj_down_t: Optional[Tensor]) -> tuple[Tensor, Tensor, Optional[Tensor]]:
+def _quant_impl(x2: Tensor, smooth: Optional[Tensor], s2: Optional[Tensor], proj_down_op: Optional[Tensor],
+                fmt: int = 0) -> tuple[Tensor, Tensor, Optional[Tensor]]:
     name = "svdq_quant"
     if x2.dim() != 2:
         raise SvdqOpError(f"{name}: x2 must be 2-D, got {tuple(x2.shape)}")
     _check_dtype(name, x2, torch.bfloat16, what="x2")
     _check_dtype(name, smooth, torch.bfloat16, what="smooth")
-    _check_dtype(name, proj_down_t, torch.bfloat16, what="proj_down_t")
+    _check_dtype(name, proj_down_op, torch.bfloat16, what="proj_down_op")
     s2 = _scalar_f32(name, s2)
-    _check_cuda(name, x2=x2, smooth=smooth, s2=s2, proj_down_t=proj_down_t)
+    _check_cuda(name, x2=x2, smooth=smooth, s2=s2, proj_down_op=proj_down_op)
     m, k = int(x2.shape[0]), int(x2.shape[1])
     if k % GROUP:
         raise SvdqOpError(f"{name}: K={k} is not a multiple of {GROUP}")
     if smooth is not None and smooth.numel() != k:
         raise SvdqOpError(f"{name}: smooth has {smooth.numel()} values for K={k}")
     rank = 0
-    if proj_down_t is not None:
-        if proj_down_t.dim() != 2 or int(proj_down_t.shape[1]) != k:
-            raise SvdqOpError(f"{name}: proj_down_t must be [rank, K={k}], got {tuple(proj_down_t.shape)}")
-        rank = int(proj_down_t.shape[0])
-    q = torch.empty(m, k // 2, dtype=torch.uint8, device=x2.device)
+    if proj_down_op is not None:
+        kp = (k + 255) // 256 * 256
+        if proj_down_op.dim() != 2 or int(proj_down_op.shape[0]) != kp:
+            raise SvdqOpError(f"{name}: proj_down_op must be [{kp}, rank] (svdq_prep_proj_down of a [K={k}, rank] "
+                              f"proj_down), got {tuple(proj_down_op.shape)}")
+        rank = int(proj_down_op.shape[1])
+    x2 = x2 if x2.stride(1) == 1 else x2.contiguous()
+    q = torch.empty(m, (3 * k) // 4 if fmt == nat.QFMT_FP6 else k // 2, dtype=torch.uint8, device=x2.device)
     s = torch.empty(m, k // GROUP, dtype=torch.float16, device=x2.device)
-    la = torch.empty(m, rank, dtype=torch.bfloat16, device=x2.device) if proj_down_t is not None else None
-    nat.call("gwa_svdq_quant_int4", nat.ptr(x2), k, nat.ptr(smooth), nat.ptr(s2), nat.ptr(proj_down_t),
-             rank, nat.ptr(q), nat.ptr(s), nat.ptr(la), m, k, nat.stream_of(x2))
+    la = torch.empty(m, rank, dtype=torch.bfloat16, device=x2.device) if proj_down_op is not None else None
+    nat.call("gwa_svdq_quant_int4", nat.ptr(x2), int(x2.stride(0)), nat.ptr(smooth), nat.ptr(s2),
+             nat.ptr(proj_down_op), rank, fmt, nat.ptr(q), nat.ptr(s), nat.ptr(la), m, k, nat.stream_of(x2))
     return q, s, la
 
 
@@ -129,20 +137,62 @@ def _(x2: Tensor, smooth: Optional[Tensor], s2: Tensor, blocked: bool) -> tuple[
     return (x2.new_empty(m, k // 2, dtype=torch.uint8), x2.new_empty(m, k // GROUP, dtype=torch.float16))
 
 
+@torch.library.custom_op("cozy_gen_worker::svdq_prep_proj_down", mutates_args=())
+def svdq_prep_proj_down(proj_down: Tensor) -> Tensor:
+    """proj_down bf16 [K, rank] -> the operand order kernel 1 reads, [ceil(K/256)*256, rank] (zero padded)."""
+    name = "svdq_prep_proj_down"
+    _check_dtype(name, proj_down, torch.bfloat16, what="proj_down")
+    _check_cuda(name, proj_down=proj_down)
+    if proj_down.dim() != 2:
+        raise SvdqOpError(f"{name}: proj_down must be [K, rank], got {tuple(proj_down.shape)}")
+    k, r = int(proj_down.shape[0]), int(proj_down.shape[1])
+    if k % GROUP or r not in (16, 32, 64, 128):
+        raise SvdqOpError(f"{name}: K={k} must be a multiple of {GROUP} and rank={r} in (16, 32, 64, 128)")
+    out = torch.empty((k + 255) // 256 * 256, r, dtype=torch.bfloat16, device=proj_down.device)
+    nat.call("gwa_svdq_prep_proj_down", nat.ptr(proj_down.contiguous()), nat.ptr(out), k, r,
+             nat.stream_of(proj_down))
+    return out
+
+
+@svdq_prep_proj_down.register_fake
+def _(proj_down):
+    k, r = int(proj_down.shape[0]), int(proj_down.shape[1])
+    return proj_down.new_empty((k + 255) // 256 * 256, r)
+
+
 @torch.library.custom_op("cozy_gen_worker::svdq_quant_lora", mutates_args=())
 def svdq_quant_lora(x2: Tensor, smooth: Optional[Tensor], s2: Optional[Tensor],
-                    proj_down_t: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+                    proj_down_op: Tensor) -> tuple[Tensor, Tensor, Tensor]:
     """Kernel 1 with the low-rank down-projection fused: (q, s, la = x2 @ proj_down)."""
-    q, s, la = _quant_impl(x2, smooth, s2, proj_down_t)
+    q, s, la = _quant_impl(x2, smooth, s2, proj_down_op)
     assert la is not None
     return q, s, la
 
 
 @svdq_quant_lora.register_fake
-def _(x2, smooth, s2, proj_down_t):
+def _(x2, smooth, s2, proj_down_op):
     m, k = int(x2.shape[0]), int(x2.shape[1])
-    r = int(proj_down_t.shape[0])
+    r = int(proj_down_op.shape[1])
     return (x2.new_empty(m, k // 2, dtype=torch.uint8), x2.new_empty(m, k // GROUP, dtype=torch.float16),
+            x2.new_empty(m, r, dtype=torch.bfloat16))
+
+
+@torch.library.custom_op("cozy_gen_worker::svdq_quant_fp6", mutates_args=())
+def svdq_quant_fp6(x2: Tensor, smooth: Optional[Tensor], s2: Optional[Tensor],
+                   proj_down_op: Optional[Tensor]) -> tuple[Tensor, Tensor, Tensor]:
+    """Kernel 1 writing the codes as e3m2 fp6 [M, 3K/4] (the fp6 GEMM's operand format); la is [M, 0]
+    when ``proj_down_op`` is None."""
+    q, s, la = _quant_impl(x2, smooth, s2, proj_down_op, nat.QFMT_FP6)
+    if la is None:
+        la = x2.new_empty(int(x2.shape[0]), 0)
+    return q, s, la
+
+
+@svdq_quant_fp6.register_fake
+def _(x2, smooth, s2, proj_down_op):
+    m, k = int(x2.shape[0]), int(x2.shape[1])
+    r = int(proj_down_op.shape[1]) if proj_down_op is not None else 0
+    return (x2.new_empty(m, (3 * k) // 4, dtype=torch.uint8), x2.new_empty(m, k // GROUP, dtype=torch.float16),
             x2.new_empty(m, r, dtype=torch.bfloat16))
 
 

@@ -154,10 +154,10 @@ class SvdqW4A4Linear(nn.Module):
         if self.rank:
             self.register_buffer("proj_down", torch.empty(in_features, self.rank, dtype=compute_dtype, device=dev))
             self.register_buffer("proj_up", torch.empty(out_features, self.rank, dtype=compute_dtype, device=dev))
-            self.register_buffer("proj_down_t", torch.empty(self.rank, in_features, dtype=compute_dtype,
-                                                            device=dev), persistent=False)
+            # proj_down in kernel 1's operand order (derived by refresh_derived, GPU only)
+            self.register_buffer("proj_down_op", None, persistent=False)
         else:
-            self.proj_down = self.proj_up = self.proj_down_t = None
+            self.proj_down = self.proj_up = self.proj_down_op = None
         if bias:
             self.bias: Optional[nn.Parameter] = nn.Parameter(
                 torch.empty(out_features, dtype=compute_dtype, device=dev), requires_grad=False)
@@ -172,11 +172,12 @@ class SvdqW4A4Linear(nn.Module):
         self.register_buffer("weight_escale", None, persistent=False)
 
     def refresh_derived(self) -> None:
-        """Recompute the derived buffers after ``weight`` / ``proj_down`` change: the transposed
-        ``proj_down`` kernel 1 reads, and (on the GPU) the prepacked fast-path weights. Weights holding a
-        -8 code keep the general int8 path."""
+        """Recompute the derived buffers after ``weight`` / ``proj_down`` change (GPU only): ``proj_down``
+        in kernel 1's operand order, and the prepacked fast-path weights. Weights holding a -8 code keep
+        the general int8 path."""
         if self.rank:
-            self.proj_down_t = self.proj_down.t().contiguous()
+            self.proj_down_op = (torch.ops.cozy_gen_worker.svdq_prep_proj_down(self.proj_down)
+                                 if self.proj_down.is_cuda else None)
         self.weight_packed = self.weight_sums = None
         self.weight_scale_packed = self.weight_corr = self.weight_escale = None
         if self.weight.is_cuda and self.in_features % 256 == 0:
@@ -209,8 +210,10 @@ class SvdqW4A4Linear(nn.Module):
             raise SvdqFusedError(f"SvdqW4A4Linear expects bf16 activations, got {x2.dtype}")
         x2 = x2.contiguous()
         out_dtype = self.out_dtype or torch.bfloat16
+        if self.rank and self.proj_down_op is None:
+            self.refresh_derived()
         if self.rank:
-            qa, sa, la = torch.ops.cozy_gen_worker.svdq_quant_lora(x2, self.smooth_factor, None, self.proj_down_t)
+            qa, sa, la = torch.ops.cozy_gen_worker.svdq_quant_lora(x2, self.smooth_factor, None, self.proj_down_op)
         else:
             qa, sa = torch.ops.cozy_gen_worker.svdq_quant(x2, self.smooth_factor, self._one, False)
             la = None

@@ -41,3 +41,26 @@ def check_output(y: torch.Tensor, ref: np.ndarray, *, what: str = "") -> dict:
     assert stats["mean_rel"] <= MEAN_REL, f"{what}: {stats}"
     assert stats["rel_fro"] <= REL_FRO, f"{what}: {stats}"
     return stats
+
+
+# e3m2 fp6 (sign, 3-bit exponent with bias 3, 2-bit mantissa): the integers -8 .. 8 it holds
+_E3M2_INT = {0x00: 0, 0x0C: 1, 0x10: 2, 0x12: 3, 0x14: 4, 0x15: 5, 0x16: 6, 0x17: 7, 0x18: 8}
+
+
+def decode_fp6_codes(q6: np.ndarray) -> np.ndarray:
+    """uint8 [M, 3K/4] (element t of each group at bits [6t, 6t+6) of its 48 bytes, little-endian)
+    -> int8 codes [M, K]; raises on any 6-bit value that is not an integer in [-8, 8]."""
+    q6 = np.asarray(q6, np.uint8)
+    m, nb = q6.shape
+    k = nb * 4 // 3
+    b = q6.reshape(m, k // 4, 3).astype(np.uint32)
+    word = b[..., 0] | (b[..., 1] << 8) | (b[..., 2] << 16)               # 4 codes per 3 bytes
+    codes = np.stack([(word >> (6 * t)) & 0x3F for t in range(4)], axis=-1).reshape(m, k)
+    mag = codes & 0x1F
+    lut = np.full(32, 127, np.int64)
+    for bits, val in _E3M2_INT.items():
+        lut[bits] = val
+    v = lut[mag]
+    if np.any(v == 127):
+        raise AssertionError(f"non-integer e3m2 code(s): {sorted(set(int(c) for c in codes[v == 127].ravel()))[:8]}")
+    return np.where(codes & 0x20, -v, v).astype(np.int8)

@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import bits16, check_output, from_bits
+from helpers import bits16, check_output, decode_fp6_codes, from_bits
 from oracle import svdq_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -67,13 +67,22 @@ def test_transpose(rows, cols, dt):
 # kernel 1: int4 activation quant (+ low-rank)
 # ---------------------------------------------------------------------------
 
-def _run_quant(x_bits, smooth_bits, down_bits, s2=None):
+def _run_quant(x_bits, smooth_bits, down_bits, s2=None, fmt="int4"):
+    """Kernel 1 -> (packed int4 codes as numpy, scale bits, la); the fp6 format is decoded and
+    re-packed so both formats compare against the same oracle arrays."""
     x = _dev16(x_bits)
     sm = _dev16(smooth_bits) if smooth_bits is not None else None
     s2t = torch.tensor(s2, dtype=torch.float32, device=DEV) if s2 is not None else None
+    if fmt == "fp6":
+        pdo = torch.ops.cozy_gen_worker.svdq_prep_proj_down(_dev16(down_bits)) if down_bits is not None else None
+        q6, s, la = torch.ops.cozy_gen_worker.svdq_quant_fp6(x, sm, s2t, pdo)
+        torch.cuda.synchronize()
+        codes = decode_fp6_codes(q6.cpu().numpy())
+        assert codes.min() >= -8 and codes.max() <= 7
+        return O.pack_int4(codes), bits16(s), (la if down_bits is not None else None)
     if down_bits is not None:
-        pdt = _dev16(down_bits).t().contiguous()
-        q, s, la = torch.ops.cozy_gen_worker.svdq_quant_lora(x, sm, s2t, pdt)
+        pdo = torch.ops.cozy_gen_worker.svdq_prep_proj_down(_dev16(down_bits))
+        q, s, la = torch.ops.cozy_gen_worker.svdq_quant_lora(x, sm, s2t, pdo)
     else:
         q, s = torch.ops.cozy_gen_worker.svdq_quant(x, sm, s2t if s2t is not None else
                                                     torch.ones((), device=DEV), False)
@@ -105,16 +114,18 @@ def test_quant_golden_second_level_scale():
     assert np.array_equal(q, f["q"]) and np.array_equal(s, f["scales"])
 
 
+@pytest.mark.parametrize("fmt", ["int4", "fp6"])
 @pytest.mark.parametrize("m,k,rank,smooth", [
     (1, 64, 0, False), (16, 128, 16, True), (77, 3072, 32, True), (333, 3072, 128, True),
-    (128, 512, 64, False), (1024, 12288, 32, True), (200, 15360, 32, True),
+    (128, 512, 64, False), (1024, 12288, 32, True), (200, 15360, 32, True), (45, 320, 32, True),
+    (19, 192, 64, True),
 ])
-def test_quant_seeded_bit_exact(m, k, rank, smooth):
+def test_quant_seeded_bit_exact(m, k, rank, smooth, fmt):
     x = _rand_act(m, k, seed=m * 7 + k)
     g = np.random.default_rng(k)
     sm = O.f32_to_bf16_bits(np.exp(g.uniform(np.log(0.25), np.log(4), k)).astype(np.float32)) if smooth else None
     down = O.f32_to_bf16_bits((g.standard_normal((k, rank)) * 0.02).astype(np.float32)) if rank else None
-    q, s, la = _run_quant(x, sm, down)
+    q, s, la = _run_quant(x, sm, down, fmt=fmt)
     wq, ws = O.quantize_act_int4(x, sm)
     assert np.array_equal(q, wq)
     assert np.array_equal(s, ws.view(np.uint16))
@@ -135,10 +146,11 @@ def test_quant_edge_values():
     x = O.f32_to_bf16_bits(np.stack(rows))
     sm = O.f32_to_bf16_bits(np.concatenate([np.full(k // 2, 1.0), np.full(k // 2, 0.3)]).astype(np.float32))
     for smooth in (None, sm):
-        q, s, _ = _run_quant(x, smooth, None)
-        wq, ws = O.quantize_act_int4(x, smooth)
-        assert np.array_equal(q, wq)
-        assert np.array_equal(s, ws.view(np.uint16))
+        for fmt in ("int4", "fp6"):
+            q, s, _ = _run_quant(x, smooth, None, fmt=fmt)
+            wq, ws = O.quantize_act_int4(x, smooth)
+            assert np.array_equal(q, wq), fmt
+            assert np.array_equal(s, ws.view(np.uint16)), fmt
 
 
 def test_quant_row_stride():
@@ -150,8 +162,8 @@ def test_quant_row_stride():
     x = big[:, :k]
     q = torch.empty(m, k // 2, dtype=torch.uint8, device=DEV)
     s = torch.empty(m, k // 64, dtype=torch.float16, device=DEV)
-    nat.call("gwa_svdq_quant_int4", x.data_ptr(), k + 64, None, None, None, 0, q.data_ptr(), s.data_ptr(), None,
-             m, k, nat.stream_of(x))
+    nat.call("gwa_svdq_quant_int4", x.data_ptr(), k + 64, None, None, None, 0, nat.QFMT_INT4, q.data_ptr(),
+             s.data_ptr(), None, m, k, nat.stream_of(x))
     q2, s2 = torch.ops.cozy_gen_worker.svdq_quant(x.contiguous(), None, torch.ones((), device=DEV), False)
     assert torch.equal(q, q2) and torch.equal(s.view(torch.int16), s2.view(torch.int16))
 
@@ -163,11 +175,12 @@ def test_quant_config1_full_size():
     x = synthetic.activation(4608, 3072, outlier_frac=0.005, outlier_scale=30.0)
     sm = synthetic.smooth_factor(3072)
     down = synthetic.normal((3072, 32), 0.02, synthetic.SEED_L1, torch.bfloat16)
-    q, s, la = _run_quant(bits16(x), bits16(sm), bits16(down))
     wq, ws = O.quantize_act_int4(bits16(x), bits16(sm))
-    assert np.array_equal(q, wq)
-    assert np.array_equal(s, ws.view(np.uint16))
-    _check_la(la, bits16(x), bits16(down))
+    for fmt in ("int4", "fp6"):
+        q, s, la = _run_quant(bits16(x), bits16(sm), bits16(down), fmt=fmt)
+        assert np.array_equal(q, wq), fmt
+        assert np.array_equal(s, ws.view(np.uint16)), fmt
+        _check_la(la, bits16(x), bits16(down))
 
 
 # ---------------------------------------------------------------------------
@@ -210,7 +223,8 @@ def _w4a4_case(m, n, k, rank, seed, smooth=True, bias=True, second=None, gelu=Fa
     smd = _dev16(sm) if sm is not None else None
     s2t = torch.tensor(s2, dtype=torch.float32, device=DEV) if s2 is not None else None
     if rank:
-        qa, sa, la = torch.ops.cozy_gen_worker.svdq_quant_lora(xd, smd, s2t, _dev16(down).t().contiguous())
+        qa, sa, la = torch.ops.cozy_gen_worker.svdq_quant_lora(
+            xd, smd, s2t, torch.ops.cozy_gen_worker.svdq_prep_proj_down(_dev16(down)))
         upd = _dev16(up)
     else:
         qa, sa = torch.ops.cozy_gen_worker.svdq_quant(xd, smd, s2t if s2t is not None else
@@ -234,8 +248,8 @@ def _w4a4_case(m, n, k, rank, seed, smooth=True, bias=True, second=None, gelu=Fa
 def test_w4a4_golden():
     f = np.load(GOLDEN / "w4a4_m64_n128_k256_r16.npz")
     xd = _dev16(f["x"])
-    qa, sa, la = torch.ops.cozy_gen_worker.svdq_quant_lora(xd, _dev16(f["smooth"]), None,
-                                                           _dev16(f["proj_down"]).t().contiguous())
+    qa, sa, la = torch.ops.cozy_gen_worker.svdq_quant_lora(
+        xd, _dev16(f["smooth"]), None, torch.ops.cozy_gen_worker.svdq_prep_proj_down(_dev16(f["proj_down"])))
     assert np.array_equal(qa.cpu().numpy(), f["qa"]) and np.array_equal(bits16(sa), f["sa"])
     y = torch.ops.cozy_gen_worker.svdq_w4a4_linear(
         qa, sa, torch.from_numpy(f["qweight"]).to(DEV), from_bits(f["wscales"], torch.float16, DEV), None, None, la,

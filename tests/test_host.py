@@ -47,8 +47,12 @@ def test_invalid_arguments_are_refused_before_any_launch():
 
     lib = _native.load()
     # K not a multiple of 64: validated on the host, no device touched
-    rc = lib.gwa_svdq_quant_int4(None, 100, None, None, None, 0, None, None, None, 4, 100, None)
+    rc = lib.gwa_svdq_quant_int4(None, 100, None, None, None, 0, 0, None, None, None, 4, 100, None)
     assert rc == 1 and "multiple of 64" in lib.gwa_last_error().decode()
+    rc = lib.gwa_svdq_quant_int4(None, 64, None, None, None, 0, 7, None, None, None, 4, 64, None)
+    assert rc == 1 and "out_format" in lib.gwa_last_error().decode()
+    rc = lib.gwa_svdq_prep_proj_down(None, None, 64, 24, None)
+    assert rc == 1 and "rank" in lib.gwa_last_error().decode()
     rc = lib.gwa_svdq_gemm_w4a4(None, None, None, None, None, None, 0, None, None, 0, None, None, 0, 0,
                                 8, 24, 128, None)
     assert rc == 1 and "multiple of 16" in lib.gwa_last_error().decode()
@@ -57,7 +61,7 @@ def test_invalid_arguments_are_refused_before_any_launch():
     rc = lib.gwa_transpose_2d(None, None, 4, 4, 3, None)
     assert rc == 1
     # empty problems are no-ops
-    assert lib.gwa_svdq_quant_int4(None, 64, None, None, None, 0, None, None, None, 0, 64, None) == 0
+    assert lib.gwa_svdq_quant_int4(None, 64, None, None, None, 0, 0, None, None, None, 0, 64, None) == 0
     assert lib.gwa_probe_add_one(None, None, 0, None) == 0
 
 
@@ -87,8 +91,11 @@ def test_fake_impls_trace_shapes():
 
     with FakeTensorMode():
         x = torch.empty(77, 384, dtype=torch.bfloat16)
-        pdt = torch.empty(32, 384, dtype=torch.bfloat16)
-        q, s, la = torch.ops.cozy_gen_worker.svdq_quant_lora(x, None, None, pdt)
+        pdo = torch.ops.cozy_gen_worker.svdq_prep_proj_down(torch.empty(384, 32, dtype=torch.bfloat16))
+        assert pdo.shape == (512, 32)
+        q, s, la = torch.ops.cozy_gen_worker.svdq_quant_lora(x, None, None, pdo)
+        q6, s6, la6 = torch.ops.cozy_gen_worker.svdq_quant_fp6(x, None, None, None)
+        assert q6.shape == (77, 288) and s6.shape == (77, 6) and la6.shape == (77, 0)
         assert q.shape == (77, 192) and s.shape == (77, 6) and la.shape == (77, 32)
         w = torch.empty(128, 192, dtype=torch.uint8)
         ws = torch.empty(128, 6, dtype=torch.float16)
