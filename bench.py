@@ -5,9 +5,10 @@
 
 A step is one pass of the hot path over one batch of synthetic input: the
 config-1 SVDQuant W4A4 linear (M = 4096 image + 512 text tokens = 4608,
-K = N = 3072, rank 32, group 64, bf16 in/out): kernel 1 (smoothing + int4
-act-quant + x @ proj_down) then kernel 2 (W4A4 GEMM + low-rank/bias
-epilogue). Inputs are resident in HBM before the timed region. The K timed
+K = N = 3072, rank 32, group 64, bf16 in/out) on the module's fp6 lane:
+kernel 1 (smoothing + int4 act-quant + x @ proj_down, codes and scales
+written as fp6 operand records) then kernel 2 (W4A4 GEMM on the fp6 MFMA +
+low-rank/bias epilogue). Inputs are resident in HBM before the timed region. The K timed
 steps are captured once into a HIP graph and replayed, so host launch cost
 is not part of the figure; the eager (per-op Python dispatch) rate is
 reported beside it. ``value`` is the linear's throughput in int-TOPS
@@ -105,22 +106,21 @@ def main() -> int:
     mod = build_svdq_w4a4_linear(qweight=L.qweight, wscales=L.wscales, smooth=L.smooth, proj_down=L.proj_down,
                                  proj_up=L.proj_up, bias=L.bias, device=dev)
     x = x_cpu.to(dev)
-    assert mod.lane == "packed", "synthetic int4 weights are in [-7, 7]: the fast lane must be armed"
+    assert mod.lane == "fp6", "K % 128 == 0: the module must take the fp6 lane"
     ops = torch.ops.cozy_gen_worker
-    packed = mod.packed_weight()
 
     def quant():
-        return ops.svdq_quant_lora(x, mod.smooth_factor, None, mod.proj_down_op)
+        return ops.svdq_quant_fp6(x, mod.smooth_factor, None, mod.proj_down_op)
 
-    qa, sa, la = quant()
+    qa, la = quant()
 
-    def gemm(qa=qa, sa=sa, la=la):
-        return ops.svdq_w4a4_linear_packed(qa, sa, *packed, None, mod.second, la, mod.proj_up, mod.bias,
-                                           torch.bfloat16, False)
+    def gemm(qa=qa, la=la):
+        return ops.svdq_w4a4_linear_fp6(qa, mod.weight_fp6, None, mod.second, la, mod.proj_up, mod.bias,
+                                        torch.bfloat16, False)
 
     def step():
-        q, s, l = quant()
-        return gemm(q, s, l)
+        q, l = quant()
+        return gemm(q, l)
 
     if args.only is not None:
         src = torch.empty(COPY_BYTES // 2, dtype=torch.bfloat16, device=dev) if args.only == "copy" else None
@@ -155,7 +155,7 @@ def main() -> int:
     int_ops = w4a4_int_ops(m, n, k)
     value_tops = int_ops / (step_ms * 1e-3) / 1e12
     gemm_tops = int_ops / (gemm_ms * 1e-3) / 1e12
-    qbytes = act_quant_bytes(m, k, r)
+    qbytes = act_quant_bytes(m, k, r, fp6=True)
     quant_gbs = qbytes / (quant_ms * 1e-3) / 1e9
     log(f"bench: step {step_ms * 1e3:.1f} us (eager {eager_ms * 1e3:.1f} us)  quant {quant_ms * 1e3:.1f} us "
         f"({quant_gbs:.0f} GB/s)  gemm {gemm_ms * 1e3:.1f} us ({gemm_tops:.0f} TOPS, "
@@ -205,7 +205,7 @@ def main() -> int:
                    "timing": "K steps in one HIP graph replay"},
         "roofline": {"bound": "mfma", "achieved": round(gemm_tops, 2), "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
                      "frac": round(gemm_tops / INT8_PEAK_TOPS, 4), "traffic": traffic,
-                     "kernel": "w4a4_gemm_fp8_kernel", "algorithmic_ops_per_launch": int_ops,
+                     "kernel": "w4a4_gemm_fp6_kernel", "algorithmic_ops_per_launch": int_ops,
                      "avg_launch_us": round(gemm_ms * 1e3, 2)},
         "pct_int8_peak": round(100 * value_tops / INT8_PEAK_TOPS, 2),
         "eager_ms_per_step": round(eager_ms, 5),

@@ -39,8 +39,20 @@ enum { GWA_EPI_GELU_TANH = 1 };
 /* activation code formats written by gwa_svdq_quant_int4 */
 enum {
   GWA_QFMT_INT4 = 0, /* uint8 [M, K/2]: two's-complement nibbles, element 2j in the low nibble (the reference contract) */
-  GWA_QFMT_FP6 = 1   /* uint8 [M, 3K/4]: the same codes as e3m2 fp6, element t of a group at bits [6t, 6t+6) of its 48 bytes */
+  GWA_QFMT_FP6 = 1   /* uint8 [K/128, M, 104] operand records of the fp6 GEMM, see below */
 };
+
+/* fp6 operand records (activations from gwa_svdq_quant_int4(..., GWA_QFMT_FP6),
+ * weights from gwa_svdq_pack_weight_fp6): stage-major, one 104-byte record per
+ * 128-element stage s of K and row r at byte offset (s * rows + r) * 104:
+ *   bytes [0, 96)   the stage's two groups as e3m2 codes: element t of group j
+ *                   at bits [6t, 6t+6) of bytes [48j, 48j+48) (little-endian)
+ *   bytes [96, 100) the two groups' fp16 scales
+ *   bytes [100,104) unused
+ * (every int4 code -8..7 is an exact e3m2 value). A tile's stage of operand
+ * rows is one contiguous run, and its LDS image keeps a bank-conflict-free
+ * row stride. */
+enum { GWA_FP6_REC = 104 };
 
 /* Library version and build description ("archs=gfx950 hip=..."). Mirrors
  * cozy_kernels::build_info, csrc/cozy_kernels/ops.cpp:23-27. */
@@ -68,8 +80,10 @@ int gwa_probe_add_one(const float* in, float* out, int64_t n, void* stream);
  *              (scale * s2), as models/nvfp4_quant.py:98-101 do for nvfp4
  *   proj_down_op  proj_down in MFMA operand order (gwa_svdq_prep_proj_down)
  *              or NULL; rank in {0, 16, 32, 64, 128}
- *   out_format GWA_QFMT_INT4 (q uint8 [M, K/2]) or GWA_QFMT_FP6 (q uint8 [M, 3K/4])
- *   scales     fp16 [M, K/64] (out)
+ *   out_format GWA_QFMT_INT4 (q uint8 [M, K/2]) or GWA_QFMT_FP6 (q: the fp6
+ *              operand records [K/128, M, 104], K % 128 == 0)
+ *   scales     fp16 [M, K/64] (out; may be NULL with GWA_QFMT_FP6, whose
+ *              records carry the scales)
  *   la         bf16 [M, rank] = x @ proj_down on RAW x (out; NULL iff proj_down_op is NULL) */
 int gwa_svdq_quant_int4(const void* x, int64_t ldx, const void* smooth, const float* s2,
                         const void* proj_down_op, int64_t rank, int out_format,
@@ -97,51 +111,13 @@ int gwa_svdq_prep_proj_down(const void* proj_down, void* out, int64_t K, int64_t
  *   bias   bf16 [N] or NULL
  *   out    [M, N] of out_dtype (GWA_DT_BF16 or GWA_DT_F16)
  * K % 64 == 0, N % 16 == 0. This is the general path (int8 MFMA on the logical
- * two's-complement weights, any code in [-8, 7]); gwa_svdq_gemm_w4a4_packed
- * is the fast path for prepacked weights. */
+ * two's-complement weights, any code in [-8, 7]); gwa_svdq_gemm_w4a4_fp6 is
+ * the fast path (K % 128 == 0) on fp6 operand records. */
 int gwa_svdq_gemm_w4a4(const uint8_t* qa, const void* sa, const uint8_t* qw, const void* sw,
                        const float* s2, const float* second, int64_t second_numel,
                        const void* la, const void* up, int64_t rank, const void* bias,
                        void* out, int out_dtype, int epilogue_flags,
                        int64_t M, int64_t N, int64_t K, void* stream);
-
-/* Prepack int4 weights for gwa_svdq_gemm_w4a4_packed (done once per weight).
- * No reference counterpart beyond the layout conversions of
- * models/svdq_layout.py:165-221 (pack_qweight & co.): converts the logical
- * [N, K/2] two's-complement codes into this library's resident fp8-ready
- * layout, rescales each row's group scales by a power of two, and prepacks
- * the terms of the GEMM's activation-offset correction.
- *   qw        uint8 [N, K/2] logical codes (in)
- *   sw        fp16 [N, K/64] group scales (in)
- *   qw_packed uint8 [N, K/2] (out)
- *   wsum      int16 [N, K/64] per-group code sums (out)
- *   sw_packed fp16 [N, K/64] = sw * 2^-e[n] (out)
- *   wcorr     fp16 [N, ceil(K/256), 8] correction pairs (out, 16-byte aligned)
- *   escale    fp32 [N] = 2^e[n] (out)
- *   n_neg8    int32 device counter, must hold 0; receives the number of -8
- *             codes (the packed layout holds [-7, 7]; any -8 means the
- *             weights must use gwa_svdq_gemm_w4a4 instead) */
-int gwa_svdq_pack_weight_int4(const uint8_t* qw, const void* sw, uint8_t* qw_packed, int16_t* wsum,
-                              void* sw_packed, void* wcorr, float* escale, int* n_neg8,
-                              int64_t N, int64_t K, void* stream);
-
-/* Kernel 2, fast path: the same contract as gwa_svdq_gemm_w4a4 (replacing
- * _gemm_w4a4 + svdq_epilogue_lora, models/w4a4.py:173-180 and
- * models/svdq_fused.py:315-377) on prepacked weights: one exact fp8 MFMA per
- * K-group. qw_packed / sw_packed / wcorr / escale from
- * gwa_svdq_pack_weight_int4 (sa is the activation scale array as produced by
- * gwa_svdq_quant_int4). K % 256 == 0, N % 16 == 0. */
-int gwa_svdq_gemm_w4a4_packed(const uint8_t* qa, const void* sa, const uint8_t* qw_packed,
-                              const void* sw_packed, const void* wcorr, const float* escale,
-                              const float* s2, const float* second, int64_t second_numel,
-                              const void* la, const void* up, int64_t rank, const void* bias,
-                              void* out, int out_dtype, int epilogue_flags,
-                              int64_t M, int64_t N, int64_t K, void* stream);
-
-/* Debug: exact per-group partial sums through the fast path's fp8 MFMA
- * arithmetic (same layout as gwa_svdq_group_psums). No reference counterpart. */
-int gwa_svdq_group_psums_packed(const uint8_t* qa, const uint8_t* qw_packed, const int16_t* wsum,
-                                int32_t* out, int64_t M, int64_t N, int64_t K, void* stream);
 
 /* Debug: exact int32 per-group partial sums out[m, n, g] = sum_{k in g} qx[m,k] qw[n,k]
  * computed by the same MFMA and unpack code as gwa_svdq_gemm_w4a4. No
@@ -149,6 +125,32 @@ int gwa_svdq_group_psums_packed(const uint8_t* qa, const uint8_t* qw_packed, con
  * integer core of kernel 2 bit-exactly. */
 int gwa_svdq_group_psums(const uint8_t* qa, const uint8_t* qw, int32_t* out,
                          int64_t M, int64_t N, int64_t K, void* stream);
+
+/* Prepack int4 weights and their group scales as fp6 operand records for
+ * gwa_svdq_gemm_w4a4_fp6 (done once per weight; no reference counterpart
+ * beyond the layout conversions of models/svdq_layout.py:165-221). Any code
+ * in [-8, 7].
+ *   qw   uint8 [N, K/2] logical two's-complement codes (in)
+ *   sw   fp16 [N, K/64] group scales (in)
+ *   qw6  uint8 [K/128, N, 104] records (out); K % 128 == 0 */
+int gwa_svdq_pack_weight_fp6(const uint8_t* qw, const void* sw, uint8_t* qw6, int64_t N, int64_t K, void* stream);
+
+/* Kernel 2, fp6 path: the contract of gwa_svdq_gemm_w4a4 (replacing
+ * _gemm_w4a4 + svdq_epilogue_lora, models/w4a4.py:173-180 and
+ * models/svdq_fused.py:315-377) on fp6 operand records: qa6 [K/128, M, 104]
+ * from gwa_svdq_quant_int4(..., GWA_QFMT_FP6, ...), qw6 [K/128, N, 104] from
+ * gwa_svdq_pack_weight_fp6 (the records carry sa and sw). One exact fp6 MFMA
+ * per K-group and 32x32 block. K % 128 == 0, N % 16 == 0. */
+int gwa_svdq_gemm_w4a4_fp6(const uint8_t* qa6, const uint8_t* qw6,
+                           const float* s2, const float* second, int64_t second_numel,
+                           const void* la, const void* up, int64_t rank, const void* bias,
+                           void* out, int out_dtype, int epilogue_flags,
+                           int64_t M, int64_t N, int64_t K, void* stream);
+
+/* Debug: exact int32 per-group partial sums (layout of gwa_svdq_group_psums)
+ * through the fp6 GEMM's MFMA on fp6 operand records. No reference counterpart. */
+int gwa_svdq_group_psums_fp6(const uint8_t* qa6, const uint8_t* qw6, int32_t* out,
+                             int64_t M, int64_t N, int64_t K, void* stream);
 
 /* Standalone epilogue: out = y0 * (s2 * second) + la @ up^T + bias (bf16 out).
  * cozy_gen_worker::svdq_epilogue_lora, models/svdq_fused.py:315-377.

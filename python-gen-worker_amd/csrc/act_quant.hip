@@ -23,8 +23,10 @@
 //
 // Output formats: GWA_QFMT_INT4 is the reference contract (two's-complement
 // nibbles, element 2j in the low nibble of byte j); GWA_QFMT_FP6 writes the
-// same codes as e3m2 fp6 (6 bits each, element t of a group at bits
-// [6t, 6t+6) of the group's 48 bytes), the operand format of the fp6 GEMM.
+// same codes as e3m2 fp6 in the fp6 GEMM's operand records (one 104-byte
+// record per 128-column stage and row, stage-major: 96 bytes of codes with
+// element t of a group at bits [6t, 6t+6) of the group's 48 bytes, then the
+// stage's two fp16 group scales).
 //
 // Arithmetic = the reference order (models/svdq_fused.py:88-103,
 // models/nvfp4_quant.py:96-102): xs = RN_bf16(RN_f32(x / smooth));
@@ -86,21 +88,6 @@ __device__ __forceinline__ bool smooth_ok(float s) {
   return a >= 1.1754943508222875e-38f && a < 8.507059173023462e37f;
 }
 
-// four nibble codes held as bytes (two's-complement nibble in the low 4 bits) -> four e3m2 bytes
-__device__ __forceinline__ uint32_t e3m2_x4(uint32_t nib) {
-  // q = 0..7 and q = -8..-1 (nibble 8..15) tables, byte j = code of nibble j / j + 8
-  const uint32_t sel = nib & 0x07070707u;
-  const uint32_t pos = __builtin_amdgcn_perm(0x17161514u, 0x12100C00u, sel);
-  const uint32_t neg = __builtin_amdgcn_perm(0x2C303234u, 0x35363738u, sel);
-  const uint32_t m = ((nib >> 3) & 0x01010101u) * 0xFFu;
-  return (neg & m) | (pos & ~m);
-}
-
-// four 6-bit codes in the low bits of four bytes -> 24 contiguous bits
-__device__ __forceinline__ uint32_t pack6_x4(uint32_t b) {
-  return (b & 0x3Fu) | ((b >> 2) & 0xFC0u) | ((b >> 4) & 0x3F000u) | ((b >> 6) & 0xFC0000u);
-}
-
 // max over the 8-lane group (lanes 8j .. 8j+7) of a 32-bit value
 __device__ __forceinline__ uint32_t oct_max(uint32_t v) {
   v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
@@ -123,9 +110,10 @@ __global__ __launch_bounds__(512) void svdq_quant_int4_kernel(
 
   // buffers: every access is unconditional; rows >= M, columns >= K read 0 / store nothing
   const rsrc_t xbuf = make_rsrc(x, (uint32_t)(((int64_t)(M - 1) * ldx + K) * 2));
-  const int64_t qrow_bytes = FMT == GWA_QFMT_FP6 ? (int64_t)K * 3 / 4 : (int64_t)K / 2;
+  // FP6: [K/128][M][104] records (96 bytes of codes, 2 fp16 scales, 4 unused bytes)
+  const int64_t qrow_bytes = FMT == GWA_QFMT_FP6 ? (int64_t)(K / 128) * GWA_FP6_REC : (int64_t)K / 2;
   const rsrc_t qbuf = make_rsrc(q, (uint32_t)((int64_t)M * qrow_bytes));
-  const rsrc_t sbuf = make_rsrc(sc, (uint32_t)((int64_t)M * G * 2));
+  const rsrc_t sbuf = make_rsrc(sc, sc ? (uint32_t)((int64_t)M * G * 2) : 0u);
   const rsrc_t pbuf = make_rsrc(pdo, (uint32_t)((int64_t)rounds * KT * RB * 32));
   const rsrc_t smbuf = make_rsrc(smooth, smooth ? (uint32_t)(K * 2) : 0u);
 
@@ -205,7 +193,7 @@ __global__ __launch_bounds__(512) void svdq_quant_int4_kernel(
       {
         const int kg = r * KT + qc;       // first column
         const int g = kg >> 6;            // group
-        const bool valid = kg < K;
+        const bool valid = kg < K && grow < M;  // rows past M must not store (fp6 records of the next stage follow)
         const v4i c0 = *(const v4i*)(base + qr * XT_STR + qc * 2);
         uint32_t w[4];
         if (!smooth) {
@@ -282,14 +270,17 @@ __global__ __launch_bounds__(512) void svdq_quant_int4_kernel(
         }
         if (FMT == GWA_QFMT_FP6) {
           // 8 codes = 48 bits per lane; lane pairs share three dwords (the even lane stores the first two)
+          // of the record of (128-column stage g / 2, row), at byte 48 (g % 2) + 6 (lane % 8)
           const uint32_t t0 = pack6_x4(e3m2_x4(nb[0])), t1 = pack6_x4(e3m2_x4(nb[1]));
           const uint32_t lo32 = t0 | (t1 << 24), hi16 = t1 >> 8;          // this lane's 48 bits
           const uint32_t nlo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)lo32, 0xB1, 0xF, 0xF, false);
           const bool even = (lane & 1) == 0;
-          const uint32_t base6 = valid ? q_row_off + (uint32_t)((kg - (lane & 1) * 8) * 3 / 4) : kOOB;
+          const uint32_t rec = (uint32_t)(((int64_t)(g >> 1) * M + grow) * GWA_FP6_REC);
+          const uint32_t base6 = valid ? rec + (uint32_t)((g & 1) * 48 + (lane & 6) * 6) : kOOB;
           // branch-free: each lane issues both stores, the one that is not its own goes out of range
           buf_store8(make_uint2(lo32, hi16 | (nlo << 16)), qbuf, even ? base6 : kOOB);
           buf_store4((lo32 >> 16) | (hi16 << 16), qbuf, (!even && valid) ? base6 + 8 : kOOB);
+          buf_store2(sh, qbuf, (valid && (lane & 7) == 0) ? rec + 96u + (uint32_t)((g & 1) * 2) : kOOB);
         } else {
           const uint32_t a = nb[0], bb = nb[1];
           const uint32_t pa = (a & 0xFu) | ((a >> 4) & 0xF0u) | ((a >> 8) & 0xF00u) | ((a >> 12) & 0xF000u);
@@ -445,15 +436,18 @@ extern "C" int gwa_svdq_quant_int4(const void* x, int64_t ldx, const void* smoot
               (long long)ldx);
   GWA_REQUIRE(out_format == GWA_QFMT_INT4 || out_format == GWA_QFMT_FP6, "svdq_quant_int4: out_format %d",
               out_format);
+  GWA_REQUIRE(out_format != GWA_QFMT_FP6 || K % 128 == 0, "svdq_quant_int4: the fp6 format needs K %% 128 == 0 (K=%lld)",
+              (long long)K);
   GWA_REQUIRE((proj_down_op == nullptr) == (la == nullptr),
               "svdq_quant_int4: proj_down_op and la must both be given or both be NULL");
   const int64_t R = proj_down_op ? rank : 0;
   GWA_REQUIRE(R == 0 || R == 16 || R == 32 || R == 64 || R == 128,
               "svdq_quant_int4: rank %lld not in {0,16,32,64,128}", (long long)R);
-  GWA_REQUIRE(M < (1ll << 31) && K < (1ll << 24) && (M * ldx * 2) < (1ll << 31),
-              "svdq_quant_int4: x must stay below 2 GiB (buffer addressing)");
+  GWA_REQUIRE(M < (1ll << 31) && K < (1ll << 24) && (M * ldx * 2) < (1ll << 31) &&
+                  M * (K / 128) * GWA_FP6_REC < (1ll << 31),
+              "svdq_quant_int4: x and q must stay below 2 GiB (buffer addressing)");
   if (M == 0) return GWA_OK;
-  GWA_REQUIRE(x && q && scales, "svdq_quant_int4: null pointer");
+  GWA_REQUIRE(x && q && (scales || out_format == GWA_QFMT_FP6), "svdq_quant_int4: null pointer");
   GWA_REQUIRE(GWA_ALIGNED(x, 16) && GWA_ALIGNED(q, 16) && GWA_ALIGNED(scales, 2) && GWA_ALIGNED(smooth, 4) &&
                   GWA_ALIGNED(proj_down_op, 16) && GWA_ALIGNED(la, 2),
               "svdq_quant_int4: x, q and proj_down_op must be 16-byte aligned");

@@ -82,6 +82,23 @@ __device__ __forceinline__ float gelu_tanh_f32(float y) {
 __device__ __forceinline__ uint32_t int4_lo_x16(uint32_t w) { return (w << 4) & 0xF0F0F0F0u; }
 __device__ __forceinline__ uint32_t int4_hi_x16(uint32_t w) { return w & 0xF0F0F0F0u; }
 
+// e3m2 ("bf6") codes: every int4 code -8..7 is an exact e3m2 value, so fp6
+// MFMAs on these codes compute integer dot products exactly.
+// four nibble codes held as bytes (two's-complement nibble in the low 4 bits) -> four e3m2 bytes
+__device__ __forceinline__ uint32_t e3m2_x4(uint32_t nib) {
+  // q = 0..7 and q = -8..-1 (nibble 8..15) tables, byte j = code of nibble j / j + 8
+  const uint32_t sel = nib & 0x07070707u;
+  const uint32_t pos = __builtin_amdgcn_perm(0x17161514u, 0x12100C00u, sel);
+  const uint32_t neg = __builtin_amdgcn_perm(0x2C303234u, 0x35363738u, sel);
+  const uint32_t m = ((nib >> 3) & 0x01010101u) * 0xFFu;
+  return (neg & m) | (pos & ~m);
+}
+
+// four 6-bit codes in the low bits of four bytes -> 24 contiguous bits
+__device__ __forceinline__ uint32_t pack6_x4(uint32_t b) {
+  return (b & 0x3Fu) | ((b >> 2) & 0xFC0u) | ((b >> 4) & 0x3F000u) | ((b >> 6) & 0xFC0000u);
+}
+
 __device__ __forceinline__ int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
 // ---------------------------------------------------------------------------
@@ -116,3 +133,24 @@ __device__ __forceinline__ void buf_store2(uint16_t v, rsrc_t r, uint32_t off) {
   __builtin_amdgcn_raw_buffer_store_b16(v, r, off, 0, 0);
 }
 constexpr uint32_t kOOB = 0x80000000u;  // an offset past every buffer this library builds (all < 2 GiB)
+
+// ---------------------------------------------------------------------------
+// GEMM tile order
+// ---------------------------------------------------------------------------
+constexpr int kXcds = 8;  // MI355X: workgroup i runs on XCD i % 8
+
+// workgroup id -> (tile_m, tile_n): a contiguous run of tiles per XCD, in an
+// order that walks GM tile rows before moving to the next tile column
+__device__ __forceinline__ bool xcd_tile_of(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
+  const int T = tiles_m * tiles_n;
+  const int per = (T + kXcds - 1) / kXcds;
+  const int t = (bid % kXcds) * per + bid / kXcds;
+  if (t >= T) return false;
+  constexpr int GM = 8;
+  const int band = t / (GM * tiles_n);
+  const int gm = min(GM, tiles_m - band * GM);
+  const int rem = t - band * GM * tiles_n;
+  tm = band * GM + rem % gm;
+  tn = rem / gm;
+  return true;
+}

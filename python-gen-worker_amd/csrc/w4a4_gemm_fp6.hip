@@ -1,0 +1,495 @@
+// W4A4 GEMM on gfx950's fp6 MFMA.
+//
+// Both operands arrive as e3m2 ("bf6") codes in fp6 operand records (one
+// 104-byte record per 128-element stage of K and row, stage-major: 96 bytes
+// of codes, the stage's two fp16 group scales, 4 unused bytes): the
+// activations straight from the act-quant kernel (GWA_QFMT_FP6), the weights
+// prepacked once (gwa_svdq_pack_weight_fp6). Every int4 code -8..7 is an exact
+// e3m2 value and the MFMA accumulates in fp32, so ONE
+// v_mfma_scale_f32_32x32x64_f8f6f4 (unit E8M0 scales) returns the exact
+// integer dot product P of a 64-element group for a 32 x 32 block
+// (|P| <= 4096), at twice the fp8/int8 MFMA rate.
+//
+// Dequantization, per group g, 32 x 32 block and element (n, m):
+//     acc += P * S,    S = sw[n][g] * sx[m][g]
+// S is the outer product of two f16 vectors, formed exactly (fp32 result) by
+// one f16 MFMA (32x32x8): lanes 0..31 of the weight-side operand hold the
+// stage's 2 group scales of their row in K slots 0..1 and lanes 32..63 hold
+// zeros; the activation-side operand holds group g's scale in slot g and zero
+// in the other slot. That leaves one VALU fma per output element and group.
+//
+// Epilogue: acc * s2 * second[n], + la @ up^T (bf16 MFMA), + bias, optional
+// GELU (tanh form), four consecutive n per lane packed to bf16 / f16.
+//
+// Tiling: a 512-thread workgroup owns a 256 (n) x 256 (m) output tile; its 8
+// waves form a 4 x 2 grid of 64 (n) x 128 (m) wave tiles (2 x 4 blocks), two
+// waves per SIMD. Operand delivery, not the MFMA, bounds this kernel, so the
+// tile is as large as the register file allows (each staged operand byte
+// feeds 256 outputs). A tile's stage of operand rows is one contiguous run of
+// records, copied linearly into LDS by direct-to-LDS buffer loads
+// (buffer_load_dwordx4 ... lds: no staging registers, no ds_write, one address
+// register); the 104-byte record stride keeps the 32 rows a block reads on
+// distinct LDS bank pairs, and the scales arrive inside the records. Three
+// stage buffers rotate, filled two stages ahead. Every wave issues the same
+// number of DMA loads per stage, so one s_waitcnt vmcnt(N) before each
+// barrier completes exactly the stage about to be read while the newest
+// stays in flight. The stage loop is unrolled by three so every LDS read
+// names its buffer statically. Within a stage the 8 blocks run in a fixed
+// order (a scheduling fence after each), keeping one block's P and S live;
+// the other wave on the SIMD fills the matrix pipe meanwhile. Tiles are
+// ordered per XCD (xcd_tile_of) so operands stay in that XCD's L2.
+#include "gwa_common.h"
+
+namespace {
+
+constexpr int TN = 256, TM = 256;
+constexpr int WBN = 2, WBM = 4;
+constexpr int WAVES_N = TN / (32 * WBN), WAVES_M = TM / (32 * WBM);  // 4, 2
+constexpr int NWAVES = WAVES_N * WAVES_M;  // 8
+constexpr int NTHREADS = 64 * NWAVES;      // 512
+constexpr int GS = 2;                      // groups per stage (one record)
+constexpr int GB = 48;                     // bytes of one row's group (64 e3m2 codes)
+constexpr int REC = GWA_FP6_REC;           // 104: record = LDS row stride
+constexpr int OFF_SC = GS * GB;            // 96: the record's scales
+constexpr int LDS_X = TM * REC;            // 26624
+constexpr int LDS_W = TN * REC;            // 26624
+constexpr int OFF_W = LDS_X;
+constexpr int LDS_STAGE = LDS_X + LDS_W;   // 53248
+constexpr int DMA_X = LDS_X / 1024;        // 26 runs of 1 KiB (64 lanes x 16 B)
+constexpr int DMA_RUNS = LDS_STAGE / 1024;                   // 52
+constexpr int DMA_SLOTS = (DMA_RUNS + NWAVES - 1) / NWAVES;  // 7 per wave
+static_assert(LDS_X % 1024 == 0 && LDS_W % 1024 == 0 && DMA_RUNS > NWAVES * (DMA_SLOTS - 1), "DMA runs");
+static_assert(DMA_SLOTS < 64, "vmcnt range");
+constexpr int kFmtE3M2 = 3;                // cbsz / blgp code of e3m2 operands
+constexpr int kUnitE8M0 = 127;             // 2^0
+
+// Direct-to-LDS copy of 16 bytes per lane: LDS [m0 + 16 lane, +16) <- buffer
+// [voff + soff, +16). Issued as asm so the compiler's wait-count pass (which
+// tracks only a few LDS-DMA writes and then waits for all of them before any
+// LDS read) leaves the waits to the kernel: every LDS read of a stage buffer
+// comes after an s_waitcnt that covers this wave's copies into it and a
+// barrier that covers everyone else's. The "memory" clobber keeps the copy
+// in program order with the surrounding LDS accesses.
+__device__ __forceinline__ void dma16(v4i rsrc, uint32_t lds_addr, uint32_t voff, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(lds_addr), "v"(voff), "s"(rsrc), "s"(soff)
+               : "memory", "m0");
+}
+
+// raw buffer descriptor as an SGPR quad (base, stride 0, num_records, 32-bit data format)
+__device__ __forceinline__ v4i raw_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = (uint64_t)base;
+  return (v4i){(int)(uint32_t)a, (int)(uint32_t)((a >> 32) & 0xFFFFu), (int)bytes, 0x00020000};
+}
+
+// compiler-only fence: keeps LDS reads and writes on their side of a barrier
+__device__ __forceinline__ void barrier_lds() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+__shared__ __attribute__((aligned(16))) uint8_t g_stage0[LDS_STAGE];
+__shared__ __attribute__((aligned(16))) uint8_t g_stage1[LDS_STAGE];
+__shared__ __attribute__((aligned(16))) uint8_t g_stage2[LDS_STAGE];
+__shared__ __attribute__((aligned(16))) float g_epi[2 * TN];
+
+// s_waitcnt vmcnt(n) lgkmcnt(0) (gfx9 encoding; expcnt left at its maximum)
+template <int n>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+  static_assert(n >= 0 && n < 64, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4));
+}
+
+__device__ __forceinline__ v16f group_mfma_fp6(v8i a, v8i b) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, (v16f){}, kFmtE3M2, kFmtE3M2, 0, kUnitE8M0, 0,
+                                                         kUnitE8M0);
+}
+
+// one lane's 32 codes of a group half: 24 bytes, three 8-byte LDS reads
+__device__ __forceinline__ v8i lds_operand(const uint8_t* p) {
+  const uint2 a = *(const uint2*)(p), b = *(const uint2*)(p + 8), c = *(const uint2*)(p + 16);
+  const v8i v = (v8i){(int)a.x, (int)a.y, (int)b.x, (int)b.y, (int)c.x, (int)c.y, 0, 0};
+  return v;
+}
+
+__device__ __forceinline__ v8i buf_operand(rsrc_t r, uint32_t off) {
+  typedef unsigned int v2u __attribute__((ext_vector_type(2)));
+  const v2u a = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+  const v2u b = __builtin_amdgcn_raw_buffer_load_b64(r, off + 8, 0, 0);
+  const v2u c = __builtin_amdgcn_raw_buffer_load_b64(r, off + 16, 0, 0);
+  return (v8i){(int)a[0], (int)a[1], (int)b[0], (int)b[1], (int)c[0], (int)c[1], 0, 0};
+}
+
+template <int RB, bool GELU, bool OUT_F16>
+__global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_kernel(
+    const uint8_t* __restrict__ qa, const uint8_t* __restrict__ qw, const float* __restrict__ s2p,
+    const float* __restrict__ second, int second_per_channel, const uint16_t* __restrict__ la,
+    const uint16_t* __restrict__ up, const uint16_t* __restrict__ bias, uint16_t* __restrict__ out, int M, int N,
+    int K) {
+  const int tid = threadIdx.x;
+  const int tiles_n = (N + TN - 1) / TN, tiles_m = (M + TM - 1) / TM;
+  int tm, tn;
+  if (!xcd_tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn)) return;  // whole workgroup, before any barrier
+  const int n0 = tn * TN, m0 = tm * TM;
+  const int nst = K >> 7;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int wn = wave % WAVES_N, wm = wave / WAVES_N;
+  const int r32 = lane & 31, h = lane >> 5;
+
+  const v4i xbuf = raw_rsrc(qa, (uint32_t)((int64_t)nst * M * REC));
+  const v4i wbuf = raw_rsrc(qw, (uint32_t)((int64_t)nst * N * REC));
+
+  // DMA: run q of a stage is LDS bytes [1024 q, +1024) of the stage buffer =
+  // bytes [1024 q', +1024) of the tile's contiguous records (q' = q for the
+  // activations, q - DMA_X for the weights). Runs are dealt round-robin; the
+  // waves left without a 7th run repeat one of the last runs (same bytes to
+  // the same place), so every wave issues DMA_SLOTS loads per stage. Rows past
+  // M / N read the next stage's records (their outputs are never stored) or
+  // nothing (past the buffer: zeros).
+  const uint32_t dvo = 16u * (uint32_t)lane;
+  // copy j (0 .. DMA_SLOTS-1) of this wave's share of stage st into `stage`
+  auto issue_one = [&](uint8_t* stage, int st, int j) __attribute__((always_inline)) {
+    int q = wave + NWAVES * j;
+    q = q < DMA_RUNS ? q : q - NWAVES / 2;
+    const bool isx = q < DMA_X;
+    const uint32_t base = isx ? (uint32_t)(((int64_t)st * M + m0) * REC) + q * 1024
+                              : (uint32_t)(((int64_t)st * N + n0) * REC) + (q - DMA_X) * 1024;
+    dma16(isx ? xbuf : wbuf, (uint32_t)(uintptr_t)(stage + q * 1024), dvo, base);
+  };
+  auto issue = [&](uint8_t* stage, int st) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < DMA_SLOTS; ++j) issue_one(stage, st, j);
+  };
+
+  v16f acc[WBN][WBM];
+#pragma unroll
+  for (int a = 0; a < WBN; ++a)
+#pragma unroll
+    for (int b = 0; b < WBM; ++b) acc[a][b] = (v16f){};
+
+  // One stage, blocks in (bn, bm) order, so one block's P and S are live at a
+  // time: empty asm statements on each block's scale operand and accumulator
+  // pin the block's MFMAs and fmas in program order (the MFMA intrinsics are
+  // pure and would otherwise be regrouped across blocks). A group's operands stay in
+  // registers; each is refilled with the next group's operand right after its
+  // last use (the first group of a stage is read at the stage start: the
+  // next stage's buffer is only complete after the barrier).
+  auto compute = [&](const uint8_t* base) __attribute__((always_inline)) {
+    const uint8_t* lx = base + (32 * WBM * wm + r32) * REC + 24 * h;
+    const uint8_t* lw = base + OFF_W + (32 * WBN * wn + r32) * REC + 24 * h;
+    const uint8_t* sx = base + (32 * WBM * wm + r32) * REC + OFF_SC;
+    const uint8_t* sw = base + OFF_W + (32 * WBN * wn + r32) * REC + OFF_SC;
+    v8i xo[WBM], wo[WBN];
+    uint32_t xs[WBM], ws[WBN];
+#pragma unroll
+    for (int bn = 0; bn < WBN; ++bn) {
+      wo[bn] = lds_operand(lw + bn * 32 * REC);
+      const uint32_t v = *(const uint32_t*)(sw + bn * 32 * REC);
+      ws[bn] = h ? 0u : v;  // K slots 4..7 (lanes 32..63) stay zero
+    }
+#pragma unroll
+    for (int bm = 0; bm < WBM; ++bm) {
+      xo[bm] = lds_operand(lx + bm * 32 * REC);
+      xs[bm] = *(const uint32_t*)(sx + bm * 32 * REC);
+    }
+#pragma unroll
+    for (int gi = 0; gi < GS; ++gi) {
+      const uint32_t mask = gi ? 0xFFFF0000u : 0x0000FFFFu;
+#pragma unroll
+      for (int bn = 0; bn < WBN; ++bn) {
+        const v4h swop = __builtin_bit_cast(v4h, make_uint2(ws[bn], 0u));
+#pragma unroll
+        for (int bm = 0; bm < WBM; ++bm) {
+          uint32_t s1 = xs[bm] & mask;
+          asm volatile("" : "+v"(s1));  // keeps this S MFMA here (it would otherwise be hoisted to the stage start)
+          const v4h sel = __builtin_bit_cast(v4h, make_uint2(s1, 0u));
+          const v16f p = group_mfma_fp6(wo[bn], xo[bm]);
+          const v16f sv = __builtin_amdgcn_mfma_f32_32x32x8f16(swop, sel, (v16f){}, 0, 0, 0);
+#pragma unroll
+          for (int v = 0; v < 16; ++v) acc[bn][bm][v] = fmaf(p[v], sv[v], acc[bn][bm][v]);
+          asm volatile("" : "+v"(acc[bn][bm]));  // this block's fmas complete here, in program order
+          if (gi + 1 < GS) {
+            if (bn == WBN - 1) xo[bm] = lds_operand(lx + bm * 32 * REC + (gi + 1) * GB);
+            if (bm == WBM - 1) wo[bn] = lds_operand(lw + bn * 32 * REC + (gi + 1) * GB);
+          }
+        }
+      }
+    }
+  };
+  // one stage: prefetch stage st + 2 into pf, compute on cur, then make stage
+  // st + 1 complete (this wave's loads, then everyone's) before moving on
+  auto stage = [&](int st, const uint8_t* cur, uint8_t* pf) __attribute__((always_inline)) {
+    const bool more = st + 2 < nst;
+    if (more) issue(pf, st + 2);
+    compute(cur);
+    if (more) wait_vm_lgkm0<DMA_SLOTS>();
+    else wait_vm_lgkm0<0>();
+    barrier_lds();
+  };
+
+  // the tile's per-column epilogue constants: s2 * second[n] and bias[n]
+  if (tid < TN) {
+    const int n = n0 + tid;
+    float mult = 0.0f, bv = 0.0f;
+    if (n < N) {
+      mult = s2p ? *s2p : 1.0f;
+      if (second) mult *= second[second_per_channel ? n : 0];
+      if (bias) bv = bf16_to_f32(bias[n]);
+    }
+    g_epi[tid] = mult;
+    g_epi[TN + tid] = bv;
+  }
+  __syncthreads();  // the epilogue constants' loads are complete before any copy is in flight
+  issue(g_stage0, 0);
+  if (nst > 1) {
+    issue(g_stage1, 1);
+    wait_vm_lgkm0<DMA_SLOTS>();
+  } else {
+    wait_vm_lgkm0<0>();
+  }
+  barrier_lds();
+  for (int st = 0; st < nst; st += 3) {
+    stage(st, g_stage0, g_stage2);
+    if (st + 1 < nst) stage(st + 1, g_stage1, g_stage0);
+    if (st + 2 < nst) stage(st + 2, g_stage2, g_stage1);
+  }
+
+  // ---------------- epilogue ----------------
+#pragma unroll
+  for (int bn = 0; bn < WBN; ++bn) {
+    const int nl = 32 * (WBN * wn + bn);
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd) {
+      const v4f cm = *(const v4f*)(g_epi + nl + 8 * qd + 4 * h);
+#pragma unroll
+      for (int bm = 0; bm < WBM; ++bm)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[bn][bm][4 * qd + e] *= cm[e];
+    }
+  }
+  if (RB > 0) {
+    constexpr int RC = RB < 2 ? RB : 2;
+    const rsrc_t ubuf = make_rsrc(up, (uint32_t)((int64_t)N * RB * 32));
+    const rsrc_t lbuf = make_rsrc(la, (uint32_t)((int64_t)M * RB * 32));
+#pragma unroll
+    for (int k0 = 0; k0 < RB; k0 += RC) {
+      v4i ua[WBN][RC > 0 ? RC : 1], lb[WBM][RC > 0 ? RC : 1];
+#pragma unroll
+      for (int bn = 0; bn < WBN; ++bn)
+#pragma unroll
+        for (int kk = 0; kk < RC; ++kk)
+          ua[bn][kk] = buf_load16(
+              ubuf, (uint32_t)((int64_t)(n0 + 32 * (WBN * wn + bn) + r32) * (RB * 32) + (k0 + kk) * 32 + 16 * h));
+#pragma unroll
+      for (int bm = 0; bm < WBM; ++bm)
+#pragma unroll
+        for (int kk = 0; kk < RC; ++kk)
+          lb[bm][kk] = buf_load16(
+              lbuf, (uint32_t)((int64_t)(m0 + 32 * (WBM * wm + bm) + r32) * (RB * 32) + (k0 + kk) * 32 + 16 * h));
+#pragma unroll
+      for (int bn = 0; bn < WBN; ++bn)
+#pragma unroll
+        for (int bm = 0; bm < WBM; ++bm)
+#pragma unroll
+          for (int kk = 0; kk < RC; ++kk)
+            acc[bn][bm] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, ua[bn][kk]),
+                                                                  __builtin_bit_cast(v8bf, lb[bm][kk]), acc[bn][bm],
+                                                                  0, 0, 0);
+    }
+  }
+  const rsrc_t obuf = make_rsrc(out, (uint32_t)((int64_t)M * N * 2));
+#pragma unroll
+  for (int bn = 0; bn < WBN; ++bn) {
+    const int nl = 32 * (WBN * wn + bn);
+#pragma unroll
+    for (int bm = 0; bm < WBM; ++bm) {
+      const int m = m0 + 32 * (WBM * wm + bm) + r32;
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd) {
+        const int n = n0 + nl + 8 * qd + 4 * h;
+        const v4f cb = *(const v4f*)(g_epi + TN + nl + 8 * qd + 4 * h);
+        float o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float t = acc[bn][bm][4 * qd + e] + cb[e];
+          if (GELU) t = gelu_tanh_f32(t);
+          o[e] = t;
+        }
+        uint2 pk;
+        if (OUT_F16) {
+          pk.x = pack_f16x2(o[0], o[1]);
+          pk.y = pack_f16x2(o[2], o[3]);
+        } else {
+          pk.x = pack_bf16x2_rn(o[0], o[1]);
+          pk.y = pack_bf16x2_rn(o[2], o[3]);
+        }
+        // branch-free store after the MFMAs: rows >= M / columns >= N fall outside the buffer
+        const uint32_t off = (m < M && n < N) ? (uint32_t)(((int64_t)m * N + n) * 2) : kOOB;
+        buf_store8(pk, obuf, off);
+      }
+    }
+  }
+}
+
+// Exact per-group partial sums through the same fp6 MFMA (debug / parity):
+// out[m][n][g] = sum_{k in g} qa[m][k] * qw[n][k], one wave per 32 x 32 block.
+__global__ __launch_bounds__(64) void w4a4_psums_fp6_kernel(const uint8_t* __restrict__ qa,
+                                                            const uint8_t* __restrict__ qw,
+                                                            int32_t* __restrict__ out, int M, int N, int K) {
+  const int lane = threadIdx.x, r32 = lane & 31, h = lane >> 5;
+  const int m0 = blockIdx.x * 32, n0 = blockIdx.y * 32;
+  const int G = K >> 6, nst = K >> 7;
+  const int m = m0 + r32, nr = n0 + r32;
+  const rsrc_t xbuf = make_rsrc(qa, (uint32_t)((int64_t)nst * M * REC));
+  const rsrc_t wbuf = make_rsrc(qw, (uint32_t)((int64_t)nst * N * REC));
+  const rsrc_t obuf = make_rsrc(out, (uint32_t)((int64_t)M * N * G * 4));
+  for (int g = 0; g < G; ++g) {
+    const int st = g >> 1, in = (g & 1) * GB + 24 * h;
+    // rows past M / N load zeros
+    const v8i a = buf_operand(wbuf, nr < N ? (uint32_t)(((int64_t)st * N + nr) * REC + in) : kOOB);
+    const v8i b = buf_operand(xbuf, m < M ? (uint32_t)(((int64_t)st * M + m) * REC + in) : kOOB);
+    const v16f p = group_mfma_fp6(a, b);
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int n = n0 + 8 * (v >> 2) + 4 * h + (v & 3);
+      const uint32_t off = (m < M && n < N) ? (uint32_t)((((int64_t)m * N + n) * G + g) * 4) : kOOB;
+      buf_store4((uint32_t)(int32_t)p[v], obuf, off);
+    }
+  }
+}
+
+// int4 weight rows (two's-complement nibbles, element 2j in the low nibble of
+// byte j) + fp16 group scales -> fp6 operand records: one thread per (row,
+// group, half) turns 16 bytes (32 codes) into 24 bytes with code t at bits
+// [6t, 6t + 6); the first half also stores the group's scale and, for the
+// stage's first group, zeros the record's unused bytes.
+__global__ __launch_bounds__(256) void pack_weight_fp6_kernel(const uint8_t* __restrict__ qw,
+                                                              const uint16_t* __restrict__ sw,
+                                                              uint8_t* __restrict__ qw6, int N, int K) {
+  const int G = K >> 6;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)N * G * 2) return;
+  const int64_t row = i / (2 * G);
+  const int rem = (int)(i - row * 2 * G), g = rem >> 1, hh = rem & 1;
+  const uint32_t* src = (const uint32_t*)(qw + row * (K / 2) + g * 32 + hh * 16);
+  uint64_t pc[4];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const uint32_t w = src[d];
+    const uint32_t ev = w & 0x0F0F0F0Fu, od = (w >> 4) & 0x0F0F0F0Fu;  // codes 8d + 0,2,4,6 / 8d + 1,3,5,7
+    const uint32_t c0 = __builtin_amdgcn_perm(od, ev, 0x05010400u);    // codes 8d + 0..3, one per byte
+    const uint32_t c1 = __builtin_amdgcn_perm(od, ev, 0x07030602u);    // codes 8d + 4..7
+    pc[d] = (uint64_t)pack6_x4(e3m2_x4(c0)) | ((uint64_t)pack6_x4(e3m2_x4(c1)) << 24);
+  }
+  uint8_t* rec = qw6 + ((int64_t)(g >> 1) * N + row) * REC;
+  uint32_t* dst = (uint32_t*)(rec + (g & 1) * GB + hh * 24);
+  dst[0] = (uint32_t)pc[0];
+  dst[1] = (uint32_t)((pc[0] >> 32) | (pc[1] << 16));
+  dst[2] = (uint32_t)(pc[1] >> 16);
+  dst[3] = (uint32_t)pc[2];
+  dst[4] = (uint32_t)((pc[2] >> 32) | (pc[3] << 16));
+  dst[5] = (uint32_t)(pc[3] >> 16);
+  if (hh == 0) {
+    *(uint16_t*)(rec + OFF_SC + (g & 1) * 2) = sw[row * G + g];
+    if ((g & 1) == 0) *(uint32_t*)(rec + OFF_SC + 4) = 0u;
+  }
+}
+
+}  // namespace
+
+extern "C" int gwa_svdq_pack_weight_fp6(const uint8_t* qw, const void* sw, uint8_t* qw6, int64_t N, int64_t K,
+                                        void* stream) {
+  GWA_REQUIRE(N > 0 && K > 0 && K % 128 == 0, "svdq_pack_weight_fp6: bad shape N=%lld K=%lld (K %% 128 == 0)",
+              (long long)N, (long long)K);
+  GWA_REQUIRE(N * (K / 64) * 2 < (1ll << 40) && K < (1ll << 30), "svdq_pack_weight_fp6: shape too large");
+  GWA_REQUIRE(qw && sw && qw6, "svdq_pack_weight_fp6: null pointer");
+  GWA_REQUIRE(GWA_ALIGNED(qw, 4) && GWA_ALIGNED(qw6, 8) && GWA_ALIGNED(sw, 2), "svdq_pack_weight_fp6: misaligned pointer");
+  const int64_t threads = N * (K / 64) * 2;
+  hipLaunchKernelGGL(pack_weight_fp6_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, qw, (const uint16_t*)sw, qw6, (int)N, (int)K);
+  return gwa_check_launch("svdq_pack_weight_fp6");
+}
+
+extern "C" int gwa_svdq_group_psums_fp6(const uint8_t* qa6, const uint8_t* qw6, int32_t* out, int64_t M, int64_t N,
+                                        int64_t K, void* stream) {
+  GWA_REQUIRE(M >= 0 && N >= 0 && K > 0 && K % 128 == 0, "svdq_group_psums_fp6: bad shape (K %% 128 == 0)");
+  GWA_REQUIRE(M < (1ll << 31) && N < (1ll << 30) && K < (1ll << 30) && M * N * (K / 64) * 4 < (1ll << 31) &&
+                  M * (K / 128) * REC < (1ll << 31) && N * (K / 128) * REC < (1ll << 31),
+              "svdq_group_psums_fp6: shape too large (buffers must stay below 2 GiB)");
+  GWA_REQUIRE((N + 31) / 32 < 65536, "svdq_group_psums_fp6: N too large");
+  if (M == 0 || N == 0) return GWA_OK;
+  GWA_REQUIRE(qa6 && qw6 && out, "svdq_group_psums_fp6: null pointer");
+  GWA_REQUIRE(GWA_ALIGNED(qa6, 8) && GWA_ALIGNED(qw6, 8) && GWA_ALIGNED(out, 4),
+              "svdq_group_psums_fp6: misaligned pointer");
+  hipLaunchKernelGGL(w4a4_psums_fp6_kernel, dim3((unsigned)((M + 31) / 32), (unsigned)((N + 31) / 32)), dim3(64), 0,
+                     (hipStream_t)stream, qa6, qw6, out, (int)M, (int)N, (int)K);
+  return gwa_check_launch("svdq_group_psums_fp6");
+}
+
+extern "C" int gwa_svdq_gemm_w4a4_fp6(const uint8_t* qa6, const uint8_t* qw6, const float* s2, const float* second,
+                                      int64_t second_numel, const void* la, const void* up, int64_t rank,
+                                      const void* bias, void* out, int out_dtype, int epilogue_flags, int64_t M,
+                                      int64_t N, int64_t K, void* stream) {
+  GWA_REQUIRE(M >= 0 && N > 0 && K > 0, "svdq_gemm_w4a4_fp6: bad shape M=%lld N=%lld K=%lld", (long long)M,
+              (long long)N, (long long)K);
+  GWA_REQUIRE(K % 128 == 0, "svdq_gemm_w4a4_fp6: K=%lld is not a multiple of 128", (long long)K);
+  GWA_REQUIRE(N % 16 == 0, "svdq_gemm_w4a4_fp6: N=%lld is not a multiple of 16", (long long)N);
+  GWA_REQUIRE(out_dtype == GWA_DT_BF16 || out_dtype == GWA_DT_F16, "svdq_gemm_w4a4_fp6: out_dtype %d", out_dtype);
+  GWA_REQUIRE((la == nullptr) == (up == nullptr), "svdq_gemm_w4a4_fp6: la and up must both be given or both NULL");
+  const int64_t R = la ? rank : 0;
+  GWA_REQUIRE(R == 0 || R == 16 || R == 32 || R == 64 || R == 128,
+              "svdq_gemm_w4a4_fp6: rank %lld not in {0,16,32,64,128}", (long long)R);
+  GWA_REQUIRE(second == nullptr || second_numel == 1 || second_numel == N,
+              "svdq_gemm_w4a4_fp6: second has %lld values for N=%lld", (long long)second_numel, (long long)N);
+  GWA_REQUIRE((epilogue_flags & ~GWA_EPI_GELU_TANH) == 0, "svdq_gemm_w4a4_fp6: unknown epilogue flags 0x%x",
+              epilogue_flags);
+  const int64_t nst = K / 128;
+  // the DMA offsets of a tile's last run stay below 2^31 + 2^16
+  GWA_REQUIRE(nst * (M + TM) * REC < (1ll << 31) && nst * (N + TN) * REC < (1ll << 31) && M * N * 2 < (1ll << 31) &&
+                  M * R * 2 < (1ll << 31),
+              "svdq_gemm_w4a4_fp6: operands must stay below 2 GiB (buffer addressing)");
+  if (M == 0) return GWA_OK;
+  GWA_REQUIRE(qa6 && qw6 && out, "svdq_gemm_w4a4_fp6: null pointer");
+  GWA_REQUIRE(GWA_ALIGNED(qa6, 16) && GWA_ALIGNED(qw6, 16) && GWA_ALIGNED(la, 16) && GWA_ALIGNED(up, 16) &&
+                  GWA_ALIGNED(out, 8) && GWA_ALIGNED(bias, 2) && GWA_ALIGNED(second, 4) && GWA_ALIGNED(s2, 4),
+              "svdq_gemm_w4a4_fp6: misaligned pointer");
+  const int64_t tiles = ((M + TM - 1) / TM) * ((N + TN - 1) / TN);
+  GWA_REQUIRE(tiles < (1ll << 30), "svdq_gemm_w4a4_fp6: too many tiles");
+  const bool gelu = epilogue_flags & GWA_EPI_GELU_TANH;
+  const bool f16 = out_dtype == GWA_DT_F16;
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t per_xcd = (tiles + kXcds - 1) / kXcds;
+  const dim3 grid((unsigned)(per_xcd * kXcds)), block(NTHREADS);
+  const int pc = second_numel > 1;
+  const uint16_t* lap = (const uint16_t*)la;
+  const uint16_t* upp = (const uint16_t*)up;
+  const uint16_t* bp = (const uint16_t*)bias;
+  uint16_t* op = (uint16_t*)out;
+  const int m = (int)M, n = (int)N, k = (int)K;
+#define GWA_FP6_LAUNCH(RBV, GL, F16V)                                                                              \
+  hipLaunchKernelGGL((w4a4_gemm_fp6_kernel<RBV, GL, F16V>), grid, block, 0, s, qa6, qw6, s2, second, pc, lap, upp, \
+                     bp, op, m, n, k)
+#define GWA_FP6_RB(RBV)                           \
+  case RBV:                                       \
+    if (gelu) {                                   \
+      if (f16) GWA_FP6_LAUNCH(RBV, true, true);   \
+      else GWA_FP6_LAUNCH(RBV, true, false);      \
+    } else {                                      \
+      if (f16) GWA_FP6_LAUNCH(RBV, false, true);  \
+      else GWA_FP6_LAUNCH(RBV, false, false);     \
+    }                                             \
+    break;
+  switch (R / 16) {
+    GWA_FP6_RB(0)
+    GWA_FP6_RB(1)
+    GWA_FP6_RB(2)
+    GWA_FP6_RB(4)
+    GWA_FP6_RB(8)
+    default: return gwa_set_error(GWA_ERR_INVALID, "svdq_gemm_w4a4_fp6: rank %lld", (long long)R);
+  }
+#undef GWA_FP6_RB
+#undef GWA_FP6_LAUNCH
+  return gwa_check_launch("svdq_gemm_w4a4_fp6");
+}

@@ -22,6 +22,7 @@ LIB_NAME = "libgen_worker_amd.so"
 DT_BF16, DT_F16, DT_F32 = 0, 1, 2
 EPI_GELU_TANH = 1
 QFMT_INT4, QFMT_FP6 = 0, 1
+FP6_REC = 104   # bytes per fp6 operand record (GWA_FP6_REC)
 
 
 class NativeUnavailable(RuntimeError):
@@ -47,10 +48,10 @@ _SIGNATURES: dict[str, tuple] = {
     "gwa_svdq_gemm_w4a4": (_vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _int, _int,
                            _i64, _i64, _i64, _vp),
     "gwa_svdq_group_psums": (_vp, _vp, _vp, _i64, _i64, _i64, _vp),
-    "gwa_svdq_pack_weight_int4": (_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp),
-    "gwa_svdq_gemm_w4a4_packed": (_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _int,
-                                  _int, _i64, _i64, _i64, _vp),
-    "gwa_svdq_group_psums_packed": (_vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp),
+    "gwa_svdq_pack_weight_fp6": (_vp, _vp, _vp, _i64, _i64, _vp),
+    "gwa_svdq_gemm_w4a4_fp6": (_vp, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _int, _int,
+                               _i64, _i64, _i64, _vp),
+    "gwa_svdq_group_psums_fp6": (_vp, _vp, _vp, _i64, _i64, _i64, _vp),
     "gwa_svdq_epilogue_lora": (_vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _i64, _i64, _vp),
     "gwa_w8a8_quant_int8": (_vp, _i64, _vp, _vp, _i64, _i64, _vp),
     "gwa_w8a8_gemm": (_vp, _vp, _vp, _vp, _vp, _int, _vp, _int, _i64, _i64, _i64, _vp),

@@ -22,7 +22,8 @@ LIB_NAME = "libgen_worker_amd.so"
 LIB_PATH = PKG_DIR / LIB_NAME
 ARCH = "gfx950"
 
-SOURCES = ("gwa_runtime.hip", "act_quant.hip", "w4a4_gemm.hip", "w4a4_gemm_fp8.hip", "w8a8_gemm.hip")
+SOURCES = ("gwa_runtime.hip", "act_quant.hip", "w4a4_gemm.hip", "w4a4_gemm_fp6.hip",
+           "w8a8_gemm.hip")
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",

@@ -20,9 +20,13 @@ separate steps):
   the operand order kernel 1 reads ([ceil(K/256)*256, rank], done once).
 * ``svdq_quant_lora(x2, smooth, s2, proj_down_op) -> (q, s, la)``: kernel 1
   with ``la = x2 @ proj_down`` fused.
-* ``svdq_quant_fp6(x2, smooth, s2, proj_down_op) -> (q6, s, la)``: the same
-  codes as e3m2 fp6 [M, 3K/4] for the fp6 GEMM (``la`` empty when
+* ``svdq_quant_fp6(x2, smooth, s2, proj_down_op) -> (q6, la)``: the same
+  codes and scales as fp6 operand records [K/128, M, 104] (e3m2 codes + fp16
+  group scales, the fp6 GEMM's operand format; ``la`` empty when
   ``proj_down_op`` is None).
+* ``svdq_pack_weight_fp6(weight, wscales)``, ``svdq_w4a4_linear_fp6(qa6,
+  weight_fp6, s2, second, la, up, bias, out_dtype, gelu)``,
+  ``svdq_group_psums_fp6(qa6, weight_fp6)``: the fp6 GEMM lane.
 * ``svdq_w4a4_linear(qa, sa, weight, wscales, s2, second, la, up, bias,
   out_dtype, gelu)``: kernel 2 on the resident ``weight`` [N, K/2] layout.
 * ``svdq_group_psums(qa, qw)``: exact int32 per-group partial sums (debug).
@@ -45,6 +49,7 @@ from torch import Tensor
 from . import _native as nat
 
 GROUP = 64
+FP6_STAGE = 128   # K elements per fp6 operand record
 
 
 class SvdqOpError(ValueError):
@@ -113,8 +118,14 @@ def _quant_impl(x2: Tensor, smooth: Optional[Tensor], s2: Optional[Tensor], proj
                               f"proj_down), got {tuple(proj_down_op.shape)}")
         rank = int(proj_down_op.shape[1])
     x2 = x2 if x2.stride(1) == 1 else x2.contiguous()
-    q = torch.empty(m, (3 * k) // 4 if fmt == nat.QFMT_FP6 else k // 2, dtype=torch.uint8, device=x2.device)
-    s = torch.empty(m, k // GROUP, dtype=torch.float16, device=x2.device)
+    if fmt == nat.QFMT_FP6:
+        if k % FP6_STAGE:
+            raise SvdqOpError(f"{name}: the fp6 records need K % {FP6_STAGE} == 0, got K={k}")
+        q = torch.empty(k // FP6_STAGE, m, nat.FP6_REC, dtype=torch.uint8, device=x2.device)
+        s = None   # the records carry the scales
+    else:
+        q = torch.empty(m, k // 2, dtype=torch.uint8, device=x2.device)
+        s = torch.empty(m, k // GROUP, dtype=torch.float16, device=x2.device)
     la = torch.empty(m, rank, dtype=torch.bfloat16, device=x2.device) if proj_down_op is not None else None
     nat.call("gwa_svdq_quant_int4", nat.ptr(x2), int(x2.stride(0)), nat.ptr(smooth), nat.ptr(s2),
              nat.ptr(proj_down_op), rank, fmt, nat.ptr(q), nat.ptr(s), nat.ptr(la), m, k, nat.stream_of(x2))
@@ -179,21 +190,20 @@ def _(x2, smooth, s2, proj_down_op):
 
 @torch.library.custom_op("cozy_gen_worker::svdq_quant_fp6", mutates_args=())
 def svdq_quant_fp6(x2: Tensor, smooth: Optional[Tensor], s2: Optional[Tensor],
-                   proj_down_op: Optional[Tensor]) -> tuple[Tensor, Tensor, Tensor]:
-    """Kernel 1 writing the codes as e3m2 fp6 [M, 3K/4] (the fp6 GEMM's operand format); la is [M, 0]
-    when ``proj_down_op`` is None."""
-    q, s, la = _quant_impl(x2, smooth, s2, proj_down_op, nat.QFMT_FP6)
+                   proj_down_op: Optional[Tensor]) -> tuple[Tensor, Tensor]:
+    """Kernel 1 writing fp6 operand records [K/128, M, 104] (e3m2 codes + the fp16 group scales: the fp6
+    GEMM's operand format); returns ``(records, la)``, la [M, 0] when ``proj_down_op`` is None."""
+    q, _, la = _quant_impl(x2, smooth, s2, proj_down_op, nat.QFMT_FP6)
     if la is None:
         la = x2.new_empty(int(x2.shape[0]), 0)
-    return q, s, la
+    return q, la
 
 
 @svdq_quant_fp6.register_fake
 def _(x2, smooth, s2, proj_down_op):
     m, k = int(x2.shape[0]), int(x2.shape[1])
     r = int(proj_down_op.shape[1]) if proj_down_op is not None else 0
-    return (x2.new_empty(m, (3 * k) // 4, dtype=torch.uint8), x2.new_empty(m, k // GROUP, dtype=torch.float16),
-            x2.new_empty(m, r, dtype=torch.bfloat16))
+    return (x2.new_empty(k // FP6_STAGE, m, nat.FP6_REC, dtype=torch.uint8), x2.new_empty(m, r, dtype=torch.bfloat16))
 
 
 # ---------------------------------------------------------------------------
@@ -255,39 +265,9 @@ def _(qa, sa, weight, wscales, s2, second, la, up, bias, out_dtype, gelu):
     return qa.new_empty(int(qa.shape[0]), int(weight.shape[0]), dtype=out_dtype)
 
 
-def _packed_impl(qa: Tensor, sa: Tensor, weight_packed: Tensor, wscales_packed: Tensor, wcorr: Tensor,
-                 escale: Tensor, s2: Optional[Tensor], second: Optional[Tensor], la: Optional[Tensor],
-                 up: Optional[Tensor], bias: Optional[Tensor], out_dtype: torch.dtype, gelu: bool) -> Tensor:
-    name = "svdq_w4a4_linear_packed"
-    s2 = _scalar_f32(name, s2)
-    if second is not None and second.dtype != torch.float32:
-        second = second.float().contiguous()
-    _check_dtype(name, qa, torch.uint8, what="qa")
-    _check_dtype(name, weight_packed, torch.uint8, what="weight_packed")
-    _check_dtype(name, sa, torch.float16, what="sa")
-    _check_dtype(name, wscales_packed, torch.float16, what="packed weight scales")
-    _check_dtype(name, wcorr, torch.float16, what="weight correction pairs")
-    _check_dtype(name, escale, torch.float32, what="row exponent scales")
-    _check_dtype(name, la, torch.bfloat16, what="la")
-    _check_dtype(name, up, torch.bfloat16, what="up")
-    _check_dtype(name, bias, torch.bfloat16, what="bias")
-    _check_cuda(name, qa=qa, sa=sa, weight_packed=weight_packed, wscales_packed=wscales_packed, wcorr=wcorr,
-                escale=escale, s2=s2, second=second, la=la, up=up, bias=bias)
-    if out_dtype not in (torch.bfloat16, torch.float16):
-        raise SvdqOpError(f"{name}: out_dtype {out_dtype} not bf16/fp16")
-    m, kh = int(qa.shape[0]), int(qa.shape[1])
-    k = 2 * kh
-    n = int(weight_packed.shape[0])
-    g = k // GROUP
-    if k % 256:
-        raise SvdqOpError(f"{name}: K={k} is not a multiple of 256 (use svdq_w4a4_linear)")
-    if (tuple(weight_packed.shape) != (n, kh) or tuple(wscales_packed.shape) != (n, g)
-            or tuple(wcorr.shape) != (n, g // 4, 8) or tuple(escale.shape) != (n,)):
-        raise SvdqOpError(f"{name}: prepacked weight {tuple(weight_packed.shape)} / scales "
-                          f"{tuple(wscales_packed.shape)} / corr {tuple(wcorr.shape)} / escale {tuple(escale.shape)} "
-                          f"do not match N={n}, K={k}")
-    if tuple(sa.shape) != (m, g):
-        raise SvdqOpError(f"{name}: activation scales {tuple(sa.shape)} do not match [M={m}, K/64={g}]")
+def _epilogue_operands(name: str, m: int, n: int, la: Optional[Tensor], up: Optional[Tensor],
+                       bias: Optional[Tensor], second: Optional[Tensor]) -> tuple[int, int]:
+    """Shape checks of the fused epilogue's operands; returns (rank, second_numel)."""
     if (la is None) != (up is None):
         raise SvdqOpError(f"{name}: la and up must both be given or both be None")
     rank = 0
@@ -297,89 +277,104 @@ def _packed_impl(qa: Tensor, sa: Tensor, weight_packed: Tensor, wscales_packed: 
             raise SvdqOpError(f"{name}: la {tuple(la.shape)} / up {tuple(up.shape)} do not match rank {rank}")
     if bias is not None and bias.numel() != n:
         raise SvdqOpError(f"{name}: bias has {bias.numel()} values for N={n}")
-    sec_n = 0 if second is None else int(second.numel())
-    out = torch.empty(m, n, dtype=out_dtype, device=qa.device)
-    nat.call("gwa_svdq_gemm_w4a4_packed", nat.ptr(qa), nat.ptr(sa), nat.ptr(weight_packed), nat.ptr(wscales_packed),
-             nat.ptr(wcorr), nat.ptr(escale), nat.ptr(s2), nat.ptr(second), sec_n, nat.ptr(la), nat.ptr(up), rank,
-             nat.ptr(bias), nat.ptr(out), _dt_code(out_dtype), nat.EPI_GELU_TANH if gelu else 0, m, n, k,
-             nat.stream_of(qa))
+    return rank, (0 if second is None else int(second.numel()))
+
+
+def _fp6_records_k(name: str, rec: Tensor, what: str) -> tuple[int, int]:
+    """(rows, K) of an fp6 operand record tensor [K/128, rows, 104]."""
+    if rec.dim() != 3 or int(rec.shape[2]) != nat.FP6_REC:
+        raise SvdqOpError(f"{name}: {what} must be fp6 records [K/{FP6_STAGE}, rows, {nat.FP6_REC}], "
+                          f"got {tuple(rec.shape)}")
+    return int(rec.shape[1]), int(rec.shape[0]) * FP6_STAGE
+
+
+def _fp6_impl(qa6: Tensor, weight_fp6: Tensor, s2: Optional[Tensor], second: Optional[Tensor],
+              la: Optional[Tensor], up: Optional[Tensor], bias: Optional[Tensor], out_dtype: torch.dtype,
+              gelu: bool) -> Tensor:
+    name = "svdq_w4a4_linear_fp6"
+    s2 = _scalar_f32(name, s2)
+    if second is not None and second.dtype != torch.float32:
+        second = second.float().contiguous()
+    _check_dtype(name, qa6, torch.uint8, what="qa6")
+    _check_dtype(name, weight_fp6, torch.uint8, what="weight_fp6")
+    _check_dtype(name, la, torch.bfloat16, what="la")
+    _check_dtype(name, up, torch.bfloat16, what="up")
+    _check_dtype(name, bias, torch.bfloat16, what="bias")
+    _check_cuda(name, qa6=qa6, weight_fp6=weight_fp6, s2=s2, second=second, la=la, up=up, bias=bias)
+    if out_dtype not in (torch.bfloat16, torch.float16):
+        raise SvdqOpError(f"{name}: out_dtype {out_dtype} not bf16/fp16")
+    m, k = _fp6_records_k(name, qa6, "qa6")
+    n, kw = _fp6_records_k(name, weight_fp6, "weight_fp6")
+    if kw != k:
+        raise SvdqOpError(f"{name}: activation K={k} and weight K={kw} differ")
+    rank, sec_n = _epilogue_operands(name, m, n, la, up, bias, second)
+    out = torch.empty(m, n, dtype=out_dtype, device=qa6.device)
+    nat.call("gwa_svdq_gemm_w4a4_fp6", nat.ptr(qa6), nat.ptr(weight_fp6.contiguous()), nat.ptr(s2), nat.ptr(second),
+             sec_n, nat.ptr(la), nat.ptr(up), rank, nat.ptr(bias), nat.ptr(out), _dt_code(out_dtype),
+             nat.EPI_GELU_TANH if gelu else 0, m, n, k, nat.stream_of(qa6))
     return out
 
 
-@torch.library.custom_op("cozy_gen_worker::svdq_w4a4_linear_packed", mutates_args=())
-def svdq_w4a4_linear_packed(qa: Tensor, sa: Tensor, weight_packed: Tensor, wscales_packed: Tensor, wcorr: Tensor,
-                            escale: Tensor, s2: Optional[Tensor], second: Optional[Tensor], la: Optional[Tensor],
-                            up: Optional[Tensor], bias: Optional[Tensor], out_dtype: torch.dtype,
-                            gelu: bool) -> Tensor:
-    """Fast W4A4 GEMM + fused epilogue on prepacked weights (the outputs of ``svdq_pack_weight``)."""
-    return _packed_impl(qa, sa, weight_packed, wscales_packed, wcorr, escale, s2, second, la, up, bias, out_dtype,
-                        gelu)
+@torch.library.custom_op("cozy_gen_worker::svdq_w4a4_linear_fp6", mutates_args=())
+def svdq_w4a4_linear_fp6(qa6: Tensor, weight_fp6: Tensor, s2: Optional[Tensor], second: Optional[Tensor],
+                         la: Optional[Tensor], up: Optional[Tensor], bias: Optional[Tensor], out_dtype: torch.dtype,
+                         gelu: bool) -> Tensor:
+    """W4A4 GEMM + fused epilogue on fp6 operand records (``svdq_quant_fp6`` activations,
+    ``svdq_pack_weight_fp6`` weights)."""
+    return _fp6_impl(qa6, weight_fp6, s2, second, la, up, bias, out_dtype, gelu)
 
 
-@svdq_w4a4_linear_packed.register_fake
-def _(qa, sa, weight_packed, wscales_packed, wcorr, escale, s2, second, la, up, bias, out_dtype, gelu):
-    return qa.new_empty(int(qa.shape[0]), int(weight_packed.shape[0]), dtype=out_dtype)
+@svdq_w4a4_linear_fp6.register_fake
+def _(qa6, weight_fp6, s2, second, la, up, bias, out_dtype, gelu):
+    return qa6.new_empty(int(qa6.shape[1]), int(weight_fp6.shape[1]), dtype=out_dtype)
 
 
-@torch.library.custom_op("cozy_gen_worker::svdq_pack_weight", mutates_args=())
-def svdq_pack_weight(weight: Tensor, wscales: Tensor) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
-    """Prepack logical int4 weights [N, K/2] with their fp16 group scales [N, K/64] for the fast GEMM.
-
-    Returns ``(packed [N, K/2] uint8, sums [N, K/64] int16, count [1] int32 of -8 codes,
-    wscales_packed [N, K/64] fp16, wcorr [N, ceil(K/256), 8] fp16, escale [N] fp32)``."""
-    name = "svdq_pack_weight"
+@torch.library.custom_op("cozy_gen_worker::svdq_pack_weight_fp6", mutates_args=())
+def svdq_pack_weight_fp6(weight: Tensor, wscales: Tensor) -> Tensor:
+    """Logical int4 weights [N, K/2] + fp16 group scales [N, K/64] -> fp6 operand records
+    [K/128, N, 104] (any code in [-8, 7])."""
+    name = "svdq_pack_weight_fp6"
     _check_dtype(name, weight, torch.uint8, what="weight")
     _check_dtype(name, wscales, torch.float16, what="wscales")
     _check_cuda(name, weight=weight, wscales=wscales)
     n, kh = int(weight.shape[0]), int(weight.shape[1])
     k = 2 * kh
-    if k % GROUP:
-        raise SvdqOpError(f"{name}: K={k} is not a multiple of {GROUP}")
-    g = k // GROUP
-    if tuple(wscales.shape) != (n, g):
-        raise SvdqOpError(f"{name}: wscales {tuple(wscales.shape)} do not match [N={n}, K/64={g}]")
-    weight = weight.contiguous()
-    wscales = wscales.contiguous()
-    packed = torch.empty_like(weight)
-    wsum = torch.empty(n, g, dtype=torch.int16, device=weight.device)
-    count = torch.zeros(1, dtype=torch.int32, device=weight.device)
-    swp = torch.empty(n, g, dtype=torch.float16, device=weight.device)
-    wcorr = torch.empty(n, (g + 3) // 4, 8, dtype=torch.float16, device=weight.device)
-    escale = torch.empty(n, dtype=torch.float32, device=weight.device)
-    nat.call("gwa_svdq_pack_weight_int4", nat.ptr(weight), nat.ptr(wscales), nat.ptr(packed), nat.ptr(wsum),
-             nat.ptr(swp), nat.ptr(wcorr), nat.ptr(escale), nat.ptr(count), n, k, nat.stream_of(weight))
-    return packed, wsum, count, swp, wcorr, escale
-
-
-@svdq_pack_weight.register_fake
-def _(weight, wscales):
-    n, kh = int(weight.shape[0]), int(weight.shape[1])
-    g = (2 * kh) // GROUP
-    return (torch.empty_like(weight), weight.new_empty(n, g, dtype=torch.int16),
-            weight.new_empty(1, dtype=torch.int32), weight.new_empty(n, g, dtype=torch.float16),
-            weight.new_empty(n, (g + 3) // 4, 8, dtype=torch.float16), weight.new_empty(n, dtype=torch.float32))
-
-
-@torch.library.custom_op("cozy_gen_worker::svdq_group_psums_packed", mutates_args=())
-def svdq_group_psums_packed(qa: Tensor, weight_packed: Tensor, wsum: Tensor) -> Tensor:
-    """Exact int32 [M, N, K/64] per-group partial sums through the fast path's fp8 arithmetic (debug)."""
-    name = "svdq_group_psums_packed"
-    _check_dtype(name, qa, torch.uint8, what="qa")
-    _check_dtype(name, weight_packed, torch.uint8, what="weight_packed")
-    _check_dtype(name, wsum, torch.int16, what="wsum")
-    _check_cuda(name, qa=qa, weight_packed=weight_packed, wsum=wsum)
-    m, kh = int(qa.shape[0]), int(qa.shape[1])
-    n = int(weight_packed.shape[0])
-    out = torch.empty(m, n, (2 * kh) // GROUP, dtype=torch.int32, device=qa.device)
-    nat.call("gwa_svdq_group_psums_packed", nat.ptr(qa), nat.ptr(weight_packed), nat.ptr(wsum), nat.ptr(out), m, n,
-             2 * kh, nat.stream_of(qa))
+    if k % FP6_STAGE:
+        raise SvdqOpError(f"{name}: K={k} is not a multiple of {FP6_STAGE}")
+    if tuple(wscales.shape) != (n, k // GROUP):
+        raise SvdqOpError(f"{name}: wscales {tuple(wscales.shape)} do not match [N={n}, K/64={k // GROUP}]")
+    out = torch.empty(k // FP6_STAGE, n, nat.FP6_REC, dtype=torch.uint8, device=weight.device)
+    nat.call("gwa_svdq_pack_weight_fp6", nat.ptr(weight.contiguous()), nat.ptr(wscales.contiguous()), nat.ptr(out),
+             n, k, nat.stream_of(weight))
     return out
 
 
-@svdq_group_psums_packed.register_fake
-def _(qa, weight_packed, wsum):
-    return qa.new_empty(int(qa.shape[0]), int(weight_packed.shape[0]), (2 * int(qa.shape[1])) // GROUP,
-                        dtype=torch.int32)
+@svdq_pack_weight_fp6.register_fake
+def _(weight, wscales):
+    return weight.new_empty(int(weight.shape[1]) * 2 // FP6_STAGE, int(weight.shape[0]), nat.FP6_REC)
+
+
+@torch.library.custom_op("cozy_gen_worker::svdq_group_psums_fp6", mutates_args=())
+def svdq_group_psums_fp6(qa6: Tensor, weight_fp6: Tensor) -> Tensor:
+    """Exact int32 [M, N, K/64] per-group partial sums through the fp6 GEMM's MFMA (debug)."""
+    name = "svdq_group_psums_fp6"
+    _check_dtype(name, qa6, torch.uint8, what="qa6")
+    _check_dtype(name, weight_fp6, torch.uint8, what="weight_fp6")
+    _check_cuda(name, qa6=qa6, weight_fp6=weight_fp6)
+    m, k = _fp6_records_k(name, qa6, "qa6")
+    n, kw = _fp6_records_k(name, weight_fp6, "weight_fp6")
+    if kw != k:
+        raise SvdqOpError(f"{name}: activation K={k} and weight K={kw} differ")
+    out = torch.empty(m, n, k // GROUP, dtype=torch.int32, device=qa6.device)
+    nat.call("gwa_svdq_group_psums_fp6", nat.ptr(qa6.contiguous()), nat.ptr(weight_fp6.contiguous()), nat.ptr(out),
+             m, n, k, nat.stream_of(qa6))
+    return out
+
+
+@svdq_group_psums_fp6.register_fake
+def _(qa6, weight_fp6):
+    return qa6.new_empty(int(qa6.shape[1]), int(weight_fp6.shape[1]), int(qa6.shape[0]) * FP6_STAGE // GROUP,
+                         dtype=torch.int32)
 
 
 @torch.library.custom_op("cozy_gen_worker::svdq_gemm_w4a4_lora", mutates_args=())

@@ -7,6 +7,10 @@ same buffer names (``weight``, ``weight_scale``, ``second``,
 structure (``:516-527``: quantize -> W4A4 GEMM -> low-rank + bias epilogue),
 but two launches instead of four: kernel 1 fuses the smoothing, the act-quant
 and ``x2 @ proj_down``; kernel 2 fuses the GEMM with the whole epilogue.
+With ``in_features % 128 == 0`` (the fp6 lane) kernel 1 writes its codes and
+scales as fp6 operand records and the GEMM runs on gfx950's fp6 MFMA against
+weights prepacked into the same records (``weight_fp6``); other shapes use
+the int4 codes and the int8-MFMA GEMM.
 
 Buffer formats (the int4 lane's own layout):
   weight        uint8 [out, in/2]   two's-complement int4 codes, low nibble = even k
@@ -164,44 +168,30 @@ class SvdqW4A4Linear(nn.Module):
         else:
             self.bias = None
         self.register_buffer("_one", torch.ones((), dtype=torch.float32, device=dev), persistent=False)
-        # resident fast-path layout (derived from ``weight`` by refresh_derived)
-        self.register_buffer("weight_packed", None, persistent=False)
-        self.register_buffer("weight_sums", None, persistent=False)
-        self.register_buffer("weight_scale_packed", None, persistent=False)
-        self.register_buffer("weight_corr", None, persistent=False)
-        self.register_buffer("weight_escale", None, persistent=False)
+        # resident fast-lane operand records (derived from ``weight`` / ``weight_scale`` by refresh_derived)
+        self.register_buffer("weight_fp6", None, persistent=False)
 
     def refresh_derived(self) -> None:
         """Recompute the derived buffers after ``weight`` / ``proj_down`` change (GPU only): ``proj_down``
-        in kernel 1's operand order, and the prepacked fast-path weights. Weights holding a -8 code keep
-        the general int8 path."""
+        in kernel 1's operand order, and the weights as fp6 operand records (``in_features % 128 == 0``;
+        other shapes keep the general int8 path)."""
         if self.rank:
             self.proj_down_op = (torch.ops.cozy_gen_worker.svdq_prep_proj_down(self.proj_down)
                                  if self.proj_down.is_cuda else None)
-        self.weight_packed = self.weight_sums = None
-        self.weight_scale_packed = self.weight_corr = self.weight_escale = None
-        if self.weight.is_cuda and self.in_features % 256 == 0:
-            packed, sums, n_neg8, swp, corr, esc = torch.ops.cozy_gen_worker.svdq_pack_weight(
-                self.weight, self.weight_scale)
-            if int(n_neg8.item()) == 0:
-                self.weight_packed, self.weight_sums = packed, sums
-                self.weight_scale_packed, self.weight_corr, self.weight_escale = swp, corr, esc
+        self.weight_fp6 = None
+        if self.weight.is_cuda and self.in_features % ops.FP6_STAGE == 0:
+            self.weight_fp6 = torch.ops.cozy_gen_worker.svdq_pack_weight_fp6(self.weight, self.weight_scale)
 
     def _load_from_state_dict(self, *args: Any, **kwargs: Any) -> None:  # noqa: D401
         super()._load_from_state_dict(*args, **kwargs)
         if self.weight.device.type != "meta":
             self.refresh_derived()
 
-    def packed_weight(self) -> tuple[Tensor, Tensor, Tensor, Tensor]:
-        """The prepacked fast-lane weight: ``(weight_packed, weight_scale_packed, weight_corr, weight_escale)``."""
-        if self.weight_packed is None:
-            raise SvdqFusedError("this layer has no prepacked weight (lane is 'general')")
-        return self.weight_packed, self.weight_scale_packed, self.weight_corr, self.weight_escale
-
     @property
     def lane(self) -> str:
-        """``"packed"`` (fast fp8-MFMA GEMM) or ``"general"`` (int8-MFMA GEMM on the logical weights)."""
-        return "packed" if self.weight_packed is not None else "general"
+        """``"fp6"`` (kernel 1 writes fp6 operand records, fp6-MFMA GEMM) or ``"general"`` (int4 codes,
+        int8-MFMA GEMM on the logical weights)."""
+        return "fp6" if self.weight_fp6 is not None else "general"
 
     def forward(self, x: Tensor) -> Tensor:
         shape = x.shape
@@ -210,21 +200,24 @@ class SvdqW4A4Linear(nn.Module):
             raise SvdqFusedError(f"SvdqW4A4Linear expects bf16 activations, got {x2.dtype}")
         x2 = x2.contiguous()
         out_dtype = self.out_dtype or torch.bfloat16
-        if self.rank and self.proj_down_op is None:
+        if (self.rank and self.proj_down_op is None) or (self.weight_fp6 is None and self.weight.is_cuda
+                                                         and self.in_features % ops.FP6_STAGE == 0):
             self.refresh_derived()
+        gelu = self.activation == "gelu_tanh"
+        if self.weight_fp6 is not None:
+            qa6, la = torch.ops.cozy_gen_worker.svdq_quant_fp6(x2, self.smooth_factor, None, self.proj_down_op)
+            y = torch.ops.cozy_gen_worker.svdq_w4a4_linear_fp6(
+                qa6, self.weight_fp6, None, self.second, la if self.rank else None, self.proj_up, self.bias,
+                out_dtype, gelu)
+            return y.reshape(*shape[:-1], self.out_features)
         if self.rank:
             qa, sa, la = torch.ops.cozy_gen_worker.svdq_quant_lora(x2, self.smooth_factor, None, self.proj_down_op)
         else:
             qa, sa = torch.ops.cozy_gen_worker.svdq_quant(x2, self.smooth_factor, self._one, False)
             la = None
-        gelu = self.activation == "gelu_tanh"
-        if self.weight_packed is not None:
-            y = torch.ops.cozy_gen_worker.svdq_w4a4_linear_packed(
-                qa, sa, *self.packed_weight(), None, self.second, la, self.proj_up, self.bias, out_dtype, gelu)
-        else:
-            y = torch.ops.cozy_gen_worker.svdq_w4a4_linear(
-                qa, sa, self.weight, self.weight_scale, None, self.second, la, self.proj_up,
-                self.bias, out_dtype, gelu)
+        y = torch.ops.cozy_gen_worker.svdq_w4a4_linear(
+            qa, sa, self.weight, self.weight_scale, None, self.second, la, self.proj_up,
+            self.bias, out_dtype, gelu)
         return y.reshape(*shape[:-1], self.out_features)
 
     def extra_repr(self) -> str:
@@ -296,10 +289,11 @@ def w4a4_int_ops(m: int, n: int, k: int) -> int:
     return 2 * m * n * k
 
 
-def act_quant_bytes(m: int, k: int, rank: int, smooth: bool = True) -> int:
-    """Minimal HBM bytes of kernel 1: x, smooth, L1, q, scales, la."""
-    return (m * k * 2 + (k * 2 if smooth else 0) + k * rank * 2 + m * k // 2 + m * (k // GROUP) * 2
-            + m * rank * 2)
+def act_quant_bytes(m: int, k: int, rank: int, smooth: bool = True, fp6: bool = False) -> int:
+    """Minimal HBM bytes of kernel 1: x, smooth, L1, codes + scales (int4 + fp16, or the fp6 operand
+    records: 104 bytes per 128 columns), la."""
+    out = m * (k // ops.FP6_STAGE) * 104 if fp6 else m * k // 2 + m * (k // GROUP) * 2
+    return m * k * 2 + (k * 2 if smooth else 0) + k * rank * 2 + out + m * rank * 2
 
 
 __all__ = [

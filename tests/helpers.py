@@ -64,3 +64,17 @@ def decode_fp6_codes(q6: np.ndarray) -> np.ndarray:
     if np.any(v == 127):
         raise AssertionError(f"non-integer e3m2 code(s): {sorted(set(int(c) for c in codes[v == 127].ravel()))[:8]}")
     return np.where(codes & 0x20, -v, v).astype(np.int8)
+
+
+FP6_REC = 104
+
+
+def decode_fp6_records(rec: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """fp6 operand records uint8 [K/128, M, 104] (per 128-column stage and row: 96 bytes of e3m2 codes,
+    then the stage's two fp16 group scales) -> (int8 codes [M, K], fp16 scale bits uint16 [M, K/64])."""
+    rec = np.asarray(rec, np.uint8)
+    s, m, width = rec.shape
+    assert width == FP6_REC, rec.shape
+    codes = decode_fp6_codes(rec[:, :, :96].transpose(1, 0, 2).reshape(m, s * 96))
+    scales = rec[:, :, 96:100].copy().view(np.uint16).transpose(1, 0, 2).reshape(m, 2 * s)
+    return codes, scales

@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import bits16, check_output, decode_fp6_codes, from_bits
+from helpers import bits16, check_output, decode_fp6_records, from_bits
 from oracle import svdq_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -75,11 +75,11 @@ def _run_quant(x_bits, smooth_bits, down_bits, s2=None, fmt="int4"):
     s2t = torch.tensor(s2, dtype=torch.float32, device=DEV) if s2 is not None else None
     if fmt == "fp6":
         pdo = torch.ops.cozy_gen_worker.svdq_prep_proj_down(_dev16(down_bits)) if down_bits is not None else None
-        q6, s, la = torch.ops.cozy_gen_worker.svdq_quant_fp6(x, sm, s2t, pdo)
+        q6, la = torch.ops.cozy_gen_worker.svdq_quant_fp6(x, sm, s2t, pdo)
         torch.cuda.synchronize()
-        codes = decode_fp6_codes(q6.cpu().numpy())
+        codes, sbits = decode_fp6_records(q6.cpu().numpy())
         assert codes.min() >= -8 and codes.max() <= 7
-        return O.pack_int4(codes), bits16(s), (la if down_bits is not None else None)
+        return O.pack_int4(codes), sbits, (la if down_bits is not None else None)
     if down_bits is not None:
         pdo = torch.ops.cozy_gen_worker.svdq_prep_proj_down(_dev16(down_bits))
         q, s, la = torch.ops.cozy_gen_worker.svdq_quant_lora(x, sm, s2t, pdo)
@@ -114,12 +114,16 @@ def test_quant_golden_second_level_scale():
     assert np.array_equal(q, f["q"]) and np.array_equal(s, f["scales"])
 
 
-@pytest.mark.parametrize("fmt", ["int4", "fp6"])
-@pytest.mark.parametrize("m,k,rank,smooth", [
+_QUANT_SHAPES = [
     (1, 64, 0, False), (16, 128, 16, True), (77, 3072, 32, True), (333, 3072, 128, True),
     (128, 512, 64, False), (1024, 12288, 32, True), (200, 15360, 32, True), (45, 320, 32, True),
-    (19, 192, 64, True),
-])
+    (19, 192, 64, True), (45, 384, 32, True), (19, 640, 64, True),
+]
+
+
+# the fp6 records hold 128-column stages: that format needs K % 128 == 0
+@pytest.mark.parametrize("m,k,rank,smooth,fmt", [(*c, "int4") for c in _QUANT_SHAPES] +
+                         [(*c, "fp6") for c in _QUANT_SHAPES if c[1] % 128 == 0])
 def test_quant_seeded_bit_exact(m, k, rank, smooth, fmt):
     x = _rand_act(m, k, seed=m * 7 + k)
     g = np.random.default_rng(k)
@@ -207,7 +211,7 @@ def test_psums_seeded_extremes(m, n, k):
 
 
 def _w4a4_case(m, n, k, rank, seed, smooth=True, bias=True, second=None, gelu=False, out_dtype=torch.bfloat16,
-               s2=None, packed=False, row_spread=False):
+               s2=None, row_spread=False, fp6=False, neg8=False):
     g = np.random.default_rng(seed)
     x = _rand_act(m, k, seed=seed)
     sm = O.f32_to_bf16_bits(np.exp(g.uniform(np.log(0.25), np.log(4), k)).astype(np.float32)) if smooth else None
@@ -215,6 +219,10 @@ def _w4a4_case(m, n, k, rank, seed, smooth=True, bias=True, second=None, gelu=Fa
     if row_spread:   # weight rows (and so their group scales) spanning six orders of magnitude
         w *= np.exp(g.uniform(np.log(1e-4), np.log(1e2), (n, 1))).astype(np.float32)
     qw, sw = O.quantize_weight_int4(w)
+    if neg8:   # -8 weight codes (which the symmetric quantizer never emits) in a few places
+        codes = O.unpack_int4(qw)
+        codes[g.integers(0, n, 8), g.integers(0, k, 8)] = -8
+        qw = O.pack_int4(codes)
     down = O.f32_to_bf16_bits((g.standard_normal((k, rank)) * 0.02).astype(np.float32)) if rank else None
     up = O.f32_to_bf16_bits((g.standard_normal((n, rank)) * 0.02).astype(np.float32)) if rank else None
     b = O.f32_to_bf16_bits((g.standard_normal(n) * 0.02).astype(np.float32)) if bias else None
@@ -222,7 +230,13 @@ def _w4a4_case(m, n, k, rank, seed, smooth=True, bias=True, second=None, gelu=Fa
     xd = _dev16(x)
     smd = _dev16(sm) if sm is not None else None
     s2t = torch.tensor(s2, dtype=torch.float32, device=DEV) if s2 is not None else None
-    if rank:
+    if fp6:
+        pdo = torch.ops.cozy_gen_worker.svdq_prep_proj_down(_dev16(down)) if rank else None
+        qa, la = torch.ops.cozy_gen_worker.svdq_quant_fp6(xd, smd, s2t, pdo)
+        upd = _dev16(up) if rank else None
+        if not rank:
+            la = None
+    elif rank:
         qa, sa, la = torch.ops.cozy_gen_worker.svdq_quant_lora(
             xd, smd, s2t, torch.ops.cozy_gen_worker.svdq_prep_proj_down(_dev16(down)))
         upd = _dev16(up)
@@ -234,11 +248,9 @@ def _w4a4_case(m, n, k, rank, seed, smooth=True, bias=True, second=None, gelu=Fa
     wd = torch.from_numpy(qw).to(DEV)
     swd = from_bits(sw.view(np.uint16), torch.float16, DEV)
     bd = _dev16(b) if b is not None else None
-    if packed:
-        wp, _, n8, swp, wc, esc = torch.ops.cozy_gen_worker.svdq_pack_weight(wd, swd)
-        assert int(n8.item()) == 0
-        y = torch.ops.cozy_gen_worker.svdq_w4a4_linear_packed(qa, sa, wp, swp, wc, esc, s2t, sec, la, upd, bd,
-                                                              out_dtype, gelu)
+    if fp6:
+        w6 = torch.ops.cozy_gen_worker.svdq_pack_weight_fp6(wd, swd)
+        y = torch.ops.cozy_gen_worker.svdq_w4a4_linear_fp6(qa, w6, s2t, sec, la, upd, bd, out_dtype, gelu)
     else:
         y = torch.ops.cozy_gen_worker.svdq_w4a4_linear(qa, sa, wd, swd, s2t, sec, la, upd, bd, out_dtype, gelu)
     torch.cuda.synchronize()
@@ -283,108 +295,103 @@ def test_w4a4_epilogue_variants():
 
 
 # ---------------------------------------------------------------------------
-# kernel 2, fast path (prepacked weights, fp8 MFMA)
+# kernel 2, fp6 path (e3m2 operands, fp6 MFMA)
 # ---------------------------------------------------------------------------
 
-def _codes_no_neg8(g, shape):
-    q = g.integers(-7, 8, size=shape).astype(np.int8)
-    return O.pack_int4(q)
+def test_pack_weight_fp6_layout():
+    """Every int4 code, -8 included, becomes its e3m2 code at bits [6t, 6t+6) of its group's 48 bytes,
+    and each record carries its stage's two group scales."""
+    g = np.random.default_rng(21)
+    codes = g.integers(-8, 8, size=(40, 384)).astype(np.int8)
+    codes[0] = np.tile(np.arange(-8, 8, dtype=np.int8), 24)
+    sw = g.uniform(1e-4, 3.0, (40, 6)).astype(np.float16)
+    w6 = torch.ops.cozy_gen_worker.svdq_pack_weight_fp6(torch.from_numpy(O.pack_int4(codes)).to(DEV),
+                                                       torch.from_numpy(sw).to(DEV))
+    assert tuple(w6.shape) == (3, 40, 104)
+    got_codes, got_scales = decode_fp6_records(w6.cpu().numpy())
+    assert np.array_equal(got_codes, codes)
+    assert np.array_equal(got_scales, sw.view(np.uint16))
+
+
+def _fp6_rows(q):
+    """int4 rows [R, K/2] -> fp6 records with unit scales (the weight prepack serves any int4 rows)."""
+    ones = torch.ones(q.shape[0], q.shape[1] // 32, dtype=torch.float16, device=DEV)
+    return torch.ops.cozy_gen_worker.svdq_pack_weight_fp6(torch.from_numpy(q).to(DEV), ones)
 
 
 @pytest.mark.parametrize("m,n,k", [(1, 16, 128), (77, 48, 256), (64, 160, 3072), (129, 96, 640)])
-def test_psums_packed_bit_exact(m, n, k):
-    """The fast path's fp8 arithmetic reproduces every int32 group partial sum exactly,
-    for activations spanning all of [-8, 7] and weights spanning [-7, 7]."""
-    g = np.random.default_rng(m * 3 + n + k)
+def test_psums_fp6_bit_exact(m, n, k):
+    """The fp6 MFMA reproduces every int32 group partial sum exactly, -8 x -8 included."""
+    g = np.random.default_rng(m * 5 + n + k)
     qa = g.integers(0, 256, size=(m, k // 2), dtype=np.uint8)
-    qa[0] = 0x88                                  # all -8 activations
-    qw = _codes_no_neg8(g, (n, k))
-    qw[0] = O.pack_int4(np.full((1, k), -7, np.int8))[0]   # extreme weights
-    ones = torch.ones(n, k // 64, dtype=torch.float16, device=DEV)
-    wp, ws, n8, _, _, _ = torch.ops.cozy_gen_worker.svdq_pack_weight(torch.from_numpy(qw).to(DEV), ones)
-    assert int(n8.item()) == 0
-    assert np.array_equal(ws.cpu().numpy().astype(np.int64),
-                          O.unpack_int4(qw).astype(np.int64).reshape(n, k // 64, 64).sum(-1))
-    ps = torch.ops.cozy_gen_worker.svdq_group_psums_packed(torch.from_numpy(qa).to(DEV), wp, ws)
+    qw = g.integers(0, 256, size=(n, k // 2), dtype=np.uint8)
+    qa[0] = 0x88
+    qw[0] = 0x88
+    ps = torch.ops.cozy_gen_worker.svdq_group_psums_fp6(_fp6_rows(qa), _fp6_rows(qw))
     assert np.array_equal(ps.cpu().numpy(), O.group_psums(qa, qw))
-    assert int(ps[0, 0, 0]) == 64 * 56
-
-
-def test_pack_counts_neg8():
-    g = np.random.default_rng(3)
-    codes = g.integers(-7, 8, size=(32, 256)).astype(np.int8)
-    codes[3, 5] = -8
-    codes[17, 200] = -8
-    ones = torch.ones(32, 4, dtype=torch.float16, device=DEV)
-    n8 = torch.ops.cozy_gen_worker.svdq_pack_weight(torch.from_numpy(O.pack_int4(codes)).to(DEV), ones)[2]
-    assert int(n8.item()) == 2
-
-
-def test_pack_scales_and_correction():
-    """sw' * escale reproduces sw exactly, escale is a power of two per row, and the correction
-    pairs hold -cw * sw' * 2^-9 to about 2^-22 (rows of very different scale magnitude)."""
-    g = np.random.default_rng(11)
-    n, k = 48, 1344                                          # 21 groups: padded to 24 in wcorr
-    codes = g.integers(-7, 8, size=(n, k)).astype(np.int8)
-    mag = np.exp(g.uniform(np.log(1e-4), np.log(1e2), (n, 1)))
-    sw = (mag * g.uniform(0.1, 1.0, (n, k // 64))).astype(np.float16)
-    sw[5, :] = np.float16(0)                                 # an all-zero row
-    wd = torch.from_numpy(O.pack_int4(codes)).to(DEV)
-    wp, ws, n8, swp, wc, esc = torch.ops.cozy_gen_worker.svdq_pack_weight(wd, torch.from_numpy(sw).to(DEV))
-    swp, wc, esc = swp.cpu().numpy(), wc.cpu().numpy().astype(np.float64), esc.cpu().numpy()
-    e = np.log2(esc)
-    assert np.array_equal(e, np.round(e)), "escale must be a power of two"
-    assert np.array_equal(swp.astype(np.float64) * esc[:, None], sw.astype(np.float64))
-    nz = sw.max(1) > 0
-    assert np.all(swp[nz].max(1) >= 2.0 ** 14) and np.all(swp[nz].max(1) < 2.0 ** 15)
-    cw = codes.astype(np.int64).reshape(n, k // 64, 64).sum(-1)
-    want = -(cw * swp.astype(np.float64)) / 512.0
-    got = np.zeros((n, 24))
-    got[:, :] = (wc[:, :, :4] + wc[:, :, 4:]).reshape(n, 24)
-    assert np.all(got[:, 21:] == 0)
-    err = np.abs(got[:, :21] - want)
-    assert np.all(err <= 2.0 ** -21 * np.abs(want).max(1, keepdims=True) + 1e-30)
+    assert int(ps[0, 0, 0]) == 64 * 64
 
 
 @pytest.mark.parametrize("m,n,k,rank", [
-    (1, 16, 256, 0), (77, 128, 512, 32), (256, 3072, 3072, 32), (333, 272, 512, 128), (130, 144, 256, 16),
-    (64, 256, 12288, 64), (300, 128, 15360, 32), (513, 400, 1024, 32), (4097, 48, 768, 16),
+    (1, 16, 128, 0), (77, 128, 512, 32), (256, 3072, 3072, 32), (333, 272, 640, 128), (130, 144, 256, 16),
+    (64, 256, 12288, 64), (300, 128, 15360, 32), (513, 400, 1152, 32), (4097, 48, 768, 16), (600, 528, 384, 32),
 ])
-def test_w4a4_packed_seeded(m, n, k, rank):
-    y, ref = _w4a4_case(m, n, k, rank, seed=m * 17 + n + k, packed=True)
-    check_output(y, ref, what=f"packed w4a4 {m}x{n}x{k} r{rank}")
+def test_w4a4_fp6_seeded(m, n, k, rank):
+    y, ref = _w4a4_case(m, n, k, rank, seed=m * 13 + n + k, fp6=True)
+    check_output(y, ref, what=f"fp6 w4a4 {m}x{n}x{k} r{rank}")
 
 
-def test_w4a4_packed_epilogue_variants():
+def test_w4a4_fp6_last_row_tail():
+    """The last activation / weight row's final stage (the end of the operand buffers) arrives intact:
+    only that row's last 8 columns are nonzero."""
+    m, n, k = 256, 128, 512
+    g = np.random.default_rng(5)
+    x = np.zeros((m, k), np.float32)
+    x[m - 1, k - 8:] = g.uniform(1.0, 3.0, 8)
+    x[m - 2, :] = g.standard_normal(k)
+    w = (g.standard_normal((n, k)) * 0.02).astype(np.float32)
+    w[n - 1, :k - 8] = 0.0
+    qw, sw = O.quantize_weight_int4(w)
+    xb = O.f32_to_bf16_bits(x)
+    ref = O.w4a4_linear(xb, None, qw, sw, None, None, None)
+    qa, _ = torch.ops.cozy_gen_worker.svdq_quant_fp6(_dev16(xb), None, None, None)
+    w6 = torch.ops.cozy_gen_worker.svdq_pack_weight_fp6(torch.from_numpy(qw).to(DEV),
+                                                       from_bits(sw.view(np.uint16), torch.float16, DEV))
+    y = torch.ops.cozy_gen_worker.svdq_w4a4_linear_fp6(qa, w6, None, None, None, None, None, torch.bfloat16, False)
+    yc = y.float().cpu().numpy()
+    assert np.abs(ref[m - 1]).max() > 0.05 and abs(float(ref[m - 1, n - 1])) > 0.0
+    check_output(y, ref, what="fp6 last-row tail")
+    assert np.allclose(yc[m - 1], ref[m - 1], rtol=1e-2, atol=1e-3)
+
+
+def test_w4a4_fp6_epilogue_variants():
     n = 256
     sec = np.linspace(0.5, 2.0, n).astype(np.float32)
     for kw, what in ((dict(second=sec), "second"), (dict(gelu=True), "gelu"), (dict(out_dtype=torch.float16), "f16"),
                      (dict(smooth=False, bias=False), "bare"), (dict(s2=0.5), "s2"),
-                     (dict(row_spread=True, bias=False), "row scale spread")):
-        y, ref = _w4a4_case(96, n, 512, 32 if what != "bare" else 0, seed=11, packed=True, **kw)
-        check_output(y, ref, what=f"packed {what}")
+                     (dict(row_spread=True, bias=False), "row scale spread"), (dict(neg8=True), "-8 weights")):
+        y, ref = _w4a4_case(96, n, 512, 32 if what != "bare" else 0, seed=12, fp6=True, **kw)
+        check_output(y, ref, what=f"fp6 {what}")
 
 
 def test_module_lanes_agree():
-    """Weights without -8 take the packed lane, weights with a -8 code the general lane; both match the oracle."""
+    """in_features % 128 == 0 takes the fp6 lane (any code, -8 included), other shapes the general lane;
+    both match the oracle."""
     from gen_worker_amd import synthetic
     from gen_worker_amd.svdq import build_svdq_w4a4_linear
 
-    L = synthetic.w4a4_layer(256, 512, 32)
-    x = synthetic.activation(100, 512, outlier_frac=0.01, outlier_scale=20.0)
-    mod = build_svdq_w4a4_linear(qweight=L.qweight, wscales=L.wscales, smooth=L.smooth, proj_down=L.proj_down,
-                                 proj_up=L.proj_up, bias=L.bias, device=DEV)
-    assert mod.lane == "packed"
-    qw = L.qweight.clone()
-    qw[0, 0] = (qw[0, 0] & 0xF0) | 0x8     # one -8 code
-    mod2 = build_svdq_w4a4_linear(qweight=qw, wscales=L.wscales, smooth=L.smooth, proj_down=L.proj_down,
-                                  proj_up=L.proj_up, bias=L.bias, device=DEV)
-    assert mod2.lane == "general"
-    for mdl, w in ((mod, L.qweight), (mod2, qw)):
-        y = mdl(x.to(DEV))
-        ref = O.w4a4_linear(bits16(x), bits16(L.smooth), w.numpy(), L.wscales.numpy(), bits16(L.proj_down),
+    for k, want in ((512, "fp6"), (320, "general")):
+        L = synthetic.w4a4_layer(256, k, 32)
+        qw = L.qweight.clone()
+        qw[0, 0] = (qw[0, 0] & 0xF0) | 0x8     # one -8 code
+        x = synthetic.activation(100, k, outlier_frac=0.01, outlier_scale=20.0)
+        mod = build_svdq_w4a4_linear(qweight=qw, wscales=L.wscales, smooth=L.smooth, proj_down=L.proj_down,
+                                     proj_up=L.proj_up, bias=L.bias, device=DEV)
+        assert mod.lane == want
+        y = mod(x.to(DEV))
+        ref = O.w4a4_linear(bits16(x), bits16(L.smooth), qw.numpy(), L.wscales.numpy(), bits16(L.proj_down),
                             bits16(L.proj_up), bits16(L.bias))
-        check_output(y, ref, what=mdl.lane)
+        check_output(y, ref, what=mod.lane)
 
 
 def test_w4a4_module_config1_full_size():
@@ -396,7 +403,7 @@ def test_w4a4_module_config1_full_size():
     x = synthetic.activation(4608, 3072, outlier_frac=0.005, outlier_scale=30.0)
     mod = build_svdq_w4a4_linear(qweight=L.qweight, wscales=L.wscales, smooth=L.smooth, proj_down=L.proj_down,
                                  proj_up=L.proj_up, bias=L.bias, device=DEV)
-    assert mod.lane == "packed"
+    assert mod.lane == "fp6"
     y = mod(x.to(DEV).reshape(1, 4608, 3072))
     assert y.shape == (1, 4608, 3072)
     ref = O.w4a4_linear(bits16(x), bits16(L.smooth), L.qweight.numpy(), L.wscales.numpy(), bits16(L.proj_down),

@@ -51,6 +51,10 @@ def test_invalid_arguments_are_refused_before_any_launch():
     assert rc == 1 and "multiple of 64" in lib.gwa_last_error().decode()
     rc = lib.gwa_svdq_quant_int4(None, 64, None, None, None, 0, 7, None, None, None, 4, 64, None)
     assert rc == 1 and "out_format" in lib.gwa_last_error().decode()
+    rc = lib.gwa_svdq_quant_int4(None, 192, None, None, None, 0, 1, None, None, None, 4, 192, None)
+    assert rc == 1 and "128" in lib.gwa_last_error().decode()
+    rc = lib.gwa_svdq_gemm_w4a4_fp6(None, None, None, None, 0, None, None, 0, None, None, 0, 0, 8, 64, 192, None)
+    assert rc == 1 and "multiple of 128" in lib.gwa_last_error().decode()
     rc = lib.gwa_svdq_prep_proj_down(None, None, 64, 24, None)
     assert rc == 1 and "rank" in lib.gwa_last_error().decode()
     rc = lib.gwa_svdq_gemm_w4a4(None, None, None, None, None, None, 0, None, None, 0, None, None, 0, 0,
@@ -94,8 +98,15 @@ def test_fake_impls_trace_shapes():
         pdo = torch.ops.cozy_gen_worker.svdq_prep_proj_down(torch.empty(384, 32, dtype=torch.bfloat16))
         assert pdo.shape == (512, 32)
         q, s, la = torch.ops.cozy_gen_worker.svdq_quant_lora(x, None, None, pdo)
-        q6, s6, la6 = torch.ops.cozy_gen_worker.svdq_quant_fp6(x, None, None, None)
-        assert q6.shape == (77, 288) and s6.shape == (77, 6) and la6.shape == (77, 0)
+        q6, la6 = torch.ops.cozy_gen_worker.svdq_quant_fp6(x, None, None, None)
+        assert q6.shape == (3, 77, 104) and la6.shape == (77, 0)
+        w6 = torch.ops.cozy_gen_worker.svdq_pack_weight_fp6(torch.empty(128, 192, dtype=torch.uint8),
+                                                           torch.empty(128, 6, dtype=torch.float16))
+        assert w6.shape == (3, 128, 104)
+        y6 = torch.ops.cozy_gen_worker.svdq_w4a4_linear_fp6(q6, w6, None, None, None, None, None, torch.bfloat16,
+                                                            False)
+        assert y6.shape == (77, 128) and y6.dtype == torch.bfloat16
+        assert torch.ops.cozy_gen_worker.svdq_group_psums_fp6(q6, w6).shape == (77, 128, 6)
         assert q.shape == (77, 192) and s.shape == (77, 6) and la.shape == (77, 32)
         w = torch.empty(128, 192, dtype=torch.uint8)
         ws = torch.empty(128, 6, dtype=torch.float16)
