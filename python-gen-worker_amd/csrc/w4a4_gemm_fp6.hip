@@ -42,26 +42,38 @@
 
 namespace {
 
-constexpr int TN = 256, TM = 256;
-constexpr int WBN = 2, WBM = 4;
-constexpr int WAVES_N = TN / (32 * WBN), WAVES_M = TM / (32 * WBM);  // 4, 2
-constexpr int NWAVES = WAVES_N * WAVES_M;  // 8
-constexpr int NTHREADS = 64 * NWAVES;      // 512
+constexpr int TM = 256;
+constexpr int NWAVES = 8, NTHREADS = 64 * NWAVES;  // 512
 constexpr int GS = 2;                      // groups per stage (one record)
 constexpr int GB = 48;                     // bytes of one row's group (64 e3m2 codes)
 constexpr int REC = GWA_FP6_REC;           // 104: record = LDS row stride
 constexpr int OFF_SC = GS * GB;            // 96: the record's scales
-constexpr int LDS_X = TM * REC;            // 26624
-constexpr int LDS_W = TN * REC;            // 26624
-constexpr int OFF_W = LDS_X;
-constexpr int LDS_STAGE = LDS_X + LDS_W;   // 53248
-constexpr int DMA_X = LDS_X / 1024;        // 26 runs of 1 KiB (64 lanes x 16 B)
-constexpr int DMA_RUNS = LDS_STAGE / 1024;                   // 52
-constexpr int DMA_SLOTS = (DMA_RUNS + NWAVES - 1) / NWAVES;  // 7 per wave
-static_assert(LDS_X % 1024 == 0 && LDS_W % 1024 == 0 && DMA_RUNS > NWAVES * (DMA_SLOTS - 1), "DMA runs");
-static_assert(DMA_SLOTS < 64, "vmcnt range");
+constexpr int kLdsBytes = 160 * 1024;      // gfx950 LDS per workgroup
 constexpr int kFmtE3M2 = 3;                // cbsz / blgp code of e3m2 operands
 constexpr int kUnitE8M0 = 127;             // 2^0
+
+// Tile configurations: TN = 128 (64 x 64 wave tiles, registers for the
+// software pipeline, four stage buffers) or TN = 256 (64 x 128 wave tiles,
+// each staged byte feeds twice the outputs, three stage buffers, blocks run
+// back to back).
+template <int TN>
+struct Cfg {
+  static constexpr int WBN = 2;
+  static constexpr int WAVES_N = TN / (32 * WBN);
+  static constexpr int WAVES_M = NWAVES / WAVES_N;
+  static constexpr int WBM = TM / (32 * WAVES_M);
+  static constexpr int LDS_X = TM * REC, OFF_W = LDS_X, LDS_W = TN * REC;
+  static constexpr int STAGE = LDS_X + LDS_W;
+  static constexpr int NB0 = (kLdsBytes - 2 * TN * 4) / STAGE;
+  static constexpr int NBUF = NB0 > 4 ? 4 : NB0;   // stage buffers; DMA runs NBUF - 1 stages ahead
+  static constexpr int RUNS = STAGE / 1024;        // 1 KiB DMA runs (64 lanes x 16 B) per stage
+  static constexpr int DMA_X = LDS_X / 1024;
+  static constexpr int SLOTS = (RUNS + NWAVES - 1) / NWAVES;  // per wave and stage
+  static constexpr bool PIPE = WBN * WBM <= 4;
+  static_assert(WAVES_N * WAVES_M == NWAVES && WBM * 32 * WAVES_M == TM, "wave grid");
+  static_assert(LDS_X % 1024 == 0 && LDS_W % 1024 == 0 && NBUF >= 3, "stage layout");
+  static_assert((NBUF - 1) * SLOTS < 64, "vmcnt range");
+};
 
 // Direct-to-LDS copy of 16 bytes per lane: LDS [m0 + 16 lane, +16) <- buffer
 // [voff + soff, +16). Issued as asm so the compiler's wait-count pass (which
@@ -90,16 +102,26 @@ __device__ __forceinline__ void barrier_lds() {
   asm volatile("" ::: "memory");
 }
 
-__shared__ __attribute__((aligned(16))) uint8_t g_stage0[LDS_STAGE];
-__shared__ __attribute__((aligned(16))) uint8_t g_stage1[LDS_STAGE];
-__shared__ __attribute__((aligned(16))) uint8_t g_stage2[LDS_STAGE];
-__shared__ __attribute__((aligned(16))) float g_epi[2 * TN];
-
 // s_waitcnt vmcnt(n) lgkmcnt(0) (gfx9 encoding; expcnt left at its maximum)
 template <int n>
 __device__ __forceinline__ void wait_vm_lgkm0() {
   static_assert(n >= 0 && n < 64, "vmcnt");
   __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4));
+}
+
+// wait until at most `newer` stages of `slots` copies each are still in flight
+template <int slots, int maxnewer>
+__device__ __forceinline__ void wait_stages(int newer) {
+  if constexpr (maxnewer >= 3) {
+    if (newer >= 3) { wait_vm_lgkm0<3 * slots>(); return; }
+  }
+  if constexpr (maxnewer >= 2) {
+    if (newer == 2) { wait_vm_lgkm0<2 * slots>(); return; }
+  }
+  if constexpr (maxnewer >= 1) {
+    if (newer == 1) { wait_vm_lgkm0<slots>(); return; }
+  }
+  wait_vm_lgkm0<0>();
 }
 
 __device__ __forceinline__ v16f group_mfma_fp6(v8i a, v8i b) {
@@ -122,12 +144,18 @@ __device__ __forceinline__ v8i buf_operand(rsrc_t r, uint32_t off) {
   return (v8i){(int)a[0], (int)a[1], (int)b[0], (int)b[1], (int)c[0], (int)c[1], 0, 0};
 }
 
-template <int RB, bool GELU, bool OUT_F16>
+template <int TN, int RB, bool GELU, bool OUT_F16>
 __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_kernel(
     const uint8_t* __restrict__ qa, const uint8_t* __restrict__ qw, const float* __restrict__ s2p,
     const float* __restrict__ second, int second_per_channel, const uint16_t* __restrict__ la,
     const uint16_t* __restrict__ up, const uint16_t* __restrict__ bias, uint16_t* __restrict__ out, int M, int N,
     int K) {
+  using C = Cfg<TN>;
+  constexpr int WBN = C::WBN, WBM = C::WBM, WAVES_N = C::WAVES_N, NBUF = C::NBUF, SLOTS = C::SLOTS;
+  constexpr int OFF_W = C::OFF_W;
+  __shared__ __attribute__((aligned(16))) uint8_t g_stage[NBUF][C::STAGE];
+  __shared__ __attribute__((aligned(16))) float g_epi[2 * TN];
+
   const int tid = threadIdx.x;
   const int tiles_n = (N + TN - 1) / TN, tiles_m = (M + TM - 1) / TM;
   int tm, tn;
@@ -143,24 +171,41 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_kernel(
 
   // DMA: run q of a stage is LDS bytes [1024 q, +1024) of the stage buffer =
   // bytes [1024 q', +1024) of the tile's contiguous records (q' = q for the
-  // activations, q - DMA_X for the weights). Runs are dealt round-robin; the
-  // waves left without a 7th run repeat one of the last runs (same bytes to
-  // the same place), so every wave issues DMA_SLOTS loads per stage. Rows past
-  // M / N read the next stage's records (their outputs are never stored) or
+  // activations, q - DMA_X for the weights). Runs are dealt round-robin; a
+  // wave left without a last run repeats the final run (same bytes to the
+  // same place), so every wave issues SLOTS copies per stage. Rows past M / N
+  // read the next stage's records (their outputs are never stored) or
   // nothing (past the buffer: zeros).
   const uint32_t dvo = 16u * (uint32_t)lane;
-  // copy j (0 .. DMA_SLOTS-1) of this wave's share of stage st into `stage`
-  auto issue_one = [&](uint8_t* stage, int st, int j) __attribute__((always_inline)) {
-    int q = wave + NWAVES * j;
-    q = q < DMA_RUNS ? q : q - NWAVES / 2;
-    const bool isx = q < DMA_X;
-    const uint32_t base = isx ? (uint32_t)(((int64_t)st * M + m0) * REC) + q * 1024
-                              : (uint32_t)(((int64_t)st * N + n0) * REC) + (q - DMA_X) * 1024;
-    dma16(isx ? xbuf : wbuf, (uint32_t)(uintptr_t)(stage + q * 1024), dvo, base);
-  };
   auto issue = [&](uint8_t* stage, int st) __attribute__((always_inline)) {
+    const uint32_t xs = (uint32_t)(((int64_t)st * M + m0) * REC);
+    const uint32_t ws = (uint32_t)(((int64_t)st * N + n0) * REC);
 #pragma unroll
-    for (int j = 0; j < DMA_SLOTS; ++j) issue_one(stage, st, j);
+    for (int j = 0; j < SLOTS; ++j) {
+      int q = wave + NWAVES * j;
+      q = q < C::RUNS ? q : C::RUNS - 1;
+      const bool isx = q < C::DMA_X;
+      dma16(isx ? xbuf : wbuf, (uint32_t)(uintptr_t)(stage + q * 1024), dvo,
+            isx ? xs + q * 1024 : ws + (q - C::DMA_X) * 1024);
+    }
+  };
+
+  // The low-rank operands of ranks up to 32 (la rows m0.., up rows n0..: two
+  // contiguous runs) are copied during the last stage into a stage buffer
+  // that stage no longer uses, as [la | up].
+  constexpr bool LR_LDS = RB == 1 || RB == 2;
+  const v4i lbuf4 = raw_rsrc(la, (uint32_t)((int64_t)M * RB * 32));
+  const v4i ubuf4 = raw_rsrc(up, (uint32_t)((int64_t)N * RB * 32));
+  auto issue_lowrank = [&](uint8_t* dst) __attribute__((always_inline)) {
+    constexpr int LA_RUNS = TM * RB * 32 / 1024, UP_RUNS = TN * RB * 32 / 1024;
+    constexpr int RUNS = LA_RUNS + UP_RUNS, PER = (RUNS + NWAVES - 1) / NWAVES;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int q = min(wave + NWAVES * j, RUNS - 1);  // a wave without a last run repeats the final one
+      const bool isl = q < LA_RUNS;
+      dma16(isl ? lbuf4 : ubuf4, (uint32_t)(uintptr_t)(dst + q * 1024), dvo,
+            isl ? (uint32_t)(m0 * RB * 32 + q * 1024) : (uint32_t)(n0 * RB * 32 + (q - LA_RUNS) * 1024));
+    }
   };
 
   v16f acc[WBN][WBM];
@@ -169,13 +214,41 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_kernel(
 #pragma unroll
     for (int b = 0; b < WBM; ++b) acc[a][b] = (v16f){};
 
-  // One stage, blocks in (bn, bm) order, so one block's P and S are live at a
-  // time: empty asm statements on each block's scale operand and accumulator
-  // pin the block's MFMAs and fmas in program order (the MFMA intrinsics are
-  // pure and would otherwise be regrouped across blocks). A group's operands stay in
+  // Pending P and S of the previous block (software pipeline, TN = 128): the
+  // pipeline starts with zero products "pending" for the last block, so the
+  // pending block is a compile-time constant everywhere.
+  v16f pp = (v16f){}, ps = (v16f){};
+  constexpr int kLast = WBN * WBM - 1;
+  auto fma_half = [&](int blk, int half) __attribute__((always_inline)) {
+#pragma unroll
+    for (int a = 0; a < WBN; ++a)
+#pragma unroll
+      for (int b = 0; b < WBM; ++b)
+        if (blk == a * WBM + b) {
+#pragma unroll
+          for (int v = 8 * half; v < 8 * half + 8; ++v) acc[a][b][v] = fmaf(pp[v], ps[v], acc[a][b][v]);
+        }
+  };
+  auto pin_acc = [&](int blk) __attribute__((always_inline)) {
+#pragma unroll
+    for (int a = 0; a < WBN; ++a)
+#pragma unroll
+      for (int b = 0; b < WBM; ++b)
+        if (blk == a * WBM + b) asm volatile("" : "+v"(acc[a][b]));
+  };
+
+  // One stage's blocks, in (bn, bm) order. A group's operands stay in
   // registers; each is refilled with the next group's operand right after its
   // last use (the first group of a stage is read at the stage start: the
-  // next stage's buffer is only complete after the barrier).
+  // next stage's buffer is only complete after the barrier). Empty asm
+  // statements pin the pure MFMA intrinsics to their place in program order.
+  //  * PIPE: one step per block b issues b's two MFMAs between the two halves
+  //    of block b-1's 16 fmas (whose P and S completed during step b-1), in
+  //    scheduling groups MFMA, 8 VALU, MFMA, 8 VALU; the step's end takes
+  //    b-1's accumulator and P_b / S_b, so nothing leaves its step. The
+  //    stage's last block hands its P and S to the next stage.
+  //  * otherwise: each block's MFMAs, then its 16 fmas (one block's P and S
+  //    live); the other wave on the SIMD fills the matrix pipe meanwhile.
   auto compute = [&](const uint8_t* base) __attribute__((always_inline)) {
     const uint8_t* lx = base + (32 * WBM * wm + r32) * REC + 24 * h;
     const uint8_t* lw = base + OFF_W + (32 * WBN * wn + r32) * REC + 24 * h;
@@ -194,6 +267,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_kernel(
       xo[bm] = lds_operand(lx + bm * 32 * REC);
       xs[bm] = *(const uint32_t*)(sx + bm * 32 * REC);
     }
+    int prev = kLast;
 #pragma unroll
     for (int gi = 0; gi < GS; ++gi) {
       const uint32_t mask = gi ? 0xFFFF0000u : 0x0000FFFFu;
@@ -203,13 +277,31 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_kernel(
 #pragma unroll
         for (int bm = 0; bm < WBM; ++bm) {
           uint32_t s1 = xs[bm] & mask;
-          asm volatile("" : "+v"(s1));  // keeps this S MFMA here (it would otherwise be hoisted to the stage start)
-          const v4h sel = __builtin_bit_cast(v4h, make_uint2(s1, 0u));
-          const v16f p = group_mfma_fp6(wo[bn], xo[bm]);
-          const v16f sv = __builtin_amdgcn_mfma_f32_32x32x8f16(swop, sel, (v16f){}, 0, 0, 0);
+          if constexpr (C::PIPE) {
+            asm volatile("" : "+v"(s1), "+v"(xo[bm]), "+v"(wo[bn]));  // step start
+            const v4h sel = __builtin_bit_cast(v4h, make_uint2(s1, 0u));
+            v16f p = group_mfma_fp6(wo[bn], xo[bm]);
+            fma_half(prev, 0);
+            v16f sv = __builtin_amdgcn_mfma_f32_32x32x8f16(swop, sel, (v16f){}, 0, 0, 0);
+            fma_half(prev, 1);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+            pin_acc(prev);
+            asm volatile("" : "+v"(p), "+v"(sv));  // step end
+            pp = p;
+            ps = sv;
+            prev = bn * WBM + bm;
+          } else {
+            asm volatile("" : "+v"(s1));  // keeps this S MFMA here (it would otherwise be hoisted to the stage start)
+            const v4h sel = __builtin_bit_cast(v4h, make_uint2(s1, 0u));
+            const v16f p = group_mfma_fp6(wo[bn], xo[bm]);
+            const v16f sv = __builtin_amdgcn_mfma_f32_32x32x8f16(swop, sel, (v16f){}, 0, 0, 0);
 #pragma unroll
-          for (int v = 0; v < 16; ++v) acc[bn][bm][v] = fmaf(p[v], sv[v], acc[bn][bm][v]);
-          asm volatile("" : "+v"(acc[bn][bm]));  // this block's fmas complete here, in program order
+            for (int v = 0; v < 16; ++v) acc[bn][bm][v] = fmaf(p[v], sv[v], acc[bn][bm][v]);
+            asm volatile("" : "+v"(acc[bn][bm]));  // this block's fmas complete here, in program order
+          }
           if (gi + 1 < GS) {
             if (bn == WBN - 1) xo[bm] = lds_operand(lx + bm * 32 * REC + (gi + 1) * GB);
             if (bm == WBM - 1) wo[bn] = lds_operand(lw + bn * 32 * REC + (gi + 1) * GB);
@@ -218,14 +310,18 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_kernel(
       }
     }
   };
-  // one stage: prefetch stage st + 2 into pf, compute on cur, then make stage
-  // st + 1 complete (this wave's loads, then everyone's) before moving on
-  auto stage = [&](int st, const uint8_t* cur, uint8_t* pf) __attribute__((always_inline)) {
-    const bool more = st + 2 < nst;
-    if (more) issue(pf, st + 2);
+  // one stage: prefetch stage st + NBUF - 1 into the buffer read in stage
+  // st - 1, compute on this stage's buffer, then make stage st + 1 complete
+  // (this wave's copies, then everyone's) before moving on
+  auto stage = [&](int st, const uint8_t* cur, uint8_t* pf, uint8_t* spare) __attribute__((always_inline)) {
+    if (st + NBUF - 1 < nst) issue(pf, st + NBUF - 1);
+    if constexpr (LR_LDS) {
+      if (st == nst - 1) issue_lowrank(spare);
+    }
     compute(cur);
-    if (more) wait_vm_lgkm0<DMA_SLOTS>();
-    else wait_vm_lgkm0<0>();
+    // copies issued after stage st + 1's: stages st + 2 .. min(st + NBUF - 1, nst - 1)
+    const int newer = min(NBUF - 2, nst - 2 - st);
+    wait_stages<SLOTS, NBUF - 2>(newer);
     barrier_lds();
   };
 
@@ -242,18 +338,19 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_kernel(
     g_epi[TN + tid] = bv;
   }
   __syncthreads();  // the epilogue constants' loads are complete before any copy is in flight
-  issue(g_stage0, 0);
-  if (nst > 1) {
-    issue(g_stage1, 1);
-    wait_vm_lgkm0<DMA_SLOTS>();
-  } else {
-    wait_vm_lgkm0<0>();
-  }
+#pragma unroll
+  for (int u = 0; u < NBUF - 1; ++u)
+    if (u < nst) issue(g_stage[u], u);
+  wait_stages<SLOTS, NBUF - 2>(min(NBUF - 2, nst - 1));  // stage 0 complete
   barrier_lds();
-  for (int st = 0; st < nst; st += 3) {
-    stage(st, g_stage0, g_stage2);
-    if (st + 1 < nst) stage(st + 1, g_stage1, g_stage0);
-    if (st + 2 < nst) stage(st + 2, g_stage2, g_stage1);
+  for (int st = 0; st < nst; st += NBUF) {
+#pragma unroll
+    for (int u = 0; u < NBUF; ++u)
+      if (st + u < nst) stage(st + u, g_stage[u], g_stage[(u + NBUF - 1) % NBUF], g_stage[(u + 1) % NBUF]);
+  }
+  if constexpr (C::PIPE) {
+    fma_half(kLast, 0);
+    fma_half(kLast, 1);
   }
 
   // ---------------- epilogue ----------------
@@ -269,13 +366,34 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_kernel(
         for (int e = 0; e < 4; ++e) acc[bn][bm][4 * qd + e] *= cm[e];
     }
   }
-  if (RB > 0) {
-    constexpr int RC = RB < 2 ? RB : 2;
+  if constexpr (LR_LDS) {
+    // la / up from the spare stage buffer of the last stage ((nst - 1 + 1) % NBUF)
+    const int spare = nst % NBUF;
+    const uint8_t* lrb = &g_stage[0][0] + spare * C::STAGE;
+    const uint8_t* upb = lrb + TM * RB * 32;
+#pragma unroll
+    for (int k0 = 0; k0 < RB; ++k0) {
+      v4i ua[WBN], lb[WBM];
+#pragma unroll
+      for (int bn = 0; bn < WBN; ++bn)
+        ua[bn] = *(const v4i*)(upb + (32 * (WBN * wn + bn) + r32) * (RB * 32) + k0 * 32 + 16 * h);
+#pragma unroll
+      for (int bm = 0; bm < WBM; ++bm)
+        lb[bm] = *(const v4i*)(lrb + (32 * (WBM * wm + bm) + r32) * (RB * 32) + k0 * 32 + 16 * h);
+#pragma unroll
+      for (int bn = 0; bn < WBN; ++bn)
+#pragma unroll
+        for (int bm = 0; bm < WBM; ++bm)
+          acc[bn][bm] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, ua[bn]),
+                                                                __builtin_bit_cast(v8bf, lb[bm]), acc[bn][bm], 0, 0, 0);
+    }
+  } else if constexpr (RB > 0) {
+    constexpr int RC = 2;
     const rsrc_t ubuf = make_rsrc(up, (uint32_t)((int64_t)N * RB * 32));
     const rsrc_t lbuf = make_rsrc(la, (uint32_t)((int64_t)M * RB * 32));
 #pragma unroll
     for (int k0 = 0; k0 < RB; k0 += RC) {
-      v4i ua[WBN][RC > 0 ? RC : 1], lb[WBM][RC > 0 ? RC : 1];
+      v4i ua[WBN][RC], lb[WBM][RC];
 #pragma unroll
       for (int bn = 0; bn < WBN; ++bn)
 #pragma unroll
@@ -299,17 +417,24 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_kernel(
                                                                   0, 0, 0);
     }
   }
-  const rsrc_t obuf = make_rsrc(out, (uint32_t)((int64_t)M * N * 2));
+  // + bias (+ GELU), packed to 16 bits, staged in LDS as [m][n] rows of OSTR
+  // bytes (the stage buffers are free; the barrier also retires the la / up
+  // reads), then stored as full rows: each lane 16 bytes, 32 lanes per 512
+  // bytes of a row, so every wave store covers whole 128-byte lines.
+  constexpr int OSTR = TN * 2 + 8;  // 8-byte pad: the 32 rows a write instruction covers hit distinct banks
+  static_assert(TM * OSTR <= NBUF * C::STAGE, "output staging");
+  uint8_t* ob = &g_stage[0][0];
+  barrier_lds();
 #pragma unroll
   for (int bn = 0; bn < WBN; ++bn) {
     const int nl = 32 * (WBN * wn + bn);
 #pragma unroll
     for (int bm = 0; bm < WBM; ++bm) {
-      const int m = m0 + 32 * (WBM * wm + bm) + r32;
+      const int ml = 32 * (WBM * wm + bm) + r32;
 #pragma unroll
       for (int qd = 0; qd < 4; ++qd) {
-        const int n = n0 + nl + 8 * qd + 4 * h;
-        const v4f cb = *(const v4f*)(g_epi + TN + nl + 8 * qd + 4 * h);
+        const int nn = nl + 8 * qd + 4 * h;
+        const v4f cb = *(const v4f*)(g_epi + TN + nn);
         float o[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -325,11 +450,23 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_kernel(
           pk.x = pack_bf16x2_rn(o[0], o[1]);
           pk.y = pack_bf16x2_rn(o[2], o[3]);
         }
-        // branch-free store after the MFMAs: rows >= M / columns >= N fall outside the buffer
-        const uint32_t off = (m < M && n < N) ? (uint32_t)(((int64_t)m * N + n) * 2) : kOOB;
-        buf_store8(pk, obuf, off);
+        *(uint2*)(ob + ml * OSTR + nn * 2) = pk;
       }
     }
+  }
+  barrier_lds();
+  constexpr int CPR = TN / 8;                 // 16-byte chunks per row
+  constexpr int RPP = NTHREADS / CPR;         // rows per pass
+  const int crow = tid / CPR, cch = tid % CPR;
+  const rsrc_t obuf = make_rsrc(out, (uint32_t)((int64_t)M * N * 2));
+  const bool col_ok = n0 + 8 * cch < N;
+#pragma unroll 4
+  for (int r0 = 0; r0 < TM; r0 += RPP) {
+    const int row = r0 + crow;
+    const uint2 lo = *(const uint2*)(ob + row * OSTR + cch * 16);
+    const uint2 hi = *(const uint2*)(ob + row * OSTR + cch * 16 + 8);
+    const uint32_t off = (col_ok && m0 + row < M) ? (uint32_t)(((int64_t)(m0 + row) * N + n0 + 8 * cch) * 2) : kOOB;
+    buf_store16((v4i){(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y}, obuf, off);
   }
 }
 
@@ -447,7 +584,7 @@ extern "C" int gwa_svdq_gemm_w4a4_fp6(const uint8_t* qa6, const uint8_t* qw6, co
               epilogue_flags);
   const int64_t nst = K / 128;
   // the DMA offsets of a tile's last run stay below 2^31 + 2^16
-  GWA_REQUIRE(nst * (M + TM) * REC < (1ll << 31) && nst * (N + TN) * REC < (1ll << 31) && M * N * 2 < (1ll << 31) &&
+  GWA_REQUIRE(nst * (M + TM) * REC < (1ll << 31) && nst * (N + 256) * REC < (1ll << 31) && M * N * 2 < (1ll << 31) &&
                   M * R * 2 < (1ll << 31),
               "svdq_gemm_w4a4_fp6: operands must stay below 2 GiB (buffer addressing)");
   if (M == 0) return GWA_OK;
@@ -455,7 +592,12 @@ extern "C" int gwa_svdq_gemm_w4a4_fp6(const uint8_t* qa6, const uint8_t* qw6, co
   GWA_REQUIRE(GWA_ALIGNED(qa6, 16) && GWA_ALIGNED(qw6, 16) && GWA_ALIGNED(la, 16) && GWA_ALIGNED(up, 16) &&
                   GWA_ALIGNED(out, 8) && GWA_ALIGNED(bias, 2) && GWA_ALIGNED(second, 4) && GWA_ALIGNED(s2, 4),
               "svdq_gemm_w4a4_fp6: misaligned pointer");
-  const int64_t tiles = ((M + TM - 1) / TM) * ((N + TN - 1) / TN);
+  // 256 x 256 tiles halve the operand bytes staged per MAC; 256 x 128 tiles keep the software pipeline
+  // and give twice the workgroups. The wider tile is taken when it still fills the chip.
+  const int64_t tiles256 = ((M + TM - 1) / TM) * ((N + 255) / 256);
+  const bool wide = tiles256 >= 192;
+  const int TNv = wide ? 256 : 128;
+  const int64_t tiles = ((M + TM - 1) / TM) * ((N + TNv - 1) / TNv);
   GWA_REQUIRE(tiles < (1ll << 30), "svdq_gemm_w4a4_fp6: too many tiles");
   const bool gelu = epilogue_flags & GWA_EPI_GELU_TANH;
   const bool f16 = out_dtype == GWA_DT_F16;
@@ -468,9 +610,13 @@ extern "C" int gwa_svdq_gemm_w4a4_fp6(const uint8_t* qa6, const uint8_t* qw6, co
   const uint16_t* bp = (const uint16_t*)bias;
   uint16_t* op = (uint16_t*)out;
   const int m = (int)M, n = (int)N, k = (int)K;
-#define GWA_FP6_LAUNCH(RBV, GL, F16V)                                                                              \
-  hipLaunchKernelGGL((w4a4_gemm_fp6_kernel<RBV, GL, F16V>), grid, block, 0, s, qa6, qw6, s2, second, pc, lap, upp, \
-                     bp, op, m, n, k)
+#define GWA_FP6_LAUNCH(RBV, GL, F16V)                                                                          \
+  if (wide)                                                                                                    \
+    hipLaunchKernelGGL((w4a4_gemm_fp6_kernel<256, RBV, GL, F16V>), grid, block, 0, s, qa6, qw6, s2, second, pc, \
+                       lap, upp, bp, op, m, n, k);                                                              \
+  else                                                                                                         \
+    hipLaunchKernelGGL((w4a4_gemm_fp6_kernel<128, RBV, GL, F16V>), grid, block, 0, s, qa6, qw6, s2, second, pc, \
+                       lap, upp, bp, op, m, n, k)
 #define GWA_FP6_RB(RBV)                           \
   case RBV:                                       \
     if (gelu) {                                   \
