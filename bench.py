@@ -18,7 +18,8 @@ The ``roofline`` object covers the dominant kernel (the GEMM): its average
 launch duration comes from HIP events around a graph of K back-to-back GEMM
 launches on the stream they run on; ``traffic`` is the HBM bytes per launch
 measured with rocprofv3 FETCH_SIZE / WRITE_SIZE, scaled by the same
-counters' reading for a copy of known size (profiles/w4a4_gemm_c1_traffic.json).
+counters' reading for a copy of known size (profiles/w4a4_gemm_c1_traffic.json,
+written by ``--summarize-traffic``).
 ``cpu_baseline`` times the reference's CPU serving lane (dense fold + one
 bf16 Linear) on a bounded sample of the same workload. Prints ONE JSON line
 on stdout; progress goes to stderr.
@@ -73,6 +74,60 @@ def graph_time_ms(torch, fn, reps: int) -> float:
     return e0.elapsed_time(e1) / reps
 
 
+def _counter_median_kib(run_dir: Path, kernel_substr: str) -> tuple[str, float]:
+    """Median per-dispatch value of the single counter collected in ``run_dir`` for the first kernel whose
+    name contains ``kernel_substr`` (rocprofv3 ``--output-format csv``)."""
+    import csv
+    import statistics
+
+    files = sorted(run_dir.rglob("*counter_collection.csv"))
+    if not files:
+        raise FileNotFoundError(f"no counter_collection.csv under {run_dir}")
+    vals: dict[str, list[float]] = {}
+    for f in files:
+        with f.open() as fh:
+            for row in csv.DictReader(fh):
+                name = row["Kernel_Name"]
+                if kernel_substr in name:
+                    vals.setdefault(name, []).append(float(row["Counter_Value"]))
+    if not vals:
+        raise KeyError(f"no kernel matching {kernel_substr!r} in {run_dir}")
+    name = sorted(vals)[0]
+    return name, statistics.median(vals[name])
+
+
+def summarize_traffic(d: Path) -> int:
+    """HBM bytes per launch of the GEMM and kernel 1 from FETCH_SIZE / WRITE_SIZE (KiB per dispatch), each
+    scaled by what the same counter reads for a copy of COPY_BYTES."""
+    import torch  # noqa: F401  (only for the package's shape helpers)
+
+    from gen_worker_amd import synthetic
+    from gen_worker_amd.svdq import act_quant_bytes
+
+    cf = _counter_median_kib(d / "f_copy", "copyBuffer")[1]
+    cw = _counter_median_kib(d / "w_copy", "copyBuffer")[1]
+    ff, wf = COPY_BYTES / 1024.0 / cf, COPY_BYTES / 1024.0 / cw
+    cfg = synthetic.C1
+    m, n, k, r = cfg["m"], cfg["n"], cfg["k"], cfg["rank"]
+    gemm_alg = (m + n) * (k // 128) * 104 + m * r * 2 + n * r * 2 + n * 2 + m * n * 2
+    out = {"workload": "svdq_w4a4_linear_c1 (M=4608, N=K=3072, rank 32, bf16 out)",
+           "calibration": {"copy_bytes": COPY_BYTES, "copy_fetch_size_kib": cf, "copy_write_size_kib": cw,
+                           "fetch_factor": round(ff, 4), "write_factor": round(wf, 4)}}
+    for key, sub, alg in (("gemm", "w4a4_gemm_fp6_kernel", gemm_alg),
+                          ("act_quant", "svdq_quant_int4_kernel", act_quant_bytes(m, k, r, fp6=True))):
+        w = "gemm" if key == "gemm" else "quant"
+        name, f_kib = _counter_median_kib(d / f"f_{w}", sub)
+        _, w_kib = _counter_median_kib(d / f"w_{w}", sub)
+        rd, wr = int(f_kib * 1024 * ff), int(w_kib * 1024 * wf)
+        out[key] = {"kernel": name, "fetch_size_kib_per_launch": f_kib, "write_size_kib_per_launch": w_kib,
+                    "hbm_read_bytes_per_launch": rd, "hbm_write_bytes_per_launch": wr,
+                    "hbm_bytes_per_launch": rd + wr, "algorithmic_bytes_per_launch": alg}
+    path = ROOT / "profiles" / "w4a4_gemm_c1_traffic.json"
+    path.write_text(json.dumps(out, indent=1) + "\n")
+    print(json.dumps(out, indent=1))
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -82,7 +137,12 @@ def main() -> int:
     ap.add_argument("--cpu-rows", type=int, default=512, help="rows of the bounded CPU sample")
     ap.add_argument("--only", choices=("step", "gemm", "quant", "copy"), default=None)
     ap.add_argument("--iters", type=int, default=5)
+    ap.add_argument("--summarize-traffic", metavar="DIR", default=None,
+                    help="write profiles/w4a4_gemm_c1_traffic.json from the FETCH_SIZE / WRITE_SIZE runs in DIR "
+                         "(subdirectories f_<w>, w_<w> for w in gemm, quant, copy)")
     args = ap.parse_args()
+    if args.summarize_traffic:
+        return summarize_traffic(Path(args.summarize_traffic))
 
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}): this build's path is a single-GPU "
@@ -165,8 +225,8 @@ def main() -> int:
     tpath = ROOT / "profiles" / "w4a4_gemm_c1_traffic.json"
     if tpath.exists():
         try:
-            traffic = json.loads(tpath.read_text()).get("hbm_bytes_per_launch")
-        except (OSError, ValueError):
+            traffic = json.loads(tpath.read_text())["gemm"]["hbm_bytes_per_launch"]
+        except (OSError, ValueError, KeyError):
             traffic = None
 
     cpu = None
