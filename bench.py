@@ -128,6 +128,49 @@ def summarize_traffic(d: Path) -> int:
     return 0
 
 
+def bench_dit(args) -> int:
+    """Config 4: one Flux-dev-shaped denoiser forward (batch 1, 4096 image + 512 text tokens, 19 + 38
+    blocks), every linear W4A4 rank 32 vs the same model with bf16 nn.Linear GEMMs; bf16 SDPA in
+    both. Each model's forward is captured once in a HIP graph and replayed ``--steps`` times."""
+    import gc
+
+    import torch
+
+    import gen_worker_amd  # noqa: F401
+    from gen_worker_amd import _native
+    from gen_worker_amd.flux_dit import FluxDiT, FluxDiTConfig, block_int_ops, inputs, time_step_ms
+
+    _native.load()
+    torch.cuda.set_device(0)
+    cfg = FluxDiTConfig()
+    args_in = inputs(cfg)
+    res = {}
+    for kind in ("w4a4", "bf16"):
+        log(f"bench: building the {kind} DiT")
+        model = FluxDiT(kind, cfg)
+        torch.cuda.synchronize()
+        log(f"bench: timing the {kind} DiT step ({args.steps} graph replays)")
+        res[kind] = time_step_ms(model, args_in, steps=args.steps, warmup=args.warmup)
+        with torch.no_grad():
+            y = model(*args_in)
+        res[kind + "_finite"] = bool(torch.isfinite(y).all())
+        del model, y
+        gc.collect()
+        torch.cuda.empty_cache()
+    ops_ = block_int_ops(cfg)
+    out = {"metric": "DiT step ms (Flux-dev-shaped, batch 1, 4096+512 tokens, 19+38 blocks)",
+           "value": round(res["w4a4"], 3), "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "higher_is_better": False, "dtype": "int4", "data": "synthetic",
+           "config": {"workload": "flux_dit_c4", "hidden": cfg.hidden, "heads": cfg.heads, "mlp": cfg.mlp,
+                      "dual_blocks": cfg.n_dual, "single_blocks": cfg.n_single, "img_tokens": cfg.img_tokens,
+                      "txt_tokens": cfg.txt_tokens, "rank": cfg.rank, "attention": "bf16 SDPA",
+                      "timing": "forward captured in one HIP graph, replayed"},
+           "bf16_gemm_ms": round(res["bf16"], 3), "speedup_vs_bf16": round(res["bf16"] / res["w4a4"], 4),
+           "block_linear_int_ops": ops_, "outputs_finite": {"w4a4": res["w4a4_finite"], "bf16": res["bf16_finite"]}}
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -137,12 +180,20 @@ def main() -> int:
     ap.add_argument("--cpu-rows", type=int, default=512, help="rows of the bounded CPU sample")
     ap.add_argument("--only", choices=("step", "gemm", "quant", "copy"), default=None)
     ap.add_argument("--iters", type=int, default=5)
+    ap.add_argument("--workload", choices=("c1", "dit"), default="c1",
+                    help="c1: the config-1 linear (the default bench line); dit: the config-4 Flux-shaped DiT "
+                         "step, W4A4 vs the same model with bf16 GEMMs")
     ap.add_argument("--summarize-traffic", metavar="DIR", default=None,
                     help="write profiles/w4a4_gemm_c1_traffic.json from the FETCH_SIZE / WRITE_SIZE runs in DIR "
                          "(subdirectories f_<w>, w_<w> for w in gemm, quant, copy)")
     args = ap.parse_args()
     if args.summarize_traffic:
         return summarize_traffic(Path(args.summarize_traffic))
+    if args.workload == "dit":
+        if args.gpus != 1:
+            print("bench.py measures one GPU only", file=sys.stderr)
+            return 2
+        return bench_dit(args)
 
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}): this build's path is a single-GPU "

@@ -1,0 +1,272 @@
+"""Synthetic Flux-dev-shaped DiT denoiser: the config-4 workload of the benchmark.
+
+One denoising forward at batch 1, 1024 x 1024 (4096 image tokens of 64 latent
+channels + 512 text tokens of 4096 T5 features), 19 dual-stream and 38
+single-stream blocks, hidden 3072, 24 heads of 128, MLP ratio 4: the block
+structure of diffusers' ``FluxTransformer2DModel`` (AdaLayerNormZero
+modulation, joint attention over [text; image] with RMSNorm on q/k and rotary
+embeddings, GELU-tanh MLPs; single blocks run attention and the MLP side by
+side and project their concatenation). The timestep / guidance / pooled-text
+conditioning enters as a seeded random embedding ``temb`` [1, 3072].
+
+Every linear is built by a factory, so the same model runs as:
+  * ``"w4a4"``: every linear an SVDQuant W4A4 layer (``SvdqW4A4Linear``, rank
+    32, group 64; int4 codes, fp16 scales, low-rank factors and bias random),
+    GELU fused into the fc1 epilogues;
+  * ``"bf16"``: every linear a bf16 ``nn.Linear`` (the bf16 GEMM path).
+Attention is bf16 ``scaled_dot_product_attention`` in both. Weights are
+random-init on the device from seeded generators; values are chosen only to
+keep activations finite and O(1) through the 57 blocks.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Callable, Optional
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+from torch import Tensor
+
+
+@dataclass(frozen=True)
+class FluxDiTConfig:
+    hidden: int = 3072
+    heads: int = 24
+    head_dim: int = 128
+    mlp: int = 12288
+    n_dual: int = 19
+    n_single: int = 38
+    img_tokens: int = 4096
+    txt_tokens: int = 512
+    in_channels: int = 64
+    txt_dim: int = 4096
+    rank: int = 32
+
+
+def _w4a4_linear(in_f: int, out_f: int, seed: int, device, rank: int, gelu: bool = False) -> nn.Module:
+    """A random-init SvdqW4A4Linear: uniform int4 codes, fp16 group scales with effective weight std ~0.02,
+    smoothing factors log-uniform in [0.5, 2], L1 / L2 / bias ~ N(0, 0.02)."""
+    from .svdq import SvdqW4A4Linear
+
+    g = torch.Generator(device=device).manual_seed(seed)
+    mod = SvdqW4A4Linear(in_f, out_f, rank=rank, bias=True, activation="gelu_tanh" if gelu else None,
+                         device=device)
+    with torch.no_grad():
+        mod.weight.copy_(torch.randint(0, 256, mod.weight.shape, generator=g, device=device, dtype=torch.int32)
+                         .to(torch.uint8))
+        # uniform codes in [-8, 7] have std ~4.6: scale for an effective weight std of ~0.02
+        sc = 0.02 / 4.61 * (0.75 + 0.5 * torch.rand(mod.weight_scale.shape, generator=g, device=device))
+        mod.weight_scale.copy_(sc.to(torch.float16))
+        u = torch.rand(in_f, generator=g, device=device)
+        mod.smooth_factor.copy_(torch.exp(math.log(0.5) + u * math.log(4.0)).to(torch.bfloat16))
+        if rank:
+            mod.proj_down.copy_(torch.randn(in_f, rank, generator=g, device=device).mul_(0.02).to(torch.bfloat16))
+            mod.proj_up.copy_(torch.randn(out_f, rank, generator=g, device=device).mul_(0.02).to(torch.bfloat16))
+        mod.bias.copy_(torch.randn(out_f, generator=g, device=device).mul_(0.02).to(torch.bfloat16))
+    mod.refresh_derived()
+    return mod
+
+
+class _Bf16Linear(nn.Module):
+    """bf16 nn.Linear (weights ~ N(0, 0.02)) with the same optional GELU-tanh as the fused lane."""
+
+    def __init__(self, in_f: int, out_f: int, seed: int, device, gelu: bool = False) -> None:
+        super().__init__()
+        g = torch.Generator(device=device).manual_seed(seed)
+        self.lin = nn.Linear(in_f, out_f, bias=True, device=device, dtype=torch.bfloat16)
+        with torch.no_grad():
+            self.lin.weight.copy_(torch.randn(out_f, in_f, generator=g, device=device).mul_(0.02))
+            self.lin.bias.copy_(torch.randn(out_f, generator=g, device=device).mul_(0.02))
+        self.gelu = gelu
+
+    def forward(self, x: Tensor) -> Tensor:
+        y = self.lin(x)
+        return F.gelu(y, approximate="tanh") if self.gelu else y
+
+
+def linear_factory(kind: str, device, rank: int) -> Callable[..., nn.Module]:
+    """``make(in_f, out_f, seed, gelu=False)`` for ``kind`` in ("w4a4", "bf16")."""
+    if kind == "w4a4":
+        return lambda i, o, s, gelu=False: _w4a4_linear(i, o, s, device, rank, gelu)
+    if kind == "bf16":
+        return lambda i, o, s, gelu=False: _Bf16Linear(i, o, s, device, gelu)
+    raise ValueError(f"linear kind {kind!r} not in ('w4a4', 'bf16')")
+
+
+def _rms(x: Tensor, w: Tensor, eps: float = 1e-6) -> Tensor:
+    xf = x.float()
+    return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)).to(x.dtype) * w
+
+
+def _ln(x: Tensor) -> Tensor:
+    return F.layer_norm(x, (x.shape[-1],), eps=1e-6)
+
+
+def _rope(x: Tensor, cos: Tensor, sin: Tensor) -> Tensor:
+    """Rotary embedding on interleaved (even, odd) pairs: x [S, H, D], cos / sin [S, 1, D/2]."""
+    xe, xo = x[..., 0::2], x[..., 1::2]
+    return torch.stack((xe * cos - xo * sin, xe * sin + xo * cos), dim=-1).flatten(-2)
+
+
+def _attention(q: Tensor, k: Tensor, v: Tensor) -> Tensor:
+    """[S, H, D] bf16 -> [S, H*D] via SDPA on [1, H, S, D]."""
+    s, h, d = q.shape
+    o = F.scaled_dot_product_attention(q.transpose(0, 1).unsqueeze(0), k.transpose(0, 1).unsqueeze(0),
+                                       v.transpose(0, 1).unsqueeze(0))
+    return o.squeeze(0).transpose(0, 1).reshape(s, h * d)
+
+
+class DualBlock(nn.Module):
+    def __init__(self, cfg: FluxDiTConfig, make, seed: int, device) -> None:
+        super().__init__()
+        c = cfg.hidden
+        self.cfg = cfg
+        self.mod_img, self.mod_txt = make(c, 6 * c, seed), make(c, 6 * c, seed + 1)
+        self.qkv_img, self.qkv_txt = make(c, 3 * c, seed + 2), make(c, 3 * c, seed + 3)
+        self.o_img, self.o_txt = make(c, c, seed + 4), make(c, c, seed + 5)
+        self.fc1_img, self.fc1_txt = make(c, cfg.mlp, seed + 6, gelu=True), make(c, cfg.mlp, seed + 7, gelu=True)
+        self.fc2_img, self.fc2_txt = make(cfg.mlp, c, seed + 8), make(cfg.mlp, c, seed + 9)
+        ones = torch.ones(cfg.head_dim, device=device, dtype=torch.bfloat16)
+        self.register_buffer("qn_img", ones.clone())
+        self.register_buffer("kn_img", ones.clone())
+        self.register_buffer("qn_txt", ones.clone())
+        self.register_buffer("kn_txt", ones.clone())
+
+    def forward(self, img: Tensor, txt: Tensor, temb: Tensor, cos: Tensor, sin: Tensor) -> tuple[Tensor, Tensor]:
+        cfg = self.cfg
+        sh1, sc1, g1, sh2, sc2, g2 = self.mod_img(temb).chunk(6, dim=-1)
+        tsh1, tsc1, tg1, tsh2, tsc2, tg2 = self.mod_txt(temb).chunk(6, dim=-1)
+        ni = _ln(img) * (1 + sc1) + sh1
+        nt = _ln(txt) * (1 + tsc1) + tsh1
+        hq = (-1, cfg.heads, cfg.head_dim)
+        qi, ki, vi = self.qkv_img(ni).chunk(3, dim=-1)
+        qt, kt, vt = self.qkv_txt(nt).chunk(3, dim=-1)
+        q = torch.cat((_rms(qt.reshape(hq), self.qn_txt), _rms(qi.reshape(hq), self.qn_img)))
+        k = torch.cat((_rms(kt.reshape(hq), self.kn_txt), _rms(ki.reshape(hq), self.kn_img)))
+        v = torch.cat((vt.reshape(hq), vi.reshape(hq)))
+        a = _attention(_rope(q, cos, sin), _rope(k, cos, sin), v)
+        at, ai = a[: txt.shape[0]], a[txt.shape[0]:]
+        img = img + g1 * self.o_img(ai.contiguous())
+        txt = txt + tg1 * self.o_txt(at.contiguous())
+        img = img + g2 * self.fc2_img(self.fc1_img(_ln(img) * (1 + sc2) + sh2))
+        txt = txt + tg2 * self.fc2_txt(self.fc1_txt(_ln(txt) * (1 + tsc2) + tsh2))
+        return img, txt
+
+
+class SingleBlock(nn.Module):
+    def __init__(self, cfg: FluxDiTConfig, make, seed: int, device) -> None:
+        super().__init__()
+        c = cfg.hidden
+        self.cfg = cfg
+        self.mod = make(c, 3 * c, seed)
+        self.qkv = make(c, 3 * c, seed + 1)
+        self.mlp = make(c, cfg.mlp, seed + 2, gelu=True)
+        self.proj_out = make(c + cfg.mlp, c, seed + 3)
+        ones = torch.ones(cfg.head_dim, device=device, dtype=torch.bfloat16)
+        self.register_buffer("qn", ones.clone())
+        self.register_buffer("kn", ones.clone())
+
+    def forward(self, x: Tensor, temb: Tensor, cos: Tensor, sin: Tensor) -> Tensor:
+        cfg = self.cfg
+        sh, sc, g = self.mod(temb).chunk(3, dim=-1)
+        n = _ln(x) * (1 + sc) + sh
+        hq = (-1, cfg.heads, cfg.head_dim)
+        q, k, v = self.qkv(n).chunk(3, dim=-1)
+        a = _attention(_rope(_rms(q.reshape(hq), self.qn), cos, sin), _rope(_rms(k.reshape(hq), self.kn), cos, sin),
+                       v.reshape(hq))
+        return x + g * self.proj_out(torch.cat((a, self.mlp(n)), dim=-1))
+
+
+class FluxDiT(nn.Module):
+    """The config-4 denoiser; ``forward(latents [4096, 64], text [512, 4096], temb [1, 3072]) -> [4096, 64]``."""
+
+    def __init__(self, kind: str, cfg: FluxDiTConfig = FluxDiTConfig(), device="cuda", seed: int = 1000) -> None:
+        super().__init__()
+        make = linear_factory(kind, device, cfg.rank)
+        self.cfg, self.kind = cfg, kind
+        c = cfg.hidden
+        self.x_embedder = make(cfg.in_channels, c, seed)
+        self.context_embedder = make(cfg.txt_dim, c, seed + 1)
+        self.dual = nn.ModuleList(DualBlock(cfg, make, seed + 100 + 10 * i, device) for i in range(cfg.n_dual))
+        self.single = nn.ModuleList(SingleBlock(cfg, make, seed + 400 + 10 * i, device)
+                                    for i in range(cfg.n_single))
+        self.norm_out = make(c, 2 * c, seed + 2)
+        self.proj_out = make(c, cfg.in_channels, seed + 3)
+        # rotary tables for the 4608 joint positions ([text; image]), theta 10000
+        s = cfg.txt_tokens + cfg.img_tokens
+        half = cfg.head_dim // 2
+        inv = 1.0 / (10000.0 ** (torch.arange(half, device=device, dtype=torch.float32) / half))
+        ang = torch.arange(s, device=device, dtype=torch.float32)[:, None] * inv[None, :]
+        self.register_buffer("cos", ang.cos().to(torch.bfloat16).unsqueeze(1))
+        self.register_buffer("sin", ang.sin().to(torch.bfloat16).unsqueeze(1))
+
+    def forward(self, latents: Tensor, text: Tensor, temb: Tensor) -> Tensor:
+        t = F.silu(temb)
+        img = self.x_embedder(latents)
+        txt = self.context_embedder(text)
+        for blk in self.dual:
+            img, txt = blk(img, txt, t, self.cos, self.sin)
+        x = torch.cat((txt, img))
+        for blk in self.single:
+            x = blk(x, t, self.cos, self.sin)
+        img = x[self.cfg.txt_tokens:]
+        scale, shift = self.norm_out(t).chunk(2, dim=-1)
+        return self.proj_out((_ln(img) * (1 + scale) + shift).contiguous())
+
+
+def inputs(cfg: FluxDiTConfig = FluxDiTConfig(), device="cuda", seed: int = 7) -> tuple[Tensor, Tensor, Tensor]:
+    """Seeded (latents [4096, 64], text features [512, 4096], temb [1, 3072]) in bf16."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    lat = torch.randn(cfg.img_tokens, cfg.in_channels, generator=g, device=device).to(torch.bfloat16)
+    txt = torch.randn(cfg.txt_tokens, cfg.txt_dim, generator=g, device=device).to(torch.bfloat16)
+    temb = torch.randn(1, cfg.hidden, generator=g, device=device).to(torch.bfloat16)
+    return lat, txt, temb
+
+
+def block_int_ops(cfg: FluxDiTConfig = FluxDiTConfig()) -> int:
+    """2 * M * N * K of every block linear (the modulation / embedding linears excluded)."""
+    c, m4, s = cfg.hidden, cfg.mlp, cfg.img_tokens + cfg.txt_tokens
+    per_stream = c * 3 * c + c * c + c * m4 + m4 * c
+    dual = 2 * (cfg.img_tokens + cfg.txt_tokens) * per_stream
+    single = 2 * s * (c * 3 * c + c * m4 + (c + m4) * c)
+    return cfg.n_dual * dual + cfg.n_single * single
+
+
+def time_step_ms(model: nn.Module, args: tuple[Tensor, ...], steps: int = 5, warmup: int = 2,
+                 graph: bool = True) -> float:
+    """Mean ms per forward, replaying ``steps`` forwards captured in one HIP graph (or eager)."""
+    with torch.no_grad():
+        for _ in range(warmup):
+            model(*args)
+        torch.cuda.synchronize()
+        if graph:
+            s = torch.cuda.Stream()
+            s.wait_stream(torch.cuda.current_stream())
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.stream(s):
+                with torch.cuda.graph(g, stream=s):
+                    out = model(*args)
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(steps):
+                g.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            del out
+            return e0.elapsed_time(e1) / steps
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            model(*args)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps
+
+
+__all__ = ["FluxDiT", "FluxDiTConfig", "block_int_ops", "inputs", "linear_factory", "time_step_ms"]
