@@ -147,6 +147,49 @@ int gwa_svdq_gemm_w4a4_fp6(const uint8_t* qa6, const uint8_t* qw6,
                            void* out, int out_dtype, int epilogue_flags,
                            int64_t M, int64_t N, int64_t K, void* stream);
 
+/* Kernel 2 with the next layer's activation quantization fused into the
+ * epilogue (config-2 fc1 -> GELU -> fc2). The reference has no kernel for
+ * this: it composes Linear -> GELU -> Linear (diffusers FeedForward), i.e.
+ * this layer's epilogue (models/svdq_fused.py:315-377) followed by the next
+ * layer's svdq_quant (models/svdq_fused.py:293-306) and `la = x2 @
+ * proj_down` (:524) on this layer's bf16 output. Here the bf16 output tile
+ * never leaves the chip:
+ *   y        = this layer's output exactly as gwa_svdq_gemm_w4a4_fp6 computes
+ *              it (bf16), also stored to `out` unless out is NULL
+ *   next_q6  uint8 [N/128, M, 104] (out): the next layer's fp6 operand
+ *            records of y — bit-identical to gwa_svdq_quant_int4(y,
+ *            next_smooth, s2 = NULL, ..., GWA_QFMT_FP6, ...). The pointer may
+ *            sit inside a larger record buffer of the same M (stage-major:
+ *            stage s at byte s * M * 104), e.g. at stage 24 of a [120, M, 104]
+ *            buffer whose first stages another producer writes.
+ *   next_la32 fp32 [M, next_rank] (in/out): next_la32 += y @ proj_down_next,
+ *            summed over this layer's column tiles with atomic adds (the
+ *            order of the fp32 additions varies from run to run); round to
+ *            bf16 for the next layer's la. NULL iff next_proj_down_op is NULL.
+ *   next_smooth       bf16 [N] (the next layer's smoothing factors) or NULL
+ *   next_proj_down_op the next layer's proj_down [N, next_rank] in MFMA operand
+ *            order (gwa_svdq_prep_proj_down), next_rank in {0,16,32,64,128}
+ * Single-level (the next layer's s2 = 1). Output dtype bf16. N % 128 == 0,
+ * K % 128 == 0. */
+int gwa_svdq_gemm_w4a4_fp6_next(const uint8_t* qa6, const uint8_t* qw6,
+                                const float* s2, const float* second, int64_t second_numel,
+                                const void* la, const void* up, int64_t rank, const void* bias,
+                                void* out, int epilogue_flags,
+                                const void* next_smooth, const void* next_proj_down_op, int64_t next_rank,
+                                uint8_t* next_q6, float* next_la32,
+                                int64_t M, int64_t N, int64_t K, void* stream);
+
+/* Kernel 1 into fp6 records with the low-rank product ACCUMULATED in fp32:
+ * la32 [M, rank] += x @ proj_down (a read-modify-write per row, ordered after
+ * every earlier writer of la32 on the stream). With
+ * gwa_svdq_gemm_w4a4_fp6_next it builds the input of a layer whose K is the
+ * concatenation of two producers' outputs (Flux's single-block proj_out
+ * takes [attention; MLP]): each producer writes its own stages of one
+ * record buffer and adds its part of x @ proj_down. Otherwise as
+ * gwa_svdq_quant_int4(..., s2 = NULL, ..., GWA_QFMT_FP6, q6, NULL, ...). */
+int gwa_svdq_quant_fp6_la_f32(const void* x, int64_t ldx, const void* smooth, const void* proj_down_op,
+                              int64_t rank, uint8_t* q6, float* la32, int64_t M, int64_t K, void* stream);
+
 /* Debug: exact int32 per-group partial sums (layout of gwa_svdq_group_psums)
  * through the fp6 GEMM's MFMA on fp6 operand records. No reference counterpart. */
 int gwa_svdq_group_psums_fp6(const uint8_t* qa6, const uint8_t* qw6, int32_t* out,

@@ -1,6 +1,7 @@
 // Activation-side kernels: int4 group-64 quantization (+ fused x @ proj_down),
 // int8 per-token quantization, and the standalone SVDQuant epilogue.
 #include "gwa_common.h"
+#include "quant_g64.h"
 
 // ---------------------------------------------------------------------------
 // Kernel 1: smoothing divide -> group-64 absmax -> fp16 scale -> int4 codes;
@@ -29,43 +30,15 @@
 // stage's two fp16 group scales).
 //
 // Arithmetic = the reference order (models/svdq_fused.py:88-103,
-// models/nvfp4_quant.py:96-102): xs = RN_bf16(RN_f32(x / smooth));
-// scale = fp16(clamp(RN_f32(amax / (7 * s2)), 2^-24, 65504));
-// code = clamp(rne(RN_f32(xs / (float(scale) * s2))), -8, 7).
-//
-// Fast path (bit-identical, no per-element division):
-//  * smoothing: xs = RN_bf16(x * r), r = RN_f32(1 / smooth). For bf16 x and a
-//    normal bf16 smooth, x/s lies at least 2^-18 (relative) from any bf16
-//    rounding tie unless it is exact, and |x*r - x/s| <= 2^-23 |x/s|, so both
-//    round to the same bf16.
-//  * codes (s2 == 1, scale a normal fp16 below the clamp): q = xs / d with an
-//    8-bit-significand xs and an 11-bit d is either an exact half-integer or
-//    more than 2^-12 from one; p = xs * rcp(d) is within 2^-19 of q. Adding
-//    3072 rounds p onto a 2^-12 grid, which lands exact ties exactly on k+1/2
-//    and leaves every other value on its own side; adding (1.5*2^23 - 3072)
-//    then rounds that grid value to an integer with ties-to-even, exactly the
-//    RNE of q. |q| <= 7*(1 + 2^-11) < 7.5 here, so no clamp is needed, and
-//    the code is the low nibble of the float's bits.
-//  Anything else (s2 != 1, non-normal smooth, clamped or subnormal scales)
-//  takes the IEEE-division path (a wave-uniform branch).
+// models/nvfp4_quant.py:96-102), computed by the per-lane quantizer of
+// quant_g64.h (bit-identical fast paths for smoothing, scale and codes).
 // ---------------------------------------------------------------------------
 namespace {
-
-constexpr float kScaleMin = 5.9604644775390625e-08f;  // 2^-24, smallest positive fp16
-constexpr float kFp16Max = 65504.0f;
-constexpr float kFp16MinNormal = 6.103515625e-05f;     // 2^-14
-constexpr float kSnap = 3072.0f;                       // 1.5 * 2^11: spacing 2^-12 on [2048, 4096)
-constexpr float kRound = 12582912.0f - 3072.0f;        // 1.5 * 2^23 - 3072
 
 constexpr int KT = 256;                 // columns per round
 constexpr int XT_STR = KT * 2 + 16;     // LDS row stride of the x tile (bytes)
 constexpr int XT_BYTES = 16 * XT_STR;   // 8448
 constexpr int QBUF = XT_BYTES + KT * 4 * 2 + 16;  // tile + reciprocals + factors + flag word
-
-typedef float v2f __attribute__((ext_vector_type(2)));
-typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
-typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
-typedef unsigned int v3u __attribute__((ext_vector_type(3)));
 
 __device__ __forceinline__ void unpack8_bf16(v4i w, float* v) {
 #pragma unroll
@@ -76,31 +49,11 @@ __device__ __forceinline__ void unpack8_bf16(v4i w, float* v) {
   }
 }
 
-__device__ __forceinline__ uint32_t int4_code_exact(float v, float d) {
-  float q = __builtin_rintf(v / d);
-  q = fminf(fmaxf(q, -8.0f), 7.0f);
-  return (uint32_t)((int)q) & 0xFu;
-}
-
-// smoothing factor usable by the multiply path: 1/s is a normal float
-__device__ __forceinline__ bool smooth_ok(float s) {
-  const float a = fabsf(s);
-  return a >= 1.1754943508222875e-38f && a < 8.507059173023462e37f;
-}
-
-// max over the 8-lane group (lanes 8j .. 8j+7) of a 32-bit value
-__device__ __forceinline__ uint32_t oct_max(uint32_t v) {
-  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
-  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));   // quad_perm 2,3,0,1
-  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));  // row_half_mirror
-  return v;
-}
-
 template <int RB, int FMT, int PF>
 __global__ __launch_bounds__(512) void svdq_quant_int4_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, const uint16_t* __restrict__ smooth,
     const float* __restrict__ s2p, const uint16_t* __restrict__ pdo, uint8_t* __restrict__ q,
-    uint16_t* __restrict__ sc, uint16_t* __restrict__ la, int M, int K) {
+    uint16_t* __restrict__ sc, void* __restrict__ la, int la_f32_add, int M, int K) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   constexpr int RBX = RB > 0 ? RB : 1;
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -151,14 +104,12 @@ __global__ __launch_bounds__(512) void svdq_quant_int4_kernel(
       rs[2 * tid + 1] = 1.0f / s1;
       fs[2 * tid] = s0;
       fs[2 * tid + 1] = s1;
-      if (r * KT + 2 * tid < K && (!smooth_ok(s0) || !smooth_ok(s1))) *(int*)(fs + KT) = r;
+      if (r * KT + 2 * tid < K && (!g64::smooth_ok(s0) || !g64::smooth_ok(s1))) *(int*)(fs + KT) = r;
     }
   };
 
   const float s2 = s2p ? *s2p : 1.0f;
   const bool s2_one = (s2 == 1.0f);
-  const float den7 = 7.0f * s2;
-  const float r7 = 1.0f / 7.0f;
 
   // quantization roles: wave w rows 2w, 2w+1; lane -> row 2w + (lane >> 5), 8 columns at 8 (lane & 31)
   const int qr = 2 * wave + (lane >> 5), qc = (lane & 31) * 8;
@@ -201,86 +152,19 @@ __global__ __launch_bounds__(512) void svdq_quant_int4_kernel(
           for (int t = 0; t < 4; ++t) w[t] = (uint32_t)c0[t];
         } else {
           const bool bad = *(const int*)(base + XT_BYTES + KT * 8) == r;
-          float v[8], f[8];
-          unpack8_bf16(c0, v);
+          float f[8];
           const float* src = (const float*)(base + XT_BYTES) + (bad ? KT : 0) + qc;
           *(v4f*)(f) = *(const v4f*)(src);
           *(v4f*)(f + 4) = *(const v4f*)(src + 4);
-          if (!bad) {
-#pragma unroll
-            for (int t = 0; t < 8; ++t) v[t] *= f[t];
-          } else {
-#pragma unroll
-            for (int t = 0; t < 8; ++t) v[t] /= f[t];
-          }
-#pragma unroll
-          for (int t = 0; t < 4; ++t)
-            w[t] = __builtin_bit_cast(uint32_t, __builtin_convertvector((v2f){v[2 * t], v[2 * t + 1]}, v2bf));
+          g64::smooth8(c0, f, bad, w);
         }
-        // group absmax on the bf16 bit patterns (|x| orders like its bits), over the 8 lanes of the group
-        v2u16 mx = {0, 0};
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-          mx = __builtin_elementwise_max(mx, __builtin_bit_cast(v2u16, w[t] & 0x7fff7fffu));
-        const uint32_t mb = oct_max(mx[0] > mx[1] ? mx[0] : mx[1]);
-        const float amax = __uint_as_float(mb << 16);
-
-        // RN(amax / 7): for a finite bf16 amax, one fma correction of amax * RN(1/7) is the correctly
-        // rounded quotient wherever it is >= 2^-24 (below that the scale clamps anyway); otherwise
-        // (s2 != 1, inf/NaN) the IEEE division (wave-uniform branch)
-        float scl;
-        const bool easy = s2_one && (mb & 0x7F80u) != 0x7F80u;
-        if (__builtin_amdgcn_ballot_w64(!easy) == 0) {
-          const float q1 = amax * r7;
-          scl = fmaf(fmaf(-7.0f, q1, amax), r7, q1);
-        } else {
-          scl = amax / den7;
-        }
-        const bool fast = !valid || (s2_one && scl >= kFp16MinNormal && scl < kFp16Max);
-        scl = fminf(fmaxf(scl, kScaleMin), kFp16Max);
-        const uint16_t sh = f32_to_f16_bits(scl);
-        const float d = f16_bits_to_f32(sh) * s2;
-
-        float v[8];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          v[2 * t] = bf16_lo(w[t]);
-          v[2 * t + 1] = bf16_hi(w[t]);
-        }
-        // codes as bytes: nb[j] holds elements 4j .. 4j+3, one nibble per byte
         uint32_t nb[2];
-        if (__builtin_amdgcn_ballot_w64(!fast) == 0) {  // wave-uniform; neither side touches memory
-          const float rd = __builtin_amdgcn_rcpf(d);
-#pragma unroll
-          for (int j4 = 0; j4 < 2; ++j4) {
-            uint32_t hb[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) hb[e] = __float_as_uint(((v[4 * j4 + e] * rd) + kSnap) + kRound);
-            nb[j4] = __builtin_amdgcn_perm(__builtin_amdgcn_perm(hb[3], hb[2], 0x0c0c0400u),
-                                           __builtin_amdgcn_perm(hb[1], hb[0], 0x0c0c0400u), 0x05040100u) &
-                     0x0F0F0F0Fu;
-          }
-        } else {
-#pragma unroll
-          for (int j4 = 0; j4 < 2; ++j4) {
-            nb[j4] = 0;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) nb[j4] |= int4_code_exact(v[4 * j4 + e], d) << (8 * e);
-          }
-        }
+        uint16_t sh;
+        g64::quant8(w, valid, s2_one, s2, nb, sh);
         if (FMT == GWA_QFMT_FP6) {
-          // 8 codes = 48 bits per lane; lane pairs share three dwords (the even lane stores the first two)
-          // of the record of (128-column stage g / 2, row), at byte 48 (g % 2) + 6 (lane % 8)
-          const uint32_t t0 = pack6_x4(e3m2_x4(nb[0])), t1 = pack6_x4(e3m2_x4(nb[1]));
-          const uint32_t lo32 = t0 | (t1 << 24), hi16 = t1 >> 8;          // this lane's 48 bits
-          const uint32_t nlo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)lo32, 0xB1, 0xF, 0xF, false);
-          const bool even = (lane & 1) == 0;
+          // record of (128-column stage g / 2, row), group g % 2 of the stage
           const uint32_t rec = (uint32_t)(((int64_t)(g >> 1) * M + grow) * GWA_FP6_REC);
-          const uint32_t base6 = valid ? rec + (uint32_t)((g & 1) * 48 + (lane & 6) * 6) : kOOB;
-          // branch-free: each lane issues both stores, the one that is not its own goes out of range
-          buf_store8(make_uint2(lo32, hi16 | (nlo << 16)), qbuf, even ? base6 : kOOB);
-          buf_store4((lo32 >> 16) | (hi16 << 16), qbuf, (!even && valid) ? base6 + 8 : kOOB);
-          buf_store2(sh, qbuf, (valid && (lane & 7) == 0) ? rec + 96u + (uint32_t)((g & 1) * 2) : kOOB);
+          g64::store_fp6(qbuf, rec, g & 1, lane, nb, sh, valid);
         } else {
           const uint32_t a = nb[0], bb = nb[1];
           const uint32_t pa = (a & 0xFu) | ((a >> 4) & 0xF0u) | ((a >> 8) & 0xF00u) | ((a >> 12) & 0xF000u);
@@ -303,7 +187,7 @@ __global__ __launch_bounds__(512) void svdq_quant_int4_kernel(
   }
 
   if (RB > 0) {
-    // sum the 8 waves' partial la blocks through LDS; wave 0 writes bf16
+    // sum the 8 waves' partial la blocks through LDS; wave 0 writes bf16 (or adds into fp32)
     __syncthreads();
     float* lap = (float*)lds;
 #pragma unroll
@@ -319,7 +203,11 @@ __global__ __launch_bounds__(512) void svdq_quant_int4_kernel(
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
           const int r = row0 + 4 * (lane >> 4) + t;
-          if (r < M) la[(int64_t)r * R + rb * 16 + (lane & 15)] = f32_to_bf16(s[t]);
+          if (r < M) {
+            const int64_t i = (int64_t)r * R + rb * 16 + (lane & 15);
+            if (la_f32_add) ((float*)la)[i] += s[t];  // rows are this workgroup's alone
+            else ((uint16_t*)la)[i] = f32_to_bf16(s[t]);
+          }
         }
       }
     }
@@ -427,9 +315,9 @@ extern "C" int gwa_svdq_prep_proj_down(const void* proj_down, void* out, int64_t
   return gwa_check_launch("svdq_prep_proj_down");
 }
 
-extern "C" int gwa_svdq_quant_int4(const void* x, int64_t ldx, const void* smooth, const float* s2,
-                                   const void* proj_down_op, int64_t rank, int out_format, uint8_t* q,
-                                   void* scales, void* la, int64_t M, int64_t K, void* stream) {
+static int quant_int4(const void* x, int64_t ldx, const void* smooth, const float* s2, const void* proj_down_op,
+                      int64_t rank, int out_format, uint8_t* q, void* scales, void* la, int la_f32_add, int64_t M,
+                      int64_t K, void* stream) {
   GWA_REQUIRE(M >= 0 && K > 0, "svdq_quant_int4: bad shape M=%lld K=%lld", (long long)M, (long long)K);
   GWA_REQUIRE(K % 64 == 0, "svdq_quant_int4: K=%lld is not a multiple of 64", (long long)K);
   GWA_REQUIRE(ldx >= K && ldx % 8 == 0, "svdq_quant_int4: row stride %lld must be >= K and a multiple of 8",
@@ -448,15 +336,15 @@ extern "C" int gwa_svdq_quant_int4(const void* x, int64_t ldx, const void* smoot
               "svdq_quant_int4: x and q must stay below 2 GiB (buffer addressing)");
   if (M == 0) return GWA_OK;
   GWA_REQUIRE(x && q && (scales || out_format == GWA_QFMT_FP6), "svdq_quant_int4: null pointer");
-  GWA_REQUIRE(GWA_ALIGNED(x, 16) && GWA_ALIGNED(q, 16) && GWA_ALIGNED(scales, 2) && GWA_ALIGNED(smooth, 4) &&
-                  GWA_ALIGNED(proj_down_op, 16) && GWA_ALIGNED(la, 2),
-              "svdq_quant_int4: x, q and proj_down_op must be 16-byte aligned");
+  GWA_REQUIRE(GWA_ALIGNED(x, 16) && GWA_ALIGNED(q, out_format == GWA_QFMT_FP6 ? 8 : 16) && GWA_ALIGNED(scales, 2) && GWA_ALIGNED(smooth, 4) &&
+                  GWA_ALIGNED(proj_down_op, 16) && GWA_ALIGNED(la, la_f32_add ? 4 : 2),
+              "svdq_quant_int4: x and proj_down_op must be 16-byte aligned, q 16 (int4) or 8 (fp6)");
   hipStream_t s = (hipStream_t)stream;
   const uint16_t* xp = (const uint16_t*)x;
   const uint16_t* sm = (const uint16_t*)smooth;
   const uint16_t* pd = (const uint16_t*)proj_down_op;
   uint16_t* sc = (uint16_t*)scales;
-  uint16_t* lp = (uint16_t*)la;
+  void* lp = la;
   const int m = (int)M, k = (int)K;
   const int rb = (int)(R / 16);
   const size_t lds = 2 * (size_t)QBUF > (size_t)rb * 8192 ? 2 * (size_t)QBUF : (size_t)rb * 8192;
@@ -465,10 +353,10 @@ extern "C" int gwa_svdq_quant_int4(const void* x, int64_t ldx, const void* smoot
 #define GWA_QUANT_LAUNCH(RBV, PFV)                                                                               \
   if (fp6)                                                                                                       \
     hipLaunchKernelGGL((svdq_quant_int4_kernel<RBV, GWA_QFMT_FP6, PFV>), grid, block, lds, s, xp, ldx, sm, s2, pd, \
-                       q, sc, lp, m, k);                                                                          \
+                       q, sc, lp, la_f32_add, m, k);                                                              \
   else                                                                                                           \
     hipLaunchKernelGGL((svdq_quant_int4_kernel<RBV, GWA_QFMT_INT4, PFV>), grid, block, lds, s, xp, ldx, sm, s2,   \
-                       pd, q, sc, lp, m, k);
+                       pd, q, sc, lp, la_f32_add, m, k);
   switch (rb) {
     case 0: GWA_QUANT_LAUNCH(0, 4) break;
     case 1: GWA_QUANT_LAUNCH(1, 4) break;
@@ -479,6 +367,18 @@ extern "C" int gwa_svdq_quant_int4(const void* x, int64_t ldx, const void* smoot
   }
 #undef GWA_QUANT_LAUNCH
   return gwa_check_launch("svdq_quant_int4");
+}
+
+extern "C" int gwa_svdq_quant_int4(const void* x, int64_t ldx, const void* smooth, const float* s2,
+                                   const void* proj_down_op, int64_t rank, int out_format, uint8_t* q,
+                                   void* scales, void* la, int64_t M, int64_t K, void* stream) {
+  return quant_int4(x, ldx, smooth, s2, proj_down_op, rank, out_format, q, scales, la, 0, M, K, stream);
+}
+
+extern "C" int gwa_svdq_quant_fp6_la_f32(const void* x, int64_t ldx, const void* smooth, const void* proj_down_op,
+                                         int64_t rank, uint8_t* q6, float* la32, int64_t M, int64_t K,
+                                         void* stream) {
+  return quant_int4(x, ldx, smooth, nullptr, proj_down_op, rank, GWA_QFMT_FP6, q6, nullptr, la32, 1, M, K, stream);
 }
 
 extern "C" int gwa_w8a8_quant_int8(const void* x, int64_t ldx, int8_t* q, float* sa, int64_t M, int64_t K,

@@ -19,7 +19,14 @@
 // in the other slot. That leaves one VALU fma per output element and group.
 //
 // Epilogue: acc * s2 * second[n], + la @ up^T (bf16 MFMA), + bias, optional
-// GELU (tanh form), four consecutive n per lane packed to bf16 / f16.
+// GELU (tanh form), four consecutive n per lane packed to bf16 / f16, staged
+// in LDS and stored as full rows. With the next-layer variant (NQ) the staged
+// bf16 tile is also the next layer's input: it is quantized there into the
+// next layer's fp6 operand records (smoothing divide, group-64 scales and
+// codes by the same per-lane quantizer as the act-quant kernel, so the
+// records equal the act-quant kernel's on this output bit for bit), and its
+// product with the next layer's proj_down rows n0 .. n0+TN is added into an
+// fp32 [M, r] buffer with atomics (the tiles of a row band sum in any order).
 //
 // Tiling: a 512-thread workgroup owns a 256 (n) x 256 (m) output tile; its 8
 // waves form a 4 x 2 grid of 64 (n) x 128 (m) wave tiles (2 x 4 blocks), two
@@ -39,6 +46,7 @@
 // the other wave on the SIMD fills the matrix pipe meanwhile. Tiles are
 // ordered per XCD (xcd_tile_of) so operands stay in that XCD's L2.
 #include "gwa_common.h"
+#include "quant_g64.h"
 
 namespace {
 
@@ -144,12 +152,24 @@ __device__ __forceinline__ v8i buf_operand(rsrc_t r, uint32_t off) {
   return (v8i){(int)a[0], (int)a[1], (int)b[0], (int)b[1], (int)c[0], (int)c[1], 0, 0};
 }
 
-template <int TN, int RB, bool GELU, bool OUT_F16>
+// The next layer's side of the NQ epilogue: smoothing factors (bf16 [N] or
+// NULL), proj_down in the act-quant kernel's MFMA operand order (or NULL),
+// its rank / 16, the records [N / 128][M][104] and the fp32 la [M, r].
+struct NextLayer {
+  const uint16_t* smooth;
+  const uint16_t* pdo;
+  int rb;
+  uint8_t* q6;
+  float* la32;
+};
+constexpr int kNextRbMax = 8;  // next-layer ranks up to 128
+
+template <int TN, int RB, bool GELU, bool OUT_F16, bool NQ>
 __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_kernel(
     const uint8_t* __restrict__ qa, const uint8_t* __restrict__ qw, const float* __restrict__ s2p,
     const float* __restrict__ second, int second_per_channel, const uint16_t* __restrict__ la,
     const uint16_t* __restrict__ up, const uint16_t* __restrict__ bias, uint16_t* __restrict__ out, int M, int N,
-    int K) {
+    int K, NextLayer nx) {
   using C = Cfg<TN>;
   constexpr int WBN = C::WBN, WBM = C::WBM, WAVES_N = C::WAVES_N, NBUF = C::NBUF, SLOTS = C::SLOTS;
   constexpr int OFF_W = C::OFF_W;
@@ -458,15 +478,101 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_kernel(
   constexpr int CPR = TN / 8;                 // 16-byte chunks per row
   constexpr int RPP = NTHREADS / CPR;         // rows per pass
   const int crow = tid / CPR, cch = tid % CPR;
-  const rsrc_t obuf = make_rsrc(out, (uint32_t)((int64_t)M * N * 2));
-  const bool col_ok = n0 + 8 * cch < N;
+  if (!NQ || out != nullptr) {
+    const rsrc_t obuf = make_rsrc(out, (uint32_t)((int64_t)M * N * 2));
+    const bool col_ok = n0 + 8 * cch < N;
 #pragma unroll 4
-  for (int r0 = 0; r0 < TM; r0 += RPP) {
-    const int row = r0 + crow;
-    const uint2 lo = *(const uint2*)(ob + row * OSTR + cch * 16);
-    const uint2 hi = *(const uint2*)(ob + row * OSTR + cch * 16 + 8);
-    const uint32_t off = (col_ok && m0 + row < M) ? (uint32_t)(((int64_t)(m0 + row) * N + n0 + 8 * cch) * 2) : kOOB;
-    buf_store16((v4i){(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y}, obuf, off);
+    for (int r0 = 0; r0 < TM; r0 += RPP) {
+      const int row = r0 + crow;
+      const uint2 lo = *(const uint2*)(ob + row * OSTR + cch * 16);
+      const uint2 hi = *(const uint2*)(ob + row * OSTR + cch * 16 + 8);
+      const uint32_t off =
+          (col_ok && m0 + row < M) ? (uint32_t)(((int64_t)(m0 + row) * N + n0 + 8 * cch) * 2) : kOOB;
+      buf_store16((v4i){(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y}, obuf, off);
+    }
+  }
+  if constexpr (NQ) {
+    // ---- the next layer's fp6 records (its K = this N; N % 128 == 0, so every column is real).
+    // Thread -> 8 fixed columns (a group = 8 consecutive lanes), rows crow, crow + RPP, ...
+    const int col = n0 + 8 * cch;
+    float f[8];
+    bool divide = false;
+    if (nx.smooth) {
+      const v4i sv = *(const v4i*)(nx.smooth + col);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        f[2 * j] = bf16_lo((uint32_t)sv[j]);
+        f[2 * j + 1] = bf16_hi((uint32_t)sv[j]);
+      }
+#pragma unroll
+      for (int t = 0; t < 8; ++t) divide |= !g64::smooth_ok(f[t]);
+      if (!divide) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) f[t] = 1.0f / f[t];
+      }
+    }
+    const rsrc_t qb = make_rsrc(nx.q6, (uint32_t)((int64_t)(N >> 7) * M * REC));
+    const int nstage = col >> 7, godd = (col >> 6) & 1;
+#pragma unroll 2
+    for (int r0 = 0; r0 < TM; r0 += RPP) {
+      const int row = r0 + crow;
+      const bool valid = m0 + row < M;
+      const v4i c = *(const v4i*)(ob + row * OSTR + cch * 16);
+      uint32_t w[4];
+      if (nx.smooth) {
+        g64::smooth8(c, f, divide, w);
+      } else {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) w[t] = (uint32_t)c[t];
+      }
+      uint32_t nb[2];
+      uint16_t sh;
+      g64::quant8(w, valid, true, 1.0f, nb, sh);
+      const uint32_t rec = valid ? (uint32_t)(((int64_t)nstage * M + m0 + row) * REC) : 0u;
+      g64::store_fp6(qb, rec, godd, lane, nb, sh, valid);
+    }
+    // ---- la_next[m0 + rows, :] += tile[rows, :] @ proj_down_next[n0 .. n0 + TN, :]: wave w takes rows
+    // 32w .. 32w + 31 (two 16-row MFMA blocks), the A operand read from the staged tile in MFMA order
+    if (nx.pdo != nullptr && nx.rb > 0) {
+      // operand-order rows of the N real columns only (the caller may pass a slice of a longer proj_down)
+      const rsrc_t pb = make_rsrc(nx.pdo, (uint32_t)((int64_t)(N >> 5) * nx.rb * 64 * 16));
+      v4f lacc[2][kNextRbMax];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int rb = 0; rb < kNextRbMax; ++rb) lacc[i][rb] = (v4f){0.f, 0.f, 0.f, 0.f};
+#pragma unroll 2
+      for (int kc = 0; kc < TN / 32; ++kc) {
+        const int kcg = (n0 >> 5) + kc;
+        if (32 * kcg >= N) break;  // the tile's columns past N (N % 128 == 0: whole 32-column chunks)
+        const uint8_t* ar = ob + (32 * wave + (lane & 15)) * OSTR + kc * 64 + (lane >> 4) * 16;
+        const v4i a0 = *(const v4i*)ar;
+        const v4i a1 = *(const v4i*)(ar + 16 * OSTR);
+#pragma unroll
+        for (int rb = 0; rb < kNextRbMax; ++rb) {
+          if (rb < nx.rb) {
+            const v4i b = buf_load16(pb, (uint32_t)((((int64_t)kcg * nx.rb + rb) * 64 + lane) * 16));
+            lacc[0][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, a0),
+                                                                  __builtin_bit_cast(v8bf, b), lacc[0][rb], 0, 0, 0);
+            lacc[1][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, a1),
+                                                                  __builtin_bit_cast(v8bf, b), lacc[1][rb], 0, 0, 0);
+          }
+        }
+      }
+      const int R = nx.rb * 16;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int rb = 0; rb < kNextRbMax; ++rb) {
+          if (rb < nx.rb) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+              const int m = m0 + 32 * wave + 16 * i + 4 * (lane >> 4) + t;
+              if (m < M) unsafeAtomicAdd(nx.la32 + (int64_t)m * R + 16 * rb + (lane & 15), lacc[i][rb][t]);
+            }
+          }
+        }
+    }
   }
 }
 
@@ -565,77 +671,135 @@ extern "C" int gwa_svdq_group_psums_fp6(const uint8_t* qa6, const uint8_t* qw6, 
   return gwa_check_launch("svdq_group_psums_fp6");
 }
 
-extern "C" int gwa_svdq_gemm_w4a4_fp6(const uint8_t* qa6, const uint8_t* qw6, const float* s2, const float* second,
-                                      int64_t second_numel, const void* la, const void* up, int64_t rank,
-                                      const void* bias, void* out, int out_dtype, int epilogue_flags, int64_t M,
-                                      int64_t N, int64_t K, void* stream) {
-  GWA_REQUIRE(M >= 0 && N > 0 && K > 0, "svdq_gemm_w4a4_fp6: bad shape M=%lld N=%lld K=%lld", (long long)M,
-              (long long)N, (long long)K);
-  GWA_REQUIRE(K % 128 == 0, "svdq_gemm_w4a4_fp6: K=%lld is not a multiple of 128", (long long)K);
-  GWA_REQUIRE(N % 16 == 0, "svdq_gemm_w4a4_fp6: N=%lld is not a multiple of 16", (long long)N);
-  GWA_REQUIRE(out_dtype == GWA_DT_BF16 || out_dtype == GWA_DT_F16, "svdq_gemm_w4a4_fp6: out_dtype %d", out_dtype);
-  GWA_REQUIRE((la == nullptr) == (up == nullptr), "svdq_gemm_w4a4_fp6: la and up must both be given or both NULL");
+namespace {
+
+struct Fp6Args {
+  const uint8_t* qa6;
+  const uint8_t* qw6;
+  const float* s2;
+  const float* second;
+  int per_channel;
+  const uint16_t* la;
+  const uint16_t* up;
+  const uint16_t* bias;
+  uint16_t* out;
+  int M, N, K;
+};
+
+template <int TN, int RB, bool GL, bool F16, bool NQ>
+void launch_fp6_tile(dim3 grid, hipStream_t s, const Fp6Args& a, const NextLayer& nx) {
+  hipLaunchKernelGGL((w4a4_gemm_fp6_kernel<TN, RB, GL, F16, NQ>), grid, dim3(NTHREADS), 0, s, a.qa6, a.qw6, a.s2,
+                     a.second, a.per_channel, a.la, a.up, a.bias, a.out, a.M, a.N, a.K, nx);
+}
+
+template <int RB, bool GL, bool F16, bool NQ>
+void launch_fp6_rb(bool wide, dim3 grid, hipStream_t s, const Fp6Args& a, const NextLayer& nx) {
+  if (wide)
+    launch_fp6_tile<256, RB, GL, F16, NQ>(grid, s, a, nx);
+  else
+    launch_fp6_tile<128, RB, GL, F16, NQ>(grid, s, a, nx);
+}
+
+template <int RB>
+void launch_fp6_flags(bool wide, bool gelu, bool f16, bool nq, dim3 grid, hipStream_t s, const Fp6Args& a,
+                      const NextLayer& nx) {
+  if (nq) {  // the next layer's input is bf16: no f16 variant
+    if (gelu) launch_fp6_rb<RB, true, false, true>(wide, grid, s, a, nx);
+    else launch_fp6_rb<RB, false, false, true>(wide, grid, s, a, nx);
+  } else if (gelu) {
+    if (f16) launch_fp6_rb<RB, true, true, false>(wide, grid, s, a, nx);
+    else launch_fp6_rb<RB, true, false, false>(wide, grid, s, a, nx);
+  } else {
+    if (f16) launch_fp6_rb<RB, false, true, false>(wide, grid, s, a, nx);
+    else launch_fp6_rb<RB, false, false, false>(wide, grid, s, a, nx);
+  }
+}
+
+// shared argument checks and launch of both GEMM entry points (nx.q6 != NULL: the NQ epilogue)
+int gemm_fp6(const char* what, const uint8_t* qa6, const uint8_t* qw6, const float* s2, const float* second,
+             int64_t second_numel, const void* la, const void* up, int64_t rank, const void* bias, void* out,
+             int out_dtype, int epilogue_flags, int64_t M, int64_t N, int64_t K, const NextLayer& nx,
+             void* stream) {
+  GWA_REQUIRE(M >= 0 && N > 0 && K > 0, "%s: bad shape M=%lld N=%lld K=%lld", what, (long long)M, (long long)N,
+              (long long)K);
+  GWA_REQUIRE(K % 128 == 0, "%s: K=%lld is not a multiple of 128", what, (long long)K);
+  GWA_REQUIRE(N % 16 == 0, "%s: N=%lld is not a multiple of 16", what, (long long)N);
+  GWA_REQUIRE(out_dtype == GWA_DT_BF16 || out_dtype == GWA_DT_F16, "%s: out_dtype %d", what, out_dtype);
+  GWA_REQUIRE((la == nullptr) == (up == nullptr), "%s: la and up must both be given or both NULL", what);
   const int64_t R = la ? rank : 0;
-  GWA_REQUIRE(R == 0 || R == 16 || R == 32 || R == 64 || R == 128,
-              "svdq_gemm_w4a4_fp6: rank %lld not in {0,16,32,64,128}", (long long)R);
-  GWA_REQUIRE(second == nullptr || second_numel == 1 || second_numel == N,
-              "svdq_gemm_w4a4_fp6: second has %lld values for N=%lld", (long long)second_numel, (long long)N);
-  GWA_REQUIRE((epilogue_flags & ~GWA_EPI_GELU_TANH) == 0, "svdq_gemm_w4a4_fp6: unknown epilogue flags 0x%x",
-              epilogue_flags);
+  GWA_REQUIRE(R == 0 || R == 16 || R == 32 || R == 64 || R == 128, "%s: rank %lld not in {0,16,32,64,128}", what,
+              (long long)R);
+  GWA_REQUIRE(second == nullptr || second_numel == 1 || second_numel == N, "%s: second has %lld values for N=%lld",
+              what, (long long)second_numel, (long long)N);
+  GWA_REQUIRE((epilogue_flags & ~GWA_EPI_GELU_TANH) == 0, "%s: unknown epilogue flags 0x%x", what, epilogue_flags);
   const int64_t nst = K / 128;
   // the DMA offsets of a tile's last run stay below 2^31 + 2^16
   GWA_REQUIRE(nst * (M + TM) * REC < (1ll << 31) && nst * (N + 256) * REC < (1ll << 31) && M * N * 2 < (1ll << 31) &&
-                  M * R * 2 < (1ll << 31),
-              "svdq_gemm_w4a4_fp6: operands must stay below 2 GiB (buffer addressing)");
+                  M * R * 2 < (1ll << 31) && (N / 128) * M * REC < (1ll << 31),
+              "%s: operands must stay below 2 GiB (buffer addressing)", what);
   if (M == 0) return GWA_OK;
-  GWA_REQUIRE(qa6 && qw6 && out, "svdq_gemm_w4a4_fp6: null pointer");
+  const bool nq = nx.q6 != nullptr;
+  GWA_REQUIRE(qa6 && qw6 && (out || nq), "%s: null pointer", what);
   GWA_REQUIRE(GWA_ALIGNED(qa6, 16) && GWA_ALIGNED(qw6, 16) && GWA_ALIGNED(la, 16) && GWA_ALIGNED(up, 16) &&
                   GWA_ALIGNED(out, 8) && GWA_ALIGNED(bias, 2) && GWA_ALIGNED(second, 4) && GWA_ALIGNED(s2, 4),
-              "svdq_gemm_w4a4_fp6: misaligned pointer");
+              "%s: misaligned pointer", what);
   // 256 x 256 tiles halve the operand bytes staged per MAC; 256 x 128 tiles keep the software pipeline
   // and give twice the workgroups. The wider tile is taken when it still fills the chip.
   const int64_t tiles256 = ((M + TM - 1) / TM) * ((N + 255) / 256);
   const bool wide = tiles256 >= 192;
   const int TNv = wide ? 256 : 128;
   const int64_t tiles = ((M + TM - 1) / TM) * ((N + TNv - 1) / TNv);
-  GWA_REQUIRE(tiles < (1ll << 30), "svdq_gemm_w4a4_fp6: too many tiles");
+  GWA_REQUIRE(tiles < (1ll << 30), "%s: too many tiles", what);
+  const int64_t per_xcd = (tiles + kXcds - 1) / kXcds;
+  const dim3 grid((unsigned)(per_xcd * kXcds));
+  const Fp6Args a{qa6, qw6, s2, second, (int)(second_numel > 1), (const uint16_t*)la, (const uint16_t*)up,
+                  (const uint16_t*)bias, (uint16_t*)out, (int)M, (int)N, (int)K};
   const bool gelu = epilogue_flags & GWA_EPI_GELU_TANH;
   const bool f16 = out_dtype == GWA_DT_F16;
   hipStream_t s = (hipStream_t)stream;
-  const int64_t per_xcd = (tiles + kXcds - 1) / kXcds;
-  const dim3 grid((unsigned)(per_xcd * kXcds)), block(NTHREADS);
-  const int pc = second_numel > 1;
-  const uint16_t* lap = (const uint16_t*)la;
-  const uint16_t* upp = (const uint16_t*)up;
-  const uint16_t* bp = (const uint16_t*)bias;
-  uint16_t* op = (uint16_t*)out;
-  const int m = (int)M, n = (int)N, k = (int)K;
-#define GWA_FP6_LAUNCH(RBV, GL, F16V)                                                                          \
-  if (wide)                                                                                                    \
-    hipLaunchKernelGGL((w4a4_gemm_fp6_kernel<256, RBV, GL, F16V>), grid, block, 0, s, qa6, qw6, s2, second, pc, \
-                       lap, upp, bp, op, m, n, k);                                                              \
-  else                                                                                                         \
-    hipLaunchKernelGGL((w4a4_gemm_fp6_kernel<128, RBV, GL, F16V>), grid, block, 0, s, qa6, qw6, s2, second, pc, \
-                       lap, upp, bp, op, m, n, k)
-#define GWA_FP6_RB(RBV)                           \
-  case RBV:                                       \
-    if (gelu) {                                   \
-      if (f16) GWA_FP6_LAUNCH(RBV, true, true);   \
-      else GWA_FP6_LAUNCH(RBV, true, false);      \
-    } else {                                      \
-      if (f16) GWA_FP6_LAUNCH(RBV, false, true);  \
-      else GWA_FP6_LAUNCH(RBV, false, false);     \
-    }                                             \
-    break;
   switch (R / 16) {
-    GWA_FP6_RB(0)
-    GWA_FP6_RB(1)
-    GWA_FP6_RB(2)
-    GWA_FP6_RB(4)
-    GWA_FP6_RB(8)
-    default: return gwa_set_error(GWA_ERR_INVALID, "svdq_gemm_w4a4_fp6: rank %lld", (long long)R);
+    case 0: launch_fp6_flags<0>(wide, gelu, f16, nq, grid, s, a, nx); break;
+    case 1: launch_fp6_flags<1>(wide, gelu, f16, nq, grid, s, a, nx); break;
+    case 2: launch_fp6_flags<2>(wide, gelu, f16, nq, grid, s, a, nx); break;
+    case 4: launch_fp6_flags<4>(wide, gelu, f16, nq, grid, s, a, nx); break;
+    case 8: launch_fp6_flags<8>(wide, gelu, f16, nq, grid, s, a, nx); break;
+    default: return gwa_set_error(GWA_ERR_INVALID, "%s: rank %lld", what, (long long)R);
   }
-#undef GWA_FP6_RB
-#undef GWA_FP6_LAUNCH
-  return gwa_check_launch("svdq_gemm_w4a4_fp6");
+  return gwa_check_launch(what);
+}
+
+}  // namespace
+
+extern "C" int gwa_svdq_gemm_w4a4_fp6(const uint8_t* qa6, const uint8_t* qw6, const float* s2, const float* second,
+                                      int64_t second_numel, const void* la, const void* up, int64_t rank,
+                                      const void* bias, void* out, int out_dtype, int epilogue_flags, int64_t M,
+                                      int64_t N, int64_t K, void* stream) {
+  const NextLayer none{nullptr, nullptr, 0, nullptr, nullptr};
+  return gemm_fp6("svdq_gemm_w4a4_fp6", qa6, qw6, s2, second, second_numel, la, up, rank, bias, out, out_dtype,
+                  epilogue_flags, M, N, K, none, stream);
+}
+
+extern "C" int gwa_svdq_gemm_w4a4_fp6_next(const uint8_t* qa6, const uint8_t* qw6, const float* s2,
+                                           const float* second, int64_t second_numel, const void* la, const void* up,
+                                           int64_t rank, const void* bias, void* out, int epilogue_flags,
+                                           const void* next_smooth, const void* next_proj_down_op, int64_t next_rank,
+                                           uint8_t* next_q6, float* next_la32, int64_t M, int64_t N, int64_t K,
+                                           void* stream) {
+  const char* what = "svdq_gemm_w4a4_fp6_next";
+  GWA_REQUIRE(N > 0 && N % 128 == 0, "%s: N=%lld is not a multiple of 128 (the next layer's fp6 stages)", what,
+              (long long)N);
+  GWA_REQUIRE(next_q6 != nullptr, "%s: next_q6 is NULL", what);
+  GWA_REQUIRE((next_proj_down_op == nullptr) == (next_la32 == nullptr),
+              "%s: next_proj_down_op and next_la32 must both be given or both NULL", what);
+  const int64_t NR = next_proj_down_op ? next_rank : 0;
+  GWA_REQUIRE(NR == 0 || NR == 16 || NR == 32 || NR == 64 || NR == 128, "%s: next rank %lld not in {0,16,32,64,128}",
+              what, (long long)NR);
+  GWA_REQUIRE(M * NR * 4 < (1ll << 40), "%s: shape too large", what);
+  GWA_REQUIRE(GWA_ALIGNED(next_smooth, 16) && GWA_ALIGNED(next_proj_down_op, 16) && GWA_ALIGNED(next_q6, 8) &&
+                  GWA_ALIGNED(next_la32, 4),
+              "%s: next_smooth and next_proj_down_op must be 16-byte, next_q6 8-byte aligned", what);
+  const NextLayer nx{(const uint16_t*)next_smooth, (const uint16_t*)next_proj_down_op, (int)(NR / 16), next_q6,
+                     next_la32};
+  return gemm_fp6(what, qa6, qw6, s2, second, second_numel, la, up, rank, bias, out, GWA_DT_BF16, epilogue_flags, M,
+                  N, K, nx, stream);
 }

@@ -52,6 +52,9 @@ _SIGNATURES: dict[str, tuple] = {
     "gwa_svdq_gemm_w4a4_fp6": (_vp, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _int, _int,
                                _i64, _i64, _i64, _vp),
     "gwa_svdq_group_psums_fp6": (_vp, _vp, _vp, _i64, _i64, _i64, _vp),
+    "gwa_svdq_gemm_w4a4_fp6_next": (_vp, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _int,
+                                    _vp, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _vp),
+    "gwa_svdq_quant_fp6_la_f32": (_vp, _i64, _vp, _vp, _i64, _vp, _vp, _i64, _i64, _vp),
     "gwa_svdq_epilogue_lora": (_vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _i64, _i64, _vp),
     "gwa_w8a8_quant_int8": (_vp, _i64, _vp, _vp, _i64, _i64, _vp),
     "gwa_w8a8_gemm": (_vp, _vp, _vp, _vp, _vp, _int, _vp, _int, _i64, _i64, _i64, _vp),

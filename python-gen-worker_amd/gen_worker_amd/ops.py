@@ -27,6 +27,10 @@ separate steps):
 * ``svdq_pack_weight_fp6(weight, wscales)``, ``svdq_w4a4_linear_fp6(qa6,
   weight_fp6, s2, second, la, up, bias, out_dtype, gelu)``,
   ``svdq_group_psums_fp6(qa6, weight_fp6)``: the fp6 GEMM lane.
+* ``svdq_w4a4_linear_fp6_next(...)`` and ``svdq_quant_fp6_accum(...)``: the
+  next layer's activation quantization fused into the GEMM epilogue (fp6
+  records + fp32 la accumulated), for fc1 -> GELU -> fc2 and for a layer
+  whose input concatenates two producers.
 * ``svdq_w4a4_linear(qa, sa, weight, wscales, s2, second, la, up, bias,
   out_dtype, gelu)``: kernel 2 on the resident ``weight`` [N, K/2] layout.
 * ``svdq_group_psums(qa, qw)``: exact int32 per-group partial sums (debug).
@@ -327,6 +331,115 @@ def svdq_w4a4_linear_fp6(qa6: Tensor, weight_fp6: Tensor, s2: Optional[Tensor], 
 @svdq_w4a4_linear_fp6.register_fake
 def _(qa6, weight_fp6, s2, second, la, up, bias, out_dtype, gelu):
     return qa6.new_empty(int(qa6.shape[1]), int(weight_fp6.shape[1]), dtype=out_dtype)
+
+
+def _next_records(name: str, q6: Tensor, m: int, k: int, stage_offset: int) -> int:
+    """Checks a record buffer [S, m, 104] that receives stages [stage_offset, stage_offset + k/128); returns the
+    byte address of the first of them."""
+    _check_dtype(name, q6, torch.uint8, what="records")
+    rows, ktot = _fp6_records_k(name, q6, "records")
+    if rows != m:
+        raise SvdqOpError(f"{name}: records hold {rows} rows, the activations {m}")
+    if stage_offset < 0 or stage_offset * FP6_STAGE + k > ktot:
+        raise SvdqOpError(f"{name}: stages [{stage_offset}, {stage_offset + k // FP6_STAGE}) do not fit records "
+                          f"of {ktot // FP6_STAGE} stages")
+    return q6.data_ptr() + stage_offset * m * nat.FP6_REC
+
+
+def _next_lowrank(name: str, proj_down_op: Optional[Tensor], la32: Optional[Tensor], m: int, k: int) -> int:
+    """Checks the next layer's (proj_down_op rows for these k columns, fp32 la accumulator); returns the rank."""
+    if (proj_down_op is None) != (la32 is None):
+        raise SvdqOpError(f"{name}: proj_down_op and la32 must both be given or both be None")
+    if proj_down_op is None:
+        return 0
+    _check_dtype(name, proj_down_op, torch.bfloat16, what="proj_down_op")
+    _check_dtype(name, la32, torch.float32, what="la32")
+    r = int(la32.shape[1]) if la32.dim() == 2 else -1
+    if la32.dim() != 2 or int(la32.shape[0]) != m:
+        raise SvdqOpError(f"{name}: la32 must be [{m}, rank], got {tuple(la32.shape)}")
+    if proj_down_op.dim() != 2 or int(proj_down_op.shape[1]) != r or int(proj_down_op.shape[0]) < k:
+        raise SvdqOpError(f"{name}: proj_down_op must be [>= {k}, {r}] rows in operand order, got "
+                          f"{tuple(proj_down_op.shape)}")
+    return r
+
+
+@torch.library.custom_op("cozy_gen_worker::svdq_w4a4_linear_fp6_next", mutates_args=("next_q6", "next_la32"))
+def svdq_w4a4_linear_fp6_next(qa6: Tensor, weight_fp6: Tensor, s2: Optional[Tensor], second: Optional[Tensor],
+                              la: Optional[Tensor], up: Optional[Tensor], bias: Optional[Tensor], gelu: bool,
+                              next_smooth: Optional[Tensor], next_proj_down_op: Optional[Tensor], next_q6: Tensor,
+                              next_la32: Optional[Tensor], stage_offset: int, write_out: bool) -> Tensor:
+    """W4A4 GEMM whose epilogue also quantizes its bf16 output as the NEXT layer's input: writes that layer's
+    fp6 records into stages ``stage_offset ..`` of ``next_q6`` [S, M, 104] (bit-identical to ``svdq_quant_fp6``
+    on the output with ``next_smooth``) and adds ``output @ proj_down_next`` into ``next_la32`` fp32 [M, r]
+    (atomic adds over column tiles). ``next_proj_down_op`` holds the next layer's proj_down rows for these N
+    columns in operand order (a prefix-aligned slice of its ``proj_down_op``). Returns the bf16 output
+    [M, N] when ``write_out``, else an empty [M, 0]."""
+    name = "svdq_w4a4_linear_fp6_next"
+    s2 = _scalar_f32(name, s2)
+    if second is not None and second.dtype != torch.float32:
+        second = second.float().contiguous()
+    _check_dtype(name, qa6, torch.uint8, what="qa6")
+    _check_dtype(name, weight_fp6, torch.uint8, what="weight_fp6")
+    _check_dtype(name, la, torch.bfloat16, what="la")
+    _check_dtype(name, up, torch.bfloat16, what="up")
+    _check_dtype(name, bias, torch.bfloat16, what="bias")
+    _check_dtype(name, next_smooth, torch.bfloat16, what="next_smooth")
+    _check_cuda(name, qa6=qa6, weight_fp6=weight_fp6, s2=s2, second=second, la=la, up=up, bias=bias,
+                next_smooth=next_smooth, next_proj_down_op=next_proj_down_op, next_q6=next_q6, next_la32=next_la32)
+    m, k = _fp6_records_k(name, qa6, "qa6")
+    n, kw = _fp6_records_k(name, weight_fp6, "weight_fp6")
+    if kw != k:
+        raise SvdqOpError(f"{name}: activation K={k} and weight K={kw} differ")
+    if n % FP6_STAGE:
+        raise SvdqOpError(f"{name}: N={n} is not a multiple of {FP6_STAGE} (whole stages of the next layer)")
+    if next_smooth is not None and next_smooth.numel() != n:
+        raise SvdqOpError(f"{name}: next_smooth has {next_smooth.numel()} values for N={n}")
+    rank, sec_n = _epilogue_operands(name, m, n, la, up, bias, second)
+    q6_addr = _next_records(name, next_q6, m, n, stage_offset)
+    nrank = _next_lowrank(name, next_proj_down_op, next_la32, m, n)
+    out = torch.empty(m, n if write_out else 0, dtype=torch.bfloat16, device=qa6.device)
+    nat.call("gwa_svdq_gemm_w4a4_fp6_next", nat.ptr(qa6), nat.ptr(weight_fp6), nat.ptr(s2), nat.ptr(second),
+             sec_n, nat.ptr(la), nat.ptr(up), rank, nat.ptr(bias), nat.ptr(out) if write_out else None,
+             nat.EPI_GELU_TANH if gelu else 0, nat.ptr(next_smooth), nat.ptr(next_proj_down_op), nrank, q6_addr,
+             nat.ptr(next_la32), m, n, k, nat.stream_of(qa6))
+    return out
+
+
+@svdq_w4a4_linear_fp6_next.register_fake
+def _(qa6, weight_fp6, s2, second, la, up, bias, gelu, next_smooth, next_proj_down_op, next_q6, next_la32,
+      stage_offset, write_out):
+    return qa6.new_empty(int(qa6.shape[1]), int(weight_fp6.shape[1]) if write_out else 0, dtype=torch.bfloat16)
+
+
+@torch.library.custom_op("cozy_gen_worker::svdq_quant_fp6_accum", mutates_args=("q6", "la32"))
+def svdq_quant_fp6_accum(x2: Tensor, smooth: Optional[Tensor], proj_down_op: Optional[Tensor], q6: Tensor,
+                         la32: Optional[Tensor]) -> None:
+    """Kernel 1 into stages [0, K/128) of the record buffer ``q6`` [S, M, 104] with ``la32`` fp32 [M, r]
+    += x2 @ proj_down (``proj_down_op``: the consumer's operand-order proj_down rows for these K columns).
+    With ``svdq_w4a4_linear_fp6_next`` writing the later stages it builds the input of a layer that takes
+    a concatenation [x2, producer output]."""
+    name = "svdq_quant_fp6_accum"
+    if x2.dim() != 2:
+        raise SvdqOpError(f"{name}: x2 must be 2-D, got {tuple(x2.shape)}")
+    _check_dtype(name, x2, torch.bfloat16, what="x2")
+    _check_dtype(name, smooth, torch.bfloat16, what="smooth")
+    _check_cuda(name, x2=x2, smooth=smooth, proj_down_op=proj_down_op, q6=q6, la32=la32)
+    m, k = int(x2.shape[0]), int(x2.shape[1])
+    if k % FP6_STAGE:
+        raise SvdqOpError(f"{name}: the fp6 records need K % {FP6_STAGE} == 0, got K={k}")
+    if smooth is not None and smooth.numel() != k:
+        raise SvdqOpError(f"{name}: smooth has {smooth.numel()} values for K={k}")
+    q6_addr = _next_records(name, q6, m, k, 0)
+    rank = _next_lowrank(name, proj_down_op, la32, m, k)
+    if proj_down_op is not None and int(proj_down_op.shape[0]) < (k + 255) // 256 * 256:
+        raise SvdqOpError(f"{name}: proj_down_op needs {(k + 255) // 256 * 256} rows for K={k}")
+    nat.call("gwa_svdq_quant_fp6_la_f32", nat.ptr(x2), int(x2.stride(0)), nat.ptr(smooth), nat.ptr(proj_down_op),
+             rank, q6_addr, nat.ptr(la32), m, k, nat.stream_of(x2))
+
+
+@svdq_quant_fp6_accum.register_fake
+def _(x2, smooth, proj_down_op, q6, la32):
+    return None
 
 
 @torch.library.custom_op("cozy_gen_worker::svdq_pack_weight_fp6", mutates_args=())

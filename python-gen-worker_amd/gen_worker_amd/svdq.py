@@ -30,7 +30,7 @@ import torch
 import torch.nn as nn
 from torch import Tensor
 
-from . import ops
+from . import _native, ops
 
 GROUP = 64
 _N_ALIGN = 16
@@ -193,16 +193,32 @@ class SvdqW4A4Linear(nn.Module):
         int8-MFMA GEMM on the logical weights)."""
         return "fp6" if self.weight_fp6 is not None else "general"
 
-    def forward(self, x: Tensor) -> Tensor:
-        shape = x.shape
-        x2 = x.reshape(-1, self.in_features)
-        if x2.dtype != torch.bfloat16:
-            raise SvdqFusedError(f"SvdqW4A4Linear expects bf16 activations, got {x2.dtype}")
-        x2 = x2.contiguous()
-        out_dtype = self.out_dtype or torch.bfloat16
+    def _ensure_derived(self) -> None:
         if (self.rank and self.proj_down_op is None) or (self.weight_fp6 is None and self.weight.is_cuda
                                                          and self.in_features % ops.FP6_STAGE == 0):
             self.refresh_derived()
+
+    def _input2d(self, x: Tensor) -> Tensor:
+        x2 = x.reshape(-1, self.in_features)
+        if x2.dtype != torch.bfloat16:
+            raise SvdqFusedError(f"SvdqW4A4Linear expects bf16 activations, got {x2.dtype}")
+        return x2.contiguous()
+
+    def forward_records(self, q6: Tensor, la: Optional[Tensor], out_dtype: Optional[torch.dtype] = None) -> Tensor:
+        """The fp6-lane GEMM on ready input records [K/128, M, 104] and la bf16 [M, rank] (e.g. written by the
+        previous layer's fused epilogue); returns [M, out_features]."""
+        self._ensure_derived()
+        if self.weight_fp6 is None:
+            raise SvdqFusedError("forward_records needs the fp6 lane (in_features % 128 == 0, weights on the GPU)")
+        return torch.ops.cozy_gen_worker.svdq_w4a4_linear_fp6(
+            q6, self.weight_fp6, None, self.second, la if self.rank else None, self.proj_up, self.bias,
+            out_dtype or self.out_dtype or torch.bfloat16, self.activation == "gelu_tanh")
+
+    def forward(self, x: Tensor) -> Tensor:
+        shape = x.shape
+        x2 = self._input2d(x)
+        out_dtype = self.out_dtype or torch.bfloat16
+        self._ensure_derived()
         gelu = self.activation == "gelu_tanh"
         if self.weight_fp6 is not None:
             qa6, la = torch.ops.cozy_gen_worker.svdq_quant_fp6(x2, self.smooth_factor, None, self.proj_down_op)
@@ -224,6 +240,75 @@ class SvdqW4A4Linear(nn.Module):
         return (f"in_features={self.in_features}, out_features={self.out_features}, rank={self.rank}, "
                 f"bias={self.bias is not None}, per_channel_scale={self.per_channel_scale}, "
                 f"smooth={self.smooth_factor is not None}, activation={self.activation}, lane=int4-g64")
+
+
+def _fusable(producer: SvdqW4A4Linear, consumer: SvdqW4A4Linear, k_offset: int) -> bool:
+    producer._ensure_derived()
+    consumer._ensure_derived()
+    return (producer.lane == "fp6" and consumer.lane == "fp6" and producer.out_features % ops.FP6_STAGE == 0
+            and producer.out_dtype in (None, torch.bfloat16) and k_offset % ops.FP6_STAGE == 0
+            and k_offset + producer.out_features == consumer.in_features)
+
+
+def _next_operands(consumer: SvdqW4A4Linear, k0: int, k1: int) -> tuple[Optional[Tensor], Optional[Tensor]]:
+    """The consumer's smoothing factors and operand-order proj_down rows for its input columns [k0, k1)."""
+    sm = consumer.smooth_factor[k0:k1] if consumer.smooth_factor is not None else None
+    pdo = consumer.proj_down_op[k0:] if consumer.rank else None
+    return sm, pdo
+
+
+def svdq_pair_forward(x: Tensor, first: SvdqW4A4Linear, second: SvdqW4A4Linear) -> Tensor:
+    """``second(first(x))`` with ``second``'s activation quantization fused into ``first``'s GEMM epilogue
+    (config 2: fc1 -> GELU -> fc2). The [M, first.out_features] bf16 intermediate never reaches HBM: the
+    epilogue writes ``second``'s fp6 records (bit-identical to quantizing the bf16 output) and adds
+    ``output @ second.proj_down`` into an fp32 buffer, rounded to bf16 for ``second``'s la. Layers that do not
+    meet the fused contract (both fp6 lane, first.out_features % 128 == 0, bf16 intermediate) run unfused."""
+    if not _fusable(first, second, 0):
+        return second(first(x))
+    shape = x.shape
+    x2 = first._input2d(x)
+    m = int(x2.shape[0])
+    q6, la = torch.ops.cozy_gen_worker.svdq_quant_fp6(x2, first.smooth_factor, None, first.proj_down_op)
+    q6n = torch.empty(second.in_features // ops.FP6_STAGE, m, _native.FP6_REC, dtype=torch.uint8, device=x2.device)
+    la32 = torch.zeros(m, second.rank, dtype=torch.float32, device=x2.device) if second.rank else None
+    sm, pdo = _next_operands(second, 0, second.in_features)
+    torch.ops.cozy_gen_worker.svdq_w4a4_linear_fp6_next(
+        q6, first.weight_fp6, None, first.second, la if first.rank else None, first.proj_up, first.bias,
+        first.activation == "gelu_tanh", sm, pdo, q6n, la32, 0, False)
+    y = second.forward_records(q6n, la32.to(torch.bfloat16) if la32 is not None else None)
+    return y.reshape(*shape[:-1], second.out_features)
+
+
+def svdq_concat_forward(consumer: SvdqW4A4Linear, x_a: Tensor, producer: SvdqW4A4Linear, x_b: Tensor) -> Tensor:
+    """``consumer(cat([x_a, producer(x_b)], -1))`` (Flux's single-block proj_out over [attention, MLP]) without
+    the concatenation: kernel 1 writes the first x_a.shape[-1] / 128 stages of ``consumer``'s input records
+    from ``x_a``, ``producer``'s fused epilogue writes the rest, and both add their part of the input @
+    proj_down into one fp32 buffer. Falls back to the unfused composition outside the fused contract
+    (x_a's width a multiple of 128, both fp6 lane)."""
+    ka = int(x_a.shape[-1])
+    if not _fusable(producer, consumer, ka):
+        return consumer(torch.cat((x_a, producer(x_b)), dim=-1))
+    shape = x_a.shape
+    xa2 = x_a.reshape(-1, ka)
+    if xa2.dtype != torch.bfloat16:
+        raise SvdqFusedError(f"svdq_concat_forward expects bf16 activations, got {xa2.dtype}")
+    xa2 = xa2.contiguous()
+    xb2 = producer._input2d(x_b)
+    m = int(xa2.shape[0])
+    if int(xb2.shape[0]) != m:
+        raise SvdqFusedError(f"svdq_concat_forward: {m} rows in x_a, {int(xb2.shape[0])} in x_b")
+    q6n = torch.empty(consumer.in_features // ops.FP6_STAGE, m, _native.FP6_REC, dtype=torch.uint8,
+                      device=xa2.device)
+    la32 = torch.zeros(m, consumer.rank, dtype=torch.float32, device=xa2.device) if consumer.rank else None
+    sm_a, pdo_a = _next_operands(consumer, 0, ka)
+    torch.ops.cozy_gen_worker.svdq_quant_fp6_accum(xa2, sm_a, pdo_a, q6n, la32)
+    q6, la = torch.ops.cozy_gen_worker.svdq_quant_fp6(xb2, producer.smooth_factor, None, producer.proj_down_op)
+    sm_b, pdo_b = _next_operands(consumer, ka, consumer.in_features)
+    torch.ops.cozy_gen_worker.svdq_w4a4_linear_fp6_next(
+        q6, producer.weight_fp6, None, producer.second, la if producer.rank else None, producer.proj_up,
+        producer.bias, producer.activation == "gelu_tanh", sm_b, pdo_b, q6n, la32, ka // ops.FP6_STAGE, False)
+    y = consumer.forward_records(q6n, la32.to(torch.bfloat16) if la32 is not None else None)
+    return y.reshape(*shape[:-1], consumer.out_features)
 
 
 def build_svdq_w4a4_linear(*, qweight: Tensor, wscales: Tensor, smooth: Optional[Tensor],
@@ -299,5 +384,6 @@ def act_quant_bytes(m: int, k: int, rank: int, smooth: bool = True, fp6: bool = 
 __all__ = [
     "SvdqFusedError", "SvdqW4A4Linear", "build_svdq_w4a4_linear", "dequantize_weight_int4",
     "fold_to_dense", "fused_shape_supported", "pack_int4", "quantize_linear_w4a4", "quantize_weight_int4",
-    "svdquant_decompose", "unpack_int4", "w4a4_int_ops", "act_quant_bytes",
+    "svdquant_decompose", "unpack_int4", "w4a4_int_ops", "act_quant_bytes", "svdq_pair_forward",
+    "svdq_concat_forward",
 ]

@@ -55,6 +55,15 @@ def test_invalid_arguments_are_refused_before_any_launch():
     assert rc == 1 and "128" in lib.gwa_last_error().decode()
     rc = lib.gwa_svdq_gemm_w4a4_fp6(None, None, None, None, 0, None, None, 0, None, None, 0, 0, 8, 64, 192, None)
     assert rc == 1 and "multiple of 128" in lib.gwa_last_error().decode()
+    # the next-layer epilogue needs whole 128-column stages and a record buffer
+    rc = lib.gwa_svdq_gemm_w4a4_fp6_next(None, None, None, None, 0, None, None, 0, None, None, 0, None, None, 0,
+                                         None, None, 8, 192, 128, None)
+    assert rc == 1 and "multiple of 128" in lib.gwa_last_error().decode()
+    rc = lib.gwa_svdq_gemm_w4a4_fp6_next(None, None, None, None, 0, None, None, 0, None, None, 0, None, None, 0,
+                                         None, None, 8, 256, 128, None)
+    assert rc == 1 and "next_q6" in lib.gwa_last_error().decode()
+    rc = lib.gwa_svdq_quant_fp6_la_f32(None, 192, None, None, 0, None, None, 4, 192, None)
+    assert rc == 1 and "128" in lib.gwa_last_error().decode()
     rc = lib.gwa_svdq_prep_proj_down(None, None, 64, 24, None)
     assert rc == 1 and "rank" in lib.gwa_last_error().decode()
     rc = lib.gwa_svdq_gemm_w4a4(None, None, None, None, None, None, 0, None, None, 0, None, None, 0, 0,
@@ -107,6 +116,14 @@ def test_fake_impls_trace_shapes():
                                                             False)
         assert y6.shape == (77, 128) and y6.dtype == torch.bfloat16
         assert torch.ops.cozy_gen_worker.svdq_group_psums_fp6(q6, w6).shape == (77, 128, 6)
+        nq = torch.empty(4, 77, 104, dtype=torch.uint8)
+        yn = torch.ops.cozy_gen_worker.svdq_w4a4_linear_fp6_next(q6, w6, None, None, None, None, None, True, None,
+                                                                 None, nq, None, 3, True)
+        assert yn.shape == (77, 128) and yn.dtype == torch.bfloat16
+        yn0 = torch.ops.cozy_gen_worker.svdq_w4a4_linear_fp6_next(q6, w6, None, None, None, None, None, False,
+                                                                  None, None, nq, None, 0, False)
+        assert yn0.shape == (77, 0)
+        assert torch.ops.cozy_gen_worker.svdq_quant_fp6_accum(x, None, None, nq, None) is None
         assert q.shape == (77, 192) and s.shape == (77, 6) and la.shape == (77, 32)
         w = torch.empty(128, 192, dtype=torch.uint8)
         ws = torch.empty(128, 6, dtype=torch.float16)
