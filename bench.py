@@ -171,6 +171,116 @@ def bench_dit(args) -> int:
     return 0
 
 
+def _w4a4_module(torch, L, dev, activation=None, out_dtype=None):
+    from gen_worker_amd.svdq import build_svdq_w4a4_linear
+
+    return build_svdq_w4a4_linear(qweight=L.qweight, wscales=L.wscales, smooth=L.smooth, proj_down=L.proj_down,
+                                  proj_up=L.proj_up, bias=L.bias, activation=activation, out_dtype=out_dtype,
+                                  device=dev)
+
+
+def bench_mlp(args) -> int:
+    """Config 2: M=4608, fc1 3072 -> 12288 with GELU-tanh, fc2 12288 -> 3072, rank 32. Three variants of the
+    same pair, each timed over ``--steps`` calls in one HIP graph: ``fused`` (fc2's act-quant in fc1's GEMM
+    epilogue, svdq_pair_forward), ``unfused`` (the two W4A4 modules back to back: fc1's bf16 output written
+    and re-quantized), ``bf16`` (two bf16 linears with torch's GELU between them)."""
+    import torch
+
+    import gen_worker_amd  # noqa: F401
+    from gen_worker_amd import _native, synthetic
+    from gen_worker_amd.svdq import svdq_pair_forward, w4a4_int_ops
+
+    _native.load()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    c = synthetic.C2
+    m, d, h, r = c["m"], c["d"], c["h"], c["rank"]
+    log(f"bench: config-2 MLP pair M={m} {d} -> {h} -> {d} r={r}")
+    L1, L2 = synthetic.w4a4_layer(h, d, r, seed_offset=0), synthetic.w4a4_layer(d, h, r, seed_offset=100)
+    fc1, fc2 = _w4a4_module(torch, L1, dev, "gelu_tanh"), _w4a4_module(torch, L2, dev)
+    x = synthetic.activation(m, d, outlier_frac=c["outlier_frac"], outlier_scale=c["outlier_scale"]).to(dev)
+    w1, w2 = L1.w_res.to(dev, torch.bfloat16), L2.w_res.to(dev, torch.bfloat16)
+    b1, b2 = L1.bias.to(dev), L2.bias.to(dev)
+    F = torch.nn.functional
+    variants = {
+        "fused": lambda: svdq_pair_forward(x, fc1, fc2),
+        "unfused": lambda: fc2(fc1(x)),
+        "bf16": lambda: F.linear(F.gelu(F.linear(x, w1, b1), approximate="tanh"), w2, b2),
+    }
+    ops_ = 2 * w4a4_int_ops(m, h, d)
+    res = {}
+    for name, fn in variants.items():
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        ms = graph_time_ms(torch, fn, args.steps)
+        res[name] = {"ms": round(ms, 5), "TOPS": round(ops_ / (ms * 1e-3) / 1e12, 1)}
+        log(f"bench: {name}: {ms * 1e3:.1f} us  {res[name]['TOPS']} TOPS")
+    out = {"metric": "MLP pair TOPS (config 2: fc1 + GELU + fc2, 2*2*M*D*H int ops)",
+           "value": res["fused"]["TOPS"], "unit": "TOPS", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "ms_per_step": res["fused"]["ms"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+           "dtype": "int4", "data": "synthetic",
+           "config": {"workload": "svdq_mlp_pair_c2", "M": m, "D": d, "H": h, "rank": r, "group": 64,
+                      "timing": "K calls in one HIP graph replay"},
+           "pct_int8_peak": round(100 * res["fused"]["TOPS"] / INT8_PEAK_TOPS, 2), "variants": res,
+           "speedup_fused_vs_unfused": round(res["unfused"]["ms"] / res["fused"]["ms"], 4),
+           "speedup_fused_vs_bf16": round(res["bf16"]["ms"] / res["fused"]["ms"], 4)}
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def bench_qkv(args) -> int:
+    """Config 3: the QKV projection K=3072 -> N=9216 over M in {256, 1024, 4608, 16384} with bf16 and fp16
+    outputs: the W4A4 module (act-quant + GEMM, rank 32), the W8A8 module (int8 act-quant + int8 GEMM) and a
+    bf16 linear, each timed over ``--steps`` calls in one HIP graph."""
+    import torch
+
+    import gen_worker_amd  # noqa: F401
+    from gen_worker_amd import _native, synthetic
+    from gen_worker_amd.svdq import w4a4_int_ops
+    from gen_worker_amd.w8a8 import build_int8_linear
+
+    _native.load()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    c = synthetic.C3
+    k, n, r = c["k"], c["n"], c["rank"]
+    L = synthetic.w4a4_layer(n, k, r)
+    L8 = synthetic.w8a8_layer(n, k)
+    wb = L.w_res.to(dev, torch.bfloat16)
+    rows = []
+    for odt in (torch.bfloat16, torch.float16):
+        w4 = _w4a4_module(torch, L, dev, out_dtype=odt)
+        w8 = build_int8_linear(qweight=L8.qweight, weight_scale=L8.weight_scale, bias=L8.bias, compute_dtype=odt,
+                               device=dev)
+        wd, bd = wb.to(odt), L.bias.to(dev, odt)
+        for m in c["ms"]:
+            x = synthetic.activation(m, k, outlier_frac=c["outlier_frac"], outlier_scale=c["outlier_scale"]).to(dev)
+            xd = x.to(odt)
+            fns = {"w4a4": lambda: w4(x), "w8a8": lambda: w8(x),
+                   "bf16" if odt == torch.bfloat16 else "fp16": lambda: torch.nn.functional.linear(xd, wd, bd)}
+            row = {"M": m, "out_dtype": str(odt).replace("torch.", "")}
+            ops_ = w4a4_int_ops(m, n, k)
+            for name, fn in fns.items():
+                for _ in range(args.warmup):
+                    fn()
+                torch.cuda.synchronize()
+                ms = graph_time_ms(torch, fn, args.steps)
+                row[name] = {"us": round(ms * 1e3, 2), "TOPS": round(ops_ / (ms * 1e-3) / 1e12, 1)}
+            log(f"bench: qkv {row}")
+            rows.append(row)
+    big = next(rw for rw in rows if rw["M"] == 4608 and rw["out_dtype"] == "bfloat16")
+    out = {"metric": "QKV projection TOPS (config 3: K=3072 -> N=9216; act-quant + GEMM per call)",
+           "value": big["w4a4"]["TOPS"], "unit": "TOPS", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "ms_per_step": round(big["w4a4"]["us"] / 1e3, 5), "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "dtype": "int4", "data": "synthetic",
+           "config": {"workload": "qkv_sweep_c3", "K": k, "N": n, "rank": r, "M": list(c["ms"]),
+                      "value_at": "M=4608, bf16 out, W4A4", "timing": "K calls in one HIP graph replay"},
+           "rows": rows}
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -180,20 +290,22 @@ def main() -> int:
     ap.add_argument("--cpu-rows", type=int, default=512, help="rows of the bounded CPU sample")
     ap.add_argument("--only", choices=("step", "gemm", "quant", "copy"), default=None)
     ap.add_argument("--iters", type=int, default=5)
-    ap.add_argument("--workload", choices=("c1", "dit"), default="c1",
-                    help="c1: the config-1 linear (the default bench line); dit: the config-4 Flux-shaped DiT "
-                         "step, W4A4 vs the same model with bf16 GEMMs")
+    ap.add_argument("--workload", choices=("c1", "mlp", "qkv", "dit"), default="c1",
+                    help="c1: the config-1 linear (the default bench line); mlp: config 2, fc1 -> GELU -> fc2 "
+                         "(fused, unfused, bf16); qkv: config 3, the QKV sweep over M and output dtype (W4A4, "
+                         "W8A8, bf16); dit: the config-4 Flux-shaped DiT step, W4A4 vs the same model with bf16 "
+                         "GEMMs")
     ap.add_argument("--summarize-traffic", metavar="DIR", default=None,
                     help="write profiles/w4a4_gemm_c1_traffic.json from the FETCH_SIZE / WRITE_SIZE runs in DIR "
                          "(subdirectories f_<w>, w_<w> for w in gemm, quant, copy)")
     args = ap.parse_args()
     if args.summarize_traffic:
         return summarize_traffic(Path(args.summarize_traffic))
-    if args.workload == "dit":
+    if args.workload != "c1":
         if args.gpus != 1:
             print("bench.py measures one GPU only", file=sys.stderr)
             return 2
-        return bench_dit(args)
+        return {"dit": bench_dit, "mlp": bench_mlp, "qkv": bench_qkv}[args.workload](args)
 
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}): this build's path is a single-GPU "

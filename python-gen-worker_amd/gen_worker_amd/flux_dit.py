@@ -12,7 +12,10 @@ conditioning enters as a seeded random embedding ``temb`` [1, 3072].
 Every linear is built by a factory, so the same model runs as:
   * ``"w4a4"``: every linear an SVDQuant W4A4 layer (``SvdqW4A4Linear``, rank
     32, group 64; int4 codes, fp16 scales, low-rank factors and bias random),
-    GELU fused into the fc1 epilogues;
+    GELU fused into the fc1 epilogues, and each MLP's second linear quantized
+    in the first one's epilogue (``svdq_pair_forward``; in the single blocks
+    ``svdq_concat_forward`` builds proj_out's input [attention, MLP] without
+    the concatenation);
   * ``"bf16"``: every linear a bf16 ``nn.Linear`` (the bf16 GEMM path).
 Attention is bf16 ``scaled_dot_product_attention`` in both. Weights are
 random-init on the device from seeded generators; values are chosen only to
@@ -119,11 +122,19 @@ def _attention(q: Tensor, k: Tensor, v: Tensor) -> Tensor:
     return o.squeeze(0).transpose(0, 1).reshape(s, h * d)
 
 
+def _mlp(fc1: nn.Module, fc2: nn.Module, x: Tensor, fused: bool) -> Tensor:
+    if fused:
+        from .svdq import svdq_pair_forward
+
+        return svdq_pair_forward(x, fc1, fc2)
+    return fc2(fc1(x))
+
+
 class DualBlock(nn.Module):
-    def __init__(self, cfg: FluxDiTConfig, make, seed: int, device) -> None:
+    def __init__(self, cfg: FluxDiTConfig, make, seed: int, device, fused: bool = False) -> None:
         super().__init__()
         c = cfg.hidden
-        self.cfg = cfg
+        self.cfg, self.fused = cfg, fused
         self.mod_img, self.mod_txt = make(c, 6 * c, seed), make(c, 6 * c, seed + 1)
         self.qkv_img, self.qkv_txt = make(c, 3 * c, seed + 2), make(c, 3 * c, seed + 3)
         self.o_img, self.o_txt = make(c, c, seed + 4), make(c, c, seed + 5)
@@ -151,16 +162,16 @@ class DualBlock(nn.Module):
         at, ai = a[: txt.shape[0]], a[txt.shape[0]:]
         img = img + g1 * self.o_img(ai.contiguous())
         txt = txt + tg1 * self.o_txt(at.contiguous())
-        img = img + g2 * self.fc2_img(self.fc1_img(_ln(img) * (1 + sc2) + sh2))
-        txt = txt + tg2 * self.fc2_txt(self.fc1_txt(_ln(txt) * (1 + tsc2) + tsh2))
+        img = img + g2 * _mlp(self.fc1_img, self.fc2_img, _ln(img) * (1 + sc2) + sh2, self.fused)
+        txt = txt + tg2 * _mlp(self.fc1_txt, self.fc2_txt, _ln(txt) * (1 + tsc2) + tsh2, self.fused)
         return img, txt
 
 
 class SingleBlock(nn.Module):
-    def __init__(self, cfg: FluxDiTConfig, make, seed: int, device) -> None:
+    def __init__(self, cfg: FluxDiTConfig, make, seed: int, device, fused: bool = False) -> None:
         super().__init__()
         c = cfg.hidden
-        self.cfg = cfg
+        self.cfg, self.fused = cfg, fused
         self.mod = make(c, 3 * c, seed)
         self.qkv = make(c, 3 * c, seed + 1)
         self.mlp = make(c, cfg.mlp, seed + 2, gelu=True)
@@ -177,6 +188,10 @@ class SingleBlock(nn.Module):
         q, k, v = self.qkv(n).chunk(3, dim=-1)
         a = _attention(_rope(_rms(q.reshape(hq), self.qn), cos, sin), _rope(_rms(k.reshape(hq), self.kn), cos, sin),
                        v.reshape(hq))
+        if self.fused:
+            from .svdq import svdq_concat_forward
+
+            return x + g * svdq_concat_forward(self.proj_out, a, self.mlp, n)
         return x + g * self.proj_out(torch.cat((a, self.mlp(n)), dim=-1))
 
 
@@ -190,8 +205,10 @@ class FluxDiT(nn.Module):
         c = cfg.hidden
         self.x_embedder = make(cfg.in_channels, c, seed)
         self.context_embedder = make(cfg.txt_dim, c, seed + 1)
-        self.dual = nn.ModuleList(DualBlock(cfg, make, seed + 100 + 10 * i, device) for i in range(cfg.n_dual))
-        self.single = nn.ModuleList(SingleBlock(cfg, make, seed + 400 + 10 * i, device)
+        fused = kind == "w4a4"
+        self.dual = nn.ModuleList(DualBlock(cfg, make, seed + 100 + 10 * i, device, fused)
+                                  for i in range(cfg.n_dual))
+        self.single = nn.ModuleList(SingleBlock(cfg, make, seed + 400 + 10 * i, device, fused)
                                     for i in range(cfg.n_single))
         self.norm_out = make(c, 2 * c, seed + 2)
         self.proj_out = make(c, cfg.in_channels, seed + 3)

@@ -90,3 +90,5 @@ def w8a8_layer(n: int, k: int, *, bias: bool = True, std: float = 0.02, seed_off
 # BASELINE configs
 C0 = dict(m=256, k=3072, n=3072, outlier_frac=0.01, outlier_scale=20.0)
 C1 = dict(m=4608, k=3072, n=3072, rank=32, outlier_frac=0.005, outlier_scale=30.0)
+C2 = dict(m=4608, d=3072, h=12288, rank=32, outlier_frac=0.005, outlier_scale=30.0)   # fc1 -> GELU -> fc2
+C3 = dict(ms=(256, 1024, 4608, 16384), k=3072, n=9216, rank=32, outlier_frac=0.005, outlier_scale=30.0)  # QKV

@@ -512,8 +512,12 @@ def test_flux_dit_small_matches_oracle_chain():
 
     cfg = FluxDiTConfig(hidden=512, heads=4, head_dim=128, mlp=2048, n_dual=1, n_single=1, img_tokens=192,
                         txt_tokens=64, in_channels=64, txt_dim=256, rank=32)
-    model = FluxDiT("w4a4", cfg, device=DEV)
+    model = FluxDiT("w4a4", cfg, device=DEV)       # MLPs and proj_out inputs through the fused epilogues
+    unfused = copy.deepcopy(model)                   # every linear through its own forward
     ref_model = copy.deepcopy(model)
+    for m_ in (unfused, ref_model):
+        for blk in list(m_.dual) + list(m_.single):
+            blk.fused = False
 
     class _OracleLinear(torch.nn.Module):
         def __init__(self, mod):
@@ -536,7 +540,7 @@ def test_flux_dit_small_matches_oracle_chain():
 
     seen = []
     hooks = [m.register_forward_hook(lambda m_, inp, out: seen.append((m_, inp[0].detach(), out.detach())))
-             for m in model.modules() if isinstance(m, SvdqW4A4Linear)]
+             for m in unfused.modules() if isinstance(m, SvdqW4A4Linear)]
     n_swapped = 0
     for mod in list(ref_model.modules()):
         for cname, child in list(mod.named_children()):
@@ -547,6 +551,7 @@ def test_flux_dit_small_matches_oracle_chain():
     args = inputs(cfg, device=DEV)
     with torch.no_grad():
         y = model(*args).float()
+        yu = unfused(*args).float()
         yr = ref_model(*args).float()
     for h in hooks:
         h.remove()
@@ -563,5 +568,7 @@ def test_flux_dit_small_matches_oracle_chain():
     assert torch.isfinite(y).all() and torch.isfinite(yr).all()
     cos = torch.nn.functional.cosine_similarity(y.flatten(), yr.flatten(), dim=0).item()
     rel = ((y - yr).norm() / yr.norm()).item()
-    print("dit small: cos", cos, "rel", rel)
+    cos_u = torch.nn.functional.cosine_similarity(y.flatten(), yu.flatten(), dim=0).item()
+    print("dit small: cos", cos, "rel", rel, "fused vs unfused cos", cos_u)
     assert cos > 0.995 and rel < 0.1, (cos, rel)
+    assert cos_u > 0.999, cos_u   # the fused model differs from the unfused one only by la's fp32 sum order
