@@ -333,7 +333,7 @@ def main() -> int:
     ops = torch.ops.cozy_gen_worker
 
     def quant():
-        return ops.svdq_quant_fp6(x, mod.smooth_factor, None, mod.proj_down_op)
+        return ops.svdq_quant_fp6(x, mod.smooth_factor, None, mod.proj_down_op6)
 
     qa, la = quant()
 

@@ -33,17 +33,20 @@ enum {
 
 enum { GWA_DT_BF16 = 0, GWA_DT_F16 = 1, GWA_DT_F32 = 2 };
 
-/* GEMM epilogue flags */
-enum { GWA_EPI_GELU_TANH = 1 };
+/* GEMM epilogue flags: GELU-tanh after the bias; la given as fp32 (rounded to
+ * bf16 in the epilogue, the fp6 GEMMs only) */
+enum { GWA_EPI_GELU_TANH = 1, GWA_EPI_LA_F32 = 2 };
 
-/* activation code formats written by gwa_svdq_quant_int4 */
+/* activation code formats */
 enum {
-  GWA_QFMT_INT4 = 0, /* uint8 [M, K/2]: two's-complement nibbles, element 2j in the low nibble (the reference contract) */
-  GWA_QFMT_FP6 = 1   /* uint8 [K/128, M, 104] operand records of the fp6 GEMM, see below */
+  GWA_QFMT_INT4 = 0, /* uint8 [M, K/2]: two's-complement nibbles, element 2j in the low nibble (the reference
+                        contract), written by gwa_svdq_quant_int4 */
+  GWA_QFMT_FP6 = 1   /* uint8 [K/128, M, 104] operand records of the fp6 GEMM (see below), written by
+                        gwa_svdq_quant_fp6 and gwa_svdq_gemm_w4a4_fp6_next */
 };
 
-/* fp6 operand records (activations from gwa_svdq_quant_int4(..., GWA_QFMT_FP6),
- * weights from gwa_svdq_pack_weight_fp6): stage-major, one 104-byte record per
+/* fp6 operand records (activations from gwa_svdq_quant_fp6, weights from
+ * gwa_svdq_pack_weight_fp6): stage-major, one 104-byte record per
  * 128-element stage s of K and row r at byte offset (s * rows + r) * 104:
  *   bytes [0, 96)   the stage's two groups as e3m2 codes: element t of group j
  *                   at bits [6t, 6t+6) of bytes [48j, 48j+48) (little-endian)
@@ -80,10 +83,9 @@ int gwa_probe_add_one(const float* in, float* out, int64_t n, void* stream);
  *              (scale * s2), as models/nvfp4_quant.py:98-101 do for nvfp4
  *   proj_down_op  proj_down in MFMA operand order (gwa_svdq_prep_proj_down)
  *              or NULL; rank in {0, 16, 32, 64, 128}
- *   out_format GWA_QFMT_INT4 (q uint8 [M, K/2]) or GWA_QFMT_FP6 (q: the fp6
- *              operand records [K/128, M, 104], K % 128 == 0)
- *   scales     fp16 [M, K/64] (out; may be NULL with GWA_QFMT_FP6, whose
- *              records carry the scales)
+ *   out_format GWA_QFMT_INT4 (q uint8 [M, K/2]); the fp6 records come from
+ *              gwa_svdq_quant_fp6
+ *   scales     fp16 [M, K/64] (out)
  *   la         bf16 [M, rank] = x @ proj_down on RAW x (out; NULL iff proj_down_op is NULL) */
 int gwa_svdq_quant_int4(const void* x, int64_t ldx, const void* smooth, const float* s2,
                         const void* proj_down_op, int64_t rank, int out_format,
@@ -138,9 +140,13 @@ int gwa_svdq_pack_weight_fp6(const uint8_t* qw, const void* sw, uint8_t* qw6, in
 /* Kernel 2, fp6 path: the contract of gwa_svdq_gemm_w4a4 (replacing
  * _gemm_w4a4 + svdq_epilogue_lora, models/w4a4.py:173-180 and
  * models/svdq_fused.py:315-377) on fp6 operand records: qa6 [K/128, M, 104]
- * from gwa_svdq_quant_int4(..., GWA_QFMT_FP6, ...), qw6 [K/128, N, 104] from
- * gwa_svdq_pack_weight_fp6 (the records carry sa and sw). One exact fp6 MFMA
- * per K-group and 32x32 block. K % 128 == 0, N % 16 == 0. */
+ * from gwa_svdq_quant_fp6, qw6 [K/128, N, 104] from gwa_svdq_pack_weight_fp6
+ * (the records carry sa and sw). qa6's storage must stay readable for 16
+ * bytes past its last record (the 16-byte operand copies of an odd M with an
+ * even K/128 end 8 bytes past it). One exact fp6 MFMA per K-group and 32x32
+ * block. la is bf16 [M, rank], or fp32 with GWA_EPI_LA_F32 in
+ * epilogue_flags (rounded to bf16 in the epilogue). K % 128 == 0,
+ * N % 16 == 0. */
 int gwa_svdq_gemm_w4a4_fp6(const uint8_t* qa6, const uint8_t* qw6,
                            const float* s2, const float* second, int64_t second_numel,
                            const void* la, const void* up, int64_t rank, const void* bias,
@@ -157,38 +163,73 @@ int gwa_svdq_gemm_w4a4_fp6(const uint8_t* qa6, const uint8_t* qw6,
  *   y        = this layer's output exactly as gwa_svdq_gemm_w4a4_fp6 computes
  *              it (bf16), also stored to `out` unless out is NULL
  *   next_q6  uint8 [N/128, M, 104] (out): the next layer's fp6 operand
- *            records of y — bit-identical to gwa_svdq_quant_int4(y,
- *            next_smooth, s2 = NULL, ..., GWA_QFMT_FP6, ...). The pointer may
+ *            records of y — bit-identical to gwa_svdq_quant_fp6(y,
+ *            next_smooth, s2 = NULL, ...). The pointer may
  *            sit inside a larger record buffer of the same M (stage-major:
  *            stage s at byte s * M * 104), e.g. at stage 24 of a [120, M, 104]
  *            buffer whose first stages another producer writes.
- *   next_la32 fp32 [M, next_rank] (in/out): next_la32 += y @ proj_down_next,
- *            summed over this layer's column tiles with atomic adds (the
- *            order of the fp32 additions varies from run to run); round to
- *            bf16 for the next layer's la. NULL iff next_proj_down_op is NULL.
+ *   next_la_part fp32 [P, M, next_rank] (out), P =
+ *            gwa_svdq_gemm_w4a4_fp6_next_partials(M, N): slot p holds
+ *            y[:, columns of column tile p] @ proj_down_next[those rows];
+ *            gwa_svdq_la_reduce of all of a layer's slots (with other
+ *            producers' slots appended, as for [x, y] inputs) gives its bf16
+ *            la. NULL iff next_proj_down_op is NULL.
  *   next_smooth       bf16 [N] (the next layer's smoothing factors) or NULL
- *   next_proj_down_op the next layer's proj_down [N, next_rank] in MFMA operand
- *            order (gwa_svdq_prep_proj_down), next_rank in {0,16,32,64,128}
- * Single-level (the next layer's s2 = 1). Output dtype bf16. N % 128 == 0,
- * K % 128 == 0. */
+ *   next_proj_down_op the next layer's proj_down rows for these N inputs in
+ *            gwa_svdq_prep_proj_down_fp6 order, next_rank in {0,16,32,64,128}
+ * Single-level (the next layer's s2 = 1). Output dtype bf16; la may be fp32
+ * (GWA_EPI_LA_F32). N % 128 == 0, K % 128 == 0. */
 int gwa_svdq_gemm_w4a4_fp6_next(const uint8_t* qa6, const uint8_t* qw6,
                                 const float* s2, const float* second, int64_t second_numel,
                                 const void* la, const void* up, int64_t rank, const void* bias,
                                 void* out, int epilogue_flags,
                                 const void* next_smooth, const void* next_proj_down_op, int64_t next_rank,
-                                uint8_t* next_q6, float* next_la32,
+                                uint8_t* next_q6, float* next_la_part,
                                 int64_t M, int64_t N, int64_t K, void* stream);
 
-/* Kernel 1 into fp6 records with the low-rank product ACCUMULATED in fp32:
- * la32 [M, rank] += x @ proj_down (a read-modify-write per row, ordered after
- * every earlier writer of la32 on the stream). With
- * gwa_svdq_gemm_w4a4_fp6_next it builds the input of a layer whose K is the
- * concatenation of two producers' outputs (Flux's single-block proj_out
- * takes [attention; MLP]): each producer writes its own stages of one
- * record buffer and adds its part of x @ proj_down. Otherwise as
- * gwa_svdq_quant_int4(..., s2 = NULL, ..., GWA_QFMT_FP6, q6, NULL, ...). */
-int gwa_svdq_quant_fp6_la_f32(const void* x, int64_t ldx, const void* smooth, const void* proj_down_op,
-                              int64_t rank, uint8_t* q6, float* la32, int64_t M, int64_t K, void* stream);
+/* Number of la partial slots gwa_svdq_gemm_w4a4_fp6_next writes (its column
+ * tiles) for M rows and N outputs. */
+int64_t gwa_svdq_gemm_w4a4_fp6_next_partials(int64_t M, int64_t N);
+
+/* Kernel 1 for the fp6 GEMM lane: the arithmetic of gwa_svdq_quant_int4
+ * (same codes and scales, bit for bit) written as fp6 operand records, with
+ * the low-rank product as fp32 partial sums (replaces
+ * cozy_gen_worker::svdq_quant, models/svdq_fused.py:293-306, plus
+ * `la = x2 @ proj_down`, :524):
+ *   x          bf16 [M, K] rows with stride ldx (elements), K % 128 == 0
+ *   smooth     bf16 [K] or NULL;  s2 fp32 device scalar or NULL (= 1.0)
+ *   proj_down_op6  proj_down in this kernel's operand order
+ *              (gwa_svdq_prep_proj_down_fp6) or NULL; rank in {0,16,32,64,128}
+ *   q6         uint8 [K/128, M, 104] records (out). The pointer may sit inside
+ *              a larger record buffer of the same M (stage s at byte s*M*104):
+ *              a layer whose input concatenates [x, other] takes its first
+ *              K/128 stages from here and the rest from another producer
+ *              (gwa_svdq_gemm_w4a4_fp6_next).
+ *   la_part    fp32 [P, M, rank] (out), P = gwa_svdq_quant_fp6_partials(M, K,
+ *              rank): partial sums of x @ proj_down on RAW x over P ranges of
+ *              K, every slot fully written; gwa_svdq_la_reduce sums them into
+ *              the bf16 la (a fixed order: deterministic). NULL iff
+ *              proj_down_op6 is NULL. */
+int gwa_svdq_quant_fp6(const void* x, int64_t ldx, const void* smooth, const float* s2,
+                       const void* proj_down_op6, int64_t rank, uint8_t* q6, float* la_part,
+                       int64_t M, int64_t K, void* stream);
+
+/* Number of la partial slots gwa_svdq_quant_fp6 writes for this shape (0 for
+ * rank 0 or a bad shape). */
+int64_t gwa_svdq_quant_fp6_partials(int64_t M, int64_t K, int64_t rank);
+
+/* la bf16 [M, rank] = RN_bf16(part[0] + part[1] + ... + part[P-1]) (fp32
+ * additions in that order; part fp32 [P, M, rank], rank % 16 == 0): the
+ * bf16 la of the reference's `x2 @ proj_down` (models/svdq_fused.py:524)
+ * from the producers' partial sums. */
+int gwa_svdq_la_reduce(const float* part, int64_t P, int64_t M, int64_t rank, void* la, void* stream);
+
+/* proj_down bf16 [K, rank] -> the operand order of gwa_svdq_quant_fp6 and of
+ * the next-layer epilogue of gwa_svdq_gemm_w4a4_fp6_next (done once per
+ * weight; no reference counterpart). K % 128 == 0.
+ *   out  bf16 [K * rank] (16-byte aligned): stage-major, element
+ *        (((s*4 + j)*(rank/16) + b)*64 + l)*8 + e = proj_down[128s + 32(l/16) + 8j + e][16b + l%16] */
+int gwa_svdq_prep_proj_down_fp6(const void* proj_down, void* out, int64_t K, int64_t rank, void* stream);
 
 /* Debug: exact int32 per-group partial sums (layout of gwa_svdq_group_psums)
  * through the fp6 GEMM's MFMA on fp6 operand records. No reference counterpart. */

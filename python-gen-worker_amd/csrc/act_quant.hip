@@ -22,12 +22,9 @@
 //    gwa_svdq_prep_proj_down), so no transpose touches global memory.
 // The eight waves' la partials are summed through LDS at the end.
 //
-// Output formats: GWA_QFMT_INT4 is the reference contract (two's-complement
-// nibbles, element 2j in the low nibble of byte j); GWA_QFMT_FP6 writes the
-// same codes as e3m2 fp6 in the fp6 GEMM's operand records (one 104-byte
-// record per 128-column stage and row, stage-major: 96 bytes of codes with
-// element t of a group at bits [6t, 6t+6) of the group's 48 bytes, then the
-// stage's two fp16 group scales).
+// Output: the reference contract (two's-complement nibbles, element 2j in the
+// low nibble of byte j; fp16 scales [M, K/64]; la bf16). The fp6 GEMM lane's
+// records come from svdq_quant_fp6_kernel below.
 //
 // Arithmetic = the reference order (models/svdq_fused.py:88-103,
 // models/nvfp4_quant.py:96-102), computed by the per-lane quantizer of
@@ -49,11 +46,11 @@ __device__ __forceinline__ void unpack8_bf16(v4i w, float* v) {
   }
 }
 
-template <int RB, int FMT, int PF>
+template <int RB, int PF>
 __global__ __launch_bounds__(512) void svdq_quant_int4_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, const uint16_t* __restrict__ smooth,
     const float* __restrict__ s2p, const uint16_t* __restrict__ pdo, uint8_t* __restrict__ q,
-    uint16_t* __restrict__ sc, void* __restrict__ la, int la_f32_add, int M, int K) {
+    uint16_t* __restrict__ sc, uint16_t* __restrict__ la, int M, int K) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   constexpr int RBX = RB > 0 ? RB : 1;
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -63,10 +60,9 @@ __global__ __launch_bounds__(512) void svdq_quant_int4_kernel(
 
   // buffers: every access is unconditional; rows >= M, columns >= K read 0 / store nothing
   const rsrc_t xbuf = make_rsrc(x, (uint32_t)(((int64_t)(M - 1) * ldx + K) * 2));
-  // FP6: [K/128][M][104] records (96 bytes of codes, 2 fp16 scales, 4 unused bytes)
-  const int64_t qrow_bytes = FMT == GWA_QFMT_FP6 ? (int64_t)(K / 128) * GWA_FP6_REC : (int64_t)K / 2;
+  const int64_t qrow_bytes = (int64_t)K / 2;
   const rsrc_t qbuf = make_rsrc(q, (uint32_t)((int64_t)M * qrow_bytes));
-  const rsrc_t sbuf = make_rsrc(sc, sc ? (uint32_t)((int64_t)M * G * 2) : 0u);
+  const rsrc_t sbuf = make_rsrc(sc, (uint32_t)((int64_t)M * G * 2));
   const rsrc_t pbuf = make_rsrc(pdo, (uint32_t)((int64_t)rounds * KT * RB * 32));
   const rsrc_t smbuf = make_rsrc(smooth, smooth ? (uint32_t)(K * 2) : 0u);
 
@@ -144,7 +140,7 @@ __global__ __launch_bounds__(512) void svdq_quant_int4_kernel(
       {
         const int kg = r * KT + qc;       // first column
         const int g = kg >> 6;            // group
-        const bool valid = kg < K && grow < M;  // rows past M must not store (fp6 records of the next stage follow)
+        const bool valid = kg < K && grow < M;
         const v4i c0 = *(const v4i*)(base + qr * XT_STR + qc * 2);
         uint32_t w[4];
         if (!smooth) {
@@ -161,16 +157,10 @@ __global__ __launch_bounds__(512) void svdq_quant_int4_kernel(
         uint32_t nb[2];
         uint16_t sh;
         g64::quant8(w, valid, s2_one, s2, nb, sh);
-        if (FMT == GWA_QFMT_FP6) {
-          // record of (128-column stage g / 2, row), group g % 2 of the stage
-          const uint32_t rec = (uint32_t)(((int64_t)(g >> 1) * M + grow) * GWA_FP6_REC);
-          g64::store_fp6(qbuf, rec, g & 1, lane, nb, sh, valid);
-        } else {
-          const uint32_t a = nb[0], bb = nb[1];
-          const uint32_t pa = (a & 0xFu) | ((a >> 4) & 0xF0u) | ((a >> 8) & 0xF00u) | ((a >> 12) & 0xF000u);
-          const uint32_t pb = (bb & 0xFu) | ((bb >> 4) & 0xF0u) | ((bb >> 8) & 0xF00u) | ((bb >> 12) & 0xF000u);
-          buf_store4(pa | (pb << 16), qbuf, valid ? q_row_off + (uint32_t)(kg / 2) : kOOB);
-        }
+        const uint32_t a = nb[0], bb = nb[1];
+        const uint32_t pa = (a & 0xFu) | ((a >> 4) & 0xF0u) | ((a >> 8) & 0xF00u) | ((a >> 12) & 0xF000u);
+        const uint32_t pb = (bb & 0xFu) | ((bb >> 4) & 0xF0u) | ((bb >> 8) & 0xF00u) | ((bb >> 12) & 0xF000u);
+        buf_store4(pa | (pb << 16), qbuf, valid ? q_row_off + (uint32_t)(kg / 2) : kOOB);
         buf_store2(sh, sbuf, valid ? s_row_off + (uint32_t)(g * 2) : kOOB);
       }
 
@@ -187,7 +177,7 @@ __global__ __launch_bounds__(512) void svdq_quant_int4_kernel(
   }
 
   if (RB > 0) {
-    // sum the 8 waves' partial la blocks through LDS; wave 0 writes bf16 (or adds into fp32)
+    // sum the 8 waves' partial la blocks through LDS; wave 0 writes bf16
     __syncthreads();
     float* lap = (float*)lds;
 #pragma unroll
@@ -203,15 +193,286 @@ __global__ __launch_bounds__(512) void svdq_quant_int4_kernel(
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
           const int r = row0 + 4 * (lane >> 4) + t;
-          if (r < M) {
-            const int64_t i = (int64_t)r * R + rb * 16 + (lane & 15);
-            if (la_f32_add) ((float*)la)[i] += s[t];  // rows are this workgroup's alone
-            else ((uint16_t*)la)[i] = f32_to_bf16(s[t]);
-          }
+          if (r < M) la[(int64_t)r * R + rb * 16 + (lane & 15)] = f32_to_bf16(s[t]);
         }
       }
     }
   }
+}
+
+// ---------------------------------------------------------------------------
+// Kernel 1, fp6 records (the fp6 GEMM lane): smoothing divide -> group-64
+// absmax -> fp16 scale -> int4 codes written as e3m2 operand records, plus
+// la += x @ proj_down on the RAW activations, in fp32.
+//
+// Work split: a task is 16 rows x one 128-column stage (one record per row).
+// A 256-thread workgroup (4 waves) owns 64 rows x CH consecutive stages; K
+// is split over workgroups (grid.y), so la is a sum of per-workgroup
+// partials: workgroup (g, y) stores its rows' partial into slot y of
+// la_part [P][M][rank] fp32 (plain stores), and gwa_svdq_la_reduce sums the
+// slots in a fixed order (deterministic). In a task, lane (r, c) = (lane %
+// 16, lane / 16) holds row r, columns 32c .. 32c+31 of the stage: half of
+// group c / 2, so a group's absmax is one max over the lane's 32 values and
+// one exchange with lane ^ 16.
+//  * Every wave issues all of its x loads (CH tasks x 4 x 16 bytes per lane)
+//    at the start, after the workgroup's copies of the stages' proj_down
+//    operands (direct-to-LDS) and smoothing factors; nothing else waits on
+//    HBM.
+//  * The smoothing reciprocals RN(1/s) of the stages are formed once per
+//    workgroup in LDS (a non-normal reciprocal flags the stage for the
+//    division path).
+//  * Codes: q = RNE(xs / d) by the 2^-12 snap of the multiply path (exact,
+//    see quant_g64.h), as floats; the lane's 32 codes are packed to e3m2 by
+//    one v_cvt_scalef32_2xpk16_bf6_f32 (unit scale: exact for every integer
+//    in [-8, 8]; element 2i from the first source's i, 2i+1 from the
+//    second's) straight into the record's bit layout and stored as 24 bytes.
+//  * la: the task's x chunks are the A operands of four 16x16x32 bf16 MFMAs
+//    per 16 ranks (lane (r, c) supplies columns 32c + 8j .. +8 at k-step j);
+//    proj_down is pre-arranged in that order (gwa_svdq_prep_proj_down_fp6)
+//    so each B operand is one 16-byte LDS read per lane.
+// Arithmetic and exactness = quant_g64.h's: identical codes and scales.
+// ---------------------------------------------------------------------------
+constexpr int Q6_WAVES = 4, Q6_THREADS = 64 * Q6_WAVES, Q6_ROWS = 16 * Q6_WAVES;
+
+__device__ __forceinline__ void dma16_lds(v4i rsrc, uint32_t lds_addr, uint32_t voff, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(lds_addr), "v"(voff), "s"(rsrc), "s"(soff)
+               : "memory", "m0");
+}
+
+__device__ __forceinline__ v4i raw_rsrc4(const void* base, uint32_t bytes) {
+  const uint64_t a = (uint64_t)base;
+  return (v4i){(int)(uint32_t)a, (int)(uint32_t)((a >> 32) & 0xFFFFu), (int)bytes, 0x00020000};
+}
+
+template <int n>
+__device__ __forceinline__ void wait_vm_lgkm0_q() {
+  static_assert(n >= 0 && n < 64, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4));
+}
+
+template <int RB, int CH>
+__global__ __launch_bounds__(Q6_THREADS) void svdq_quant_fp6_kernel(
+    const uint16_t* __restrict__ x, int64_t ldx, const uint16_t* __restrict__ smooth, const float* __restrict__ s2p,
+    const uint16_t* __restrict__ pdo, uint8_t* __restrict__ q6, float* __restrict__ la_part, int M, int K) {
+  constexpr int RBX = RB > 0 ? RB : 1;
+  constexpr int PDO_STAGE = RB * 4096;                       // bytes of proj_down operands per stage
+  constexpr int RCP_OFF = CH * PDO_STAGE;                    // [CH][128] reciprocals, [CH][128] factors
+  constexpr int FLAG_OFF = RCP_OFF + CH * 128 * 4 * 2;       // [CH] division-path flags
+  __shared__ __attribute__((aligned(16))) uint8_t lds[FLAG_OFF + CH * 4];
+
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int S = K >> 7;
+  const int st0 = blockIdx.y * CH;
+  const int r = lane & 15, c = lane >> 4;
+  const int row0 = blockIdx.x * Q6_ROWS + 16 * wave;
+  const int grow = row0 + r;
+  const bool row_ok = grow < M;
+
+  // 1. the stages' proj_down operands, direct to LDS: CH * RB * 4 runs of 1 KB, dealt round-robin (every
+  //    wave issues the same number). The offset goes in the VGPR operand, the one the hardware range-checks:
+  //    the runs of stages past K read zeros.
+  if constexpr (RB > 0) {
+    const v4i pbuf = raw_rsrc4(pdo, (uint32_t)((int64_t)S * PDO_STAGE));
+    constexpr int RUNS = CH * RB * 4, PER = RUNS / Q6_WAVES;
+    static_assert(RUNS % Q6_WAVES == 0, "proj_down runs");
+    const uint32_t valid = (uint32_t)(S - st0) * PDO_STAGE;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int qr = wave + Q6_WAVES * j;
+      const uint32_t in_chunk = (uint32_t)(qr * 1024) + 16u * (uint32_t)lane;
+      dma16_lds(pbuf, (uint32_t)(uintptr_t)(lds + qr * 1024),
+                in_chunk < valid ? (uint32_t)st0 * PDO_STAGE + in_chunk : kOOB, 0u);
+    }
+  }
+  // 2. smoothing factors: thread t holds columns 2t, 2t + 1 of the chunk (CH * 128 columns)
+  const rsrc_t smbuf = make_rsrc(smooth, smooth ? (uint32_t)(K * 2) : 0u);
+  static_assert(CH * 128 <= 2 * Q6_THREADS, "smoothing columns per thread");
+  const int scol = st0 * 128 + 2 * tid;
+  const bool s_role = smooth && 2 * tid < CH * 128;
+  const uint32_t sv = s_role ? buf_load4(smbuf, scol < K ? (uint32_t)(scol * 2) : kOOB) : 0u;
+  // 3. x: all CH tasks, 4 x 16 bytes per lane each (rows past M / stages past K read 0)
+  const rsrc_t xbuf = make_rsrc(x, (uint32_t)(((int64_t)(M - 1) * ldx + K) * 2));
+  v4i xv[CH][4];
+#pragma unroll
+  for (int t = 0; t < CH; ++t)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int col = (st0 + t) * 128 + 32 * c + 8 * j;
+      xv[t][j] = buf_load16(xbuf, (row_ok && st0 + t < S) ? (uint32_t)(((int64_t)grow * ldx + col) * 2) : kOOB);
+    }
+  // 4. reciprocals (the copies and the factors are complete once at most CH * 4 loads remain)
+  wait_vm_lgkm0_q<CH * 4>();
+  if (s_role) {
+    const float s0 = bf16_lo(sv), s1 = bf16_hi(sv);
+    float* rcp = (float*)(lds + RCP_OFF);
+    const int i = 2 * tid;
+    rcp[i] = 1.0f / s0;
+    rcp[i + 1] = 1.0f / s1;
+    rcp[CH * 128 + i] = s0;
+    rcp[CH * 128 + i + 1] = s1;
+  }
+  if (tid < CH) *(int*)(lds + FLAG_OFF + 4 * tid) = 0;
+  __syncthreads();
+  if (s_role && scol < K && (!g64::smooth_ok(bf16_lo(sv)) || !g64::smooth_ok(bf16_hi(sv))))
+    *(int*)(lds + FLAG_OFF + 4 * (tid / 64)) = 1;   // columns 2t, 2t+1 lie in stage t / 64 of the chunk
+  __syncthreads();
+
+  const float s2 = s2p ? *s2p : 1.0f;
+  const bool s2_one = s2 == 1.0f;
+  const rsrc_t qbuf = make_rsrc(q6, (uint32_t)((int64_t)S * M * GWA_FP6_REC));
+  v4f acc[RBX];
+#pragma unroll
+  for (int rb = 0; rb < RBX; ++rb) acc[rb] = (v4f){0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+  for (int t = 0; t < CH; ++t) {
+    const int st = st0 + t;
+    if (st >= S) break;  // workgroup-uniform
+    // ---- xs = RN_bf16(x / smooth) as floats, and the lane's absmax
+    float v[32];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[8 * j + 2 * e] = bf16_lo((uint32_t)xv[t][j][e]);
+        v[8 * j + 2 * e + 1] = bf16_hi((uint32_t)xv[t][j][e]);
+      }
+    if (smooth) {
+      // the stage's flag is workgroup-uniform: one scalar branch, not one per element
+      const int divide = __builtin_amdgcn_readfirstlane(*(const int*)(lds + FLAG_OFF + 4 * t));
+      const float* f = (const float*)(lds + RCP_OFF) + t * 128 + 32 * c;
+      if (!divide) {
+#pragma unroll
+        for (int i = 0; i < 32; i += 4) {
+          const v4f fv = *(const v4f*)(f + i);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[i + e] *= fv[e];
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 32; i += 4) {
+          const v4f fv = *(const v4f*)(f + CH * 128 + i);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[i + e] /= fv[e];
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 32; i += 2) {
+        const uint32_t pk = pack_bf16x2_rn(v[i], v[i + 1]);
+        v[i] = bf16_lo(pk);
+        v[i + 1] = bf16_hi(pk);
+      }
+    }
+    // absmax on the bit patterns (|x| orders like its bits; a NaN ranks above inf, as in quant_g64.h),
+    // then the group's other half in lane ^ 16
+    uint32_t mu = 0;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) mu = max(mu, __float_as_uint(v[i]) & 0x7fffffffu);
+    mu = max(mu, (uint32_t)__shfl_xor((int)mu, 16));
+    const float amax = __uint_as_float(mu);
+    const uint32_t mb = mu >> 16;  // the bf16 bits of amax
+
+    // ---- scale and codes (quant_g64.h's arithmetic, 32 elements per lane)
+    float scl;
+    const float r7 = 1.0f / 7.0f;
+    const bool easy = s2_one && (mb & 0x7F80u) != 0x7F80u;
+    if (__builtin_amdgcn_ballot_w64(!easy) == 0) {
+      const float q1 = amax * r7;
+      scl = fmaf(fmaf(-7.0f, q1, amax), r7, q1);
+    } else {
+      scl = amax / (7.0f * s2);
+    }
+    const bool fast = !row_ok || (s2_one && scl >= g64::kFp16MinNormal && scl < g64::kFp16Max);
+    scl = fminf(fmaxf(scl, g64::kScaleMin), g64::kFp16Max);
+    const uint16_t sh = f32_to_f16_bits(scl);
+    const float d = f16_bits_to_f32(sh) * s2;
+    v16f qa, qb;  // codes 2i / 2i + 1, as floats
+    if (__builtin_amdgcn_ballot_w64(!fast) == 0) {
+      const float rd = __builtin_amdgcn_rcpf(d);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        qa[i] = (((v[2 * i] * rd) + g64::kSnap) + g64::kRound) - 12582912.0f;
+        qb[i] = (((v[2 * i + 1] * rd) + g64::kSnap) + g64::kRound) - 12582912.0f;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        // + 0.0f: a -0 code is stored as +0 (e3m2 0x00), as the nibble path does
+        qa[i] = fminf(fmaxf(__builtin_rintf(v[2 * i] / d), -8.0f), 7.0f) + 0.0f;
+        qb[i] = fminf(fmaxf(__builtin_rintf(v[2 * i + 1] / d), -8.0f), 7.0f) + 0.0f;
+      }
+    }
+    typedef unsigned int v6u __attribute__((ext_vector_type(6)));
+    const v6u pk = __builtin_amdgcn_cvt_scalef32_2xpk16_bf6_f32(qa, qb, 1.0f);
+    // ---- record (stage st, row grow): bytes [24c, 24c + 24) hold this half-group; 96 + 2 g the scale
+    const uint32_t rec = (uint32_t)(((int64_t)st * M + grow) * GWA_FP6_REC);
+    buf_store16((v4i){(int)pk[0], (int)pk[1], (int)pk[2], (int)pk[3]}, qbuf, row_ok ? rec + 24u * c : kOOB);
+    buf_store8(make_uint2(pk[4], pk[5]), qbuf, row_ok ? rec + 24u * c + 16u : kOOB);
+    buf_store2(sh, qbuf, (row_ok && (c & 1) == 0) ? rec + 96u + (uint32_t)(c & 2) : kOOB);
+
+    // ---- la += x[rows, stage] @ proj_down[stage, :]
+    if constexpr (RB > 0) {
+      const uint8_t* pb = lds + t * PDO_STAGE + 16 * lane;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+          acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, xv[t][j]),
+                                                            *(const v8bf*)(pb + (j * RB + rb) * 1024), acc[rb],
+                                                            0, 0, 0);
+    }
+  }
+  if constexpr (RB > 0) {
+    // lane holds the partial la[row0 + 4c + i][16 rb + r], i = 0..3: slot blockIdx.y of la_part
+    const int R = RB * 16;
+    float* slot = la_part + (int64_t)blockIdx.y * M * R;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = row0 + 4 * c + i;
+        if (m < M) slot[(int64_t)m * R + 16 * rb + r] = acc[rb][i];
+      }
+  }
+}
+
+// la = RN_bf16(sum over p of part[p]) in the order p = 0, 1, ...: one thread per row and 4 ranks.
+__global__ __launch_bounds__(256) void la_reduce_kernel(const float* __restrict__ part, int P, int64_t MR,
+                                                         uint16_t* __restrict__ la) {
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i >= MR) return;
+  v4f s = *(const v4f*)(part + i);
+  for (int p = 1; p < P; ++p) s += *(const v4f*)(part + (int64_t)p * MR + i);
+  *(uint2*)(la + i) = make_uint2(pack_bf16x2_rn(s[0], s[1]), pack_bf16x2_rn(s[2], s[3]));
+}
+
+// proj_down [K, R] bf16 -> the operand order of svdq_quant_fp6_kernel and of
+// the fp6 GEMM's next-layer epilogue: stage-major, per stage 4 k-steps x R/16
+// blocks of 64 lanes x 8 values,
+// out[(((s * 4 + j) * RB + rb) * 64 + lane) * 8 + e] =
+//     proj_down[128 s + 32 (lane / 16) + 8 j + e][16 rb + lane % 16].
+__global__ __launch_bounds__(256) void prep_proj_down_fp6_kernel(const uint16_t* __restrict__ pd,
+                                                                 uint16_t* __restrict__ out, int K, int R) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int RB = R / 16;
+  if (idx >= (int64_t)(K / 128) * 4 * RB * 64) return;
+  const int lane = (int)(idx % 64);
+  const int rb = (int)((idx / 64) % RB);
+  const int j = (int)((idx / (64 * RB)) % 4);
+  const int st = (int)(idx / (64 * RB * 4));
+  const int col = rb * 16 + (lane & 15);
+  const int k0 = st * 128 + 32 * (lane >> 4) + 8 * j;
+  uint16_t v[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = pd[(int64_t)(k0 + e) * R + col];
+  uint4 o;
+  o.x = (uint32_t)v[0] | ((uint32_t)v[1] << 16);
+  o.y = (uint32_t)v[2] | ((uint32_t)v[3] << 16);
+  o.z = (uint32_t)v[4] | ((uint32_t)v[5] << 16);
+  o.w = (uint32_t)v[6] | ((uint32_t)v[7] << 16);
+  *(uint4*)(out + idx * 8) = o;
 }
 
 // proj_down [K, R] bf16 -> MFMA B-operand order for kernel 1, zero padded to
@@ -302,6 +563,100 @@ __global__ __launch_bounds__(256) void svdq_epilogue_kernel(const uint16_t* __re
 
 }  // namespace
 
+extern "C" int gwa_svdq_prep_proj_down_fp6(const void* proj_down, void* out, int64_t K, int64_t rank,
+                                           void* stream) {
+  GWA_REQUIRE(K > 0 && K % 128 == 0 && K < (1ll << 24), "svdq_prep_proj_down_fp6: K=%lld is not a multiple of 128",
+              (long long)K);
+  GWA_REQUIRE(rank == 16 || rank == 32 || rank == 64 || rank == 128,
+              "svdq_prep_proj_down_fp6: rank %lld not in {16,32,64,128}", (long long)rank);
+  GWA_REQUIRE(proj_down && out, "svdq_prep_proj_down_fp6: null pointer");
+  GWA_REQUIRE(GWA_ALIGNED(proj_down, 2) && GWA_ALIGNED(out, 16), "svdq_prep_proj_down_fp6: out must be 16-byte aligned");
+  const int64_t total = (K / 128) * 4 * (rank / 16) * 64;
+  hipLaunchKernelGGL(prep_proj_down_fp6_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, (const uint16_t*)proj_down, (uint16_t*)out, (int)K, (int)rank);
+  return gwa_check_launch("svdq_prep_proj_down_fp6");
+}
+
+// stages per workgroup of svdq_quant_fp6_kernel: as many as keep >= 256 workgroups (a workgroup's loads all
+// go out at once), with the proj_down operands of a workgroup's stages within 32 KB of LDS
+static int quant_fp6_stages_per_group(int64_t M, int64_t K, int64_t R) {
+  const int64_t S = K / 128, groups = (M + Q6_ROWS - 1) / Q6_ROWS;
+  int ch = 4;
+  while (ch > 1 && (groups * ((S + ch - 1) / ch) < 256 || ch * (R / 16) > 8)) ch /= 2;
+  return ch;
+}
+
+extern "C" int64_t gwa_svdq_quant_fp6_partials(int64_t M, int64_t K, int64_t rank) {
+  if (M <= 0 || K <= 0 || K % 128 || rank <= 0) return 0;
+  const int64_t S = K / 128;
+  const int ch = quant_fp6_stages_per_group(M, K, rank);
+  return (S + ch - 1) / ch;
+}
+
+extern "C" int gwa_svdq_la_reduce(const float* part, int64_t P, int64_t M, int64_t rank, void* la, void* stream) {
+  GWA_REQUIRE(P >= 1 && M >= 0 && rank % 16 == 0 && rank > 0 && P * M * rank * 4 < (1ll << 40),
+              "svdq_la_reduce: bad shape P=%lld M=%lld rank=%lld", (long long)P, (long long)M, (long long)rank);
+  if (M == 0) return GWA_OK;
+  GWA_REQUIRE(part && la, "svdq_la_reduce: null pointer");
+  GWA_REQUIRE(GWA_ALIGNED(part, 16) && GWA_ALIGNED(la, 8), "svdq_la_reduce: part must be 16-byte, la 8-byte aligned");
+  const int64_t mr = M * rank, threads = mr / 4;
+  hipLaunchKernelGGL(la_reduce_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                     part, (int)P, mr, (uint16_t*)la);
+  return gwa_check_launch("svdq_la_reduce");
+}
+
+extern "C" int gwa_svdq_quant_fp6(const void* x, int64_t ldx, const void* smooth, const float* s2,
+                                  const void* proj_down_op6, int64_t rank, uint8_t* q6, float* la_part, int64_t M,
+                                  int64_t K, void* stream) {
+  const char* what = "svdq_quant_fp6";
+  GWA_REQUIRE(M >= 0 && K > 0 && K % 128 == 0, "%s: K=%lld is not a multiple of 128", what, (long long)K);
+  GWA_REQUIRE(ldx >= K && ldx % 8 == 0, "%s: row stride %lld must be >= K and a multiple of 8", what,
+              (long long)ldx);
+  GWA_REQUIRE((proj_down_op6 == nullptr) == (la_part == nullptr),
+              "%s: proj_down_op6 and la_part must both be given or both be NULL", what);
+  const int64_t R = proj_down_op6 ? rank : 0;
+  GWA_REQUIRE(R == 0 || R == 16 || R == 32 || R == 64 || R == 128, "%s: rank %lld not in {0,16,32,64,128}", what,
+              (long long)R);
+  GWA_REQUIRE(M < (1ll << 31) && K < (1ll << 24) && M * ldx * 2 < (1ll << 31) &&
+                  M * (K / 128) * GWA_FP6_REC < (1ll << 31) && (K / 128) * R * 256 < (1ll << 31),
+              "%s: x and q6 must stay below 2 GiB (buffer addressing)", what);
+  if (M == 0) return GWA_OK;
+  GWA_REQUIRE(x && q6, "%s: null pointer", what);
+  GWA_REQUIRE(GWA_ALIGNED(x, 16) && GWA_ALIGNED(q6, 8) && GWA_ALIGNED(smooth, 4) && GWA_ALIGNED(proj_down_op6, 16) &&
+                  GWA_ALIGNED(la_part, 4) && GWA_ALIGNED(s2, 4),
+              "%s: x and proj_down_op6 must be 16-byte, q6 8-byte aligned", what);
+  const int rb = (int)(R / 16);
+  const int64_t S = K / 128, groups = (M + Q6_ROWS - 1) / Q6_ROWS;
+  const int ch = quant_fp6_stages_per_group(M, K, R);
+  const dim3 grid((unsigned)groups, (unsigned)((S + ch - 1) / ch)), block(Q6_THREADS);
+  GWA_REQUIRE(groups < (1ll << 31) && grid.y < 65536u, "%s: grid too large", what);
+  hipStream_t st = (hipStream_t)stream;
+  const uint16_t* xp = (const uint16_t*)x;
+  const uint16_t* sm = (const uint16_t*)smooth;
+  const uint16_t* pd = (const uint16_t*)proj_down_op6;
+  const int m = (int)M, k = (int)K;
+#define GWA_Q6_LAUNCH(RBV, CHV) \
+  hipLaunchKernelGGL((svdq_quant_fp6_kernel<RBV, CHV>), grid, block, 0, st, xp, ldx, sm, s2, pd, q6, la_part, m, k)
+#define GWA_Q6_CH(RBV)                         \
+  if (ch == 4) GWA_Q6_LAUNCH(RBV, 4);          \
+  else if (ch == 2) GWA_Q6_LAUNCH(RBV, 2);     \
+  else GWA_Q6_LAUNCH(RBV, 1);
+  switch (rb) {
+    case 0: GWA_Q6_CH(0) break;
+    case 1: GWA_Q6_CH(1) break;
+    case 2: GWA_Q6_CH(2) break;
+    case 4:  // ch <= 2 here
+      if (ch == 2) GWA_Q6_LAUNCH(4, 2);
+      else GWA_Q6_LAUNCH(4, 1);
+      break;
+    case 8: GWA_Q6_LAUNCH(8, 1); break;  // ch == 1 here
+    default: return gwa_set_error(GWA_ERR_INVALID, "%s: rank %lld", what, (long long)R);
+  }
+#undef GWA_Q6_CH
+#undef GWA_Q6_LAUNCH
+  return gwa_check_launch(what);
+}
+
 extern "C" int gwa_svdq_prep_proj_down(const void* proj_down, void* out, int64_t K, int64_t rank, void* stream) {
   GWA_REQUIRE(K > 0 && K % 64 == 0 && K < (1ll << 24), "svdq_prep_proj_down: bad K=%lld", (long long)K);
   GWA_REQUIRE(rank == 16 || rank == 32 || rank == 64 || rank == 128, "svdq_prep_proj_down: rank %lld not in {16,32,64,128}",
@@ -315,70 +670,49 @@ extern "C" int gwa_svdq_prep_proj_down(const void* proj_down, void* out, int64_t
   return gwa_check_launch("svdq_prep_proj_down");
 }
 
-static int quant_int4(const void* x, int64_t ldx, const void* smooth, const float* s2, const void* proj_down_op,
-                      int64_t rank, int out_format, uint8_t* q, void* scales, void* la, int la_f32_add, int64_t M,
-                      int64_t K, void* stream) {
+extern "C" int gwa_svdq_quant_int4(const void* x, int64_t ldx, const void* smooth, const float* s2,
+                                   const void* proj_down_op, int64_t rank, int out_format, uint8_t* q,
+                                   void* scales, void* la, int64_t M, int64_t K, void* stream) {
   GWA_REQUIRE(M >= 0 && K > 0, "svdq_quant_int4: bad shape M=%lld K=%lld", (long long)M, (long long)K);
   GWA_REQUIRE(K % 64 == 0, "svdq_quant_int4: K=%lld is not a multiple of 64", (long long)K);
   GWA_REQUIRE(ldx >= K && ldx % 8 == 0, "svdq_quant_int4: row stride %lld must be >= K and a multiple of 8",
               (long long)ldx);
-  GWA_REQUIRE(out_format == GWA_QFMT_INT4 || out_format == GWA_QFMT_FP6, "svdq_quant_int4: out_format %d",
-              out_format);
-  GWA_REQUIRE(out_format != GWA_QFMT_FP6 || K % 128 == 0, "svdq_quant_int4: the fp6 format needs K %% 128 == 0 (K=%lld)",
-              (long long)K);
+  GWA_REQUIRE(out_format == GWA_QFMT_INT4,
+              "svdq_quant_int4: out_format %d (fp6 operand records come from gwa_svdq_quant_fp6)", out_format);
   GWA_REQUIRE((proj_down_op == nullptr) == (la == nullptr),
               "svdq_quant_int4: proj_down_op and la must both be given or both be NULL");
   const int64_t R = proj_down_op ? rank : 0;
   GWA_REQUIRE(R == 0 || R == 16 || R == 32 || R == 64 || R == 128,
               "svdq_quant_int4: rank %lld not in {0,16,32,64,128}", (long long)R);
-  GWA_REQUIRE(M < (1ll << 31) && K < (1ll << 24) && (M * ldx * 2) < (1ll << 31) &&
-                  M * (K / 128) * GWA_FP6_REC < (1ll << 31),
+  GWA_REQUIRE(M < (1ll << 31) && K < (1ll << 24) && (M * ldx * 2) < (1ll << 31),
               "svdq_quant_int4: x and q must stay below 2 GiB (buffer addressing)");
   if (M == 0) return GWA_OK;
-  GWA_REQUIRE(x && q && (scales || out_format == GWA_QFMT_FP6), "svdq_quant_int4: null pointer");
-  GWA_REQUIRE(GWA_ALIGNED(x, 16) && GWA_ALIGNED(q, out_format == GWA_QFMT_FP6 ? 8 : 16) && GWA_ALIGNED(scales, 2) && GWA_ALIGNED(smooth, 4) &&
-                  GWA_ALIGNED(proj_down_op, 16) && GWA_ALIGNED(la, la_f32_add ? 4 : 2),
-              "svdq_quant_int4: x and proj_down_op must be 16-byte aligned, q 16 (int4) or 8 (fp6)");
+  GWA_REQUIRE(x && q && scales, "svdq_quant_int4: null pointer");
+  GWA_REQUIRE(GWA_ALIGNED(x, 16) && GWA_ALIGNED(q, 16) && GWA_ALIGNED(scales, 2) && GWA_ALIGNED(smooth, 4) &&
+                  GWA_ALIGNED(proj_down_op, 16) && GWA_ALIGNED(la, 2),
+              "svdq_quant_int4: x, q and proj_down_op must be 16-byte aligned");
   hipStream_t s = (hipStream_t)stream;
   const uint16_t* xp = (const uint16_t*)x;
   const uint16_t* sm = (const uint16_t*)smooth;
   const uint16_t* pd = (const uint16_t*)proj_down_op;
   uint16_t* sc = (uint16_t*)scales;
-  void* lp = la;
+  uint16_t* lp = (uint16_t*)la;
   const int m = (int)M, k = (int)K;
   const int rb = (int)(R / 16);
   const size_t lds = 2 * (size_t)QBUF > (size_t)rb * 8192 ? 2 * (size_t)QBUF : (size_t)rb * 8192;
   const dim3 grid((unsigned)((M + 15) / 16)), block(512);
-  const bool fp6 = out_format == GWA_QFMT_FP6;
-#define GWA_QUANT_LAUNCH(RBV, PFV)                                                                               \
-  if (fp6)                                                                                                       \
-    hipLaunchKernelGGL((svdq_quant_int4_kernel<RBV, GWA_QFMT_FP6, PFV>), grid, block, lds, s, xp, ldx, sm, s2, pd, \
-                       q, sc, lp, la_f32_add, m, k);                                                              \
-  else                                                                                                           \
-    hipLaunchKernelGGL((svdq_quant_int4_kernel<RBV, GWA_QFMT_INT4, PFV>), grid, block, lds, s, xp, ldx, sm, s2,   \
-                       pd, q, sc, lp, la_f32_add, m, k);
+#define GWA_QUANT_LAUNCH(RBV, PFV)                                                                             \
+  hipLaunchKernelGGL((svdq_quant_int4_kernel<RBV, PFV>), grid, block, lds, s, xp, ldx, sm, s2, pd, q, sc, lp, m, k)
   switch (rb) {
-    case 0: GWA_QUANT_LAUNCH(0, 4) break;
-    case 1: GWA_QUANT_LAUNCH(1, 4) break;
-    case 2: GWA_QUANT_LAUNCH(2, 4) break;
-    case 4: GWA_QUANT_LAUNCH(4, 3) break;
-    case 8: GWA_QUANT_LAUNCH(8, 2) break;
+    case 0: GWA_QUANT_LAUNCH(0, 4); break;
+    case 1: GWA_QUANT_LAUNCH(1, 4); break;
+    case 2: GWA_QUANT_LAUNCH(2, 4); break;
+    case 4: GWA_QUANT_LAUNCH(4, 3); break;
+    case 8: GWA_QUANT_LAUNCH(8, 2); break;
     default: return gwa_set_error(GWA_ERR_INVALID, "svdq_quant_int4: rank %lld not in {0,16,32,64,128}", (long long)R);
   }
 #undef GWA_QUANT_LAUNCH
   return gwa_check_launch("svdq_quant_int4");
-}
-
-extern "C" int gwa_svdq_quant_int4(const void* x, int64_t ldx, const void* smooth, const float* s2,
-                                   const void* proj_down_op, int64_t rank, int out_format, uint8_t* q,
-                                   void* scales, void* la, int64_t M, int64_t K, void* stream) {
-  return quant_int4(x, ldx, smooth, s2, proj_down_op, rank, out_format, q, scales, la, 0, M, K, stream);
-}
-
-extern "C" int gwa_svdq_quant_fp6_la_f32(const void* x, int64_t ldx, const void* smooth, const void* proj_down_op,
-                                         int64_t rank, uint8_t* q6, float* la32, int64_t M, int64_t K,
-                                         void* stream) {
-  return quant_int4(x, ldx, smooth, nullptr, proj_down_op, rank, GWA_QFMT_FP6, q6, nullptr, la32, 1, M, K, stream);
 }
 
 extern "C" int gwa_w8a8_quant_int8(const void* x, int64_t ldx, int8_t* q, float* sa, int64_t M, int64_t K,

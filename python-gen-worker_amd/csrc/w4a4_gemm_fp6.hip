@@ -25,8 +25,9 @@
 // next layer's fp6 operand records (smoothing divide, group-64 scales and
 // codes by the same per-lane quantizer as the act-quant kernel, so the
 // records equal the act-quant kernel's on this output bit for bit), and its
-// product with the next layer's proj_down rows n0 .. n0+TN is added into an
-// fp32 [M, r] buffer with atomics (the tiles of a row band sum in any order).
+// product with the next layer's proj_down rows n0 .. n0+TN is stored as the
+// column tile's partial (slot tn of an fp32 [tiles_n][M][r] buffer, which
+// gwa_svdq_la_reduce sums in a fixed order).
 //
 // Tiling: a 512-thread workgroup owns a 256 (n) x 256 (m) output tile; its 8
 // waves form a 4 x 2 grid of 64 (n) x 128 (m) wave tiles (2 x 4 blocks), two
@@ -84,7 +85,10 @@ struct Cfg {
 };
 
 // Direct-to-LDS copy of 16 bytes per lane: LDS [m0 + 16 lane, +16) <- buffer
-// [voff + soff, +16). Issued as asm so the compiler's wait-count pass (which
+// [voff + soff, +16). The hardware range check covers voff only (not the
+// SGPR offset), so callers put the whole offset in voff and mark a lane's
+// chunk that lies past the valid bytes with kOOB there (the lane then reads
+// zeros and touches no memory). Issued as asm so the compiler's wait-count pass (which
 // tracks only a few LDS-DMA writes and then waits for all of them before any
 // LDS read) leaves the waits to the kernel: every LDS read of a stage buffer
 // comes after an s_waitcnt that covers this wave's copies into it and a
@@ -153,21 +157,31 @@ __device__ __forceinline__ v8i buf_operand(rsrc_t r, uint32_t off) {
 }
 
 // The next layer's side of the NQ epilogue: smoothing factors (bf16 [N] or
-// NULL), proj_down in the act-quant kernel's MFMA operand order (or NULL),
-// its rank / 16, the records [N / 128][M][104] and the fp32 la [M, r].
+// NULL), proj_down in the fp6 act-quant kernel's operand order (or NULL),
+// its rank / 16, the records [N / 128][M][104] and the la partial slots
+// [tiles_n][M][r] fp32.
 struct NextLayer {
   const uint16_t* smooth;
   const uint16_t* pdo;
   int rb;
   uint8_t* q6;
-  float* la32;
+  float* la_part;
 };
 constexpr int kNextRbMax = 8;  // next-layer ranks up to 128
+
+// la (bf16 or, with la_f32, fp32) row m, ranks 8 (k0 / 8) .. +8 -> 8 bf16 MFMA operand values
+__device__ __forceinline__ v4i la_operand_lds(const uint8_t* lrb, int row, int rowbytes, int k, bool la_f32) {
+  if (!la_f32) return *(const v4i*)(lrb + row * rowbytes + k * 2);
+  const v4f a = *(const v4f*)(lrb + row * rowbytes + k * 4);
+  const v4f b = *(const v4f*)(lrb + row * rowbytes + k * 4 + 16);
+  return (v4i){(int)pack_bf16x2_rn(a[0], a[1]), (int)pack_bf16x2_rn(a[2], a[3]), (int)pack_bf16x2_rn(b[0], b[1]),
+               (int)pack_bf16x2_rn(b[2], b[3])};
+}
 
 template <int TN, int RB, bool GELU, bool OUT_F16, bool NQ>
 __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_kernel(
     const uint8_t* __restrict__ qa, const uint8_t* __restrict__ qw, const float* __restrict__ s2p,
-    const float* __restrict__ second, int second_per_channel, const uint16_t* __restrict__ la,
+    const float* __restrict__ second, int second_per_channel, const void* __restrict__ la, int la_f32,
     const uint16_t* __restrict__ up, const uint16_t* __restrict__ bias, uint16_t* __restrict__ out, int M, int N,
     int K, NextLayer nx) {
   using C = Cfg<TN>;
@@ -193,10 +207,13 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_kernel(
   // bytes [1024 q', +1024) of the tile's contiguous records (q' = q for the
   // activations, q - DMA_X for the weights). Runs are dealt round-robin; a
   // wave left without a last run repeats the final run (same bytes to the
-  // same place), so every wave issues SLOTS copies per stage. Rows past M / N
-  // read the next stage's records (their outputs are never stored) or
-  // nothing (past the buffer: zeros).
+  // same place), so every wave issues SLOTS copies per stage. A lane's 16
+  // bytes wholly past the tile's rows < M (< N) read zeros; a chunk that
+  // straddles the last real row's end (activations only: N % 16 == 0 keeps
+  // weight runs on 16-byte boundaries) reads up to 8 bytes past it, which in
+  // the last stage is the 16 bytes of slack the activation records carry.
   const uint32_t dvo = 16u * (uint32_t)lane;
+  const uint32_t x_valid = (uint32_t)(M - m0) * REC, w_valid = (uint32_t)(N - n0) * REC;
   auto issue = [&](uint8_t* stage, int st) __attribute__((always_inline)) {
     const uint32_t xs = (uint32_t)(((int64_t)st * M + m0) * REC);
     const uint32_t ws = (uint32_t)(((int64_t)st * N + n0) * REC);
@@ -205,26 +222,30 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_kernel(
       int q = wave + NWAVES * j;
       q = q < C::RUNS ? q : C::RUNS - 1;
       const bool isx = q < C::DMA_X;
-      dma16(isx ? xbuf : wbuf, (uint32_t)(uintptr_t)(stage + q * 1024), dvo,
-            isx ? xs + q * 1024 : ws + (q - C::DMA_X) * 1024);
+      const uint32_t in_run = (uint32_t)((isx ? q : q - C::DMA_X) * 1024) + dvo;
+      const uint32_t voff = in_run < (isx ? x_valid : w_valid) ? (isx ? xs : ws) + in_run : kOOB;
+      dma16(isx ? xbuf : wbuf, (uint32_t)(uintptr_t)(stage + q * 1024), voff, 0u);
     }
   };
 
   // The low-rank operands of ranks up to 32 (la rows m0.., up rows n0..: two
-  // contiguous runs) are copied during the last stage into a stage buffer
-  // that stage no longer uses, as [la | up].
+  // contiguous runs) are copied during the last stage into the two stage
+  // buffers that follow it (neither is read in the last stage), la into the
+  // first, up into the second. The loop's final wait (vmcnt(0)) covers them.
   constexpr bool LR_LDS = RB == 1 || RB == 2;
-  const v4i lbuf4 = raw_rsrc(la, (uint32_t)((int64_t)M * RB * 32));
+  const int la_row = RB * 32 * (la_f32 ? 2 : 1);  // bytes per la row
+  const v4i lbuf4 = raw_rsrc(la, (uint32_t)((int64_t)M * la_row));
   const v4i ubuf4 = raw_rsrc(up, (uint32_t)((int64_t)N * RB * 32));
-  auto issue_lowrank = [&](uint8_t* dst) __attribute__((always_inline)) {
-    constexpr int LA_RUNS = TM * RB * 32 / 1024, UP_RUNS = TN * RB * 32 / 1024;
-    constexpr int RUNS = LA_RUNS + UP_RUNS, PER = (RUNS + NWAVES - 1) / NWAVES;
-#pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      const int q = min(wave + NWAVES * j, RUNS - 1);  // a wave without a last run repeats the final one
-      const bool isl = q < LA_RUNS;
-      dma16(isl ? lbuf4 : ubuf4, (uint32_t)(uintptr_t)(dst + q * 1024), dvo,
-            isl ? (uint32_t)(m0 * RB * 32 + q * 1024) : (uint32_t)(n0 * RB * 32 + (q - LA_RUNS) * 1024));
+  auto issue_lowrank = [&](uint8_t* dla, uint8_t* dup) __attribute__((always_inline)) {
+    const int la_runs = TM * la_row / 1024;
+    constexpr int UP_RUNS = TN * RB * 32 / 1024;
+    for (int q = wave; q < la_runs + UP_RUNS; q += NWAVES) {
+      const bool isl = q < la_runs;
+      const uint32_t in_run = (uint32_t)((isl ? q : q - la_runs) * 1024) + dvo;  // rows past M / N: zeros
+      const uint32_t voff = isl ? (in_run < (uint32_t)((M - m0) * la_row) ? (uint32_t)(m0 * la_row) + in_run : kOOB)
+                                : (in_run < (uint32_t)((N - n0) * RB * 32) ? (uint32_t)(n0 * RB * 32) + in_run : kOOB);
+      dma16(isl ? lbuf4 : ubuf4, (uint32_t)(uintptr_t)(isl ? dla + q * 1024 : dup + (q - la_runs) * 1024), voff,
+            0u);
     }
   };
 
@@ -333,10 +354,11 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_kernel(
   // one stage: prefetch stage st + NBUF - 1 into the buffer read in stage
   // st - 1, compute on this stage's buffer, then make stage st + 1 complete
   // (this wave's copies, then everyone's) before moving on
-  auto stage = [&](int st, const uint8_t* cur, uint8_t* pf, uint8_t* spare) __attribute__((always_inline)) {
+  auto stage = [&](int st, const uint8_t* cur, uint8_t* pf, uint8_t* spare1, uint8_t* spare2)
+      __attribute__((always_inline)) {
     if (st + NBUF - 1 < nst) issue(pf, st + NBUF - 1);
     if constexpr (LR_LDS) {
-      if (st == nst - 1) issue_lowrank(spare);
+      if (st == nst - 1) issue_lowrank(spare1, spare2);
     }
     compute(cur);
     // copies issued after stage st + 1's: stages st + 2 .. min(st + NBUF - 1, nst - 1)
@@ -366,7 +388,9 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_kernel(
   for (int st = 0; st < nst; st += NBUF) {
 #pragma unroll
     for (int u = 0; u < NBUF; ++u)
-      if (st + u < nst) stage(st + u, g_stage[u], g_stage[(u + NBUF - 1) % NBUF], g_stage[(u + 1) % NBUF]);
+      if (st + u < nst)
+        stage(st + u, g_stage[u], g_stage[(u + NBUF - 1) % NBUF], g_stage[(u + 1) % NBUF],
+              g_stage[(u + 2) % NBUF]);
   }
   if constexpr (C::PIPE) {
     fma_half(kLast, 0);
@@ -387,10 +411,9 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_kernel(
     }
   }
   if constexpr (LR_LDS) {
-    // la / up from the spare stage buffer of the last stage ((nst - 1 + 1) % NBUF)
-    const int spare = nst % NBUF;
-    const uint8_t* lrb = &g_stage[0][0] + spare * C::STAGE;
-    const uint8_t* upb = lrb + TM * RB * 32;
+    // la / up from the two stage buffers after the last stage's
+    const uint8_t* lrb = &g_stage[0][0] + (nst % NBUF) * C::STAGE;
+    const uint8_t* upb = &g_stage[0][0] + ((nst + 1) % NBUF) * C::STAGE;
 #pragma unroll
     for (int k0 = 0; k0 < RB; ++k0) {
       v4i ua[WBN], lb[WBM];
@@ -399,7 +422,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_kernel(
         ua[bn] = *(const v4i*)(upb + (32 * (WBN * wn + bn) + r32) * (RB * 32) + k0 * 32 + 16 * h);
 #pragma unroll
       for (int bm = 0; bm < WBM; ++bm)
-        lb[bm] = *(const v4i*)(lrb + (32 * (WBM * wm + bm) + r32) * (RB * 32) + k0 * 32 + 16 * h);
+        lb[bm] = la_operand_lds(lrb, 32 * (WBM * wm + bm) + r32, la_row, k0 * 16 + 8 * h, la_f32);
 #pragma unroll
       for (int bn = 0; bn < WBN; ++bn)
 #pragma unroll
@@ -410,7 +433,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_kernel(
   } else if constexpr (RB > 0) {
     constexpr int RC = 2;
     const rsrc_t ubuf = make_rsrc(up, (uint32_t)((int64_t)N * RB * 32));
-    const rsrc_t lbuf = make_rsrc(la, (uint32_t)((int64_t)M * RB * 32));
+    const rsrc_t lbuf = make_rsrc(la, (uint32_t)((int64_t)M * la_row));
 #pragma unroll
     for (int k0 = 0; k0 < RB; k0 += RC) {
       v4i ua[WBN][RC], lb[WBM][RC];
@@ -423,9 +446,18 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_kernel(
 #pragma unroll
       for (int bm = 0; bm < WBM; ++bm)
 #pragma unroll
-        for (int kk = 0; kk < RC; ++kk)
-          lb[bm][kk] = buf_load16(
-              lbuf, (uint32_t)((int64_t)(m0 + 32 * (WBM * wm + bm) + r32) * (RB * 32) + (k0 + kk) * 32 + 16 * h));
+        for (int kk = 0; kk < RC; ++kk) {
+          const uint32_t row_off = (uint32_t)((int64_t)(m0 + 32 * (WBM * wm + bm) + r32) * la_row);
+          const int k = (k0 + kk) * 16 + 8 * h;
+          if (la_f32) {
+            const v4i a = buf_load16(lbuf, row_off + k * 4), b = buf_load16(lbuf, row_off + k * 4 + 16);
+            const v4f fa = __builtin_bit_cast(v4f, a), fb = __builtin_bit_cast(v4f, b);
+            lb[bm][kk] = (v4i){(int)pack_bf16x2_rn(fa[0], fa[1]), (int)pack_bf16x2_rn(fa[2], fa[3]),
+                               (int)pack_bf16x2_rn(fb[0], fb[1]), (int)pack_bf16x2_rn(fb[2], fb[3])};
+          } else {
+            lb[bm][kk] = buf_load16(lbuf, row_off + k * 2);
+          }
+        }
 #pragma unroll
       for (int bn = 0; bn < WBN; ++bn)
 #pragma unroll
@@ -532,34 +564,39 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_kernel(
       g64::store_fp6(qb, rec, godd, lane, nb, sh, valid);
     }
     // ---- la_next[m0 + rows, :] += tile[rows, :] @ proj_down_next[n0 .. n0 + TN, :]: wave w takes rows
-    // 32w .. 32w + 31 (two 16-row MFMA blocks), the A operand read from the staged tile in MFMA order
+    // 32w .. 32w + 31 (two 16-row MFMA blocks); per 128-column stage, k-step j, lane (r, c) = (lane % 16,
+    // lane / 16) supplies columns 32c + 8j .. +8 of row r, the order gwa_svdq_prep_proj_down_fp6 arranges
+    // proj_down in
     if (nx.pdo != nullptr && nx.rb > 0) {
-      // operand-order rows of the N real columns only (the caller may pass a slice of a longer proj_down)
-      const rsrc_t pb = make_rsrc(nx.pdo, (uint32_t)((int64_t)(N >> 5) * nx.rb * 64 * 16));
+      const rsrc_t pb = make_rsrc(nx.pdo, (uint32_t)((int64_t)(N >> 7) * nx.rb * 4096));
       v4f lacc[2][kNextRbMax];
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int rb = 0; rb < kNextRbMax; ++rb) lacc[i][rb] = (v4f){0.f, 0.f, 0.f, 0.f};
-#pragma unroll 2
-      for (int kc = 0; kc < TN / 32; ++kc) {
-        const int kcg = (n0 >> 5) + kc;
-        if (32 * kcg >= N) break;  // the tile's columns past N (N % 128 == 0: whole 32-column chunks)
-        const uint8_t* ar = ob + (32 * wave + (lane & 15)) * OSTR + kc * 64 + (lane >> 4) * 16;
-        const v4i a0 = *(const v4i*)ar;
-        const v4i a1 = *(const v4i*)(ar + 16 * OSTR);
 #pragma unroll
-        for (int rb = 0; rb < kNextRbMax; ++rb) {
-          if (rb < nx.rb) {
-            const v4i b = buf_load16(pb, (uint32_t)((((int64_t)kcg * nx.rb + rb) * 64 + lane) * 16));
-            lacc[0][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, a0),
-                                                                  __builtin_bit_cast(v8bf, b), lacc[0][rb], 0, 0, 0);
-            lacc[1][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, a1),
-                                                                  __builtin_bit_cast(v8bf, b), lacc[1][rb], 0, 0, 0);
+      for (int ts = 0; ts < TN / 128; ++ts) {
+        const int sg = (n0 >> 7) + ts;
+        if (128 * sg >= N) break;  // the tile's columns past N (N % 128 == 0: whole stages)
+#pragma unroll 2
+        for (int j = 0; j < 4; ++j) {
+          const uint8_t* ar = ob + (32 * wave + (lane & 15)) * OSTR + (128 * ts + 32 * (lane >> 4) + 8 * j) * 2;
+          const v4i a0 = *(const v4i*)ar;
+          const v4i a1 = *(const v4i*)(ar + 16 * OSTR);
+#pragma unroll
+          for (int rb = 0; rb < kNextRbMax; ++rb) {
+            if (rb < nx.rb) {
+              const v4i b = buf_load16(pb, (uint32_t)(((((int64_t)sg * 4 + j) * nx.rb + rb) * 64 + lane) * 16));
+              lacc[0][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, a0),
+                                                                    __builtin_bit_cast(v8bf, b), lacc[0][rb], 0, 0, 0);
+              lacc[1][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, a1),
+                                                                    __builtin_bit_cast(v8bf, b), lacc[1][rb], 0, 0, 0);
+            }
           }
         }
       }
       const int R = nx.rb * 16;
+      float* slot = nx.la_part + (int64_t)tn * M * R;  // this column tile's partial
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -568,7 +605,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_kernel(
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
               const int m = m0 + 32 * wave + 16 * i + 4 * (lane >> 4) + t;
-              if (m < M) unsafeAtomicAdd(nx.la32 + (int64_t)m * R + 16 * rb + (lane & 15), lacc[i][rb][t]);
+              if (m < M) slot[(int64_t)m * R + 16 * rb + (lane & 15)] = lacc[i][rb][t];
             }
           }
         }
@@ -679,7 +716,8 @@ struct Fp6Args {
   const float* s2;
   const float* second;
   int per_channel;
-  const uint16_t* la;
+  const void* la;
+  int la_f32;
   const uint16_t* up;
   const uint16_t* bias;
   uint16_t* out;
@@ -689,7 +727,7 @@ struct Fp6Args {
 template <int TN, int RB, bool GL, bool F16, bool NQ>
 void launch_fp6_tile(dim3 grid, hipStream_t s, const Fp6Args& a, const NextLayer& nx) {
   hipLaunchKernelGGL((w4a4_gemm_fp6_kernel<TN, RB, GL, F16, NQ>), grid, dim3(NTHREADS), 0, s, a.qa6, a.qw6, a.s2,
-                     a.second, a.per_channel, a.la, a.up, a.bias, a.out, a.M, a.N, a.K, nx);
+                     a.second, a.per_channel, a.la, a.la_f32, a.up, a.bias, a.out, a.M, a.N, a.K, nx);
 }
 
 template <int RB, bool GL, bool F16, bool NQ>
@@ -715,6 +753,13 @@ void launch_fp6_flags(bool wide, bool gelu, bool f16, bool nq, dim3 grid, hipStr
   }
 }
 
+// 256 x 256 tiles halve the operand bytes staged per MAC; 256 x 128 tiles keep the software pipeline and
+// give twice the workgroups. The wider tile is taken when it still fills the chip.
+int fp6_tile_n(int64_t M, int64_t N) {
+  const int64_t tiles256 = ((M + TM - 1) / TM) * ((N + 255) / 256);
+  return tiles256 >= 192 ? 256 : 128;
+}
+
 // shared argument checks and launch of both GEMM entry points (nx.q6 != NULL: the NQ epilogue)
 int gemm_fp6(const char* what, const uint8_t* qa6, const uint8_t* qw6, const float* s2, const float* second,
              int64_t second_numel, const void* la, const void* up, int64_t rank, const void* bias, void* out,
@@ -731,11 +776,13 @@ int gemm_fp6(const char* what, const uint8_t* qa6, const uint8_t* qw6, const flo
               (long long)R);
   GWA_REQUIRE(second == nullptr || second_numel == 1 || second_numel == N, "%s: second has %lld values for N=%lld",
               what, (long long)second_numel, (long long)N);
-  GWA_REQUIRE((epilogue_flags & ~GWA_EPI_GELU_TANH) == 0, "%s: unknown epilogue flags 0x%x", what, epilogue_flags);
+  GWA_REQUIRE((epilogue_flags & ~(GWA_EPI_GELU_TANH | GWA_EPI_LA_F32)) == 0, "%s: unknown epilogue flags 0x%x",
+              what, epilogue_flags);
+  const int la_f32 = (epilogue_flags & GWA_EPI_LA_F32) ? 1 : 0;
   const int64_t nst = K / 128;
   // the DMA offsets of a tile's last run stay below 2^31 + 2^16
   GWA_REQUIRE(nst * (M + TM) * REC < (1ll << 31) && nst * (N + 256) * REC < (1ll << 31) && M * N * 2 < (1ll << 31) &&
-                  M * R * 2 < (1ll << 31) && (N / 128) * M * REC < (1ll << 31),
+                  M * R * 4 < (1ll << 31) && (N / 128) * M * REC < (1ll << 31),
               "%s: operands must stay below 2 GiB (buffer addressing)", what);
   if (M == 0) return GWA_OK;
   const bool nq = nx.q6 != nullptr;
@@ -743,16 +790,13 @@ int gemm_fp6(const char* what, const uint8_t* qa6, const uint8_t* qw6, const flo
   GWA_REQUIRE(GWA_ALIGNED(qa6, 16) && GWA_ALIGNED(qw6, 16) && GWA_ALIGNED(la, 16) && GWA_ALIGNED(up, 16) &&
                   GWA_ALIGNED(out, 8) && GWA_ALIGNED(bias, 2) && GWA_ALIGNED(second, 4) && GWA_ALIGNED(s2, 4),
               "%s: misaligned pointer", what);
-  // 256 x 256 tiles halve the operand bytes staged per MAC; 256 x 128 tiles keep the software pipeline
-  // and give twice the workgroups. The wider tile is taken when it still fills the chip.
-  const int64_t tiles256 = ((M + TM - 1) / TM) * ((N + 255) / 256);
-  const bool wide = tiles256 >= 192;
-  const int TNv = wide ? 256 : 128;
+  const int TNv = fp6_tile_n(M, N);
+  const bool wide = TNv == 256;
   const int64_t tiles = ((M + TM - 1) / TM) * ((N + TNv - 1) / TNv);
   GWA_REQUIRE(tiles < (1ll << 30), "%s: too many tiles", what);
   const int64_t per_xcd = (tiles + kXcds - 1) / kXcds;
   const dim3 grid((unsigned)(per_xcd * kXcds));
-  const Fp6Args a{qa6, qw6, s2, second, (int)(second_numel > 1), (const uint16_t*)la, (const uint16_t*)up,
+  const Fp6Args a{qa6, qw6, s2, second, (int)(second_numel > 1), la, la_f32, (const uint16_t*)up,
                   (const uint16_t*)bias, (uint16_t*)out, (int)M, (int)N, (int)K};
   const bool gelu = epilogue_flags & GWA_EPI_GELU_TANH;
   const bool f16 = out_dtype == GWA_DT_F16;
@@ -783,23 +827,29 @@ extern "C" int gwa_svdq_gemm_w4a4_fp6_next(const uint8_t* qa6, const uint8_t* qw
                                            const float* second, int64_t second_numel, const void* la, const void* up,
                                            int64_t rank, const void* bias, void* out, int epilogue_flags,
                                            const void* next_smooth, const void* next_proj_down_op, int64_t next_rank,
-                                           uint8_t* next_q6, float* next_la32, int64_t M, int64_t N, int64_t K,
+                                           uint8_t* next_q6, float* next_la_part, int64_t M, int64_t N, int64_t K,
                                            void* stream) {
   const char* what = "svdq_gemm_w4a4_fp6_next";
   GWA_REQUIRE(N > 0 && N % 128 == 0, "%s: N=%lld is not a multiple of 128 (the next layer's fp6 stages)", what,
               (long long)N);
   GWA_REQUIRE(next_q6 != nullptr, "%s: next_q6 is NULL", what);
-  GWA_REQUIRE((next_proj_down_op == nullptr) == (next_la32 == nullptr),
-              "%s: next_proj_down_op and next_la32 must both be given or both NULL", what);
+  GWA_REQUIRE((next_proj_down_op == nullptr) == (next_la_part == nullptr),
+              "%s: next_proj_down_op and next_la_part must both be given or both NULL", what);
   const int64_t NR = next_proj_down_op ? next_rank : 0;
   GWA_REQUIRE(NR == 0 || NR == 16 || NR == 32 || NR == 64 || NR == 128, "%s: next rank %lld not in {0,16,32,64,128}",
               what, (long long)NR);
   GWA_REQUIRE(M * NR * 4 < (1ll << 40), "%s: shape too large", what);
   GWA_REQUIRE(GWA_ALIGNED(next_smooth, 16) && GWA_ALIGNED(next_proj_down_op, 16) && GWA_ALIGNED(next_q6, 8) &&
-                  GWA_ALIGNED(next_la32, 4),
+                  GWA_ALIGNED(next_la_part, 4),
               "%s: next_smooth and next_proj_down_op must be 16-byte, next_q6 8-byte aligned", what);
   const NextLayer nx{(const uint16_t*)next_smooth, (const uint16_t*)next_proj_down_op, (int)(NR / 16), next_q6,
-                     next_la32};
+                     next_la_part};
   return gemm_fp6(what, qa6, qw6, s2, second, second_numel, la, up, rank, bias, out, GWA_DT_BF16, epilogue_flags, M,
                   N, K, nx, stream);
+}
+
+extern "C" int64_t gwa_svdq_gemm_w4a4_fp6_next_partials(int64_t M, int64_t N) {
+  if (M <= 0 || N <= 0) return 0;
+  const int tn = fp6_tile_n(M, N);
+  return (N + tn - 1) / tn;
 }

@@ -21,6 +21,7 @@ LIB_NAME = "libgen_worker_amd.so"
 
 DT_BF16, DT_F16, DT_F32 = 0, 1, 2
 EPI_GELU_TANH = 1
+EPI_LA_F32 = 2
 QFMT_INT4, QFMT_FP6 = 0, 1
 FP6_REC = 104   # bytes per fp6 operand record (GWA_FP6_REC)
 
@@ -54,13 +55,18 @@ _SIGNATURES: dict[str, tuple] = {
     "gwa_svdq_group_psums_fp6": (_vp, _vp, _vp, _i64, _i64, _i64, _vp),
     "gwa_svdq_gemm_w4a4_fp6_next": (_vp, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _int,
                                     _vp, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _vp),
-    "gwa_svdq_quant_fp6_la_f32": (_vp, _i64, _vp, _vp, _i64, _vp, _vp, _i64, _i64, _vp),
+    "gwa_svdq_quant_fp6": (_vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _i64, _vp),
+    "gwa_svdq_prep_proj_down_fp6": (_vp, _vp, _i64, _i64, _vp),
+    "gwa_svdq_quant_fp6_partials": (_i64, _i64, _i64),
+    "gwa_svdq_gemm_w4a4_fp6_next_partials": (_i64, _i64),
+    "gwa_svdq_la_reduce": (_vp, _i64, _i64, _i64, _vp, _vp),
     "gwa_svdq_epilogue_lora": (_vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _i64, _i64, _vp),
     "gwa_w8a8_quant_int8": (_vp, _i64, _vp, _vp, _i64, _i64, _vp),
     "gwa_w8a8_gemm": (_vp, _vp, _vp, _vp, _vp, _int, _vp, _int, _i64, _i64, _i64, _vp),
     "gwa_transpose_2d": (_vp, _vp, _i64, _i64, _i64, _vp),
 }
-_RESTYPES = {"gwa_build_info": ctypes.c_char_p, "gwa_last_error": ctypes.c_char_p}
+_RESTYPES = {"gwa_build_info": ctypes.c_char_p, "gwa_last_error": ctypes.c_char_p,
+             "gwa_svdq_quant_fp6_partials": ctypes.c_int64, "gwa_svdq_gemm_w4a4_fp6_next_partials": ctypes.c_int64}
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
 

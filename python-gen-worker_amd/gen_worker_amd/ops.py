@@ -20,17 +20,19 @@ separate steps):
   the operand order kernel 1 reads ([ceil(K/256)*256, rank], done once).
 * ``svdq_quant_lora(x2, smooth, s2, proj_down_op) -> (q, s, la)``: kernel 1
   with ``la = x2 @ proj_down`` fused.
-* ``svdq_quant_fp6(x2, smooth, s2, proj_down_op) -> (q6, la)``: the same
-  codes and scales as fp6 operand records [K/128, M, 104] (e3m2 codes + fp16
-  group scales, the fp6 GEMM's operand format; ``la`` empty when
-  ``proj_down_op`` is None).
+* ``svdq_prep_proj_down_fp6(proj_down)`` and ``svdq_quant_fp6(x2, smooth,
+  s2, proj_down_op6) -> (q6, la)``: the same codes and scales as fp6
+  operand records [K/128, M, 104] (e3m2 codes + fp16 group scales, the fp6
+  GEMM's operand format) and the bf16 la ([M, 0] when ``proj_down_op6`` is
+  None); the fp6 GEMM takes la in bf16 or fp32.
 * ``svdq_pack_weight_fp6(weight, wscales)``, ``svdq_w4a4_linear_fp6(qa6,
   weight_fp6, s2, second, la, up, bias, out_dtype, gelu)``,
   ``svdq_group_psums_fp6(qa6, weight_fp6)``: the fp6 GEMM lane.
-* ``svdq_w4a4_linear_fp6_next(...)`` and ``svdq_quant_fp6_accum(...)``: the
-  next layer's activation quantization fused into the GEMM epilogue (fp6
-  records + fp32 la accumulated), for fc1 -> GELU -> fc2 and for a layer
-  whose input concatenates two producers.
+* ``svdq_w4a4_linear_fp6_next(...)``, ``svdq_quant_fp6_into(...)`` and
+  ``svdq_la_reduce(la_part)``: the next layer's activation quantization
+  fused into the GEMM epilogue (fp6 records + fp32 la partial slots, summed
+  in a fixed order), for fc1 -> GELU -> fc2 and for a layer whose input
+  concatenates two producers.
 * ``svdq_w4a4_linear(qa, sa, weight, wscales, s2, second, la, up, bias,
   out_dtype, gelu)``: kernel 2 on the resident ``weight`` [N, K/2] layout.
 * ``svdq_group_psums(qa, qw)``: exact int32 per-group partial sums (debug).
@@ -99,8 +101,8 @@ def _dt_code(dtype: torch.dtype) -> int:
 # kernel 1
 # ---------------------------------------------------------------------------
 
-def _quant_impl(x2: Tensor, smooth: Optional[Tensor], s2: Optional[Tensor], proj_down_op: Optional[Tensor],
-                fmt: int = 0) -> tuple[Tensor, Tensor, Optional[Tensor]]:
+def _quant_impl(x2: Tensor, smooth: Optional[Tensor], s2: Optional[Tensor],
+                proj_down_op: Optional[Tensor]) -> tuple[Tensor, Tensor, Optional[Tensor]]:
     name = "svdq_quant"
     if x2.dim() != 2:
         raise SvdqOpError(f"{name}: x2 must be 2-D, got {tuple(x2.shape)}")
@@ -122,17 +124,12 @@ def _quant_impl(x2: Tensor, smooth: Optional[Tensor], s2: Optional[Tensor], proj
                               f"proj_down), got {tuple(proj_down_op.shape)}")
         rank = int(proj_down_op.shape[1])
     x2 = x2 if x2.stride(1) == 1 else x2.contiguous()
-    if fmt == nat.QFMT_FP6:
-        if k % FP6_STAGE:
-            raise SvdqOpError(f"{name}: the fp6 records need K % {FP6_STAGE} == 0, got K={k}")
-        q = torch.empty(k // FP6_STAGE, m, nat.FP6_REC, dtype=torch.uint8, device=x2.device)
-        s = None   # the records carry the scales
-    else:
-        q = torch.empty(m, k // 2, dtype=torch.uint8, device=x2.device)
-        s = torch.empty(m, k // GROUP, dtype=torch.float16, device=x2.device)
+    q = torch.empty(m, k // 2, dtype=torch.uint8, device=x2.device)
+    s = torch.empty(m, k // GROUP, dtype=torch.float16, device=x2.device)
     la = torch.empty(m, rank, dtype=torch.bfloat16, device=x2.device) if proj_down_op is not None else None
     nat.call("gwa_svdq_quant_int4", nat.ptr(x2), int(x2.stride(0)), nat.ptr(smooth), nat.ptr(s2),
-             nat.ptr(proj_down_op), rank, fmt, nat.ptr(q), nat.ptr(s), nat.ptr(la), m, k, nat.stream_of(x2))
+             nat.ptr(proj_down_op), rank, nat.QFMT_INT4, nat.ptr(q), nat.ptr(s), nat.ptr(la), m, k,
+             nat.stream_of(x2))
     return q, s, la
 
 
@@ -192,22 +189,137 @@ def _(x2, smooth, s2, proj_down_op):
             x2.new_empty(m, r, dtype=torch.bfloat16))
 
 
+RECORD_SLACK = 64  # readable bytes after a record buffer that the fp6 GEMM reads as activations
+
+
+def records_empty(stages: int, rows: int, device) -> Tensor:
+    """An uninitialised fp6 record buffer [stages, rows, 104] whose storage runs 64 bytes past its end: the fp6
+    GEMM's 16-byte operand copies may read up to 8 bytes past the last record (when rows is odd and stages
+    even), so every record buffer it takes as activations is allocated here."""
+    n = stages * rows * nat.FP6_REC
+    return torch.empty(n + RECORD_SLACK, dtype=torch.uint8, device=device)[:n].view(stages, rows, nat.FP6_REC)
+
+
+def la_partials_quant(m: int, k: int, rank: int) -> int:
+    """la partial slots the fp6 act-quant kernel writes for [m, k] at this rank."""
+    return int(nat.load().gwa_svdq_quant_fp6_partials(m, k, rank))
+
+
+def la_partials_next(m: int, n: int) -> int:
+    """la partial slots the next-layer GEMM epilogue writes for m rows and n outputs."""
+    return int(nat.load().gwa_svdq_gemm_w4a4_fp6_next_partials(m, n))
+
+
+def _la_part_check(name: str, la_part: Optional[Tensor], proj_down_op6: Optional[Tensor], m: int, k: int,
+                   slots: int) -> int:
+    """Checks a partial-slot buffer [>= slots, m, rank] and the operand-order proj_down rows for k inputs; returns
+    the rank (0 without a low-rank branch)."""
+    if (proj_down_op6 is None) != (la_part is None):
+        raise SvdqOpError(f"{name}: proj_down_op6 and la_part must both be given or both be None")
+    if proj_down_op6 is None:
+        return 0
+    _check_dtype(name, proj_down_op6, torch.bfloat16, what="proj_down_op6")
+    _check_dtype(name, la_part, torch.float32, what="la_part")
+    if la_part.dim() != 3 or int(la_part.shape[1]) != m or int(la_part.shape[0]) < slots:
+        raise SvdqOpError(f"{name}: la_part must be [>= {slots}, {m}, rank], got {tuple(la_part.shape)}")
+    r = int(la_part.shape[2])
+    if proj_down_op6.dim() != 2 or int(proj_down_op6.shape[1]) != r or int(proj_down_op6.shape[0]) < k:
+        raise SvdqOpError(f"{name}: proj_down_op6 must be [>= {k}, {r}] rows in operand order, got "
+                          f"{tuple(proj_down_op6.shape)}")
+    return r
+
+
+def _fp6_quant_into(name: str, x2: Tensor, smooth: Optional[Tensor], s2: Optional[Tensor],
+                    proj_down_op6: Optional[Tensor], q6: Tensor, la_part: Optional[Tensor]) -> None:
+    """Checks and the launch of the fp6-record act-quant kernel into stages [0, K/128) of ``q6`` and the first
+    partial slots of ``la_part``."""
+    if x2.dim() != 2:
+        raise SvdqOpError(f"{name}: x2 must be 2-D, got {tuple(x2.shape)}")
+    _check_dtype(name, x2, torch.bfloat16, what="x2")
+    _check_dtype(name, smooth, torch.bfloat16, what="smooth")
+    s2 = _scalar_f32(name, s2)
+    _check_cuda(name, x2=x2, smooth=smooth, s2=s2, proj_down_op6=proj_down_op6, q6=q6, la_part=la_part)
+    m, k = int(x2.shape[0]), int(x2.shape[1])
+    if k % FP6_STAGE:
+        raise SvdqOpError(f"{name}: the fp6 records need K % {FP6_STAGE} == 0, got K={k}")
+    if smooth is not None and smooth.numel() != k:
+        raise SvdqOpError(f"{name}: smooth has {smooth.numel()} values for K={k}")
+    q6_addr = _next_records(name, q6, m, k, 0)
+    r = int(la_part.shape[2]) if la_part is not None and la_part.dim() == 3 else 0
+    rank = _la_part_check(name, la_part, proj_down_op6, m, k, la_partials_quant(m, k, r) if r else 0)
+    if x2.stride(1) != 1:
+        x2 = x2.contiguous()
+    nat.call("gwa_svdq_quant_fp6", nat.ptr(x2), int(x2.stride(0)), nat.ptr(smooth), nat.ptr(s2),
+             nat.ptr(proj_down_op6), rank, q6_addr, nat.ptr(la_part), m, k, nat.stream_of(x2))
+
+
+def _la_reduce(la_part: Tensor) -> Tensor:
+    p, m, r = (int(d) for d in la_part.shape)
+    la = torch.empty(m, r, dtype=torch.bfloat16, device=la_part.device)
+    nat.call("gwa_svdq_la_reduce", nat.ptr(la_part), p, m, r, nat.ptr(la), nat.stream_of(la_part))
+    return la
+
+
+@torch.library.custom_op("cozy_gen_worker::svdq_la_reduce", mutates_args=())
+def svdq_la_reduce(la_part: Tensor) -> Tensor:
+    """bf16 la [M, rank] = the fixed-order fp32 sum of the partial slots ``la_part`` [P, M, rank]."""
+    name = "svdq_la_reduce"
+    _check_dtype(name, la_part, torch.float32, what="la_part")
+    _check_cuda(name, la_part=la_part)
+    if la_part.dim() != 3 or int(la_part.shape[0]) < 1 or int(la_part.shape[2]) % 16:
+        raise SvdqOpError(f"{name}: la_part must be [P >= 1, M, rank % 16 == 0], got {tuple(la_part.shape)}")
+    return _la_reduce(la_part)
+
+
+@svdq_la_reduce.register_fake
+def _(la_part):
+    return la_part.new_empty(int(la_part.shape[1]), int(la_part.shape[2]), dtype=torch.bfloat16)
+
+
+@torch.library.custom_op("cozy_gen_worker::svdq_prep_proj_down_fp6", mutates_args=())
+def svdq_prep_proj_down_fp6(proj_down: Tensor) -> Tensor:
+    """proj_down [K, rank] bf16 -> the operand order of the fp6-lane act-quant kernel and of the next-layer
+    epilogue ([K, rank], stage-major; K % 128 == 0). Done once per weight."""
+    name = "svdq_prep_proj_down_fp6"
+    _check_dtype(name, proj_down, torch.bfloat16, what="proj_down")
+    _check_cuda(name, proj_down=proj_down)
+    if proj_down.dim() != 2:
+        raise SvdqOpError(f"{name}: proj_down must be [K, rank], got {tuple(proj_down.shape)}")
+    k, r = int(proj_down.shape[0]), int(proj_down.shape[1])
+    out = torch.empty(k, r, dtype=torch.bfloat16, device=proj_down.device)
+    nat.call("gwa_svdq_prep_proj_down_fp6", nat.ptr(proj_down), nat.ptr(out), k, r, nat.stream_of(proj_down))
+    return out
+
+
+@svdq_prep_proj_down_fp6.register_fake
+def _(proj_down):
+    return proj_down.new_empty(int(proj_down.shape[0]), int(proj_down.shape[1]))
+
+
 @torch.library.custom_op("cozy_gen_worker::svdq_quant_fp6", mutates_args=())
 def svdq_quant_fp6(x2: Tensor, smooth: Optional[Tensor], s2: Optional[Tensor],
-                   proj_down_op: Optional[Tensor]) -> tuple[Tensor, Tensor]:
-    """Kernel 1 writing fp6 operand records [K/128, M, 104] (e3m2 codes + the fp16 group scales: the fp6
-    GEMM's operand format); returns ``(records, la)``, la [M, 0] when ``proj_down_op`` is None."""
-    q, _, la = _quant_impl(x2, smooth, s2, proj_down_op, nat.QFMT_FP6)
-    if la is None:
-        la = x2.new_empty(int(x2.shape[0]), 0)
-    return q, la
+                   proj_down_op6: Optional[Tensor]) -> tuple[Tensor, Tensor]:
+    """Kernel 1 for the fp6 lane: ``(records [K/128, M, 104], la bf16 [M, rank])`` — the codes and group scales
+    as fp6 operand records (e3m2 codes + fp16 scales: the fp6 GEMM's operand format) and ``x2 @ proj_down``
+    (fp32 partial sums over K ranges, reduced in a fixed order, rounded to bf16); la is [M, 0] when
+    ``proj_down_op6`` (``svdq_prep_proj_down_fp6``) is None."""
+    m, k = int(x2.shape[0]), int(x2.shape[-1])
+    q6 = records_empty(k // FP6_STAGE, m, x2.device)
+    r = int(proj_down_op6.shape[1]) if proj_down_op6 is not None else 0
+    if not r:
+        _fp6_quant_into("svdq_quant_fp6", x2, smooth, s2, None, q6, None)
+        return q6, x2.new_empty(m, 0)
+    part = torch.empty(la_partials_quant(m, k, r), m, r, dtype=torch.float32, device=x2.device)
+    _fp6_quant_into("svdq_quant_fp6", x2, smooth, s2, proj_down_op6, q6, part)
+    return q6, _la_reduce(part)
 
 
 @svdq_quant_fp6.register_fake
-def _(x2, smooth, s2, proj_down_op):
+def _(x2, smooth, s2, proj_down_op6):
     m, k = int(x2.shape[0]), int(x2.shape[1])
-    r = int(proj_down_op.shape[1]) if proj_down_op is not None else 0
-    return (x2.new_empty(k // FP6_STAGE, m, nat.FP6_REC, dtype=torch.uint8), x2.new_empty(m, r, dtype=torch.bfloat16))
+    r = int(proj_down_op6.shape[1]) if proj_down_op6 is not None else 0
+    return (x2.new_empty(k // FP6_STAGE, m, nat.FP6_REC, dtype=torch.uint8),
+            x2.new_empty(m, r, dtype=torch.bfloat16))
 
 
 # ---------------------------------------------------------------------------
@@ -284,6 +396,10 @@ def _epilogue_operands(name: str, m: int, n: int, la: Optional[Tensor], up: Opti
     return rank, (0 if second is None else int(second.numel()))
 
 
+def _epi_flags(gelu: bool, la: Optional[Tensor]) -> int:
+    return (nat.EPI_GELU_TANH if gelu else 0) | (nat.EPI_LA_F32 if la is not None and la.dtype == torch.float32 else 0)
+
+
 def _fp6_records_k(name: str, rec: Tensor, what: str) -> tuple[int, int]:
     """(rows, K) of an fp6 operand record tensor [K/128, rows, 104]."""
     if rec.dim() != 3 or int(rec.shape[2]) != nat.FP6_REC:
@@ -301,7 +417,7 @@ def _fp6_impl(qa6: Tensor, weight_fp6: Tensor, s2: Optional[Tensor], second: Opt
         second = second.float().contiguous()
     _check_dtype(name, qa6, torch.uint8, what="qa6")
     _check_dtype(name, weight_fp6, torch.uint8, what="weight_fp6")
-    _check_dtype(name, la, torch.bfloat16, what="la")
+    _check_dtype(name, la, torch.bfloat16, torch.float32, what="la")
     _check_dtype(name, up, torch.bfloat16, what="up")
     _check_dtype(name, bias, torch.bfloat16, what="bias")
     _check_cuda(name, qa6=qa6, weight_fp6=weight_fp6, s2=s2, second=second, la=la, up=up, bias=bias)
@@ -315,7 +431,7 @@ def _fp6_impl(qa6: Tensor, weight_fp6: Tensor, s2: Optional[Tensor], second: Opt
     out = torch.empty(m, n, dtype=out_dtype, device=qa6.device)
     nat.call("gwa_svdq_gemm_w4a4_fp6", nat.ptr(qa6), nat.ptr(weight_fp6.contiguous()), nat.ptr(s2), nat.ptr(second),
              sec_n, nat.ptr(la), nat.ptr(up), rank, nat.ptr(bias), nat.ptr(out), _dt_code(out_dtype),
-             nat.EPI_GELU_TANH if gelu else 0, m, n, k, nat.stream_of(qa6))
+             _epi_flags(gelu, la), m, n, k, nat.stream_of(qa6))
     return out
 
 
@@ -346,46 +462,31 @@ def _next_records(name: str, q6: Tensor, m: int, k: int, stage_offset: int) -> i
     return q6.data_ptr() + stage_offset * m * nat.FP6_REC
 
 
-def _next_lowrank(name: str, proj_down_op: Optional[Tensor], la32: Optional[Tensor], m: int, k: int) -> int:
-    """Checks the next layer's (proj_down_op rows for these k columns, fp32 la accumulator); returns the rank."""
-    if (proj_down_op is None) != (la32 is None):
-        raise SvdqOpError(f"{name}: proj_down_op and la32 must both be given or both be None")
-    if proj_down_op is None:
-        return 0
-    _check_dtype(name, proj_down_op, torch.bfloat16, what="proj_down_op")
-    _check_dtype(name, la32, torch.float32, what="la32")
-    r = int(la32.shape[1]) if la32.dim() == 2 else -1
-    if la32.dim() != 2 or int(la32.shape[0]) != m:
-        raise SvdqOpError(f"{name}: la32 must be [{m}, rank], got {tuple(la32.shape)}")
-    if proj_down_op.dim() != 2 or int(proj_down_op.shape[1]) != r or int(proj_down_op.shape[0]) < k:
-        raise SvdqOpError(f"{name}: proj_down_op must be [>= {k}, {r}] rows in operand order, got "
-                          f"{tuple(proj_down_op.shape)}")
-    return r
-
-
-@torch.library.custom_op("cozy_gen_worker::svdq_w4a4_linear_fp6_next", mutates_args=("next_q6", "next_la32"))
+@torch.library.custom_op("cozy_gen_worker::svdq_w4a4_linear_fp6_next", mutates_args=("next_q6", "next_la_part"))
 def svdq_w4a4_linear_fp6_next(qa6: Tensor, weight_fp6: Tensor, s2: Optional[Tensor], second: Optional[Tensor],
                               la: Optional[Tensor], up: Optional[Tensor], bias: Optional[Tensor], gelu: bool,
                               next_smooth: Optional[Tensor], next_proj_down_op: Optional[Tensor], next_q6: Tensor,
-                              next_la32: Optional[Tensor], stage_offset: int, write_out: bool) -> Tensor:
+                              next_la_part: Optional[Tensor], stage_offset: int, write_out: bool) -> Tensor:
     """W4A4 GEMM whose epilogue also quantizes its bf16 output as the NEXT layer's input: writes that layer's
     fp6 records into stages ``stage_offset ..`` of ``next_q6`` [S, M, 104] (bit-identical to ``svdq_quant_fp6``
-    on the output with ``next_smooth``) and adds ``output @ proj_down_next`` into ``next_la32`` fp32 [M, r]
-    (atomic adds over column tiles). ``next_proj_down_op`` holds the next layer's proj_down rows for these N
-    columns in operand order (a prefix-aligned slice of its ``proj_down_op``). Returns the bf16 output
-    [M, N] when ``write_out``, else an empty [M, 0]."""
+    on the output with ``next_smooth``) and ``output @ proj_down_next`` as one fp32 partial per column tile
+    into the first ``la_partials_next(M, N)`` slots of ``next_la_part`` [P, M, r] (``svdq_la_reduce`` makes the
+    next layer's la). ``next_proj_down_op`` holds the next layer's proj_down rows for these N columns in
+    operand order (a row slice of its ``proj_down_op6``). Returns the bf16 output [M, N] when ``write_out``,
+    else an empty [M, 0]."""
     name = "svdq_w4a4_linear_fp6_next"
     s2 = _scalar_f32(name, s2)
     if second is not None and second.dtype != torch.float32:
         second = second.float().contiguous()
     _check_dtype(name, qa6, torch.uint8, what="qa6")
     _check_dtype(name, weight_fp6, torch.uint8, what="weight_fp6")
-    _check_dtype(name, la, torch.bfloat16, what="la")
+    _check_dtype(name, la, torch.bfloat16, torch.float32, what="la")
     _check_dtype(name, up, torch.bfloat16, what="up")
     _check_dtype(name, bias, torch.bfloat16, what="bias")
     _check_dtype(name, next_smooth, torch.bfloat16, what="next_smooth")
     _check_cuda(name, qa6=qa6, weight_fp6=weight_fp6, s2=s2, second=second, la=la, up=up, bias=bias,
-                next_smooth=next_smooth, next_proj_down_op=next_proj_down_op, next_q6=next_q6, next_la32=next_la32)
+                next_smooth=next_smooth, next_proj_down_op=next_proj_down_op, next_q6=next_q6,
+                next_la_part=next_la_part)
     m, k = _fp6_records_k(name, qa6, "qa6")
     n, kw = _fp6_records_k(name, weight_fp6, "weight_fp6")
     if kw != k:
@@ -396,49 +497,33 @@ def svdq_w4a4_linear_fp6_next(qa6: Tensor, weight_fp6: Tensor, s2: Optional[Tens
         raise SvdqOpError(f"{name}: next_smooth has {next_smooth.numel()} values for N={n}")
     rank, sec_n = _epilogue_operands(name, m, n, la, up, bias, second)
     q6_addr = _next_records(name, next_q6, m, n, stage_offset)
-    nrank = _next_lowrank(name, next_proj_down_op, next_la32, m, n)
+    nrank = _la_part_check(name, next_la_part, next_proj_down_op, m, n, la_partials_next(m, n))
     out = torch.empty(m, n if write_out else 0, dtype=torch.bfloat16, device=qa6.device)
     nat.call("gwa_svdq_gemm_w4a4_fp6_next", nat.ptr(qa6), nat.ptr(weight_fp6), nat.ptr(s2), nat.ptr(second),
              sec_n, nat.ptr(la), nat.ptr(up), rank, nat.ptr(bias), nat.ptr(out) if write_out else None,
-             nat.EPI_GELU_TANH if gelu else 0, nat.ptr(next_smooth), nat.ptr(next_proj_down_op), nrank, q6_addr,
-             nat.ptr(next_la32), m, n, k, nat.stream_of(qa6))
+             _epi_flags(gelu, la), nat.ptr(next_smooth), nat.ptr(next_proj_down_op), nrank, q6_addr,
+             nat.ptr(next_la_part), m, n, k, nat.stream_of(qa6))
     return out
 
 
 @svdq_w4a4_linear_fp6_next.register_fake
-def _(qa6, weight_fp6, s2, second, la, up, bias, gelu, next_smooth, next_proj_down_op, next_q6, next_la32,
+def _(qa6, weight_fp6, s2, second, la, up, bias, gelu, next_smooth, next_proj_down_op, next_q6, next_la_part,
       stage_offset, write_out):
     return qa6.new_empty(int(qa6.shape[1]), int(weight_fp6.shape[1]) if write_out else 0, dtype=torch.bfloat16)
 
 
-@torch.library.custom_op("cozy_gen_worker::svdq_quant_fp6_accum", mutates_args=("q6", "la32"))
-def svdq_quant_fp6_accum(x2: Tensor, smooth: Optional[Tensor], proj_down_op: Optional[Tensor], q6: Tensor,
-                         la32: Optional[Tensor]) -> None:
-    """Kernel 1 into stages [0, K/128) of the record buffer ``q6`` [S, M, 104] with ``la32`` fp32 [M, r]
-    += x2 @ proj_down (``proj_down_op``: the consumer's operand-order proj_down rows for these K columns).
-    With ``svdq_w4a4_linear_fp6_next`` writing the later stages it builds the input of a layer that takes
-    a concatenation [x2, producer output]."""
-    name = "svdq_quant_fp6_accum"
-    if x2.dim() != 2:
-        raise SvdqOpError(f"{name}: x2 must be 2-D, got {tuple(x2.shape)}")
-    _check_dtype(name, x2, torch.bfloat16, what="x2")
-    _check_dtype(name, smooth, torch.bfloat16, what="smooth")
-    _check_cuda(name, x2=x2, smooth=smooth, proj_down_op=proj_down_op, q6=q6, la32=la32)
-    m, k = int(x2.shape[0]), int(x2.shape[1])
-    if k % FP6_STAGE:
-        raise SvdqOpError(f"{name}: the fp6 records need K % {FP6_STAGE} == 0, got K={k}")
-    if smooth is not None and smooth.numel() != k:
-        raise SvdqOpError(f"{name}: smooth has {smooth.numel()} values for K={k}")
-    q6_addr = _next_records(name, q6, m, k, 0)
-    rank = _next_lowrank(name, proj_down_op, la32, m, k)
-    if proj_down_op is not None and int(proj_down_op.shape[0]) < (k + 255) // 256 * 256:
-        raise SvdqOpError(f"{name}: proj_down_op needs {(k + 255) // 256 * 256} rows for K={k}")
-    nat.call("gwa_svdq_quant_fp6_la_f32", nat.ptr(x2), int(x2.stride(0)), nat.ptr(smooth), nat.ptr(proj_down_op),
-             rank, q6_addr, nat.ptr(la32), m, k, nat.stream_of(x2))
+@torch.library.custom_op("cozy_gen_worker::svdq_quant_fp6_into", mutates_args=("q6", "la_part"))
+def svdq_quant_fp6_into(x2: Tensor, smooth: Optional[Tensor], proj_down_op6: Optional[Tensor], q6: Tensor,
+                        la_part: Optional[Tensor]) -> None:
+    """Kernel 1 into stages [0, K/128) of the record buffer ``q6`` [S, M, 104] and the first
+    ``la_partials_quant(M, K, rank)`` slots of ``la_part`` [P, M, rank] (``proj_down_op6``: the consumer's
+    operand-order proj_down rows for these K columns). With ``svdq_w4a4_linear_fp6_next`` writing the later
+    stages and slots it builds the input of a layer that takes a concatenation [x2, producer output]."""
+    _fp6_quant_into("svdq_quant_fp6_into", x2, smooth, None, proj_down_op6, q6, la_part)
 
 
-@svdq_quant_fp6_accum.register_fake
-def _(x2, smooth, proj_down_op, q6, la32):
+@svdq_quant_fp6_into.register_fake
+def _(x2, smooth, proj_down_op6, q6, la_part):
     return None
 
 

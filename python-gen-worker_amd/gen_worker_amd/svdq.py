@@ -30,7 +30,7 @@ import torch
 import torch.nn as nn
 from torch import Tensor
 
-from . import _native, ops
+from . import ops
 
 GROUP = 64
 _N_ALIGN = 16
@@ -158,10 +158,12 @@ class SvdqW4A4Linear(nn.Module):
         if self.rank:
             self.register_buffer("proj_down", torch.empty(in_features, self.rank, dtype=compute_dtype, device=dev))
             self.register_buffer("proj_up", torch.empty(out_features, self.rank, dtype=compute_dtype, device=dev))
-            # proj_down in kernel 1's operand order (derived by refresh_derived, GPU only)
+            # proj_down in the act-quant kernels' operand orders (derived by refresh_derived, GPU only):
+            # the general lane's and the fp6 lane's
             self.register_buffer("proj_down_op", None, persistent=False)
+            self.register_buffer("proj_down_op6", None, persistent=False)
         else:
-            self.proj_down = self.proj_up = self.proj_down_op = None
+            self.proj_down = self.proj_up = self.proj_down_op = self.proj_down_op6 = None
         if bias:
             self.bias: Optional[nn.Parameter] = nn.Parameter(
                 torch.empty(out_features, dtype=compute_dtype, device=dev), requires_grad=False)
@@ -175,11 +177,14 @@ class SvdqW4A4Linear(nn.Module):
         """Recompute the derived buffers after ``weight`` / ``proj_down`` change (GPU only): ``proj_down``
         in kernel 1's operand order, and the weights as fp6 operand records (``in_features % 128 == 0``;
         other shapes keep the general int8 path)."""
+        fp6 = self.weight.is_cuda and self.in_features % ops.FP6_STAGE == 0
         if self.rank:
-            self.proj_down_op = (torch.ops.cozy_gen_worker.svdq_prep_proj_down(self.proj_down)
-                                 if self.proj_down.is_cuda else None)
+            on_gpu = self.proj_down.is_cuda
+            self.proj_down_op = torch.ops.cozy_gen_worker.svdq_prep_proj_down(self.proj_down) if on_gpu else None
+            self.proj_down_op6 = (torch.ops.cozy_gen_worker.svdq_prep_proj_down_fp6(self.proj_down)
+                                  if on_gpu and fp6 else None)
         self.weight_fp6 = None
-        if self.weight.is_cuda and self.in_features % ops.FP6_STAGE == 0:
+        if fp6:
             self.weight_fp6 = torch.ops.cozy_gen_worker.svdq_pack_weight_fp6(self.weight, self.weight_scale)
 
     def _load_from_state_dict(self, *args: Any, **kwargs: Any) -> None:  # noqa: D401
@@ -194,8 +199,9 @@ class SvdqW4A4Linear(nn.Module):
         return "fp6" if self.weight_fp6 is not None else "general"
 
     def _ensure_derived(self) -> None:
-        if (self.rank and self.proj_down_op is None) or (self.weight_fp6 is None and self.weight.is_cuda
-                                                         and self.in_features % ops.FP6_STAGE == 0):
+        fp6 = self.weight.is_cuda and self.in_features % ops.FP6_STAGE == 0
+        if ((self.rank and (self.proj_down_op is None or (fp6 and self.proj_down_op6 is None)))
+                or (self.weight_fp6 is None and fp6)):
             self.refresh_derived()
 
     def _input2d(self, x: Tensor) -> Tensor:
@@ -205,8 +211,8 @@ class SvdqW4A4Linear(nn.Module):
         return x2.contiguous()
 
     def forward_records(self, q6: Tensor, la: Optional[Tensor], out_dtype: Optional[torch.dtype] = None) -> Tensor:
-        """The fp6-lane GEMM on ready input records [K/128, M, 104] and la bf16 [M, rank] (e.g. written by the
-        previous layer's fused epilogue); returns [M, out_features]."""
+        """The fp6-lane GEMM on ready input records [K/128, M, 104] and la [M, rank] (bf16, or fp32); returns
+        [M, out_features]."""
         self._ensure_derived()
         if self.weight_fp6 is None:
             raise SvdqFusedError("forward_records needs the fp6 lane (in_features % 128 == 0, weights on the GPU)")
@@ -221,7 +227,7 @@ class SvdqW4A4Linear(nn.Module):
         self._ensure_derived()
         gelu = self.activation == "gelu_tanh"
         if self.weight_fp6 is not None:
-            qa6, la = torch.ops.cozy_gen_worker.svdq_quant_fp6(x2, self.smooth_factor, None, self.proj_down_op)
+            qa6, la = torch.ops.cozy_gen_worker.svdq_quant_fp6(x2, self.smooth_factor, None, self.proj_down_op6)
             y = torch.ops.cozy_gen_worker.svdq_w4a4_linear_fp6(
                 qa6, self.weight_fp6, None, self.second, la if self.rank else None, self.proj_up, self.bias,
                 out_dtype, gelu)
@@ -253,41 +259,44 @@ def _fusable(producer: SvdqW4A4Linear, consumer: SvdqW4A4Linear, k_offset: int) 
 def _next_operands(consumer: SvdqW4A4Linear, k0: int, k1: int) -> tuple[Optional[Tensor], Optional[Tensor]]:
     """The consumer's smoothing factors and operand-order proj_down rows for its input columns [k0, k1)."""
     sm = consumer.smooth_factor[k0:k1] if consumer.smooth_factor is not None else None
-    pdo = consumer.proj_down_op[k0:] if consumer.rank else None
+    pdo = consumer.proj_down_op6[k0:k1] if consumer.rank else None
     return sm, pdo
 
 
 def svdq_pair_forward(x: Tensor, first: SvdqW4A4Linear, second: SvdqW4A4Linear) -> Tensor:
     """``second(first(x))`` with ``second``'s activation quantization fused into ``first``'s GEMM epilogue
     (config 2: fc1 -> GELU -> fc2). The [M, first.out_features] bf16 intermediate never reaches HBM: the
-    epilogue writes ``second``'s fp6 records (bit-identical to quantizing the bf16 output) and adds
-    ``output @ second.proj_down`` into an fp32 buffer, rounded to bf16 for ``second``'s la. Layers that do not
-    meet the fused contract (both fp6 lane, first.out_features % 128 == 0, bf16 intermediate) run unfused."""
+    epilogue writes ``second``'s fp6 records (bit-identical to quantizing the bf16 output) and per-column-tile
+    partials of ``output @ second.proj_down``, summed in a fixed order into ``second``'s bf16 la. Layers that do
+    not meet the fused contract (both fp6 lane, first.out_features % 128 == 0, bf16 intermediate) run unfused."""
     if not _fusable(first, second, 0):
         return second(first(x))
+    cg = torch.ops.cozy_gen_worker
     shape = x.shape
     x2 = first._input2d(x)
     m = int(x2.shape[0])
-    q6, la = torch.ops.cozy_gen_worker.svdq_quant_fp6(x2, first.smooth_factor, None, first.proj_down_op)
-    q6n = torch.empty(second.in_features // ops.FP6_STAGE, m, _native.FP6_REC, dtype=torch.uint8, device=x2.device)
-    la32 = torch.zeros(m, second.rank, dtype=torch.float32, device=x2.device) if second.rank else None
+    q6, la = cg.svdq_quant_fp6(x2, first.smooth_factor, None, first.proj_down_op6)
+    q6n = ops.records_empty(second.in_features // ops.FP6_STAGE, m, x2.device)
+    part = (torch.empty(ops.la_partials_next(m, first.out_features), m, second.rank, dtype=torch.float32,
+                        device=x2.device) if second.rank else None)
     sm, pdo = _next_operands(second, 0, second.in_features)
-    torch.ops.cozy_gen_worker.svdq_w4a4_linear_fp6_next(
-        q6, first.weight_fp6, None, first.second, la if first.rank else None, first.proj_up, first.bias,
-        first.activation == "gelu_tanh", sm, pdo, q6n, la32, 0, False)
-    y = second.forward_records(q6n, la32.to(torch.bfloat16) if la32 is not None else None)
+    cg.svdq_w4a4_linear_fp6_next(q6, first.weight_fp6, None, first.second, la if first.rank else None,
+                                 first.proj_up, first.bias, first.activation == "gelu_tanh", sm, pdo, q6n, part, 0,
+                                 False)
+    y = second.forward_records(q6n, cg.svdq_la_reduce(part) if part is not None else None)
     return y.reshape(*shape[:-1], second.out_features)
 
 
 def svdq_concat_forward(consumer: SvdqW4A4Linear, x_a: Tensor, producer: SvdqW4A4Linear, x_b: Tensor) -> Tensor:
     """``consumer(cat([x_a, producer(x_b)], -1))`` (Flux's single-block proj_out over [attention, MLP]) without
     the concatenation: kernel 1 writes the first x_a.shape[-1] / 128 stages of ``consumer``'s input records
-    from ``x_a``, ``producer``'s fused epilogue writes the rest, and both add their part of the input @
-    proj_down into one fp32 buffer. Falls back to the unfused composition outside the fused contract
-    (x_a's width a multiple of 128, both fp6 lane)."""
+    from ``x_a``, ``producer``'s fused epilogue writes the rest, and both store their partials of the input @
+    proj_down into one slot buffer, summed in a fixed order into ``consumer``'s la. Falls back to the unfused
+    composition outside the fused contract (x_a's width a multiple of 128, both fp6 lane)."""
     ka = int(x_a.shape[-1])
     if not _fusable(producer, consumer, ka):
         return consumer(torch.cat((x_a, producer(x_b)), dim=-1))
+    cg = torch.ops.cozy_gen_worker
     shape = x_a.shape
     xa2 = x_a.reshape(-1, ka)
     if xa2.dtype != torch.bfloat16:
@@ -297,17 +306,21 @@ def svdq_concat_forward(consumer: SvdqW4A4Linear, x_a: Tensor, producer: SvdqW4A
     m = int(xa2.shape[0])
     if int(xb2.shape[0]) != m:
         raise SvdqFusedError(f"svdq_concat_forward: {m} rows in x_a, {int(xb2.shape[0])} in x_b")
-    q6n = torch.empty(consumer.in_features // ops.FP6_STAGE, m, _native.FP6_REC, dtype=torch.uint8,
-                      device=xa2.device)
-    la32 = torch.zeros(m, consumer.rank, dtype=torch.float32, device=xa2.device) if consumer.rank else None
+    q6n = ops.records_empty(consumer.in_features // ops.FP6_STAGE, m, xa2.device)
+    part = None
+    pa = 0
+    if consumer.rank:
+        pa = ops.la_partials_quant(m, ka, consumer.rank)
+        pb = ops.la_partials_next(m, producer.out_features)
+        part = torch.empty(pa + pb, m, consumer.rank, dtype=torch.float32, device=xa2.device)
     sm_a, pdo_a = _next_operands(consumer, 0, ka)
-    torch.ops.cozy_gen_worker.svdq_quant_fp6_accum(xa2, sm_a, pdo_a, q6n, la32)
-    q6, la = torch.ops.cozy_gen_worker.svdq_quant_fp6(xb2, producer.smooth_factor, None, producer.proj_down_op)
+    cg.svdq_quant_fp6_into(xa2, sm_a, pdo_a, q6n, part)
+    q6, la = cg.svdq_quant_fp6(xb2, producer.smooth_factor, None, producer.proj_down_op6)
     sm_b, pdo_b = _next_operands(consumer, ka, consumer.in_features)
-    torch.ops.cozy_gen_worker.svdq_w4a4_linear_fp6_next(
-        q6, producer.weight_fp6, None, producer.second, la if producer.rank else None, producer.proj_up,
-        producer.bias, producer.activation == "gelu_tanh", sm_b, pdo_b, q6n, la32, ka // ops.FP6_STAGE, False)
-    y = consumer.forward_records(q6n, la32.to(torch.bfloat16) if la32 is not None else None)
+    cg.svdq_w4a4_linear_fp6_next(q6, producer.weight_fp6, None, producer.second, la if producer.rank else None,
+                                 producer.proj_up, producer.bias, producer.activation == "gelu_tanh", sm_b, pdo_b,
+                                 q6n, part[pa:] if part is not None else None, ka // ops.FP6_STAGE, False)
+    y = consumer.forward_records(q6n, cg.svdq_la_reduce(part) if part is not None else None)
     return y.reshape(*shape[:-1], consumer.out_features)
 
 
@@ -376,9 +389,9 @@ def w4a4_int_ops(m: int, n: int, k: int) -> int:
 
 def act_quant_bytes(m: int, k: int, rank: int, smooth: bool = True, fp6: bool = False) -> int:
     """Minimal HBM bytes of kernel 1: x, smooth, L1, codes + scales (int4 + fp16, or the fp6 operand
-    records: 104 bytes per 128 columns), la."""
+    records: 104 bytes per 128 columns), la (bf16, or fp32 in the fp6 lane)."""
     out = m * (k // ops.FP6_STAGE) * 104 if fp6 else m * k // 2 + m * (k // GROUP) * 2
-    return m * k * 2 + (k * 2 if smooth else 0) + k * rank * 2 + out + m * rank * 2
+    return m * k * 2 + (k * 2 if smooth else 0) + k * rank * 2 + out + m * rank * (4 if fp6 else 2)
 
 
 __all__ = [

@@ -1,7 +1,8 @@
 """GPU parity of the next-layer fusion (config 2's fc1 -> GELU -> fc2 and a
 layer whose input concatenates two producers): the GEMM epilogue that writes
-the next layer's fp6 records and fp32 low-rank partials, kernel 1's fp32
-accumulate mode, and the module helpers built on them.
+the next layer's fp6 records and fp32 low-rank partial slots, kernel 1 into
+larger record / slot buffers, the fixed-order la reduction, and the module
+helpers built on them.
 
 Records must equal the act-quant kernel's on the unfused bf16 output byte
 for byte (codes and scales also against the oracle's quantizer); the fp32
@@ -18,6 +19,8 @@ import torch
 
 from helpers import bits16, check_output, decode_fp6_records
 from oracle import svdq_oracle as O
+
+from gen_worker_amd.ops import la_partials_next, la_partials_quant, records_empty
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -51,7 +54,7 @@ def _ops():
 
 
 def _prep(down):
-    return _ops().svdq_prep_proj_down(down.to(DEV)) if down is not None else None
+    return _ops().svdq_prep_proj_down_fp6(down.to(DEV)) if down is not None else None
 
 
 def _dev(t):
@@ -98,13 +101,13 @@ def test_next_epilogue_matches_unfused(m, k, n, r1, r2, sm2, gelu):
     y = ops.svdq_w4a4_linear_fp6(q6, w6, None, None, la, _dev(L1.proj_up), _dev(L1.bias), torch.bfloat16, gelu)
     pdo2 = _prep(L2.proj_down)
     qn_ref, _ = ops.svdq_quant_fp6(y, _dev(L2.smooth), None, pdo2)
-    # fused, into stages 2 .. 2 + n/128 of a larger buffer; la32 pre-filled (the epilogue adds)
+    # fused, into stages 2 .. 2 + n/128 of a larger buffer and the first slots of a larger partial buffer
     s = n // 128
-    qn = torch.full((s + 3, m, 104), 0xAB, dtype=torch.uint8, device=DEV)
-    la32 = torch.randn(m, r2, device=DEV) if r2 else None
-    la0 = la32.clone() if r2 else None
+    qn = records_empty(s + 3, m, DEV).fill_(0xAB)
+    npart = la_partials_next(m, n)
+    part = torch.full((npart + 1, m, r2), 7.0, device=DEV) if r2 else None
     out = ops.svdq_w4a4_linear_fp6_next(q6, w6, None, None, la, _dev(L1.proj_up), _dev(L1.bias), gelu,
-                                        _dev(L2.smooth), pdo2, qn, la32, 2, True)
+                                        _dev(L2.smooth), pdo2, qn, part, 2, True)
     torch.cuda.synchronize()
     assert torch.equal(out, y)
     assert torch.equal(qn[2:2 + s, :, :REC_BYTES], qn_ref[:, :, :REC_BYTES])
@@ -112,41 +115,58 @@ def test_next_epilogue_matches_unfused(m, k, n, r1, r2, sm2, gelu):
     y_bits = bits16(y.cpu())
     _check_records(qn[2:2 + s].cpu().numpy(), y_bits, bits16(L2.smooth) if sm2 else None)
     if r2:
+        assert bool((part[npart] == 7.0).all())  # slots past this producer's are untouched
         d_bits = bits16(L2.proj_down)
         ref = O.lowrank_down(y_bits, d_bits)
-        got = (la32 - la0).double().cpu().numpy()
-        assert np.all(np.abs(got - ref) <= _lowrank_tol(y_bits, d_bits) + 1e-6 * np.abs(la0.cpu().numpy())), \
-            float(np.max(np.abs(got - ref)))
+        got = part[:npart].double().sum(0).cpu().numpy()
+        assert np.all(np.abs(got - ref) <= _lowrank_tol(y_bits, d_bits)), float(np.max(np.abs(got - ref)))
+        la_n = ops.svdq_la_reduce(part[:npart])
+        assert la_n.dtype == torch.bfloat16 and la_n.shape == (m, r2)
+        assert torch.equal(la_n, part[:npart].sum(0).to(torch.bfloat16)) or \
+            float((la_n.float() - torch.from_numpy(ref).float().to(DEV)).abs().max()) <= \
+            float(2.0 ** -7 * np.abs(ref).max() + 1e-6)
+        # deterministic: a second run gives the same partials bit for bit
+        part2 = torch.empty_like(part[:npart])
+        ops.svdq_w4a4_linear_fp6_next(q6, w6, None, None, la, _dev(L1.proj_up), _dev(L1.bias), gelu,
+                                      _dev(L2.smooth), pdo2, records_empty(s, m, DEV), part2, 0, False)
+        assert torch.equal(part2, part[:npart])
     # without the bf16 output: the same records
-    qn2 = torch.empty(s, m, 104, dtype=torch.uint8, device=DEV)
-    la2 = torch.zeros(m, r2, device=DEV) if r2 else None
+    qn2 = records_empty(s, m, DEV)
+    part3 = torch.empty(npart, m, r2, device=DEV) if r2 else None
     none = ops.svdq_w4a4_linear_fp6_next(q6, w6, None, None, la, _dev(L1.proj_up), _dev(L1.bias), gelu,
-                                         _dev(L2.smooth), pdo2, qn2, la2, 0, False)
+                                         _dev(L2.smooth), pdo2, qn2, part3, 0, False)
     torch.cuda.synchronize()
     assert none.shape == (m, 0)
     assert torch.equal(qn2[:, :, :REC_BYTES], qn_ref[:, :, :REC_BYTES])
 
 
-@pytest.mark.parametrize("m,k,rank", [(77, 384, 32), (256, 3072, 32), (5, 128, 128), (300, 1024, 0)])
-def test_quant_fp6_accum(m, k, rank):
+@pytest.mark.parametrize("m,k,rank", [(77, 384, 32), (256, 3072, 32), (5, 128, 128), (300, 1024, 0),
+                                      (4608, 15360, 32), (64, 12288, 64)])
+def test_quant_fp6_into(m, k, rank):
+    """Kernel 1 into the head of larger record / partial buffers: the same records as svdq_quant_fp6, partial
+    slots that sum to x @ proj_down, the same bf16 la through svdq_la_reduce, bit for bit on a second run."""
     ops = _ops()
     L = _layer(64, k, rank, so=k)
     x = _act(m, k, seed=k)
     pdo = _prep(L.proj_down)
-    q_ref, _ = ops.svdq_quant_fp6(x, _dev(L.smooth), None, pdo)
+    q_ref, la_ref = ops.svdq_quant_fp6(x, _dev(L.smooth), None, pdo)
     s = k // 128
-    q6 = torch.full((s + 2, m, 104), 0x5A, dtype=torch.uint8, device=DEV)
-    la32 = torch.randn(m, rank, device=DEV) if rank else None
-    la0 = la32.clone() if rank else None
-    ops.svdq_quant_fp6_accum(x, _dev(L.smooth), pdo, q6, la32)
+    q6 = records_empty(s + 2, m, DEV).fill_(0x5A)
+    npart = la_partials_quant(m, k, rank) if rank else 0
+    part = torch.full((npart + 1, m, rank), 3.0, device=DEV) if rank else None
+    ops.svdq_quant_fp6_into(x, _dev(L.smooth), pdo, q6, part)
     torch.cuda.synchronize()
     assert torch.equal(q6[:s, :, :REC_BYTES], q_ref[:, :, :REC_BYTES])
     assert bool((q6[s:] == 0x5A).all())
     if rank:
+        assert bool((part[npart] == 3.0).all())
         x_bits, d_bits = bits16(x.cpu()), bits16(L.proj_down)
         ref = O.lowrank_down(x_bits, d_bits)
-        got = (la32 - la0).double().cpu().numpy()
-        assert np.all(np.abs(got - ref) <= _lowrank_tol(x_bits, d_bits) + 1e-6 * np.abs(la0.cpu().numpy()))
+        got = part[:npart].double().sum(0).cpu().numpy()
+        assert np.all(np.abs(got - ref) <= _lowrank_tol(x_bits, d_bits))
+        assert torch.equal(ops.svdq_la_reduce(part[:npart]), la_ref)
+        q2, la2 = ops.svdq_quant_fp6(x, _dev(L.smooth), None, pdo)
+        assert torch.equal(la2, la_ref) and torch.equal(q2[:, :, :REC_BYTES], q_ref[:, :, :REC_BYTES])
 
 
 def _module(L, activation=None):
@@ -177,8 +197,11 @@ def test_pair_forward(m, d, h, rank):
     y_unfused = fc2(y1)
     torch.cuda.synchronize()
     assert y.shape == (m, d)
+    # the same records; fc2's la sums the same products grouped by fc1's column tiles instead of kernel 1's
+    # K ranges, so its bf16 value may differ in the last bit
     diff = (y.float() - y_unfused.float()).abs()
     assert float(diff.max()) <= 2.0 ** -6 * float(y_unfused.float().abs().max())
+    assert torch.equal(svdq_pair_forward(x, fc1, fc2), y)   # deterministic
     ref = _oracle(bits16(y1.cpu()), L2)
     check_output(y, ref, what=f"pair {m}x{d}x{h}")
 
@@ -197,6 +220,8 @@ def test_concat_forward(m, ka, d, h, n, rank):
     y_unfused = cons(torch.cat((a, yb), dim=-1))
     torch.cuda.synchronize()
     assert y.shape == (m, n)
+    # the same records; la's fp32 partials are grouped differently (K split at the concatenation), so the
+    # bf16 la may differ in its last bit
     diff = (y.float() - y_unfused.float()).abs()
     assert float(diff.max()) <= 2.0 ** -6 * float(y_unfused.float().abs().max())
     ref = _oracle(np.concatenate((bits16(a.cpu()), bits16(yb.cpu())), axis=1), Lc)

@@ -74,7 +74,7 @@ def _run_quant(x_bits, smooth_bits, down_bits, s2=None, fmt="int4"):
     sm = _dev16(smooth_bits) if smooth_bits is not None else None
     s2t = torch.tensor(s2, dtype=torch.float32, device=DEV) if s2 is not None else None
     if fmt == "fp6":
-        pdo = torch.ops.cozy_gen_worker.svdq_prep_proj_down(_dev16(down_bits)) if down_bits is not None else None
+        pdo = torch.ops.cozy_gen_worker.svdq_prep_proj_down_fp6(_dev16(down_bits)) if down_bits is not None else None
         q6, la = torch.ops.cozy_gen_worker.svdq_quant_fp6(x, sm, s2t, pdo)
         torch.cuda.synchronize()
         codes, sbits = decode_fp6_records(q6.cpu().numpy())
@@ -231,7 +231,7 @@ def _w4a4_case(m, n, k, rank, seed, smooth=True, bias=True, second=None, gelu=Fa
     smd = _dev16(sm) if sm is not None else None
     s2t = torch.tensor(s2, dtype=torch.float32, device=DEV) if s2 is not None else None
     if fp6:
-        pdo = torch.ops.cozy_gen_worker.svdq_prep_proj_down(_dev16(down)) if rank else None
+        pdo = torch.ops.cozy_gen_worker.svdq_prep_proj_down_fp6(_dev16(down)) if rank else None
         qa, la = torch.ops.cozy_gen_worker.svdq_quant_fp6(xd, smd, s2t, pdo)
         upd = _dev16(up) if rank else None
         if not rank:

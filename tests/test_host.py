@@ -52,7 +52,19 @@ def test_invalid_arguments_are_refused_before_any_launch():
     rc = lib.gwa_svdq_quant_int4(None, 64, None, None, None, 0, 7, None, None, None, 4, 64, None)
     assert rc == 1 and "out_format" in lib.gwa_last_error().decode()
     rc = lib.gwa_svdq_quant_int4(None, 192, None, None, None, 0, 1, None, None, None, 4, 192, None)
-    assert rc == 1 and "128" in lib.gwa_last_error().decode()
+    assert rc == 1 and "gwa_svdq_quant_fp6" in lib.gwa_last_error().decode()
+    rc = lib.gwa_svdq_quant_fp6(None, 192, None, None, None, 0, None, None, 4, 192, None)
+    assert rc == 1 and "multiple of 128" in lib.gwa_last_error().decode()
+    rc = lib.gwa_svdq_prep_proj_down_fp6(None, None, 192, 32, None)
+    assert rc == 1 and "multiple of 128" in lib.gwa_last_error().decode()
+    rc = lib.gwa_svdq_la_reduce(None, 0, 4, 32, None, None)
+    assert rc == 1 and "bad shape" in lib.gwa_last_error().decode()
+    # partial-slot counts: kernel 1 splits K=3072 of 4608 rows over 6 ranges; the 256-wide GEMM tiles of
+    # N = 12288 give 48 column tiles, the 128-wide tiles of a small M twice as many per N
+    assert lib.gwa_svdq_quant_fp6_partials(4608, 3072, 32) == 6
+    assert lib.gwa_svdq_gemm_w4a4_fp6_next_partials(4608, 12288) == 48
+    assert lib.gwa_svdq_gemm_w4a4_fp6_next_partials(256, 3072) == 24
+    assert lib.gwa_svdq_quant_fp6_partials(4608, 3072, 0) == 0
     rc = lib.gwa_svdq_gemm_w4a4_fp6(None, None, None, None, 0, None, None, 0, None, None, 0, 0, 8, 64, 192, None)
     assert rc == 1 and "multiple of 128" in lib.gwa_last_error().decode()
     # the next-layer epilogue needs whole 128-column stages and a record buffer
@@ -62,8 +74,6 @@ def test_invalid_arguments_are_refused_before_any_launch():
     rc = lib.gwa_svdq_gemm_w4a4_fp6_next(None, None, None, None, 0, None, None, 0, None, None, 0, None, None, 0,
                                          None, None, 8, 256, 128, None)
     assert rc == 1 and "next_q6" in lib.gwa_last_error().decode()
-    rc = lib.gwa_svdq_quant_fp6_la_f32(None, 192, None, None, 0, None, None, 4, 192, None)
-    assert rc == 1 and "128" in lib.gwa_last_error().decode()
     rc = lib.gwa_svdq_prep_proj_down(None, None, 64, 24, None)
     assert rc == 1 and "rank" in lib.gwa_last_error().decode()
     rc = lib.gwa_svdq_gemm_w4a4(None, None, None, None, None, None, 0, None, None, 0, None, None, 0, 0,
@@ -109,6 +119,9 @@ def test_fake_impls_trace_shapes():
         q, s, la = torch.ops.cozy_gen_worker.svdq_quant_lora(x, None, None, pdo)
         q6, la6 = torch.ops.cozy_gen_worker.svdq_quant_fp6(x, None, None, None)
         assert q6.shape == (3, 77, 104) and la6.shape == (77, 0)
+        pdo6 = torch.ops.cozy_gen_worker.svdq_prep_proj_down_fp6(torch.empty(384, 32, dtype=torch.bfloat16))
+        q6b, la6b = torch.ops.cozy_gen_worker.svdq_quant_fp6(x, None, None, pdo6)
+        assert pdo6.shape == (384, 32) and la6b.shape == (77, 32) and la6b.dtype == torch.bfloat16
         w6 = torch.ops.cozy_gen_worker.svdq_pack_weight_fp6(torch.empty(128, 192, dtype=torch.uint8),
                                                            torch.empty(128, 6, dtype=torch.float16))
         assert w6.shape == (3, 128, 104)
@@ -123,7 +136,9 @@ def test_fake_impls_trace_shapes():
         yn0 = torch.ops.cozy_gen_worker.svdq_w4a4_linear_fp6_next(q6, w6, None, None, None, None, None, False,
                                                                   None, None, nq, None, 0, False)
         assert yn0.shape == (77, 0)
-        assert torch.ops.cozy_gen_worker.svdq_quant_fp6_accum(x, None, None, nq, None) is None
+        assert torch.ops.cozy_gen_worker.svdq_quant_fp6_into(x, None, None, nq, None) is None
+        la_r = torch.ops.cozy_gen_worker.svdq_la_reduce(torch.empty(3, 77, 32))
+        assert la_r.shape == (77, 32) and la_r.dtype == torch.bfloat16
         assert q.shape == (77, 192) and s.shape == (77, 6) and la.shape == (77, 32)
         w = torch.empty(128, 192, dtype=torch.uint8)
         ws = torch.empty(128, 6, dtype=torch.float16)
