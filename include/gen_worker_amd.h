@@ -134,17 +134,18 @@ int gwa_svdq_group_psums(const uint8_t* qa, const uint8_t* qw, int32_t* out,
  * in [-8, 7].
  *   qw   uint8 [N, K/2] logical two's-complement codes (in)
  *   sw   fp16 [N, K/64] group scales (in)
- *   qw6  uint8 [K/128, N, 104] records (out); K % 128 == 0 */
+ *   qw6  uint8 [K/128, N, 104] records (out); K % 128 == 0. Allocate 1024
+ *        bytes of slack after it (gwa_svdq_gemm_w4a4_fp6 reads up to 1 KB past). */
 int gwa_svdq_pack_weight_fp6(const uint8_t* qw, const void* sw, uint8_t* qw6, int64_t N, int64_t K, void* stream);
 
 /* Kernel 2, fp6 path: the contract of gwa_svdq_gemm_w4a4 (replacing
  * _gemm_w4a4 + svdq_epilogue_lora, models/w4a4.py:173-180 and
  * models/svdq_fused.py:315-377) on fp6 operand records: qa6 [K/128, M, 104]
  * from gwa_svdq_quant_fp6, qw6 [K/128, N, 104] from gwa_svdq_pack_weight_fp6
- * (the records carry sa and sw). qa6's storage must stay readable for 16
- * bytes past its last record (the 16-byte operand copies of an odd M with an
- * even K/128 end 8 bytes past it). One exact fp6 MFMA per K-group and 32x32
- * block. la is bf16 [M, rank], or fp32 with GWA_EPI_LA_F32 in
+ * (the records carry sa and sw). The storage of qa6 and of qw6 must stay
+ * readable for 1024 bytes past its last record (operand records are copied
+ * in 1 KB runs; the run holding a tile's last real row may reach past it).
+ * One exact fp6 MFMA per K-group and 32x32 block. la is bf16 [M, rank], or fp32 with GWA_EPI_LA_F32 in
  * epilogue_flags (rounded to bf16 in the epilogue). K % 128 == 0,
  * N % 16 == 0. */
 int gwa_svdq_gemm_w4a4_fp6(const uint8_t* qa6, const uint8_t* qw6,

@@ -86,9 +86,10 @@ struct Cfg {
 
 // Direct-to-LDS copy of 16 bytes per lane: LDS [m0 + 16 lane, +16) <- buffer
 // [voff + soff, +16). The hardware range check covers voff only (not the
-// SGPR offset), so callers put the whole offset in voff and mark a lane's
-// chunk that lies past the valid bytes with kOOB there (the lane then reads
-// zeros and touches no memory). Issued as asm so the compiler's wait-count pass (which
+// SGPR offset): a copy whose SGPR offset may point past the buffer must keep
+// its real address inside readable memory, or put its offset in voff (where
+// kOOB makes the lane read zeros without touching memory). Issued as asm so
+// the compiler's wait-count pass (which
 // tracks only a few LDS-DMA writes and then waits for all of them before any
 // LDS read) leaves the waits to the kernel: every LDS read of a stage buffer
 // comes after an s_waitcnt that covers this wave's copies into it and a
@@ -207,11 +208,11 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_kernel(
   // bytes [1024 q', +1024) of the tile's contiguous records (q' = q for the
   // activations, q - DMA_X for the weights). Runs are dealt round-robin; a
   // wave left without a last run repeats the final run (same bytes to the
-  // same place), so every wave issues SLOTS copies per stage. A lane's 16
-  // bytes wholly past the tile's rows < M (< N) read zeros; a chunk that
-  // straddles the last real row's end (activations only: N % 16 == 0 keeps
-  // weight runs on 16-byte boundaries) reads up to 8 bytes past it, which in
-  // the last stage is the 16 bytes of slack the activation records carry.
+  // same place), so every wave issues SLOTS copies per stage. The offsets
+  // are scalar (the hardware does not range-check the SGPR offset): a run
+  // that starts past the tile's last real row reads the stage's first run
+  // instead, and the one run that straddles it reads up to 1 KB past it,
+  // which in the last stage is the 1 KB of slack every record buffer carries.
   const uint32_t dvo = 16u * (uint32_t)lane;
   const uint32_t x_valid = (uint32_t)(M - m0) * REC, w_valid = (uint32_t)(N - n0) * REC;
   auto issue = [&](uint8_t* stage, int st) __attribute__((always_inline)) {
@@ -222,9 +223,11 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_kernel(
       int q = wave + NWAVES * j;
       q = q < C::RUNS ? q : C::RUNS - 1;
       const bool isx = q < C::DMA_X;
-      const uint32_t in_run = (uint32_t)((isx ? q : q - C::DMA_X) * 1024) + dvo;
-      const uint32_t voff = in_run < (isx ? x_valid : w_valid) ? (isx ? xs : ws) + in_run : kOOB;
-      dma16(isx ? xbuf : wbuf, (uint32_t)(uintptr_t)(stage + q * 1024), voff, 0u);
+      // a run that starts past the tile's last real row re-reads the stage's first run (its rows' results are
+      // never stored); a run that straddles it reads up to 1 KB past it: the record buffers' slack
+      const uint32_t r0 = (uint32_t)((isx ? q : q - C::DMA_X) * 1024);
+      const uint32_t soff = (isx ? xs : ws) + (r0 < (isx ? x_valid : w_valid) ? r0 : 0u);
+      dma16(isx ? xbuf : wbuf, (uint32_t)(uintptr_t)(stage + q * 1024), dvo, soff);
     }
   };
 

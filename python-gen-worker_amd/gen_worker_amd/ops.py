@@ -189,13 +189,13 @@ def _(x2, smooth, s2, proj_down_op):
             x2.new_empty(m, r, dtype=torch.bfloat16))
 
 
-RECORD_SLACK = 64  # readable bytes after a record buffer that the fp6 GEMM reads as activations
+RECORD_SLACK = 1024  # readable bytes after every fp6 record buffer the GEMM reads
 
 
 def records_empty(stages: int, rows: int, device) -> Tensor:
-    """An uninitialised fp6 record buffer [stages, rows, 104] whose storage runs 64 bytes past its end: the fp6
-    GEMM's 16-byte operand copies may read up to 8 bytes past the last record (when rows is odd and stages
-    even), so every record buffer it takes as activations is allocated here."""
+    """An uninitialised fp6 record buffer [stages, rows, 104] whose storage runs 1 KB past its end: the fp6
+    GEMM copies operand records in 1 KB runs and the run that holds a tile's last real row may reach up to
+    1 KB past it, so every record buffer it reads (activations and weights) is allocated here."""
     n = stages * rows * nat.FP6_REC
     return torch.empty(n + RECORD_SLACK, dtype=torch.uint8, device=device)[:n].view(stages, rows, nat.FP6_REC)
 
@@ -541,7 +541,7 @@ def svdq_pack_weight_fp6(weight: Tensor, wscales: Tensor) -> Tensor:
         raise SvdqOpError(f"{name}: K={k} is not a multiple of {FP6_STAGE}")
     if tuple(wscales.shape) != (n, k // GROUP):
         raise SvdqOpError(f"{name}: wscales {tuple(wscales.shape)} do not match [N={n}, K/64={k // GROUP}]")
-    out = torch.empty(k // FP6_STAGE, n, nat.FP6_REC, dtype=torch.uint8, device=weight.device)
+    out = records_empty(k // FP6_STAGE, n, weight.device)
     nat.call("gwa_svdq_pack_weight_fp6", nat.ptr(weight.contiguous()), nat.ptr(wscales.contiguous()), nat.ptr(out),
              n, k, nat.stream_of(weight))
     return out

@@ -1,0 +1,322 @@
+"""Qualification gates of the int4 lane, run once per process (the reference's arming protocol).
+
+The reference arms its quantized lanes only after self-checks on the device
+and degrades to a dequantized lane when one fails:
+
+* ``extension_available`` (``models/native_kernels.py:120-143``): the native
+  library loads, exports the probe op, and the probe computes ``x + 1``.
+* quantizer bit-identity (``_bit_identical``, ``models/nvfp4_quant.py:209-230``,
+  probes ``:21``): the fused activation quantizer's codes and scales equal the
+  torch chain's byte for byte.
+* ``fused_self_check`` (``models/svdq_fused.py:421-464``, probes ``:25``):
+  quantizer bit-identity with smoothing, and the fused epilogue within
+  relative Frobenius error 5e-3 of its torch reference (rank 128).
+* ``_numerics_ok`` (``models/w4a4.py:183-207``): the W4A4 GEMM at
+  128 x 256 x 128 within relative Frobenius error 2e-2 of
+  dequantize-then-matmul.
+* ``_gemm_profitable`` (``models/w4a4.py:210-259``): median of 10 timed calls
+  after 3 warmups at M = N = K = 4096, at least 1.10x faster than the bf16
+  matmul.
+* ``w4a4_gemm_mode`` (``models/w4a4.py:262-286``): the lane, chosen once.
+
+Here the lanes are ``"int4"`` (the HIP kernels: ``SvdqW4A4Linear``) and
+``"dense"`` (``fold_to_dense``: one bf16 ``nn.Linear`` per layer on the same
+GPU, the reference's dequant lane). Without a GPU or without the library the
+lane is ``"unavailable"``: there is no CPU path for the int4 kernels. The
+torch chains below (quantizer, dequantize-then-matmul, epilogue) run on the
+GPU with torch ops; they state the reference's arithmetic with int4 group-64
+codes (``models/nvfp4_quant.py:92-103`` with e2m1 -> int4, fp16 scales).
+"""
+
+from __future__ import annotations
+
+import functools
+import logging
+from dataclasses import dataclass, field
+from typing import Any, Optional
+
+import torch
+from torch import Tensor
+
+from . import _native
+
+logger = logging.getLogger(__name__)
+
+GROUP = 64
+IDENTITY_PROBES = ((128, 512), (333, 3072), (1024, 12288))      # (m, k): models/nvfp4_quant.py:21
+SELF_CHECK_PROBES = ((128, 512, 256), (77, 3072, 384))          # (m, k, n): models/svdq_fused.py:25
+SELF_CHECK_RANK = 128
+NUMERICS_PROBE = (128, 256, 128)                                # (m, k, n): models/w4a4.py:186
+GEMM_REL_TOL = 2e-2                                             # models/w4a4.py:201-202
+EPILOGUE_REL_TOL = 5e-3                                         # models/svdq_fused.py:462
+BENCH_DIM, BENCH_WARMUP, BENCH_ITERS, BENCH_MIN_SPEEDUP = 4096, 3, 10, 1.10   # models/w4a4.py:210-213
+
+# e3m2 code -> integer value (the 17 codes of -8 .. 8; sign in bit 5)
+_E3M2 = {0x00: 0, 0x0C: 1, 0x10: 2, 0x12: 3, 0x14: 4, 0x15: 5, 0x16: 6, 0x17: 7, 0x18: 8}
+
+
+# ---------------------------------------------------------------------------
+# torch chains (the reference arithmetic, int4 group-64)
+# ---------------------------------------------------------------------------
+
+def quantize_act_torch(x2: Tensor, smooth: Optional[Tensor]) -> tuple[Tensor, Tensor]:
+    """bf16 [M, K] -> (int8 codes [M, K] in [-8, 7], fp16 scales [M, K/64]): ``xs = bf16(x / smooth)`` (fp32
+    divide), group absmax, ``scale = fp16(clamp(amax / 7, 2^-24, 65504))``, ``q = clamp(rne(xs / scale), -8, 7)``
+    (the divide by the stored-precision scale, ``models/nvfp4_quant.py:96-102``)."""
+    xs = x2 if smooth is None else (x2.float() / smooth.float().reshape(1, -1)).to(torch.bfloat16)
+    m, k = xs.shape
+    xb = xs.float().reshape(m, k // GROUP, GROUP)
+    amax = xb.abs().amax(-1)
+    scale = (amax / 7.0).clamp(min=2.0 ** -24, max=65504.0).to(torch.float16)
+    q = torch.round(xb / scale.float().unsqueeze(-1)).clamp(-8, 7).to(torch.int8)
+    return q.reshape(m, k), scale
+
+
+def pack_int4_torch(q: Tensor) -> Tensor:
+    """int8 codes [M, K] -> uint8 [M, K/2], element 2j in the low nibble of byte j."""
+    u = (q.to(torch.int16) & 0xF).to(torch.uint8)
+    return u[:, 0::2] | (u[:, 1::2] << 4)
+
+
+def decode_fp6_records_torch(rec: Tensor) -> tuple[Tensor, Tensor]:
+    """fp6 records [S, M, 104] -> (int8 codes [M, 128 S], fp16 scales [M, 2 S])."""
+    s, m, _ = rec.shape
+    b = rec[:, :, :96].reshape(s, m, 32, 3).to(torch.int32)
+    c = torch.stack((b[..., 0] & 63, (b[..., 0] >> 6) | ((b[..., 1] & 15) << 2),
+                     (b[..., 1] >> 4) | ((b[..., 2] & 3) << 4), b[..., 2] >> 2), dim=-1).reshape(s, m, 128)
+    lut = torch.full((64,), 127, dtype=torch.int8, device=rec.device)   # 127: not a code of -8 .. 8
+    for code, v in _E3M2.items():
+        lut[code] = v
+        if v:
+            lut[code | 0x20] = -v
+    codes = lut[c.long()].permute(1, 0, 2).reshape(m, 128 * s)
+    scales = rec[:, :, 96:100].contiguous().view(torch.float16).reshape(s, m, 2).permute(1, 0, 2).reshape(m, 2 * s)
+    return codes, scales
+
+
+def dequantize_torch(q: Tensor, scale: Tensor) -> Tensor:
+    m, k = q.shape
+    return (q.float().reshape(m, k // GROUP, GROUP) * scale.float().unsqueeze(-1)).reshape(m, k)
+
+
+def _rel(a: Tensor, b: Tensor) -> float:
+    return float((a.float() - b.float()).norm() / b.float().norm().clamp(min=1e-9))
+
+
+# ---------------------------------------------------------------------------
+# gates
+# ---------------------------------------------------------------------------
+
+def extension_available() -> bool:
+    """Library loaded, probe op present, probe numerics on the GPU (``models/native_kernels.py:120-143``)."""
+    try:
+        _native.load()
+        if not torch.cuda.is_available():
+            return False
+        ns = torch.ops.cozy_kernels
+        if not hasattr(ns, "probe_add_one"):
+            logger.warning("gen_worker_amd: library loaded but the probe op is missing")
+            return False
+        x = torch.arange(8, device="cuda", dtype=torch.float32)
+        return bool(torch.equal(ns.probe_add_one(x), x + 1))
+    except Exception as exc:  # noqa: BLE001 — any gap => not available
+        logger.warning("gen_worker_amd: extension probe failed (%s)", exc)
+        return False
+
+
+def _probe_inputs(m: int, k: int, smooth: bool) -> tuple[Tensor, Optional[Tensor]]:
+    g = torch.Generator(device="cuda").manual_seed(0)
+    x = torch.randn(m, k, generator=g, device="cuda").to(torch.bfloat16)
+    sm = (torch.rand(k, generator=g, device="cuda") + 0.5).to(torch.bfloat16) if smooth else None
+    return x, sm
+
+
+def quantizer_bit_identical() -> Optional[str]:
+    """Kernel 1 (int4 codes + fp16 scales, and the fp6 records) against the torch chain, with and without
+    smoothing, at the reference's identity probes; None when every byte matches, else the first mismatch."""
+    ops = torch.ops.cozy_gen_worker
+    one = torch.ones((), device="cuda")
+    for m, k in IDENTITY_PROBES:
+        for smooth in (False, True):
+            x, sm = _probe_inputs(m, k, smooth)
+            want_q, want_s = quantize_act_torch(x, sm)
+            got_q, got_s = ops.svdq_quant(x, sm, one, False)
+            if not torch.equal(got_q, pack_int4_torch(want_q)):
+                return f"int4 codes differ at {m}x{k} (smooth={smooth})"
+            if not torch.equal(got_s.view(torch.uint8), want_s.view(torch.uint8)):
+                return f"int4 scales differ at {m}x{k} (smooth={smooth})"
+            if k % 128 == 0:
+                q6, _ = ops.svdq_quant_fp6(x, sm, None, None)
+                c6, s6 = decode_fp6_records_torch(q6)
+                if not torch.equal(c6, want_q):
+                    return f"fp6 record codes differ at {m}x{k} (smooth={smooth})"
+                if not torch.equal(s6.view(torch.uint8), want_s.view(torch.uint8)):
+                    return f"fp6 record scales differ at {m}x{k} (smooth={smooth})"
+    return None
+
+
+def fused_self_check() -> Optional[str]:
+    """``fused_self_check`` (``models/svdq_fused.py:421-464``): quantizer bit-identity with smoothing at the
+    self-check probes, and the standalone epilogue within 5e-3 of ``y0 * (s2 * second) + la @ up^T + bias``."""
+    ops = torch.ops.cozy_gen_worker
+    r = SELF_CHECK_RANK
+    for m, k, n in SELF_CHECK_PROBES:
+        x, sm = _probe_inputs(m, k, True)
+        want_q, want_s = quantize_act_torch(x, sm)
+        got_q, got_s = ops.svdq_quant(x, sm, torch.ones((), device="cuda"), False)
+        if not torch.equal(got_q, pack_int4_torch(want_q)) or not torch.equal(got_s.view(torch.uint8),
+                                                                              want_s.view(torch.uint8)):
+            return f"quant not bit-identical at {m}x{k}"
+        g = torch.Generator(device="cuda").manual_seed(1)
+        up = (torch.randn(n, r, generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+        bias = torch.randn(n, generator=g, device="cuda").to(torch.bfloat16)
+        second = torch.rand(n, generator=g, device="cuda") + 0.1
+        y0 = torch.randn(m, n, generator=g, device="cuda").to(torch.bfloat16)
+        la = torch.randn(m, r, generator=g, device="cuda").to(torch.bfloat16)
+        s2 = torch.ones((), device="cuda")
+        y = ops.svdq_epilogue_lora(y0, la, up, s2, second, bias)
+        ref = y0.float() * second.reshape(1, n) + la.float() @ up.float().t() + bias.float()
+        rel = _rel(y, ref)
+        if rel > EPILOGUE_REL_TOL:
+            return f"fused epilogue rel err {rel:.4f} at {m}x{n}"
+    return None
+
+
+def _probe_layer(n: int, k: int, rank: int):
+    from .svdq import build_svdq_w4a4_linear, quantize_weight_int4
+
+    g = torch.Generator(device="cuda").manual_seed(2)
+    w = torch.randn(n, k, generator=g, device="cuda") * 0.02
+    qw, sw = quantize_weight_int4(w.cpu())
+    down = (torch.randn(k, rank, generator=g, device="cuda") * 0.02).to(torch.bfloat16) if rank else None
+    up = (torch.randn(n, rank, generator=g, device="cuda") * 0.02).to(torch.bfloat16) if rank else None
+    bias = (torch.randn(n, generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    mod = build_svdq_w4a4_linear(qweight=qw, wscales=sw, smooth=None, proj_down=down, proj_up=up, bias=bias,
+                                 device="cuda")
+    return mod, qw.cuda(), sw.cuda(), down, up, bias
+
+
+def gemm_numerics_ok() -> Optional[str]:
+    """``_numerics_ok`` (``models/w4a4.py:183-207``): the W4A4 linear (both lanes of the module: fp6 records for
+    K % 128 == 0, and the general int4 path) within 2e-2 of dequantize-then-matmul at the numerics probe and the
+    self-check probes (with rank-128 low-rank branch and bias)."""
+    from .svdq import unpack_int4
+
+    # + one K % 128 != 0 shape: the general (int8-MFMA) path of the module
+    probes = ([(*NUMERICS_PROBE, 0)] + [(m, k, n, SELF_CHECK_RANK) for m, k, n in SELF_CHECK_PROBES]
+              + [(64, 320, 128, 16)])
+    for m, k, n, rank in probes:
+        mod, qw, sw, down, up, bias = _probe_layer(n, k, rank)
+        x, _ = _probe_inputs(m, k, False)
+        y = mod(x)
+        qx, sx = quantize_act_torch(x, None)
+        wd = dequantize_torch(unpack_int4(qw.cpu()).cuda(), sw)
+        ref = dequantize_torch(qx, sx) @ wd.t() + bias.float()
+        if rank:
+            ref = ref + (x.float() @ down.float()).to(torch.bfloat16).float() @ up.float().t()
+        rel = _rel(y, ref)
+        if rel >= GEMM_REL_TOL:
+            return f"W4A4 linear rel err {rel:.4f} at {m}x{k}x{n} (lane {mod.lane})"
+    return None
+
+
+def _median_ms(fn: Any) -> float:
+    for _ in range(BENCH_WARMUP):
+        fn()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(BENCH_ITERS):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        fn()
+        e1.record()
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1))
+    times.sort()
+    return times[len(times) // 2]
+
+
+def gemm_speedup() -> tuple[float, float, float]:
+    """``_gemm_profitable`` (``models/w4a4.py:235-259``): (int4 GEMM ms, bf16 matmul ms, speedup) at
+    M = N = K = 4096; the int4 side is the fp6-lane GEMM with its epilogue on ready activation records."""
+    ops = torch.ops.cozy_gen_worker
+    d = BENCH_DIM
+    g = torch.Generator(device="cuda").manual_seed(3)
+    x = torch.randn(d, d, generator=g, device="cuda").to(torch.bfloat16)
+    w = torch.randn(d, d, generator=g, device="cuda").to(torch.bfloat16)
+    qw = torch.randint(0, 255, (d, d // 2), generator=g, device="cuda", dtype=torch.int32).to(torch.uint8)
+    sw = torch.ones(d, d // GROUP, device="cuda", dtype=torch.float16)
+    w6 = ops.svdq_pack_weight_fp6(qw, sw)
+    q6, _ = ops.svdq_quant_fp6(x, None, None, None)
+    int4_ms = _median_ms(lambda: ops.svdq_w4a4_linear_fp6(q6, w6, None, None, None, None, None, torch.bfloat16,
+                                                         False))
+    bf16_ms = _median_ms(lambda: x @ w.t())
+    return int4_ms, bf16_ms, bf16_ms / max(int4_ms, 1e-9)
+
+
+@dataclass
+class Qualification:
+    lane: str                       # "int4", "dense" or "unavailable"
+    reasons: list[str] = field(default_factory=list)
+    int4_ms: Optional[float] = None
+    bf16_ms: Optional[float] = None
+    speedup: Optional[float] = None
+
+
+def qualify() -> Qualification:
+    """Run every gate (no caching); the lane is "int4" only when all pass."""
+    if not extension_available():
+        return Qualification("unavailable", ["the HIP library or a GPU is missing (no CPU path for the int4 lane)"])
+    reasons = []
+    try:
+        for gate in (quantizer_bit_identical, fused_self_check, gemm_numerics_ok):
+            why = gate()
+            if why is not None:
+                reasons.append(why)
+        int4_ms, bf16_ms, speedup = gemm_speedup()
+        if speedup < BENCH_MIN_SPEEDUP:
+            reasons.append(f"int4 GEMM {int4_ms:.3f} ms vs bf16 {bf16_ms:.3f} ms: speedup {speedup:.2f}x "
+                           f"< {BENCH_MIN_SPEEDUP:.2f}x")
+    except Exception as exc:  # noqa: BLE001 — a failing probe degrades the lane, as in the reference
+        return Qualification("dense", [f"qualification raised {exc!r}"])
+    q = Qualification("int4" if not reasons else "dense", reasons, int4_ms, bf16_ms, speedup)
+    if reasons:
+        logger.warning("gen_worker_amd: int4 lane not armed (%s); dense lane", "; ".join(reasons))
+    else:
+        logger.info("gen_worker_amd: int4 lane armed (GEMM %.3f ms vs bf16 %.3f ms, %.2fx)", int4_ms, bf16_ms,
+                    speedup)
+    return q
+
+
+@functools.lru_cache(maxsize=1)
+def qualification() -> Qualification:
+    """The once-per-process result (``w4a4_gemm_mode``, ``models/w4a4.py:262-286``)."""
+    return qualify()
+
+
+def w4a4_lane() -> str:
+    return qualification().lane
+
+
+def serving_linear(mod: Any) -> Any:
+    """The module to serve for an int4 layer: the layer itself in the int4 lane, its dense fold (one bf16
+    ``nn.Linear`` on the layer's device, GELU kept) in the dense lane; raises when neither can run."""
+    from .svdq import fold_to_dense
+
+    lane = w4a4_lane()
+    if lane == "int4":
+        return mod
+    if lane == "unavailable":
+        raise RuntimeError("gen_worker_amd: the int4 lane is unavailable (no GPU / HIP library)")
+    dense = fold_to_dense(mod).to(mod.weight.device)
+    if mod.activation == "gelu_tanh":
+        return torch.nn.Sequential(dense, torch.nn.GELU(approximate="tanh"))
+    return dense
+
+
+__all__ = [
+    "EPILOGUE_REL_TOL", "GEMM_REL_TOL", "IDENTITY_PROBES", "Qualification", "SELF_CHECK_PROBES",
+    "decode_fp6_records_torch", "extension_available", "fused_self_check", "gemm_numerics_ok", "gemm_speedup",
+    "pack_int4_torch", "qualification", "qualify", "quantize_act_torch", "quantizer_bit_identical",
+    "serving_linear", "w4a4_lane",
+]

@@ -572,3 +572,24 @@ def test_flux_dit_small_matches_oracle_chain():
     print("dit small: cos", cos, "rel", rel, "fused vs unfused cos", cos_u)
     assert cos > 0.995 and rel < 0.1, (cos, rel)
     assert cos_u > 0.999, cos_u   # the fused model differs from the unfused one only by la's fp32 sum order
+
+
+def test_qualification_gates():
+    """The arming protocol on the device: every numerics gate passes; the profitability gate measures the
+    int4 GEMM against the bf16 matmul at 4096^3 and the lane follows it (int4 at >= 1.10x, else dense)."""
+    from gen_worker_amd import qualify
+
+    assert qualify.extension_available()
+    assert qualify.quantizer_bit_identical() is None
+    assert qualify.fused_self_check() is None
+    assert qualify.gemm_numerics_ok() is None
+    q = qualify.qualify()
+    print("qualification", q)
+    assert q.speedup is not None and q.speedup > 0
+    assert q.lane == ("int4" if q.speedup >= qualify.BENCH_MIN_SPEEDUP else "dense")
+    # the record decoder of the gates agrees with the test helper's
+    x = torch.randn(77, 384, device=DEV).to(torch.bfloat16)
+    q6, _ = torch.ops.cozy_gen_worker.svdq_quant_fp6(x, None, None, None)
+    c1, s1 = qualify.decode_fp6_records_torch(q6)
+    c2, s2 = decode_fp6_records(q6.cpu().numpy())
+    assert np.array_equal(c1.cpu().numpy(), c2) and np.array_equal(s1.cpu().view(torch.int16).numpy().view(np.uint16), s2)

@@ -219,3 +219,54 @@ def test_synthetic_inputs_are_deterministic():
     assert int((a.float().abs().amax(dim=0) > 20).sum()) > 0
     s = synthetic.smooth_factor(3072)
     assert float(s.float().min()) >= 0.25 and float(s.float().max()) <= 4.0
+
+
+def test_qualification_torch_chains_match_oracle():
+    """The qualification gates' torch chains (the quantizer the kernels must equal byte for byte, the int4
+    packer, the fp6 record decoder) against the oracle on the CPU."""
+    import numpy as np
+
+    from helpers import bits16
+    from oracle import svdq_oracle as O
+
+    from gen_worker_amd import qualify
+
+    g = torch.Generator().manual_seed(5)
+    for m, k, smooth in ((33, 256, True), (7, 640, False), (64, 3072, True)):
+        x = (torch.randn(m, k, generator=g) * 3).to(torch.bfloat16)
+        x[0, :64] = 0.0                                   # a zero group
+        x[1, 5] = 1000.0                                  # an outlier
+        sm = (torch.rand(k, generator=g) * 3.75 + 0.25).to(torch.bfloat16) if smooth else None
+        q, s = qualify.quantize_act_torch(x, sm)
+        wq, ws = O.quantize_act_int4(bits16(x), bits16(sm) if smooth else None)
+        assert np.array_equal(qualify.pack_int4_torch(q).numpy(), wq)
+        assert np.array_equal(s.view(torch.int16).numpy().view(np.uint16), ws.view(np.uint16))
+    # fp6 records: encode known codes (element t of a group at bits 6t of the group's 48 bytes)
+    e3m2 = {0: 0x00, 1: 0x0C, 2: 0x10, 3: 0x12, 4: 0x14, 5: 0x15, 6: 0x16, 7: 0x17}
+    rng = np.random.default_rng(0)
+    S, M = 3, 5
+    codes = rng.integers(-8, 8, size=(M, 128 * S))
+    scales = rng.standard_normal((M, 2 * S)).astype(np.float16)
+    rec = np.zeros((S, M, 104), np.uint8)
+    for st in range(S):
+        for r in range(M):
+            for gi in range(2):
+                bits = 0
+                for t in range(64):
+                    c = int(codes[r, 128 * st + 64 * gi + t])
+                    v = (0x20 | (0x18 if c == -8 else e3m2[-c])) if c < 0 else e3m2[c]
+                    bits |= v << (6 * t)
+                rec[st, r, 48 * gi:48 * gi + 48] = np.frombuffer(bits.to_bytes(48, "little"), np.uint8)
+            rec[st, r, 96:100] = np.frombuffer(scales[r, 2 * st:2 * st + 2].tobytes(), np.uint8)
+    dc, ds = qualify.decode_fp6_records_torch(torch.from_numpy(rec))
+    assert np.array_equal(dc.numpy(), codes.astype(np.int8))
+    assert np.array_equal(ds.numpy().view(np.uint16), scales.view(np.uint16))
+
+
+def test_qualification_without_gpu_is_unavailable():
+    from gen_worker_amd import qualify
+
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    q = qualify.qualify()
+    assert q.lane == "unavailable" and q.reasons
