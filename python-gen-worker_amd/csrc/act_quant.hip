@@ -342,70 +342,18 @@ __global__ __launch_bounds__(Q6_THREADS) void svdq_quant_fp6_kernel(
     if (smooth) {
       // the stage's flag is workgroup-uniform: one scalar branch, not one per element
       const int divide = __builtin_amdgcn_readfirstlane(*(const int*)(lds + FLAG_OFF + 4 * t));
-      const float* f = (const float*)(lds + RCP_OFF) + t * 128 + 32 * c;
-      if (!divide) {
+      const float* f = (const float*)(lds + RCP_OFF) + (divide ? CH * 128 : 0) + t * 128 + 32 * c;
+      float fv[32];
 #pragma unroll
-        for (int i = 0; i < 32; i += 4) {
-          const v4f fv = *(const v4f*)(f + i);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) v[i + e] *= fv[e];
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < 32; i += 4) {
-          const v4f fv = *(const v4f*)(f + CH * 128 + i);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) v[i + e] /= fv[e];
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < 32; i += 2) {
-        const uint32_t pk = pack_bf16x2_rn(v[i], v[i + 1]);
-        v[i] = bf16_lo(pk);
-        v[i + 1] = bf16_hi(pk);
-      }
+      for (int i = 0; i < 32; i += 4) *(v4f*)(fv + i) = *(const v4f*)(f + i);
+      g64::smooth32(v, fv, divide != 0);
     }
-    // absmax on the bit patterns (|x| orders like its bits; a NaN ranks above inf, as in quant_g64.h),
-    // then the group's other half in lane ^ 16
-    uint32_t mu = 0;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) mu = max(mu, __float_as_uint(v[i]) & 0x7fffffffu);
+    // group absmax: this lane's half, then the other half in lane ^ 16
+    uint32_t mu = g64::absmax_bits32(v);
     mu = max(mu, (uint32_t)__shfl_xor((int)mu, 16));
-    const float amax = __uint_as_float(mu);
-    const uint32_t mb = mu >> 16;  // the bf16 bits of amax
-
-    // ---- scale and codes (quant_g64.h's arithmetic, 32 elements per lane)
-    float scl;
-    const float r7 = 1.0f / 7.0f;
-    const bool easy = s2_one && (mb & 0x7F80u) != 0x7F80u;
-    if (__builtin_amdgcn_ballot_w64(!easy) == 0) {
-      const float q1 = amax * r7;
-      scl = fmaf(fmaf(-7.0f, q1, amax), r7, q1);
-    } else {
-      scl = amax / (7.0f * s2);
-    }
-    const bool fast = !row_ok || (s2_one && scl >= g64::kFp16MinNormal && scl < g64::kFp16Max);
-    scl = fminf(fmaxf(scl, g64::kScaleMin), g64::kFp16Max);
-    const uint16_t sh = f32_to_f16_bits(scl);
-    const float d = f16_bits_to_f32(sh) * s2;
-    v16f qa, qb;  // codes 2i / 2i + 1, as floats
-    if (__builtin_amdgcn_ballot_w64(!fast) == 0) {
-      const float rd = __builtin_amdgcn_rcpf(d);
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        qa[i] = (((v[2 * i] * rd) + g64::kSnap) + g64::kRound) - 12582912.0f;
-        qb[i] = (((v[2 * i + 1] * rd) + g64::kSnap) + g64::kRound) - 12582912.0f;
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        // + 0.0f: a -0 code is stored as +0 (e3m2 0x00), as the nibble path does
-        qa[i] = fminf(fmaxf(__builtin_rintf(v[2 * i] / d), -8.0f), 7.0f) + 0.0f;
-        qb[i] = fminf(fmaxf(__builtin_rintf(v[2 * i + 1] / d), -8.0f), 7.0f) + 0.0f;
-      }
-    }
-    typedef unsigned int v6u __attribute__((ext_vector_type(6)));
-    const v6u pk = __builtin_amdgcn_cvt_scalef32_2xpk16_bf6_f32(qa, qb, 1.0f);
+    g64::v6u pk;
+    uint16_t sh;
+    g64::quant32(v, mu, row_ok, s2_one, s2, pk, sh);
     // ---- record (stage st, row grow): bytes [24c, 24c + 24) hold this half-group; 96 + 2 g the scale
     const uint32_t rec = (uint32_t)(((int64_t)st * M + grow) * GWA_FP6_REC);
     buf_store16((v4i){(int)pk[0], (int)pk[1], (int)pk[2], (int)pk[3]}, qbuf, row_ok ? rec + 24u * c : kOOB);
@@ -438,13 +386,22 @@ __global__ __launch_bounds__(Q6_THREADS) void svdq_quant_fp6_kernel(
   }
 }
 
-// la = RN_bf16(sum over p of part[p]) in the order p = 0, 1, ...: one thread per row and 4 ranks.
+// la = RN_bf16(sum over p of part[p]) in the order p = 0, 1, ...: one thread per 4 consecutive values, the
+// partials loaded 8 at a time (independent loads in flight) and added in order.
 __global__ __launch_bounds__(256) void la_reduce_kernel(const float* __restrict__ part, int P, int64_t MR,
                                                          uint16_t* __restrict__ la) {
   const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
   if (i >= MR) return;
-  v4f s = *(const v4f*)(part + i);
-  for (int p = 1; p < P; ++p) s += *(const v4f*)(part + (int64_t)p * MR + i);
+  v4f s = (v4f){0.f, 0.f, 0.f, 0.f};
+  for (int p0 = 0; p0 < P; p0 += 8) {
+    v4f v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      v[u] = p0 + u < P ? *(const v4f*)(part + (int64_t)(p0 + u) * MR + i) : (v4f){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (p0 + u < P) s = (p0 + u == 0) ? v[u] : s + v[u];
+  }
   *(uint2*)(la + i) = make_uint2(pack_bf16x2_rn(s[0], s[1]), pack_bf16x2_rn(s[2], s[3]));
 }
 

@@ -161,4 +161,79 @@ __device__ __forceinline__ void store_fp6(rsrc_t qbuf, uint32_t rec, int godd, i
   buf_store2(sh, qbuf, (valid && (lane & 7) == 0) ? rec + 96u + (uint32_t)(godd * 2) : kOOB);
 }
 
+// ---------------------------------------------------------------------------
+// 32 consecutive elements per lane (half a group; the group's other half in a
+// partner lane): the fp6-record path. Same arithmetic and exactness as
+// quant8, codes packed to e3m2 by the hardware converter.
+// ---------------------------------------------------------------------------
+typedef unsigned int v6u __attribute__((ext_vector_type(6)));
+typedef float v16f_ __attribute__((ext_vector_type(16)));
+
+// v[i] = RN_bf16(v[i] * f[i]) (f = RN(1/smooth)) or RN_bf16(v[i] / f[i]) (f = smooth) when `divide`
+// (wave-uniform; both give the same bf16 for a normal smooth)
+__device__ __forceinline__ void smooth32(float* v, const float* f, bool divide) {
+  if (!divide) {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) v[i] *= f[i];
+  } else {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) v[i] /= f[i];
+  }
+#pragma unroll
+  for (int i = 0; i < 32; i += 2) {
+    const uint32_t pk = pack_bf16x2_rn(v[i], v[i + 1]);
+    v[i] = bf16_lo(pk);
+    v[i + 1] = bf16_hi(pk);
+  }
+}
+
+// the lane's absmax as bit patterns of bf16-exact floats (|x| orders like its bits; NaN above inf)
+__device__ __forceinline__ uint32_t absmax_bits32(const float* v) {
+  uint32_t mu = 0;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) mu = max(mu, __float_as_uint(v[i]) & 0x7fffffffu);
+  return mu;
+}
+
+// codes of v[32] given the group's absmax bits mu: pk = the 32 e3m2 codes (element t at bits [6t, 6t+6)
+// of the 24 bytes), sh = the group's fp16 scale. !valid lanes never force the slow paths. Every lane of
+// the wave must call this together.
+__device__ __forceinline__ void quant32(const float* v, uint32_t mu, bool valid, bool s2_one, float s2, v6u& pk,
+                                        uint16_t& sh) {
+  const float amax = __uint_as_float(mu);
+  const uint32_t mb = mu >> 16;  // the bf16 bits of amax
+  float scl;
+  const float r7 = 1.0f / 7.0f;
+  const bool easy = s2_one && (mb & 0x7F80u) != 0x7F80u;
+  if (__builtin_amdgcn_ballot_w64(!easy) == 0) {
+    const float q1 = amax * r7;
+    scl = fmaf(fmaf(-7.0f, q1, amax), r7, q1);
+  } else {
+    scl = amax / (7.0f * s2);
+  }
+  const bool fast = !valid || (s2_one && scl >= kFp16MinNormal && scl < kFp16Max);
+  scl = fminf(fmaxf(scl, kScaleMin), kFp16Max);
+  sh = f32_to_f16_bits(scl);
+  const float d = f16_bits_to_f32(sh) * s2;
+  v16f_ qa, qb;  // codes 2i / 2i + 1, as floats
+  if (__builtin_amdgcn_ballot_w64(!fast) == 0) {
+    const float rd = __builtin_amdgcn_rcpf(d);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      qa[i] = (((v[2 * i] * rd) + kSnap) + kRound) - 12582912.0f;
+      qb[i] = (((v[2 * i + 1] * rd) + kSnap) + kRound) - 12582912.0f;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      // + 0.0f: a -0 code is stored as +0 (e3m2 0x00), as the nibble path does
+      qa[i] = fminf(fmaxf(__builtin_rintf(v[2 * i] / d), -8.0f), 7.0f) + 0.0f;
+      qb[i] = fminf(fmaxf(__builtin_rintf(v[2 * i + 1] / d), -8.0f), 7.0f) + 0.0f;
+    }
+  }
+  // v_cvt_scalef32_2xpk16_bf6_f32: element 2i from the first source's i, 2i+1 from the second's, divided
+  // by the scale (1: exact for the integers -8 .. 8)
+  pk = __builtin_amdgcn_cvt_scalef32_2xpk16_bf6_f32(qa, qb, 1.0f);
+}
+
 }  // namespace g64

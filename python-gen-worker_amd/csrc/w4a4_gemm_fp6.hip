@@ -252,6 +252,23 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_kernel(
     }
   };
 
+  // NQ: the next layer's proj_down operands for this tile's TN columns (one contiguous run of
+  // (TN / 128) * nx.rb * 4 KB in the fp6 act-quant order) are copied into the LDS past the staged output
+  // tile at the start of the epilogue, when they fit; else the epilogue loads them from global memory
+  constexpr int OSTR = TN * 2 + 8;  // output staging row stride (bytes); 8-byte pad: distinct banks per write
+  constexpr int NQ_PDO_OFF = (TM * OSTR + 1023) / 1024 * 1024;
+  const int pdo_runs = NQ ? (TN / 128) * nx.rb * 4 : 0;
+  const bool pdo_lds = NQ && nx.pdo != nullptr && nx.rb > 0 && NQ_PDO_OFF + pdo_runs * 1024 <= NBUF * C::STAGE;
+  const v4i pdo4 = raw_rsrc(nx.pdo, NQ ? (uint32_t)((int64_t)(N >> 7) * nx.rb * 4096) : 0u);
+  auto issue_next_pdo = [&](uint8_t* dst) __attribute__((always_inline)) {
+    const uint32_t base = (uint32_t)(n0 >> 7) * (uint32_t)nx.rb * 4096u;
+    const uint32_t valid = (uint32_t)((N - n0 + 127) >> 7) * (uint32_t)nx.rb * 4096u;  // stages past N: none
+    for (int q = wave; q < pdo_runs; q += NWAVES) {
+      const uint32_t in_run = (uint32_t)q * 1024u + dvo;
+      dma16(pdo4, (uint32_t)(uintptr_t)(dst + q * 1024), in_run < valid ? base + in_run : kOOB, 0u);
+    }
+  };
+
   v16f acc[WBN][WBM];
 #pragma unroll
   for (int a = 0; a < WBN; ++a)
@@ -363,6 +380,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_kernel(
     if constexpr (LR_LDS) {
       if (st == nst - 1) issue_lowrank(spare1, spare2);
     }
+
     compute(cur);
     // copies issued after stage st + 1's: stages st + 2 .. min(st + NBUF - 1, nst - 1)
     const int newer = min(NBUF - 2, nst - 2 - st);
@@ -476,10 +494,12 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_kernel(
   // bytes (the stage buffers are free; the barrier also retires the la / up
   // reads), then stored as full rows: each lane 16 bytes, 32 lanes per 512
   // bytes of a row, so every wave store covers whole 128-byte lines.
-  constexpr int OSTR = TN * 2 + 8;  // 8-byte pad: the 32 rows a write instruction covers hit distinct banks
   static_assert(TM * OSTR <= NBUF * C::STAGE, "output staging");
   uint8_t* ob = &g_stage[0][0];
   barrier_lds();
+  if constexpr (NQ) {
+    if (pdo_lds) issue_next_pdo(ob + NQ_PDO_OFF);  // past the staged tile; completes behind the staging
+  }
 #pragma unroll
   for (int bn = 0; bn < WBN; ++bn) {
     const int nl = 32 * (WBN * wn + bn);
@@ -513,58 +533,10 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_kernel(
   constexpr int CPR = TN / 8;                 // 16-byte chunks per row
   constexpr int RPP = NTHREADS / CPR;         // rows per pass
   const int crow = tid / CPR, cch = tid % CPR;
-  if (!NQ || out != nullptr) {
-    const rsrc_t obuf = make_rsrc(out, (uint32_t)((int64_t)M * N * 2));
-    const bool col_ok = n0 + 8 * cch < N;
-#pragma unroll 4
-    for (int r0 = 0; r0 < TM; r0 += RPP) {
-      const int row = r0 + crow;
-      const uint2 lo = *(const uint2*)(ob + row * OSTR + cch * 16);
-      const uint2 hi = *(const uint2*)(ob + row * OSTR + cch * 16 + 8);
-      const uint32_t off =
-          (col_ok && m0 + row < M) ? (uint32_t)(((int64_t)(m0 + row) * N + n0 + 8 * cch) * 2) : kOOB;
-      buf_store16((v4i){(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y}, obuf, off);
-    }
-  }
   if constexpr (NQ) {
-    // ---- the next layer's fp6 records (its K = this N; N % 128 == 0, so every column is real).
-    // Thread -> 8 fixed columns (a group = 8 consecutive lanes), rows crow, crow + RPP, ...
-    const int col = n0 + 8 * cch;
-    float f[8];
-    bool divide = false;
-    if (nx.smooth) {
-      const v4i sv = *(const v4i*)(nx.smooth + col);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        f[2 * j] = bf16_lo((uint32_t)sv[j]);
-        f[2 * j + 1] = bf16_hi((uint32_t)sv[j]);
-      }
-#pragma unroll
-      for (int t = 0; t < 8; ++t) divide |= !g64::smooth_ok(f[t]);
-      if (!divide) {
-#pragma unroll
-        for (int t = 0; t < 8; ++t) f[t] = 1.0f / f[t];
-      }
-    }
-    const rsrc_t qb = make_rsrc(nx.q6, (uint32_t)((int64_t)(N >> 7) * M * REC));
-    const int nstage = col >> 7, godd = (col >> 6) & 1;
-#pragma unroll 2
-    for (int r0 = 0; r0 < TM; r0 += RPP) {
-      const int row = r0 + crow;
-      const bool valid = m0 + row < M;
-      const v4i c = *(const v4i*)(ob + row * OSTR + cch * 16);
-      uint32_t w[4];
-      if (nx.smooth) {
-        g64::smooth8(c, f, divide, w);
-      } else {
-#pragma unroll
-        for (int t = 0; t < 4; ++t) w[t] = (uint32_t)c[t];
-      }
-      uint32_t nb[2];
-      uint16_t sh;
-      g64::quant8(w, valid, true, 1.0f, nb, sh);
-      const uint32_t rec = valid ? (uint32_t)(((int64_t)nstage * M + m0 + row) * REC) : 0u;
-      g64::store_fp6(qb, rec, godd, lane, nb, sh, valid);
+    if (pdo_lds) {  // this wave's copies, then everyone's
+      wait_vm_lgkm0<0>();
+      barrier_lds();
     }
     // ---- la_next[m0 + rows, :] += tile[rows, :] @ proj_down_next[n0 .. n0 + TN, :]: wave w takes rows
     // 32w .. 32w + 31 (two 16-row MFMA blocks); per 128-column stage, k-step j, lane (r, c) = (lane % 16,
@@ -572,24 +544,29 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_kernel(
     // proj_down in
     if (nx.pdo != nullptr && nx.rb > 0) {
       const rsrc_t pb = make_rsrc(nx.pdo, (uint32_t)((int64_t)(N >> 7) * nx.rb * 4096));
+      const uint8_t* pl = ob + NQ_PDO_OFF + 16 * lane;
       v4f lacc[2][kNextRbMax];
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int rb = 0; rb < kNextRbMax; ++rb) lacc[i][rb] = (v4f){0.f, 0.f, 0.f, 0.f};
+      // MFMA block i of wave w: rows 32w + 2r + i (r = lane % 16): a stride of two rows puts the 16 rows of a
+      // read on distinct LDS banks
+      const uint8_t* arow = ob + (32 * wave + 2 * (lane & 15)) * OSTR + 64 * (lane >> 4);
 #pragma unroll
       for (int ts = 0; ts < TN / 128; ++ts) {
         const int sg = (n0 >> 7) + ts;
         if (128 * sg >= N) break;  // the tile's columns past N (N % 128 == 0: whole stages)
 #pragma unroll 2
         for (int j = 0; j < 4; ++j) {
-          const uint8_t* ar = ob + (32 * wave + (lane & 15)) * OSTR + (128 * ts + 32 * (lane >> 4) + 8 * j) * 2;
+          const uint8_t* ar = arow + (128 * ts + 8 * j) * 2;
           const v4i a0 = *(const v4i*)ar;
-          const v4i a1 = *(const v4i*)(ar + 16 * OSTR);
+          const v4i a1 = *(const v4i*)(ar + OSTR);
 #pragma unroll
           for (int rb = 0; rb < kNextRbMax; ++rb) {
             if (rb < nx.rb) {
-              const v4i b = buf_load16(pb, (uint32_t)(((((int64_t)sg * 4 + j) * nx.rb + rb) * 64 + lane) * 16));
+              const v4i b = pdo_lds ? *(const v4i*)(pl + ((ts * 4 + j) * nx.rb + rb) * 1024)
+                                    : buf_load16(pb, (uint32_t)(((((int64_t)sg * 4 + j) * nx.rb + rb) * 64 + lane) * 16));
               lacc[0][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, a0),
                                                                     __builtin_bit_cast(v8bf, b), lacc[0][rb], 0, 0, 0);
               lacc[1][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, a1),
@@ -607,11 +584,83 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_kernel(
           if (rb < nx.rb) {
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-              const int m = m0 + 32 * wave + 16 * i + 4 * (lane >> 4) + t;
+              const int m = m0 + 32 * wave + 2 * (4 * (lane >> 4) + t) + i;
               if (m < M) slot[(int64_t)m * R + 16 * rb + (lane & 15)] = lacc[i][rb][t];
             }
           }
         }
+    }
+  }
+  if (!NQ || out != nullptr) {
+    const rsrc_t obuf = make_rsrc(out, (uint32_t)((int64_t)M * N * 2));
+    const bool col_ok = n0 + 8 * cch < N;
+#pragma unroll 4
+    for (int r0 = 0; r0 < TM; r0 += RPP) {
+      const int row = r0 + crow;
+      const uint2 lo = *(const uint2*)(ob + row * OSTR + cch * 16);
+      const uint2 hi = *(const uint2*)(ob + row * OSTR + cch * 16 + 8);
+      const uint32_t off =
+          (col_ok && m0 + row < M) ? (uint32_t)(((int64_t)(m0 + row) * N + n0 + 8 * cch) * 2) : kOOB;
+      buf_store16((v4i){(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y}, obuf, off);
+    }
+  }
+  if constexpr (NQ) {
+    // ---- the next layer's fp6 records (its K = this N; N % 128 == 0, so every column is real).
+    // Thread -> 32 fixed consecutive columns (half a group; the other half in lane ^ 1), rows crow, crow +
+    // RPP32, ...: the fp6 act-quant kernel's per-lane quantizer, so the records match it bit for bit.
+    constexpr int CPR32 = TN / 32, RPP32 = NTHREADS / CPR32;
+    const int crow32 = tid / CPR32, cch32 = tid % CPR32;
+    const int col = n0 + 32 * cch32;
+    float f[32];
+    bool divide = false;
+    if (nx.smooth) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        // columns past N (the second half of a 256-wide tile when N % 256 == 128): any real factors (those
+        // rows' records fall past the buffer and are not stored)
+        const v4i sv = *(const v4i*)(nx.smooth + (col < N ? col : 0) + 8 * q);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          f[8 * q + 2 * j] = bf16_lo((uint32_t)sv[j]);
+          f[8 * q + 2 * j + 1] = bf16_hi((uint32_t)sv[j]);
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < 32; ++t) divide |= !g64::smooth_ok(f[t]);
+      divide = __builtin_amdgcn_ballot_w64(divide) != 0;  // wave-uniform: both paths give the same bf16
+      if (!divide) {
+#pragma unroll
+        for (int t = 0; t < 32; ++t) f[t] = 1.0f / f[t];
+      }
+    }
+    const rsrc_t qb = make_rsrc(nx.q6, (uint32_t)((int64_t)(N >> 7) * M * REC));
+    const int nstage = col >> 7;
+    const uint32_t in_rec = (uint32_t)(48 * ((cch32 >> 1) & 1) + 24 * (cch32 & 1));
+    const uint32_t sc_off = (cch32 & 1) ? kOOB : (uint32_t)(96 + 2 * ((cch32 >> 1) & 1));
+#pragma unroll 1
+    for (int r0 = 0; r0 < TM; r0 += RPP32) {
+      const int row = r0 + crow32;
+      const bool valid = m0 + row < M;
+      float v[32];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const v4i c = *(const v4i*)(ob + row * OSTR + cch32 * 64 + 16 * q);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          v[8 * q + 2 * j] = bf16_lo((uint32_t)c[j]);
+          v[8 * q + 2 * j + 1] = bf16_hi((uint32_t)c[j]);
+        }
+      }
+      if (nx.smooth) g64::smooth32(v, f, divide);
+      uint32_t mu = g64::absmax_bits32(v);
+      mu = max(mu, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mu, 0xB1, 0xF, 0xF, false));  // lane ^ 1
+      g64::v6u pk;
+      uint16_t sh;
+      g64::quant32(v, mu, valid, true, 1.0f, pk, sh);
+      const uint32_t rec = (uint32_t)(((int64_t)nstage * M + m0 + row) * REC);
+      buf_store16((v4i){(int)pk[0], (int)pk[1], (int)pk[2], (int)pk[3]}, qb, valid ? rec + in_rec : kOOB);
+      buf_store8(make_uint2(pk[4], pk[5]), qb, valid ? rec + in_rec + 16u : kOOB);
+      buf_store2(sh, qb, (valid && sc_off != kOOB) ? rec + sc_off : kOOB);
     }
   }
 }
