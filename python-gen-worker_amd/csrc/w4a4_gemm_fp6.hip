@@ -38,14 +38,19 @@
 // (buffer_load_dwordx4 ... lds: no staging registers, no ds_write, one address
 // register); the 104-byte record stride keeps the 32 rows a block reads on
 // distinct LDS bank pairs, and the scales arrive inside the records. Three
-// stage buffers rotate, filled two stages ahead. Every wave issues the same
-// number of DMA loads per stage, so one s_waitcnt vmcnt(N) before each
-// barrier completes exactly the stage about to be read while the newest
-// stays in flight. The stage loop is unrolled by three so every LDS read
-// names its buffer statically. Within a stage the 8 blocks run in a fixed
-// order (a scheduling fence after each), keeping one block's P and S live;
-// the other wave on the SIMD fills the matrix pipe meanwhile. Tiles are
-// ordered per XCD (xcd_tile_of) so operands stay in that XCD's L2.
+// stage buffers rotate: a buffer is refilled (stage st + 3) as soon as every
+// wave has read its last operand from it, at stage st's sync point in the
+// middle of the stage. Every wave issues the same number of DMA loads per
+// stage, so one s_waitcnt vmcnt(N) before that barrier completes exactly the
+// stage read next while the newer one stays in flight. Operands live in
+// registers across stages (the next group's are read right after their last
+// use), so no wave waits on LDS at a stage start. The stage loop is unrolled
+// by three so every LDS read names its buffer statically. Within a stage the
+// 16 blocks run in a fixed order (a scheduling fence after each), keeping one
+// block's P and S live; the other wave on the SIMD fills the matrix pipe
+// meanwhile. The fp32 accumulators are scalars so each fma accumulates in
+// place (v_fmac_f32, the 4-byte encoding). Tiles are ordered per XCD
+// (xcd_tile_of) so operands stay in that XCD's L2.
 #include "gwa_common.h"
 #include "quant_g64.h"
 
@@ -81,7 +86,7 @@ struct Cfg {
   static constexpr bool PIPE = WBN * WBM <= 4;
   static_assert(WAVES_N * WAVES_M == NWAVES && WBM * 32 * WAVES_M == TM, "wave grid");
   static_assert(LDS_X % 1024 == 0 && LDS_W % 1024 == 0 && NBUF >= 3, "stage layout");
-  static_assert((NBUF - 1) * SLOTS < 64, "vmcnt range");
+  static_assert(NBUF * SLOTS < 64, "vmcnt range");
 };
 
 // Direct-to-LDS copy of 16 bytes per lane: LDS [m0 + 16 lane, +16) <- buffer
@@ -232,9 +237,9 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_kernel(
   };
 
   // The low-rank operands of ranks up to 32 (la rows m0.., up rows n0..: two
-  // contiguous runs) are copied during the last stage into the two stage
-  // buffers that follow it (neither is read in the last stage), la into the
-  // first, up into the second. The loop's final wait (vmcnt(0)) covers them.
+  // contiguous runs) are copied into two stage buffers that no stage reads or
+  // fills once stage max(nst - 2, 0)'s sync has passed (spare1 / spare2), la
+  // into the first, up into the second. The wait after the loop covers them.
   constexpr bool LR_LDS = RB == 1 || RB == 2;
   const int la_row = RB * 32 * (la_f32 ? 2 : 1);  // bytes per la row
   const v4i lbuf4 = raw_rsrc(la, (uint32_t)((int64_t)M * la_row));
@@ -269,11 +274,18 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_kernel(
     }
   };
 
-  v16f acc[WBN][WBM];
+  // the main loop's fp32 accumulators, as scalars: each block's fmas then accumulate in place (v_fmac)
+  float acc[WBN][WBM][16];
 #pragma unroll
   for (int a = 0; a < WBN; ++a)
 #pragma unroll
-    for (int b = 0; b < WBM; ++b) acc[a][b] = (v16f){};
+    for (int b = 0; b < WBM; ++b)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.0f;
+  auto pin16 = [](float* a) __attribute__((always_inline)) {
+    asm volatile("" : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(a[4]), "+v"(a[5]), "+v"(a[6]), "+v"(a[7]),
+                 "+v"(a[8]), "+v"(a[9]), "+v"(a[10]), "+v"(a[11]), "+v"(a[12]), "+v"(a[13]), "+v"(a[14]), "+v"(a[15]));
+  };
 
   // Pending P and S of the previous block (software pipeline, TN = 128): the
   // pipeline starts with zero products "pending" for the last block, so the
@@ -295,14 +307,20 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_kernel(
     for (int a = 0; a < WBN; ++a)
 #pragma unroll
       for (int b = 0; b < WBM; ++b)
-        if (blk == a * WBM + b) asm volatile("" : "+v"(acc[a][b]));
+        if (blk == a * WBM + b) pin16(acc[a][b]);
   };
 
-  // One stage's blocks, in (bn, bm) order. A group's operands stay in
-  // registers; each is refilled with the next group's operand right after its
-  // last use (the first group of a stage is read at the stage start: the
-  // next stage's buffer is only complete after the barrier). Empty asm
-  // statements pin the pure MFMA intrinsics to their place in program order.
+  // The operands of the group about to run (both operands' 32-code halves and
+  // the stage's scales) live in registers across stages; each is refilled
+  // with the next group's right after its last use, so LDS reads overlap the
+  // MFMAs and fmas. Group 0 refills group 1's operands from this stage's
+  // buffer; group 1 refills group 0's (and the scales) from the next stage's
+  // buffer, which is complete only after that stage's copies are waited for
+  // and the workgroup barrier: `sync` runs inside group 1 before its first
+  // read of the next buffer (after the first bn row of blocks, whose
+  // operands are already in registers), so no wave starts a stage waiting for
+  // LDS. Empty asm statements pin the pure MFMA intrinsics to their place in
+  // program order.
   //  * PIPE: one step per block b issues b's two MFMAs between the two halves
   //    of block b-1's 16 fmas (whose P and S completed during step b-1), in
   //    scheduling groups MFMA, 8 VALU, MFMA, 8 VALU; the step's end takes
@@ -310,24 +328,44 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_kernel(
   //    stage's last block hands its P and S to the next stage.
   //  * otherwise: each block's MFMAs, then its 16 fmas (one block's P and S
   //    live); the other wave on the SIMD fills the matrix pipe meanwhile.
-  auto compute = [&](const uint8_t* base) __attribute__((always_inline)) {
-    const uint8_t* lx = base + (32 * WBM * wm + r32) * REC + 24 * h;
-    const uint8_t* lw = base + OFF_W + (32 * WBN * wn + r32) * REC + 24 * h;
-    const uint8_t* sx = base + (32 * WBM * wm + r32) * REC + OFF_SC;
-    const uint8_t* sw = base + OFF_W + (32 * WBN * wn + r32) * REC + OFF_SC;
-    v8i xo[WBM], wo[WBN];
-    uint32_t xs[WBM], ws[WBN];
-#pragma unroll
-    for (int bn = 0; bn < WBN; ++bn) {
-      wo[bn] = lds_operand(lw + bn * 32 * REC);
-      const uint32_t v = *(const uint32_t*)(sw + bn * 32 * REC);
-      ws[bn] = h ? 0u : v;  // K slots 4..7 (lanes 32..63) stay zero
+  v8i xo[WBM], wo[WBN];
+  uint32_t xs[WBM], ws[WBN];
+  const int xrow = (32 * WBM * wm + r32) * REC, wrow = OFF_W + (32 * WBN * wn + r32) * REC;
+  auto read_x = [&](const uint8_t* base, int bm, int gi) __attribute__((always_inline)) {
+    xo[bm] = lds_operand(base + xrow + bm * 32 * REC + 24 * h + gi * GB);
+  };
+  auto read_w = [&](const uint8_t* base, int bn, int gi) __attribute__((always_inline)) {
+    wo[bn] = lds_operand(base + wrow + bn * 32 * REC + 24 * h + gi * GB);
+  };
+  auto read_xs = [&](const uint8_t* base, int bm) __attribute__((always_inline)) {
+    xs[bm] = *(const uint32_t*)(base + xrow + bm * 32 * REC + OFF_SC);
+  };
+  auto read_ws = [&](const uint8_t* base, int bn) __attribute__((always_inline)) {
+    const uint32_t v = *(const uint32_t*)(base + wrow + bn * 32 * REC + OFF_SC);
+    ws[bn] = h ? 0u : v;  // K slots 4..7 (lanes 32..63) stay zero
+  };
+
+  // the spare buffers for the low-rank operands: neither is read or filled
+  // again once stage max(nst - 2, 0)'s sync has passed
+  uint8_t* const spare1 = &g_stage[0][0] + (nst % NBUF) * C::STAGE;
+  uint8_t* const spare2 = &g_stage[0][0] + ((nst + 1) % NBUF) * C::STAGE;
+  // stage st's sync: stage st + 1 complete (this wave's copies, then
+  // everyone's; the barrier also retires every wave's reads of this stage's
+  // buffer), then this stage's buffer takes stage st + NBUF
+  auto sync = [&](int st, uint8_t* buf) __attribute__((always_inline)) {
+    if (st + 1 < nst) {
+      // copies issued after stage st + 1's: stages st + 2 .. min(st + NBUF - 1, nst - 1)
+      wait_stages<SLOTS, NBUF - 2>(min(NBUF - 2, nst - 2 - st));
+      barrier_lds();
     }
-#pragma unroll
-    for (int bm = 0; bm < WBM; ++bm) {
-      xo[bm] = lds_operand(lx + bm * 32 * REC);
-      xs[bm] = *(const uint32_t*)(sx + bm * 32 * REC);
+    if (st + NBUF < nst) issue(buf, st + NBUF);
+    if constexpr (LR_LDS) {
+      if (st == max(nst - 2, 0)) issue_lowrank(spare1, spare2);
     }
+  };
+
+  // One stage's blocks, in (bn, bm) order, on operands already in registers.
+  auto stage = [&](int st, uint8_t* cur, const uint8_t* nxt) __attribute__((always_inline)) {
     int prev = kLast;
 #pragma unroll
     for (int gi = 0; gi < GS; ++gi) {
@@ -361,31 +399,26 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_kernel(
             const v16f sv = __builtin_amdgcn_mfma_f32_32x32x8f16(swop, sel, (v16f){}, 0, 0, 0);
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[bn][bm][v] = fmaf(p[v], sv[v], acc[bn][bm][v]);
-            asm volatile("" : "+v"(acc[bn][bm]));  // this block's fmas complete here, in program order
+            pin16(acc[bn][bm]);  // this block's fmas complete here, in program order
           }
-          if (gi + 1 < GS) {
-            if (bn == WBN - 1) xo[bm] = lds_operand(lx + bm * 32 * REC + (gi + 1) * GB);
-            if (bm == WBM - 1) wo[bn] = lds_operand(lw + bn * 32 * REC + (gi + 1) * GB);
+          if (gi == 0) {
+            if (bn == WBN - 1) read_x(cur, bm, 1);
+            if (bm == WBM - 1) read_w(cur, bn, 1);
+          } else {
+            // past the last stage the reads below fetch unused values (in bounds of the LDS)
+            if (bn == 0 && bm == WBM - 1) sync(st, cur);
+            if (bn == WBN - 1) {
+              read_x(nxt, bm, 0);
+              read_xs(nxt, bm);
+            }
+            if (bm == WBM - 1) {
+              read_w(nxt, bn, 0);
+              read_ws(nxt, bn);
+            }
           }
         }
       }
     }
-  };
-  // one stage: prefetch stage st + NBUF - 1 into the buffer read in stage
-  // st - 1, compute on this stage's buffer, then make stage st + 1 complete
-  // (this wave's copies, then everyone's) before moving on
-  auto stage = [&](int st, const uint8_t* cur, uint8_t* pf, uint8_t* spare1, uint8_t* spare2)
-      __attribute__((always_inline)) {
-    if (st + NBUF - 1 < nst) issue(pf, st + NBUF - 1);
-    if constexpr (LR_LDS) {
-      if (st == nst - 1) issue_lowrank(spare1, spare2);
-    }
-
-    compute(cur);
-    // copies issued after stage st + 1's: stages st + 2 .. min(st + NBUF - 1, nst - 1)
-    const int newer = min(NBUF - 2, nst - 2 - st);
-    wait_stages<SLOTS, NBUF - 2>(newer);
-    barrier_lds();
   };
 
   // the tile's per-column epilogue constants: s2 * second[n] and bias[n]
@@ -401,24 +434,43 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_kernel(
     g_epi[TN + tid] = bv;
   }
   __syncthreads();  // the epilogue constants' loads are complete before any copy is in flight
+  // stages 0 .. NBUF - 1 in flight; stage 0 complete; its first group's operands and scales into registers
 #pragma unroll
-  for (int u = 0; u < NBUF - 1; ++u)
+  for (int u = 0; u < NBUF; ++u)
     if (u < nst) issue(g_stage[u], u);
-  wait_stages<SLOTS, NBUF - 2>(min(NBUF - 2, nst - 1));  // stage 0 complete
+  wait_stages<SLOTS, NBUF - 1>(min(NBUF - 1, nst - 1));
   barrier_lds();
+#pragma unroll
+  for (int bn = 0; bn < WBN; ++bn) {
+    read_w(g_stage[0], bn, 0);
+    read_ws(g_stage[0], bn);
+  }
+#pragma unroll
+  for (int bm = 0; bm < WBM; ++bm) {
+    read_x(g_stage[0], bm, 0);
+    read_xs(g_stage[0], bm);
+  }
+  // unrolled by NBUF so every LDS address is static
   for (int st = 0; st < nst; st += NBUF) {
 #pragma unroll
     for (int u = 0; u < NBUF; ++u)
-      if (st + u < nst)
-        stage(st + u, g_stage[u], g_stage[(u + NBUF - 1) % NBUF], g_stage[(u + 1) % NBUF],
-              g_stage[(u + 2) % NBUF]);
+      if (st + u < nst) stage(st + u, g_stage[u], g_stage[(u + 1) % NBUF]);
   }
   if constexpr (C::PIPE) {
     fma_half(kLast, 0);
     fma_half(kLast, 1);
   }
+  wait_vm_lgkm0<0>();  // the low-rank copies (and the reads past the last stage) complete
+  barrier_lds();
 
   // ---------------- epilogue ----------------
+  v16f accv[WBN][WBM];
+#pragma unroll
+  for (int a = 0; a < WBN; ++a)
+#pragma unroll
+    for (int b = 0; b < WBM; ++b)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) accv[a][b][v] = acc[a][b][v];
 #pragma unroll
   for (int bn = 0; bn < WBN; ++bn) {
     const int nl = 32 * (WBN * wn + bn);
@@ -428,7 +480,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_kernel(
 #pragma unroll
       for (int bm = 0; bm < WBM; ++bm)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) acc[bn][bm][4 * qd + e] *= cm[e];
+        for (int e = 0; e < 4; ++e) accv[bn][bm][4 * qd + e] *= cm[e];
     }
   }
   if constexpr (LR_LDS) {
@@ -448,11 +500,11 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_kernel(
       for (int bn = 0; bn < WBN; ++bn)
 #pragma unroll
         for (int bm = 0; bm < WBM; ++bm)
-          acc[bn][bm] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, ua[bn]),
-                                                                __builtin_bit_cast(v8bf, lb[bm]), acc[bn][bm], 0, 0, 0);
+          accv[bn][bm] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, ua[bn]),
+                                                                __builtin_bit_cast(v8bf, lb[bm]), accv[bn][bm], 0, 0, 0);
     }
   } else if constexpr (RB > 0) {
-    constexpr int RC = 2;
+    constexpr int RC = 1;
     const rsrc_t ubuf = make_rsrc(up, (uint32_t)((int64_t)N * RB * 32));
     const rsrc_t lbuf = make_rsrc(la, (uint32_t)((int64_t)M * la_row));
 #pragma unroll
@@ -485,8 +537,8 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_kernel(
         for (int bm = 0; bm < WBM; ++bm)
 #pragma unroll
           for (int kk = 0; kk < RC; ++kk)
-            acc[bn][bm] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, ua[bn][kk]),
-                                                                  __builtin_bit_cast(v8bf, lb[bm][kk]), acc[bn][bm],
+            accv[bn][bm] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, ua[bn][kk]),
+                                                                  __builtin_bit_cast(v8bf, lb[bm][kk]), accv[bn][bm],
                                                                   0, 0, 0);
     }
   }
@@ -513,7 +565,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_kernel(
         float o[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          float t = acc[bn][bm][4 * qd + e] + cb[e];
+          float t = accv[bn][bm][4 * qd + e] + cb[e];
           if (GELU) t = gelu_tanh_f32(t);
           o[e] = t;
         }
