@@ -130,8 +130,9 @@ def summarize_traffic(d: Path) -> int:
 
 def bench_dit(args) -> int:
     """Config 4: one Flux-dev-shaped denoiser forward (batch 1, 4096 image + 512 text tokens, 19 + 38
-    blocks), every linear W4A4 rank 32 vs the same model with bf16 nn.Linear GEMMs; bf16 SDPA in
-    both. Each model's forward is captured once in a HIP graph and replayed ``--steps`` times."""
+    blocks), every block linear W4A4 rank 32 (the one-token adaLN modulation linears AWQ W4A16, as an svdq
+    checkpoint stores them) vs the same model with bf16 nn.Linear GEMMs; bf16 SDPA in both. Each model's
+    forward is captured once in a HIP graph and replayed ``--steps`` times."""
     import gc
 
     import torch
@@ -164,6 +165,7 @@ def bench_dit(args) -> int:
            "config": {"workload": "flux_dit_c4", "hidden": cfg.hidden, "heads": cfg.heads, "mlp": cfg.mlp,
                       "dual_blocks": cfg.n_dual, "single_blocks": cfg.n_single, "img_tokens": cfg.img_tokens,
                       "txt_tokens": cfg.txt_tokens, "rank": cfg.rank, "attention": "bf16 SDPA",
+                      "modulation": "AWQ W4A16 g64 (one token)",
                       "timing": "forward captured in one HIP graph, replayed"},
            "bf16_gemm_ms": round(res["bf16"], 3), "speedup_vs_bf16": round(res["bf16"] / res["w4a4"], 4),
            "block_linear_int_ops": ops_, "outputs_finite": {"w4a4": res["w4a4_finite"], "bf16": res["bf16_finite"]}}
@@ -281,6 +283,56 @@ def bench_qkv(args) -> int:
     return 0
 
 
+def bench_mod(args) -> int:
+    """The adaLN modulation linears of the config-4 DiT (one token, K=3072): the AWQ W4A16 GEMV
+    (``awq_w4a16_mm``) at the dual-block (N=18432) and single-block (N=9216) shapes, M = 1 and 2, against
+    the same layer as an SVDQuant W4A4 module (act-quant + GEMM) and as a bf16 linear. Each variant runs
+    ``--steps`` calls in one HIP graph; the GEMV's bound is HBM (its weight, scale and zero bytes)."""
+    import torch
+
+    import gen_worker_amd  # noqa: F401
+    from gen_worker_amd import _native, synthetic
+    from gen_worker_amd.flux_dit import _awq_linear
+
+    _native.load()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    k, r = 3072, 32
+    rows = []
+    for n in (18432, 9216):
+        awq_mod = _awq_linear(k, n, 5, dev)
+        L = synthetic.w4a4_layer(n, k, r)
+        w4 = _w4a4_module(torch, L, dev)
+        wb, bb = L.w_res.to(dev, torch.bfloat16), L.bias.to(dev, torch.bfloat16)
+        for m in (1, 2):
+            x = synthetic.activation(m, k, outlier_frac=0.0, outlier_scale=1.0).to(dev)
+            fns = {"awq_w4a16": lambda: awq_mod(x), "w4a4": lambda: w4(x),
+                   "bf16": lambda: torch.nn.functional.linear(x, wb, bb)}
+            row = {"M": m, "N": n, "K": k}
+            for name, fn in fns.items():
+                for _ in range(args.warmup):
+                    fn()
+                torch.cuda.synchronize()
+                row[name + "_us"] = round(graph_time_ms(torch, fn, args.steps) * 1e3, 2)
+            byt = n * k // 2 + 2 * n * (k // 64) * 2 + m * k * 2 + n * 2 + m * n * 2
+            row["awq_GBps"] = round(byt / row["awq_w4a16_us"] / 1e3, 1)
+            row["awq_frac_hbm_peak"] = round(row["awq_GBps"] / HBM_PEAK_GBS, 4)
+            log(f"bench: modulation {row}")
+            rows.append(row)
+    big = rows[0]
+    out = {"metric": "AWQ W4A16 modulation GEMV GB/s (M=1, K=3072 -> N=18432)",
+           "value": big["awq_GBps"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "ms_per_step": round(big["awq_w4a16_us"] / 1e3, 5), "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "dtype": "uint4 x bf16", "data": "synthetic",
+           "config": {"workload": "awq_modulation_c4", "K": k, "N": [18432, 9216], "M": [1, 2],
+                      "timing": "K calls in one HIP graph replay"},
+           "roofline": {"bound": "hbm", "achieved": big["awq_GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": big["awq_frac_hbm_peak"], "kernel": "awq_w4a16_gemv_kernel<1>"},
+           "rows": rows}
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -290,11 +342,11 @@ def main() -> int:
     ap.add_argument("--cpu-rows", type=int, default=512, help="rows of the bounded CPU sample")
     ap.add_argument("--only", choices=("step", "gemm", "quant", "copy"), default=None)
     ap.add_argument("--iters", type=int, default=5)
-    ap.add_argument("--workload", choices=("c1", "mlp", "qkv", "dit"), default="c1",
+    ap.add_argument("--workload", choices=("c1", "mlp", "qkv", "dit", "mod"), default="c1",
                     help="c1: the config-1 linear (the default bench line); mlp: config 2, fc1 -> GELU -> fc2 "
                          "(fused, unfused, bf16); qkv: config 3, the QKV sweep over M and output dtype (W4A4, "
                          "W8A8, bf16); dit: the config-4 Flux-shaped DiT step, W4A4 vs the same model with bf16 "
-                         "GEMMs")
+                         "GEMMs; mod: the DiT's one-token modulation linears (AWQ W4A16 GEMV vs W4A4 vs bf16)")
     ap.add_argument("--summarize-traffic", metavar="DIR", default=None,
                     help="write profiles/w4a4_gemm_c1_traffic.json from the FETCH_SIZE / WRITE_SIZE runs in DIR "
                          "(subdirectories f_<w>, w_<w> for w in gemm, quant, copy)")
@@ -305,7 +357,7 @@ def main() -> int:
         if args.gpus != 1:
             print("bench.py measures one GPU only", file=sys.stderr)
             return 2
-        return {"dit": bench_dit, "mlp": bench_mlp, "qkv": bench_qkv}[args.workload](args)
+        return {"dit": bench_dit, "mlp": bench_mlp, "qkv": bench_qkv, "mod": bench_mod}[args.workload](args)
 
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}): this build's path is a single-GPU "

@@ -263,6 +263,24 @@ int gwa_w8a8_gemm(const int8_t* qa, const int8_t* qw, const float* sa, const flo
                   const void* bias, int bias_dtype, void* out, int out_dtype,
                   int64_t M, int64_t N, int64_t K, void* stream);
 
+/* AWQ W4A16 linear (the M = 1 adaLN modulation layers).
+ * Replaces cozy_gen_worker::awq_w4a16_mm (models/svdq_awq_packed.py:48-115;
+ * schema "(Tensor x2, Tensor weight, Tensor wscales, Tensor wzeros, Tensor? bias) -> Tensor"):
+ *   y[m, n] = sum_k RN_bf16(code[n, k] * wscales[n, k/64] + wzeros[n, k/64]) * x[m, k] + bias[n]
+ * in fp32, rounded to bf16.
+ *   x bf16 [M, K] (row stride ldx, 16-byte aligned); weight uint8 [N, K/2] (code of column 2j in the
+ *   low nibble of byte j, 0..15); wscales, wzeros bf16 [N, K/64]; bias bf16 [N] or NULL; out bf16 [M, N].
+ * N % 16 == 0, K % 128 == 0 (models/svdq_awq_packed.py:23-24), K <= 32768. */
+int gwa_awq_w4a16_mm(const void* x, int64_t ldx, const void* weight, const void* wscales, const void* wzeros,
+                     const void* bias, void* out, int64_t M, int64_t N, int64_t K, void* stream);
+
+/* AWQ W4A16 weight -> bf16 [N, K] (16-byte aligned), the values gwa_awq_w4a16_mm multiplies by:
+ * the dequantized weight of the reference's decode path (models/svdq_awq.py:74-82, rounded to bf16 as
+ * decode_awq_linear's copy into a bf16 Linear does, :112-114). For callers with many activation rows
+ * (a library GEMM follows). K % 64 == 0. */
+int gwa_awq_w4a16_dequant(const void* weight, const void* wscales, const void* wzeros, void* out,
+                          int64_t N, int64_t K, void* stream);
+
 /* Row-major 2-D transpose of 1/2/4-byte elements: dst[c, r] = src[r, c].
  * Layout plumbing for the reference's K-major operands (wq_kn [K/2, N] of
  * models/svdq_fused.py:214, proj_down [in, rank] of :506-507). */

@@ -10,12 +10,14 @@ side and project their concatenation). The timestep / guidance / pooled-text
 conditioning enters as a seeded random embedding ``temb`` [1, 3072].
 
 Every linear is built by a factory, so the same model runs as:
-  * ``"w4a4"``: every linear an SVDQuant W4A4 layer (``SvdqW4A4Linear``, rank
-    32, group 64; int4 codes, fp16 scales, low-rank factors and bias random),
-    GELU fused into the fc1 epilogues, and each MLP's second linear quantized
-    in the first one's epilogue (``svdq_pair_forward``; in the single blocks
-    ``svdq_concat_forward`` builds proj_out's input [attention, MLP] without
-    the concatenation);
+  * ``"w4a4"``: every block linear an SVDQuant W4A4 layer (``SvdqW4A4Linear``,
+    rank 32, group 64; int4 codes, fp16 scales, low-rank factors and bias
+    random), GELU fused into the fc1 epilogues, and each MLP's second linear
+    quantized in the first one's epilogue (``svdq_pair_forward``; in the
+    single blocks ``svdq_concat_forward`` builds proj_out's input [attention,
+    MLP] without the concatenation); the blocks' adaLN modulation linears
+    (one token) AWQ W4A16 (``AwqPackedLinear``), the format an svdq
+    checkpoint keeps them in;
   * ``"bf16"``: every linear a bf16 ``nn.Linear`` (the bf16 GEMM path).
 Attention is bf16 ``scaled_dot_product_attention`` in both. Weights are
 random-init on the device from seeded generators; values are chosen only to
@@ -73,6 +75,23 @@ def _w4a4_linear(in_f: int, out_f: int, seed: int, device, rank: int, gelu: bool
     return mod
 
 
+def _awq_linear(in_f: int, out_f: int, seed: int, device) -> nn.Module:
+    """A random-init AWQ W4A16 modulation linear: uniform uint4 codes, bf16 group scales for an effective
+    weight std of ~0.02 and zeros centring the codes (w = code * s + z ~ 0 on average), bias ~ N(0, 0.02)."""
+    from .awq import AwqPackedLinear
+
+    g = torch.Generator(device=device).manual_seed(seed)
+    mod = AwqPackedLinear(in_f, out_f, bias=True, device=device)
+    with torch.no_grad():
+        mod.weight.copy_(torch.randint(0, 256, mod.weight.shape, generator=g, device=device, dtype=torch.int32)
+                         .to(torch.uint8))
+        sc = 0.02 / 4.61 * (0.75 + 0.5 * torch.rand(mod.wscales.shape, generator=g, device=device))
+        mod.wscales.copy_(sc.to(torch.bfloat16))
+        mod.wzeros.copy_((-7.5 * sc).to(torch.bfloat16))
+        mod.bias.copy_(torch.randn(out_f, generator=g, device=device).mul_(0.02).to(torch.bfloat16))
+    return mod
+
+
 class _Bf16Linear(nn.Module):
     """bf16 nn.Linear (weights ~ N(0, 0.02)) with the same optional GELU-tanh as the fused lane."""
 
@@ -96,6 +115,17 @@ def linear_factory(kind: str, device, rank: int) -> Callable[..., nn.Module]:
         return lambda i, o, s, gelu=False: _w4a4_linear(i, o, s, device, rank, gelu)
     if kind == "bf16":
         return lambda i, o, s, gelu=False: _Bf16Linear(i, o, s, device, gelu)
+    raise ValueError(f"linear kind {kind!r} not in ('w4a4', 'bf16')")
+
+
+def modulation_factory(kind: str, device) -> Callable[..., nn.Module]:
+    """``make(in_f, out_f, seed)`` for the adaLN modulation linears: an svdq checkpoint keeps them as AWQ
+    W4A16 (``models/svdq_awq.py:1``), so the "w4a4" model runs them through the AWQ GEMV; "bf16" keeps
+    bf16 linears."""
+    if kind == "w4a4":
+        return lambda i, o, s: _awq_linear(i, o, s, device)
+    if kind == "bf16":
+        return lambda i, o, s: _Bf16Linear(i, o, s, device)
     raise ValueError(f"linear kind {kind!r} not in ('w4a4', 'bf16')")
 
 
@@ -131,11 +161,12 @@ def _mlp(fc1: nn.Module, fc2: nn.Module, x: Tensor, fused: bool) -> Tensor:
 
 
 class DualBlock(nn.Module):
-    def __init__(self, cfg: FluxDiTConfig, make, seed: int, device, fused: bool = False) -> None:
+    def __init__(self, cfg: FluxDiTConfig, make, seed: int, device, fused: bool = False, make_mod=None) -> None:
         super().__init__()
         c = cfg.hidden
         self.cfg, self.fused = cfg, fused
-        self.mod_img, self.mod_txt = make(c, 6 * c, seed), make(c, 6 * c, seed + 1)
+        make_mod = make_mod or (lambda i, o, s: make(i, o, s))
+        self.mod_img, self.mod_txt = make_mod(c, 6 * c, seed), make_mod(c, 6 * c, seed + 1)
         self.qkv_img, self.qkv_txt = make(c, 3 * c, seed + 2), make(c, 3 * c, seed + 3)
         self.o_img, self.o_txt = make(c, c, seed + 4), make(c, c, seed + 5)
         self.fc1_img, self.fc1_txt = make(c, cfg.mlp, seed + 6, gelu=True), make(c, cfg.mlp, seed + 7, gelu=True)
@@ -168,11 +199,12 @@ class DualBlock(nn.Module):
 
 
 class SingleBlock(nn.Module):
-    def __init__(self, cfg: FluxDiTConfig, make, seed: int, device, fused: bool = False) -> None:
+    def __init__(self, cfg: FluxDiTConfig, make, seed: int, device, fused: bool = False, make_mod=None) -> None:
         super().__init__()
         c = cfg.hidden
         self.cfg, self.fused = cfg, fused
-        self.mod = make(c, 3 * c, seed)
+        make_mod = make_mod or (lambda i, o, s: make(i, o, s))
+        self.mod = make_mod(c, 3 * c, seed)
         self.qkv = make(c, 3 * c, seed + 1)
         self.mlp = make(c, cfg.mlp, seed + 2, gelu=True)
         self.proj_out = make(c + cfg.mlp, c, seed + 3)
@@ -201,14 +233,15 @@ class FluxDiT(nn.Module):
     def __init__(self, kind: str, cfg: FluxDiTConfig = FluxDiTConfig(), device="cuda", seed: int = 1000) -> None:
         super().__init__()
         make = linear_factory(kind, device, cfg.rank)
+        make_mod = modulation_factory(kind, device)
         self.cfg, self.kind = cfg, kind
         c = cfg.hidden
         self.x_embedder = make(cfg.in_channels, c, seed)
         self.context_embedder = make(cfg.txt_dim, c, seed + 1)
         fused = kind == "w4a4"
-        self.dual = nn.ModuleList(DualBlock(cfg, make, seed + 100 + 10 * i, device, fused)
+        self.dual = nn.ModuleList(DualBlock(cfg, make, seed + 100 + 10 * i, device, fused, make_mod)
                                   for i in range(cfg.n_dual))
-        self.single = nn.ModuleList(SingleBlock(cfg, make, seed + 400 + 10 * i, device, fused)
+        self.single = nn.ModuleList(SingleBlock(cfg, make, seed + 400 + 10 * i, device, fused, make_mod)
                                     for i in range(cfg.n_single))
         self.norm_out = make(c, 2 * c, seed + 2)
         self.proj_out = make(c, cfg.in_channels, seed + 3)

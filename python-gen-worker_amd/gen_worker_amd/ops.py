@@ -38,6 +38,10 @@ separate steps):
 * ``svdq_group_psums(qa, qw)``: exact int32 per-group partial sums (debug).
 * ``w8a8_quant(x2) -> (q, sa)`` and ``w8a8_scaled_mm(qa, weight, sa,
   weight_scale, bias, out_dtype)``: the int8 lane.
+* ``awq_w4a16_mm(x2, weight, wscales, wzeros, bias)``: the reference's packed
+  AWQ W4A16 op (``models/svdq_awq_packed.py:48-115``, same name and schema)
+  for the M = 1 modulation layers, and ``awq_w4a16_dequant(weight, wscales,
+  wzeros)``: its weight as bf16.
 
 Every op runs on the current HIP stream and allocates its outputs with
 ``torch.empty`` on the input's device, as the reference launchers do
@@ -694,6 +698,74 @@ def w8a8_scaled_mm(qa: Tensor, weight: Tensor, sa: Tensor, weight_scale: Tensor,
 @w8a8_scaled_mm.register_fake
 def _(qa, weight, sa, weight_scale, bias, out_dtype):
     return qa.new_empty(int(qa.shape[0]), int(weight.shape[0]), dtype=out_dtype)
+
+
+# ---------------------------------------------------------------------------
+# AWQ W4A16 (the adaLN modulation layers)
+# ---------------------------------------------------------------------------
+
+AWQ_GEMV_MAX_M = 16   # activation rows up to which the GEMV kernel runs; above, dequant + library GEMM
+
+
+def _awq_check(name: str, weight: Tensor, wscales: Tensor, wzeros: Tensor, k: Optional[int]) -> tuple[int, int]:
+    _check_dtype(name, weight, torch.uint8, what="weight")
+    _check_dtype(name, wscales, torch.bfloat16, what="wscales")
+    _check_dtype(name, wzeros, torch.bfloat16, what="wzeros")
+    n, kk = int(weight.shape[0]), 2 * int(weight.shape[1])
+    if k is not None and kk != k:
+        raise SvdqOpError(f"{name}: weight {tuple(weight.shape)} holds K={kk} columns, x has K={k}")
+    if n % 16 or kk % 128:
+        raise SvdqOpError(f"{name}: [N={n}, K={kk}] breaks the packed contract (N % 16, K % 128)")
+    if tuple(wscales.shape) != (n, kk // GROUP) or tuple(wzeros.shape) != (n, kk // GROUP):
+        raise SvdqOpError(f"{name}: wscales {tuple(wscales.shape)} / wzeros {tuple(wzeros.shape)} must be "
+                          f"[{n}, {kk // GROUP}]")
+    return n, kk
+
+
+@torch.library.custom_op("cozy_gen_worker::awq_w4a16_dequant", mutates_args=())
+def awq_w4a16_dequant(weight: Tensor, wscales: Tensor, wzeros: Tensor) -> Tensor:
+    """bf16 [N, K] = RN_bf16(code * wscales + wzeros): the weight ``awq_w4a16_mm`` multiplies by."""
+    name = "awq_w4a16_dequant"
+    _check_cuda(name, weight=weight, wscales=wscales, wzeros=wzeros)
+    n, k = _awq_check(name, weight, wscales, wzeros, None)
+    out = torch.empty(n, k, dtype=torch.bfloat16, device=weight.device)
+    nat.call("gwa_awq_w4a16_dequant", nat.ptr(weight), nat.ptr(wscales), nat.ptr(wzeros), nat.ptr(out), n, k,
+             nat.stream_of(weight))
+    return out
+
+
+@awq_w4a16_dequant.register_fake
+def _(weight, wscales, wzeros):
+    return weight.new_empty(int(weight.shape[0]), 2 * int(weight.shape[1]), dtype=torch.bfloat16)
+
+
+@torch.library.custom_op("cozy_gen_worker::awq_w4a16_mm", mutates_args=())
+def awq_w4a16_mm(x2: Tensor, weight: Tensor, wscales: Tensor, wzeros: Tensor, bias: Optional[Tensor]) -> Tensor:
+    """The reference's packed AWQ op (``models/svdq_awq_packed.py:48-115``, same name and schema):
+    x2 bf16 [M, K], weight uint8 [N, K/2] (column 2j in the low nibble of byte j), wscales / wzeros bf16
+    [N, K/64], bias bf16 [N] or None -> bf16 [M, N]. Up to ``AWQ_GEMV_MAX_M`` rows run the HIP GEMV
+    (the weight read once per four rows); more rows dequantize the weight to bf16 once (HIP) and run a
+    library GEMM on it."""
+    name = "awq_w4a16_mm"
+    _check_dtype(name, x2, torch.bfloat16, what="x2")
+    _check_dtype(name, bias, torch.bfloat16, what="bias")
+    _check_cuda(name, x2=x2, weight=weight, wscales=wscales, wzeros=wzeros, bias=bias)
+    m, k = int(x2.shape[0]), int(x2.shape[1])
+    n, _ = _awq_check(name, weight, wscales, wzeros, k)
+    if bias is not None and bias.numel() != n:
+        raise SvdqOpError(f"{name}: bias has {bias.numel()} values for N={n}")
+    if m > AWQ_GEMV_MAX_M:
+        w = awq_w4a16_dequant(weight, wscales, wzeros)
+        return torch.nn.functional.linear(x2, w, bias)
+    out = torch.empty(m, n, dtype=torch.bfloat16, device=x2.device)
+    nat.call("gwa_awq_w4a16_mm", nat.ptr(x2), k, nat.ptr(weight), nat.ptr(wscales), nat.ptr(wzeros), nat.ptr(bias),
+             nat.ptr(out), m, n, k, nat.stream_of(x2))
+    return out
+
+
+@awq_w4a16_mm.register_fake
+def _(x2, weight, wscales, wzeros, bias):
+    return x2.new_empty(int(x2.shape[0]), int(weight.shape[0]), dtype=torch.bfloat16)
 
 
 # ---------------------------------------------------------------------------

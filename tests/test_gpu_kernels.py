@@ -501,14 +501,16 @@ def test_w8a8_module_config0():
 
 
 def test_flux_dit_small_matches_oracle_chain():
-    """A small Flux-shaped DiT (1 dual + 1 single block) with every linear W4A4 against the same model with
-    each linear replaced by the dequantize-then-matmul oracle (float64, output rounded to bf16 like the
-    kernels). Every other op is shared, so the two differ only by the per-layer output error and the rare
+    """A small Flux-shaped DiT (1 dual + 1 single block) with every block linear W4A4 (the adaLN modulation
+    linears AWQ W4A16) against the same model with each linear replaced by its dequantize-then-matmul
+    oracle (float64, output rounded to bf16 like the kernels). Every other op is shared, so the two differ only by the per-layer output error and the rare
     activation codes that flip when an input differs by one bf16 ulp."""
     import copy
 
+    from gen_worker_amd.awq import AwqPackedLinear
     from gen_worker_amd.flux_dit import FluxDiT, FluxDiTConfig, inputs
     from gen_worker_amd.svdq import SvdqW4A4Linear
+    from oracle import awq_oracle as AO
 
     cfg = FluxDiTConfig(hidden=512, heads=4, head_dim=128, mlp=2048, n_dual=1, n_single=1, img_tokens=192,
                         txt_tokens=64, in_channels=64, txt_dim=256, rank=32)
@@ -538,16 +540,37 @@ def test_flux_dit_small_matches_oracle_chain():
                               self.b, second=self.second, gelu=self.gelu)
             return torch.from_numpy(y.astype(np.float32)).to(DEV).to(torch.bfloat16).reshape(*lead, self.n)
 
-    seen = []
+    class _OracleAwq(torch.nn.Module):
+        """The AWQ W4A16 modulation linears through the AWQ oracle on the module's own bytes."""
+
+        def __init__(self, mod):
+            super().__init__()
+            self.k, self.n = mod.in_features, mod.out_features
+            wb = mod.weight.cpu().numpy()
+            self.codes = np.stack([wb & 0xF, wb >> 4], axis=-1).reshape(self.n, self.k).astype(np.uint8)
+            self.s, self.z = bits16(mod.wscales.cpu()), bits16(mod.wzeros.cpu())
+            self.b = bits16(mod.bias.cpu()) if mod.bias is not None else None
+
+        def forward(self, x):
+            lead = x.shape[:-1]
+            y = AO.awq_linear(bits16(x.reshape(-1, self.k).cpu()), self.codes, self.s, self.z, self.b)
+            return torch.from_numpy(y.astype(np.float32)).to(DEV).to(torch.bfloat16).reshape(*lead, self.n)
+
+    seen, seen_awq = [], []
     hooks = [m.register_forward_hook(lambda m_, inp, out: seen.append((m_, inp[0].detach(), out.detach())))
              for m in unfused.modules() if isinstance(m, SvdqW4A4Linear)]
-    n_swapped = 0
+    hooks += [m.register_forward_hook(lambda m_, inp, out: seen_awq.append((m_, inp[0].detach(), out.detach())))
+              for m in unfused.modules() if isinstance(m, AwqPackedLinear)]
+    n_swapped = n_awq = 0
     for mod in list(ref_model.modules()):
         for cname, child in list(mod.named_children()):
             if isinstance(child, SvdqW4A4Linear):
                 setattr(mod, cname, _OracleLinear(child))
                 n_swapped += 1
-    assert n_swapped == 4 + 10 + 4
+            elif isinstance(child, AwqPackedLinear):
+                setattr(mod, cname, _OracleAwq(child))
+                n_awq += 1
+    assert n_swapped == 4 + 8 + 3 and n_awq == 2 + 1
     args = inputs(cfg, device=DEV)
     with torch.no_grad():
         y = model(*args).float()
@@ -562,6 +585,11 @@ def test_flux_dit_small_matches_oracle_chain():
         ref = O.w4a4_linear(bits16(x.reshape(-1, ol.k).cpu()), ol.sm, ol.qw, ol.sw, ol.down, ol.up, ol.b,
                             second=ol.second, gelu=ol.gelu)
         check_output(out.reshape(-1, ol.n), ref, what=f"{mod.in_features}->{mod.out_features} lane {mod.lane}")
+    assert len(seen_awq) == n_awq
+    for mod, x, out in seen_awq:
+        oa = _OracleAwq(mod)
+        ref = AO.awq_linear(bits16(x.reshape(-1, oa.k).cpu()), oa.codes, oa.s, oa.z, oa.b)
+        check_output(out.reshape(-1, oa.n), ref, what=f"awq {mod.in_features}->{mod.out_features}")
     # end to end: the chain amplifies the one-ulp input differences through code flips, layer norms and
     # attention, so the two models agree statistically, not to the per-layer bar
     assert y.shape == (cfg.img_tokens, cfg.in_channels)
