@@ -1,7 +1,8 @@
 """Benchmark of the SVDQuant W4A4 linear hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-    python bench.py --only {step,gemm,quant,copy} [--iters N]     (profiling driver)
+    python bench.py --only {step,gemm,quant,copy,awq} [--iters N] (profiling driver)
+    python bench.py --workload {mlp,qkv,dit,mod}                  (configs 2-4, modulation layers)
 
 A step is one pass of the hot path over one batch of synthetic input: the
 config-1 SVDQuant W4A4 linear (M = 4096 image + 512 text tokens = 4608,
@@ -333,6 +334,29 @@ def bench_mod(args) -> int:
     return 0
 
 
+def only_awq(args) -> int:
+    """``--only awq``: the dual-block modulation GEMV (M=1, K=3072 -> N=18432) eagerly ``--iters`` times
+    after 3 warmups, for rocprofv3."""
+    import torch
+
+    import gen_worker_amd  # noqa: F401
+    from gen_worker_amd import _native, synthetic
+    from gen_worker_amd.flux_dit import _awq_linear
+
+    _native.load()
+    dev = torch.device("cuda:0")
+    mod = _awq_linear(3072, 18432, 5, dev)
+    x = synthetic.activation(1, 3072, outlier_frac=0.0, outlier_scale=1.0).to(dev)
+    for _ in range(3):
+        mod(x)
+    torch.cuda.synchronize()
+    for _ in range(args.iters):
+        mod(x)
+    torch.cuda.synchronize()
+    log(f"bench: ran awq x{args.iters}")
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -340,7 +364,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-rows", type=int, default=512, help="rows of the bounded CPU sample")
-    ap.add_argument("--only", choices=("step", "gemm", "quant", "copy"), default=None)
+    ap.add_argument("--only", choices=("step", "gemm", "quant", "copy", "awq"), default=None)
     ap.add_argument("--iters", type=int, default=5)
     ap.add_argument("--workload", choices=("c1", "mlp", "qkv", "dit", "mod"), default="c1",
                     help="c1: the config-1 linear (the default bench line); mlp: config 2, fc1 -> GELU -> fc2 "
@@ -353,6 +377,8 @@ def main() -> int:
     args = ap.parse_args()
     if args.summarize_traffic:
         return summarize_traffic(Path(args.summarize_traffic))
+    if args.only == "awq":
+        return only_awq(args)
     if args.workload != "c1":
         if args.gpus != 1:
             print("bench.py measures one GPU only", file=sys.stderr)
