@@ -12,7 +12,9 @@ written as fp6 operand records) then kernel 2 (W4A4 GEMM on the fp6 MFMA +
 low-rank/bias epilogue). Inputs are resident in HBM before the timed region. The K timed
 steps are captured once into a HIP graph and replayed, so host launch cost
 is not part of the figure; the eager (per-op Python dispatch) rate is
-reported beside it. ``value`` is the linear's throughput in int-TOPS
+reported beside it. The timed replay follows at least 40 ms of untimed
+replays of the same graph: after an idle gap the shader clock ramps up over
+the first ~20 ms of load (the first replays run up to 15 % slower). ``value`` is the linear's throughput in int-TOPS
 (2*M*N*K per step).
 
 The ``roofline`` object covers the dominant kernel (the GEMM): its average
@@ -52,9 +54,14 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def graph_time_ms(torch, fn, reps: int) -> float:
-    """Average ms of ``fn`` from one replay of a HIP graph holding ``reps`` back-to-back calls,
-    timed with events on the stream the graph runs on."""
+WARM_MS = 40.0  # untimed load before a timed replay: the shader clock ramps up over the first ~20 ms of load
+
+
+def graph_time_ms(torch, fn, reps: int, warm_calls: int = 0) -> float:
+    """Average ms of ``fn`` per call from ONE timed replay of a HIP graph holding ``reps`` back-to-back calls,
+    synchronized on both sides and timed with events on the stream the graph runs on. Before it the graph is
+    replayed untimed for at least ``warm_calls`` calls and at least WARM_MS of load (page-in, and the clock
+    ramp: right after an idle gap the first ~20 ms of replays run up to 15 % slower than steady state)."""
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     g = torch.cuda.CUDAGraph()
@@ -63,11 +70,18 @@ def graph_time_ms(torch, fn, reps: int) -> float:
             for _ in range(reps):
                 fn()
     torch.cuda.synchronize()
-    g.replay()                                   # first replay: page-in, not timed
-    torch.cuda.synchronize()
+    cur = torch.cuda.current_stream()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
-    cur = torch.cuda.current_stream()
+    e0.record(cur)
+    g.replay()                                   # first replay: page-in; its time sizes the warm-up
+    e1.record(cur)
+    torch.cuda.synchronize()
+    first_ms = max(e0.elapsed_time(e1), 1e-3)
+    warm = max(-(-warm_calls // reps), int(WARM_MS / first_ms) + 1)
+    for _ in range(warm):
+        g.replay()
+    torch.cuda.synchronize()
     e0.record(cur)
     g.replay()
     e1.record(cur)
@@ -224,7 +238,7 @@ def bench_mlp(args) -> int:
            "ms_per_step": res["fused"]["ms"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
            "dtype": "int4", "data": "synthetic",
            "config": {"workload": "svdq_mlp_pair_c2", "M": m, "D": d, "H": h, "rank": r, "group": 64,
-                      "timing": "K calls in one HIP graph replay"},
+                      "timing": "K calls in one HIP graph replay, after >= 40 ms of untimed replays"},
            "pct_int8_peak": round(100 * res["fused"]["TOPS"] / INT8_PEAK_TOPS, 2), "variants": res,
            "speedup_fused_vs_unfused": round(res["unfused"]["ms"] / res["fused"]["ms"], 4),
            "speedup_fused_vs_bf16": round(res["bf16"]["ms"] / res["fused"]["ms"], 4)}
@@ -278,7 +292,7 @@ def bench_qkv(args) -> int:
            "ms_per_step": round(big["w4a4"]["us"] / 1e3, 5), "higher_is_better": True, "scaling": "weak",
            "vs_baseline": None, "dtype": "int4", "data": "synthetic",
            "config": {"workload": "qkv_sweep_c3", "K": k, "N": n, "rank": r, "M": list(c["ms"]),
-                      "value_at": "M=4608, bf16 out, W4A4", "timing": "K calls in one HIP graph replay"},
+                      "value_at": "M=4608, bf16 out, W4A4", "timing": "K calls in one HIP graph replay, after >= 40 ms of untimed replays"},
            "rows": rows}
     print(json.dumps(out), flush=True)
     return 0
@@ -326,7 +340,7 @@ def bench_mod(args) -> int:
            "ms_per_step": round(big["awq_w4a16_us"] / 1e3, 5), "higher_is_better": True, "scaling": "weak",
            "vs_baseline": None, "dtype": "uint4 x bf16", "data": "synthetic",
            "config": {"workload": "awq_modulation_c4", "K": k, "N": [18432, 9216], "M": [1, 2],
-                      "timing": "K calls in one HIP graph replay"},
+                      "timing": "K calls in one HIP graph replay, after >= 40 ms of untimed replays"},
            "roofline": {"bound": "hbm", "achieved": big["awq_GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                         "frac": big["awq_frac_hbm_peak"], "kernel": "awq_w4a16_gemv_kernel<1>"},
            "rows": rows}
@@ -443,15 +457,15 @@ def main() -> int:
 
     # timed region: K steps captured in one graph, one replay, synchronize on both sides
     log(f"bench: timing {args.steps} steps (graph)")
-    step_ms = graph_time_ms(torch, step, args.steps)
+    step_ms = graph_time_ms(torch, step, args.steps, warm_calls=args.warmup)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
         step()
     torch.cuda.synchronize()
     eager_ms = (time.perf_counter() - t0) * 1e3 / args.steps
-    gemm_ms = graph_time_ms(torch, gemm, args.steps)
-    quant_ms = graph_time_ms(torch, quant, args.steps)
+    gemm_ms = graph_time_ms(torch, gemm, args.steps, warm_calls=args.warmup)
+    quant_ms = graph_time_ms(torch, quant, args.steps, warm_calls=args.warmup)
 
     int_ops = w4a4_int_ops(m, n, k)
     value_tops = int_ops / (step_ms * 1e-3) / 1e12
@@ -503,7 +517,7 @@ def main() -> int:
         "data": "synthetic",
         "config": {"workload": "svdq_w4a4_linear_c1", "M": m, "N": n, "K": k, "rank": r, "group": 64,
                    "in_dtype": "bf16", "out_dtype": "bf16", "parallelism": "none",
-                   "timing": "K steps in one HIP graph replay"},
+                   "timing": "K steps in one HIP graph replay, after >= 40 ms of untimed replays"},
         "roofline": {"bound": "mfma", "achieved": round(gemm_tops, 2), "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
                      "frac": round(gemm_tops / INT8_PEAK_TOPS, 4), "traffic": traffic,
                      "kernel": "w4a4_gemm_fp6_kernel", "algorithmic_ops_per_launch": int_ops,

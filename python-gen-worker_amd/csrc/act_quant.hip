@@ -387,19 +387,21 @@ __global__ __launch_bounds__(Q6_THREADS) void svdq_quant_fp6_kernel(
 }
 
 // la = RN_bf16(sum over p of part[p]) in the order p = 0, 1, ...: one thread per 4 consecutive values, the
-// partials loaded 8 at a time (independent loads in flight) and added in order.
+// partials loaded 32 at a time (a small-M launch has up to K/128 slots and few threads: the loads of all of
+// them go out together, one memory round trip) and added in order.
 __global__ __launch_bounds__(256) void la_reduce_kernel(const float* __restrict__ part, int P, int64_t MR,
                                                          uint16_t* __restrict__ la) {
+  constexpr int kBatch = 32;
   const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
   if (i >= MR) return;
   v4f s = (v4f){0.f, 0.f, 0.f, 0.f};
-  for (int p0 = 0; p0 < P; p0 += 8) {
-    v4f v[8];
+  for (int p0 = 0; p0 < P; p0 += kBatch) {
+    v4f v[kBatch];
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
+    for (int u = 0; u < kBatch; ++u)
       v[u] = p0 + u < P ? *(const v4f*)(part + (int64_t)(p0 + u) * MR + i) : (v4f){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
+    for (int u = 0; u < kBatch; ++u)
       if (p0 + u < P) s = (p0 + u == 0) ? v[u] : s + v[u];
   }
   *(uint2*)(la + i) = make_uint2(pack_bf16x2_rn(s[0], s[1]), pack_bf16x2_rn(s[2], s[3]));
