@@ -2,7 +2,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
     python bench.py --only {step,gemm,quant,copy,awq} [--iters N] (profiling driver)
-    python bench.py --workload {mlp,qkv,dit,mod}                  (configs 2-4, modulation layers)
+    python bench.py --workload {mlp,qkv,dit,mod,nvfp4}            (configs 2-4, modulation layers, nvfp4 lane)
 
 A step is one pass of the hot path over one batch of synthetic input: the
 config-1 SVDQuant W4A4 linear (M = 4096 image + 512 text tokens = 4608,
@@ -348,6 +348,58 @@ def bench_mod(args) -> int:
     return 0
 
 
+def bench_nvfp4(args) -> int:
+    """The nvfp4 compatibility lane at the config-1 shape (M=4608, K=N=3072): the activation quantizer
+    (codes + flat scales + exact bf16 values; HBM-bound: x read, codes, scales and bf16 values written), the
+    module forward (quantizer + bf16 GEMM + scale and bias) and a bf16 linear, each over ``--steps`` calls in
+    one HIP graph."""
+    import torch
+
+    import gen_worker_amd  # noqa: F401
+    from gen_worker_amd import _native, nvfp4, synthetic
+
+    _native.load()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    c = synthetic.C1
+    m, n, k = c["m"], c["n"], c["k"]
+    g = torch.Generator().manual_seed(11)
+    w = torch.randn(n, k, generator=g) * 0.02
+    q, s, ws2 = nvfp4.quantize_nvfp4_tensor(w)
+    bias = (torch.randn(n, generator=g) * 0.02).to(torch.bfloat16)
+    mod = nvfp4.build_nvfp4_linear(q, nvfp4.to_blocked_scales(s), ws2.reshape(1, 1), bias=bias, device=dev)
+    x = synthetic.activation(m, k, outlier_frac=c["outlier_frac"], outlier_scale=c["outlier_scale"]).to(dev)
+    s2 = nvfp4.dynamic_input_scale(x)
+    wb = torch.ops.cozy_gen_worker.nvfp4_dequant(q.to(dev), s.view(torch.uint8).to(dev), False)
+    bd = bias.to(dev)
+    fns = {"quant": lambda: torch.ops.cozy_gen_worker.nvfp4_quant_act(x, s2, False, True),
+           "module": lambda: mod(x),
+           "bf16": lambda: torch.nn.functional.linear(x, wb, bd)}
+    res = {}
+    for name, fn in fns.items():
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        res[name] = graph_time_ms(torch, fn, args.steps, warm_calls=args.warmup)
+    qbytes = m * k * 2 + m * k // 2 + m * k // 16 + m * k * 2
+    qgbs = qbytes / (res["quant"] * 1e-3) / 1e9
+    ops_ = 2 * m * n * k
+    log(f"bench: nvfp4 quant {res['quant'] * 1e3:.1f} us ({qgbs:.0f} GB/s)  module {res['module'] * 1e3:.1f} us  "
+        f"bf16 {res['bf16'] * 1e3:.1f} us")
+    out = {"metric": "nvfp4 compatibility lane: module forward TOPS at the config-1 shape", "unit": "TOPS",
+           "value": round(ops_ / (res["module"] * 1e-3) / 1e12, 1), "n_gpus": 1, "steps": args.steps,
+           "warmup": args.warmup, "ms_per_step": round(res["module"], 5), "higher_is_better": True,
+           "scaling": "weak", "vs_baseline": None, "dtype": "e2m1 x e4m3 -> bf16 products", "data": "synthetic",
+           "config": {"workload": "nvfp4_linear_c1", "M": m, "N": n, "K": k, "block": 16, "s2": "dynamic",
+                      "timing": "K calls in one HIP graph replay, after >= 40 ms of untimed replays"},
+           "variants_us": {kk: round(v * 1e3, 2) for kk, v in res.items()},
+           "roofline": {"bound": "hbm", "kernel": "nvfp4_quant_act_kernel", "achieved": round(qgbs, 1),
+                        "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(qgbs / HBM_PEAK_GBS, 4),
+                        "algorithmic_bytes_per_launch": qbytes, "traffic": None}}
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def only_awq(args) -> int:
     """``--only awq``: the dual-block modulation GEMV (M=1, K=3072 -> N=18432) eagerly ``--iters`` times
     after 3 warmups, for rocprofv3."""
@@ -380,11 +432,12 @@ def main() -> int:
     ap.add_argument("--cpu-rows", type=int, default=512, help="rows of the bounded CPU sample")
     ap.add_argument("--only", choices=("step", "gemm", "quant", "copy", "awq"), default=None)
     ap.add_argument("--iters", type=int, default=5)
-    ap.add_argument("--workload", choices=("c1", "mlp", "qkv", "dit", "mod"), default="c1",
+    ap.add_argument("--workload", choices=("c1", "mlp", "qkv", "dit", "mod", "nvfp4"), default="c1",
                     help="c1: the config-1 linear (the default bench line); mlp: config 2, fc1 -> GELU -> fc2 "
                          "(fused, unfused, bf16); qkv: config 3, the QKV sweep over M and output dtype (W4A4, "
                          "W8A8, bf16); dit: the config-4 Flux-shaped DiT step, W4A4 vs the same model with bf16 "
-                         "GEMMs; mod: the DiT's one-token modulation linears (AWQ W4A16 GEMV vs W4A4 vs bf16)")
+                         "GEMMs; mod: the DiT's one-token modulation linears (AWQ W4A16 GEMV vs W4A4 vs bf16); "
+                         "nvfp4: the nvfp4 compatibility lane at the config-1 shape")
     ap.add_argument("--summarize-traffic", metavar="DIR", default=None,
                     help="write profiles/w4a4_gemm_c1_traffic.json from the FETCH_SIZE / WRITE_SIZE runs in DIR "
                          "(subdirectories f_<w>, w_<w> for w in gemm, quant, copy)")
@@ -397,7 +450,8 @@ def main() -> int:
         if args.gpus != 1:
             print("bench.py measures one GPU only", file=sys.stderr)
             return 2
-        return {"dit": bench_dit, "mlp": bench_mlp, "qkv": bench_qkv, "mod": bench_mod}[args.workload](args)
+        return {"dit": bench_dit, "mlp": bench_mlp, "qkv": bench_qkv, "mod": bench_mod,
+                "nvfp4": bench_nvfp4}[args.workload](args)
 
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}): this build's path is a single-GPU "

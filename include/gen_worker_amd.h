@@ -281,6 +281,44 @@ int gwa_awq_w4a16_mm(const void* x, int64_t ldx, const void* weight, const void*
 int gwa_awq_w4a16_dequant(const void* weight, const void* wscales, const void* wzeros, void* out,
                           int64_t N, int64_t K, void* stream);
 
+/* nvfp4 compatibility lane (the reference's modelopt nvfp4 contract: e2m1
+ * codes, element 2j in the low nibble; e4m3 scales per block of 16 along K;
+ * a second-level fp32 scale). Scale grids [rows, K/16] are flat or in the
+ * cuBLAS 128 x 4 blocked order of to_blocked_scales
+ * (models/nvfp4_quant.py:72-84), whose size is
+ * gwa_nvfp4_blocked_scale_numel(rows, K/16) (blocked_scale_numel, :87-89). */
+enum { GWA_NVFP4_SCALES_FLAT = 0, GWA_NVFP4_SCALES_BLOCKED = 1 };
+
+int64_t gwa_nvfp4_blocked_scale_numel(int64_t rows, int64_t kblocks);
+
+/* Activation quantization, bit-identical to quantize_activation_torch
+ * (models/nvfp4_quant.py:92-103; the op cozy_gen_worker::quant_nvfp4_act,
+ * :185-187):
+ *   x       bf16 [M, K] rows with stride ldx (elements), K % 16 == 0
+ *   s2      fp32 device scalar: the second-level scale
+ *   q       uint8 [M, K/2] codes (out)
+ *   scales  e4m3 bytes (out): flat [M, K/16] or blocked (only the real
+ *           entries are written; the caller zeroes the padding)
+ *   xdq     bf16 [M, K] (out, or NULL): code * e4m3 scale (exact), the
+ *           operand of the lane's bf16 GEMM (torch._scaled_mm's product,
+ *           models/w4a4.py:173-180, without s2) */
+int gwa_nvfp4_quant_act(const void* x, int64_t ldx, const float* s2, uint8_t* q, uint8_t* scales,
+                        int scale_layout, void* xdq, int64_t M, int64_t K, void* stream);
+
+/* codes uint8 [rows, K/2] + e4m3 scales (flat or blocked) -> bf16 [rows, K]
+ * = code * scale, exact (dequantize_nvfp4_tensor, models/w4a4.py:157-164,
+ * without the second-level scale). */
+int gwa_nvfp4_dequant(const uint8_t* q, const uint8_t* scales, int scale_layout, void* out, int64_t rows,
+                      int64_t K, void* stream);
+
+/* The module's epilogue after the bf16 GEMM (_W4A4Linear.forward,
+ * models/w4a4.py:349-351), in place on y bf16 [M, N] (N % 8 == 0):
+ * y = RN_bf16(RN_bf16(y * c) + bias), c = RN_bf16(s2 * ws2) (s2, ws2 fp32
+ * device scalars; bias bf16 [N] or NULL), each step rounded as torch's bf16
+ * multiply and add round. */
+int gwa_nvfp4_scale_bias(void* y, const float* s2, const float* ws2, const void* bias, int64_t M, int64_t N,
+                         void* stream);
+
 /* Row-major 2-D transpose of 1/2/4-byte elements: dst[c, r] = src[r, c].
  * Layout plumbing for the reference's K-major operands (wq_kn [K/2, N] of
  * models/svdq_fused.py:214, proj_down [in, rank] of :506-507). */

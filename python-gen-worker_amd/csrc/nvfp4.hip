@@ -1,0 +1,230 @@
+// nvfp4 compatibility lane: the reference's modelopt nvfp4 W4A4 contract
+// (e2m1 codes, e4m3 scales per block of 16 along K, a second-level fp32
+// scale) on MI355X. CDNA4's block-scaled MFMA takes E8M0 scales per 32
+// elements, not e4m3 per 16, and a dequantized value code * scale has up to
+// 6 significant bits, more than any MX element format holds; it is exact in
+// bf16. So the lane quantizes activations exactly as the reference does and
+// runs the product on the exact bf16 values (a plain library GEMM).
+//
+// Activation quantization = quantize_activation_torch
+// (models/nvfp4_quant.py:92-103), per 16-element block of a row, in fp32:
+//   bmax  = max |x|                                   (exact)
+//   sa    = e4m3_rne(clamp(bmax / RN(6 * s2), 2^-9, 448))
+//   q_i   = x_i / RN(sa * s2)                         (IEEE division)
+//   code  = cast_e2m1(q_i) (:41-51): sign bit 8 when q < 0; magnitude = the
+//           number of bounds {0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0} below |q|,
+//           plus one at the ties |q| in {0.75, 1.75, 2.5}
+//   packed: element 2j in the low nibble of byte j (pack_e2m1, :54-56)
+// Scales are written flat [M, K/16] or in the cuBLAS 128 x 4 blocked order of
+// to_blocked_scales (:72-84): entry (r, c) at
+//   ((r / 128) * ncb + c / 4) * 512 + (r % 32) * 16 + ((r % 128) / 32) * 4 + c % 4,
+// ncb = ceil((K/16) / 4); padding entries are the caller's (zeros).
+// The same pass may also write the dequantized activations code * sa as bf16
+// (exact), the operand of the bf16 GEMM.
+//
+// Two lanes per block: 16 bytes of x in per lane, 4 bytes of codes and 16 of
+// bf16 values out, one scale byte per pair: HBM-bound.
+#include "gwa_common.h"
+
+namespace {
+
+constexpr int NV_THREADS = 256;
+
+// e2m1 code (sign bit 3) -> its value: magnitude m = code & 7 is 0 or 0.5 (m < 2), else
+// 2^((m >> 1) - 1) * (1 + (m & 1) / 2), built from its fp32 exponent and top mantissa bit
+__device__ __forceinline__ float e2m1_value(uint32_t code) {
+  const uint32_t m = code & 7u;
+  const uint32_t mag = m < 2u ? (m ? 0x3F000000u : 0u) : ((((m >> 1) + 126u) << 23) | ((m & 1u) << 22));
+  return __uint_as_float(mag | ((code & 8u) << 28));
+}
+
+// fp32 in [2^-9, 448] -> e4m3fn bits (bias 7, 3 mantissa bits), round to nearest, ties to even
+__device__ __forceinline__ uint32_t e4m3_rne(float v) {
+  const uint32_t u = __float_as_uint(v);
+  const int e = (int)(u >> 23) - 127;
+  if (e < -6) return (uint32_t)rintf(v * 512.0f);  // subnormal grid 2^-9 (8 = the smallest normal, code 8)
+  const uint32_t m = u & 0x7FFFFFu;
+  uint32_t r = m >> 20;
+  const uint32_t rem = m & 0xFFFFFu;
+  if (rem > 0x80000u || (rem == 0x80000u && (r & 1u))) ++r;
+  return ((uint32_t)(e + 7) << 3) + r;  // r == 8 carries into the exponent
+}
+
+__device__ __forceinline__ float e4m3_value(uint32_t c) {
+  const uint32_t ex = (c >> 3) & 15u, m = c & 7u;
+  return ex == 0 ? (float)m * (1.0f / 512.0f) : __uint_as_float(((ex + 120u) << 23) | (m << 20));
+}
+
+__device__ __forceinline__ uint32_t e2m1_code(float q) {
+  const float a = fabsf(q);
+  uint32_t c = (a > 0.25f) + (a > 0.75f) + (a > 1.25f) + (a > 1.75f) + (a > 2.5f) + (a > 3.5f) + (a > 5.0f);
+  c += (a == 0.75f) | (a == 1.75f) | (a == 2.5f);
+  return c | (q < 0.0f ? 8u : 0u);
+}
+
+__device__ __forceinline__ int64_t blocked_index(int64_t r, int64_t c, int64_t ncb) {
+  return ((r >> 7) * ncb + (c >> 2)) * 512 + (r & 31) * 16 + ((r & 127) >> 5) * 4 + (c & 3);
+}
+
+// Two lanes per block (lane pair 2p, 2p + 1 holds its elements 0-7 and 8-15), so every load and store of a
+// wave covers one contiguous run; the block maximum is one exchange within the pair.
+__global__ __launch_bounds__(NV_THREADS) void nvfp4_quant_act_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                                     const float* __restrict__ s2p,
+                                                                     uint8_t* __restrict__ q,
+                                                                     uint8_t* __restrict__ scales, int blocked,
+                                                                     uint16_t* __restrict__ xdq, int64_t M, int KB) {
+  const int64_t t = (int64_t)blockIdx.x * NV_THREADS + threadIdx.x;  // half-block index over [M, KB, 2]
+  if (t >= 2 * M * KB) return;  // the total is even: a pair is active together
+  const int64_t b = t >> 1;
+  const int h = (int)(t & 1);
+  const int64_t row = b / KB;
+  const int c = (int)(b - row * KB);
+  const v4i w = *(const v4i*)(x + row * ldx + 16 * c + 8 * h);
+  float v[8];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    v[2 * j] = bf16_lo((uint32_t)w[j]);
+    v[2 * j + 1] = bf16_hi((uint32_t)w[j]);
+  }
+  float bmax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) bmax = fmaxf(bmax, fabsf(v[i]));
+  bmax = fmaxf(bmax, __shfl_xor(bmax, 1));
+  const float s2 = *s2p;
+  float tq = bmax / (6.0f * s2);
+  tq = fminf(fmaxf(tq, 1.0f / 512.0f), 448.0f);
+  const uint32_t sc = e4m3_rne(tq);
+  const float sa = e4m3_value(sc);
+  const float den = sa * s2;
+  uint32_t codes = 0;
+  uint32_t dq[4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t code = e2m1_code(v[i] / den);
+    codes |= code << (4 * i);
+    if (xdq) {
+      const float d = e2m1_value(code) * sa;  // exact in bf16
+      const uint32_t bits = __float_as_uint(d) >> 16;
+      if (i & 1) dq[i >> 1] |= bits << 16;
+      else dq[i >> 1] = bits;
+    }
+  }
+  *(uint32_t*)(q + b * 8 + 4 * h) = codes;
+  if (h == 0) {
+    const int64_t ncb = (KB + 3) / 4;
+    scales[blocked ? blocked_index(row, c, ncb) : b] = (uint8_t)sc;
+  }
+  if (xdq) *(v4i*)(xdq + b * 16 + 8 * h) = (v4i){(int)dq[0], (int)dq[1], (int)dq[2], (int)dq[3]};
+}
+
+// codes [rows, K/2] + e4m3 scales (flat or blocked) -> bf16 [rows, K] = code * scale (exact)
+__global__ __launch_bounds__(NV_THREADS) void nvfp4_dequant_kernel(const uint8_t* __restrict__ q,
+                                                                   const uint8_t* __restrict__ scales, int blocked,
+                                                                   uint16_t* __restrict__ out, int64_t rows, int KB) {
+  const int64_t b = (int64_t)blockIdx.x * NV_THREADS + threadIdx.x;
+  if (b >= rows * KB) return;
+  const int64_t row = b / KB;
+  const int c = (int)(b - row * KB);
+  const int64_t ncb = (KB + 3) / 4;
+  const float sa = e4m3_value(scales[blocked ? blocked_index(row, c, ncb) : b]);
+  const uint2 w = *(const uint2*)(q + b * 8);
+  uint32_t dq[8];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const uint32_t code = ((i < 8 ? w.x : w.y) >> (4 * (i & 7))) & 15u;
+    const float d = e2m1_value(code) * sa;
+    const uint32_t bits = __float_as_uint(d) >> 16;
+    if (i & 1) dq[i >> 1] |= bits << 16;
+    else dq[i >> 1] = bits;
+  }
+  uint16_t* dst = out + b * 16;
+  *(v4i*)dst = (v4i){(int)dq[0], (int)dq[1], (int)dq[2], (int)dq[3]};
+  *(v4i*)(dst + 8) = (v4i){(int)dq[4], (int)dq[5], (int)dq[6], (int)dq[7]};
+}
+
+// y (bf16 [M, N], in place) = RN_bf16(RN_bf16(y * c) + bias), c = RN_bf16(s2 * ws2): the module's
+// `y * (s2 * weight_scale_2).to(y.dtype)` then `+ bias` (models/w4a4.py:349-351), each rounded to bf16 as
+// torch's bf16 ops round; 8 elements per thread
+__global__ __launch_bounds__(NV_THREADS) void nvfp4_scale_bias_kernel(uint16_t* __restrict__ y,
+                                                                      const float* __restrict__ s2,
+                                                                      const float* __restrict__ ws2,
+                                                                      const uint16_t* __restrict__ bias, int64_t M,
+                                                                      int N) {
+  const int64_t i = ((int64_t)blockIdx.x * NV_THREADS + threadIdx.x) * 8;
+  if (i >= M * N) return;
+  const float c = bf16_to_f32(f32_to_bf16(*s2 * *ws2));
+  const int n0 = (int)(i % N);
+  v4i w = *(const v4i*)(y + i);
+  v4i b = bias ? *(const v4i*)(bias + n0) : (v4i){0, 0, 0, 0};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float lo = bf16_to_f32(f32_to_bf16(bf16_lo((uint32_t)w[j]) * c));
+    float hi = bf16_to_f32(f32_to_bf16(bf16_hi((uint32_t)w[j]) * c));
+    if (bias) {
+      lo += bf16_lo((uint32_t)b[j]);
+      hi += bf16_hi((uint32_t)b[j]);
+    }
+    w[j] = (int)pack_bf16x2_rn(lo, hi);
+  }
+  *(v4i*)(y + i) = w;
+}
+
+}  // namespace
+
+extern "C" int gwa_nvfp4_scale_bias(void* y, const float* s2, const float* ws2, const void* bias, int64_t M,
+                                    int64_t N, void* stream) {
+  const char* what = "nvfp4_scale_bias";
+  GWA_REQUIRE(M >= 0 && N > 0 && N % 8 == 0 && M * N < (1ll << 40), "%s: bad shape [%lld, %lld] (N %% 8)", what,
+              (long long)M, (long long)N);
+  if (M == 0) return GWA_OK;
+  GWA_REQUIRE(y && s2 && ws2, "%s: null pointer", what);
+  GWA_REQUIRE(GWA_ALIGNED(y, 16) && GWA_ALIGNED(bias, 16) && GWA_ALIGNED(s2, 4) && GWA_ALIGNED(ws2, 4),
+              "%s: y and bias must be 16-byte aligned", what);
+  const int64_t threads = M * N / 8;
+  hipLaunchKernelGGL(nvfp4_scale_bias_kernel, dim3((unsigned)((threads + NV_THREADS - 1) / NV_THREADS)),
+                     dim3(NV_THREADS), 0, (hipStream_t)stream, (uint16_t*)y, s2, ws2, (const uint16_t*)bias, M,
+                     (int)N);
+  return gwa_check_launch(what);
+}
+
+extern "C" int64_t gwa_nvfp4_blocked_scale_numel(int64_t rows, int64_t kblocks) {
+  if (rows <= 0 || kblocks <= 0) return 0;
+  return (rows + 127) / 128 * 128 * ((kblocks + 3) / 4) * 4;
+}
+
+extern "C" int gwa_nvfp4_quant_act(const void* x, int64_t ldx, const float* s2, uint8_t* q, uint8_t* scales,
+                                   int scale_layout, void* xdq, int64_t M, int64_t K, void* stream) {
+  const char* what = "nvfp4_quant_act";
+  GWA_REQUIRE(M >= 0 && K > 0 && K % 16 == 0, "%s: K=%lld is not a multiple of 16", what, (long long)K);
+  GWA_REQUIRE(ldx >= K && ldx % 8 == 0, "%s: row stride %lld must be >= K and a multiple of 8", what,
+              (long long)ldx);
+  GWA_REQUIRE(scale_layout == GWA_NVFP4_SCALES_FLAT || scale_layout == GWA_NVFP4_SCALES_BLOCKED,
+              "%s: scale_layout %d", what, scale_layout);
+  GWA_REQUIRE(M * K < (1ll << 40), "%s: shape too large", what);
+  if (M == 0) return GWA_OK;
+  GWA_REQUIRE(x && s2 && q && scales, "%s: null pointer", what);
+  GWA_REQUIRE(GWA_ALIGNED(x, 16) && GWA_ALIGNED(q, 8) && GWA_ALIGNED(s2, 4) && GWA_ALIGNED(xdq, 16),
+              "%s: x and xdq must be 16-byte, q 8-byte aligned", what);
+  const int64_t halves = 2 * M * (K / 16);
+  hipLaunchKernelGGL(nvfp4_quant_act_kernel, dim3((unsigned)((halves + NV_THREADS - 1) / NV_THREADS)),
+                     dim3(NV_THREADS), 0, (hipStream_t)stream, (const uint16_t*)x, ldx, s2, q, scales,
+                     scale_layout == GWA_NVFP4_SCALES_BLOCKED ? 1 : 0, (uint16_t*)xdq, M, (int)(K / 16));
+  return gwa_check_launch(what);
+}
+
+extern "C" int gwa_nvfp4_dequant(const uint8_t* q, const uint8_t* scales, int scale_layout, void* out, int64_t rows,
+                                 int64_t K, void* stream) {
+  const char* what = "nvfp4_dequant";
+  GWA_REQUIRE(rows >= 0 && K > 0 && K % 16 == 0 && rows * K < (1ll << 40), "%s: bad shape [%lld, %lld]", what,
+              (long long)rows, (long long)K);
+  GWA_REQUIRE(scale_layout == GWA_NVFP4_SCALES_FLAT || scale_layout == GWA_NVFP4_SCALES_BLOCKED,
+              "%s: scale_layout %d", what, scale_layout);
+  if (rows == 0) return GWA_OK;
+  GWA_REQUIRE(q && scales && out, "%s: null pointer", what);
+  GWA_REQUIRE(GWA_ALIGNED(q, 8) && GWA_ALIGNED(out, 16), "%s: q must be 8-byte, out 16-byte aligned", what);
+  const int64_t blocks = rows * (K / 16);
+  hipLaunchKernelGGL(nvfp4_dequant_kernel, dim3((unsigned)((blocks + NV_THREADS - 1) / NV_THREADS)),
+                     dim3(NV_THREADS), 0, (hipStream_t)stream, q, scales,
+                     scale_layout == GWA_NVFP4_SCALES_BLOCKED ? 1 : 0, (uint16_t*)out, rows, (int)(K / 16));
+  return gwa_check_launch(what);
+}

@@ -21,6 +21,7 @@ LIB_NAME = "libgen_worker_amd.so"
 
 DT_BF16, DT_F16, DT_F32 = 0, 1, 2
 EPI_GELU_TANH = 1
+NVFP4_SCALES_FLAT, NVFP4_SCALES_BLOCKED = 0, 1
 EPI_LA_F32 = 2
 QFMT_INT4, QFMT_FP6 = 0, 1
 FP6_REC = 104   # bytes per fp6 operand record (GWA_FP6_REC)
@@ -66,9 +67,14 @@ _SIGNATURES: dict[str, tuple] = {
     "gwa_awq_w4a16_mm": (_vp, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp),
     "gwa_awq_w4a16_dequant": (_vp, _vp, _vp, _vp, _i64, _i64, _vp),
     "gwa_transpose_2d": (_vp, _vp, _i64, _i64, _i64, _vp),
+    "gwa_nvfp4_blocked_scale_numel": (_i64, _i64),
+    "gwa_nvfp4_quant_act": (_vp, _i64, _vp, _vp, _vp, _int, _vp, _i64, _i64, _vp),
+    "gwa_nvfp4_dequant": (_vp, _vp, _int, _vp, _i64, _i64, _vp),
+    "gwa_nvfp4_scale_bias": (_vp, _vp, _vp, _vp, _i64, _i64, _vp),
 }
 _RESTYPES = {"gwa_build_info": ctypes.c_char_p, "gwa_last_error": ctypes.c_char_p,
-             "gwa_svdq_quant_fp6_partials": ctypes.c_int64, "gwa_svdq_gemm_w4a4_fp6_next_partials": ctypes.c_int64}
+             "gwa_svdq_quant_fp6_partials": ctypes.c_int64, "gwa_svdq_gemm_w4a4_fp6_next_partials": ctypes.c_int64,
+             "gwa_nvfp4_blocked_scale_numel": ctypes.c_int64}
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
 

@@ -790,3 +790,130 @@ def _(x):
 def build_info() -> str:
     """Library build description (``cozy_kernels::build_info``, ``csrc/cozy_kernels/ops.cpp:23-27``)."""
     return f"torch={torch.__version__} {nat.build_info()}"
+
+
+# ---------------------------------------------------------------------------
+# nvfp4 compatibility lane
+# ---------------------------------------------------------------------------
+
+NVFP4_BLOCK = 16
+
+
+def nvfp4_blocked_scale_numel(rows: int, kblocks: int) -> int:
+    """Element count of the blocked scale layout (``blocked_scale_numel``, models/nvfp4_quant.py:87-89)."""
+    return int(nat.load().gwa_nvfp4_blocked_scale_numel(rows, kblocks))
+
+
+def _nvfp4_quant_impl(x2: Tensor, s2: Tensor, blocked: bool, dequant: bool) -> tuple[Tensor, Tensor, Tensor]:
+    name = "nvfp4_quant_act"
+    if x2.dim() != 2:
+        raise SvdqOpError(f"{name}: x2 must be 2-D, got {tuple(x2.shape)}")
+    _check_dtype(name, x2, torch.bfloat16, what="x2")
+    s2 = _scalar_f32(name, s2)
+    if s2 is None:
+        raise SvdqOpError(f"{name}: s2 is required")
+    if x2.stride(1) != 1:
+        x2 = x2.contiguous()
+    _check_cuda(name, s2=s2)
+    if not x2.is_cuda:
+        raise SvdqOpError(f"{name}: x2 is on {x2.device}; the nvfp4 lane runs on the GPU only")
+    m, k = int(x2.shape[0]), int(x2.shape[1])
+    if k % NVFP4_BLOCK:
+        raise SvdqOpError(f"{name}: K={k} is not a multiple of {NVFP4_BLOCK}")
+    kb = k // NVFP4_BLOCK
+    q = torch.empty(m, k // 2, dtype=torch.uint8, device=x2.device)
+    if blocked:
+        sc = torch.zeros(nvfp4_blocked_scale_numel(m, kb), dtype=torch.uint8, device=x2.device)
+    else:
+        sc = torch.empty(m, kb, dtype=torch.uint8, device=x2.device)
+    xdq = torch.empty(m, k, dtype=torch.bfloat16, device=x2.device) if dequant else x2.new_empty(0, k)
+    nat.call("gwa_nvfp4_quant_act", nat.ptr(x2), int(x2.stride(0)), nat.ptr(s2), nat.ptr(q), nat.ptr(sc),
+             nat.NVFP4_SCALES_BLOCKED if blocked else nat.NVFP4_SCALES_FLAT, nat.ptr(xdq) if dequant else None,
+             m, k, nat.stream_of(x2))
+    return q, sc, xdq
+
+
+@torch.library.custom_op("cozy_gen_worker::nvfp4_quant_act", mutates_args=())
+def nvfp4_quant_act(x2: Tensor, s2: Tensor, blocked: bool, dequant: bool) -> tuple[Tensor, Tensor, Tensor]:
+    """nvfp4 activation quantization, bit-identical to quantize_activation_torch (models/nvfp4_quant.py:92-103):
+    ``(codes uint8 [M, K/2], e4m3 scale bytes (flat [M, K/16] or blocked), dequantized bf16 [M, K] or [0, K])``;
+    the dequantized activations are code * scale without s2 (exact in bf16)."""
+    return _nvfp4_quant_impl(x2, s2, blocked, dequant)
+
+
+@nvfp4_quant_act.register_fake
+def _(x2, s2, blocked, dequant):
+    m, k = int(x2.shape[0]), int(x2.shape[1])
+    kb = k // NVFP4_BLOCK
+    sc = (x2.new_empty(((m + 127) // 128) * 128 * ((kb + 3) // 4) * 4, dtype=torch.uint8) if blocked
+          else x2.new_empty(m, kb, dtype=torch.uint8))
+    return (x2.new_empty(m, k // 2, dtype=torch.uint8), sc, x2.new_empty(m if dequant else 0, k))
+
+
+@torch.library.custom_op("cozy_gen_worker::quant_nvfp4_act", mutates_args=())
+def quant_nvfp4_act(x2: Tensor, s2: Tensor) -> tuple[Tensor, Tensor]:
+    """The reference op's contract (models/nvfp4_quant.py:185-187): (packed codes [M, K/2], e4m3 scales in the
+    cuBLAS blocked layout)."""
+    q, sc, _ = _nvfp4_quant_impl(x2, s2, True, False)
+    return q, sc.view(torch.float8_e4m3fn)
+
+
+@quant_nvfp4_act.register_fake
+def _(x2, s2):
+    m, k = int(x2.shape[0]), int(x2.shape[1])
+    kb = k // NVFP4_BLOCK
+    return (x2.new_empty(m, k // 2, dtype=torch.uint8),
+            x2.new_empty(((m + 127) // 128) * 128 * ((kb + 3) // 4) * 4, dtype=torch.float8_e4m3fn))
+
+
+@torch.library.custom_op("cozy_gen_worker::nvfp4_dequant", mutates_args=())
+def nvfp4_dequant(q: Tensor, scales: Tensor, blocked: bool) -> Tensor:
+    """codes uint8 [rows, K/2] + e4m3 scales (flat [rows, K/16] or blocked bytes) -> bf16 [rows, K] = code *
+    scale, exact (dequantize_nvfp4_tensor, models/w4a4.py:157-164, without the second-level scale)."""
+    name = "nvfp4_dequant"
+    if scales.dtype == torch.float8_e4m3fn:
+        scales = scales.view(torch.uint8)
+    _check_dtype(name, q, torch.uint8, what="q")
+    _check_dtype(name, scales, torch.uint8, what="scales")
+    _check_cuda(name, q=q, scales=scales)
+    if q.dim() != 2:
+        raise SvdqOpError(f"{name}: q must be [rows, K/2], got {tuple(q.shape)}")
+    rows, k = int(q.shape[0]), 2 * int(q.shape[1])
+    if k % NVFP4_BLOCK:
+        raise SvdqOpError(f"{name}: K={k} is not a multiple of {NVFP4_BLOCK}")
+    kb = k // NVFP4_BLOCK
+    need = nvfp4_blocked_scale_numel(rows, kb) if blocked else rows * kb
+    if scales.numel() != need:
+        raise SvdqOpError(f"{name}: {scales.numel()} scales for [{rows}, {kb}] blocks ({'blocked' if blocked else 'flat'}"
+                          f" layout needs {need})")
+    out = torch.empty(rows, k, dtype=torch.bfloat16, device=q.device)
+    nat.call("gwa_nvfp4_dequant", nat.ptr(q), nat.ptr(scales), nat.NVFP4_SCALES_BLOCKED if blocked else
+             nat.NVFP4_SCALES_FLAT, nat.ptr(out), rows, k, nat.stream_of(q))
+    return out
+
+
+@nvfp4_dequant.register_fake
+def _(q, scales, blocked):
+    return q.new_empty(int(q.shape[0]), 2 * int(q.shape[1]), dtype=torch.bfloat16)
+
+
+@torch.library.custom_op("cozy_gen_worker::nvfp4_scale_bias", mutates_args=("y",))
+def nvfp4_scale_bias(y: Tensor, s2: Tensor, ws2: Tensor, bias: Optional[Tensor]) -> None:
+    """In place on bf16 y [M, N]: y = RN_bf16(RN_bf16(y * RN_bf16(s2 * ws2)) + bias), the nvfp4 module's
+    epilogue (models/w4a4.py:349-351) in one pass."""
+    name = "nvfp4_scale_bias"
+    _check_dtype(name, y, torch.bfloat16, what="y")
+    _check_dtype(name, bias, torch.bfloat16, what="bias")
+    s2, ws2 = _scalar_f32(name, s2), _scalar_f32(name, ws2)
+    _check_cuda(name, y=y, s2=s2, ws2=ws2, bias=bias)
+    if y.dim() != 2 or int(y.shape[1]) % 8:
+        raise SvdqOpError(f"{name}: y must be [M, N] with N % 8 == 0, got {tuple(y.shape)}")
+    if bias is not None and bias.numel() != int(y.shape[1]):
+        raise SvdqOpError(f"{name}: bias has {bias.numel()} values for N={int(y.shape[1])}")
+    nat.call("gwa_nvfp4_scale_bias", nat.ptr(y), nat.ptr(s2), nat.ptr(ws2), nat.ptr(bias), int(y.shape[0]),
+             int(y.shape[1]), nat.stream_of(y))
+
+
+@nvfp4_scale_bias.register_fake
+def _(y, s2, ws2, bias):
+    return None
