@@ -305,6 +305,15 @@ int64_t gwa_nvfp4_blocked_scale_numel(int64_t rows, int64_t kblocks);
 int gwa_nvfp4_quant_act(const void* x, int64_t ldx, const float* s2, uint8_t* q, uint8_t* scales,
                         int scale_layout, void* xdq, int64_t M, int64_t K, void* stream);
 
+/* gwa_nvfp4_quant_act with the forward's dynamic second-level scale
+ * (models/w4a4.py:342-343: s2 = max(max|x| / (6 * 448), 1e-12), fp32)
+ * computed on the device: a first pass writes per-workgroup maxima into
+ * parts (fp32 scratch of 1024 values), the quantizer folds them and also
+ * writes s2 to s2_out (fp32 device scalar) for the epilogue. NaN inputs are
+ * not supported. */
+int gwa_nvfp4_quant_act_dyn(const void* x, int64_t ldx, float* s2_out, float* parts, uint8_t* q,
+                            uint8_t* scales, int scale_layout, void* xdq, int64_t M, int64_t K, void* stream);
+
 /* codes uint8 [rows, K/2] + e4m3 scales (flat or blocked) -> bf16 [rows, K]
  * = code * scale, exact (dequantize_nvfp4_tensor, models/w4a4.py:157-164,
  * without the second-level scale). */

@@ -24,6 +24,8 @@
 //
 // Two lanes per block: 16 bytes of x in per lane, 4 bytes of codes and 16 of
 // bf16 values out, one scale byte per pair: HBM-bound.
+#include <algorithm>
+
 #include "gwa_common.h"
 
 namespace {
@@ -66,13 +68,61 @@ __device__ __forceinline__ int64_t blocked_index(int64_t r, int64_t c, int64_t n
   return ((r >> 7) * ncb + (c >> 2)) * 512 + (r & 31) * 16 + ((r & 127) >> 5) * 4 + (c & 3);
 }
 
+// Dynamic second-level scale (the forward without a static input_scale, models/w4a4.py:342-343):
+// s2 = max(max|x| / 2688, 1e-12) in fp32. Pass 1 writes one partial max |x| per workgroup (no
+// initialised accumulator, no atomics); the quantizer's workgroups each fold the partials again.
+constexpr int NV_MAX_PARTS = 1024;
+
+__global__ __launch_bounds__(NV_THREADS) void nvfp4_absmax_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                                  int64_t M, int K, float* __restrict__ part) {
+  __shared__ float red[NV_THREADS / 64];
+  const int64_t chunks = M * (K / 8);
+  float mx = 0.0f;
+  for (int64_t i = (int64_t)blockIdx.x * NV_THREADS + threadIdx.x; i < chunks; i += (int64_t)gridDim.x * NV_THREADS) {
+    const int64_t row = i / (K / 8);
+    const int col = (int)(i - row * (K / 8)) * 8;
+    const v4i w = *(const v4i*)(x + row * ldx + col);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) mx = fmaxf(mx, fmaxf(fabsf(bf16_lo((uint32_t)w[j])), fabsf(bf16_hi((uint32_t)w[j]))));
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float m = red[0];
+    for (int w = 1; w < NV_THREADS / 64; ++w) m = fmaxf(m, red[w]);
+    part[blockIdx.x] = m;
+  }
+}
+
+// s2 from the parts (every thread of the workgroup gets it)
+__device__ __forceinline__ float nvfp4_dynamic_s2(const float* __restrict__ part, int nparts) {
+  __shared__ float red[NV_THREADS / 64];
+  float mx = 0.0f;
+  for (int i = threadIdx.x; i < nparts; i += NV_THREADS) mx = fmaxf(mx, part[i]);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  float m = red[0];
+#pragma unroll
+  for (int w = 1; w < NV_THREADS / 64; ++w) m = fmaxf(m, red[w]);
+  return fmaxf(m / 2688.0f, 1e-12f);
+}
+
 // Two lanes per block (lane pair 2p, 2p + 1 holds its elements 0-7 and 8-15), so every load and store of a
 // wave covers one contiguous run; the block maximum is one exchange within the pair.
 __global__ __launch_bounds__(NV_THREADS) void nvfp4_quant_act_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                                                                      const float* __restrict__ s2p,
                                                                      uint8_t* __restrict__ q,
                                                                      uint8_t* __restrict__ scales, int blocked,
-                                                                     uint16_t* __restrict__ xdq, int64_t M, int KB) {
+                                                                     uint16_t* __restrict__ xdq, int64_t M, int KB,
+                                                                     const float* __restrict__ parts, int nparts,
+                                                                     float* __restrict__ s2_out) {
+  // dynamic s2: every workgroup folds the partial maxima (before any thread leaves)
+  const float s2 = parts ? nvfp4_dynamic_s2(parts, nparts) : *s2p;
+  if (parts && blockIdx.x == 0 && threadIdx.x == 0) *s2_out = s2;
   const int64_t t = (int64_t)blockIdx.x * NV_THREADS + threadIdx.x;  // half-block index over [M, KB, 2]
   if (t >= 2 * M * KB) return;  // the total is even: a pair is active together
   const int64_t b = t >> 1;
@@ -90,7 +140,6 @@ __global__ __launch_bounds__(NV_THREADS) void nvfp4_quant_act_kernel(const uint1
 #pragma unroll
   for (int i = 0; i < 8; ++i) bmax = fmaxf(bmax, fabsf(v[i]));
   bmax = fmaxf(bmax, __shfl_xor(bmax, 1));
-  const float s2 = *s2p;
   float tq = bmax / (6.0f * s2);
   tq = fminf(fmaxf(tq, 1.0f / 512.0f), 448.0f);
   const uint32_t sc = e4m3_rne(tq);
@@ -192,9 +241,9 @@ extern "C" int64_t gwa_nvfp4_blocked_scale_numel(int64_t rows, int64_t kblocks) 
   return (rows + 127) / 128 * 128 * ((kblocks + 3) / 4) * 4;
 }
 
-extern "C" int gwa_nvfp4_quant_act(const void* x, int64_t ldx, const float* s2, uint8_t* q, uint8_t* scales,
-                                   int scale_layout, void* xdq, int64_t M, int64_t K, void* stream) {
-  const char* what = "nvfp4_quant_act";
+static int nvfp4_quant(const char* what, const void* x, int64_t ldx, const float* s2, float* s2_out, float* parts,
+                       uint8_t* q, uint8_t* scales, int scale_layout, void* xdq, int64_t M, int64_t K,
+                       void* stream) {
   GWA_REQUIRE(M >= 0 && K > 0 && K % 16 == 0, "%s: K=%lld is not a multiple of 16", what, (long long)K);
   GWA_REQUIRE(ldx >= K && ldx % 8 == 0, "%s: row stride %lld must be >= K and a multiple of 8", what,
               (long long)ldx);
@@ -202,14 +251,38 @@ extern "C" int gwa_nvfp4_quant_act(const void* x, int64_t ldx, const float* s2, 
               "%s: scale_layout %d", what, scale_layout);
   GWA_REQUIRE(M * K < (1ll << 40), "%s: shape too large", what);
   if (M == 0) return GWA_OK;
-  GWA_REQUIRE(x && s2 && q && scales, "%s: null pointer", what);
-  GWA_REQUIRE(GWA_ALIGNED(x, 16) && GWA_ALIGNED(q, 8) && GWA_ALIGNED(s2, 4) && GWA_ALIGNED(xdq, 16),
+  GWA_REQUIRE(x && (s2 || (s2_out && parts)) && q && scales, "%s: null pointer", what);
+  GWA_REQUIRE(GWA_ALIGNED(x, 16) && GWA_ALIGNED(q, 8) && GWA_ALIGNED(s2, 4) && GWA_ALIGNED(s2_out, 4) &&
+                  GWA_ALIGNED(parts, 4) && GWA_ALIGNED(xdq, 16),
               "%s: x and xdq must be 16-byte, q 8-byte aligned", what);
+  hipStream_t st = (hipStream_t)stream;
+  int nparts = 0;
+  if (parts) {
+    const int64_t chunks = M * (K / 8);
+    nparts = (int)std::min<int64_t>(NV_MAX_PARTS, (chunks + NV_THREADS * 8 - 1) / (NV_THREADS * 8));
+    hipLaunchKernelGGL(nvfp4_absmax_kernel, dim3((unsigned)nparts), dim3(NV_THREADS), 0, st, (const uint16_t*)x,
+                       ldx, M, (int)K, parts);
+    const int rc = gwa_check_launch(what);
+    if (rc != GWA_OK) return rc;
+  }
   const int64_t halves = 2 * M * (K / 16);
   hipLaunchKernelGGL(nvfp4_quant_act_kernel, dim3((unsigned)((halves + NV_THREADS - 1) / NV_THREADS)),
-                     dim3(NV_THREADS), 0, (hipStream_t)stream, (const uint16_t*)x, ldx, s2, q, scales,
-                     scale_layout == GWA_NVFP4_SCALES_BLOCKED ? 1 : 0, (uint16_t*)xdq, M, (int)(K / 16));
+                     dim3(NV_THREADS), 0, st, (const uint16_t*)x, ldx, s2, q, scales,
+                     scale_layout == GWA_NVFP4_SCALES_BLOCKED ? 1 : 0, (uint16_t*)xdq, M, (int)(K / 16), parts,
+                     nparts, s2_out);
   return gwa_check_launch(what);
+}
+
+extern "C" int gwa_nvfp4_quant_act(const void* x, int64_t ldx, const float* s2, uint8_t* q, uint8_t* scales,
+                                   int scale_layout, void* xdq, int64_t M, int64_t K, void* stream) {
+  return nvfp4_quant("nvfp4_quant_act", x, ldx, s2, nullptr, nullptr, q, scales, scale_layout, xdq, M, K, stream);
+}
+
+extern "C" int gwa_nvfp4_quant_act_dyn(const void* x, int64_t ldx, float* s2_out, float* parts, uint8_t* q,
+                                       uint8_t* scales, int scale_layout, void* xdq, int64_t M, int64_t K,
+                                       void* stream) {
+  return nvfp4_quant("nvfp4_quant_act_dyn", x, ldx, nullptr, s2_out, parts, q, scales, scale_layout, xdq, M, K,
+                     stream);
 }
 
 extern "C" int gwa_nvfp4_dequant(const uint8_t* q, const uint8_t* scales, int scale_layout, void* out, int64_t rows,

@@ -69,6 +69,7 @@ _SIGNATURES: dict[str, tuple] = {
     "gwa_transpose_2d": (_vp, _vp, _i64, _i64, _i64, _vp),
     "gwa_nvfp4_blocked_scale_numel": (_i64, _i64),
     "gwa_nvfp4_quant_act": (_vp, _i64, _vp, _vp, _vp, _int, _vp, _i64, _i64, _vp),
+    "gwa_nvfp4_quant_act_dyn": (_vp, _i64, _vp, _vp, _vp, _vp, _int, _vp, _i64, _i64, _vp),
     "gwa_nvfp4_dequant": (_vp, _vp, _int, _vp, _i64, _i64, _vp),
     "gwa_nvfp4_scale_bias": (_vp, _vp, _vp, _vp, _i64, _i64, _vp),
 }

@@ -16,7 +16,8 @@ holds but bf16 does. So this lane keeps the reference's numerics with:
 
 * ``cozy_gen_worker::nvfp4_quant_act`` (HIP): the activation codes and scales,
   bit-identical to the reference chain, and in the same pass the exact bf16
-  values code * scale;
+  values code * scale (``nvfp4_quant_act_dyn``: with the dynamic second-level
+  scale max|x| / (6 * 448) computed on the device, one partial-max pass before);
 * the weight decoded once to the exact bf16 values code * scale
   (``cozy_gen_worker::nvfp4_dequant``, HIP) and kept resident;
 * one plain bf16 GEMM (``F.linear``: hipBLASLt, fp32 accumulation, bf16 out),
@@ -139,8 +140,11 @@ class Nvfp4Linear(nn.Module):
         x2 = x.reshape(-1, self.in_features)
         if self.pre_quant_scale is not None:
             x2 = x2 * self.pre_quant_scale
-        s2 = self.input_scale.reshape(()) if self.input_scale is not None else dynamic_input_scale(x2)
-        _, _, xdq = torch.ops.cozy_gen_worker.nvfp4_quant_act(x2.contiguous(), s2, False, True)
+        if self.input_scale is not None:
+            s2 = self.input_scale.reshape(())
+            _, _, xdq = torch.ops.cozy_gen_worker.nvfp4_quant_act(x2.contiguous(), s2, False, True)
+        else:   # s2 = max|x| / (6 * 448) computed on the device, in the quantizer's launch
+            _, _, xdq, s2 = torch.ops.cozy_gen_worker.nvfp4_quant_act_dyn(x2.contiguous(), False, True)
         y = F.linear(xdq, self.weight_dq)
         torch.ops.cozy_gen_worker.nvfp4_scale_bias(y, s2, self.weight_scale_2.reshape(()), self.bias)
         return y.reshape(*shape[:-1], self.out_features)

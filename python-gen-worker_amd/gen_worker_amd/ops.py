@@ -804,15 +804,18 @@ def nvfp4_blocked_scale_numel(rows: int, kblocks: int) -> int:
     return int(nat.load().gwa_nvfp4_blocked_scale_numel(rows, kblocks))
 
 
-def _nvfp4_quant_impl(x2: Tensor, s2: Tensor, blocked: bool, dequant: bool) -> tuple[Tensor, Tensor, Tensor]:
+NVFP4_MAX_PARTS = 1024   # per-workgroup maxima of the dynamic-scale pass
+
+
+def _nvfp4_quant_impl(x2: Tensor, s2: Optional[Tensor], blocked: bool,
+                      dequant: bool) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """s2 None: the dynamic scale computed on the device (returned as the 4th output), else s2 itself."""
     name = "nvfp4_quant_act"
     if x2.dim() != 2:
         raise SvdqOpError(f"{name}: x2 must be 2-D, got {tuple(x2.shape)}")
     _check_dtype(name, x2, torch.bfloat16, what="x2")
     s2 = _scalar_f32(name, s2)
-    if s2 is None:
-        raise SvdqOpError(f"{name}: s2 is required")
-    if x2.stride(1) != 1:
+    if x2.stride(1) != 1 or x2.stride(0) % 8:
         x2 = x2.contiguous()
     _check_cuda(name, s2=s2)
     if not x2.is_cuda:
@@ -827,10 +830,16 @@ def _nvfp4_quant_impl(x2: Tensor, s2: Tensor, blocked: bool, dequant: bool) -> t
     else:
         sc = torch.empty(m, kb, dtype=torch.uint8, device=x2.device)
     xdq = torch.empty(m, k, dtype=torch.bfloat16, device=x2.device) if dequant else x2.new_empty(0, k)
-    nat.call("gwa_nvfp4_quant_act", nat.ptr(x2), int(x2.stride(0)), nat.ptr(s2), nat.ptr(q), nat.ptr(sc),
-             nat.NVFP4_SCALES_BLOCKED if blocked else nat.NVFP4_SCALES_FLAT, nat.ptr(xdq) if dequant else None,
-             m, k, nat.stream_of(x2))
-    return q, sc, xdq
+    layout = nat.NVFP4_SCALES_BLOCKED if blocked else nat.NVFP4_SCALES_FLAT
+    if s2 is not None:
+        nat.call("gwa_nvfp4_quant_act", nat.ptr(x2), int(x2.stride(0)), nat.ptr(s2), nat.ptr(q), nat.ptr(sc),
+                 layout, nat.ptr(xdq) if dequant else None, m, k, nat.stream_of(x2))
+        return q, sc, xdq, s2
+    s2o = torch.empty((), dtype=torch.float32, device=x2.device)
+    parts = torch.empty(NVFP4_MAX_PARTS, dtype=torch.float32, device=x2.device)
+    nat.call("gwa_nvfp4_quant_act_dyn", nat.ptr(x2), int(x2.stride(0)), nat.ptr(s2o), nat.ptr(parts), nat.ptr(q),
+             nat.ptr(sc), layout, nat.ptr(xdq) if dequant else None, m, k, nat.stream_of(x2))
+    return q, sc, xdq, s2o
 
 
 @torch.library.custom_op("cozy_gen_worker::nvfp4_quant_act", mutates_args=())
@@ -838,7 +847,7 @@ def nvfp4_quant_act(x2: Tensor, s2: Tensor, blocked: bool, dequant: bool) -> tup
     """nvfp4 activation quantization, bit-identical to quantize_activation_torch (models/nvfp4_quant.py:92-103):
     ``(codes uint8 [M, K/2], e4m3 scale bytes (flat [M, K/16] or blocked), dequantized bf16 [M, K] or [0, K])``;
     the dequantized activations are code * scale without s2 (exact in bf16)."""
-    return _nvfp4_quant_impl(x2, s2, blocked, dequant)
+    return _nvfp4_quant_impl(x2, s2, blocked, dequant)[:3]
 
 
 @nvfp4_quant_act.register_fake
@@ -850,11 +859,30 @@ def _(x2, s2, blocked, dequant):
     return (x2.new_empty(m, k // 2, dtype=torch.uint8), sc, x2.new_empty(m if dequant else 0, k))
 
 
+@torch.library.custom_op("cozy_gen_worker::nvfp4_quant_act_dyn", mutates_args=())
+def nvfp4_quant_act_dyn(x2: Tensor, blocked: bool, dequant: bool) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """``nvfp4_quant_act`` with the forward's dynamic second-level scale (models/w4a4.py:342-343) computed on the
+    device: ``(codes, scales, dequantized bf16 or [0, K], s2 fp32 0-d)``."""
+    return _nvfp4_quant_impl(x2, None, blocked, dequant)
+
+
+@nvfp4_quant_act_dyn.register_fake
+def _(x2, blocked, dequant):
+    m, k = int(x2.shape[0]), int(x2.shape[1])
+    kb = k // NVFP4_BLOCK
+    sc = (x2.new_empty(((m + 127) // 128) * 128 * ((kb + 3) // 4) * 4, dtype=torch.uint8) if blocked
+          else x2.new_empty(m, kb, dtype=torch.uint8))
+    return (x2.new_empty(m, k // 2, dtype=torch.uint8), sc, x2.new_empty(m if dequant else 0, k),
+            x2.new_empty((), dtype=torch.float32))
+
+
 @torch.library.custom_op("cozy_gen_worker::quant_nvfp4_act", mutates_args=())
 def quant_nvfp4_act(x2: Tensor, s2: Tensor) -> tuple[Tensor, Tensor]:
     """The reference op's contract (models/nvfp4_quant.py:185-187): (packed codes [M, K/2], e4m3 scales in the
     cuBLAS blocked layout)."""
-    q, sc, _ = _nvfp4_quant_impl(x2, s2, True, False)
+    if s2 is None:
+        raise SvdqOpError("quant_nvfp4_act: s2 is required")
+    q, sc, _, _ = _nvfp4_quant_impl(x2, s2, True, False)
     return q, sc.view(torch.float8_e4m3fn)
 
 

@@ -64,14 +64,17 @@ def test_quant_act_bit_exact(m, k, static):
     if static:
         s2v = np.float32(0.0037)
         s2 = torch.tensor(s2v, dtype=torch.float32, device=DEV)
+    else:   # the reference's formula (models/w4a4.py:342-343) in float32 on the CPU
+        s2v = np.float32(max(np.float32(np.abs(x).max()) / np.float32(2688.0), np.float32(1e-12)))
+        s2 = None
+    print(f"nvfp4 act-quant: M={m} K={k} s2={s2v} static={static}", flush=True)
+    if static:
+        q, sc, xdq = torch.ops.cozy_gen_worker.nvfp4_quant_act(xd, s2, False, True)
+        qb, scb, _ = torch.ops.cozy_gen_worker.nvfp4_quant_act(xd, s2, True, False)
     else:
-        from gen_worker_amd import nvfp4
-
-        s2 = nvfp4.dynamic_input_scale(xd)
-        s2v = np.float32(s2.item())
-    print(f"nvfp4 act-quant: M={m} K={k} s2={s2v}", flush=True)
-    q, sc, xdq = torch.ops.cozy_gen_worker.nvfp4_quant_act(xd, s2, False, True)
-    qb, scb, _ = torch.ops.cozy_gen_worker.nvfp4_quant_act(xd, s2, True, False)
+        q, sc, xdq, s2d = torch.ops.cozy_gen_worker.nvfp4_quant_act_dyn(xd, False, True)
+        qb, scb, _, _ = torch.ops.cozy_gen_worker.nvfp4_quant_act_dyn(xd, True, False)
+        assert np.float32(s2d.item()) == s2v
     oq, osc = N.quantize_activation(x, s2v)
     assert np.array_equal(q.cpu().numpy(), oq)
     assert np.array_equal(sc.cpu().numpy(), osc)

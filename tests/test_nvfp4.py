@@ -164,6 +164,8 @@ def test_nvfp4_fake_impls():
         x = torch.empty(77, 384, dtype=torch.bfloat16)
         q, s, d = torch.ops.cozy_gen_worker.nvfp4_quant_act(x, torch.empty(()), True, True)
         assert q.shape == (77, 192) and s.shape == (128 * 24,) and d.shape == (77, 384)
+        q3, s3, d3, sd = torch.ops.cozy_gen_worker.nvfp4_quant_act_dyn(x, False, False)
+        assert s3.shape == (77, 24) and d3.shape == (0, 384) and sd.shape == ()
         q2, s2 = torch.ops.cozy_gen_worker.quant_nvfp4_act(x, torch.empty(()))
         assert s2.dtype == torch.float8_e4m3fn and s2.shape == (128 * 24,)
         w = torch.ops.cozy_gen_worker.nvfp4_dequant(torch.empty(64, 96, dtype=torch.uint8),
