@@ -56,7 +56,7 @@
 
 namespace {
 
-constexpr int TM = 256;
+constexpr int kTmMax = 256;                // tile rows: 256, or 128 for small-M grids
 constexpr int NWAVES = 8, NTHREADS = 64 * NWAVES;  // 512
 constexpr int GS = 2;                      // groups per stage (one record)
 constexpr int GB = 48;                     // bytes of one row's group (64 e3m2 codes)
@@ -70,7 +70,7 @@ constexpr int kUnitE8M0 = 127;             // 2^0
 // software pipeline, four stage buffers) or TN = 256 (64 x 128 wave tiles,
 // each staged byte feeds twice the outputs, three stage buffers, blocks run
 // back to back).
-template <int TN>
+template <int TM, int TN>
 struct Cfg {
   static constexpr int WBN = 2;
   static constexpr int WAVES_N = TN / (32 * WBN);
@@ -184,13 +184,14 @@ __device__ __forceinline__ v4i la_operand_lds(const uint8_t* lrb, int row, int r
                (int)pack_bf16x2_rn(b[2], b[3])};
 }
 
-template <int TN, int RB, bool GELU, bool OUT_F16, bool NQ>
+template <int TM, int TN, int RB, bool GELU, bool OUT_F16, bool NQ>
 __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_kernel(
     const uint8_t* __restrict__ qa, const uint8_t* __restrict__ qw, const float* __restrict__ s2p,
     const float* __restrict__ second, int second_per_channel, const void* __restrict__ la, int la_f32,
     const uint16_t* __restrict__ up, const uint16_t* __restrict__ bias, uint16_t* __restrict__ out, int M, int N,
     int K, NextLayer nx) {
-  using C = Cfg<TN>;
+  using C = Cfg<TM, TN>;
+  static_assert(!NQ || TM == 256, "the next-layer epilogue's la rows are 32 per wave: 256-row tiles");
   constexpr int WBN = C::WBN, WBM = C::WBM, WAVES_N = C::WAVES_N, NBUF = C::NBUF, SLOTS = C::SLOTS;
   constexpr int OFF_W = C::OFF_W;
   __shared__ __attribute__((aligned(16))) uint8_t g_stage[NBUF][C::STAGE];
@@ -828,41 +829,65 @@ struct Fp6Args {
   int M, N, K;
 };
 
-template <int TN, int RB, bool GL, bool F16, bool NQ>
+// tile shapes: 256 x 256 (the 128 x 64 wave tile), 256 x 128 and 128 x 128 (64 x 64 and 32 x 64 wave tiles,
+// with the software pipeline)
+enum Fp6Tile { kTile256x256 = 0, kTile256x128 = 1, kTile128x128 = 2 };
+
+template <int TM, int TN, int RB, bool GL, bool F16, bool NQ>
 void launch_fp6_tile(dim3 grid, hipStream_t s, const Fp6Args& a, const NextLayer& nx) {
-  hipLaunchKernelGGL((w4a4_gemm_fp6_kernel<TN, RB, GL, F16, NQ>), grid, dim3(NTHREADS), 0, s, a.qa6, a.qw6, a.s2,
+  hipLaunchKernelGGL((w4a4_gemm_fp6_kernel<TM, TN, RB, GL, F16, NQ>), grid, dim3(NTHREADS), 0, s, a.qa6, a.qw6, a.s2,
                      a.second, a.per_channel, a.la, a.la_f32, a.up, a.bias, a.out, a.M, a.N, a.K, nx);
 }
 
 template <int RB, bool GL, bool F16, bool NQ>
-void launch_fp6_rb(bool wide, dim3 grid, hipStream_t s, const Fp6Args& a, const NextLayer& nx) {
-  if (wide)
-    launch_fp6_tile<256, RB, GL, F16, NQ>(grid, s, a, nx);
+void launch_fp6_rb(int tile, dim3 grid, hipStream_t s, const Fp6Args& a, const NextLayer& nx) {
+  if (tile == kTile256x256)
+    launch_fp6_tile<256, 256, RB, GL, F16, NQ>(grid, s, a, nx);
+  else if (NQ || tile == kTile256x128)
+    launch_fp6_tile<256, 128, RB, GL, F16, NQ>(grid, s, a, nx);
   else
-    launch_fp6_tile<128, RB, GL, F16, NQ>(grid, s, a, nx);
+    launch_fp6_tile<128, 128, RB, GL, F16, false>(grid, s, a, nx);
 }
 
 template <int RB>
-void launch_fp6_flags(bool wide, bool gelu, bool f16, bool nq, dim3 grid, hipStream_t s, const Fp6Args& a,
+void launch_fp6_flags(int tile, bool gelu, bool f16, bool nq, dim3 grid, hipStream_t s, const Fp6Args& a,
                       const NextLayer& nx) {
   if (nq) {  // the next layer's input is bf16: no f16 variant
-    if (gelu) launch_fp6_rb<RB, true, false, true>(wide, grid, s, a, nx);
-    else launch_fp6_rb<RB, false, false, true>(wide, grid, s, a, nx);
+    if (gelu) launch_fp6_rb<RB, true, false, true>(tile, grid, s, a, nx);
+    else launch_fp6_rb<RB, false, false, true>(tile, grid, s, a, nx);
   } else if (gelu) {
-    if (f16) launch_fp6_rb<RB, true, true, false>(wide, grid, s, a, nx);
-    else launch_fp6_rb<RB, true, false, false>(wide, grid, s, a, nx);
+    if (f16) launch_fp6_rb<RB, true, true, false>(tile, grid, s, a, nx);
+    else launch_fp6_rb<RB, true, false, false>(tile, grid, s, a, nx);
   } else {
-    if (f16) launch_fp6_rb<RB, false, true, false>(wide, grid, s, a, nx);
-    else launch_fp6_rb<RB, false, false, false>(wide, grid, s, a, nx);
+    if (f16) launch_fp6_rb<RB, false, true, false>(tile, grid, s, a, nx);
+    else launch_fp6_rb<RB, false, false, false>(tile, grid, s, a, nx);
   }
 }
 
-// 256 x 256 tiles halve the operand bytes staged per MAC; 256 x 128 tiles keep the software pipeline and
-// give twice the workgroups. The wider tile is taken when it still fills the chip.
-int fp6_tile_n(int64_t M, int64_t N) {
-  const int64_t tiles256 = ((M + TM - 1) / TM) * ((N + 255) / 256);
-  return tiles256 >= 192 ? 256 : 128;
+// One workgroup per CU (the stage buffers fill the LDS), so a grid runs in rounds of kCus tiles. Grids of
+// at least 192 256 x 256 tiles take that tile (it stages the fewest operand bytes per MAC); a smaller grid
+// takes the shape with the least estimated time: rounds x the tile's MACs x its time per MAC relative to
+// the 256 x 256 tile (one round of each at M=256, N=9216, K=3072: 51.4, 31.9, 23.0 us for 36, 72, 144
+// tiles). The next-layer epilogue needs 256-row tiles.
+constexpr int kCus = 256;
+int fp6_tile(int64_t M, int64_t N, bool nq) {
+  struct Shape { int tm, tn; double per_mac; };
+  static const Shape shapes[3] = {{256, 256, 1.0}, {256, 128, 1.24}, {128, 128, 1.80}};
+  if (((M + 255) / 256) * ((N + 255) / 256) >= 192) return kTile256x256;
+  int best = 0;
+  double best_t = 0.0;
+  for (int i = 0; i < (nq ? 2 : 3); ++i) {
+    const int64_t tiles = ((M + shapes[i].tm - 1) / shapes[i].tm) * ((N + shapes[i].tn - 1) / shapes[i].tn);
+    const double t = (double)((tiles + kCus - 1) / kCus) * shapes[i].tm * shapes[i].tn * shapes[i].per_mac;
+    if (i == 0 || t < best_t * 0.999) {
+      best = i;
+      best_t = t;
+    }
+  }
+  return best;
 }
+int fp6_tile_m(int tile) { return tile == kTile128x128 ? 128 : 256; }
+int fp6_tile_n(int tile) { return tile == kTile256x256 ? 256 : 128; }
 
 // shared argument checks and launch of both GEMM entry points (nx.q6 != NULL: the NQ epilogue)
 int gemm_fp6(const char* what, const uint8_t* qa6, const uint8_t* qw6, const float* s2, const float* second,
@@ -885,7 +910,7 @@ int gemm_fp6(const char* what, const uint8_t* qa6, const uint8_t* qw6, const flo
   const int la_f32 = (epilogue_flags & GWA_EPI_LA_F32) ? 1 : 0;
   const int64_t nst = K / 128;
   // the DMA offsets of a tile's last run stay below 2^31 + 2^16
-  GWA_REQUIRE(nst * (M + TM) * REC < (1ll << 31) && nst * (N + 256) * REC < (1ll << 31) && M * N * 2 < (1ll << 31) &&
+  GWA_REQUIRE(nst * (M + kTmMax) * REC < (1ll << 31) && nst * (N + 256) * REC < (1ll << 31) && M * N * 2 < (1ll << 31) &&
                   M * R * 4 < (1ll << 31) && (N / 128) * M * REC < (1ll << 31),
               "%s: operands must stay below 2 GiB (buffer addressing)", what);
   if (M == 0) return GWA_OK;
@@ -894,9 +919,9 @@ int gemm_fp6(const char* what, const uint8_t* qa6, const uint8_t* qw6, const flo
   GWA_REQUIRE(GWA_ALIGNED(qa6, 16) && GWA_ALIGNED(qw6, 16) && GWA_ALIGNED(la, 16) && GWA_ALIGNED(up, 16) &&
                   GWA_ALIGNED(out, 8) && GWA_ALIGNED(bias, 2) && GWA_ALIGNED(second, 4) && GWA_ALIGNED(s2, 4),
               "%s: misaligned pointer", what);
-  const int TNv = fp6_tile_n(M, N);
-  const bool wide = TNv == 256;
-  const int64_t tiles = ((M + TM - 1) / TM) * ((N + TNv - 1) / TNv);
+  const int tile = fp6_tile(M, N, nq);
+  const int TMv = fp6_tile_m(tile), TNv = fp6_tile_n(tile);
+  const int64_t tiles = ((M + TMv - 1) / TMv) * ((N + TNv - 1) / TNv);
   GWA_REQUIRE(tiles < (1ll << 30), "%s: too many tiles", what);
   const int64_t per_xcd = (tiles + kXcds - 1) / kXcds;
   const dim3 grid((unsigned)(per_xcd * kXcds));
@@ -906,11 +931,11 @@ int gemm_fp6(const char* what, const uint8_t* qa6, const uint8_t* qw6, const flo
   const bool f16 = out_dtype == GWA_DT_F16;
   hipStream_t s = (hipStream_t)stream;
   switch (R / 16) {
-    case 0: launch_fp6_flags<0>(wide, gelu, f16, nq, grid, s, a, nx); break;
-    case 1: launch_fp6_flags<1>(wide, gelu, f16, nq, grid, s, a, nx); break;
-    case 2: launch_fp6_flags<2>(wide, gelu, f16, nq, grid, s, a, nx); break;
-    case 4: launch_fp6_flags<4>(wide, gelu, f16, nq, grid, s, a, nx); break;
-    case 8: launch_fp6_flags<8>(wide, gelu, f16, nq, grid, s, a, nx); break;
+    case 0: launch_fp6_flags<0>(tile, gelu, f16, nq, grid, s, a, nx); break;
+    case 1: launch_fp6_flags<1>(tile, gelu, f16, nq, grid, s, a, nx); break;
+    case 2: launch_fp6_flags<2>(tile, gelu, f16, nq, grid, s, a, nx); break;
+    case 4: launch_fp6_flags<4>(tile, gelu, f16, nq, grid, s, a, nx); break;
+    case 8: launch_fp6_flags<8>(tile, gelu, f16, nq, grid, s, a, nx); break;
     default: return gwa_set_error(GWA_ERR_INVALID, "%s: rank %lld", what, (long long)R);
   }
   return gwa_check_launch(what);
@@ -954,6 +979,6 @@ extern "C" int gwa_svdq_gemm_w4a4_fp6_next(const uint8_t* qa6, const uint8_t* qw
 
 extern "C" int64_t gwa_svdq_gemm_w4a4_fp6_next_partials(int64_t M, int64_t N) {
   if (M <= 0 || N <= 0) return 0;
-  const int tn = fp6_tile_n(M, N);
+  const int tn = fp6_tile_n(fp6_tile(M, N, true));
   return (N + tn - 1) / tn;
 }
