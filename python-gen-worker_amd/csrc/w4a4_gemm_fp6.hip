@@ -56,7 +56,7 @@
 
 namespace {
 
-constexpr int kTmMax = 256;                // tile rows: 256, or 128 for small-M grids
+constexpr int kTmMax = 256;                // tile rows: 256, or 192 / 128 for grids that leave CUs idle
 constexpr int NWAVES = 8, NTHREADS = 64 * NWAVES;  // 512
 constexpr int GS = 2;                      // groups per stage (one record)
 constexpr int GB = 48;                     // bytes of one row's group (64 e3m2 codes)
@@ -76,7 +76,9 @@ struct Cfg {
   static constexpr int WAVES_N = TN / (32 * WBN);
   static constexpr int WAVES_M = NWAVES / WAVES_N;
   static constexpr int WBM = TM / (32 * WAVES_M);
-  static constexpr int LDS_X = TM * REC, OFF_W = LDS_X, LDS_W = TN * REC;
+  // the activation rows' region is a whole number of 1 KB copy runs (192 rows: 19.5 KB -> 20 KB; the half
+  // run past the tile's rows lands in the padding)
+  static constexpr int LDS_X = (TM * REC + 1023) / 1024 * 1024, OFF_W = LDS_X, LDS_W = TN * REC;
   static constexpr int STAGE = LDS_X + LDS_W;
   static constexpr int NB0 = (kLdsBytes - 2 * TN * 4) / STAGE;
   static constexpr int NBUF = NB0 > 4 ? 4 : NB0;   // stage buffers; DMA runs NBUF - 1 stages ahead
@@ -829,9 +831,9 @@ struct Fp6Args {
   int M, N, K;
 };
 
-// tile shapes: 256 x 256 (the 128 x 64 wave tile), 256 x 128 and 128 x 128 (64 x 64 and 32 x 64 wave tiles,
-// with the software pipeline)
-enum Fp6Tile { kTile256x256 = 0, kTile256x128 = 1, kTile128x128 = 2 };
+// tile shapes: 256 x 256 and 192 x 256 (128 x 64 and 96 x 64 wave tiles), 256 x 128 and 128 x 128 (64 x 64
+// and 32 x 64 wave tiles, with the software pipeline)
+enum Fp6Tile { kTile256x256 = 0, kTile256x128 = 1, kTile128x128 = 2, kTile192x256 = 3 };
 
 template <int TM, int TN, int RB, bool GL, bool F16, bool NQ>
 void launch_fp6_tile(dim3 grid, hipStream_t s, const Fp6Args& a, const NextLayer& nx) {
@@ -843,6 +845,8 @@ template <int RB, bool GL, bool F16, bool NQ>
 void launch_fp6_rb(int tile, dim3 grid, hipStream_t s, const Fp6Args& a, const NextLayer& nx) {
   if (tile == kTile256x256)
     launch_fp6_tile<256, 256, RB, GL, F16, NQ>(grid, s, a, nx);
+  else if (!NQ && tile == kTile192x256)
+    launch_fp6_tile<192, 256, RB, GL, F16, false>(grid, s, a, nx);
   else if (NQ || tile == kTile256x128)
     launch_fp6_tile<256, 128, RB, GL, F16, NQ>(grid, s, a, nx);
   else
@@ -867,16 +871,17 @@ void launch_fp6_flags(int tile, bool gelu, bool f16, bool nq, dim3 grid, hipStre
 // One workgroup per CU (the stage buffers fill the LDS), so a grid runs in rounds of kCus tiles. Grids of
 // at least 192 256 x 256 tiles take that tile (it stages the fewest operand bytes per MAC); a smaller grid
 // takes the shape with the least estimated time: rounds x the tile's MACs x its time per MAC relative to
-// the 256 x 256 tile (one round of each at M=256, N=9216, K=3072: 51.4, 31.9, 23.0 us for 36, 72, 144
+// the 256 x 256 tile (one round of each at M=256, N=9216, K=3072: 51.4, 31.9, 23.0 us for 36 256 x 256,
+// 72 256 x 128 and 144 128 x 128 tiles; at M=1024: 54.3 and 44.0 us for 144 256 x 256 and 216 192 x 256
 // tiles). The next-layer epilogue needs 256-row tiles.
 constexpr int kCus = 256;
 int fp6_tile(int64_t M, int64_t N, bool nq) {
   struct Shape { int tm, tn; double per_mac; };
-  static const Shape shapes[3] = {{256, 256, 1.0}, {256, 128, 1.24}, {128, 128, 1.80}};
+  static const Shape shapes[4] = {{256, 256, 1.0}, {256, 128, 1.24}, {128, 128, 1.80}, {192, 256, 1.08}};
   if (((M + 255) / 256) * ((N + 255) / 256) >= 192) return kTile256x256;
   int best = 0;
   double best_t = 0.0;
-  for (int i = 0; i < (nq ? 2 : 3); ++i) {
+  for (int i = 0; i < (nq ? 2 : 4); ++i) {
     const int64_t tiles = ((M + shapes[i].tm - 1) / shapes[i].tm) * ((N + shapes[i].tn - 1) / shapes[i].tn);
     const double t = (double)((tiles + kCus - 1) / kCus) * shapes[i].tm * shapes[i].tn * shapes[i].per_mac;
     if (i == 0 || t < best_t * 0.999) {
@@ -886,8 +891,8 @@ int fp6_tile(int64_t M, int64_t N, bool nq) {
   }
   return best;
 }
-int fp6_tile_m(int tile) { return tile == kTile128x128 ? 128 : 256; }
-int fp6_tile_n(int tile) { return tile == kTile256x256 ? 256 : 128; }
+int fp6_tile_m(int tile) { return tile == kTile128x128 ? 128 : (tile == kTile192x256 ? 192 : 256); }
+int fp6_tile_n(int tile) { return tile == kTile256x256 || tile == kTile192x256 ? 256 : 128; }
 
 // shared argument checks and launch of both GEMM entry points (nx.q6 != NULL: the NQ epilogue)
 int gemm_fp6(const char* what, const uint8_t* qa6, const uint8_t* qw6, const float* s2, const float* second,
