@@ -237,6 +237,37 @@ int gwa_svdq_prep_proj_down_fp6(const void* proj_down, void* out, int64_t K, int
 int gwa_svdq_group_psums_fp6(const uint8_t* qa6, const uint8_t* qw6, int32_t* out,
                              int64_t M, int64_t N, int64_t K, void* stream);
 
+/* One whole SVDQuant W4A4 linear on the fp6 lane: the forward of the
+ * reference's fused module, _SvdqFusedLinear.forward
+ * (models/svdq_fused.py:516-527: svdq_quant -> _gemm_w4a4 -> x2 @ proj_down
+ * -> svdq_epilogue_lora), as one call: gwa_svdq_quant_fp6 (records + la
+ * partial slots), gwa_svdq_la_reduce and gwa_svdq_gemm_w4a4_fp6, enqueued on
+ * `stream`. Arguments as those entry points take them:
+ *   x        bf16 [M, K] rows with stride ldx; smooth bf16 [K] or NULL;
+ *            s2 fp32 device scalar or NULL (= 1.0)
+ *   proj_down_op6  gwa_svdq_prep_proj_down_fp6 order, or NULL (rank 0);
+ *            proj_up bf16 [N, rank] (NULL iff proj_down_op6 is NULL)
+ *   qw6      the weight's fp6 records (gwa_svdq_pack_weight_fp6, with 1 KB of
+ *            readable slack after them)
+ *   second / bias / out / out_dtype as gwa_svdq_gemm_w4a4_fp6; epilogue_flags
+ *            GWA_EPI_GELU_TANH or 0
+ *   workspace  device memory of workspace_bytes >=
+ *            gwa_svdq_w4a4_linear_fp6_workspace(M, K, rank), 256-byte aligned:
+ *            the activation records (+ slack), the la partial slots and the
+ *            bf16 la. Nothing in it needs to be initialised; it must not be
+ *            reused by another call until this call's work on `stream` ends.
+ * K % 128 == 0, N % 16 == 0. */
+int gwa_svdq_w4a4_linear_fp6(const void* x, int64_t ldx, const void* smooth, const float* s2,
+                             const void* proj_down_op6, int64_t rank, const uint8_t* qw6,
+                             const float* second, int64_t second_numel, const void* proj_up,
+                             const void* bias, void* out, int out_dtype, int epilogue_flags,
+                             int64_t M, int64_t N, int64_t K, void* workspace, int64_t workspace_bytes,
+                             void* stream);
+
+/* Workspace bytes gwa_svdq_w4a4_linear_fp6 needs for M rows, K inputs and
+ * this rank (0 for an unsupported shape). */
+int64_t gwa_svdq_w4a4_linear_fp6_workspace(int64_t M, int64_t K, int64_t rank);
+
 /* Standalone epilogue: out = y0 * (s2 * second) + la @ up^T + bias (bf16 out).
  * cozy_gen_worker::svdq_epilogue_lora, models/svdq_fused.py:315-377.
  *   y0 bf16 [M, N]; la bf16 [M, rank]; up bf16 [N, rank]; bias bf16 [N] or NULL */

@@ -1,0 +1,76 @@
+// One SVDQuant W4A4 linear per call on the fp6 lane: kernel 1 (smoothing, int4 group-64 act-quant written
+// as fp6 operand records, x @ proj_down as fp32 partial slots), the fixed-order la reduction, and the W4A4
+// GEMM with its fused epilogue, enqueued on one stream. The intermediates (records, partial slots, bf16 la)
+// live in a workspace the caller passes in; gwa_svdq_w4a4_linear_fp6_workspace gives its size.
+#include "gwa_common.h"
+
+namespace {
+
+constexpr int64_t kAlign = 256;
+constexpr int64_t kRecordSlack = 1024;  // the GEMM copies records in 1 KB runs and may read this far past them
+
+int64_t align_up(int64_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+// workspace layout: [records + slack | la partial slots fp32 [P, M, R] | la bf16 [M, R]]
+struct Scratch {
+  int64_t partials = 0, la = 0, total = 0, slots = 0;
+};
+
+Scratch scratch_layout(int64_t M, int64_t K, int64_t R) {
+  Scratch s;
+  s.slots = R ? gwa_svdq_quant_fp6_partials(M, K, R) : 0;
+  s.partials = align_up(M * (K / 128) * GWA_FP6_REC + kRecordSlack);
+  s.la = align_up(s.partials + s.slots * M * R * 4);
+  s.total = align_up(s.la + M * R * 2);
+  return s;
+}
+
+int linear_fp6_run(const char* what, const void* x, int64_t ldx, const void* smooth, const float* s2,
+                   const void* proj_down_op6, int64_t rank, const uint8_t* qw6, const float* second,
+                   int64_t second_numel, const void* proj_up, const void* bias, void* out, int out_dtype,
+                   int epilogue_flags, int64_t M, int64_t N, int64_t K, uint8_t* ws, int64_t ws_bytes, void* stream) {
+  GWA_REQUIRE(M >= 0 && N > 0 && K > 0 && K % 128 == 0, "%s: bad shape M=%lld N=%lld K=%lld (K %% 128 == 0)", what,
+              (long long)M, (long long)N, (long long)K);
+  GWA_REQUIRE((proj_down_op6 == nullptr) == (proj_up == nullptr),
+              "%s: proj_down_op6 and proj_up must both be given or both be NULL", what);
+  GWA_REQUIRE((epilogue_flags & ~GWA_EPI_GELU_TANH) == 0, "%s: epilogue flags 0x%x (only GWA_EPI_GELU_TANH)", what,
+              epilogue_flags);
+  const int64_t R = proj_down_op6 ? rank : 0;
+  GWA_REQUIRE(R == 0 || R == 16 || R == 32 || R == 64 || R == 128, "%s: rank %lld not in {0,16,32,64,128}", what,
+              (long long)R);
+  GWA_REQUIRE(M < (1ll << 31) && K < (1ll << 24), "%s: shape too large", what);
+  if (M == 0) return GWA_OK;
+  const Scratch s = scratch_layout(M, K, R);
+  GWA_REQUIRE(ws != nullptr && ws_bytes >= s.total, "%s: workspace of %lld bytes, this shape needs %lld", what,
+              (long long)ws_bytes, (long long)s.total);
+  GWA_REQUIRE(GWA_ALIGNED(ws, 256), "%s: workspace must be 256-byte aligned", what);
+  float* part = R ? (float*)(ws + s.partials) : nullptr;
+  uint8_t* la = R ? ws + s.la : nullptr;
+  int rc = gwa_svdq_quant_fp6(x, ldx, smooth, s2, proj_down_op6, R, ws, part, M, K, stream);
+  if (rc != GWA_OK) return rc;
+  if (R) {
+    rc = gwa_svdq_la_reduce(part, s.slots, M, R, la, stream);
+    if (rc != GWA_OK) return rc;
+  }
+  return gwa_svdq_gemm_w4a4_fp6(ws, qw6, s2, second, second_numel, la, R ? proj_up : nullptr, R, bias, out, out_dtype,
+                                epilogue_flags, M, N, K, stream);
+}
+
+}  // namespace
+
+extern "C" int64_t gwa_svdq_w4a4_linear_fp6_workspace(int64_t M, int64_t K, int64_t rank) {
+  if (M <= 0 || K <= 0 || K % 128 || M >= (1ll << 31) || K >= (1ll << 24)) return 0;
+  if (rank != 0 && rank != 16 && rank != 32 && rank != 64 && rank != 128) return 0;
+  return scratch_layout(M, K, rank).total;
+}
+
+extern "C" int gwa_svdq_w4a4_linear_fp6(const void* x, int64_t ldx, const void* smooth, const float* s2,
+                                        const void* proj_down_op6, int64_t rank, const uint8_t* qw6,
+                                        const float* second, int64_t second_numel, const void* proj_up,
+                                        const void* bias, void* out, int out_dtype, int epilogue_flags, int64_t M,
+                                        int64_t N, int64_t K, void* workspace, int64_t workspace_bytes,
+                                        void* stream) {
+  return linear_fp6_run("svdq_w4a4_linear_fp6", x, ldx, smooth, s2, proj_down_op6, rank, qw6, second,
+                        second_numel, proj_up, bias, out, out_dtype, epilogue_flags, M, N, K, (uint8_t*)workspace,
+                        workspace_bytes, stream);
+}

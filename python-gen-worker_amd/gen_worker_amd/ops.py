@@ -204,6 +204,23 @@ def records_empty(stages: int, rows: int, device) -> Tensor:
     return torch.empty(n + RECORD_SLACK, dtype=torch.uint8, device=device)[:n].view(stages, rows, nat.FP6_REC)
 
 
+def record_slack_bytes(rec: Tensor) -> int:
+    """Readable bytes of ``rec``'s storage past its last element."""
+    end = (rec.storage_offset() + rec.numel()) * rec.element_size()
+    return rec.untyped_storage().nbytes() - end
+
+
+def _check_record_slack(name: str, rec: Tensor, what: str) -> None:
+    """The fp6 GEMM copies operand records in 1 KB runs with unchecked scalar offsets: the run holding a tile's
+    last real row may read up to RECORD_SLACK bytes past the last record, so a record tensor handed to it must own
+    that much storage after its end (``records_empty`` allocates it; a ``clone()``, ``.to()`` copy or
+    deserialized tensor does not)."""
+    slack = record_slack_bytes(rec)
+    if slack < RECORD_SLACK:
+        raise SvdqOpError(f"{name}: {what} has {slack} readable bytes past its last record, the fp6 GEMM needs "
+                          f"{RECORD_SLACK} (allocate record buffers with ops.records_empty)")
+
+
 def la_partials_quant(m: int, k: int, rank: int) -> int:
     """la partial slots the fp6 act-quant kernel writes for [m, k] at this rank."""
     return int(nat.load().gwa_svdq_quant_fp6_partials(m, k, rank))
@@ -431,9 +448,11 @@ def _fp6_impl(qa6: Tensor, weight_fp6: Tensor, s2: Optional[Tensor], second: Opt
     n, kw = _fp6_records_k(name, weight_fp6, "weight_fp6")
     if kw != k:
         raise SvdqOpError(f"{name}: activation K={k} and weight K={kw} differ")
+    _check_record_slack(name, qa6, "qa6")
+    _check_record_slack(name, weight_fp6, "weight_fp6")
     rank, sec_n = _epilogue_operands(name, m, n, la, up, bias, second)
     out = torch.empty(m, n, dtype=out_dtype, device=qa6.device)
-    nat.call("gwa_svdq_gemm_w4a4_fp6", nat.ptr(qa6), nat.ptr(weight_fp6.contiguous()), nat.ptr(s2), nat.ptr(second),
+    nat.call("gwa_svdq_gemm_w4a4_fp6", nat.ptr(qa6), nat.ptr(weight_fp6), nat.ptr(s2), nat.ptr(second),
              sec_n, nat.ptr(la), nat.ptr(up), rank, nat.ptr(bias), nat.ptr(out), _dt_code(out_dtype),
              _epi_flags(gelu, la), m, n, k, nat.stream_of(qa6))
     return out
@@ -451,6 +470,72 @@ def svdq_w4a4_linear_fp6(qa6: Tensor, weight_fp6: Tensor, s2: Optional[Tensor], 
 @svdq_w4a4_linear_fp6.register_fake
 def _(qa6, weight_fp6, s2, second, la, up, bias, out_dtype, gelu):
     return qa6.new_empty(int(qa6.shape[1]), int(weight_fp6.shape[1]), dtype=out_dtype)
+
+
+def linear_fp6_workspace_bytes(m: int, k: int, rank: int) -> int:
+    """Workspace bytes of one ``svdq_forward_fp6`` call (activation records + slack, la partial slots, la)."""
+    return int(nat.load().gwa_svdq_w4a4_linear_fp6_workspace(m, k, rank))
+
+
+@torch.library.custom_op("cozy_gen_worker::svdq_forward_fp6", mutates_args=())
+def svdq_forward_fp6(x2: Tensor, smooth: Optional[Tensor], s2: Optional[Tensor], proj_down_op6: Optional[Tensor],
+                     weight_fp6: Tensor, second: Optional[Tensor], proj_up: Optional[Tensor], bias: Optional[Tensor],
+                     out_dtype: torch.dtype, gelu: bool) -> Tensor:
+    """The whole fp6-lane linear in one library call (``_SvdqFusedLinear.forward``, ``models/svdq_fused.py:516-527``):
+    kernel 1 into a workspace (records, la partial slots), the fixed-order la reduction and the GEMM with its
+    epilogue; bit-identical to ``svdq_quant_fp6`` followed by ``svdq_w4a4_linear_fp6``."""
+    name = "svdq_forward_fp6"
+    if x2.dim() != 2:
+        raise SvdqOpError(f"{name}: x2 must be 2-D, got {tuple(x2.shape)}")
+    s2 = _scalar_f32(name, s2)
+    if second is not None and second.dtype != torch.float32:
+        second = second.float().contiguous()
+    _check_dtype(name, x2, torch.bfloat16, what="x2")
+    _check_dtype(name, smooth, torch.bfloat16, what="smooth")
+    _check_dtype(name, proj_down_op6, torch.bfloat16, what="proj_down_op6")
+    _check_dtype(name, weight_fp6, torch.uint8, what="weight_fp6")
+    _check_dtype(name, proj_up, torch.bfloat16, what="proj_up")
+    _check_dtype(name, bias, torch.bfloat16, what="bias")
+    if out_dtype not in (torch.bfloat16, torch.float16):
+        raise SvdqOpError(f"{name}: out_dtype {out_dtype} not bf16/fp16")
+    if x2.stride(1) != 1 or x2.stride(0) % 8:
+        x2 = x2.contiguous()
+    _check_cuda(name, smooth=smooth, s2=s2, proj_down_op6=proj_down_op6, weight_fp6=weight_fp6, second=second,
+                proj_up=proj_up, bias=bias)
+    if not x2.is_cuda:
+        raise SvdqOpError(f"{name}: x2 is on {x2.device}; the int4/int8 path runs on the GPU only")
+    m, k = int(x2.shape[0]), int(x2.shape[1])
+    n, kw = _fp6_records_k(name, weight_fp6, "weight_fp6")
+    if kw != k:
+        raise SvdqOpError(f"{name}: x2 has K={k}, weight_fp6 K={kw}")
+    if smooth is not None and smooth.numel() != k:
+        raise SvdqOpError(f"{name}: smooth has {smooth.numel()} values for K={k}")
+    _check_record_slack(name, weight_fp6, "weight_fp6")
+    if (proj_down_op6 is None) != (proj_up is None):
+        raise SvdqOpError(f"{name}: proj_down_op6 and proj_up must both be given or both be None")
+    rank = 0
+    if proj_up is not None:
+        rank = int(proj_up.shape[1])
+        if tuple(proj_up.shape) != (n, rank) or tuple(proj_down_op6.shape) != (k, rank):
+            raise SvdqOpError(f"{name}: proj_up {tuple(proj_up.shape)} / proj_down_op6 {tuple(proj_down_op6.shape)} "
+                              f"do not match [N={n}, r] / [K={k}, r]")
+    if bias is not None and bias.numel() != n:
+        raise SvdqOpError(f"{name}: bias has {bias.numel()} values for N={n}")
+    out = torch.empty(m, n, dtype=out_dtype, device=x2.device)
+    if m == 0:
+        return out
+    ws = torch.empty(linear_fp6_workspace_bytes(m, k, rank), dtype=torch.uint8, device=x2.device)
+    nat.call("gwa_svdq_w4a4_linear_fp6", nat.ptr(x2), int(x2.stride(0)), nat.ptr(smooth), nat.ptr(s2),
+             nat.ptr(proj_down_op6), rank, nat.ptr(weight_fp6), nat.ptr(second),
+             0 if second is None else int(second.numel()), nat.ptr(proj_up), nat.ptr(bias), nat.ptr(out),
+             _dt_code(out_dtype), nat.EPI_GELU_TANH if gelu else 0, m, n, k, nat.ptr(ws), int(ws.numel()),
+             nat.stream_of(x2))
+    return out
+
+
+@svdq_forward_fp6.register_fake
+def _(x2, smooth, s2, proj_down_op6, weight_fp6, second, proj_up, bias, out_dtype, gelu):
+    return x2.new_empty(int(x2.shape[0]), int(weight_fp6.shape[1]), dtype=out_dtype)
 
 
 def _next_records(name: str, q6: Tensor, m: int, k: int, stage_offset: int) -> int:
@@ -499,6 +584,8 @@ def svdq_w4a4_linear_fp6_next(qa6: Tensor, weight_fp6: Tensor, s2: Optional[Tens
         raise SvdqOpError(f"{name}: N={n} is not a multiple of {FP6_STAGE} (whole stages of the next layer)")
     if next_smooth is not None and next_smooth.numel() != n:
         raise SvdqOpError(f"{name}: next_smooth has {next_smooth.numel()} values for N={n}")
+    _check_record_slack(name, qa6, "qa6")
+    _check_record_slack(name, weight_fp6, "weight_fp6")
     rank, sec_n = _epilogue_operands(name, m, n, la, up, bias, second)
     q6_addr = _next_records(name, next_q6, m, n, stage_offset)
     nrank = _la_part_check(name, next_la_part, next_proj_down_op, m, n, la_partials_next(m, n))

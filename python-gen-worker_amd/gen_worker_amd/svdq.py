@@ -187,6 +187,18 @@ class SvdqW4A4Linear(nn.Module):
         if fp6:
             self.weight_fp6 = torch.ops.cozy_gen_worker.svdq_pack_weight_fp6(self.weight, self.weight_scale)
 
+    def _apply(self, fn: Any, recurse: bool = True) -> "SvdqW4A4Linear":
+        """Module moves and casts (``.to()``, ``.cuda()``, ``.cpu()``) copy buffers without the 1 KB of readable
+        slack the fp6 GEMM needs after its operand records, and ``proj_down``'s operand orders depend only on
+        ``proj_down``: the derived buffers are dropped here and rebuilt from the primary ones on the next
+        forward."""
+        super()._apply(fn, recurse)
+        self.weight_fp6 = None
+        if self.rank:
+            self.proj_down_op = None
+            self.proj_down_op6 = None
+        return self
+
     def _load_from_state_dict(self, *args: Any, **kwargs: Any) -> None:  # noqa: D401
         super()._load_from_state_dict(*args, **kwargs)
         if self.weight.device.type != "meta":
@@ -227,10 +239,9 @@ class SvdqW4A4Linear(nn.Module):
         self._ensure_derived()
         gelu = self.activation == "gelu_tanh"
         if self.weight_fp6 is not None:
-            qa6, la = torch.ops.cozy_gen_worker.svdq_quant_fp6(x2, self.smooth_factor, None, self.proj_down_op6)
-            y = torch.ops.cozy_gen_worker.svdq_w4a4_linear_fp6(
-                qa6, self.weight_fp6, None, self.second, la if self.rank else None, self.proj_up, self.bias,
-                out_dtype, gelu)
+            y = torch.ops.cozy_gen_worker.svdq_forward_fp6(
+                x2, self.smooth_factor, None, self.proj_down_op6 if self.rank else None, self.weight_fp6, self.second,
+                self.proj_up, self.bias, out_dtype, gelu)
             return y.reshape(*shape[:-1], self.out_features)
         if self.rank:
             qa, sa, la = torch.ops.cozy_gen_worker.svdq_quant_lora(x2, self.smooth_factor, None, self.proj_down_op)

@@ -270,3 +270,33 @@ def test_qualification_without_gpu_is_unavailable():
         pytest.skip("a GPU is present")
     q = qualify.qualify()
     assert q.lane == "unavailable" and q.reasons
+
+
+def test_record_slack_helpers_on_cpu_tensors():
+    """The slack the fp6 GEMM needs past a record tensor is measured on its storage, views included."""
+    from gen_worker_amd import ops
+
+    n = 3 * 5 * 104
+    full = torch.empty(n + ops.RECORD_SLACK, dtype=torch.uint8)
+    rec = full[:n].view(3, 5, 104)
+    assert ops.record_slack_bytes(rec) == ops.RECORD_SLACK
+    ops._check_record_slack("t", rec, "rec")
+    inner = full[104:104 + 2 * 104].view(1, 2, 104)          # a view deep inside the storage
+    assert ops.record_slack_bytes(inner) == n + ops.RECORD_SLACK - 3 * 104
+    bare = rec.clone()
+    assert ops.record_slack_bytes(bare) == 0
+    with pytest.raises(ops.SvdqOpError, match="records_empty"):
+        ops._check_record_slack("t", bare, "rec")
+
+
+def test_module_move_drops_derived_buffers():
+    """Moves and casts drop the derived operand-order buffers (rebuilt with slack on the next GPU forward)."""
+    from gen_worker_amd.svdq import SvdqW4A4Linear
+
+    mod = SvdqW4A4Linear(256, 128, rank=16, bias=True, device="cpu")
+    mod.weight_fp6 = torch.zeros(2, 128, 104, dtype=torch.uint8)
+    mod.proj_down_op6 = torch.zeros(256, 16, dtype=torch.bfloat16)
+    mod.proj_down_op = torch.zeros(256, 16, dtype=torch.bfloat16)
+    mod = mod.to("cpu")
+    assert mod.weight_fp6 is None and mod.proj_down_op6 is None and mod.proj_down_op is None
+    assert mod.weight.shape == (128, 128) and mod.proj_down.shape == (256, 16)
