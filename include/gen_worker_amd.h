@@ -268,6 +268,35 @@ int gwa_svdq_w4a4_linear_fp6(const void* x, int64_t ldx, const void* smooth, con
  * this rank (0 for an unsupported shape). */
 int64_t gwa_svdq_w4a4_linear_fp6_workspace(int64_t M, int64_t K, int64_t rank);
 
+/* Size of the static scratch of gwa_svdq_w4a4_linear_fp6_noalloc (128 MiB). */
+enum { GWA_NOALLOC_SCRATCH_MIB = 128 };
+#define GWA_NOALLOC_SCRATCH_BYTES ((int64_t)GWA_NOALLOC_SCRATCH_MIB << 20)
+
+/* gwa_svdq_w4a4_linear_fp6 without a workspace argument, for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). No counterpart in the reference.
+ * Its intermediates live in a static device array of
+ * GWA_NOALLOC_SCRATCH_BYTES inside this library (one copy per GPU, held
+ * until the process ends); a shape whose
+ * gwa_svdq_w4a4_linear_fp6_workspace(M, K, rank) exceeds it is refused with
+ * GWA_ERR_INVALID before anything is enqueued (at rank 32: K = 3072 fits up
+ * to 40,329 rows, K = 12288 up to 10,229, K = 15360 up to 8,191, so every
+ * linear of the 4608-token Flux-shaped DiT fits). Calls no hipMalloc, hipFree or
+ * other allocating routine. Every call on one GPU shares that GPU's array:
+ * calls that overlap on one GPU (different streams or threads without
+ * ordering between them) race. Nothing in the array needs to start at zero
+ * (every byte a call reads back was written earlier in the same call). Call it
+ * with the stream's device current. Same arguments and results as
+ * gwa_svdq_w4a4_linear_fp6. */
+int gwa_svdq_w4a4_linear_fp6_noalloc(const void* x, int64_t ldx, const void* smooth, const float* s2,
+                                     const void* proj_down_op6, int64_t rank, const uint8_t* qw6,
+                                     const float* second, int64_t second_numel, const void* proj_up,
+                                     const void* bias, void* out, int out_dtype, int epilogue_flags,
+                                     int64_t M, int64_t N, int64_t K, void* stream);
+
+/* GWA_NOALLOC_SCRATCH_BYTES, as the built library sees it. */
+int64_t gwa_svdq_w4a4_linear_fp6_noalloc_scratch_bytes(void);
+
 /* Standalone epilogue: out = y0 * (s2 * second) + la @ up^T + bias (bf16 out).
  * cozy_gen_worker::svdq_epilogue_lora, models/svdq_fused.py:315-377.
  *   y0 bf16 [M, N]; la bf16 [M, rank]; up bf16 [N, rank]; bias bf16 [N] or NULL */

@@ -2,6 +2,14 @@
 // as fp6 operand records, x @ proj_down as fp32 partial slots), the fixed-order la reduction, and the W4A4
 // GEMM with its fused epilogue, enqueued on one stream. The intermediates (records, partial slots, bf16 la)
 // live in a workspace the caller passes in; gwa_svdq_w4a4_linear_fp6_workspace gives its size.
+//
+// gwa_svdq_w4a4_linear_fp6_noalloc is the same call for callers that cannot allocate device memory: its
+// intermediates live in `scratch`, a fixed-size array of this library's code object (one copy per GPU, held
+// until the process ends). Host code never passes the array's name to a kernel: on the host that name is a
+// stand-in, not a device address. The device address of each GPU's copy is looked up once per device with
+// hipGetSymbolAddress (with that device current) and only that address is used.
+#include <mutex>
+
 #include "gwa_common.h"
 
 namespace {
@@ -57,6 +65,65 @@ int linear_fp6_run(const char* what, const void* x, int64_t ldx, const void* smo
 }
 
 }  // namespace
+
+// ---------------------------------------------------------------------------
+// zero-allocation variant
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr int64_t kScratchBytes = GWA_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+uint8_t* g_scratch_ptr[kMaxDevices] = {};
+
+// the device address of the current device's copy of `scratch` (looked up on the first call per device)
+int current_scratch(const char* what, uint8_t** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return gwa_set_error(GWA_ERR_HIP, "%s: hipGetDevice failed: %s", what, hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return gwa_set_error(GWA_ERR_INVALID, "%s: device %d is beyond the %d devices this library tracks", what, dev,
+                         kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return gwa_set_error(GWA_ERR_HIP, "%s: hipGetSymbolAddress(scratch) on device %d failed: %s", what, dev,
+                           hipGetErrorString(e));
+    if (!GWA_ALIGNED(p, 256))
+      return gwa_set_error(GWA_ERR_HIP, "%s: scratch on device %d is not 256-byte aligned", what, dev);
+    g_scratch_ptr[dev] = (uint8_t*)p;
+  }
+  *out = g_scratch_ptr[dev];
+  return GWA_OK;
+}
+
+}  // namespace
+
+extern "C" int gwa_svdq_w4a4_linear_fp6_noalloc(const void* x, int64_t ldx, const void* smooth, const float* s2,
+                                                const void* proj_down_op6, int64_t rank, const uint8_t* qw6,
+                                                const float* second, int64_t second_numel, const void* proj_up,
+                                                const void* bias, void* out, int out_dtype, int epilogue_flags,
+                                                int64_t M, int64_t N, int64_t K, void* stream) {
+  const char* what = "svdq_w4a4_linear_fp6_noalloc";
+  const int64_t need = gwa_svdq_w4a4_linear_fp6_workspace(M, K, proj_down_op6 ? rank : 0);
+  GWA_REQUIRE(need <= kScratchBytes,
+              "%s: M=%lld K=%lld rank=%lld needs %lld bytes of scratch; the library's static scratch holds %lld "
+              "(use gwa_svdq_w4a4_linear_fp6 with a workspace, or split the rows)",
+              what, (long long)M, (long long)K, (long long)rank, (long long)need, (long long)kScratchBytes);
+  uint8_t* ws = nullptr;
+  if (M > 0) {
+    const int rc = current_scratch(what, &ws);
+    if (rc != GWA_OK) return rc;
+  }
+  return linear_fp6_run(what, x, ldx, smooth, s2, proj_down_op6, rank, qw6, second, second_numel, proj_up, bias, out,
+                        out_dtype, epilogue_flags, M, N, K, ws, kScratchBytes, stream);
+}
+
+extern "C" int64_t gwa_svdq_w4a4_linear_fp6_noalloc_scratch_bytes(void) { return kScratchBytes; }
 
 extern "C" int64_t gwa_svdq_w4a4_linear_fp6_workspace(int64_t M, int64_t K, int64_t rank) {
   if (M <= 0 || K <= 0 || K % 128 || M >= (1ll << 31) || K >= (1ll << 24)) return 0;
