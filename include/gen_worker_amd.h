@@ -192,6 +192,21 @@ int gwa_svdq_gemm_w4a4_fp6_next(const uint8_t* qa6, const uint8_t* qw6,
  * tiles) for M rows and N outputs. */
 int64_t gwa_svdq_gemm_w4a4_fp6_next_partials(int64_t M, int64_t N);
 
+/* The output tile gwa_svdq_gemm_w4a4_fp6 uses for M rows and N outputs
+ * (GWA_FP6_TILE_*; -1 for an empty shape). No reference counterpart: the
+ * reference's Triton GEMM autotunes its tile (models/svdq_fused.py:157-178). */
+enum {
+  GWA_FP6_TILE_256x256 = 0, GWA_FP6_TILE_256x128 = 1, GWA_FP6_TILE_128x128 = 2, GWA_FP6_TILE_192x256 = 3,
+  GWA_FP6_TILE_288x192 = 4, GWA_FP6_TILE_256x192 = 5
+};
+int gwa_svdq_gemm_w4a4_fp6_tile(int64_t M, int64_t N);
+
+/* Test and tuning hook: every later gwa_svdq_gemm_w4a4_fp6 (and the one-call
+ * linears) uses this tile instead of the model's choice (-1 restores the
+ * model; the next-layer GEMM keeps its own 256-row tiles). Process-wide;
+ * returns the previous setting. */
+int gwa_svdq_gemm_w4a4_fp6_force_tile(int tile);
+
 /* Kernel 1 for the fp6 GEMM lane: the arithmetic of gwa_svdq_quant_int4
  * (same codes and scales, bit for bit) written as fp6 operand records, with
  * the low-rank product as fp32 partial sums (replaces

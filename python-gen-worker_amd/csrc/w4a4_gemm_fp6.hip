@@ -51,20 +51,13 @@
 // meanwhile. The fp32 accumulators are scalars so each fma accumulates in
 // place (v_fmac_f32, the 4-byte encoding). Tiles are ordered per XCD
 // (xcd_tile_of) so operands stay in that XCD's L2.
-#include "gwa_common.h"
+#include <atomic>
+
+#include "fp6_gemm_common.h"
 #include "quant_g64.h"
 
 namespace {
 
-constexpr int kTmMax = 256;                // tile rows: 256, or 192 / 128 for grids that leave CUs idle
-constexpr int NWAVES = 8, NTHREADS = 64 * NWAVES;  // 512
-constexpr int GS = 2;                      // groups per stage (one record)
-constexpr int GB = 48;                     // bytes of one row's group (64 e3m2 codes)
-constexpr int REC = GWA_FP6_REC;           // 104: record = LDS row stride
-constexpr int OFF_SC = GS * GB;            // 96: the record's scales
-constexpr int kLdsBytes = 160 * 1024;      // gfx950 LDS per workgroup
-constexpr int kFmtE3M2 = 3;                // cbsz / blgp code of e3m2 operands
-constexpr int kUnitE8M0 = 127;             // 2^0
 
 // Tile configurations: TN = 128 (64 x 64 wave tiles, registers for the
 // software pipeline, four stage buffers) or TN = 256 (64 x 128 wave tiles,
@@ -90,101 +83,6 @@ struct Cfg {
   static_assert(LDS_X % 1024 == 0 && LDS_W % 1024 == 0 && NBUF >= 3, "stage layout");
   static_assert(NBUF * SLOTS < 64, "vmcnt range");
 };
-
-// Direct-to-LDS copy of 16 bytes per lane: LDS [m0 + 16 lane, +16) <- buffer
-// [voff + soff, +16). The hardware range check covers voff only (not the
-// SGPR offset): a copy whose SGPR offset may point past the buffer must keep
-// its real address inside readable memory, or put its offset in voff (where
-// kOOB makes the lane read zeros without touching memory). Issued as asm so
-// the compiler's wait-count pass (which
-// tracks only a few LDS-DMA writes and then waits for all of them before any
-// LDS read) leaves the waits to the kernel: every LDS read of a stage buffer
-// comes after an s_waitcnt that covers this wave's copies into it and a
-// barrier that covers everyone else's. The "memory" clobber keeps the copy
-// in program order with the surrounding LDS accesses.
-__device__ __forceinline__ void dma16(v4i rsrc, uint32_t lds_addr, uint32_t voff, uint32_t soff) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-               :
-               : "s"(lds_addr), "v"(voff), "s"(rsrc), "s"(soff)
-               : "memory", "m0");
-}
-
-// raw buffer descriptor as an SGPR quad (base, stride 0, num_records, 32-bit data format)
-__device__ __forceinline__ v4i raw_rsrc(const void* base, uint32_t bytes) {
-  const uint64_t a = (uint64_t)base;
-  return (v4i){(int)(uint32_t)a, (int)(uint32_t)((a >> 32) & 0xFFFFu), (int)bytes, 0x00020000};
-}
-
-// compiler-only fence: keeps LDS reads and writes on their side of a barrier
-__device__ __forceinline__ void barrier_lds() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
-// s_waitcnt vmcnt(n) lgkmcnt(0) (gfx9 encoding; expcnt left at its maximum)
-template <int n>
-__device__ __forceinline__ void wait_vm_lgkm0() {
-  static_assert(n >= 0 && n < 64, "vmcnt");
-  __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4));
-}
-
-// wait until at most `newer` stages of `slots` copies each are still in flight
-template <int slots, int maxnewer>
-__device__ __forceinline__ void wait_stages(int newer) {
-  if constexpr (maxnewer >= 3) {
-    if (newer >= 3) { wait_vm_lgkm0<3 * slots>(); return; }
-  }
-  if constexpr (maxnewer >= 2) {
-    if (newer == 2) { wait_vm_lgkm0<2 * slots>(); return; }
-  }
-  if constexpr (maxnewer >= 1) {
-    if (newer == 1) { wait_vm_lgkm0<slots>(); return; }
-  }
-  wait_vm_lgkm0<0>();
-}
-
-__device__ __forceinline__ v16f group_mfma_fp6(v8i a, v8i b) {
-  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, (v16f){}, kFmtE3M2, kFmtE3M2, 0, kUnitE8M0, 0,
-                                                         kUnitE8M0);
-}
-
-// one lane's 32 codes of a group half: 24 bytes, three 8-byte LDS reads
-__device__ __forceinline__ v8i lds_operand(const uint8_t* p) {
-  const uint2 a = *(const uint2*)(p), b = *(const uint2*)(p + 8), c = *(const uint2*)(p + 16);
-  const v8i v = (v8i){(int)a.x, (int)a.y, (int)b.x, (int)b.y, (int)c.x, (int)c.y, 0, 0};
-  return v;
-}
-
-__device__ __forceinline__ v8i buf_operand(rsrc_t r, uint32_t off) {
-  typedef unsigned int v2u __attribute__((ext_vector_type(2)));
-  const v2u a = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
-  const v2u b = __builtin_amdgcn_raw_buffer_load_b64(r, off + 8, 0, 0);
-  const v2u c = __builtin_amdgcn_raw_buffer_load_b64(r, off + 16, 0, 0);
-  return (v8i){(int)a[0], (int)a[1], (int)b[0], (int)b[1], (int)c[0], (int)c[1], 0, 0};
-}
-
-// The next layer's side of the NQ epilogue: smoothing factors (bf16 [N] or
-// NULL), proj_down in the fp6 act-quant kernel's operand order (or NULL),
-// its rank / 16, the records [N / 128][M][104] and the la partial slots
-// [tiles_n][M][r] fp32.
-struct NextLayer {
-  const uint16_t* smooth;
-  const uint16_t* pdo;
-  int rb;
-  uint8_t* q6;
-  float* la_part;
-};
-constexpr int kNextRbMax = 8;  // next-layer ranks up to 128
-
-// la (bf16 or, with la_f32, fp32) row m, ranks 8 (k0 / 8) .. +8 -> 8 bf16 MFMA operand values
-__device__ __forceinline__ v4i la_operand_lds(const uint8_t* lrb, int row, int rowbytes, int k, bool la_f32) {
-  if (!la_f32) return *(const v4i*)(lrb + row * rowbytes + k * 2);
-  const v4f a = *(const v4f*)(lrb + row * rowbytes + k * 4);
-  const v4f b = *(const v4f*)(lrb + row * rowbytes + k * 4 + 16);
-  return (v4i){(int)pack_bf16x2_rn(a[0], a[1]), (int)pack_bf16x2_rn(a[2], a[3]), (int)pack_bf16x2_rn(b[0], b[1]),
-               (int)pack_bf16x2_rn(b[2], b[3])};
-}
 
 template <int TM, int TN, int RB, bool GELU, bool OUT_F16, bool NQ>
 __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_kernel(
@@ -817,32 +715,23 @@ extern "C" int gwa_svdq_group_psums_fp6(const uint8_t* qa6, const uint8_t* qw6, 
 
 namespace {
 
-struct Fp6Args {
-  const uint8_t* qa6;
-  const uint8_t* qw6;
-  const float* s2;
-  const float* second;
-  int per_channel;
-  const void* la;
-  int la_f32;
-  const uint16_t* up;
-  const uint16_t* bias;
-  uint16_t* out;
-  int M, N, K;
-};
-
 // tile shapes: 256 x 256 and 192 x 256 (128 x 64 and 96 x 64 wave tiles), 256 x 128 and 128 x 128 (64 x 64
-// and 32 x 64 wave tiles, with the software pipeline)
-enum Fp6Tile { kTile256x256 = 0, kTile256x128 = 1, kTile128x128 = 2, kTile192x256 = 3 };
+// and 32 x 64 wave tiles, with the software pipeline), and the pipelined kernel's 288 x 192 and 256 x 192
+// (w4a4_gemm_fp6_pipe.hip)
+enum Fp6Tile {
+  kTile256x256 = 0, kTile256x128 = 1, kTile128x128 = 2, kTile192x256 = 3, kTile288x192 = 4, kTile256x192 = 5,
+  kTileCount = 6
+};
+bool fp6_tile_pipelined(int tile) { return tile == kTile288x192 || tile == kTile256x192; }
 
 template <int TM, int TN, int RB, bool GL, bool F16, bool NQ>
-void launch_fp6_tile(dim3 grid, hipStream_t s, const Fp6Args& a, const NextLayer& nx) {
+void launch_fp6_tile(dim3 grid, hipStream_t s, const GwaFp6Args& a, const NextLayer& nx) {
   hipLaunchKernelGGL((w4a4_gemm_fp6_kernel<TM, TN, RB, GL, F16, NQ>), grid, dim3(NTHREADS), 0, s, a.qa6, a.qw6, a.s2,
                      a.second, a.per_channel, a.la, a.la_f32, a.up, a.bias, a.out, a.M, a.N, a.K, nx);
 }
 
 template <int RB, bool GL, bool F16, bool NQ>
-void launch_fp6_rb(int tile, dim3 grid, hipStream_t s, const Fp6Args& a, const NextLayer& nx) {
+void launch_fp6_rb(int tile, dim3 grid, hipStream_t s, const GwaFp6Args& a, const NextLayer& nx) {
   if (tile == kTile256x256)
     launch_fp6_tile<256, 256, RB, GL, F16, NQ>(grid, s, a, nx);
   else if (!NQ && tile == kTile192x256)
@@ -854,7 +743,7 @@ void launch_fp6_rb(int tile, dim3 grid, hipStream_t s, const Fp6Args& a, const N
 }
 
 template <int RB>
-void launch_fp6_flags(int tile, bool gelu, bool f16, bool nq, dim3 grid, hipStream_t s, const Fp6Args& a,
+void launch_fp6_flags(int tile, bool gelu, bool f16, bool nq, dim3 grid, hipStream_t s, const GwaFp6Args& a,
                       const NextLayer& nx) {
   if (nq) {  // the next layer's input is bf16: no f16 variant
     if (gelu) launch_fp6_rb<RB, true, false, true>(tile, grid, s, a, nx);
@@ -868,31 +757,42 @@ void launch_fp6_flags(int tile, bool gelu, bool f16, bool nq, dim3 grid, hipStre
   }
 }
 
-// One workgroup per CU (the stage buffers fill the LDS), so a grid runs in rounds of kCus tiles. Grids of
-// at least 192 256 x 256 tiles take that tile (it stages the fewest operand bytes per MAC); a smaller grid
-// takes the shape with the least estimated time: rounds x the tile's MACs x its time per MAC relative to
-// the 256 x 256 tile (one round of each at M=256, N=9216, K=3072: 51.4, 31.9, 23.0 us for 36 256 x 256,
-// 72 256 x 128 and 144 128 x 128 tiles; at M=1024: 54.3 and 44.0 us for 144 256 x 256 and 216 192 x 256
-// tiles). The next-layer epilogue needs 256-row tiles.
+// One workgroup per CU (the stage buffers fill the LDS), so a grid runs in rounds of kCus tiles. A grid takes
+// the tile shape with the least estimated time: rounds x the tile's MACs x its time per MAC relative to the
+// 256 x 256 tile (one round of each at M=256, N=9216, K=3072: 51.4, 31.9, 23.0 us for 36 256 x 256, 72
+// 256 x 128 and 144 128 x 128 tiles; at M=1024: 54.3 and 44.0 us for 144 256 x 256 and 216 192 x 256
+// tiles; one round of the 288 x 192 and 256 x 192 tiles at K=3072: 54.3 and 43.9 us against 54.9 and 54.6 us
+// for the 256 x 256 tile). The next-layer epilogue needs the 256-row, 256- or 128-column tiles.
 constexpr int kCus = 256;
+struct Fp6Shape {
+  int tile, tm, tn;
+  double per_mac;
+};
+constexpr Fp6Shape kFp6Shapes[kTileCount] = {{kTile256x256, 256, 256, 1.0},  {kTile256x128, 256, 128, 1.24},
+                                             {kTile128x128, 128, 128, 1.80}, {kTile192x256, 192, 256, 1.08},
+                                             {kTile288x192, 288, 192, 1.17}, {kTile256x192, 256, 192, 1.07}};
+std::atomic<int> g_force_tile{-1};  // test / tuning hook (gwa_svdq_gemm_w4a4_fp6_force_tile)
+
+bool fp6_tile_allowed(int tile, bool nq) { return !nq || tile == kTile256x256 || tile == kTile256x128; }
+
 int fp6_tile(int64_t M, int64_t N, bool nq) {
-  struct Shape { int tm, tn; double per_mac; };
-  static const Shape shapes[4] = {{256, 256, 1.0}, {256, 128, 1.24}, {128, 128, 1.80}, {192, 256, 1.08}};
-  if (((M + 255) / 256) * ((N + 255) / 256) >= 192) return kTile256x256;
-  int best = 0;
+  const int forced = g_force_tile.load(std::memory_order_relaxed);
+  if (forced >= 0 && forced < kTileCount && fp6_tile_allowed(forced, nq)) return forced;
+  int best = kTile256x256;
   double best_t = 0.0;
-  for (int i = 0; i < (nq ? 2 : 4); ++i) {
-    const int64_t tiles = ((M + shapes[i].tm - 1) / shapes[i].tm) * ((N + shapes[i].tn - 1) / shapes[i].tn);
-    const double t = (double)((tiles + kCus - 1) / kCus) * shapes[i].tm * shapes[i].tn * shapes[i].per_mac;
-    if (i == 0 || t < best_t * 0.999) {
-      best = i;
+  for (const Fp6Shape& sh : kFp6Shapes) {
+    if (!fp6_tile_allowed(sh.tile, nq)) continue;
+    const int64_t tiles = ((M + sh.tm - 1) / sh.tm) * ((N + sh.tn - 1) / sh.tn);
+    const double t = (double)((tiles + kCus - 1) / kCus) * sh.tm * sh.tn * sh.per_mac;
+    if (sh.tile == kTile256x256 || t < best_t * 0.999) {
+      best = sh.tile;
       best_t = t;
     }
   }
   return best;
 }
-int fp6_tile_m(int tile) { return tile == kTile128x128 ? 128 : (tile == kTile192x256 ? 192 : 256); }
-int fp6_tile_n(int tile) { return tile == kTile256x256 || tile == kTile192x256 ? 256 : 128; }
+int fp6_tile_m(int tile) { return kFp6Shapes[tile].tm; }
+int fp6_tile_n(int tile) { return kFp6Shapes[tile].tn; }
 
 // shared argument checks and launch of both GEMM entry points (nx.q6 != NULL: the NQ epilogue)
 int gemm_fp6(const char* what, const uint8_t* qa6, const uint8_t* qw6, const float* s2, const float* second,
@@ -915,7 +815,7 @@ int gemm_fp6(const char* what, const uint8_t* qa6, const uint8_t* qw6, const flo
   const int la_f32 = (epilogue_flags & GWA_EPI_LA_F32) ? 1 : 0;
   const int64_t nst = K / 128;
   // the DMA offsets of a tile's last run stay below 2^31 + 2^16
-  GWA_REQUIRE(nst * (M + kTmMax) * REC < (1ll << 31) && nst * (N + 256) * REC < (1ll << 31) && M * N * 2 < (1ll << 31) &&
+  GWA_REQUIRE(nst * (M + 288) * REC < (1ll << 31) && nst * (N + 256) * REC < (1ll << 31) && M * N * 2 < (1ll << 31) &&
                   M * R * 4 < (1ll << 31) && (N / 128) * M * REC < (1ll << 31),
               "%s: operands must stay below 2 GiB (buffer addressing)", what);
   if (M == 0) return GWA_OK;
@@ -930,11 +830,16 @@ int gemm_fp6(const char* what, const uint8_t* qa6, const uint8_t* qw6, const flo
   GWA_REQUIRE(tiles < (1ll << 30), "%s: too many tiles", what);
   const int64_t per_xcd = (tiles + kXcds - 1) / kXcds;
   const dim3 grid((unsigned)(per_xcd * kXcds));
-  const Fp6Args a{qa6, qw6, s2, second, (int)(second_numel > 1), la, la_f32, (const uint16_t*)up,
+  const GwaFp6Args a{qa6, qw6, s2, second, (int)(second_numel > 1), la, la_f32, (const uint16_t*)up,
                   (const uint16_t*)bias, (uint16_t*)out, (int)M, (int)N, (int)K};
   const bool gelu = epilogue_flags & GWA_EPI_GELU_TANH;
   const bool f16 = out_dtype == GWA_DT_F16;
   hipStream_t s = (hipStream_t)stream;
+  if (fp6_tile_pipelined(tile)) {
+    if (gwa_fp6_pipe_launch(TMv, (int)(R / 16), gelu, f16, grid, s, a) != 0)
+      return gwa_set_error(GWA_ERR_INVALID, "%s: rank %lld", what, (long long)R);
+    return gwa_check_launch(what);
+  }
   switch (R / 16) {
     case 0: launch_fp6_flags<0>(tile, gelu, f16, nq, grid, s, a, nx); break;
     case 1: launch_fp6_flags<1>(tile, gelu, f16, nq, grid, s, a, nx); break;
@@ -980,6 +885,15 @@ extern "C" int gwa_svdq_gemm_w4a4_fp6_next(const uint8_t* qa6, const uint8_t* qw
                      next_la_part};
   return gemm_fp6(what, qa6, qw6, s2, second, second_numel, la, up, rank, bias, out, GWA_DT_BF16, epilogue_flags, M,
                   N, K, nx, stream);
+}
+
+extern "C" int gwa_svdq_gemm_w4a4_fp6_tile(int64_t M, int64_t N) {
+  if (M <= 0 || N <= 0) return -1;
+  return fp6_tile(M, N, false);
+}
+
+extern "C" int gwa_svdq_gemm_w4a4_fp6_force_tile(int tile) {
+  return g_force_tile.exchange(tile >= 0 && tile < kTileCount ? tile : -1);
 }
 
 extern "C" int64_t gwa_svdq_gemm_w4a4_fp6_next_partials(int64_t M, int64_t N) {

@@ -66,6 +66,8 @@ _SIGNATURES: dict[str, tuple] = {
     "gwa_svdq_prep_proj_down_fp6": (_vp, _vp, _i64, _i64, _vp),
     "gwa_svdq_quant_fp6_partials": (_i64, _i64, _i64),
     "gwa_svdq_gemm_w4a4_fp6_next_partials": (_i64, _i64),
+    "gwa_svdq_gemm_w4a4_fp6_tile": (_i64, _i64),
+    "gwa_svdq_gemm_w4a4_fp6_force_tile": (_int,),
     "gwa_svdq_la_reduce": (_vp, _i64, _i64, _i64, _vp, _vp),
     "gwa_svdq_epilogue_lora": (_vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _i64, _i64, _vp),
     "gwa_w8a8_quant_int8": (_vp, _i64, _vp, _vp, _i64, _i64, _vp),

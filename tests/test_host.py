@@ -42,6 +42,25 @@ def test_library_is_a_gfx950_code_object():
     assert b"amdgcn-amd-amdhsa--gfx950" in data
 
 
+def test_fp6_tile_model_choices():
+    """The tile model (host code only): 288-row tiles for 4608-token layers (one tile per CU at N=3072),
+    256 x 192 for 4096 tokens, small tiles for short inputs, the forced tile while one is set."""
+    from gen_worker_amd import _native
+
+    lib = _native.load()
+    tile = lib.gwa_svdq_gemm_w4a4_fp6_tile
+    assert tile(0, 3072) == -1 and tile(16, 0) == -1
+    assert tile(4608, 3072) == 4 and tile(4608, 9216) == 4
+    assert tile(4096, 3072) == 5
+    assert tile(1024, 3072) == 2
+    prev = lib.gwa_svdq_gemm_w4a4_fp6_force_tile(1)
+    try:
+        assert tile(4608, 3072) == 1
+    finally:
+        lib.gwa_svdq_gemm_w4a4_fp6_force_tile(prev)
+    assert tile(4608, 3072) == 4
+
+
 def test_invalid_arguments_are_refused_before_any_launch():
     from gen_worker_amd import _native
 
