@@ -327,14 +327,28 @@ int gwa_svdq_epilogue_lora(const void* y0, const void* la, const void* up, int64
 int gwa_w8a8_quant_int8(const void* x, int64_t ldx, int8_t* q, float* sa,
                         int64_t M, int64_t K, void* stream);
 
-/* Kernel 3 — W8A8 GEMM with per-token x per-channel scales.
+/* W8A8 activation quantization in the reference's three modes: quantize(x2,
+ * pertensor, static) of models/w8a8.py:261-273 with the int8 formula above.
+ *   input_scale != NULL (static, the layer's input_scale buffer [1, 1] fp32):
+ *       sa = input_scale[0] unchanged; sa is [1] if pertensor, else [M] (the
+ *       reference's static.expand(M, 1));
+ *   input_scale == NULL, pertensor: sa [1] = max(amax(|x|)/127, 1e-12) over
+ *       the whole tensor; amax_ws is 4 bytes of device memory the call uses;
+ *   input_scale == NULL, !pertensor: per token, as gwa_w8a8_quant_int8.
+ *   q = clamp(rne(x / sa), -127, 127). */
+int gwa_w8a8_quant(const void* x, int64_t ldx, int8_t* q, float* sa, const float* input_scale, int pertensor,
+                   uint32_t* amax_ws, int64_t M, int64_t K, void* stream);
+
+/* Kernel 3 — W8A8 GEMM with per-token (sa_numel == M) or per-tensor
+ * (sa_numel == 1) activation scales and per-channel weight scales.
  * Replaces torch._scaled_mm(xq, W.t(), scale_a=sa, scale_b=weight_scale.t(),
- * bias, out_dtype) of models/w8a8.py:374-378:
- *   y[m,n] = (sum_k qa[m,k] qw[n,k]) * sa[m] * sw[n] + bias[n]
- *   qa int8 [M, K]; qw int8 [N, K]; sa fp32 [M]; sw fp32 [N]
+ * bias, out_dtype) of models/w8a8.py:374-378, and the pertensor branch
+ * (:366-372) with its weight scale and bias fused in fp32:
+ *   y[m,n] = (sum_k qa[m,k] qw[n,k]) * sa[m or 0] * sw[n] + bias[n]
+ *   qa int8 [M, K]; qw int8 [N, K]; sa fp32 [M] or [1]; sw fp32 [N]
  *   bias of bias_dtype [N] or NULL; out [M, N] of out_dtype (bf16/f16)
  * K % 64 == 0, N % 16 == 0. */
-int gwa_w8a8_gemm(const int8_t* qa, const int8_t* qw, const float* sa, const float* sw,
+int gwa_w8a8_gemm(const int8_t* qa, const int8_t* qw, const float* sa, int64_t sa_numel, const float* sw,
                   const void* bias, int bias_dtype, void* out, int out_dtype,
                   int64_t M, int64_t N, int64_t K, void* stream);
 

@@ -23,7 +23,8 @@ path in nvfp4 (e2m1 codes, e4m3 block-16 scales) and fp8; it refuses int4
   (``models/nvfp4_quant.py:54-56``), two's-complement nibbles;
 * int8 per-token activation quant = the reference's only int8 quantizer
   ``quantize_lowrank(scheme="int8")`` with the block = one row
-  (``models/svdq_layout.py:261-275``);
+  (``models/svdq_layout.py:261-275``); the W8A8 quantizer's per-tensor and
+  static-scale modes (``models/w8a8.py:261-273``) with the same formula;
 * GEMM + epilogue ``y = acc * (s2 * second) + la @ up^T + bias``
   (``models/svdq_fused.py:220-238``, ``:333-352``), with ``la = x @ proj_down``
   on RAW x (``models/svdq_fused.py:524``);
@@ -291,16 +292,26 @@ def fold_to_dense(qw: np.ndarray, sw: np.ndarray, smooth_bits: np.ndarray | None
 # a8 / a9: W8A8 int8
 # ----------------------------------------------------------------------------
 
-def quantize_act_int8(x_bits: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
-    """Per-token symmetric int8: (codes int8 [M, K], fp32 scales [M, 1]).
+def quantize_act_int8(x_bits: np.ndarray, pertensor: bool = False,
+                      static: float | None = None) -> tuple[np.ndarray, np.ndarray]:
+    """Symmetric int8 activation quant: (codes int8 [M, K], fp32 scales [M, 1] or [1, 1]).
 
     ``quantize_lowrank(scheme="int8")`` (``models/svdq_layout.py:261-275``)
     with the block = one row: ``scale = (absmax / 127).clamp(min=1e-12)``,
-    ``q = (x32 / scale).round().clamp(-127, 127)``.
+    ``q = (x32 / scale).round().clamp(-127, 127)``. The reference W8A8
+    quantizer's other modes (``models/w8a8.py:261-273``): ``pertensor`` takes
+    the absmax over the whole tensor (scale [1, 1]); a ``static`` scale is
+    used as given, [1, 1] if ``pertensor`` else repeated per row.
     """
     x = bf16_bits_to_f32(x_bits)
-    amax = np.abs(x).max(axis=-1, keepdims=True).astype(np.float32)
-    sa = np.maximum((amax / np.float32(INT8_QMAX)).astype(np.float32), np.float32(INT8_SCALE_MIN))
+    m = x.shape[0]
+    if static is not None:
+        sa = np.full((1 if pertensor else m, 1), static, np.float32)
+    else:
+        amax = np.abs(x).max(axis=-1, keepdims=True).astype(np.float32)
+        if pertensor:
+            amax = amax.max(axis=0, keepdims=True)
+        sa = np.maximum((amax / np.float32(INT8_QMAX)).astype(np.float32), np.float32(INT8_SCALE_MIN))
     with np.errstate(divide="ignore", invalid="ignore"):
         q = (x / sa).astype(np.float32)
     q = np.clip(np.rint(q), -INT8_QMAX, INT8_QMAX).astype(np.int8)
@@ -322,9 +333,11 @@ def int8_gemm(qa: np.ndarray, qw: np.ndarray) -> np.ndarray:
 
 
 def w8a8_linear(x_bits: np.ndarray, qw: np.ndarray, sw: np.ndarray,
-                bias: np.ndarray | None) -> np.ndarray:
-    """``_scaled_mm(xq, W^T, scale_a=sa, scale_b=sw^T, bias)`` (``models/w8a8.py:374-378``) in float64."""
-    qa, sa = quantize_act_int8(x_bits)
+                bias: np.ndarray | None, pertensor: bool = False,
+                static: float | None = None) -> np.ndarray:
+    """``_scaled_mm(xq, W^T, scale_a=sa, scale_b=sw^T, bias)`` (``models/w8a8.py:374-378``; the pertensor
+    branch ``:366-372`` applies the same scales) in float64, activation quant as :func:`quantize_act_int8`."""
+    qa, sa = quantize_act_int8(x_bits, pertensor, static)
     acc = int8_gemm(qa, qw).astype(np.float64)
     y = acc * sa.astype(np.float64) * sw.astype(np.float64).reshape(1, -1)
     if bias is not None:

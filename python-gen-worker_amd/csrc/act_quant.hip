@@ -459,16 +459,14 @@ __global__ __launch_bounds__(256) void prep_proj_down_kernel(const uint16_t* __r
 }
 
 // ---------------------------------------------------------------------------
-// int8 per-token quantization: one 256-thread block per row.
+// int8 activation quantization in the three modes of the reference's W8A8 quantizer: per-token scales from
+// each row's |x| maximum, one per-tensor scale from the whole tensor's maximum, or a static scale given by the
+// layer. One 256-thread block per row.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void w8a8_quant_int8_kernel(const uint16_t* __restrict__ x, int64_t ldx,
-                                                              int8_t* __restrict__ q, float* __restrict__ sa,
-                                                              int M, int K) {
-  __shared__ float red[4];
-  const int row = blockIdx.x;
-  const uint16_t* xr = x + (int64_t)row * ldx;
-  int8_t* qr = q + (int64_t)row * K;
-  const int nchunk = K >> 3;
+enum { kW8Row = 0, kW8Tensor = 1, kW8Static = 2 };
+
+// |x| maximum of one row (every thread of the block gets it)
+__device__ __forceinline__ float w8a8_row_amax(const uint16_t* xr, int nchunk, float* red) {
   float am = 0.0f;
   for (int c = threadIdx.x; c < nchunk; c += 256) {
     float v[8];
@@ -480,8 +478,37 @@ __global__ __launch_bounds__(256) void w8a8_quant_int8_kernel(const uint16_t* __
   for (int off = 32; off >= 1; off >>= 1) am = fmaxf(am, __shfl_xor(am, off));
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = am;
   __syncthreads();
-  am = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  const float s = fmaxf(am / 127.0f, 1e-12f);
+  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+// Per-tensor maximum: each block folds the maximum of its rows into *amax_bits with an atomic max on the bit
+// pattern (non-negative floats order as their bits); w8a8_clear_kernel zeroes the cell first.
+__global__ void w8a8_clear_kernel(uint32_t* __restrict__ cell) { *cell = 0u; }
+
+__global__ __launch_bounds__(256) void w8a8_amax_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                        uint32_t* __restrict__ amax_bits, int M, int K) {
+  __shared__ float red[4];
+  float am = 0.0f;
+  for (int row = blockIdx.x; row < M; row += gridDim.x) {
+    am = fmaxf(am, w8a8_row_amax(x + (int64_t)row * ldx, K >> 3, red));
+    __syncthreads();  // red is reused by the next row
+  }
+  if (threadIdx.x == 0) atomicMax(amax_bits, __float_as_uint(am));
+}
+
+template <int MODE>
+__global__ __launch_bounds__(256) void w8a8_quant_int8_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                              int8_t* __restrict__ q, float* __restrict__ sa,
+                                                              const float* __restrict__ src, int sa_per_row, int K) {
+  __shared__ float red[4];
+  const int row = blockIdx.x;
+  const uint16_t* xr = x + (int64_t)row * ldx;
+  int8_t* qr = q + (int64_t)row * K;
+  const int nchunk = K >> 3;
+  float s;
+  if constexpr (MODE == kW8Row) s = fmaxf(w8a8_row_amax(xr, nchunk, red) / 127.0f, 1e-12f);
+  else if constexpr (MODE == kW8Tensor) s = fmaxf(__uint_as_float(*(const uint32_t*)src) / 127.0f, 1e-12f);
+  else s = *src;
   for (int c = threadIdx.x; c < nchunk; c += 256) {
     float v[8];
     unpack8_bf16(*(const v4i*)(xr + c * 8), v);
@@ -494,7 +521,8 @@ __global__ __launch_bounds__(256) void w8a8_quant_int8_kernel(const uint16_t* __
     }
     *(uint2*)(qr + c * 8) = make_uint2(w[0], w[1]);
   }
-  if (threadIdx.x == 0) sa[row] = s;
+  // one scale per row ([M] output), or the one per-tensor scale ([1] output) from row 0
+  if (threadIdx.x == 0 && (sa_per_row || row == 0)) sa[sa_per_row ? row : 0] = s;
 }
 
 // ---------------------------------------------------------------------------
@@ -674,19 +702,42 @@ extern "C" int gwa_svdq_quant_int4(const void* x, int64_t ldx, const void* smoot
   return gwa_check_launch("svdq_quant_int4");
 }
 
+extern "C" int gwa_w8a8_quant(const void* x, int64_t ldx, int8_t* q, float* sa, const float* input_scale,
+                              int pertensor, uint32_t* amax_ws, int64_t M, int64_t K, void* stream) {
+  const char* what = "w8a8_quant";
+  GWA_REQUIRE(M >= 0 && K > 0 && K % 8 == 0, "%s: bad shape M=%lld K=%lld (K %% 8 == 0)", what, (long long)M,
+              (long long)K);
+  GWA_REQUIRE(ldx >= K && ldx % 8 == 0, "%s: bad row stride %lld", what, (long long)ldx);
+  GWA_REQUIRE(M < (1ll << 31) && K < (1ll << 30), "%s: shape too large", what);
+  GWA_REQUIRE(pertensor == 0 || pertensor == 1, "%s: pertensor must be 0 or 1", what);
+  if (M == 0) return GWA_OK;
+  GWA_REQUIRE(x && q && sa, "%s: null pointer", what);
+  GWA_REQUIRE(!pertensor || input_scale || amax_ws, "%s: the dynamic per-tensor mode needs amax_ws", what);
+  GWA_REQUIRE(GWA_ALIGNED(x, 16) && GWA_ALIGNED(q, 8) && GWA_ALIGNED(sa, 4) && GWA_ALIGNED(input_scale, 4) &&
+                  GWA_ALIGNED(amax_ws, 4),
+              "%s: x must be 16-byte, q 8-byte and the scales 4-byte aligned", what);
+  hipStream_t s = (hipStream_t)stream;
+  const uint16_t* xp = (const uint16_t*)x;
+  const dim3 grid((unsigned)M), block(256);
+  const int per_row = pertensor ? 0 : 1;
+  if (input_scale) {
+    hipLaunchKernelGGL((w8a8_quant_int8_kernel<kW8Static>), grid, block, 0, s, xp, ldx, q, sa, input_scale, per_row,
+                       (int)K);
+  } else if (pertensor) {
+    hipLaunchKernelGGL(w8a8_clear_kernel, dim3(1), dim3(1), 0, s, amax_ws);
+    const unsigned amax_blocks = (unsigned)(M < 2048 ? M : 2048);
+    hipLaunchKernelGGL(w8a8_amax_kernel, dim3(amax_blocks), block, 0, s, xp, ldx, amax_ws, (int)M, (int)K);
+    hipLaunchKernelGGL((w8a8_quant_int8_kernel<kW8Tensor>), grid, block, 0, s, xp, ldx, q, sa,
+                       (const float*)amax_ws, 0, (int)K);
+  } else {
+    hipLaunchKernelGGL((w8a8_quant_int8_kernel<kW8Row>), grid, block, 0, s, xp, ldx, q, sa, nullptr, 1, (int)K);
+  }
+  return gwa_check_launch(what);
+}
+
 extern "C" int gwa_w8a8_quant_int8(const void* x, int64_t ldx, int8_t* q, float* sa, int64_t M, int64_t K,
                                    void* stream) {
-  GWA_REQUIRE(M >= 0 && K > 0 && K % 8 == 0, "w8a8_quant_int8: bad shape M=%lld K=%lld (K %% 8 == 0)",
-              (long long)M, (long long)K);
-  GWA_REQUIRE(ldx >= K && ldx % 8 == 0, "w8a8_quant_int8: bad row stride %lld", (long long)ldx);
-  GWA_REQUIRE(M < (1ll << 31) && K < (1ll << 30), "w8a8_quant_int8: shape too large");
-  if (M == 0) return GWA_OK;
-  GWA_REQUIRE(x && q && sa, "w8a8_quant_int8: null pointer");
-  GWA_REQUIRE(GWA_ALIGNED(x, 16) && GWA_ALIGNED(q, 8) && GWA_ALIGNED(sa, 4),
-              "w8a8_quant_int8: x must be 16-byte and q 8-byte aligned");
-  hipLaunchKernelGGL(w8a8_quant_int8_kernel, dim3((unsigned)M), dim3(256), 0, (hipStream_t)stream,
-                     (const uint16_t*)x, ldx, q, sa, (int)M, (int)K);
-  return gwa_check_launch("w8a8_quant_int8");
+  return gwa_w8a8_quant(x, ldx, q, sa, nullptr, 0, nullptr, M, K, stream);
 }
 
 extern "C" int gwa_svdq_epilogue_lora(const void* y0, const void* la, const void* up, int64_t rank,

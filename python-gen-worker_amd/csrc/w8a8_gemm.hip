@@ -1,6 +1,8 @@
 // W8A8 GEMM: int8 MFMA 32x32x32 with int32 accumulation over the whole K and
-// the per-token x per-output-channel fp32 epilogue of torch._scaled_mm's
-// rowwise mode (models/w8a8.py:374-378).
+// the fp32 epilogue acc * sa * sw[n] + bias[n] of torch._scaled_mm: per-token
+// activation scales in the rowwise mode (models/w8a8.py:374-378), one scalar in
+// the pertensor mode (:366-372, whose weight scale and bias the reference
+// applies as two further bf16 ops; here they are fused in fp32).
 //
 // Same orientation as the W4A4 kernel: A operand = weight rows (n), B operand
 // = activation rows (m); accumulator block D[n][m], lane l holds m = l % 32
@@ -21,7 +23,8 @@ __global__ __launch_bounds__(256) void w8a8_gemm_kernel(const int8_t* __restrict
                                                         const float* __restrict__ sa,
                                                         const float* __restrict__ sw,
                                                         const void* __restrict__ bias,
-                                                        uint16_t* __restrict__ out, int M, int N, int K) {
+                                                        uint16_t* __restrict__ out, int M, int N, int K,
+                                                        int sa_row) {
   __shared__ __attribute__((aligned(16))) uint8_t lds_w[2][LDS_TILE];
   __shared__ __attribute__((aligned(16))) uint8_t lds_x[2][LDS_TILE];
 
@@ -96,7 +99,7 @@ __global__ __launch_bounds__(256) void w8a8_gemm_kernel(const int8_t* __restrict
     for (int bm = 0; bm < 2; ++bm) {
       const int m = m0 + 64 * wm + 32 * bm + r32;
       if (m >= M) continue;
-      const float am = sa[m];
+      const float am = sa[sa_row ? m : 0];
 #pragma unroll
       for (int qd = 0; qd < 4; ++qd) {
         const int n = nb + 8 * qd + 4 * h;
@@ -126,9 +129,9 @@ __global__ __launch_bounds__(256) void w8a8_gemm_kernel(const int8_t* __restrict
 
 }  // namespace
 
-extern "C" int gwa_w8a8_gemm(const int8_t* qa, const int8_t* qw, const float* sa, const float* sw,
-                             const void* bias, int bias_dtype, void* out, int out_dtype, int64_t M, int64_t N,
-                             int64_t K, void* stream) {
+extern "C" int gwa_w8a8_gemm(const int8_t* qa, const int8_t* qw, const float* sa, int64_t sa_numel,
+                             const float* sw, const void* bias, int bias_dtype, void* out, int out_dtype, int64_t M,
+                             int64_t N, int64_t K, void* stream) {
   GWA_REQUIRE(M >= 0 && N > 0 && K > 0, "w8a8_gemm: bad shape M=%lld N=%lld K=%lld", (long long)M, (long long)N,
               (long long)K);
   GWA_REQUIRE(K % 64 == 0, "w8a8_gemm: K=%lld is not a multiple of 64", (long long)K);
@@ -139,6 +142,8 @@ extern "C" int gwa_w8a8_gemm(const int8_t* qa, const int8_t* qw, const float* sa
               "w8a8_gemm: bias_dtype %d", bias_dtype);
   GWA_REQUIRE(M < (1ll << 31) && N < (1ll << 30) && K < (1ll << 30), "w8a8_gemm: shape too large");
   if (M == 0) return GWA_OK;
+  GWA_REQUIRE(sa_numel == 1 || sa_numel == M, "w8a8_gemm: sa has %lld values for M=%lld (1 or M)",
+              (long long)sa_numel, (long long)M);
   GWA_REQUIRE(qa && qw && sa && sw && out, "w8a8_gemm: null pointer");
   GWA_REQUIRE(GWA_ALIGNED(qa, 16) && GWA_ALIGNED(qw, 16) && GWA_ALIGNED(out, 8) && GWA_ALIGNED(sa, 4) &&
                   GWA_ALIGNED(sw, 4) && GWA_ALIGNED(bias, 2),
@@ -149,11 +154,11 @@ extern "C" int gwa_w8a8_gemm(const int8_t* qa, const int8_t* qw, const float* sa
   const dim3 grid((unsigned)tiles), block(256);
   const bool f16 = out_dtype == GWA_DT_F16;
   uint16_t* op = (uint16_t*)out;
-  const int m = (int)M, n = (int)N, k = (int)K;
+  const int m = (int)M, n = (int)N, k = (int)K, sr = sa_numel == M && M > 1 ? 1 : 0;
 #define GWA_W8A8_LAUNCH(BD)                                                                                   \
   do {                                                                                                        \
-    if (f16) hipLaunchKernelGGL((w8a8_gemm_kernel<BD, true>), grid, block, 0, s, qa, qw, sa, sw, bias, op, m, n, k); \
-    else hipLaunchKernelGGL((w8a8_gemm_kernel<BD, false>), grid, block, 0, s, qa, qw, sa, sw, bias, op, m, n, k);    \
+    if (f16) hipLaunchKernelGGL((w8a8_gemm_kernel<BD, true>), grid, block, 0, s, qa, qw, sa, sw, bias, op, m, n, k, sr); \
+    else hipLaunchKernelGGL((w8a8_gemm_kernel<BD, false>), grid, block, 0, s, qa, qw, sa, sw, bias, op, m, n, k, sr);    \
   } while (0)
   if (!bias) GWA_W8A8_LAUNCH(-1);
   else if (bias_dtype == GWA_DT_F32) GWA_W8A8_LAUNCH(GWA_DT_F32);

@@ -36,8 +36,9 @@ separate steps):
 * ``svdq_w4a4_linear(qa, sa, weight, wscales, s2, second, la, up, bias,
   out_dtype, gelu)``: kernel 2 on the resident ``weight`` [N, K/2] layout.
 * ``svdq_group_psums(qa, qw)``: exact int32 per-group partial sums (debug).
-* ``w8a8_quant(x2) -> (q, sa)`` and ``w8a8_scaled_mm(qa, weight, sa,
-  weight_scale, bias, out_dtype)``: the int8 lane.
+* ``w8a8_quant(x2, pertensor=False, static=None) -> (q, sa)`` and
+  ``w8a8_scaled_mm(qa, weight, sa, weight_scale, bias, out_dtype)``: the int8
+  lane, in the reference's rowwise, pertensor and static-scale modes.
 * ``awq_w4a16_mm(x2, weight, wscales, wzeros, bias)``: the reference's packed
   AWQ W4A16 op (``models/svdq_awq_packed.py:48-115``, same name and schema)
   for the M = 1 modulation layers, and ``awq_w4a16_dequant(weight, wscales,
@@ -737,28 +738,37 @@ def _(qa, qw):
 # ---------------------------------------------------------------------------
 
 @torch.library.custom_op("cozy_gen_worker::w8a8_quant", mutates_args=())
-def w8a8_quant(x2: Tensor) -> tuple[Tensor, Tensor]:
-    """Per-token int8: (q int8 [M, K], sa fp32 [M, 1])."""
+def w8a8_quant(x2: Tensor, pertensor: bool = False, static: Optional[Tensor] = None) -> tuple[Tensor, Tensor]:
+    """int8 activation quant in the modes of the reference's ``quantize(x2, pertensor, static)``
+    (``models/w8a8.py:261-273``): ``static`` (the layer's ``input_scale`` [1, 1] fp32) is used unchanged,
+    as ``sa`` [1, 1] when ``pertensor`` else expanded to [M, 1]; without it ``sa`` is ``max(amax/127, 1e-12)``
+    over the whole tensor ([1, 1]) or per token ([M, 1]). Returns (q int8 [M, K], sa)."""
     name = "w8a8_quant"
     _check_dtype(name, x2, torch.bfloat16, what="x2")
-    _check_cuda(name, x2=x2)
+    _check_dtype(name, static, torch.float32, what="static")
+    _check_cuda(name, x2=x2, static=static)
+    if static is not None and static.numel() != 1:
+        raise SvdqOpError(f"{name}: static has {static.numel()} values; the input scale is one scalar")
     m, k = int(x2.shape[0]), int(x2.shape[1])
     q = torch.empty(m, k, dtype=torch.int8, device=x2.device)
-    sa = torch.empty(m, 1, dtype=torch.float32, device=x2.device)
-    nat.call("gwa_w8a8_quant_int8", nat.ptr(x2), k, nat.ptr(q), nat.ptr(sa), m, k, nat.stream_of(x2))
+    sa = torch.empty(1 if pertensor else m, 1, dtype=torch.float32, device=x2.device)
+    ws = torch.empty(1, dtype=torch.int32, device=x2.device) if pertensor and static is None else None
+    nat.call("gwa_w8a8_quant", nat.ptr(x2), k, nat.ptr(q), nat.ptr(sa), nat.ptr(static), int(bool(pertensor)),
+             nat.ptr(ws), m, k, nat.stream_of(x2))
     return q, sa
 
 
 @w8a8_quant.register_fake
-def _(x2):
+def _(x2, pertensor=False, static=None):
     m, k = int(x2.shape[0]), int(x2.shape[1])
-    return x2.new_empty(m, k, dtype=torch.int8), x2.new_empty(m, 1, dtype=torch.float32)
+    return x2.new_empty(m, k, dtype=torch.int8), x2.new_empty(1 if pertensor else m, 1, dtype=torch.float32)
 
 
 @torch.library.custom_op("cozy_gen_worker::w8a8_scaled_mm", mutates_args=())
 def w8a8_scaled_mm(qa: Tensor, weight: Tensor, sa: Tensor, weight_scale: Tensor, bias: Optional[Tensor],
                    out_dtype: torch.dtype) -> Tensor:
-    """``_scaled_mm(qa, weight.t(), scale_a=sa, scale_b=weight_scale.t(), bias, out_dtype)`` on int8 codes."""
+    """``_scaled_mm(qa, weight.t(), scale_a=sa, scale_b=weight_scale.t(), bias, out_dtype)`` on int8 codes;
+    ``sa`` holds one scale per row ([M, 1], rowwise) or one for the tensor ([1, 1], pertensor)."""
     name = "w8a8_scaled_mm"
     _check_dtype(name, qa, torch.int8, what="qa")
     _check_dtype(name, weight, torch.int8, what="weight")
@@ -770,15 +780,15 @@ def w8a8_scaled_mm(qa: Tensor, weight: Tensor, sa: Tensor, weight_scale: Tensor,
         raise SvdqOpError(f"{name}: out_dtype {out_dtype} not bf16/fp16")
     m, k = int(qa.shape[0]), int(qa.shape[1])
     n = int(weight.shape[0])
-    if int(weight.shape[1]) != k or sa.numel() != m or weight_scale.numel() != n:
+    if int(weight.shape[1]) != k or sa.numel() not in (1, m) or weight_scale.numel() != n:
         raise SvdqOpError(f"{name}: shapes qa {tuple(qa.shape)} weight {tuple(weight.shape)} sa {tuple(sa.shape)} "
                           f"weight_scale {tuple(weight_scale.shape)} disagree")
     if bias is not None and bias.numel() != n:
         raise SvdqOpError(f"{name}: bias has {bias.numel()} values for N={n}")
     out = torch.empty(m, n, dtype=out_dtype, device=qa.device)
-    nat.call("gwa_w8a8_gemm", nat.ptr(qa), nat.ptr(weight), nat.ptr(sa), nat.ptr(weight_scale), nat.ptr(bias),
-             _dt_code(bias.dtype) if bias is not None else 0, nat.ptr(out), _dt_code(out_dtype), m, n, k,
-             nat.stream_of(qa))
+    nat.call("gwa_w8a8_gemm", nat.ptr(qa), nat.ptr(weight), nat.ptr(sa), sa.numel(), nat.ptr(weight_scale),
+             nat.ptr(bias), _dt_code(bias.dtype) if bias is not None else 0, nat.ptr(out), _dt_code(out_dtype),
+             m, n, k, nat.stream_of(qa))
     return out
 
 

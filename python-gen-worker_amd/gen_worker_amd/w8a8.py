@@ -2,10 +2,13 @@
 
 ``Int8ScaledLinear`` is the int8 counterpart of the reference's
 ``_Fp8ScaledLinear`` (``src/gen_worker/models/w8a8.py:319-388``): buffers
-``weight`` [out, in], ``weight_scale`` [out, 1] fp32, optional ``bias``,
-optional ``lora_a`` / ``lora_b``; forward = per-token activation quant
-(``:363``) -> scaled int8 GEMM with per-token x per-channel scales and the
-bias in the epilogue (``:374-378``) -> optional LoRA addend (``:379-380``).
+``weight`` [out, in], ``weight_scale`` [out, 1] fp32, ``input_scale`` [1, 1]
+fp32 when the checkpoint carries a static activation scale, optional ``bias``,
+optional ``lora_a`` / ``lora_b``; ``gemm_mode`` "rowwise" (per-token
+activation scales) or "pertensor" (one activation scale per call). forward =
+activation quant in that mode (``:363``) -> scaled int8 GEMM with the
+activation scale(s), per-channel weight scales and the bias in the epilogue
+(``:366-378``) -> optional LoRA addend (``:379-380``).
 The quantizer is the reference's int8 formula (``models/svdq_layout.py:261-275``)
 with one block per row.
 """
@@ -36,23 +39,38 @@ def quantize_weight_int8(w: Tensor) -> tuple[Tensor, Tensor]:
     return q, scale.float()
 
 
+GEMM_MODES = ("rowwise", "pertensor")
+
+
 class Int8ScaledLinear(nn.Module):
-    """Per-token x per-channel W8A8 linear on the HIP int8 GEMM."""
+    """W8A8 linear on the HIP int8 GEMM: per-token or per-tensor activation scales (dynamic, or the static
+    ``input_scale``) x per-channel weight scales."""
 
     _cozy_w8a8_linear = True
 
     def __init__(self, in_features: int, out_features: int, *, bias: bool, compute_dtype: Any = torch.bfloat16,
-                 bias_dtype: Optional[torch.dtype] = None, device: Any = None) -> None:
+                 bias_dtype: Optional[torch.dtype] = None, device: Any = None, static_input_scale: bool = False,
+                 gemm_mode: str = "rowwise") -> None:
         super().__init__()
         if in_features % 64 or out_features % _DIM_ALIGN:
             raise W8a8Error(f"Int8ScaledLinear [{out_features}, {in_features}] breaks the kernel contract "
                             f"(in%64, out%{_DIM_ALIGN})")
+        if gemm_mode not in GEMM_MODES:
+            raise W8a8Error(f"Int8ScaledLinear: gemm_mode {gemm_mode!r} is not one of {GEMM_MODES}")
         self.in_features = int(in_features)
         self.out_features = int(out_features)
         self.compute_dtype = compute_dtype
+        self.gemm_mode = gemm_mode
         dev = torch.device(device) if device is not None else torch.device("meta")
         self.register_buffer("weight", torch.empty(out_features, in_features, dtype=torch.int8, device=dev))
         self.register_buffer("weight_scale", torch.empty(out_features, 1, dtype=torch.float32, device=dev))
+        # a static activation scale is a state-dict entry of the checkpoints that carry one; dynamic layers
+        # have no such key
+        self.input_scale: Optional[Tensor]
+        if static_input_scale:
+            self.register_buffer("input_scale", torch.empty(1, 1, dtype=torch.float32, device=dev))
+        else:
+            self.input_scale = None
         if bias:
             self.bias: Optional[nn.Parameter] = nn.Parameter(
                 torch.empty(out_features, dtype=bias_dtype or compute_dtype, device=dev), requires_grad=False)
@@ -70,7 +88,7 @@ class Int8ScaledLinear(nn.Module):
         if x2.dtype != torch.bfloat16:
             raise W8a8Error(f"Int8ScaledLinear expects bf16 activations, got {x2.dtype}")
         x2 = x2.contiguous()
-        xq, sa = torch.ops.cozy_gen_worker.w8a8_quant(x2)
+        xq, sa = torch.ops.cozy_gen_worker.w8a8_quant(x2, self.gemm_mode == "pertensor", self.input_scale)
         y = torch.ops.cozy_gen_worker.w8a8_scaled_mm(xq, self.weight, sa, self.weight_scale, self.bias,
                                                      self.compute_dtype)
         if self.lora_a is not None:
@@ -79,17 +97,25 @@ class Int8ScaledLinear(nn.Module):
 
     def extra_repr(self) -> str:
         return (f"in_features={self.in_features}, out_features={self.out_features}, "
-                f"bias={self.bias is not None}, lane=int8-rowwise")
+                f"bias={self.bias is not None}, gemm_mode={self.gemm_mode}, "
+                f"static_input_scale={self.input_scale is not None}")
 
 
 def build_int8_linear(*, qweight: Tensor, weight_scale: Tensor, bias: Optional[Tensor],
-                      compute_dtype: Any = torch.bfloat16, device: Any = "cuda") -> Int8ScaledLinear:
+                      compute_dtype: Any = torch.bfloat16, device: Any = "cuda",
+                      input_scale: Optional[Tensor] = None, gemm_mode: str = "rowwise") -> Int8ScaledLinear:
     n, k = int(qweight.shape[0]), int(qweight.shape[1])
     mod = Int8ScaledLinear(k, n, bias=bias is not None, compute_dtype=compute_dtype,
-                           bias_dtype=bias.dtype if bias is not None else None, device=device)
+                           bias_dtype=bias.dtype if bias is not None else None, device=device,
+                           static_input_scale=input_scale is not None, gemm_mode=gemm_mode)
     with torch.no_grad():
         mod.weight.copy_(qweight.to(torch.int8))
         mod.weight_scale.copy_(weight_scale.float().reshape(n, 1))
+        if input_scale is not None:
+            if input_scale.numel() != 1:
+                raise W8a8Error(f"input_scale has {input_scale.numel()} values; a static activation scale is "
+                                f"one scalar")
+            mod.input_scale.copy_(input_scale.float().reshape(1, 1))
         if bias is not None:
             mod.bias.copy_(bias.reshape(-1))
     return mod
@@ -103,4 +129,5 @@ def quantize_linear_w8a8(linear: nn.Linear, *, compute_dtype: Any = torch.bfloat
     return build_int8_linear(qweight=q, weight_scale=s, bias=b, compute_dtype=compute_dtype, device=device)
 
 
-__all__ = ["Int8ScaledLinear", "W8a8Error", "build_int8_linear", "quantize_linear_w8a8", "quantize_weight_int8"]
+__all__ = ["GEMM_MODES", "Int8ScaledLinear", "W8a8Error", "build_int8_linear", "quantize_linear_w8a8",
+           "quantize_weight_int8"]

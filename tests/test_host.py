@@ -98,7 +98,7 @@ def test_invalid_arguments_are_refused_before_any_launch():
     rc = lib.gwa_svdq_gemm_w4a4(None, None, None, None, None, None, 0, None, None, 0, None, None, 0, 0,
                                 8, 24, 128, None)
     assert rc == 1 and "multiple of 16" in lib.gwa_last_error().decode()
-    rc = lib.gwa_w8a8_gemm(None, None, None, None, None, 0, None, 7, 8, 64, 64, None)
+    rc = lib.gwa_w8a8_gemm(None, None, None, 8, None, None, 0, None, 7, 8, 64, 64, None)
     assert rc == 1 and "out_dtype" in lib.gwa_last_error().decode()
     rc = lib.gwa_transpose_2d(None, None, 4, 4, 3, None)
     assert rc == 1
@@ -111,7 +111,7 @@ def test_native_error_is_raised_with_message():
     from gen_worker_amd import _native
 
     with pytest.raises(_native.NativeError, match="multiple of 64"):
-        _native.call("gwa_w8a8_gemm", None, None, None, None, None, 0, None, 0, 8, 64, 100, None)
+        _native.call("gwa_w8a8_gemm", None, None, None, 8, None, None, 0, None, 0, 8, 64, 100, None)
 
 
 def test_ops_refuse_cpu_tensors():
@@ -319,3 +319,23 @@ def test_module_move_drops_derived_buffers():
     mod = mod.to("cpu")
     assert mod.weight_fp6 is None and mod.proj_down_op6 is None and mod.proj_down_op is None
     assert mod.weight.shape == (128, 128) and mod.proj_down.shape == (256, 16)
+
+
+def test_w8a8_module_modes_on_cpu():
+    """Int8ScaledLinear's mode contract, host side: the reference's two GEMM modes only, an ``input_scale``
+    state-dict entry exactly when the layer has a static scale, and a static scale must be one scalar."""
+    from gen_worker_amd import synthetic
+    from gen_worker_amd.w8a8 import Int8ScaledLinear, W8a8Error, build_int8_linear
+
+    with pytest.raises(W8a8Error, match="gemm_mode"):
+        Int8ScaledLinear(64, 64, bias=False, gemm_mode="blockwise")
+    assert "input_scale" not in Int8ScaledLinear(64, 64, bias=False).state_dict()
+    sd = Int8ScaledLinear(64, 64, bias=False, static_input_scale=True, gemm_mode="pertensor").state_dict()
+    assert sd["input_scale"].shape == (1, 1) and sd["input_scale"].dtype == torch.float32
+    L = synthetic.w8a8_layer(64, 64)
+    mod = build_int8_linear(qweight=L.qweight, weight_scale=L.weight_scale, bias=None, device="cpu",
+                            input_scale=torch.tensor(0.5), gemm_mode="pertensor")
+    assert float(mod.input_scale) == 0.5 and mod.gemm_mode == "pertensor"
+    with pytest.raises(W8a8Error, match="one scalar"):
+        build_int8_linear(qweight=L.qweight, weight_scale=L.weight_scale, bias=None, device="cpu",
+                          input_scale=torch.ones(2))

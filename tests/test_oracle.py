@@ -277,6 +277,65 @@ def test_int8_exact_rational():
             assert q[r, j] == want
 
 
+def test_int8_pertensor_and_static_known_answers():
+    """The W8A8 quantizer's other modes (models/w8a8.py:261-273) on hand-computed rows: per-tensor takes
+    the largest |x| of any row (rows with small values then quantize coarsely), a static scale is used as
+    given (no clamp), and a static scale of 2^-3 turns multiples of 1/8 into their integer codes."""
+    x = np.zeros((3, 8), np.float32)
+    x[0, :3] = [127.0, -63.5, 0.5]
+    x[1, :3] = [1.5, -2.5, 0.25]
+    xb = O.f32_to_bf16_bits(x)
+    q, sa = O.quantize_act_int8(xb, pertensor=True)
+    assert sa.shape == (1, 1) and sa[0, 0] == 1.0
+    assert q[0, :3].tolist() == [127, -64, 0] and q[1, :3].tolist() == [2, -2, 0] and not q[2].any()
+    q, sa = O.quantize_act_int8(O.f32_to_bf16_bits(np.zeros((2, 8), np.float32)), pertensor=True)
+    assert sa[0, 0] == np.float32(1e-12) and not q.any()
+    codes = np.arange(-127, 129, dtype=np.int64).reshape(2, 128)
+    codes[1, -1] = 500                                          # beyond the int8 range: clamps to 127
+    xs = O.f32_to_bf16_bits((codes / 8.0).astype(np.float32))
+    for pt in (False, True):
+        q, sa = O.quantize_act_int8(xs, pertensor=pt, static=0.125)
+        assert sa.shape == ((1, 1) if pt else (2, 1)) and (sa == np.float32(0.125)).all()
+        assert q.astype(np.int64).tolist() == np.clip(codes, -127, 127).tolist()
+    q, sa = O.quantize_act_int8(O.f32_to_bf16_bits(np.full((1, 8), 3.0, np.float32)), static=1e-20)
+    assert sa[0, 0] == np.float32(1e-20) and (q == 127).all()   # no 1e-12 floor on a static scale
+
+
+def test_int8_pertensor_exact_rational():
+    """Per-tensor codes against exact rational arithmetic, with the tensor's scale from its largest |x|."""
+    g = np.random.default_rng(19)
+    xf = (g.standard_normal((5, 64)) * np.array([0.01, 1, 30, 0.5, 2])[:, None]).astype(np.float32)
+    x = O.f32_to_bf16_bits(xf)
+    q, sa = O.quantize_act_int8(x, pertensor=True)
+    xv = O.bf16_bits_to_f32(x)
+    s = _rn_f32(Fraction(float(np.abs(xv).max())) / 127)
+    assert Fraction(float(sa[0, 0])) == s
+    for r in range(5):
+        for j in range(64):
+            assert q[r, j] == max(-127, min(127, _rne_int(_rn_f32(Fraction(float(xv[r, j])) / s))))
+    # the per-tensor scale is the largest per-token scale, and the row holding the maximum quantizes alike
+    qr, sr = O.quantize_act_int8(x)
+    assert sa[0, 0] == sr.max()
+    top = int(np.argmax(sr[:, 0]))
+    assert np.array_equal(q[top], qr[top])
+
+
+def test_w8a8_linear_modes_agree_on_shared_scales():
+    """With one row the per-tensor and per-token modes coincide, and a static scale equal to the dynamic
+    one reproduces the dynamic output; the pertensor linear equals int GEMM x scalar x per-channel scale."""
+    g = np.random.default_rng(23)
+    x = O.f32_to_bf16_bits(g.standard_normal((1, 128)).astype(np.float32))
+    qw, sw = O.quantize_weight_int8((g.standard_normal((32, 128)) * 0.05).astype(np.float32))
+    y_tok = O.w8a8_linear(x, qw, sw, None)
+    assert np.array_equal(O.w8a8_linear(x, qw, sw, None, pertensor=True), y_tok)
+    _, sa = O.quantize_act_int8(x)
+    assert np.array_equal(O.w8a8_linear(x, qw, sw, None, static=float(sa[0, 0])), y_tok)
+    xm = O.f32_to_bf16_bits(g.standard_normal((6, 128)).astype(np.float32))
+    qa, s = O.quantize_act_int8(xm, pertensor=True)
+    want = (qa.astype(np.int64) @ qw.astype(np.int64).T) * float(s[0, 0]) * sw.astype(np.float64).reshape(1, -1)
+    assert np.array_equal(O.w8a8_linear(xm, qw, sw, None, pertensor=True), want)
+
+
 def test_w4a4_linear_reference_consistency():
     """The oracle's linear equals an independent float64 assembly of its documented formula."""
     g = np.random.default_rng(4)
