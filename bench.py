@@ -24,8 +24,12 @@ measured with rocprofv3 FETCH_SIZE / WRITE_SIZE, scaled by the same
 counters' reading for a copy of known size (profiles/w4a4_gemm_c1_traffic.json,
 written by ``--summarize-traffic``).
 ``cpu_baseline`` times the reference's CPU serving lane (dense fold + one
-bf16 Linear) on a bounded sample of the same workload. Prints ONE JSON line
-on stdout; progress goes to stderr.
+bf16 Linear) on a bounded sample of the same workload. The metric's second
+half, the config-4 DiT step (every linear W4A4 in the process's qualified
+lane, against the same model with bf16 GEMMs, each forward one HIP graph
+replayed ``--dit-steps`` times), goes into the same line as ``dit_step_ms``
+and ``dit_bf16_step_ms``. Prints ONE JSON line on stdout; progress goes to
+stderr.
 
 ``--only`` runs one piece eagerly ``--iters`` times (after 3 warmups) and
 prints nothing on stdout: it is the command the committed rocprofv3
@@ -46,6 +50,7 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "W4A4 linear TOPS (% int8 MFMA peak) at M=4608 K=N=3072; DiT step ms"
 INT8_PEAK_TOPS = 5000.0      # MI355X dense int8 MFMA, 5.0 POP/s
+TILE_NAMES = {0: "256x256", 1: "256x128", 2: "128x128", 3: "192x256", 4: "288x192", 5: "256x192"}
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, 8 TB/s
 COPY_BYTES = 64 << 20        # calibration copy for the traffic counters
 
@@ -128,7 +133,7 @@ def summarize_traffic(d: Path) -> int:
     out = {"workload": "svdq_w4a4_linear_c1 (M=4608, N=K=3072, rank 32, bf16 out)",
            "calibration": {"copy_bytes": COPY_BYTES, "copy_fetch_size_kib": cf, "copy_write_size_kib": cw,
                            "fetch_factor": round(ff, 4), "write_factor": round(wf, 4)}}
-    for key, sub, alg in (("gemm", "w4a4_gemm_fp6_kernel", gemm_alg),
+    for key, sub, alg in (("gemm", "w4a4_gemm_fp6", gemm_alg),
                           ("act_quant", "svdq_quant_fp6_kernel", act_quant_bytes(m, k, r, fp6=True))):
         w = "gemm" if key == "gemm" else "quant"
         name, f_kib = _counter_median_kib(d / f"f_{w}", sub)
@@ -143,36 +148,49 @@ def summarize_traffic(d: Path) -> int:
     return 0
 
 
-def bench_dit(args) -> int:
+def dit_step_pair(steps: int, warmup: int, modulation: str = "w4a4") -> dict:
     """Config 4: one Flux-dev-shaped denoiser forward (batch 1, 4096 image + 512 text tokens, 19 + 38
-    blocks), every block linear W4A4 rank 32 (the one-token adaLN modulation linears AWQ W4A16, as an svdq
-    checkpoint stores them) vs the same model with bf16 nn.Linear GEMMs; bf16 SDPA in both. Each model's
-    forward is captured once in a HIP graph and replayed ``--steps`` times."""
+    blocks), every linear W4A4 rank 32 in the process's qualified lane (``modulation="awq"``: the one-token
+    adaLN modulation linears AWQ W4A16, as an svdq checkpoint stores them) vs the same model with bf16
+    nn.Linear GEMMs; bf16 SDPA in both. Each model's forward is captured once in a HIP graph and replayed
+    ``steps`` times."""
     import gc
 
     import torch
 
-    import gen_worker_amd  # noqa: F401
-    from gen_worker_amd import _native
-    from gen_worker_amd.flux_dit import FluxDiT, FluxDiTConfig, block_int_ops, inputs, time_step_ms
+    from gen_worker_amd.flux_dit import FluxDiT, FluxDiTConfig, inputs, time_step_ms
 
-    _native.load()
-    torch.cuda.set_device(0)
     cfg = FluxDiTConfig()
     args_in = inputs(cfg)
-    res = {}
+    res = {"cfg": cfg}
     for kind in ("w4a4", "bf16"):
         log(f"bench: building the {kind} DiT")
-        model = FluxDiT(kind, cfg)
+        model = FluxDiT(kind, cfg, modulation=modulation)
+        res[kind + "_lane"] = model.lane
         torch.cuda.synchronize()
-        log(f"bench: timing the {kind} DiT step ({args.steps} graph replays)")
-        res[kind] = time_step_ms(model, args_in, steps=args.steps, warmup=args.warmup)
+        log(f"bench: timing the {kind} DiT step ({steps} graph replays, {model.lane} lane)")
+        res[kind] = time_step_ms(model, args_in, steps=steps, warmup=warmup)
         with torch.no_grad():
             y = model(*args_in)
         res[kind + "_finite"] = bool(torch.isfinite(y).all())
         del model, y
         gc.collect()
         torch.cuda.empty_cache()
+    return res
+
+
+def bench_dit(args) -> int:
+    """Config 4 as its own bench line (see ``dit_step_pair``), with ``--modulation``."""
+    import torch
+
+    import gen_worker_amd  # noqa: F401
+    from gen_worker_amd import _native
+    from gen_worker_amd.flux_dit import block_int_ops
+
+    _native.load()
+    torch.cuda.set_device(0)
+    res = dit_step_pair(args.steps, args.warmup, args.modulation)
+    cfg = res["cfg"]
     ops_ = block_int_ops(cfg)
     out = {"metric": "DiT step ms (Flux-dev-shaped, batch 1, 4096+512 tokens, 19+38 blocks)",
            "value": round(res["w4a4"], 3), "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -180,8 +198,9 @@ def bench_dit(args) -> int:
            "config": {"workload": "flux_dit_c4", "hidden": cfg.hidden, "heads": cfg.heads, "mlp": cfg.mlp,
                       "dual_blocks": cfg.n_dual, "single_blocks": cfg.n_single, "img_tokens": cfg.img_tokens,
                       "txt_tokens": cfg.txt_tokens, "rank": cfg.rank, "attention": "bf16 SDPA",
-                      "modulation": "AWQ W4A16 g64 (one token)",
-                      "timing": "forward captured in one HIP graph, replayed"},
+                      "modulation": ("W4A4 (one token)" if args.modulation == "w4a4"
+                                     else "AWQ W4A16 g64 (one token)"),
+                      "lane": res["w4a4_lane"], "timing": "forward captured in one HIP graph, replayed"},
            "bf16_gemm_ms": round(res["bf16"], 3), "speedup_vs_bf16": round(res["bf16"] / res["w4a4"], 4),
            "block_linear_int_ops": ops_, "outputs_finite": {"w4a4": res["w4a4_finite"], "bf16": res["bf16_finite"]}}
     print(json.dumps(out), flush=True)
@@ -438,6 +457,11 @@ def main() -> int:
                          "W8A8, bf16); dit: the config-4 Flux-shaped DiT step, W4A4 vs the same model with bf16 "
                          "GEMMs; mod: the DiT's one-token modulation linears (AWQ W4A16 GEMV vs W4A4 vs bf16); "
                          "nvfp4: the nvfp4 compatibility lane at the config-1 shape")
+    ap.add_argument("--modulation", choices=("w4a4", "awq"), default="w4a4",
+                    help="the DiT's one-token adaLN modulation linears: W4A4 like every other linear (config 4 "
+                         "as stated), or AWQ W4A16 as an svdq checkpoint stores them")
+    ap.add_argument("--dit-steps", type=int, default=3,
+                    help="graph replays of each DiT forward in the default (c1) line; 0 skips the DiT half")
     ap.add_argument("--summarize-traffic", metavar="DIR", default=None,
                     help="write profiles/w4a4_gemm_c1_traffic.json from the FETCH_SIZE / WRITE_SIZE runs in DIR "
                          "(subdirectories f_<w>, w_<w> for w in gemm, quant, copy)")
@@ -522,6 +546,8 @@ def main() -> int:
     quant_ms = graph_time_ms(torch, quant, args.steps, warm_calls=args.warmup)
 
     int_ops = w4a4_int_ops(m, n, k)
+    tile = _native.load().gwa_svdq_gemm_w4a4_fp6_tile(m, n)
+    gemm_kernel = "w4a4_gemm_fp6_pipe_kernel" if tile in (4, 5) else "w4a4_gemm_fp6_kernel"
     value_tops = int_ops / (step_ms * 1e-3) / 1e12
     gemm_tops = int_ops / (gemm_ms * 1e-3) / 1e12
     qbytes = act_quant_bytes(m, k, r, fp6=True)
@@ -572,10 +598,10 @@ def main() -> int:
         "config": {"workload": "svdq_w4a4_linear_c1", "M": m, "N": n, "K": k, "rank": r, "group": 64,
                    "in_dtype": "bf16", "out_dtype": "bf16", "parallelism": "none",
                    "timing": "K steps in one HIP graph replay, after >= 40 ms of untimed replays"},
-        "roofline": {"bound": "mfma", "achieved": round(gemm_tops, 2), "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
+        "roofline": {"bound": "mfma", "achieved": round(gemm_tops, 2), "peak": INT8_PEAK_TOPS, "unit": "TOPS",
                      "frac": round(gemm_tops / INT8_PEAK_TOPS, 4), "traffic": traffic,
-                     "kernel": "w4a4_gemm_fp6_kernel", "algorithmic_ops_per_launch": int_ops,
-                     "avg_launch_us": round(gemm_ms * 1e3, 2)},
+                     "kernel": gemm_kernel, "tile": TILE_NAMES.get(tile, str(tile)),
+                     "algorithmic_ops_per_launch": int_ops, "avg_launch_us": round(gemm_ms * 1e3, 2)},
         "pct_int8_peak": round(100 * value_tops / INT8_PEAK_TOPS, 2),
         "eager_ms_per_step": round(eager_ms, 5),
         "act_quant": {"kernel": "svdq_quant_fp6_kernel + la_reduce_kernel", "avg_launch_us": round(quant_ms * 1e3, 2),
@@ -583,6 +609,14 @@ def main() -> int:
                       "frac_hbm_peak": round(quant_gbs / HBM_PEAK_GBS, 4)},
         "cpu_baseline": cpu,
     }
+    if args.dit_steps > 0:
+        # the metric's second half: the config-4 DiT step, W4A4 (qualified lane) against bf16 GEMMs
+        torch.cuda.empty_cache()
+        res = dit_step_pair(args.dit_steps, 1, args.modulation)
+        out.update({"dit_step_ms": round(res["w4a4"], 3), "dit_bf16_step_ms": round(res["bf16"], 3),
+                    "dit_speedup_vs_bf16": round(res["bf16"] / res["w4a4"], 4), "dit_lane": res["w4a4_lane"],
+                    "dit_modulation": args.modulation,
+                    "dit_outputs_finite": res["w4a4_finite"] and res["bf16_finite"]})
     print(json.dumps(out), flush=True)
     return 0
 

@@ -10,14 +10,17 @@ side and project their concatenation). The timestep / guidance / pooled-text
 conditioning enters as a seeded random embedding ``temb`` [1, 3072].
 
 Every linear is built by a factory, so the same model runs as:
-  * ``"w4a4"``: every block linear an SVDQuant W4A4 layer (``SvdqW4A4Linear``,
+  * ``"w4a4"``: every linear an SVDQuant W4A4 layer (``SvdqW4A4Linear``,
     rank 32, group 64; int4 codes, fp16 scales, low-rank factors and bias
     random), GELU fused into the fc1 epilogues, and each MLP's second linear
     quantized in the first one's epilogue (``svdq_pair_forward``; in the
     single blocks ``svdq_concat_forward`` builds proj_out's input [attention,
-    MLP] without the concatenation); the blocks' adaLN modulation linears
-    (one token) AWQ W4A16 (``AwqPackedLinear``), the format an svdq
-    checkpoint keeps them in;
+    MLP] without the concatenation). The blocks' adaLN modulation linears
+    (one token) are W4A4 too, or with ``modulation="awq"`` AWQ W4A16
+    (``AwqPackedLinear``), the format an svdq checkpoint keeps them in. The
+    int4 layers follow the process's qualified lane (``qualify.resolve_lane``,
+    or ``lane=`` to pin it): in the dense lane each is served as its folded
+    bf16 Linear, as the reference's swap does;
   * ``"bf16"``: every linear a bf16 ``nn.Linear`` (the bf16 GEMM path).
 Attention is bf16 ``scaled_dot_product_attention`` in both. Weights are
 random-init on the device from seeded generators; values are chosen only to
@@ -109,19 +112,31 @@ class _Bf16Linear(nn.Module):
         return F.gelu(y, approximate="tanh") if self.gelu else y
 
 
-def linear_factory(kind: str, device, rank: int) -> Callable[..., nn.Module]:
-    """``make(in_f, out_f, seed, gelu=False)`` for ``kind`` in ("w4a4", "bf16")."""
+def linear_factory(kind: str, device, rank: int, lane: str = "int4") -> Callable[..., nn.Module]:
+    """``make(in_f, out_f, seed, gelu=False)`` for ``kind`` in ("w4a4", "bf16"); a "w4a4" layer in the dense
+    lane is served as its fold."""
     if kind == "w4a4":
-        return lambda i, o, s, gelu=False: _w4a4_linear(i, o, s, device, rank, gelu)
+        from .qualify import serving_linear
+
+        return lambda i, o, s, gelu=False: serving_linear(_w4a4_linear(i, o, s, device, rank, gelu), lane)
     if kind == "bf16":
         return lambda i, o, s, gelu=False: _Bf16Linear(i, o, s, device, gelu)
     raise ValueError(f"linear kind {kind!r} not in ('w4a4', 'bf16')")
 
 
-def modulation_factory(kind: str, device) -> Callable[..., nn.Module]:
-    """``make(in_f, out_f, seed)`` for the adaLN modulation linears: an svdq checkpoint keeps them as AWQ
-    W4A16 (``models/svdq_awq.py:1``), so the "w4a4" model runs them through the AWQ GEMV; "bf16" keeps
-    bf16 linears."""
+MODULATIONS = ("w4a4", "awq")
+
+
+def modulation_factory(kind: str, device, rank: int = 32, lane: str = "int4",
+                       modulation: str = "w4a4") -> Callable[..., nn.Module]:
+    """``make(in_f, out_f, seed)`` for the adaLN modulation linears (one token): in the "w4a4" model W4A4
+    layers like every other linear, or with ``modulation="awq"`` AWQ W4A16 through the AWQ GEMV (an svdq
+    checkpoint keeps them in that format, ``models/svdq_awq.py:1``); "bf16" keeps bf16 linears."""
+    if modulation not in MODULATIONS:
+        raise ValueError(f"modulation {modulation!r} not in {MODULATIONS}")
+    if kind == "w4a4" and modulation == "w4a4":
+        make = linear_factory(kind, device, rank, lane)
+        return lambda i, o, s: make(i, o, s)
     if kind == "w4a4":
         return lambda i, o, s: _awq_linear(i, o, s, device)
     if kind == "bf16":
@@ -230,15 +245,22 @@ class SingleBlock(nn.Module):
 class FluxDiT(nn.Module):
     """The config-4 denoiser; ``forward(latents [4096, 64], text [512, 4096], temb [1, 3072]) -> [4096, 64]``."""
 
-    def __init__(self, kind: str, cfg: FluxDiTConfig = FluxDiTConfig(), device="cuda", seed: int = 1000) -> None:
+    def __init__(self, kind: str, cfg: FluxDiTConfig = FluxDiTConfig(), device="cuda", seed: int = 1000,
+                 lane: Optional[str] = None, modulation: str = "w4a4") -> None:
         super().__init__()
-        make = linear_factory(kind, device, cfg.rank)
-        make_mod = modulation_factory(kind, device)
-        self.cfg, self.kind = cfg, kind
+        if kind == "w4a4":
+            from .qualify import resolve_lane
+
+            self.lane = resolve_lane(lane)
+        else:
+            self.lane = "bf16"
+        make = linear_factory(kind, device, cfg.rank, self.lane)
+        make_mod = modulation_factory(kind, device, cfg.rank, self.lane, modulation)
+        self.cfg, self.kind, self.modulation = cfg, kind, modulation
         c = cfg.hidden
         self.x_embedder = make(cfg.in_channels, c, seed)
         self.context_embedder = make(cfg.txt_dim, c, seed + 1)
-        fused = kind == "w4a4"
+        fused = self.lane == "int4"
         self.dual = nn.ModuleList(DualBlock(cfg, make, seed + 100 + 10 * i, device, fused, make_mod)
                                   for i in range(cfg.n_dual))
         self.single = nn.ModuleList(SingleBlock(cfg, make, seed + 400 + 10 * i, device, fused, make_mod)

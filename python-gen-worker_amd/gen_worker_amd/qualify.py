@@ -221,14 +221,28 @@ def gemm_numerics_ok() -> Optional[str]:
 
 
 def _median_ms(fn: Any) -> float:
+    """Median ms of ``BENCH_ITERS`` timed calls after ``BENCH_WARMUP`` untimed ones (``models/w4a4.py:216-232``).
+    Each call is ``fn`` captured alone in a HIP graph and replayed, so the events bracket the GPU work of the
+    op only: the int4 op's host side (Python custom op + ctypes, ~20-30 us) and torch's C++ matmul dispatch
+    would otherwise enter the two sides unequally."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()                      # allocations of the op's outputs happen outside the capture
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            fn()
+    torch.cuda.synchronize()
     for _ in range(BENCH_WARMUP):
-        fn()
+        graph.replay()
     torch.cuda.synchronize()
     times = []
     for _ in range(BENCH_ITERS):
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
-        fn()
+        graph.replay()
         e1.record()
         torch.cuda.synchronize()
         times.append(e0.elapsed_time(e1))
@@ -238,7 +252,8 @@ def _median_ms(fn: Any) -> float:
 
 def gemm_speedup() -> tuple[float, float, float]:
     """``_gemm_profitable`` (``models/w4a4.py:235-259``): (int4 GEMM ms, bf16 matmul ms, speedup) at
-    M = N = K = 4096; the int4 side is the fp6-lane GEMM with its epilogue on ready activation records."""
+    M = N = K = 4096; the int4 side is the fp6-lane GEMM with its epilogue on ready activation records, as the
+    reference times its fp4 GEMM on ready operands."""
     ops = torch.ops.cozy_gen_worker
     d = BENCH_DIM
     g = torch.Generator(device="cuda").manual_seed(3)
@@ -298,16 +313,28 @@ def w4a4_lane() -> str:
     return qualification().lane
 
 
-def serving_linear(mod: Any) -> Any:
-    """The module to serve for an int4 layer: the layer itself in the int4 lane, its dense fold (one bf16
-    ``nn.Linear`` on the layer's device, GELU kept) in the dense lane; raises when neither can run."""
+LANES = ("int4", "dense")
+
+
+def resolve_lane(lane: Optional[str] = None) -> str:
+    """``lane`` when given ("int4" or "dense"), else the process's qualified lane; an unavailable int4 lane
+    resolves to "dense" (the reference degrades to its dequant lane and never refuses,
+    ``models/w4a4.py:281-283``, ``models/svdq_native.py:283-286``)."""
+    if lane is None:
+        lane = w4a4_lane()
+        return "int4" if lane == "int4" else "dense"
+    if lane not in LANES:
+        raise ValueError(f"lane {lane!r} is not one of {LANES}")
+    return lane
+
+
+def serving_linear(mod: Any, lane: Optional[str] = None) -> Any:
+    """The module to serve for an int4 layer: the layer itself in the int4 lane; in the dense lane its fold
+    (one bf16 ``nn.Linear`` on the layer's device, GELU kept)."""
     from .svdq import fold_to_dense
 
-    lane = w4a4_lane()
-    if lane == "int4":
+    if resolve_lane(lane) == "int4":
         return mod
-    if lane == "unavailable":
-        raise RuntimeError("gen_worker_amd: the int4 lane is unavailable (no GPU / HIP library)")
     dense = fold_to_dense(mod).to(mod.weight.device)
     if mod.activation == "gelu_tanh":
         return torch.nn.Sequential(dense, torch.nn.GELU(approximate="tanh"))
@@ -317,6 +344,6 @@ def serving_linear(mod: Any) -> Any:
 __all__ = [
     "EPILOGUE_REL_TOL", "GEMM_REL_TOL", "IDENTITY_PROBES", "Qualification", "SELF_CHECK_PROBES",
     "decode_fp6_records_torch", "extension_available", "fused_self_check", "gemm_numerics_ok", "gemm_speedup",
-    "pack_int4_torch", "qualification", "qualify", "quantize_act_torch", "quantizer_bit_identical",
-    "serving_linear", "w4a4_lane",
+    "LANES", "pack_int4_torch", "qualification", "qualify", "quantize_act_torch", "quantizer_bit_identical",
+    "resolve_lane", "serving_linear", "w4a4_lane",
 ]

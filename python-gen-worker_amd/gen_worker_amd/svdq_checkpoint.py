@@ -25,8 +25,9 @@ with int4 arithmetic:
 splits nunchaku's fused projections (``to_qkv`` -> ``to_q``/``to_k``/``to_v``,
 ``svdq_layout.py:441-470``) in that domain, and ``swap_svdq_linears`` /
 ``plan_targets`` (``models/svdq_native.py:239-321``) replace a model's
-``nn.Linear`` modules with ``SvdqW4A4Linear`` (or a folded dense Linear where
-the kernel contract does not hold). AWQ W4A16 modulation layers go through
+``nn.Linear`` modules with ``SvdqW4A4Linear`` in the qualified int4 lane (or a
+folded dense Linear in the dense lane and where the kernel contract does not
+hold). AWQ W4A16 modulation layers go through
 ``swap_awq_linears`` with the exporter's adaLN split count
 (``models/svdq_native.py:324-338``). ``load_svdq_int4_checkpoint`` reads a
 safetensors file into a caller-built module skeleton (the reference builds
@@ -295,12 +296,14 @@ def fold_decoded(dec: DecodedInt4Linear, *, compute_dtype=torch.bfloat16, device
     return lin
 
 
-def build_module(dec: DecodedInt4Linear, *, device: Any = "cuda") -> nn.Module:
-    """The device module for one decoded linear: ``SvdqW4A4Linear`` when the kernel contract holds,
-    else the folded dense Linear."""
+def build_module(dec: DecodedInt4Linear, *, device: Any = "cuda", lane: Optional[str] = None) -> nn.Module:
+    """The device module for one decoded linear: ``SvdqW4A4Linear`` in the int4 lane when the kernel contract
+    holds, else the folded dense Linear. ``lane`` None takes the process's qualified lane
+    (``qualify.resolve_lane``; the reference decides its mode once, ``models/svdq_native.py:283-286``)."""
+    from .qualify import resolve_lane
     from .svdq import build_svdq_w4a4_linear, fused_shape_supported
 
-    if not fused_shape_supported(dec.out_features, dec.in_features, dec.rank):
+    if resolve_lane(lane) != "int4" or not fused_shape_supported(dec.out_features, dec.in_features, dec.rank):
         return fold_decoded(dec, device=device)
     packed = (dec.codes[:, 0::2] & 0xF) | ((dec.codes[:, 1::2] & 0xF) << 4)
     return build_svdq_w4a4_linear(qweight=packed, wscales=dec.scales, smooth=dec.smooth_factor,
@@ -310,75 +313,98 @@ def build_module(dec: DecodedInt4Linear, *, device: Any = "cuda") -> nn.Module:
 
 
 # ---------------------------------------------------------------------------
-# swapping into a model
+# swapping into a model: every replacement is resolved and checked against the model first, then applied,
+# so a checkpoint that does not fit leaves the model untouched
 # ---------------------------------------------------------------------------
 
-def _module_at(model: nn.Module, path: str) -> Optional[nn.Module]:
-    try:
-        return model.get_submodule(path)
-    except AttributeError:
-        return None
+@dataclass(frozen=True)
+class SwapTarget:
+    """One ``nn.Linear`` of the model that a checkpoint linear, or one part of a fused one, replaces."""
+
+    path: str
+    in_features: int
+    out_features: int
 
 
-def _set_module(model: nn.Module, path: str, new: nn.Module) -> None:
-    parent, _, leaf = path.rpartition(".")
-    setattr(model.get_submodule(parent) if parent else model, leaf, new)
+def _linear_index(model: nn.Module) -> Dict[str, nn.Linear]:
+    return {name: mod for name, mod in model.named_modules() if isinstance(mod, nn.Linear)}
+
+
+def _replace(model: nn.Module, path: str, new: nn.Module) -> None:
+    head, _, leaf = path.rpartition(".")
+    setattr(model.get_submodule(head) if head else model, leaf, new)
+
+
+def _resolve_targets(index: Dict[str, nn.Linear], prefix: str, model_name: str) -> tuple[SwapTarget, ...]:
+    """The Linear named ``prefix``, or the Linears a fused projection name stands for (``to_qkv`` ->
+    ``to_q``, ``to_k``, ``to_v`` beside it)."""
+    lin = index.get(prefix)
+    if lin is not None:
+        return (SwapTarget(prefix, int(lin.in_features), int(lin.out_features)),)
+    head, _, leaf = prefix.rpartition(".")
+    parts = _FUSED_SPLITS.get(leaf)
+    if parts is None:
+        raise SvdqLayoutError(f"{prefix!r}: {model_name} has no nn.Linear of this name and {leaf!r} is not a fused "
+                              f"projection this loader splits (it splits: {', '.join(sorted(_FUSED_SPLITS))})")
+    paths = [f"{head}.{p}" if head else p for p in parts]
+    missing = [p for p in paths if p not in index]
+    if missing:
+        raise SvdqLayoutError(f"{prefix!r} splits into {', '.join(paths)}, but {model_name} has no nn.Linear at "
+                              f"{', '.join(missing)}")
+    return tuple(SwapTarget(p, int(index[p].in_features), int(index[p].out_features)) for p in paths)
 
 
 def plan_targets(model: nn.Module, prefix: str) -> tuple[tuple[str, int], ...]:
-    """Where one checkpoint linear lands in ``model`` (``models/svdq_native.py:239-267``): the Linear at
-    ``prefix``, or the separate projections a fused one (``to_qkv`` ...) splits into."""
-    direct = _module_at(model, prefix)
-    if isinstance(direct, nn.Linear):
-        return ((prefix, int(direct.out_features)),)
-    parent, _, leaf = prefix.rpartition(".")
-    parts = _FUSED_SPLITS.get(leaf)
-    if parts is None:
-        raise SvdqLayoutError(f"checkpoint names {prefix!r}, which is neither a Linear in {type(model).__name__} "
-                              f"nor a known fused projection ({', '.join(sorted(_FUSED_SPLITS))})")
-    out = []
-    for part in parts:
-        path = f"{parent}.{part}" if parent else part
-        mod = _module_at(model, path)
-        if not isinstance(mod, nn.Linear):
-            raise SvdqLayoutError(f"fused prefix {prefix!r} needs {path!r} to be a Linear in {type(model).__name__}")
-        out.append((path, int(mod.out_features)))
-    return tuple(out)
+    """(path, out_features) of each Linear one checkpoint linear replaces (the reference's ``plan_targets``,
+    ``models/svdq_native.py:239-267``, answers the same question)."""
+    return tuple((t.path, t.out_features) for t in _resolve_targets(_linear_index(model), prefix,
+                                                                     type(model).__name__))
 
 
-def swap_svdq_linears(model: nn.Module, decoded: Dict[str, DecodedInt4Linear], *, device: Any = "cuda") -> dict:
-    """Replace ``model``'s Linears with the checkpoint's int4 linears (``swap_svdq_linears``,
-    ``models/svdq_native.py:270-321``); fused projections are split first."""
-    counts = {"prefixes": 0, "linears": 0, "int4": 0, "dense": 0}
+def swap_svdq_linears(model: nn.Module, decoded: Dict[str, DecodedInt4Linear], *, device: Any = "cuda",
+                      lane: Optional[str] = None) -> dict:
+    """Install the checkpoint's int4 linears in ``model`` (the role of the reference's ``swap_svdq_linears``,
+    ``models/svdq_native.py:270-321``): fused projections are split in the decoded domain, every piece must
+    match the shape of the Linear it replaces, and each becomes ``SvdqW4A4Linear`` in the int4 lane (the
+    process's qualified lane unless ``lane`` says otherwise) or a folded dense Linear. Returns counts and the
+    lane used."""
+    from .qualify import resolve_lane
+
+    index = _linear_index(model)
+    name = type(model).__name__
+    plan: list[tuple[SwapTarget, DecodedInt4Linear]] = []
     for prefix in sorted(decoded):
         dec = decoded[prefix]
-        targets = plan_targets(model, prefix)
-        counts["prefixes"] += 1
-        parts = (dec,) if len(targets) == 1 else split_decoded(dec, tuple(o for _, o in targets))
-        for (path, out_f), part in zip(targets, parts):
-            if part.out_features != out_f:
-                raise SvdqLayoutError(f"{prefix!r} -> {path!r}: decoded out_features {part.out_features} != "
-                                      f"module {out_f}")
-            old = _module_at(model, path)
-            if int(old.in_features) != part.in_features:
-                raise SvdqLayoutError(f"{prefix!r} -> {path!r}: decoded in_features {part.in_features} != module "
-                                      f"{int(old.in_features)}")
-            new = build_module(part, device=device)
-            counts["int4" if not isinstance(new, nn.Linear) else "dense"] += 1
-            counts["linears"] += 1
-            _set_module(model, path, new)
-    logger.info("svdq int4 swap: %s", counts)
+        targets = _resolve_targets(index, prefix, name)
+        pieces = (dec,) if len(targets) == 1 else split_decoded(dec, tuple(t.out_features for t in targets))
+        for t, piece in zip(targets, pieces):
+            if (piece.out_features, piece.in_features) != (t.out_features, t.in_features):
+                raise SvdqLayoutError(f"{prefix!r} -> {t.path!r}: the checkpoint holds [{piece.out_features}, "
+                                      f"{piece.in_features}], the model's nn.Linear is [{t.out_features}, "
+                                      f"{t.in_features}]")
+            plan.append((t, piece))
+    chosen = resolve_lane(lane)
+    counts: dict = {"prefixes": len(decoded), "linears": len(plan), "int4": 0, "dense": 0, "lane": chosen}
+    for t, piece in plan:
+        new = build_module(piece, device=device, lane=chosen)
+        counts["dense" if isinstance(new, nn.Linear) else "int4"] += 1
+        _replace(model, t.path, new)
+    logger.info("svdq int4 swap (%s lane): %d checkpoint linears -> %d modules (%d int4, %d dense)", chosen,
+                counts["prefixes"], counts["linears"], counts["int4"], counts["dense"])
     return counts
 
 
 def adanorm_splits_for(model_class: str, prefix: str) -> int:
-    """adaLN split count of one AWQ modulation layer (``models/svdq_native.py:324-338``), or a typed refusal:
-    a wrong count corrupts the output silently, so it is never inferred."""
-    for (cls, suffix), n in _ADANORM_SPLITS.items():
-        if cls == model_class and prefix.endswith(suffix):
+    """adaLN split count of one AWQ modulation layer from the verified table, matched on the longest tail of
+    ``prefix`` (whole path components); anything else is refused, since a wrong count scrambles the
+    modulation without any error (the reference keeps the same rule, ``models/svdq_native.py:324-338``)."""
+    parts = prefix.split(".")
+    for width in range(len(parts), 0, -1):
+        n = _ADANORM_SPLITS.get((model_class, ".".join(parts[-width:])))
+        if n is not None:
             return n
-    raise SvdqLayoutError(f"unknown adaLN split count for AWQ layer {prefix!r} in {model_class}; pass it "
-                          f"explicitly (adanorm_splits=) after verifying it")
+    raise SvdqLayoutError(f"{prefix!r} in {model_class or 'an unnamed model class'}: no verified adaLN split "
+                          f"count; give it as adanorm_splits={{{prefix!r}: n}}")
 
 
 def swap_awq_linears(model: nn.Module, layers: Dict[str, dict], *, model_class: str = "",
@@ -386,19 +412,19 @@ def swap_awq_linears(model: nn.Module, layers: Dict[str, dict], *, model_class: 
     """Replace the AWQ W4A16 modulation Linears with packed modules (``models/svdq_native.py:414-436``)."""
     from .awq import build_awq_packed_linear
 
-    n = 0
+    index = _linear_index(model)
+    plan = []
     for prefix in sorted(layers):
-        target = _module_at(model, prefix)
-        if not isinstance(target, nn.Linear):
-            raise SvdqLayoutError(f"AWQ layer {prefix!r} has no Linear in {type(model).__name__}")
+        target = index.get(prefix)
+        if target is None:
+            raise SvdqLayoutError(f"AWQ layer {prefix!r}: {type(model).__name__} has no nn.Linear of this name")
         splits = (adanorm_splits or {}).get(prefix)
-        if splits is None:
-            splits = adanorm_splits_for(model_class, prefix)
-        mod = build_awq_packed_linear(layers[prefix], int(target.out_features), int(target.in_features),
-                                      adanorm_splits=splits, device=device)
-        _set_module(model, prefix, mod)
-        n += 1
-    return n
+        plan.append((prefix, target, adanorm_splits_for(model_class, prefix) if splits is None else splits))
+    for prefix, target, splits in plan:
+        _replace(model, prefix, build_awq_packed_linear(layers[prefix], int(target.out_features),
+                                                        int(target.in_features), adanorm_splits=splits,
+                                                        device=device))
+    return len(plan)
 
 
 def _group_by_prefix(names) -> dict[str, list[str]]:
@@ -410,7 +436,8 @@ def _group_by_prefix(names) -> dict[str, list[str]]:
 
 
 def load_svdq_int4_checkpoint(path, model: nn.Module, *, model_class: str = "",
-                              adanorm_splits: Optional[Dict[str, int]] = None, device: Any = "cuda") -> dict:
+                              adanorm_splits: Optional[Dict[str, int]] = None, device: Any = "cuda",
+                              lane: Optional[str] = None) -> dict:
     """Read an int4 svdq safetensors file into ``model`` (a skeleton whose module names match the
     checkpoint's): int4 linears swapped for ``SvdqW4A4Linear`` (fused projections split), AWQ modulation
     linears for ``AwqPackedLinear``, every other tensor copied into the parameter / buffer of that name."""
@@ -428,16 +455,15 @@ def load_svdq_int4_checkpoint(path, model: nn.Module, *, model_class: str = "",
             if is_awq_linear(tensors):
                 awq_layers[prefix] = tensors
             elif "qweight" in tensors:
-                target = plan_targets(model, prefix)
-                n = sum(o for _, o in target)
-                k = int(_module_at(model, target[0][0]).in_features)
-                decoded[prefix] = decode_int4_linear(tensors, n, k)
+                targets = _resolve_targets(_linear_index(model), prefix, type(model).__name__)
+                decoded[prefix] = decode_int4_linear(tensors, sum(t.out_features for t in targets),
+                                                     targets[0].in_features)
             else:
                 for leaf, t in tensors.items():
                     plain[f"{prefix}.{leaf}" if prefix else leaf] = t
     counts["awq"] = swap_awq_linears(model, awq_layers, model_class=model_class, adanorm_splits=adanorm_splits,
                                      device=device)
-    counts.update(swap_svdq_linears(model, decoded, device=device))
+    counts.update(swap_svdq_linears(model, decoded, device=device, lane=lane))
     counts["int4_prefixes"] = len(decoded)
     state = dict(model.named_parameters())
     state.update(dict(model.named_buffers()))
@@ -463,7 +489,7 @@ def load_svdq_int4_checkpoint(path, model: nn.Module, *, model_class: str = "",
 
 
 __all__ = [
-    "DecodedInt4Linear", "SvdqLayoutError", "adanorm_splits_for", "build_module", "decode_int4_linear",
+    "DecodedInt4Linear", "SvdqLayoutError", "SwapTarget", "adanorm_splits_for", "build_module", "decode_int4_linear",
     "dequantize_decoded", "fold_decoded", "is_int4_svdq_linear", "load_svdq_int4_checkpoint", "pack_group_scales",
     "pack_lowrank", "pack_qweight", "pack_vector", "plan_targets", "split_decoded", "swap_awq_linears",
     "swap_svdq_linears", "unpack_group_scales", "unpack_lowrank", "unpack_qweight", "unpack_vector",

@@ -514,7 +514,8 @@ def test_flux_dit_small_matches_oracle_chain():
 
     cfg = FluxDiTConfig(hidden=512, heads=4, head_dim=128, mlp=2048, n_dual=1, n_single=1, img_tokens=192,
                         txt_tokens=64, in_channels=64, txt_dim=256, rank=32)
-    model = FluxDiT("w4a4", cfg, device=DEV)       # MLPs and proj_out inputs through the fused epilogues
+    # MLPs and proj_out inputs through the fused epilogues; the modulation linears as AWQ W4A16
+    model = FluxDiT("w4a4", cfg, device=DEV, lane="int4", modulation="awq")
     unfused = copy.deepcopy(model)                   # every linear through its own forward
     ref_model = copy.deepcopy(model)
     for m_ in (unfused, ref_model):
@@ -602,9 +603,35 @@ def test_flux_dit_small_matches_oracle_chain():
     assert cos_u > 0.999, cos_u   # the fused model differs from the unfused one only by la's fp32 sum order
 
 
+def test_flux_dit_lanes_agree():
+    """The all-W4A4 DiT (modulation linears W4A4 too) in the int4 lane and the same weights in the dense lane
+    (each layer its folded bf16 Linear): the modules are what the lane says, and the outputs differ by the
+    activation quantization the dense lane skips (int4 group-64 codes carry ~10% error per element, which
+    compounds over the ~18 chained linears of the two blocks: cosine ~0.97 measured)."""
+    from gen_worker_amd.flux_dit import FluxDiT, FluxDiTConfig, inputs
+    from gen_worker_amd.svdq import SvdqW4A4Linear
+
+    cfg = FluxDiTConfig(hidden=512, heads=4, head_dim=128, mlp=2048, n_dual=1, n_single=1, img_tokens=192,
+                        txt_tokens=64, in_channels=64, txt_dim=256, rank=32)
+    m4 = FluxDiT("w4a4", cfg, device=DEV, lane="int4")
+    md = FluxDiT("w4a4", cfg, device=DEV, lane="dense")
+    assert m4.lane == "int4" and md.lane == "dense"
+    n4 = sum(isinstance(m, SvdqW4A4Linear) for m in m4.modules())
+    assert n4 == 4 + 10 + 4   # embedders, norm_out, proj_out; dual block 8 + 2 modulation; single 3 + 1
+    assert not any(isinstance(m, SvdqW4A4Linear) for m in md.modules())
+    assert isinstance(m4.dual[0].mod_img, SvdqW4A4Linear)
+    args = inputs(cfg, device=DEV)
+    with torch.no_grad():
+        y4, yd = m4(*args).float(), md(*args).float()
+    assert torch.isfinite(y4).all() and torch.isfinite(yd).all()
+    cos = torch.nn.functional.cosine_similarity(y4.flatten(), yd.flatten(), dim=0).item()
+    print("dit lanes: cos", cos)
+    assert cos > 0.95, cos
+
+
 def test_qualification_gates():
-    """The arming protocol on the device: every numerics gate passes; the profitability gate measures the
-    int4 GEMM against the bf16 matmul at 4096^3 and the lane follows it (int4 at >= 1.10x, else dense)."""
+    """The arming protocol on the device: every numerics gate passes, and the profitability gate (the int4
+    GEMM against the bf16 matmul at 4096^3, >= 1.10x) arms the int4 lane on MI355X."""
     from gen_worker_amd import qualify
 
     assert qualify.extension_available()
@@ -614,7 +641,8 @@ def test_qualification_gates():
     q = qualify.qualify()
     print("qualification", q)
     assert q.speedup is not None and q.speedup > 0
-    assert q.lane == ("int4" if q.speedup >= qualify.BENCH_MIN_SPEEDUP else "dense")
+    assert q.speedup >= qualify.BENCH_MIN_SPEEDUP and q.lane == "int4", q
+    assert qualify.resolve_lane() == "int4"
     # the record decoder of the gates agrees with the test helper's
     x = torch.randn(77, 384, device=DEV).to(torch.bfloat16)
     q6, _ = torch.ops.cozy_gen_worker.svdq_quant_fp6(x, None, None, None)

@@ -61,7 +61,8 @@ def test_load_int4_checkpoint(tmp_path):
 
     model = nn.Module()
     model.blocks = nn.ModuleList([_Block()])
-    counts = C.load_svdq_int4_checkpoint(path, model, adanorm_splits={"blocks.0.norm1.linear": 6}, device=DEV)
+    counts = C.load_svdq_int4_checkpoint(path, model, adanorm_splits={"blocks.0.norm1.linear": 6}, device=DEV,
+                                         lane="int4")
     assert counts["int4_prefixes"] == 3 and counts["linears"] == 5 and counts["int4"] == 5
     assert counts["awq"] == 1 and counts["plain"] == 1
     blk = model.blocks[0]

@@ -208,3 +208,77 @@ def test_adanorm_split_table():
     assert C.adanorm_splits_for("QwenImageTransformer2DModel", "transformer_blocks.3.img_mod.1") == 6
     with pytest.raises(C.SvdqLayoutError):
         C.adanorm_splits_for("FluxTransformer2DModel", "transformer_blocks.0.norm1.linear")
+
+
+def _skeleton(d):
+    m = nn.Module()
+    m.blocks = nn.ModuleList([_Block(d)])
+    return m
+
+
+def _decoded_qkv_and_out(d):
+    _, qkv = synthetic_int4_layer(3 * d, d, 16, seed=21)
+    _, out = synthetic_int4_layer(d, d, 16, seed=22)
+    return {"blocks.0.attn.to_qkv": C.decode_int4_linear(qkv, 3 * d, d),
+            "blocks.0.attn.to_out.0": C.decode_int4_linear(out, d, d)}
+
+
+def test_swap_follows_the_dense_lane(monkeypatch):
+    """The swap asks the process's qualified lane once; in the dense lane every linear becomes the folded
+    bf16 Linear (the reference's dequant lane), with the fused projection split first."""
+    from gen_worker_amd import qualify
+
+    calls = []
+
+    def fake_qualification():
+        calls.append(1)
+        return qualify.Qualification("dense", ["stubbed: int4 GEMM not profitable"])
+
+    monkeypatch.setattr(qualify, "qualification", fake_qualification)
+    d = 128
+    model = _skeleton(d)
+    decoded = _decoded_qkv_and_out(d)
+    counts = C.swap_svdq_linears(model, decoded, device="cpu")
+    assert counts == {"prefixes": 2, "linears": 4, "int4": 0, "dense": 4, "lane": "dense"}
+    assert len(calls) == 1
+    attn = model.blocks[0].attn
+    for mod in (attn.to_q, attn.to_k, attn.to_v, attn.to_out[0]):
+        assert type(mod) is nn.Linear and mod.weight.dtype == torch.bfloat16
+    q_part = C.split_decoded(decoded["blocks.0.attn.to_qkv"], (d, d, d))[0]
+    assert torch.equal(attn.to_q.weight, C.fold_decoded(q_part, device="cpu").weight)
+
+
+def test_unavailable_lane_degrades_to_dense():
+    """Without a GPU the int4 lane is unavailable: the lane resolves to dense instead of refusing."""
+    from gen_worker_amd import qualify
+
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    assert qualify.resolve_lane() == "dense"
+    assert qualify.resolve_lane("int4") == "int4"
+    with pytest.raises(ValueError):
+        qualify.resolve_lane("fp8")
+    d = 128
+    model = _skeleton(d)
+    counts = C.swap_svdq_linears(model, _decoded_qkv_and_out(d), device="cpu")
+    assert counts["lane"] == "dense" and counts["dense"] == 4
+
+
+def test_swap_checks_the_whole_plan_before_changing_the_model():
+    """A checkpoint linear whose shape does not fit its target is refused before any module is replaced."""
+    d = 128
+    model = _skeleton(d)
+    decoded = _decoded_qkv_and_out(d)
+    _, wide = synthetic_int4_layer(2 * d, d, 16, seed=23)
+    decoded["blocks.0.norm1.linear"] = C.decode_int4_linear(wide, 2 * d, d)     # the model's Linear is [6d, d]
+    before = {n: type(m) for n, m in model.named_modules()}
+    with pytest.raises(C.SvdqLayoutError, match="norm1.linear"):
+        C.swap_svdq_linears(model, decoded, device="cpu", lane="dense")
+    assert {n: type(m) for n, m in model.named_modules()} == before
+
+
+def test_adanorm_split_matches_whole_components():
+    """The split table matches whole trailing path components, so a look-alike name is refused."""
+    assert C.adanorm_splits_for("QwenImageTransformer2DModel", "img_mod.1") == 6
+    with pytest.raises(C.SvdqLayoutError):
+        C.adanorm_splits_for("QwenImageTransformer2DModel", "blocks.0.ximg_mod.1")
