@@ -234,6 +234,20 @@ int gwa_svdq_quant_fp6(const void* x, int64_t ldx, const void* smooth, const flo
  * rank 0 or a bad shape). */
 int64_t gwa_svdq_quant_fp6_partials(int64_t M, int64_t K, int64_t rank);
 
+/* Kernel 1 for the fp6 lane with la written as bf16 (replaces
+ * cozy_gen_worker::svdq_quant, models/svdq_fused.py:293-306, plus
+ * `la = x2 @ proj_down`, :524, in one call): gwa_svdq_quant_fp6 into the
+ * partial slots in la_ws, then gwa_svdq_la_reduce into la bf16 [M, rank]
+ * (rank in {16,32,64,128}). la_ws_bytes must be at least
+ * gwa_svdq_quant_fp6_la_workspace(M, K, rank). */
+int gwa_svdq_quant_fp6_la(const void* x, int64_t ldx, const void* smooth, const float* s2,
+                          const void* proj_down_op6, int64_t rank, uint8_t* q6, void* la, float* la_ws,
+                          int64_t la_ws_bytes, int64_t M, int64_t K, void* stream);
+
+/* Bytes of la workspace gwa_svdq_quant_fp6_la needs for this shape (0 for a
+ * bad shape). */
+int64_t gwa_svdq_quant_fp6_la_workspace(int64_t M, int64_t K, int64_t rank);
+
 /* la bf16 [M, rank] = RN_bf16(part[0] + part[1] + ... + part[P-1]) (fp32
  * additions in that order; part fp32 [P, M, rank], rank % 16 == 0): the
  * bf16 la of the reference's `x2 @ proj_down` (models/svdq_fused.py:524)

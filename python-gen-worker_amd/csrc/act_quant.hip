@@ -592,6 +592,11 @@ extern "C" int gwa_svdq_la_reduce(const float* part, int64_t P, int64_t M, int64
   return gwa_check_launch("svdq_la_reduce");
 }
 
+extern "C" int64_t gwa_svdq_quant_fp6_la_workspace(int64_t M, int64_t K, int64_t rank) {
+  if (M <= 0 || K <= 0 || K % 128 || rank <= 0 || K >= (1ll << 24)) return 0;
+  return gwa_svdq_quant_fp6_partials(M, K, rank) * M * rank * 4;
+}
+
 extern "C" int gwa_svdq_quant_fp6(const void* x, int64_t ldx, const void* smooth, const float* s2,
                                   const void* proj_down_op6, int64_t rank, uint8_t* q6, float* la_part, int64_t M,
                                   int64_t K, void* stream) {
@@ -642,6 +647,25 @@ extern "C" int gwa_svdq_quant_fp6(const void* x, int64_t ldx, const void* smooth
 #undef GWA_Q6_CH
 #undef GWA_Q6_LAUNCH
   return gwa_check_launch(what);
+}
+
+extern "C" int gwa_svdq_quant_fp6_la(const void* x, int64_t ldx, const void* smooth, const float* s2,
+                                     const void* proj_down_op6, int64_t rank, uint8_t* q6, void* la, float* la_ws,
+                                     int64_t la_ws_bytes, int64_t M, int64_t K, void* stream) {
+  const char* what = "svdq_quant_fp6_la";
+  GWA_REQUIRE(M >= 0 && K > 0 && K % 128 == 0, "%s: K=%lld is not a multiple of 128", what, (long long)K);
+  GWA_REQUIRE(rank == 16 || rank == 32 || rank == 64 || rank == 128, "%s: rank %lld not in {16,32,64,128}", what,
+              (long long)rank);
+  GWA_REQUIRE(M < (1ll << 31) && K < (1ll << 24), "%s: shape too large", what);
+  if (M == 0) return GWA_OK;
+  GWA_REQUIRE(proj_down_op6 && la, "%s: null pointer", what);
+  GWA_REQUIRE(GWA_ALIGNED(la, 8), "%s: la must be 8-byte aligned", what);
+  const int64_t slots = gwa_svdq_quant_fp6_partials(M, K, rank);
+  GWA_REQUIRE(la_ws && la_ws_bytes >= slots * M * rank * 4, "%s: la workspace of %lld bytes, this shape needs %lld",
+              what, (long long)la_ws_bytes, (long long)(slots * M * rank * 4));
+  const int rc = gwa_svdq_quant_fp6(x, ldx, smooth, s2, proj_down_op6, rank, q6, la_ws, M, K, stream);
+  if (rc != GWA_OK) return rc;
+  return gwa_svdq_la_reduce(la_ws, slots, M, rank, la, stream);
 }
 
 extern "C" int gwa_svdq_prep_proj_down(const void* proj_down, void* out, int64_t K, int64_t rank, void* stream) {

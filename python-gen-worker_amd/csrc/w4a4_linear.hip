@@ -1,7 +1,8 @@
 // One SVDQuant W4A4 linear per call on the fp6 lane: kernel 1 (smoothing, int4 group-64 act-quant written
-// as fp6 operand records, x @ proj_down as fp32 partial slots), the fixed-order la reduction, and the W4A4
-// GEMM with its fused epilogue, enqueued on one stream. The intermediates (records, partial slots, bf16 la)
-// live in a workspace the caller passes in; gwa_svdq_w4a4_linear_fp6_workspace gives its size.
+// as fp6 operand records, la = x @ proj_down as fp32 partial slots and their fixed-order reduction to
+// bf16) and the W4A4 GEMM with its fused epilogue, enqueued on one stream. The intermediates (records,
+// partial slots, bf16 la) live in a workspace the caller passes in; gwa_svdq_w4a4_linear_fp6_workspace gives
+// its size.
 //
 // gwa_svdq_w4a4_linear_fp6_noalloc is the same call for callers that cannot allocate device memory: its
 // intermediates live in `scratch`, a fixed-size array of this library's code object (one copy per GPU, held
@@ -19,16 +20,16 @@ constexpr int64_t kRecordSlack = 1024;  // the GEMM copies records in 1 KB runs 
 
 int64_t align_up(int64_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
-// workspace layout: [records + slack | la partial slots fp32 [P, M, R] | la bf16 [M, R]]
+// workspace layout: [records + slack | la partial slots fp32 (kernel 1's la workspace) | la bf16 [M, R]]
 struct Scratch {
-  int64_t partials = 0, la = 0, total = 0, slots = 0;
+  int64_t partials = 0, partial_bytes = 0, la = 0, total = 0;
 };
 
 Scratch scratch_layout(int64_t M, int64_t K, int64_t R) {
   Scratch s;
-  s.slots = R ? gwa_svdq_quant_fp6_partials(M, K, R) : 0;
+  s.partial_bytes = R ? gwa_svdq_quant_fp6_la_workspace(M, K, R) : 0;
   s.partials = align_up(M * (K / 128) * GWA_FP6_REC + kRecordSlack);
-  s.la = align_up(s.partials + s.slots * M * R * 4);
+  s.la = align_up(s.partials + s.partial_bytes);
   s.total = align_up(s.la + M * R * 2);
   return s;
 }
@@ -52,14 +53,11 @@ int linear_fp6_run(const char* what, const void* x, int64_t ldx, const void* smo
   GWA_REQUIRE(ws != nullptr && ws_bytes >= s.total, "%s: workspace of %lld bytes, this shape needs %lld", what,
               (long long)ws_bytes, (long long)s.total);
   GWA_REQUIRE(GWA_ALIGNED(ws, 256), "%s: workspace must be 256-byte aligned", what);
-  float* part = R ? (float*)(ws + s.partials) : nullptr;
   uint8_t* la = R ? ws + s.la : nullptr;
-  int rc = gwa_svdq_quant_fp6(x, ldx, smooth, s2, proj_down_op6, R, ws, part, M, K, stream);
+  const int rc = R ? gwa_svdq_quant_fp6_la(x, ldx, smooth, s2, proj_down_op6, R, ws, la, (float*)(ws + s.partials),
+                                           s.partial_bytes, M, K, stream)
+                   : gwa_svdq_quant_fp6(x, ldx, smooth, s2, nullptr, 0, ws, nullptr, M, K, stream);
   if (rc != GWA_OK) return rc;
-  if (R) {
-    rc = gwa_svdq_la_reduce(part, s.slots, M, R, la, stream);
-    if (rc != GWA_OK) return rc;
-  }
   return gwa_svdq_gemm_w4a4_fp6(ws, qw6, s2, second, second_numel, la, R ? proj_up : nullptr, R, bias, out, out_dtype,
                                 epilogue_flags, M, N, K, stream);
 }

@@ -331,9 +331,29 @@ def svdq_quant_fp6(x2: Tensor, smooth: Optional[Tensor], s2: Optional[Tensor],
     if not r:
         _fp6_quant_into("svdq_quant_fp6", x2, smooth, s2, None, q6, None)
         return q6, x2.new_empty(m, 0)
-    part = torch.empty(la_partials_quant(m, k, r), m, r, dtype=torch.float32, device=x2.device)
-    _fp6_quant_into("svdq_quant_fp6", x2, smooth, s2, proj_down_op6, q6, part)
-    return q6, _la_reduce(part)
+    name = "svdq_quant_fp6"
+    if x2.dim() != 2:
+        raise SvdqOpError(f"{name}: x2 must be 2-D, got {tuple(x2.shape)}")
+    _check_dtype(name, x2, torch.bfloat16, what="x2")
+    _check_dtype(name, smooth, torch.bfloat16, what="smooth")
+    _check_dtype(name, proj_down_op6, torch.bfloat16, what="proj_down_op6")
+    s2 = _scalar_f32(name, s2)
+    _check_cuda(name, x2=x2, smooth=smooth, s2=s2, proj_down_op6=proj_down_op6)
+    if k % FP6_STAGE:
+        raise SvdqOpError(f"{name}: the fp6 records need K % {FP6_STAGE} == 0, got K={k}")
+    if smooth is not None and smooth.numel() != k:
+        raise SvdqOpError(f"{name}: smooth has {smooth.numel()} values for K={k}")
+    if proj_down_op6.dim() != 2 or int(proj_down_op6.shape[0]) < k:
+        raise SvdqOpError(f"{name}: proj_down_op6 must be [>= {k}, rank] rows in operand order, got "
+                          f"{tuple(proj_down_op6.shape)}")
+    if x2.stride(1) != 1:
+        x2 = x2.contiguous()
+    la = torch.empty(m, r, dtype=torch.bfloat16, device=x2.device)
+    ws_bytes = int(nat.load().gwa_svdq_quant_fp6_la_workspace(m, k, r))
+    ws = torch.empty(max(ws_bytes, 4) // 4, dtype=torch.float32, device=x2.device)
+    nat.call("gwa_svdq_quant_fp6_la", nat.ptr(x2), int(x2.stride(0)), nat.ptr(smooth), nat.ptr(s2),
+             nat.ptr(proj_down_op6), r, nat.ptr(q6), nat.ptr(la), nat.ptr(ws), ws_bytes, m, k, nat.stream_of(x2))
+    return q6, la
 
 
 @svdq_quant_fp6.register_fake
