@@ -449,8 +449,10 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-rows", type=int, default=512, help="rows of the bounded CPU sample")
-    ap.add_argument("--only", choices=("step", "gemm", "quant", "copy", "awq"), default=None)
+    ap.add_argument("--only", choices=("step", "gemm", "quant", "copy", "awq", "w8a8"), default=None)
     ap.add_argument("--iters", type=int, default=5)
+    ap.add_argument("--tile", type=int, default=-1,
+                    help="with --only gemm/step: force the fp6 GEMM's output tile (GWA_FP6_TILE_*; -1: the model's)")
     ap.add_argument("--workload", choices=("c1", "mlp", "qkv", "dit", "mod", "nvfp4"), default="c1",
                     help="c1: the config-1 linear (the default bench line); mlp: config 2, fc1 -> GELU -> fc2 "
                          "(fused, unfused, bf16); qkv: config 3, the QKV sweep over M and output dtype (W4A4, "
@@ -516,9 +518,19 @@ def main() -> int:
         return gemm(q, l)
 
     if args.only is not None:
+        if args.tile >= 0:
+            _native.load().gwa_svdq_gemm_w4a4_fp6_force_tile(args.tile)
         src = torch.empty(COPY_BYTES // 2, dtype=torch.bfloat16, device=dev) if args.only == "copy" else None
         dst = torch.empty_like(src) if src is not None else None
-        fn = {"step": step, "gemm": gemm, "quant": quant, "copy": lambda: dst.copy_(src)}[args.only]
+        if args.only == "w8a8":
+            # the W8A8 linear (per-token quant + int8 GEMM) at the config-1 shape, for profiling
+            from gen_worker_amd.w8a8 import build_int8_linear
+
+            L8 = synthetic.w8a8_layer(n, k)
+            lin8 = build_int8_linear(qweight=L8.qweight, weight_scale=L8.weight_scale, bias=L8.bias, device=dev)
+            fn = lambda: lin8(x)  # noqa: E731
+        else:
+            fn = {"step": step, "gemm": gemm, "quant": quant, "copy": lambda: dst.copy_(src)}[args.only]
         for _ in range(3):
             fn()
         torch.cuda.synchronize()
