@@ -11,14 +11,19 @@ of that lane on the HIP kernels of ``libgen_worker_amd.so``:
   pre-scaled and pre-negated, so w = code * s + z), and the exporter's adaLN
   transform (``adanorm_splits``: output rows interleaved and +1 folded into
   the bias of splits 1 and splits - 2);
-* the packed-resident module ``AwqPackedLinear`` (``models/svdq_awq_packed.py:
-  152-207``: weight uint8 [oc, ic/2], wscales / wzeros [oc, ic/64]) whose
-  forward is the ``cozy_gen_worker::awq_w4a16_mm`` op, and
-  ``build_awq_packed_linear`` from the on-disk tensors
-  (``models/svdq_awq_packed.py:221-253``);
-* ``decode_awq_linear``: the reference's any-hardware lane (a plain bf16
-  ``nn.Linear`` holding the dequantized weight) and ``encode_awq_linear``,
-  the exporter-layout producer used to synthesize inputs.
+* ``decode_awq_tensors``: one validating decoder from the on-disk tensors to
+  ``AwqDecoded`` (codes, scale / zero grids, group size, bias), whose
+  ``in_original_order`` undoes the adaLN row interleave; every consumer
+  starts from it:
+* the packed-resident module ``AwqPackedLinear`` (the reference's packed
+  module's buffer names, ``models/svdq_awq_packed.py:152-207``: weight uint8
+  [oc, ic/2], wscales / wzeros [oc, ic/64]) whose forward is the
+  ``cozy_gen_worker::awq_w4a16_mm`` op, built by
+  ``AwqPackedLinear.from_decoded`` / ``build_awq_packed_linear``;
+* ``decode_awq_linear``: the any-hardware lane (a plain bf16 ``nn.Linear``
+  holding the dequantized weight), ``awq_packed_self_check`` (the packed lane
+  against it on the device), and ``encode_awq_linear``, the exporter-layout
+  producer used to synthesize inputs.
 
 The TinyChat interleave and the adaLN transform are formats fixed by the
 checkpoints, so the functions here compute exactly what the reference's
@@ -27,6 +32,7 @@ functions of the same names compute, written independently.
 
 from __future__ import annotations
 
+from dataclasses import dataclass
 from typing import Any, Optional
 
 import torch
@@ -93,36 +99,100 @@ def unpack_w4x16(qweight: Tensor, out_features: int, in_features: int) -> Tensor
     return nibbles.reshape(oc, ic).to(torch.uint8)
 
 
+def _live_groups(wscales: Tensor, wzeros: Tensor, oc: int, ic: int) -> tuple[int, int]:
+    """(groups, group size) of padded [rows, oc] grids: the groups are the leading rows holding any nonzero
+    scale (the exporter zero-fills the padding rows), which must divide in_features, and the padded row
+    count must be the exporter's for that group size."""
+    if wscales.dim() != 2 or int(wscales.shape[1]) != oc:
+        raise AwqLayoutError(f"wscales {tuple(wscales.shape)}: expected [rows, {oc}] for {oc} output channels")
+    if tuple(wzeros.shape) != tuple(wscales.shape):
+        raise AwqLayoutError(f"wzeros {tuple(wzeros.shape)} and wscales {tuple(wscales.shape)} differ in shape")
+    nonzero = (wscales != 0).any(dim=1).tolist()
+    groups = nonzero.index(False) if False in nonzero else len(nonzero)
+    if groups == 0 or any(nonzero[groups:]):
+        raise AwqLayoutError("wscales: the rows holding scales are not a leading block followed by zero padding")
+    if ic % groups:
+        raise AwqLayoutError(f"{groups} scale groups do not divide in_features {ic}")
+    gs = ic // groups
+    if int(wscales.shape[0]) != num_scale_rows(ic, gs):
+        raise AwqLayoutError(f"wscales has {int(wscales.shape[0])} rows; group size {gs} at in_features {ic} "
+                             f"pads to {num_scale_rows(ic, gs)}")
+    return groups, gs
+
+
 def scales_and_zeros(wscales: Tensor, wzeros: Tensor, out_features: int,
                      in_features: int) -> tuple[Tensor, Tensor, int]:
-    """Padded grids [rows, oc] -> (scale, zero) fp32 [oc, groups] and the group size
-    (``models/svdq_awq.py:49-71``: the live groups are the leading rows with a nonzero scale)."""
+    """Padded grids [rows, oc] -> (scale, zero) fp32 [oc, groups] and the group size (the grid layout of
+    ``models/svdq_awq.py:49-71``)."""
+    groups, gs = _live_groups(wscales, wzeros, int(out_features), int(in_features))
+    return (wscales[:groups].float().t().contiguous(), wzeros[:groups].float().t().contiguous(), gs)
+
+
+@dataclass(frozen=True)
+class AwqDecoded:
+    """One AWQ W4A16 linear in logical form: codes uint8 [oc, ic] (0..15), scale and zero fp32
+    [oc, groups] (w = code * scale + zero), the group size and the bias as stored; rows in the order the
+    tensors hold them (``in_original_order`` undoes the exporter's adaLN row interleave)."""
+
+    codes: Tensor
+    scale: Tensor
+    zero: Tensor
+    group_size: int
+    bias: Optional[Tensor]
+
+    @property
+    def out_features(self) -> int:
+        return int(self.codes.shape[0])
+
+    @property
+    def in_features(self) -> int:
+        return int(self.codes.shape[1])
+
+    def in_original_order(self, splits: int) -> "AwqDecoded":
+        """The layer before the exporter's adaLN transform (``models/svdq_awq.py:85-103`` states it): stored
+        row j * splits + s is original row s * per + j, and splits 1 and splits - 2 carry +1 in the bias."""
+        if splits <= 1:
+            return self
+        oc = self.out_features
+        if oc % splits:
+            raise AwqLayoutError(f"out_features {oc} is not a multiple of adanorm_splits {splits}")
+        per = oc // splits
+        i = torch.arange(oc, device=self.codes.device)
+        stored_row = (i % per) * splits + i // per
+        bias = None
+        if self.bias is not None:
+            bias = _unshift_split_bias(self.bias.float().reshape(per, splits).t(), splits).reshape(oc)
+        return AwqDecoded(self.codes[stored_row], self.scale[stored_row], self.zero[stored_row], self.group_size,
+                          bias)
+
+    def weight(self) -> Tensor:
+        """fp32 [oc, ic] = code * scale + zero."""
+        oc, ic, gs = self.out_features, self.in_features, self.group_size
+        w = self.codes.float().reshape(oc, ic // gs, gs)
+        return (w * self.scale.unsqueeze(-1) + self.zero.unsqueeze(-1)).reshape(oc, ic)
+
+
+def decode_awq_tensors(tensors: dict[str, Tensor], out_features: int, in_features: int) -> AwqDecoded:
+    """The on-disk tensors of one AWQ linear (``qweight``, ``wscales``, ``wzeros``, optional ``bias``),
+    validated, in logical form."""
+    missing = [k for k in ("qweight", "wscales", "wzeros") if k not in tensors]
+    if missing:
+        raise AwqLayoutError(f"an AWQ W4A16 linear needs qweight, wscales and wzeros; {', '.join(missing)} missing")
     oc, ic = int(out_features), int(in_features)
-    if int(wscales.shape[1]) != oc or tuple(wzeros.shape) != tuple(wscales.shape):
-        raise AwqLayoutError(f"AWQ scale/zero grids {tuple(wscales.shape)}/{tuple(wzeros.shape)} do not match "
-                             f"out_features {oc}")
-    s = wscales.float()
-    live = (s != 0).any(dim=1)
-    ng = int(live.sum())
-    if ng == 0 or not bool(live[:ng].all()):
-        raise AwqLayoutError("AWQ wscales has zero rows before its last live row (not the padded layout)")
-    if ic % ng:
-        raise AwqLayoutError(f"in_features {ic} not divisible by {ng} live scale groups")
-    gs = ic // ng
-    if num_scale_rows(ic, gs) != int(wscales.shape[0]):
-        raise AwqLayoutError(f"AWQ scale rows {int(wscales.shape[0])} != num_scale_rows({ic}, {gs}) = "
-                             f"{num_scale_rows(ic, gs)}")
-    return s[:ng].t().contiguous(), wzeros.float()[:ng].t().contiguous(), gs
+    codes = unpack_w4x16(tensors["qweight"], oc, ic)
+    scale, zero, gs = scales_and_zeros(tensors["wscales"].to(codes.device), tensors["wzeros"].to(codes.device),
+                                       oc, ic)
+    bias = tensors.get("bias")
+    if bias is not None and int(bias.numel()) != oc:
+        raise AwqLayoutError(f"bias has {int(bias.numel())} values for {oc} output channels")
+    return AwqDecoded(codes, scale, zero, gs, bias.to(codes.device) if bias is not None else None)
 
 
 def dequantize_w4x16(qweight: Tensor, wscales: Tensor, wzeros: Tensor, out_features: int,
                      in_features: int) -> Tensor:
-    """AWQ tensors -> fp32 weight [oc, ic] = code * scale + zero (``models/svdq_awq.py:74-82``)."""
-    codes = unpack_w4x16(qweight, out_features, in_features)
-    scale, zero, gs = scales_and_zeros(wscales, wzeros, out_features, in_features)
-    oc, ic = int(out_features), int(in_features)
-    w = codes.float().reshape(oc, ic // gs, gs)
-    return (w * scale.unsqueeze(-1) + zero.unsqueeze(-1)).reshape(oc, ic)
+    """AWQ tensors -> fp32 weight [oc, ic] = code * scale + zero (rows as stored)."""
+    return decode_awq_tensors({"qweight": qweight, "wscales": wscales, "wzeros": wzeros}, out_features,
+                              in_features).weight()
 
 
 def _split_delta(splits: int, dtype, device) -> Tensor:
@@ -148,30 +218,24 @@ def apply_adanorm_splits(weight: Tensor, bias: Optional[Tensor], splits: int) ->
     return w, b.transpose(0, 1).reshape(oc)
 
 
+def _unshift_split_bias(by_split: Tensor, splits: int) -> Tensor:
+    """[splits, per] bias without the +1 the exporter folds into splits 1 and splits - 2 (one split when
+    they coincide)."""
+    return by_split - _split_delta(splits, by_split.dtype, by_split.device).reshape(splits, 1)
+
+
 def undo_adanorm_splits(weight: Tensor, bias: Optional[Tensor], splits: int) -> tuple[Tensor, Optional[Tensor]]:
-    """Inverse of :func:`apply_adanorm_splits` (``models/svdq_awq.py:85-103``)."""
+    """Inverse of :func:`apply_adanorm_splits` on a dense weight (``models/svdq_awq.py:85-103``)."""
     if splits <= 1:
         return weight, bias
     oc = int(weight.shape[0])
     if oc % splits:
-        raise AwqLayoutError(f"out_features {oc} not divisible by adanorm_splits {splits}")
+        raise AwqLayoutError(f"out_features {oc} is not a multiple of adanorm_splits {splits}")
     per = oc // splits
     w = weight.reshape(per, splits, -1).transpose(0, 1).reshape(oc, -1)
-    return w, (_undo_split_bias(bias, splits) if bias is not None else None)
-
-
-def _undo_split_bias(bias: Tensor, splits: int) -> Tensor:
-    oc = int(bias.numel())
-    b = bias.float().reshape(oc // splits, splits).transpose(0, 1)
-    b = b - _split_delta(splits, b.dtype, b.device).reshape(splits, 1)
-    return b.reshape(oc)
-
-
-def _undo_interleave_rows(oc: int, splits: int, device) -> Tensor:
-    """Index of the stored row that holds original row i (original row s * per + j is stored at j * splits + s)."""
-    per = oc // splits
-    i = torch.arange(oc, device=device)
-    return (i % per) * splits + i // per
+    if bias is None:
+        return w, None
+    return w, _unshift_split_bias(bias.float().reshape(per, splits).t(), splits).reshape(oc)
 
 
 def encode_awq_linear(weight: Tensor, bias: Optional[Tensor], *, group_size: int = GROUP_SIZE,
@@ -211,55 +275,75 @@ def is_awq_linear(tensors: dict[str, Any]) -> bool:
 def decode_awq_linear(tensors: dict[str, Tensor], out_features: int, in_features: int, *,
                       adanorm_splits: int = 1, compute_dtype: Optional[torch.dtype] = None,
                       device=None) -> nn.Linear:
-    """The reference's decode lane (``models/svdq_awq.py:106-129``): a plain ``nn.Linear`` in
-    ``compute_dtype`` (bf16) holding the dequantized weight, adaLN transform undone."""
-    missing = [k for k in ("qweight", "wscales", "wzeros") if k not in tensors]
-    if missing:
-        raise AwqLayoutError(f"not an AWQ W4A16 linear (missing {missing})")
-    compute = compute_dtype or torch.bfloat16
-    w = dequantize_w4x16(tensors["qweight"], tensors["wscales"], tensors["wzeros"], out_features, in_features)
-    w, bias = undo_adanorm_splits(w, tensors.get("bias"), int(adanorm_splits))
-    lin = nn.Linear(int(in_features), int(out_features), bias=bias is not None, dtype=compute, device=device)
+    """The any-hardware lane (the role of ``models/svdq_awq.py:106-129``): a plain ``nn.Linear`` in
+    ``compute_dtype`` (bf16) holding the dequantized weight in the original row order."""
+    dec = decode_awq_tensors(tensors, out_features, in_features).in_original_order(int(adanorm_splits))
+    dtype = compute_dtype or torch.bfloat16
+    lin = nn.Linear(dec.in_features, dec.out_features, bias=dec.bias is not None, dtype=dtype, device=device)
     with torch.no_grad():
-        lin.weight.copy_(w.to(compute))
-        if bias is not None:
-            lin.bias.copy_(bias.to(compute))
-    lin.requires_grad_(False)
-    return lin
+        lin.weight.copy_(dec.weight().to(dtype))
+        if dec.bias is not None:
+            lin.bias.copy_(dec.bias.to(dtype))
+    return lin.requires_grad_(False)
+
+
+def _packed_contract(out_features: int, in_features: int, compute_dtype: torch.dtype) -> Optional[str]:
+    """Why a shape / dtype cannot take the packed lane (None when it can)."""
+    if compute_dtype != torch.bfloat16:
+        return f"the packed AWQ lane computes in bf16, not {compute_dtype}"
+    if not awq_packed_supported(out_features, in_features):
+        return (f"the packed AWQ lane needs out_features % 16 == 0 and in_features % 128 == 0, got "
+                f"[{out_features}, {in_features}]")
+    return None
 
 
 class AwqPackedLinear(nn.Module):
-    """Packed-resident AWQ W4A16 linear (``models/svdq_awq_packed.py:152-207``): buffers ``weight``
-    uint8 [oc, ic/2] (column 2j in the low nibble of byte j), ``wscales`` / ``wzeros`` bf16 [oc, ic/64],
-    ``bias`` bf16 [oc] or None; forward = ``cozy_gen_worker::awq_w4a16_mm``."""
+    """AWQ W4A16 linear served from its packed form (the module of ``models/svdq_awq_packed.py:152-207``,
+    same buffer names): ``weight`` uint8 [oc, ic/2] (column 2j in the low nibble of byte j), ``wscales`` /
+    ``wzeros`` bf16 [oc, ic/64], ``bias`` bf16 [oc] or None; forward = ``cozy_gen_worker::awq_w4a16_mm``."""
 
     _cozy_awq_packed = True
 
     def __init__(self, in_features: int, out_features: int, *, bias: bool,
                  compute_dtype: torch.dtype = torch.bfloat16, device=None) -> None:
         super().__init__()
-        if compute_dtype != torch.bfloat16:
-            raise AwqPackedError(f"AwqPackedLinear computes in bf16, not {compute_dtype}")
-        if not awq_packed_supported(out_features, in_features):
-            raise AwqPackedError(f"AwqPackedLinear [{out_features}, {in_features}] breaks the packed contract "
-                                 f"(out % 16, in % 128)")
-        self.compute_dtype = compute_dtype
+        why = _packed_contract(int(out_features), int(in_features), compute_dtype)
+        if why is not None:
+            raise AwqPackedError(why)
         self.in_features, self.out_features = int(in_features), int(out_features)
-        ng = in_features // GROUP_SIZE
-        self.register_buffer("weight", torch.zeros(out_features, in_features // 2, dtype=torch.uint8, device=device))
-        self.register_buffer("wscales", torch.zeros(out_features, ng, dtype=compute_dtype, device=device))
-        self.register_buffer("wzeros", torch.zeros(out_features, ng, dtype=compute_dtype, device=device))
-        if bias:
-            self.bias: Optional[nn.Parameter] = nn.Parameter(
-                torch.zeros(out_features, dtype=compute_dtype, device=device), requires_grad=False)
-        else:
-            self.bias = None
+        self.compute_dtype = compute_dtype
+        groups = self.in_features // GROUP_SIZE
+        empty = lambda *shape, dtype: torch.zeros(*shape, dtype=dtype, device=device)  # noqa: E731
+        self.register_buffer("weight", empty(self.out_features, self.in_features // 2, dtype=torch.uint8))
+        self.register_buffer("wscales", empty(self.out_features, groups, dtype=compute_dtype))
+        self.register_buffer("wzeros", empty(self.out_features, groups, dtype=compute_dtype))
+        self.bias: Optional[nn.Parameter] = (
+            nn.Parameter(empty(self.out_features, dtype=compute_dtype), requires_grad=False) if bias else None)
+
+    @classmethod
+    def from_decoded(cls, dec: AwqDecoded, *, compute_dtype: Optional[torch.dtype] = None,
+                     device=None) -> "AwqPackedLinear":
+        """The packed module of a decoded layer (rows as they should be served)."""
+        if dec.group_size != GROUP_SIZE:
+            raise AwqPackedError(f"the packed AWQ lane serves group size {GROUP_SIZE}, this layer has "
+                                 f"{dec.group_size} (decode_awq_linear serves it)")
+        dev = torch.device(device) if device is not None else dec.codes.device
+        mod = cls(dec.in_features, dec.out_features, bias=dec.bias is not None,
+                  compute_dtype=compute_dtype or torch.bfloat16, device=dev)
+        codes = dec.codes.to(dev)
+        with torch.no_grad():
+            mod.weight.copy_(codes[:, 0::2] | (codes[:, 1::2] << 4))
+            mod.wscales.copy_(dec.scale.to(dev, mod.compute_dtype))
+            mod.wzeros.copy_(dec.zero.to(dev, mod.compute_dtype))
+            if dec.bias is not None:
+                mod.bias.copy_(dec.bias.reshape(-1).to(dev, mod.compute_dtype))
+        return mod
 
     def forward(self, x: Tensor) -> Tensor:
-        shape = x.shape
-        x2 = x.reshape(-1, self.in_features).contiguous()
-        y = torch.ops.cozy_gen_worker.awq_w4a16_mm(x2, self.weight, self.wscales, self.wzeros, self.bias)
-        return y.reshape(*shape[:-1], self.out_features)
+        lead = x.shape[:-1]
+        y = torch.ops.cozy_gen_worker.awq_w4a16_mm(x.reshape(-1, self.in_features).contiguous(), self.weight,
+                                                   self.wscales, self.wzeros, self.bias)
+        return y.reshape(*lead, self.out_features)
 
     def extra_repr(self) -> str:
         return (f"in_features={self.in_features}, out_features={self.out_features}, "
@@ -269,59 +353,43 @@ class AwqPackedLinear(nn.Module):
 def build_awq_packed_linear(tensors: dict[str, Tensor], out_features: int, in_features: int, *,
                             adanorm_splits: int = 1, compute_dtype: Optional[torch.dtype] = None,
                             device=None) -> AwqPackedLinear:
-    """Packed-resident module from the on-disk tensors (``models/svdq_awq_packed.py:221-253``): codes
-    unpacked and re-packed two per byte, grids un-padded and transposed to [oc, groups], the adaLN row
-    interleave and bias offsets undone."""
-    compute = compute_dtype or torch.bfloat16
-    oc, ic = int(out_features), int(in_features)
-    dev = torch.device(device) if device is not None else tensors["qweight"].device
-    codes = unpack_w4x16(tensors["qweight"].to(dev), oc, ic)
-    scale, zero, gs = scales_and_zeros(tensors["wscales"].to(dev), tensors["wzeros"].to(dev), oc, ic)
-    if gs != GROUP_SIZE:
-        raise AwqPackedError(f"AWQ group size {gs} != {GROUP_SIZE}: the packed lane serves group {GROUP_SIZE} "
-                             f"only (decode_awq_linear serves this layer)")
-    bias = tensors.get("bias")
-    splits = int(adanorm_splits)
-    if splits > 1:
-        if oc % splits:
-            raise AwqLayoutError(f"out_features {oc} not divisible by adanorm_splits {splits}")
-        rows = _undo_interleave_rows(oc, splits, codes.device)
-        codes, scale, zero = codes[rows], scale[rows], zero[rows]
-        if bias is not None:
-            bias = _undo_split_bias(bias.to(codes.device), splits)
-    mod = AwqPackedLinear(ic, oc, bias=bias is not None, compute_dtype=compute, device=dev)
-    with torch.no_grad():
-        mod.weight.copy_((codes[:, 1::2] << 4) | codes[:, 0::2])
-        mod.wscales.copy_(scale.to(compute))
-        mod.wzeros.copy_(zero.to(compute))
-        if bias is not None:
-            mod.bias.copy_(bias.reshape(-1).to(compute))
-    return mod
+    """The packed module from the on-disk tensors (the role of ``models/svdq_awq_packed.py:221-253``):
+    decoded, put back in the original row order, re-packed two codes per byte."""
+    src = tensors["qweight"].device if "qweight" in tensors else None
+    dev = torch.device(device) if device is not None else src
+    on_dev = {k: v.to(dev) for k, v in tensors.items()}
+    dec = decode_awq_tensors(on_dev, out_features, in_features).in_original_order(int(adanorm_splits))
+    return AwqPackedLinear.from_decoded(dec, compute_dtype=compute_dtype, device=dev)
+
+
+# (out_features, in_features, adaLN splits, activation rows): the GEMV path and the dequantize + GEMM path
+# of awq_w4a16_mm, with and without the adaLN row interleave
+_SELF_CHECK_CASES = ((256, 384, 1, 1), (384, 256, 6, 1), (384, 256, 6, 24))
+SELF_CHECK_REL_TOL = 5e-3   # the reference's bar for its packed lane (models/svdq_awq_packed.py:256-285)
 
 
 def awq_packed_self_check(device="cuda") -> Optional[str]:
-    """The reference's packed-lane check (``models/svdq_awq_packed.py:256-285``): the packed module
-    against the decoded bf16 Linear at [512, 256] and [768, 256] with 6 adaLN splits, rel-Frobenius
-    <= 5e-3; None when it passes, else the failure."""
-    for oc, ic, splits in ((512, 256, 1), (768, 256, 6)):
-        g = torch.Generator().manual_seed(0)
-        w = torch.randn(oc, ic, generator=g) * 0.05
-        b = torch.randn(oc, generator=g)
-        tensors = encode_awq_linear(w, b, adanorm_splits=splits)
-        ref = decode_awq_linear(tensors, oc, ic, adanorm_splits=splits, device=device)
-        mod = build_awq_packed_linear(tensors, oc, ic, adanorm_splits=splits, device=device)
-        x = torch.randn(3, ic, generator=g).to(device=device, dtype=torch.bfloat16)
+    """The packed lane against the decoded bf16 Linear of the same tensors on the device: None when every
+    case is within ``SELF_CHECK_REL_TOL`` (relative Frobenius error), else the first failing case."""
+    for oc, ic, splits, rows in _SELF_CHECK_CASES:
+        g = torch.Generator().manual_seed(1000 * splits + rows)
+        tensors = encode_awq_linear(torch.randn(oc, ic, generator=g) * 0.04,
+                                    torch.randn(oc, generator=g) * 0.1, adanorm_splits=splits)
+        packed = build_awq_packed_linear(tensors, oc, ic, adanorm_splits=splits, device=device)
+        dense = decode_awq_linear(tensors, oc, ic, adanorm_splits=splits, device=device)
+        x = torch.randn(rows, ic, generator=g).to(device=device, dtype=torch.bfloat16)
         with torch.no_grad():
-            got, want = mod(x).float(), ref(x).float()
-        rel = ((got - want).norm() / want.norm().clamp(min=1e-9)).item()
-        if rel > 5e-3:
-            return f"awq packed rel err {rel:.4f} vs decoded Linear at [{oc},{ic}] splits={splits}"
+            got, want = packed(x).float(), dense(x).float()
+        rel = float((got - want).norm() / want.norm().clamp(min=1e-12))
+        if not rel <= SELF_CHECK_REL_TOL:
+            return (f"packed AWQ [{oc} x {ic}], {splits} adaLN split(s), {rows} row(s): relative error {rel:.2e} "
+                    f"against its decoded Linear exceeds {SELF_CHECK_REL_TOL}")
     return None
 
 
 __all__ = [
-    "AwqLayoutError", "AwqPackedError", "AwqPackedLinear", "GROUP_SIZE", "apply_adanorm_splits",
-    "awq_packed_self_check", "awq_packed_supported", "build_awq_packed_linear", "decode_awq_linear",
-    "dequantize_w4x16", "encode_awq_linear", "is_awq_linear", "num_scale_rows", "pack_w4x16",
-    "scales_and_zeros", "undo_adanorm_splits", "unpack_w4x16",
+    "AwqDecoded", "AwqLayoutError", "AwqPackedError", "AwqPackedLinear", "GROUP_SIZE", "SELF_CHECK_REL_TOL",
+    "apply_adanorm_splits", "awq_packed_self_check", "awq_packed_supported", "build_awq_packed_linear",
+    "decode_awq_linear", "decode_awq_tensors", "dequantize_w4x16", "encode_awq_linear", "is_awq_linear",
+    "num_scale_rows", "pack_w4x16", "scales_and_zeros", "undo_adanorm_splits", "unpack_w4x16",
 ]

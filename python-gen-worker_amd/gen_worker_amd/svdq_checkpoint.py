@@ -19,7 +19,11 @@ with int4 arithmetic:
   ``wcscales`` / ``wtscale`` (an optional second-level scale);
 * ``proj_down`` [in, rank] and ``proj_up`` [out, rank]: ``pack_lowrank_weight``
   16 x 16 packs (``svdq_layout.py:140-161``); proj_down is applied to the RAW
-  activation (the exporter pre-divided it by the smoothing factors).
+  activation (the exporter pre-divided it by the smoothing factors). An
+  artifact whose ``__metadata__`` declares ``lowrank_quant`` = int8 / fp8_e4m3
+  stores the two factors plain row-major in that dtype with fp32 scales per
+  32-block (``proj_down_scale`` [in/32, rank], ``proj_up_scale`` [out,
+  rank/32]; ``svdq_layout.py:34-38``, ``:261-298``), decoded to bf16.
 
 ``decode_int4_linear`` returns the logical (row-major) tensors, ``split_decoded``
 splits nunchaku's fused projections (``to_qkv`` -> ``to_q``/``to_k``/``to_v``,
@@ -207,9 +211,96 @@ def _exact_fp16(t: Tensor, what: str) -> Tensor:
     return h
 
 
-def decode_int4_linear(tensors: dict[str, Tensor], out_features: int, in_features: int) -> DecodedInt4Linear:
+# Quantized low-rank branch (an artifact's ``__metadata__["lowrank_quant"]``, ``models/svdq_layout.py:34-38``):
+# proj_down [in, rank] / proj_up [out, rank] stored PLAIN row-major as int8 or fp8 e4m3, with fp32 scales per
+# block of 32 along each factor's contraction dimension: proj_down_scale [in/32, rank], proj_up_scale
+# [out, rank/32]; the factor is RN_bf16(code * scale).
+LOWRANK_QUANT_KEY = "lowrank_quant"
+LOWRANK_SCHEMES = {"int8": torch.int8, "fp8_e4m3": torch.float8_e4m3fn}
+LOWRANK_BLOCK = 32
+
+
+def _lowrank_scheme(t: Tensor) -> str:
+    for name, dt in LOWRANK_SCHEMES.items():
+        if t.dtype == dt:
+            return name
+    return "bf16"
+
+
+def dequantize_lowrank_factor(q: Tensor, scale: Tensor, *, along_rows: bool) -> Tensor:
+    """bf16 factor = RN_bf16(code * scale), the scale of each block of 32 along the rows (proj_down: its
+    input dimension) or along the columns (proj_up: the rank)."""
+    rows, cols = int(q.shape[0]), int(q.shape[1])
+    n = rows if along_rows else cols
+    if n % LOWRANK_BLOCK:
+        raise SvdqLayoutError(f"a quantized low-rank factor [{rows}, {cols}] needs its blocked dimension to be a "
+                              f"multiple of {LOWRANK_BLOCK}")
+    want = (n // LOWRANK_BLOCK, cols) if along_rows else (rows, n // LOWRANK_BLOCK)
+    if tuple(scale.shape) != want:
+        raise SvdqLayoutError(f"low-rank block scales {tuple(scale.shape)}: expected {want} for a [{rows}, {cols}] "
+                              f"factor")
+    per_elem = scale.float().repeat_interleave(LOWRANK_BLOCK, dim=0 if along_rows else 1)
+    return (q.float() * per_elem).to(torch.bfloat16)
+
+
+def quantize_lowrank_factor(w: Tensor, scheme: str, *, along_rows: bool) -> tuple[Tensor, Tensor]:
+    """Producer of the quantized low-rank format (for synthetic checkpoints): per block of 32, scale =
+    max(absmax / qmax, 1e-12) (qmax 127 for int8, 448 for e4m3), codes = round-to-nearest-even clamped
+    (int8) or the e4m3 cast of the scaled value (``models/svdq_layout.py:261-275``)."""
+    if scheme not in LOWRANK_SCHEMES:
+        raise SvdqLayoutError(f"unknown low-rank scheme {scheme!r} (known: {', '.join(LOWRANK_SCHEMES)})")
+    w32 = w.float()
+    dim = 0 if along_rows else 1
+    n = int(w32.shape[dim])
+    if n % LOWRANK_BLOCK:
+        raise SvdqLayoutError(f"dimension {n} is not a multiple of {LOWRANK_BLOCK}")
+    blocks = w32.reshape(n // LOWRANK_BLOCK, LOWRANK_BLOCK, -1) if along_rows else \
+        w32.reshape(w32.shape[0], n // LOWRANK_BLOCK, LOWRANK_BLOCK)
+    qmax = 127.0 if scheme == "int8" else 448.0
+    scale = (blocks.abs().amax(dim=1 if along_rows else 2) / qmax).clamp(min=1e-12)
+    scaled = w32 / scale.repeat_interleave(LOWRANK_BLOCK, dim=dim)
+    if scheme == "int8":
+        q = torch.round(scaled).clamp(-127, 127).to(torch.int8)
+    else:
+        q = scaled.clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+    return q, scale.float()
+
+
+def _decode_lowrank(down: Tensor, up: Tensor, tensors: dict[str, Tensor], n: int, k: int,
+                    declared: Optional[str]) -> tuple[Tensor, Tensor, int]:
+    """(proj_down bf16 [k, rank], proj_up bf16 [n, rank], rank) from either packaging of the branch."""
+    scheme = _lowrank_scheme(down)
+    if _lowrank_scheme(up) != scheme:
+        raise SvdqLayoutError(f"proj_down is {down.dtype} but proj_up is {up.dtype}: one scheme per branch")
+    if declared is not None and declared not in ("bf16",) + tuple(LOWRANK_SCHEMES):
+        raise SvdqLayoutError(f"the artifact declares {LOWRANK_QUANT_KEY}={declared!r}, not one of bf16, "
+                              f"{', '.join(LOWRANK_SCHEMES)}")
+    if declared is not None and declared != scheme:
+        raise SvdqLayoutError(f"the artifact declares {LOWRANK_QUANT_KEY}={declared!r} but the branch is stored "
+                              f"as {scheme}")
+    rank = int(down.shape[1])
+    if int(down.shape[0]) != k or tuple(up.shape) != (n, rank):
+        raise SvdqLayoutError(f"low-rank factors {tuple(down.shape)} / {tuple(up.shape)} do not match [{n}, {k}]")
+    has_scales = "proj_down_scale" in tensors or "proj_up_scale" in tensors
+    if scheme == "bf16":
+        if has_scales:
+            raise SvdqLayoutError("low-rank block scales are present but the factors are not stored quantized")
+        if down.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+            raise SvdqLayoutError(f"low-rank branch stored as {down.dtype}: not a 16/32-bit or int8 / fp8 factor")
+        return unpack_lowrank(down, down=True).to(torch.bfloat16), unpack_lowrank(up, down=False).to(
+            torch.bfloat16), rank
+    for key in ("proj_down_scale", "proj_up_scale"):
+        if key not in tensors:
+            raise SvdqLayoutError(f"the {scheme} low-rank branch has no {key}")
+    return (dequantize_lowrank_factor(down, tensors["proj_down_scale"], along_rows=True),
+            dequantize_lowrank_factor(up, tensors["proj_up_scale"], along_rows=False), rank)
+
+
+def decode_int4_linear(tensors: dict[str, Tensor], out_features: int, in_features: int, *,
+                       lowrank_quant: Optional[str] = None) -> DecodedInt4Linear:
     """One int4 svdq linear's stored tensors -> :class:`DecodedInt4Linear` (``decode_linear``,
-    ``models/svdq_layout.py:366-434``, with int4 group-64 arithmetic)."""
+    ``models/svdq_layout.py:366-434``, with int4 group-64 arithmetic); ``lowrank_quant`` is the artifact's
+    declared low-rank scheme (None: whatever the factors' dtype says)."""
     missing = [k for k in ("qweight", "wscales") if k not in tensors]
     if missing:
         raise SvdqLayoutError(f"not an svdq W4A4 linear (missing {missing})")
@@ -231,14 +322,7 @@ def decode_int4_linear(tensors: dict[str, Tensor], out_features: int, in_feature
         raise SvdqLayoutError("svdq linear has only one half of the low-rank branch")
     rank = 0
     if down is not None:
-        rank = int(down.shape[1])
-        if int(down.shape[0]) != k or tuple(up.shape) != (n, rank):
-            raise SvdqLayoutError(f"low-rank factors {tuple(down.shape)} / {tuple(up.shape)} do not match "
-                                  f"[{n}, {k}]")
-        if down.dtype not in (torch.bfloat16, torch.float16, torch.float32):
-            raise SvdqLayoutError(f"low-rank branch stored as {down.dtype}: only 16/32-bit factors are read here")
-        down = unpack_lowrank(down, down=True).to(torch.bfloat16)
-        up = unpack_lowrank(up, down=False).to(torch.bfloat16)
+        down, up, rank = _decode_lowrank(down, up, tensors, n, k, lowrank_quant)
     smooth = tensors.get("smooth_factor")
     if smooth is not None:
         smooth = unpack_vector(smooth.reshape(-1), k).to(torch.bfloat16)
@@ -437,7 +521,7 @@ def _group_by_prefix(names) -> dict[str, list[str]]:
 
 def load_svdq_int4_checkpoint(path, model: nn.Module, *, model_class: str = "",
                               adanorm_splits: Optional[Dict[str, int]] = None, device: Any = "cuda",
-                              lane: Optional[str] = None) -> dict:
+                              lane: Optional[str] = None, lowrank_quant: Optional[str] = None) -> dict:
     """Read an int4 svdq safetensors file into ``model`` (a skeleton whose module names match the
     checkpoint's): int4 linears swapped for ``SvdqW4A4Linear`` (fused projections split), AWQ modulation
     linears for ``AwqPackedLinear``, every other tensor copied into the parameter / buffer of that name."""
@@ -457,7 +541,7 @@ def load_svdq_int4_checkpoint(path, model: nn.Module, *, model_class: str = "",
             elif "qweight" in tensors:
                 targets = _resolve_targets(_linear_index(model), prefix, type(model).__name__)
                 decoded[prefix] = decode_int4_linear(tensors, sum(t.out_features for t in targets),
-                                                     targets[0].in_features)
+                                                     targets[0].in_features, lowrank_quant=lowrank_quant)
             else:
                 for leaf, t in tensors.items():
                     plain[f"{prefix}.{leaf}" if prefix else leaf] = t
@@ -489,7 +573,8 @@ def load_svdq_int4_checkpoint(path, model: nn.Module, *, model_class: str = "",
 
 
 __all__ = [
-    "DecodedInt4Linear", "SvdqLayoutError", "SwapTarget", "adanorm_splits_for", "build_module", "decode_int4_linear",
+    "DecodedInt4Linear", "LOWRANK_QUANT_KEY", "LOWRANK_SCHEMES", "SvdqLayoutError", "SwapTarget",
+    "adanorm_splits_for", "dequantize_lowrank_factor", "quantize_lowrank_factor", "build_module", "decode_int4_linear",
     "dequantize_decoded", "fold_decoded", "is_int4_svdq_linear", "load_svdq_int4_checkpoint", "pack_group_scales",
     "pack_lowrank", "pack_qweight", "pack_vector", "plan_targets", "split_decoded", "swap_awq_linears",
     "swap_svdq_linears", "unpack_group_scales", "unpack_lowrank", "unpack_qweight", "unpack_vector",

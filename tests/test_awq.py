@@ -212,3 +212,19 @@ def test_op_refuses_cpu_and_bad_shapes():
     s = torch.zeros(32, 4, dtype=torch.bfloat16)
     with pytest.raises(SvdqOpError):
         torch.ops.cozy_gen_worker.awq_w4a16_mm(x, wt, s, s, None)        # CPU tensors
+
+
+@pytest.mark.parametrize("splits", [1, 2, 3, 6])
+def test_decoded_original_order_matches_dense_undo(splits):
+    """The decoder's row reorder and bias fix (on codes and grids) equal the dense inverse transform applied
+    to the dequantized stored weight, for every split count (3: the two shifted splits coincide)."""
+    g = torch.Generator().manual_seed(40 + splits)
+    oc, ic = 48, 128
+    t = awq.encode_awq_linear(torch.randn(oc, ic, generator=g) * 0.05, torch.randn(oc, generator=g),
+                              adanorm_splits=splits)
+    stored = awq.decode_awq_tensors(t, oc, ic)
+    assert stored.group_size == 64 and (stored.out_features, stored.in_features) == (oc, ic)
+    dec = stored.in_original_order(splits)
+    w_ref, b_ref = awq.undo_adanorm_splits(stored.weight(), t["bias"], splits)
+    assert torch.equal(dec.weight(), w_ref)
+    assert torch.equal(dec.bias, b_ref.float() if splits > 1 else t["bias"])

@@ -90,3 +90,40 @@ def test_load_int4_checkpoint(tmp_path):
     with torch.no_grad():
         y, yl = blk.norm1.linear(x).float(), lin(x).float()
     assert ((y - yl).norm() / yl.norm()).item() <= 5e-3
+
+
+@pytest.mark.parametrize("scheme", ["int8", "fp8_e4m3"])
+def test_load_artifact_quantized_lowrank(tmp_path, scheme):
+    """A snapshot whose svdq-int4 artifact (detected by its metadata in transformer/) stores the low-rank
+    branch as int8 / fp8 with block scales: routed onto the int4 lane, each swapped module against the oracle
+    on the dequantized factors."""
+    import json
+
+    from safetensors.torch import save_file
+
+    from gen_worker_amd import svdq_artifact as SA
+    from test_svdq_artifact import _quantized_layer
+
+    logical, stored, down, up = _quantized_layer(3 * D, D, 32, 31, scheme)
+    tensors = {f"blocks.0.attn.to_qkv.{k}": v.contiguous() for k, v in stored.items()}
+    meta = {"model_class": "NunchakuFluxTransformer2DModel", "lowrank_quant": scheme,
+            "quantization_config": json.dumps({"method": "svdquant", "weight": {"dtype": "int4"}, "rank": 32})}
+    (tmp_path / "transformer").mkdir()
+    save_file(tensors, str(tmp_path / "transformer" / "svdq.safetensors"), metadata=meta)
+    model = nn.Module()
+    model.blocks = nn.ModuleList([_Block()])
+    counts = SA.load_svdq_artifact(tmp_path, model, device=DEV, lane="int4")
+    assert counts["int4"] == 3 and counts["artifact"].lowrank_quant == scheme
+    blk = model.blocks[0]
+    gx = torch.Generator().manual_seed(33)
+    for i, mod in enumerate((blk.attn.to_q, blk.attn.to_k, blk.attn.to_v)):
+        assert isinstance(mod, SvdqW4A4Linear)
+        rows = slice(i * D, (i + 1) * D)
+        x = torch.randn(65, D, generator=gx).to(torch.bfloat16)
+        with torch.no_grad():
+            y = mod(x.to(DEV))
+        codes = logical["codes"][rows]
+        packed = (codes[:, 0::2] & 0xF) | ((codes[:, 1::2] & 0xF) << 4)
+        ref = O.w4a4_linear(bits16(x), bits16(logical["smooth"]), packed, logical["scales"][rows], bits16(down),
+                            bits16(up[rows]), bits16(logical["bias"][rows]))
+        check_output(y, ref, what=f"quantized low-rank ({scheme}) part {i}")
