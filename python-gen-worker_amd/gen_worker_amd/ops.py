@@ -687,13 +687,79 @@ def _(qa6, weight_fp6):
                          dtype=torch.int32)
 
 
+class _Fp6WeightCache:
+    """fp6 records of reference-schema weights (``wq_kn`` [K/2, N] + ``ws`` [N, K/64]), one entry per weight
+    tensor pair: an entry holds weak references to both tensors and their version counters, so it is used
+    only while both are alive and unmodified (an in-place update or a freed-and-reused address misses)."""
+
+    LIMIT = 256
+
+    def __init__(self) -> None:
+        import threading
+        from collections import OrderedDict
+
+        self._lock = threading.Lock()
+        self._entries: "OrderedDict[tuple, tuple]" = OrderedDict()
+        self.hits = self.misses = 0
+
+    def get(self, wq_kn: Tensor, ws: Tensor) -> Tensor:
+        import weakref
+
+        key = (wq_kn.data_ptr(), ws.data_ptr(), tuple(wq_kn.shape), tuple(ws.shape), str(wq_kn.device))
+        with self._lock:
+            hit = self._entries.get(key)
+            if hit is not None:
+                wref, sref, versions, rec = hit
+                if wref() is wq_kn and sref() is ws and versions == (wq_kn._version, ws._version):
+                    self._entries.move_to_end(key)
+                    self.hits += 1
+                    return rec
+        kh, n = int(wq_kn.shape[0]), int(wq_kn.shape[1])
+        w_nk = torch.empty(n, kh, dtype=torch.uint8, device=wq_kn.device)
+        nat.call("gwa_transpose_2d", nat.ptr(wq_kn), nat.ptr(w_nk), kh, n, 1, nat.stream_of(wq_kn))
+        rec = svdq_pack_weight_fp6(w_nk, ws)
+        with self._lock:
+            self._entries[key] = (weakref.ref(wq_kn), weakref.ref(ws), (wq_kn._version, ws._version), rec)
+            while len(self._entries) > self.LIMIT:
+                self._entries.popitem(last=False)
+            self.misses += 1
+        return rec
+
+    def clear(self) -> None:
+        with self._lock:
+            self._entries.clear()
+            self.hits = self.misses = 0
+
+
+_REF_WEIGHT_FP6 = _Fp6WeightCache()
+
+
+def reference_gemm_weight_cache() -> _Fp6WeightCache:
+    """The process's cache of fp6 weight records behind ``svdq_gemm_w4a4_lora``."""
+    return _REF_WEIGHT_FP6
+
+
 @torch.library.custom_op("cozy_gen_worker::svdq_gemm_w4a4_lora", mutates_args=())
 def svdq_gemm_w4a4_lora(qa: Tensor, sa: Tensor, wq_kn: Tensor, ws: Tensor, s2: Tensor, second: Tensor,
                         lora_act: Tensor, up: Tensor, bias: Optional[Tensor]) -> Tensor:
-    """The reference schema (``models/svdq_fused.py:379-389``): K-major weight ``wq_kn`` [K/2, N], bf16 out."""
-    _check_cuda("svdq_gemm_w4a4_lora", wq_kn=wq_kn)
-    _check_dtype("svdq_gemm_w4a4_lora", wq_kn, torch.uint8, what="wq_kn")
+    """The reference schema (``models/svdq_fused.py:379-389``): int4 nibble activations ``qa`` [M, K/2] with
+    fp16 scales ``sa`` [M, K/64], the K-major weight ``wq_kn`` [K/2, N] with ``ws`` [N, K/64], bf16 out.
+    With K % 128 == 0 it runs the fp6 lane: the activations repacked as fp6 records each call, the weight's
+    records built once per weight tensor (``reference_gemm_weight_cache``); otherwise the general lane."""
+    name = "svdq_gemm_w4a4_lora"
+    _check_cuda(name, wq_kn=wq_kn, qa=qa, sa=sa, ws=ws)
+    _check_dtype(name, wq_kn, torch.uint8, what="wq_kn")
+    _check_dtype(name, qa, torch.uint8, what="qa")
+    _check_dtype(name, sa, torch.float16, what="sa")
+    _check_dtype(name, ws, torch.float16, what="ws")
     kh, n = int(wq_kn.shape[0]), int(wq_kn.shape[1])
+    m, k = int(qa.shape[0]), 2 * kh
+    r = int(up.shape[1]) if up is not None else 0
+    if (k % FP6_STAGE == 0 and r in (0, 16, 32, 64, 128) and n % 16 == 0 and m > 0
+            and tuple(qa.shape) == (m, kh) and tuple(sa.shape) == (m, k // GROUP) and tuple(ws.shape) == (n, k // GROUP)):
+        w6 = _REF_WEIGHT_FP6.get(wq_kn, ws)
+        q6 = svdq_pack_weight_fp6(qa, sa)
+        return _fp6_impl(q6, w6, s2, second, lora_act if r else None, up if r else None, bias, torch.bfloat16, False)
     w_nk = torch.empty(n, kh, dtype=torch.uint8, device=wq_kn.device)
     nat.call("gwa_transpose_2d", nat.ptr(wq_kn), nat.ptr(w_nk), kh, n, 1, nat.stream_of(wq_kn))
     return _gemm_impl(qa, sa, w_nk, ws, s2, second, lora_act, up, bias, torch.bfloat16, False)

@@ -412,28 +412,86 @@ def test_w4a4_module_config1_full_size():
     print("config1", stats)
 
 
-def test_reference_schema_ops():
-    """cozy_gen_worker::svdq_gemm_w4a4_lora (K-major wq_kn) and svdq_epilogue_lora keep the reference schemas."""
-    g = np.random.default_rng(8)
-    m, n, k, r = 70, 128, 256, 32
-    x = _rand_act(m, k, seed=8)
+def _ref_schema_case(m, n, k, r, seed):
+    g = np.random.default_rng(seed)
+    x = _rand_act(m, k, seed=seed)
     qw, sw = O.quantize_weight_int4((g.standard_normal((n, k)) * 0.02).astype(np.float32))
     up = O.f32_to_bf16_bits((g.standard_normal((n, r)) * 0.02).astype(np.float32))
     la = O.f32_to_bf16_bits(g.standard_normal((m, r)).astype(np.float32))
     b = O.f32_to_bf16_bits((g.standard_normal(n) * 0.02).astype(np.float32))
     second = (g.random(n) + 0.5).astype(np.float32)
-    qa, sa = torch.ops.cozy_gen_worker.svdq_quant(_dev16(x), None, torch.ones((), device=DEV), False)
-    wq_kn = torch.from_numpy(np.ascontiguousarray(qw.T)).to(DEV)
-    s2 = torch.tensor(1.0, device=DEV)
-    y = torch.ops.cozy_gen_worker.svdq_gemm_w4a4_lora(
-        qa, sa, wq_kn, from_bits(sw.view(np.uint16), torch.float16, DEV), s2, torch.from_numpy(second).to(DEV),
-        _dev16(la), _dev16(up), _dev16(b))
+    return x, qw, sw, up, la, b, second
+
+
+def _ref_schema_oracle(x, qw, sw, up, la, b, second):
     wqa, wsa = O.quantize_act_int4(x)
     ref = (O.dequantize_int4(wqa, wsa) @ O.dequantize_int4(qw, sw).T) * second.astype(np.float64)
     ref += O.bf16_bits_to_f32(la).astype(np.float64) @ O.bf16_bits_to_f32(up).astype(np.float64).T
-    ref += O.bf16_bits_to_f32(b).astype(np.float64)
-    check_output(y, ref, what="svdq_gemm_w4a4_lora")
+    return ref + O.bf16_bits_to_f32(b).astype(np.float64)
 
+
+@pytest.mark.parametrize("m,n,k,r", [(70, 128, 256, 32), (70, 128, 320, 32), (513, 384, 1024, 16),
+                                     (4608, 3072, 3072, 32)])
+def test_reference_schema_gemm(m, n, k, r):
+    """cozy_gen_worker::svdq_gemm_w4a4_lora keeps the reference schema (nibble activations, K-major wq_kn):
+    against the oracle, and with K % 128 == 0 on the fp6 lane, bit-identical to svdq_w4a4_linear_fp6 on the
+    same operands (the general lane serves K % 128 != 0)."""
+    x, qw, sw, up, la, b, second = _ref_schema_case(m, n, k, r, seed=m + k)
+    cg = torch.ops.cozy_gen_worker
+    qa, sa = cg.svdq_quant(_dev16(x), None, torch.ones((), device=DEV), False)
+    wq_kn = torch.from_numpy(np.ascontiguousarray(qw.T)).to(DEV)
+    swd = from_bits(sw.view(np.uint16), torch.float16, DEV)
+    s2 = torch.tensor(1.0, device=DEV)
+    sec = torch.from_numpy(second).to(DEV)
+    y = cg.svdq_gemm_w4a4_lora(qa, sa, wq_kn, swd, s2, sec, _dev16(la), _dev16(up), _dev16(b))
+    rows = np.unique(np.r_[0:min(m, 64), m - min(m, 64):m])
+    check_output(y[rows], _ref_schema_oracle(x[rows], qw, sw, up, la[rows], b, second),
+                 what=f"svdq_gemm_w4a4_lora {m}x{n}x{k}")
+    if k % 128 == 0:
+        w6 = cg.svdq_pack_weight_fp6(torch.from_numpy(qw).to(DEV), swd)
+        q6 = cg.svdq_pack_weight_fp6(qa, sa)
+        y6 = cg.svdq_w4a4_linear_fp6(q6, w6, s2, sec, _dev16(la), _dev16(up), _dev16(b), torch.bfloat16, False)
+        assert torch.equal(y.view(torch.int16), y6.view(torch.int16))
+
+
+def test_reference_schema_weight_cache():
+    """The weight's fp6 records are built once per weight tensor: a second call hits, an in-place update of
+    wq_kn misses and the output follows the new weight, a different tensor with the same values misses."""
+    from gen_worker_amd import ops
+
+    cache = ops.reference_gemm_weight_cache()
+    m, n, k, r = 96, 256, 512, 32
+    x, qw, sw, up, la, b, second = _ref_schema_case(m, n, k, r, seed=5)
+    cg = torch.ops.cozy_gen_worker
+    qa, sa = cg.svdq_quant(_dev16(x), None, torch.ones((), device=DEV), False)
+    wq_kn = torch.from_numpy(np.ascontiguousarray(qw.T)).to(DEV)
+    swd = from_bits(sw.view(np.uint16), torch.float16, DEV)
+    args = lambda w: (qa, sa, w, swd, torch.tensor(1.0, device=DEV), torch.from_numpy(second).to(DEV),  # noqa
+                      _dev16(la), _dev16(up), _dev16(b))
+    h0, m0 = cache.hits, cache.misses
+    y1 = cg.svdq_gemm_w4a4_lora(*args(wq_kn))
+    y2 = cg.svdq_gemm_w4a4_lora(*args(wq_kn))
+    assert (cache.hits - h0, cache.misses - m0) == (1, 1)
+    assert torch.equal(y1, y2)
+    qw2 = qw.copy()
+    qw2[:, :8] ^= 0x77                        # new codes in the first 16 columns of every row
+    wq_kn.copy_(torch.from_numpy(np.ascontiguousarray(qw2.T)).to(DEV))
+    y3 = cg.svdq_gemm_w4a4_lora(*args(wq_kn))
+    assert cache.misses - m0 == 2
+    check_output(y3, _ref_schema_oracle(x, qw2, sw, up, la, b, second), what="after an in-place weight update")
+    cg.svdq_gemm_w4a4_lora(*args(wq_kn.clone()))
+    assert cache.misses - m0 == 3
+
+
+def test_reference_schema_epilogue():
+    """cozy_gen_worker::svdq_epilogue_lora keeps the reference schema."""
+    g = np.random.default_rng(8)
+    m, n, r = 70, 128, 32
+    up = O.f32_to_bf16_bits((g.standard_normal((n, r)) * 0.02).astype(np.float32))
+    la = O.f32_to_bf16_bits(g.standard_normal((m, r)).astype(np.float32))
+    b = O.f32_to_bf16_bits((g.standard_normal(n) * 0.02).astype(np.float32))
+    second = (g.random(n) + 0.5).astype(np.float32)
+    s2 = torch.tensor(1.0, device=DEV)
     y0 = O.f32_to_bf16_bits(g.standard_normal((m, n)).astype(np.float32))
     out = torch.ops.cozy_gen_worker.svdq_epilogue_lora(_dev16(y0), _dev16(la), _dev16(up), s2,
                                                        torch.from_numpy(second).to(DEV), _dev16(b))
