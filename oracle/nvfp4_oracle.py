@@ -32,15 +32,21 @@ BOUNDS = np.array([0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0], np.float32)
 SCALE_MIN, FP8_MAX, E2M1_MAX = np.float32(2.0 ** -9), np.float32(448.0), np.float32(6.0)
 
 
+E4M3_NAN = 0x7F   # float8_e4m3fn has no infinity; S.1111.111 is NaN
+
+
 def e4m3_value(code) -> np.ndarray:
-    """float8_e4m3fn bits (0..0x7E, sign bit ignored) -> float32."""
+    """float8_e4m3fn bits (sign bit ignored) -> float32; 0x7F is NaN."""
     c = np.asarray(code, np.int64) & 0x7F
     e, m = c >> 3, c & 7
-    return np.where(e == 0, m / 512.0, (1.0 + m / 8.0) * np.exp2(e - 7.0)).astype(np.float32)
+    with np.errstate(invalid="ignore"):
+        v = np.where(e == 0, m / 512.0, (1.0 + m / 8.0) * np.exp2(e - 7.0))
+    return np.where(c == E4M3_NAN, np.nan, v).astype(np.float32)
 
 
 def e4m3_rne(v) -> np.ndarray:
-    """fp32 in [2^-9, 448] -> e4m3fn bits, nearest value, ties to the even code."""
+    """fp32 in [2^-9, 448] -> e4m3fn bits, nearest value, ties to the even code; NaN -> 0x7F (torch's
+    ``.to(torch.float8_e4m3fn)`` of a NaN, what the reference's clamp passes through)."""
     v = np.asarray(v, np.float32)
     u = v.view(np.uint32).astype(np.int64)
     e = (u >> 23) - 127
@@ -49,18 +55,30 @@ def e4m3_rne(v) -> np.ndarray:
     rem = m & 0xFFFFF
     up = (rem > 0x80000) | ((rem == 0x80000) & ((r & 1) == 1))
     normal = ((e + 7) << 3) + r + up
-    sub = np.rint(v.astype(np.float64) * 512.0).astype(np.int64)  # exact scaling; np.rint is ties-to-even
-    return np.where(e < -6, sub, normal).astype(np.uint8)
+    with np.errstate(invalid="ignore"):
+        sub = np.rint(np.nan_to_num(v.astype(np.float64)) * 512.0).astype(np.int64)  # exact; ties to even
+    out = np.where(e < -6, sub, normal)
+    return np.where(np.isnan(v), E4M3_NAN, out).astype(np.uint8)
 
 
 def cast_e2m1(q) -> np.ndarray:
+    """``cast_e2m1``: the count of bounds below |q| (``searchsorted``), tie bumps, sign from q < 0; a NaN
+    sorts after every bound (code 7, sign clear: NaN < 0 is false)."""
     q = np.asarray(q, np.float32)
     a = np.abs(q)
     c = np.zeros(q.shape, np.int64)
     for b in BOUNDS:
         c += a > b
     c += (a == 0.75) | (a == 1.75) | (a == 2.5)
+    c = np.where(np.isnan(a), len(BOUNDS), c)
     return (c + 8 * (q < 0)).astype(np.uint8)
+
+
+def dynamic_s2(x: np.ndarray) -> np.float32:
+    """The forward's dynamic second-level scale (``models/w4a4.py:342-343``): max(max|x| / 2688, 1e-12);
+    a NaN anywhere makes it NaN (torch's amax and clamp propagate NaN)."""
+    amax = np.float32(np.abs(np.asarray(x, np.float32)).max())
+    return np.float32(np.maximum(np.float32(amax / np.float32(2688.0)), np.float32(1e-12)))
 
 
 def pack_e2m1(codes: np.ndarray) -> np.ndarray:

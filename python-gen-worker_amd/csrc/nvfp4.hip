@@ -52,17 +52,26 @@ __device__ __forceinline__ uint32_t e4m3_rne(float v) {
   return ((uint32_t)(e + 7) << 3) + r;  // r == 8 carries into the exponent
 }
 
+constexpr uint32_t kE4m3Nan = 0x7Fu;  // e4m3fn has no infinity: S.1111.111 is NaN
+
 __device__ __forceinline__ float e4m3_value(uint32_t c) {
+  if ((c & 0x7Fu) == kE4m3Nan) return __uint_as_float(0x7FC00000u);
   const uint32_t ex = (c >> 3) & 15u, m = c & 7u;
   return ex == 0 ? (float)m * (1.0f / 512.0f) : __uint_as_float(((ex + 120u) << 23) | (m << 20));
 }
 
+// a NaN sorts past every bound (code 7, sign clear), as the reference's searchsorted places it
 __device__ __forceinline__ uint32_t e2m1_code(float q) {
   const float a = fabsf(q);
+  if (a != a) return 7u;
   uint32_t c = (a > 0.25f) + (a > 0.75f) + (a > 1.25f) + (a > 1.75f) + (a > 2.5f) + (a > 3.5f) + (a > 5.0f);
   c += (a == 0.75f) | (a == 1.75f) | (a == 2.5f);
   return c | (q < 0.0f ? 8u : 0u);
 }
+
+// max of |x| over a set as the bit pattern of a non-negative float: unsigned order is value order, and a NaN
+// (any payload, sign cleared) sits above infinity, so it propagates like the reference's amax
+__device__ __forceinline__ uint32_t abs_bits(float v) { return __float_as_uint(v) & 0x7FFFFFFFu; }
 
 __device__ __forceinline__ int64_t blocked_index(int64_t r, int64_t c, int64_t ncb) {
   return ((r >> 7) * ncb + (c >> 2)) * 512 + (r & 31) * 16 + ((r & 127) >> 5) * 4 + (c & 3);
@@ -75,40 +84,41 @@ constexpr int NV_MAX_PARTS = 1024;
 
 __global__ __launch_bounds__(NV_THREADS) void nvfp4_absmax_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                                                                   int64_t M, int K, float* __restrict__ part) {
-  __shared__ float red[NV_THREADS / 64];
+  __shared__ uint32_t red[NV_THREADS / 64];
   const int64_t chunks = M * (K / 8);
-  float mx = 0.0f;
+  uint32_t mx = 0u;
   for (int64_t i = (int64_t)blockIdx.x * NV_THREADS + threadIdx.x; i < chunks; i += (int64_t)gridDim.x * NV_THREADS) {
     const int64_t row = i / (K / 8);
     const int col = (int)(i - row * (K / 8)) * 8;
     const v4i w = *(const v4i*)(x + row * ldx + col);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) mx = fmaxf(mx, fmaxf(fabsf(bf16_lo((uint32_t)w[j])), fabsf(bf16_hi((uint32_t)w[j]))));
+    for (int j = 0; j < 4; ++j) mx = max(mx, max(abs_bits(bf16_lo((uint32_t)w[j])), abs_bits(bf16_hi((uint32_t)w[j]))));
   }
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  for (int o = 32; o > 0; o >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, o));
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
   __syncthreads();
   if (threadIdx.x == 0) {
-    float m = red[0];
-    for (int w = 1; w < NV_THREADS / 64; ++w) m = fmaxf(m, red[w]);
-    part[blockIdx.x] = m;
+    uint32_t m = red[0];
+    for (int w = 1; w < NV_THREADS / 64; ++w) m = max(m, red[w]);
+    part[blockIdx.x] = __uint_as_float(m);
   }
 }
 
 // s2 from the parts (every thread of the workgroup gets it)
 __device__ __forceinline__ float nvfp4_dynamic_s2(const float* __restrict__ part, int nparts) {
-  __shared__ float red[NV_THREADS / 64];
-  float mx = 0.0f;
-  for (int i = threadIdx.x; i < nparts; i += NV_THREADS) mx = fmaxf(mx, part[i]);
+  __shared__ uint32_t red[NV_THREADS / 64];
+  uint32_t mx = 0u;
+  for (int i = threadIdx.x; i < nparts; i += NV_THREADS) mx = max(mx, abs_bits(part[i]));
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  for (int o = 32; o > 0; o >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, o));
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
   __syncthreads();
-  float m = red[0];
+  uint32_t m = red[0];
 #pragma unroll
-  for (int w = 1; w < NV_THREADS / 64; ++w) m = fmaxf(m, red[w]);
-  return fmaxf(m / 2688.0f, 1e-12f);
+  for (int w = 1; w < NV_THREADS / 64; ++w) m = max(m, red[w]);
+  const float s = __uint_as_float(m) / 2688.0f;
+  return s != s ? s : fmaxf(s, 1e-12f);  // the reference's clamp keeps a NaN
 }
 
 // Two lanes per block (lane pair 2p, 2p + 1 holds its elements 0-7 and 8-15), so every load and store of a
@@ -136,13 +146,13 @@ __global__ __launch_bounds__(NV_THREADS) void nvfp4_quant_act_kernel(const uint1
     v[2 * j] = bf16_lo((uint32_t)w[j]);
     v[2 * j + 1] = bf16_hi((uint32_t)w[j]);
   }
-  float bmax = 0.0f;
+  uint32_t mb = 0u;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) bmax = fmaxf(bmax, fabsf(v[i]));
-  bmax = fmaxf(bmax, __shfl_xor(bmax, 1));
-  float tq = bmax / (6.0f * s2);
-  tq = fminf(fmaxf(tq, 1.0f / 512.0f), 448.0f);
-  const uint32_t sc = e4m3_rne(tq);
+  for (int i = 0; i < 8; ++i) mb = max(mb, abs_bits(v[i]));
+  mb = max(mb, (uint32_t)__shfl_xor((int)mb, 1));
+  const float tq = __uint_as_float(mb) / (6.0f * s2);
+  // a NaN block maximum (or s2) stays NaN through the reference's clamp and casts to the NaN code
+  const uint32_t sc = tq != tq ? kE4m3Nan : e4m3_rne(fminf(fmaxf(tq, 1.0f / 512.0f), 448.0f));
   const float sa = e4m3_value(sc);
   const float den = sa * s2;
   uint32_t codes = 0;

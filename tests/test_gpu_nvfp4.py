@@ -97,6 +97,30 @@ def test_quant_act_edge_values():
     assert np.array_equal(xdq.float().cpu().numpy().view(np.uint32), N.dequantize(oq, osc).view(np.uint32))
 
 
+def test_quant_act_non_finite():
+    """NaN and infinite inputs take the reference's values: a block holding a NaN gets the e4m3 NaN scale
+    (0x7F) and code 7 everywhere, an infinity clamps its block scale to 448 and takes code 7 with its sign;
+    with the dynamic second-level scale one NaN makes s2 NaN and every block NaN."""
+    x = _act(4, 64, seed=3)
+    x[0, 5] = np.nan
+    x[1, 17] = np.inf
+    x[2, 40] = -np.inf
+    s2v = np.float32(0.01)
+    q, sc, xdq = torch.ops.cozy_gen_worker.nvfp4_quant_act(_bf16(x), torch.tensor(s2v, device=DEV), False, True)
+    oq, osc = N.quantize_activation(x, s2v)
+    assert np.array_equal(q.cpu().numpy(), oq) and np.array_equal(sc.cpu().numpy(), osc)
+    assert osc[0, 0] == N.E4M3_NAN and osc[1, 1] == 0x7E and osc[2, 2] == 0x7E
+    got, want = xdq.float().cpu().numpy(), N.dequantize(oq, osc)
+    assert np.array_equal(np.isnan(got), np.isnan(want)) and np.isnan(got[0, :16]).all()
+    fin = ~np.isnan(want)
+    assert np.array_equal(got[fin].view(np.uint32), want[fin].view(np.uint32))
+    q2, sc2, xdq2, s2d = torch.ops.cozy_gen_worker.nvfp4_quant_act_dyn(_bf16(x), False, True)
+    assert np.isnan(s2d.item()) and np.isnan(N.dynamic_s2(x))
+    oq2, osc2 = N.quantize_activation(x, N.dynamic_s2(x))
+    assert np.array_equal(q2.cpu().numpy(), oq2) and np.array_equal(sc2.cpu().numpy(), osc2)
+    assert (osc2 == N.E4M3_NAN).all() and torch.isnan(xdq2.float()).all()
+
+
 def test_reference_op_contract():
     """quant_nvfp4_act returns (codes, blocked e4m3 scales), the reference op's outputs."""
     x = _act(333, 3072, seed=5)

@@ -171,3 +171,30 @@ def test_nvfp4_fake_impls():
         w = torch.ops.cozy_gen_worker.nvfp4_dequant(torch.empty(64, 96, dtype=torch.uint8),
                                                     torch.empty(64, 12, dtype=torch.uint8), False)
         assert w.shape == (64, 192) and w.dtype == torch.bfloat16
+
+
+def test_nan_handling_matches_torch_ops():
+    """Non-finite inputs follow the reference's torch ops: amax and clamp keep a NaN, the e4m3 cast of a NaN
+    is 0x7F, searchsorted puts a NaN past every e2m1 bound (code 7, sign clear), an infinite block maximum
+    clamps to 448 and its infinity takes code 7 with its sign."""
+    assert int(torch.tensor([float("nan")]).to(torch.float8_e4m3fn).view(torch.uint8)[0]) == N.E4M3_NAN
+    assert int(N.e4m3_rne(np.array([np.nan], np.float32))[0]) == N.E4M3_NAN
+    assert np.isnan(N.e4m3_value(N.E4M3_NAN)) and not np.isnan(N.e4m3_value(0x7E))
+    bounds = torch.tensor(N.BOUNDS)
+    for v in (float("nan"), -float("nan"), float("inf"), -float("inf")):
+        t = torch.tensor([v], dtype=torch.float32)
+        want = int(torch.searchsorted(bounds, t.abs())[0]) + 8 * int(t[0] < 0)
+        assert int(N.cast_e2m1(np.array([v], np.float32))[0]) == want
+    x = np.ones((2, 32), np.float32)
+    x[0, 3] = np.nan                       # block (0, 0) holds a NaN
+    x[1, 20] = np.inf                      # block (1, 1) holds an infinity
+    q, sc = N.quantize_activation(x, 1.0)
+    vals = N.unpack_e2m1(q)                # e2m1 values of the codes
+    assert sc[0, 0] == N.E4M3_NAN and (vals[0, :16] == 6.0).all()          # every quotient NaN -> code 7
+    assert (vals[1, 16:] == np.where(x[1, 16:] == np.inf, 6.0, vals[1, 16:])).all() and vals[1, 20] == 6.0
+    xt = torch.from_numpy(x)
+    bmax = xt.reshape(2, 2, 16).abs().amax(-1)
+    sa = (bmax / 6.0).clamp(min=2.0 ** -9, max=448.0).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(sc, sa)
+    assert np.isnan(N.dynamic_s2(x)) and N.dynamic_s2(np.ones((1, 16), np.float32)) == np.float32(1.0 / 2688.0)
+    assert N.dynamic_s2(np.zeros((1, 16), np.float32)) == np.float32(1e-12)
