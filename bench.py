@@ -1,8 +1,9 @@
 """Benchmark of the SVDQuant W4A4 linear hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-    python bench.py --only {step,gemm,quant,copy,awq} [--iters N] (profiling driver)
-    python bench.py --workload {mlp,qkv,dit,mod,nvfp4}            (configs 2-4, modulation layers, nvfp4 lane)
+    python bench.py --only {step,gemm,quant,copy,awq,w8a8,w8a8_gemm} [--iters N] (profiling driver)
+    python bench.py --workload {mlp,qkv,dit,mod,nvfp4,w8a8}  (configs 2-4, modulation layers, nvfp4 lane,
+                                                              the int8 GEMM sweep)
 
 A step is one pass of the hot path over one batch of synthetic input: the
 config-1 SVDQuant W4A4 linear (M = 4096 image + 512 text tokens = 4608,
@@ -317,6 +318,75 @@ def bench_qkv(args) -> int:
     return 0
 
 
+def bench_w8a8(args) -> int:
+    """The W8A8 int8 GEMM alone (``gwa_w8a8_gemm``: per-token x per-channel scales, bf16 bias and output) at
+    4096^3, the config-1 shape and config 3's QKV at 4608 and 16384 tokens, with each output tile forced and
+    with the tile choice, against torch's bf16 linear on the same shape; each timed over ``--steps`` calls in
+    one HIP graph."""
+    import torch
+
+    import gen_worker_amd  # noqa: F401
+    from gen_worker_amd import _native
+    from gen_worker_amd.svdq import w4a4_int_ops
+
+    lib = _native.load()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    cg = torch.ops.cozy_gen_worker
+    g = torch.Generator(device=dev).manual_seed(3)
+    rows = []
+    for m, n, k in ((4096, 4096, 4096), (4608, 3072, 3072), (4608, 9216, 3072), (16384, 9216, 3072)):
+        qa = torch.randint(-127, 128, (m, k), dtype=torch.int8, device=dev, generator=g)
+        qw = torch.randint(-127, 128, (n, k), dtype=torch.int8, device=dev, generator=g)
+        sa = torch.rand(m, device=dev, generator=g) * 1e-3
+        sw = torch.rand(n, device=dev, generator=g) * 1e-3
+        bias = torch.randn(n, device=dev, generator=g).to(torch.bfloat16)
+        xd = torch.randn(m, k, device=dev, generator=g).to(torch.bfloat16)
+        wd = torch.randn(n, k, device=dev, generator=g).to(torch.bfloat16)
+        ops_ = w4a4_int_ops(m, n, k)
+        row = {"M": m, "N": n, "K": k, "tile": int(lib.gwa_w8a8_gemm_tile(m, n, k))}
+        qwt = qw.t()  # torch._int_mm's [K, N] operand, column-major as hipBLASLt takes it
+        variants = {"tile_128x128": 0, "tile_256x256": 1, "chosen": -1, "bf16": None, "torch_int_mm": "int_mm"}
+        for name, tile in variants.items():
+            if tile is None:
+                fn = lambda: torch.nn.functional.linear(xd, wd, bias)  # noqa: E731
+            elif tile == "int_mm":
+                # the vendor library's int8 GEMM (int32 out, no epilogue), for reference only
+                fn = lambda: torch._int_mm(qa, qwt)  # noqa: E731
+                try:
+                    fn()
+                    torch.cuda.synchronize()
+                except RuntimeError as e:
+                    row[name] = {"unavailable": str(e).splitlines()[0][:120]}
+                    continue
+            else:
+                lib.gwa_w8a8_gemm_force_tile(tile)
+                fn = lambda: cg.w8a8_scaled_mm(qa, qw, sa, sw, bias, torch.bfloat16)  # noqa: E731
+            for _ in range(args.warmup):
+                fn()
+            torch.cuda.synchronize()
+            ms = graph_time_ms(torch, fn, args.steps)
+            row[name] = {"us": round(ms * 1e3, 2), "TOPS": round(ops_ / (ms * 1e-3) / 1e12, 1)}
+        lib.gwa_w8a8_gemm_force_tile(-1)
+        row["vs_bf16"] = round(row["bf16"]["us"] / row["chosen"]["us"], 3)
+        row["pct_int8_peak"] = round(100 * row["chosen"]["TOPS"] / INT8_PEAK_TOPS, 1)
+        log(f"bench: w8a8 {row}")
+        rows.append(row)
+        del qa, qw, xd, wd
+    big = next(rw for rw in rows if rw["M"] == 4608 and rw["N"] == 9216)
+    out = {"metric": "W8A8 int8 GEMM TOPS (gwa_w8a8_gemm, per-token x per-channel scales, bf16 bias and out)",
+           "value": big["chosen"]["TOPS"], "unit": "TOPS", "n_gpus": 1, "steps": args.steps,
+           "warmup": args.warmup, "ms_per_step": round(big["chosen"]["us"] / 1e3, 5), "higher_is_better": True,
+           "scaling": "weak", "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+           "config": {"workload": "w8a8_gemm_sweep", "value_at": "QKV M=4608, N=9216, K=3072",
+                      "timing": "K calls in one HIP graph replay, after >= 40 ms of untimed replays"},
+           "roofline": {"bound": "mfma", "achieved": big["chosen"]["TOPS"], "peak": INT8_PEAK_TOPS, "unit": "TOPS",
+                        "frac": round(big["chosen"]["TOPS"] / INT8_PEAK_TOPS, 4)},
+           "rows": rows}
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def bench_mod(args) -> int:
     """The adaLN modulation linears of the config-4 DiT (one token, K=3072): the AWQ W4A16 GEMV
     (``awq_w4a16_mm``) at the dual-block (N=18432) and single-block (N=9216) shapes, M = 1 and 2, against
@@ -449,16 +519,18 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-rows", type=int, default=512, help="rows of the bounded CPU sample")
-    ap.add_argument("--only", choices=("step", "gemm", "quant", "copy", "awq", "w8a8"), default=None)
+    ap.add_argument("--only", choices=("step", "gemm", "quant", "copy", "awq", "w8a8", "w8a8_gemm"), default=None)
     ap.add_argument("--iters", type=int, default=5)
     ap.add_argument("--tile", type=int, default=-1,
-                    help="with --only gemm/step: force the fp6 GEMM's output tile (GWA_FP6_TILE_*; -1: the model's)")
-    ap.add_argument("--workload", choices=("c1", "mlp", "qkv", "dit", "mod", "nvfp4"), default="c1",
+                    help="with --only gemm/step: force the fp6 GEMM's output tile (GWA_FP6_TILE_*; -1: the model's); "
+                         "with --only w8a8_gemm: the int8 GEMM's (GWA_W8A8_TILE_*)")
+    ap.add_argument("--workload", choices=("c1", "mlp", "qkv", "dit", "mod", "nvfp4", "w8a8"), default="c1",
                     help="c1: the config-1 linear (the default bench line); mlp: config 2, fc1 -> GELU -> fc2 "
                          "(fused, unfused, bf16); qkv: config 3, the QKV sweep over M and output dtype (W4A4, "
                          "W8A8, bf16); dit: the config-4 Flux-shaped DiT step, W4A4 vs the same model with bf16 "
                          "GEMMs; mod: the DiT's one-token modulation linears (AWQ W4A16 GEMV vs W4A4 vs bf16); "
-                         "nvfp4: the nvfp4 compatibility lane at the config-1 shape")
+                         "nvfp4: the nvfp4 compatibility lane at the config-1 shape; w8a8: the int8 GEMM alone "
+                         "(both tiles and the chosen one vs bf16) at 4096^3, config 1 and QKV")
     ap.add_argument("--modulation", choices=("w4a4", "awq"), default="w4a4",
                     help="the DiT's one-token adaLN modulation linears: W4A4 like every other linear (config 4 "
                          "as stated), or AWQ W4A16 as an svdq checkpoint stores them")
@@ -477,7 +549,7 @@ def main() -> int:
             print("bench.py measures one GPU only", file=sys.stderr)
             return 2
         return {"dit": bench_dit, "mlp": bench_mlp, "qkv": bench_qkv, "mod": bench_mod,
-                "nvfp4": bench_nvfp4}[args.workload](args)
+                "nvfp4": bench_nvfp4, "w8a8": bench_w8a8}[args.workload](args)
 
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}): this build's path is a single-GPU "
@@ -518,11 +590,23 @@ def main() -> int:
         return gemm(q, l)
 
     if args.only is not None:
-        if args.tile >= 0:
+        if args.tile >= 0 and args.only == "w8a8_gemm":
+            _native.load().gwa_w8a8_gemm_force_tile(args.tile)
+        elif args.tile >= 0:
             _native.load().gwa_svdq_gemm_w4a4_fp6_force_tile(args.tile)
         src = torch.empty(COPY_BYTES // 2, dtype=torch.bfloat16, device=dev) if args.only == "copy" else None
         dst = torch.empty_like(src) if src is not None else None
-        if args.only == "w8a8":
+        if args.only == "w8a8_gemm":
+            # the int8 GEMM alone at config 3's QKV shape (M=4608, N=9216, K=3072), the tile it chooses
+            m8, n8 = m, synthetic.C3["n"]
+            g8 = torch.Generator(device=dev).manual_seed(3)
+            qa8 = torch.randint(-127, 128, (m8, k), dtype=torch.int8, device=dev, generator=g8)
+            qw8 = torch.randint(-127, 128, (n8, k), dtype=torch.int8, device=dev, generator=g8)
+            sa8, sw8 = torch.rand(m8, device=dev) * 1e-3, torch.rand(n8, device=dev) * 1e-3
+            b8 = torch.randn(n8, device=dev).to(torch.bfloat16)
+            cg8 = torch.ops.cozy_gen_worker
+            fn = lambda: cg8.w8a8_scaled_mm(qa8, qw8, sa8, sw8, b8, torch.bfloat16)  # noqa: E731
+        elif args.only == "w8a8":
             # the W8A8 linear (per-token quant + int8 GEMM) at the config-1 shape, for profiling
             from gen_worker_amd.w8a8 import build_int8_linear
 

@@ -366,6 +366,19 @@ int gwa_w8a8_gemm(const int8_t* qa, const int8_t* qw, const float* sa, int64_t s
                   const void* bias, int bias_dtype, void* out, int out_dtype,
                   int64_t M, int64_t N, int64_t K, void* stream);
 
+/* The output tile gwa_w8a8_gemm uses for this shape (GWA_W8A8_TILE_*; -1 for
+ * an empty shape): 256 x 256 tiles (direct-to-LDS copies, 512 threads; K a
+ * multiple of 128) when their rounds over the CUs finish before those of
+ * 128 x 128 tiles, else 128 x 128. No reference counterpart: torch._scaled_mm
+ * picks its own kernel. */
+enum { GWA_W8A8_TILE_128x128 = 0, GWA_W8A8_TILE_256x256 = 1 };
+int gwa_w8a8_gemm_tile(int64_t M, int64_t N, int64_t K);
+
+/* Test and tuning hook: every later gwa_w8a8_gemm uses this tile (-1
+ * restores the choice above; K % 128 != 0 or K >= 2^23 always takes
+ * 128 x 128). Process-wide; returns the previous setting. */
+int gwa_w8a8_gemm_force_tile(int tile);
+
 /* AWQ W4A16 linear (the M = 1 adaLN modulation layers).
  * Replaces cozy_gen_worker::awq_w4a16_mm (models/svdq_awq_packed.py:48-115;
  * schema "(Tensor x2, Tensor weight, Tensor wscales, Tensor wzeros, Tensor? bias) -> Tensor"):

@@ -7,7 +7,9 @@
 // Same orientation as the W4A4 kernel: A operand = weight rows (n), B operand
 // = activation rows (m); accumulator block D[n][m], lane l holds m = l % 32
 // and n = 8*(v/4) + 4*(l/32) + (v%4).
-#include "gwa_common.h"
+#include <atomic>
+
+#include "fp6_gemm_common.h"
 
 namespace {
 
@@ -127,7 +129,211 @@ __global__ __launch_bounds__(256) void w8a8_gemm_kernel(const int8_t* __restrict
   }
 }
 
+// ---------------------------------------------------------------------------
+// 256 x 256 tiles for grids that fill the GPU. Operand delivery is the W4A4 kernels': direct-to-LDS 1 KB
+// copies (no staging registers, no ds_write), here into two stage buffers of 128 K-bytes of 256 activation
+// rows and 256 weight rows (64 KB each), the next stage's copies in flight while a stage is consumed. A copy
+// reads whole 128-byte lines: lane l of a copy takes 16 bytes of row 8 q + l / 8 (eight rows per copy), so
+// rows past M or N read zeros through the range-checked per-lane offset and the stage advance rides in the
+// scalar offset. In LDS the 16-byte chunk c of row r sits at slot c ^ ((r / 2) % 8) of the row, so the 16
+// rows a quarter of a read instruction touches fill all banks. 8 waves form a 2 (n) x 4 (m) grid of
+// 128 x 64 wave tiles: per k-step of 32 bytes, 6 operand reads feed 8 int8 MFMAs that accumulate in place.
+// The loop is software-pipelined: the reads of k-step s + 1 are issued between the MFMAs of k-step s, and
+// at a stage boundary the wave waits for its copies, meets the barrier, issues the copies two stages ahead
+// into the buffer just drained and reads the next stage's first k-step under the last k-step's MFMAs.
+// ---------------------------------------------------------------------------
+constexpr int L_TM = 256, L_TN = 256, L_KS = 128;  // tile rows (m, n); K bytes per stage
+constexpr int kCus = 256;                          // MI355X compute units
+constexpr int L_REG = 256 * L_KS;                  // one operand region of a stage buffer: 32 KB
+constexpr int L_STAGE = 2 * L_REG;                 // activation region, then weight region
+constexpr int L_RUNS = L_REG / 1024;               // 1 KB copies per operand and stage: 32
+constexpr int L_SLOTS = L_STAGE / 1024 / NWAVES;   // copies per wave and stage: 8 (4 activation, 4 weight)
+static_assert(2 * L_STAGE <= kLdsBytes && L_SLOTS * NWAVES * 1024 == L_STAGE, "stage layout");
+
+__device__ __forceinline__ int l_swz(int r) { return (r >> 1) & 7; }
+
+// pins the order of one k-step: MFMA and operand read alternate (6 reads under 8 MFMAs)
+__device__ __forceinline__ void pin_kstep() {
+#pragma unroll
+  for (int i = 0; i < 6; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+  }
+  __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+template <int BIAS_DT, bool OUT_F16>
+__global__ __launch_bounds__(NTHREADS, 1) void w8a8_gemm_lds_kernel(const int8_t* __restrict__ qa,
+                                                                    const int8_t* __restrict__ qw,
+                                                                    const float* __restrict__ sa,
+                                                                    const float* __restrict__ sw,
+                                                                    const void* __restrict__ bias,
+                                                                    uint16_t* __restrict__ out, int M, int N, int K,
+                                                                    int sa_row) {
+  __shared__ __attribute__((aligned(16))) uint8_t g_lds[2 * L_STAGE];
+  const int tid = threadIdx.x;
+  const int tiles_n = (N + L_TN - 1) / L_TN, tiles_m = (M + L_TM - 1) / L_TM;
+  int tm, tn;
+  if (!xcd_tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn)) return;  // whole workgroup, before any barrier
+  const int m0 = tm * L_TM, n0 = tn * L_TN;
+  const int nst = K / L_KS;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int wn = wave & 1, wm = wave >> 1;
+  const int r32 = lane & 31, h = lane >> 5;
+
+  // descriptors over this tile's rows only (256 K < 2^31 bytes, checked on the host, so kOOB lies past them)
+  const v4i xbuf = raw_rsrc(qa + (int64_t)m0 * K, (uint32_t)(min(M - m0, L_TM) * K));
+  const v4i wbuf = raw_rsrc(qw + (int64_t)n0 * K, (uint32_t)(min(N - n0, L_TN) * K));
+  // copy j of this wave is run q = wave + 8 j of a stage: runs 0..31 carry activation rows, 32..63 weight
+  // rows (j < 4: activations); lane -> row 8 (q % 32) + lane / 8 of the region, LDS slot lane % 8
+  uint32_t voff[L_SLOTS];
+  uint32_t ldst[L_SLOTS];
+#pragma unroll
+  for (int j = 0; j < L_SLOTS; ++j) {
+    const int q = wave + NWAVES * j;
+    const bool isx = j < L_SLOTS / 2;
+    const int row = 8 * (q % L_RUNS) + (lane >> 3);
+    const int chunk = (lane & 7) ^ l_swz(row);
+    const bool live = (isx ? m0 : n0) + row < (isx ? M : N);
+    voff[j] = live ? (uint32_t)(row * K + 16 * chunk) : kOOB;
+    ldst[j] = (uint32_t)(uintptr_t)(g_lds + (isx ? 0 : L_REG) + (q % L_RUNS) * 1024);
+  }
+  auto issue = [&](int u, int st) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < L_SLOTS; ++j)
+      dma16(j < L_SLOTS / 2 ? xbuf : wbuf, ldst[j] + (uint32_t)(u * L_STAGE), voff[j], (uint32_t)(st * L_KS));
+  };
+
+  v16i acc[4][2];
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b) acc[a][b] = (v16i){};
+  // operand rows of this lane: weight block bn row 128 wn + 32 bn + r32, activation block bm row 64 wm + 32 bm + r32
+  int wrow[4], xrow[2];
+#pragma unroll
+  for (int bn = 0; bn < 4; ++bn) wrow[bn] = 128 * wn + 32 * bn + r32;
+#pragma unroll
+  for (int bm = 0; bm < 2; ++bm) xrow[bm] = 64 * wm + 32 * bm + r32;
+  // k-step ks (32 bytes) of a stage buffer: this lane's half h of each operand row
+  auto read_ops = [&](const uint8_t* buf, int ks, v4i (&a)[4], v4i (&b)[2]) __attribute__((always_inline)) {
+    const int c = 2 * ks + h;
+#pragma unroll
+    for (int bn = 0; bn < 4; ++bn) a[bn] = *(const v4i*)(buf + L_REG + wrow[bn] * L_KS + 16 * (c ^ l_swz(wrow[bn])));
+#pragma unroll
+    for (int bm = 0; bm < 2; ++bm) b[bm] = *(const v4i*)(buf + xrow[bm] * L_KS + 16 * (c ^ l_swz(xrow[bm])));
+  };
+  auto mma = [&](const v4i (&a)[4], const v4i (&b)[2]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int bn = 0; bn < 4; ++bn)
+#pragma unroll
+      for (int bm = 0; bm < 2; ++bm)
+        acc[bn][bm] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[bn], b[bm], acc[bn][bm], 0, 0, 0);
+  };
+  // k-steps 1..3 of a stage, each read under the previous k-step's MFMAs; leaves k-step 3 in (a1, b1)
+  v4i a0[4], b0[2], a1[4], b1[2];
+  auto stage_body = [&](const uint8_t* buf) __attribute__((always_inline)) {
+    read_ops(buf, 1, a1, b1);
+    mma(a0, b0);
+    pin_kstep();
+    read_ops(buf, 2, a0, b0);
+    mma(a1, b1);
+    pin_kstep();
+    read_ops(buf, 3, a1, b1);
+    mma(a0, b0);
+    pin_kstep();
+  };
+
+  issue(0, 0);
+  wait_vm_lgkm0<0>();
+  barrier_lds();
+  if (1 < nst) issue(1, 1);
+  read_ops(g_lds, 0, a0, b0);
+  for (int st = 0; st < nst - 1; ++st) {
+    stage_body(g_lds + (st & 1) * L_STAGE);
+    // stage st + 1's copies (this wave's: the only ones in flight) and this wave's reads of stage st are
+    // complete; after the barrier everyone's are, so buffer st & 1 takes the copies of stage st + 2
+    wait_vm_lgkm0<0>();
+    barrier_lds();
+    if (st + 2 < nst) issue(st & 1, st + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    read_ops(g_lds + ((st + 1) & 1) * L_STAGE, 0, a0, b0);
+    mma(a1, b1);
+    pin_kstep();
+  }
+  stage_body(g_lds + ((nst - 1) & 1) * L_STAGE);
+  mma(a1, b1);
+
+#pragma unroll
+  for (int bn = 0; bn < 4; ++bn) {
+    const int nb = n0 + 128 * wn + 32 * bn;
+#pragma unroll
+    for (int bm = 0; bm < 2; ++bm) {
+      const int m = m0 + 64 * wm + 32 * bm + r32;
+      if (m >= M) continue;
+      const float am = sa[sa_row ? m : 0];
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd) {
+        const int n = nb + 8 * qd + 4 * h;
+        if (n >= N) continue;
+        float o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float y = (float)acc[bn][bm][4 * qd + e] * am * sw[n + e];
+          if (BIAS_DT == GWA_DT_F32) y += ((const float*)bias)[n + e];
+          if (BIAS_DT == GWA_DT_BF16) y += bf16_to_f32(((const uint16_t*)bias)[n + e]);
+          if (BIAS_DT == GWA_DT_F16) y += f16_bits_to_f32(((const uint16_t*)bias)[n + e]);
+          o[e] = y;
+        }
+        uint2 pk;
+        if (OUT_F16) {
+          pk.x = pack_f16x2(o[0], o[1]);
+          pk.y = pack_f16x2(o[2], o[3]);
+        } else {
+          pk.x = pack_bf16x2(o[0], o[1]);
+          pk.y = pack_bf16x2(o[2], o[3]);
+        }
+        *(uint2*)(out + (int64_t)m * N + n) = pk;
+      }
+    }
+  }
+}
+
+std::atomic<int> g_w8a8_force_tile{-1};  // test / tuning hook (gwa_w8a8_gemm_force_tile)
+
+using W8Kernel = void (*)(const int8_t*, const int8_t*, const float*, const float*, const void*, uint16_t*, int, int,
+                          int, int);
+
+template <int BD>
+W8Kernel pick_kernel(int tile, bool f16) {
+  if (tile == GWA_W8A8_TILE_256x256) return f16 ? w8a8_gemm_lds_kernel<BD, true> : w8a8_gemm_lds_kernel<BD, false>;
+  return f16 ? w8a8_gemm_kernel<BD, true> : w8a8_gemm_kernel<BD, false>;
+}
+
+// 256 x 256 tiles when their rounds over the CUs finish first: a 256 x 256 tile takes about three times as
+// long as a 128 x 128 one (four times the work at a higher rate), so the choice compares ceil(tiles / CUs)
+// rounds of each; 128-byte stages need K % 128 == 0, and the per-tile descriptors 256 K < 2^31
+int w8a8_tile(int64_t M, int64_t N, int64_t K) {
+  if (K % L_KS || K >= (1ll << 23)) return GWA_W8A8_TILE_128x128;
+  const int forced = g_w8a8_force_tile.load(std::memory_order_relaxed);
+  if (forced >= 0) return forced;
+  const int64_t big = ((M + L_TM - 1) / L_TM) * ((N + L_TN - 1) / L_TN);
+  const int64_t small = ((M + TILE - 1) / TILE) * ((N + TILE - 1) / TILE);
+  const int64_t rounds_big = (big + kCus - 1) / kCus, rounds_small = (small + kCus - 1) / kCus;
+  return 3 * rounds_big < rounds_small ? GWA_W8A8_TILE_256x256 : GWA_W8A8_TILE_128x128;
+}
+
 }  // namespace
+
+extern "C" int gwa_w8a8_gemm_tile(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || N <= 0 || K <= 0) return -1;
+  return w8a8_tile(M, N, K);
+}
+
+extern "C" int gwa_w8a8_gemm_force_tile(int tile) {
+  return g_w8a8_force_tile.exchange(tile == GWA_W8A8_TILE_128x128 || tile == GWA_W8A8_TILE_256x256 ? tile : -1);
+}
 
 extern "C" int gwa_w8a8_gemm(const int8_t* qa, const int8_t* qw, const float* sa, int64_t sa_numel,
                              const float* sw, const void* bias, int bias_dtype, void* out, int out_dtype, int64_t M,
@@ -151,19 +357,20 @@ extern "C" int gwa_w8a8_gemm(const int8_t* qa, const int8_t* qw, const float* sa
   const int64_t tiles = ((M + TILE - 1) / TILE) * ((N + TILE - 1) / TILE);
   GWA_REQUIRE(tiles < (1ll << 31), "w8a8_gemm: too many tiles");
   hipStream_t s = (hipStream_t)stream;
-  const dim3 grid((unsigned)tiles), block(256);
   const bool f16 = out_dtype == GWA_DT_F16;
   uint16_t* op = (uint16_t*)out;
   const int m = (int)M, n = (int)N, k = (int)K, sr = sa_numel == M && M > 1 ? 1 : 0;
-#define GWA_W8A8_LAUNCH(BD)                                                                                   \
-  do {                                                                                                        \
-    if (f16) hipLaunchKernelGGL((w8a8_gemm_kernel<BD, true>), grid, block, 0, s, qa, qw, sa, sw, bias, op, m, n, k, sr); \
-    else hipLaunchKernelGGL((w8a8_gemm_kernel<BD, false>), grid, block, 0, s, qa, qw, sa, sw, bias, op, m, n, k, sr);    \
-  } while (0)
-  if (!bias) GWA_W8A8_LAUNCH(-1);
-  else if (bias_dtype == GWA_DT_F32) GWA_W8A8_LAUNCH(GWA_DT_F32);
-  else if (bias_dtype == GWA_DT_BF16) GWA_W8A8_LAUNCH(GWA_DT_BF16);
-  else GWA_W8A8_LAUNCH(GWA_DT_F16);
-#undef GWA_W8A8_LAUNCH
+  const int tile = w8a8_tile(M, N, K);
+  const bool lds = tile != GWA_W8A8_TILE_128x128;
+  const int64_t big = ((M + L_TM - 1) / L_TM) * ((N + L_TN - 1) / L_TN);
+  const int64_t per_xcd = (big + kXcds - 1) / kXcds;
+  const dim3 grid(lds ? (unsigned)(per_xcd * kXcds) : (unsigned)tiles), block(lds ? NTHREADS : 256);
+  const int bd = bias ? bias_dtype : -1;
+  W8Kernel kern = nullptr;
+  if (bd == -1) kern = pick_kernel<-1>(tile, f16);
+  else if (bd == GWA_DT_F32) kern = pick_kernel<GWA_DT_F32>(tile, f16);
+  else if (bd == GWA_DT_BF16) kern = pick_kernel<GWA_DT_BF16>(tile, f16);
+  else kern = pick_kernel<GWA_DT_F16>(tile, f16);
+  hipLaunchKernelGGL(kern, grid, block, 0, s, qa, qw, sa, sw, bias, op, m, n, k, sr);
   return gwa_check_launch("w8a8_gemm");
 }

@@ -75,6 +75,8 @@ _SIGNATURES: dict[str, tuple] = {
     "gwa_w8a8_quant_int8": (_vp, _i64, _vp, _vp, _i64, _i64, _vp),
     "gwa_w8a8_quant": (_vp, _i64, _vp, _vp, _vp, _int, _vp, _i64, _i64, _vp),
     "gwa_w8a8_gemm": (_vp, _vp, _vp, _i64, _vp, _vp, _int, _vp, _int, _i64, _i64, _i64, _vp),
+    "gwa_w8a8_gemm_tile": (_i64, _i64, _i64),
+    "gwa_w8a8_gemm_force_tile": (_int,),
     "gwa_awq_w4a16_mm": (_vp, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp),
     "gwa_awq_w4a16_dequant": (_vp, _vp, _vp, _vp, _i64, _i64, _vp),
     "gwa_transpose_2d": (_vp, _vp, _i64, _i64, _i64, _vp),

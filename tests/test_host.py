@@ -61,6 +61,29 @@ def test_fp6_tile_model_choices():
     assert tile(4608, 3072) == 4
 
 
+def test_w8a8_tile_choice():
+    """The W8A8 GEMM's tile choice (host code only): 256 x 256 when its rounds over the 256 CUs take less time
+    than the 128 x 128 grid's (QKV, 4096^3, config 1's 216 tiles), 128 x 128 for small grids, for K % 128 != 0
+    and for K >= 2^23; the forced tile while one is set."""
+    from gen_worker_amd import _native
+
+    lib = _native.load()
+    tile = lib.gwa_w8a8_gemm_tile
+    assert tile(0, 3072, 3072) == -1 and tile(16, 0, 128) == -1
+    assert tile(4608, 9216, 3072) == 1 and tile(4096, 4096, 4096) == 1 and tile(4608, 3072, 3072) == 1
+    assert tile(16384, 9216, 3072) == 1
+    assert tile(256, 9216, 3072) == 0 and tile(1024, 3072, 3072) == 0
+    assert tile(4608, 9216, 3136) == 0 and tile(4608, 9216, 1 << 23) == 0
+    prev = lib.gwa_w8a8_gemm_force_tile(0)
+    try:
+        assert tile(4608, 9216, 3072) == 0
+        lib.gwa_w8a8_gemm_force_tile(1)
+        assert tile(256, 9216, 3072) == 1 and tile(4608, 9216, 3136) == 0
+    finally:
+        lib.gwa_w8a8_gemm_force_tile(prev)
+    assert tile(4608, 9216, 3072) == 1
+
+
 def test_invalid_arguments_are_refused_before_any_launch():
     from gen_worker_amd import _native
 
