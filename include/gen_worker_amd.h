@@ -375,7 +375,7 @@ enum { GWA_W8A8_TILE_128x128 = 0, GWA_W8A8_TILE_256x256 = 1 };
 int gwa_w8a8_gemm_tile(int64_t M, int64_t N, int64_t K);
 
 /* Test and tuning hook: every later gwa_w8a8_gemm uses this tile (-1
- * restores the choice above; K % 128 != 0 or K >= 2^23 always takes
+ * restores the choice above; K % 128 != 0, K >= 2^23 or N >= 2^21 always takes
  * 128 x 128). Process-wide; returns the previous setting. */
 int gwa_w8a8_gemm_force_tile(int tile);
 

@@ -148,7 +148,9 @@ constexpr int L_REG = 256 * L_KS;                  // one operand region of a st
 constexpr int L_STAGE = 2 * L_REG;                 // activation region, then weight region
 constexpr int L_RUNS = L_REG / 1024;               // 1 KB copies per operand and stage: 32
 constexpr int L_SLOTS = L_STAGE / 1024 / NWAVES;   // copies per wave and stage: 8 (4 activation, 4 weight)
-static_assert(2 * L_STAGE <= kLdsBytes && L_SLOTS * NWAVES * 1024 == L_STAGE, "stage layout");
+constexpr int L_OSTR = L_TN * 2 + 8;              // output staging row: 8-byte pad, distinct banks per write
+constexpr int L_LDS = 2 * L_STAGE > L_TM * L_OSTR ? 2 * L_STAGE : L_TM * L_OSTR;
+static_assert(L_LDS <= kLdsBytes && L_SLOTS * NWAVES * 1024 == L_STAGE, "stage layout");
 
 __device__ __forceinline__ int l_swz(int r) { return (r >> 1) & 7; }
 
@@ -171,7 +173,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void w8a8_gemm_lds_kernel(const int8_t
                                                                     const void* __restrict__ bias,
                                                                     uint16_t* __restrict__ out, int M, int N, int K,
                                                                     int sa_row) {
-  __shared__ __attribute__((aligned(16))) uint8_t g_lds[2 * L_STAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t g_lds[L_LDS];
   const int tid = threadIdx.x;
   const int tiles_n = (N + L_TN - 1) / L_TN, tiles_m = (M + L_TM - 1) / L_TM;
   int tm, tn;
@@ -265,18 +267,22 @@ __global__ __launch_bounds__(NTHREADS, 1) void w8a8_gemm_lds_kernel(const int8_t
   stage_body(g_lds + ((nst - 1) & 1) * L_STAGE);
   mma(a1, b1);
 
+  // epilogue: y = acc * sa[m] * sw[n] + bias[n], packed to 16 bits and staged in LDS as [m][n] rows of OSTR
+  // bytes (the stage buffers are free once every wave has passed the barrier), then stored as whole row
+  // segments, consecutive threads on consecutive 16-byte chunks of a row (a 32-row column of 8-byte pieces
+  // per store instruction, as the accumulator layout gives, spreads every store over 32 rows of the output)
+  uint8_t* ob = g_lds;
+  barrier_lds();
 #pragma unroll
-  for (int bn = 0; bn < 4; ++bn) {
-    const int nb = n0 + 128 * wn + 32 * bn;
+  for (int bm = 0; bm < 2; ++bm) {
+    const int ml = 64 * wm + 32 * bm + r32, m = m0 + ml;
+    const float am = sa[sa_row ? min(m, M - 1) : 0];  // rows past M are computed but never stored
 #pragma unroll
-    for (int bm = 0; bm < 2; ++bm) {
-      const int m = m0 + 64 * wm + 32 * bm + r32;
-      if (m >= M) continue;
-      const float am = sa[sa_row ? m : 0];
+    for (int bn = 0; bn < 4; ++bn) {
 #pragma unroll
       for (int qd = 0; qd < 4; ++qd) {
-        const int n = nb + 8 * qd + 4 * h;
-        if (n >= N) continue;
+        const int nl = 128 * wn + 32 * bn + 8 * qd + 4 * h, n = n0 + nl;
+        if (n >= N) continue;  // N % 16 == 0: n < N covers n + 3
         float o[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -294,9 +300,22 @@ __global__ __launch_bounds__(NTHREADS, 1) void w8a8_gemm_lds_kernel(const int8_t
           pk.x = pack_bf16x2(o[0], o[1]);
           pk.y = pack_bf16x2(o[2], o[3]);
         }
-        *(uint2*)(out + (int64_t)m * N + n) = pk;
+        *(uint2*)(ob + ml * L_OSTR + nl * 2) = pk;
       }
     }
+  }
+  barrier_lds();
+  // a descriptor over this tile's output span (255 N + 256 elements < 2^30, checked on the host)
+  const int rows = min(M - m0, L_TM), cols = min(N - n0, L_TN);
+  const rsrc_t obuf = make_rsrc(out + (int64_t)m0 * N + n0, (uint32_t)(((rows - 1) * N + cols) * 2));
+  constexpr int CPR = L_TN / 8;  // 16-byte chunks per row
+#pragma unroll 4
+  for (int i = tid; i < L_TM * CPR; i += NTHREADS) {
+    const int row = i / CPR, c = i % CPR;
+    const uint2 lo = *(const uint2*)(ob + row * L_OSTR + c * 16);
+    const uint2 hi = *(const uint2*)(ob + row * L_OSTR + c * 16 + 8);
+    const uint32_t off = row < rows && 8 * c < cols ? (uint32_t)((row * N + 8 * c) * 2) : kOOB;
+    buf_store16((v4i){(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y}, obuf, off);
   }
 }
 
@@ -313,9 +332,10 @@ W8Kernel pick_kernel(int tile, bool f16) {
 
 // 256 x 256 tiles when their rounds over the CUs finish first: a 256 x 256 tile takes about three times as
 // long as a 128 x 128 one (four times the work at a higher rate), so the choice compares ceil(tiles / CUs)
-// rounds of each; 128-byte stages need K % 128 == 0, and the per-tile descriptors 256 K < 2^31
+// rounds of each; 128-byte stages need K % 128 == 0, and the per-tile descriptors 256 K < 2^31 and
+// 512 N < 2^31
 int w8a8_tile(int64_t M, int64_t N, int64_t K) {
-  if (K % L_KS || K >= (1ll << 23)) return GWA_W8A8_TILE_128x128;
+  if (K % L_KS || K >= (1ll << 23) || N >= (1ll << 21)) return GWA_W8A8_TILE_128x128;
   const int forced = g_w8a8_force_tile.load(std::memory_order_relaxed);
   if (forced >= 0) return forced;
   const int64_t big = ((M + L_TM - 1) / L_TM) * ((N + L_TN - 1) / L_TN);
