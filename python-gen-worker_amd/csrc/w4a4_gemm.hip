@@ -214,8 +214,8 @@ __global__ __launch_bounds__(256) void w4a4_gemm_kernel(
           pk.x = pack_f16x2(o[0], o[1]);
           pk.y = pack_f16x2(o[2], o[3]);
         } else {
-          pk.x = pack_bf16x2(o[0], o[1]);
-          pk.y = pack_bf16x2(o[2], o[3]);
+          pk.x = pack_bf16x2_rn(o[0], o[1]);
+          pk.y = pack_bf16x2_rn(o[2], o[3]);
         }
         // branch-free store after the MFMAs: rows >= M / columns >= N fall outside the buffer
         const uint32_t off = (m < M && n < N) ? (uint32_t)(((int64_t)m * N + n) * 2) : kOOB;

@@ -18,6 +18,8 @@ constexpr int KT = 128;                 // int8 bytes (= K elements) per row per
 constexpr int LDS_STRIDE = KT + 16;
 constexpr int LDS_TILE = TILE * LDS_STRIDE;
 constexpr int LOADS = TILE * KT / 16 / 256;
+constexpr int OSTR = TILE * 2 + 8;     // output staging row: 8-byte pad
+static_assert(TILE * OSTR <= 2 * LDS_TILE, "output staging fits the weight buffers");
 
 template <int BIAS_DT, bool OUT_F16>  // BIAS_DT: -1 none, else GWA_DT_*
 __global__ __launch_bounds__(256) void w8a8_gemm_kernel(const int8_t* __restrict__ qa,
@@ -29,6 +31,7 @@ __global__ __launch_bounds__(256) void w8a8_gemm_kernel(const int8_t* __restrict
                                                         int sa_row) {
   __shared__ __attribute__((aligned(16))) uint8_t lds_w[2][LDS_TILE];
   __shared__ __attribute__((aligned(16))) uint8_t lds_x[2][LDS_TILE];
+  __shared__ __attribute__((aligned(16))) float g_epi[2 * TILE];  // the tile's sw, then its bias as fp32
 
   const int tiles_n = (N + TILE - 1) / TILE;
   const int tn = blockIdx.x % tiles_n, tm = blockIdx.x / tiles_n;
@@ -68,6 +71,18 @@ __global__ __launch_bounds__(256) void w8a8_gemm_kernel(const int8_t* __restrict
   };
 
   load(0);
+  if (t < TILE) {  // the epilogue's per-column constants (published by the next barrier)
+    const int n = n0 + t;
+    float wv = 0.0f, bv = 0.0f;
+    if (n < N) {
+      wv = sw[n];
+      if (BIAS_DT == GWA_DT_F32) bv = ((const float*)bias)[n];
+      if (BIAS_DT == GWA_DT_BF16) bv = bf16_to_f32(((const uint16_t*)bias)[n]);
+      if (BIAS_DT == GWA_DT_F16) bv = f16_bits_to_f32(((const uint16_t*)bias)[n]);
+    }
+    g_epi[t] = wv;
+    g_epi[TILE + t] = bv;
+  }
   store(0);
   __syncthreads();
   for (int st = 0; st < nstages; ++st) {
@@ -94,25 +109,26 @@ __global__ __launch_bounds__(256) void w8a8_gemm_kernel(const int8_t* __restrict
     __syncthreads();
   }
 
+  // epilogue as in the 256 x 256 kernel: constants from LDS, the packed tile staged in the (free) weight
+  // buffers as [m][n] rows, stored as whole row segments
+  uint8_t* ob = lds_w[0];
 #pragma unroll
-  for (int bn = 0; bn < 2; ++bn) {
-    const int nb = n0 + 64 * wn + 32 * bn;
+  for (int bm = 0; bm < 2; ++bm) {
+    const int ml = 64 * wm + 32 * bm + r32, m = m0 + ml;
+    const float am = sa[sa_row ? min(m, M - 1) : 0];  // rows past M are computed but never stored
 #pragma unroll
-    for (int bm = 0; bm < 2; ++bm) {
-      const int m = m0 + 64 * wm + 32 * bm + r32;
-      if (m >= M) continue;
-      const float am = sa[sa_row ? m : 0];
+    for (int bn = 0; bn < 2; ++bn) {
 #pragma unroll
       for (int qd = 0; qd < 4; ++qd) {
-        const int n = nb + 8 * qd + 4 * h;
-        if (n >= N) continue;
+        const int nl = 64 * wn + 32 * bn + 8 * qd + 4 * h;
+        if (n0 + nl >= N) continue;  // N % 16 == 0: n < N covers n + 3
+        const v4f cw = *(const v4f*)(g_epi + nl);
+        const v4f cb = *(const v4f*)(g_epi + TILE + nl);
         float o[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          float y = (float)acc[bn][bm][4 * qd + e] * am * sw[n + e];
-          if (BIAS_DT == GWA_DT_F32) y += ((const float*)bias)[n + e];
-          if (BIAS_DT == GWA_DT_BF16) y += bf16_to_f32(((const uint16_t*)bias)[n + e]);
-          if (BIAS_DT == GWA_DT_F16) y += f16_bits_to_f32(((const uint16_t*)bias)[n + e]);
+          float y = (float)acc[bn][bm][4 * qd + e] * am * cw[e];
+          if (BIAS_DT >= 0) y += cb[e];
           o[e] = y;
         }
         uint2 pk;
@@ -120,12 +136,25 @@ __global__ __launch_bounds__(256) void w8a8_gemm_kernel(const int8_t* __restrict
           pk.x = pack_f16x2(o[0], o[1]);
           pk.y = pack_f16x2(o[2], o[3]);
         } else {
-          pk.x = pack_bf16x2(o[0], o[1]);
-          pk.y = pack_bf16x2(o[2], o[3]);
+          pk.x = pack_bf16x2_rn(o[0], o[1]);
+          pk.y = pack_bf16x2_rn(o[2], o[3]);
         }
-        *(uint2*)(out + (int64_t)m * N + n) = pk;
+        *(uint2*)(ob + ml * OSTR + nl * 2) = pk;
       }
     }
+  }
+  __syncthreads();
+  // a descriptor over this tile's output span (127 N + 128 elements < 2^28: N < 2^21 is checked on the host)
+  const int rows = min(M - m0, TILE), cols = min(N - n0, TILE);
+  const rsrc_t obuf = make_rsrc(out + (int64_t)m0 * N + n0, (uint32_t)(((rows - 1) * N + cols) * 2));
+  constexpr int CPR = TILE / 8;  // 16-byte chunks per row
+#pragma unroll 4
+  for (int i = t; i < TILE * CPR; i += 256) {
+    const int row = i / CPR, c = i % CPR;
+    const uint2 lo = *(const uint2*)(ob + row * OSTR + c * 16);
+    const uint2 hi = *(const uint2*)(ob + row * OSTR + c * 16 + 8);
+    const uint32_t off = row < rows && 8 * c < cols ? (uint32_t)((row * N + 8 * c) * 2) : kOOB;
+    buf_store16((v4i){(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y}, obuf, off);
   }
 }
 
@@ -174,6 +203,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void w8a8_gemm_lds_kernel(const int8_t
                                                                     uint16_t* __restrict__ out, int M, int N, int K,
                                                                     int sa_row) {
   __shared__ __attribute__((aligned(16))) uint8_t g_lds[L_LDS];
+  __shared__ __attribute__((aligned(16))) float g_epi[2 * L_TN];  // the tile's sw, then its bias as fp32
   const int tid = threadIdx.x;
   const int tiles_n = (N + L_TN - 1) / L_TN, tiles_m = (M + L_TM - 1) / L_TM;
   int tm, tn;
@@ -248,6 +278,19 @@ __global__ __launch_bounds__(NTHREADS, 1) void w8a8_gemm_lds_kernel(const int8_t
   };
 
   issue(0, 0);
+  // the epilogue's per-column constants, once per tile (the first barrier publishes them)
+  if (tid < L_TN) {
+    const int n = n0 + tid;
+    float wv = 0.0f, bv = 0.0f;
+    if (n < N) {
+      wv = sw[n];
+      if (BIAS_DT == GWA_DT_F32) bv = ((const float*)bias)[n];
+      if (BIAS_DT == GWA_DT_BF16) bv = bf16_to_f32(((const uint16_t*)bias)[n]);
+      if (BIAS_DT == GWA_DT_F16) bv = f16_bits_to_f32(((const uint16_t*)bias)[n]);
+    }
+    g_epi[tid] = wv;
+    g_epi[L_TN + tid] = bv;
+  }
   wait_vm_lgkm0<0>();
   barrier_lds();
   if (1 < nst) issue(1, 1);
@@ -267,7 +310,9 @@ __global__ __launch_bounds__(NTHREADS, 1) void w8a8_gemm_lds_kernel(const int8_t
   stage_body(g_lds + ((nst - 1) & 1) * L_STAGE);
   mma(a1, b1);
 
-  // epilogue: y = acc * sa[m] * sw[n] + bias[n], packed to 16 bits and staged in LDS as [m][n] rows of OSTR
+  // epilogue: y = acc * sa[m] * sw[n] + bias[n] (sw and bias from the tile's LDS copy: per-element global
+  // loads of them would cost the texture path two 64-lane instructions per output pair), packed to 16 bits and
+  // staged in LDS as [m][n] rows of OSTR
   // bytes (the stage buffers are free once every wave has passed the barrier), then stored as whole row
   // segments, consecutive threads on consecutive 16-byte chunks of a row (a 32-row column of 8-byte pieces
   // per store instruction, as the accumulator layout gives, spreads every store over 32 rows of the output)
@@ -283,13 +328,13 @@ __global__ __launch_bounds__(NTHREADS, 1) void w8a8_gemm_lds_kernel(const int8_t
       for (int qd = 0; qd < 4; ++qd) {
         const int nl = 128 * wn + 32 * bn + 8 * qd + 4 * h, n = n0 + nl;
         if (n >= N) continue;  // N % 16 == 0: n < N covers n + 3
+        const v4f cw = *(const v4f*)(g_epi + nl);
+        const v4f cb = *(const v4f*)(g_epi + L_TN + nl);
         float o[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          float y = (float)acc[bn][bm][4 * qd + e] * am * sw[n + e];
-          if (BIAS_DT == GWA_DT_F32) y += ((const float*)bias)[n + e];
-          if (BIAS_DT == GWA_DT_BF16) y += bf16_to_f32(((const uint16_t*)bias)[n + e]);
-          if (BIAS_DT == GWA_DT_F16) y += f16_bits_to_f32(((const uint16_t*)bias)[n + e]);
+          float y = (float)acc[bn][bm][4 * qd + e] * am * cw[e];
+          if (BIAS_DT >= 0) y += cb[e];
           o[e] = y;
         }
         uint2 pk;
@@ -297,15 +342,15 @@ __global__ __launch_bounds__(NTHREADS, 1) void w8a8_gemm_lds_kernel(const int8_t
           pk.x = pack_f16x2(o[0], o[1]);
           pk.y = pack_f16x2(o[2], o[3]);
         } else {
-          pk.x = pack_bf16x2(o[0], o[1]);
-          pk.y = pack_bf16x2(o[2], o[3]);
+          pk.x = pack_bf16x2_rn(o[0], o[1]);
+          pk.y = pack_bf16x2_rn(o[2], o[3]);
         }
         *(uint2*)(ob + ml * L_OSTR + nl * 2) = pk;
       }
     }
   }
   barrier_lds();
-  // a descriptor over this tile's output span (255 N + 256 elements < 2^30, checked on the host)
+  // a descriptor over this tile's output span (255 N + 256 elements < 2^29: N < 2^21 is checked on the host)
   const int rows = min(M - m0, L_TM), cols = min(N - n0, L_TN);
   const rsrc_t obuf = make_rsrc(out + (int64_t)m0 * N + n0, (uint32_t)(((rows - 1) * N + cols) * 2));
   constexpr int CPR = L_TN / 8;  // 16-byte chunks per row
@@ -330,18 +375,18 @@ W8Kernel pick_kernel(int tile, bool f16) {
   return f16 ? w8a8_gemm_kernel<BD, true> : w8a8_gemm_kernel<BD, false>;
 }
 
-// 256 x 256 tiles when their rounds over the CUs finish first: a 256 x 256 tile takes about three times as
-// long as a 128 x 128 one (four times the work at a higher rate), so the choice compares ceil(tiles / CUs)
-// rounds of each; 128-byte stages need K % 128 == 0, and the per-tile descriptors 256 K < 2^31 and
-// 512 N < 2^31
+// 256 x 256 tiles when their rounds over the CUs finish first: a 256 x 256 tile takes about 2.7 times as
+// long as a 128 x 128 one (four times the work at a higher rate: 50 us against 18.3 us at K = 3072), so the
+// choice compares ceil(tiles / CUs) rounds of each; 128-byte stages need K % 128 == 0, and the per-tile
+// descriptors 256 K < 2^31
 int w8a8_tile(int64_t M, int64_t N, int64_t K) {
-  if (K % L_KS || K >= (1ll << 23) || N >= (1ll << 21)) return GWA_W8A8_TILE_128x128;
+  if (K % L_KS || K >= (1ll << 23)) return GWA_W8A8_TILE_128x128;
   const int forced = g_w8a8_force_tile.load(std::memory_order_relaxed);
   if (forced >= 0) return forced;
   const int64_t big = ((M + L_TM - 1) / L_TM) * ((N + L_TN - 1) / L_TN);
   const int64_t small = ((M + TILE - 1) / TILE) * ((N + TILE - 1) / TILE);
   const int64_t rounds_big = (big + kCus - 1) / kCus, rounds_small = (small + kCus - 1) / kCus;
-  return 3 * rounds_big < rounds_small ? GWA_W8A8_TILE_256x256 : GWA_W8A8_TILE_128x128;
+  return 27 * rounds_big < 10 * rounds_small ? GWA_W8A8_TILE_256x256 : GWA_W8A8_TILE_128x128;
 }
 
 }  // namespace
@@ -366,7 +411,7 @@ extern "C" int gwa_w8a8_gemm(const int8_t* qa, const int8_t* qw, const float* sa
               out_dtype);
   GWA_REQUIRE(bias == nullptr || bias_dtype == GWA_DT_BF16 || bias_dtype == GWA_DT_F16 || bias_dtype == GWA_DT_F32,
               "w8a8_gemm: bias_dtype %d", bias_dtype);
-  GWA_REQUIRE(M < (1ll << 31) && N < (1ll << 30) && K < (1ll << 30), "w8a8_gemm: shape too large");
+  GWA_REQUIRE(M < (1ll << 31) && N < (1ll << 21) && K < (1ll << 30), "w8a8_gemm: shape too large");
   if (M == 0) return GWA_OK;
   GWA_REQUIRE(sa_numel == 1 || sa_numel == M, "w8a8_gemm: sa has %lld values for M=%lld (1 or M)",
               (long long)sa_numel, (long long)M);

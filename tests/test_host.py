@@ -62,9 +62,9 @@ def test_fp6_tile_model_choices():
 
 
 def test_w8a8_tile_choice():
-    """The W8A8 GEMM's tile choice (host code only): 256 x 256 when its rounds over the 256 CUs take less time
-    than the 128 x 128 grid's (QKV, 4096^3, config 1's 216 tiles), 128 x 128 for small grids, for K % 128 != 0
-    and for K >= 2^23; the forced tile while one is set."""
+    """The W8A8 GEMM's tile choice (host code only): 256 x 256 when its rounds over the 256 CUs (2.7 times a
+    128 x 128 round each) take less time than the 128 x 128 grid's (QKV, 4096^3, config 1's 216 tiles, QKV at
+    M=1024), 128 x 128 for small grids, for K % 128 != 0 and for K >= 2^23; the forced tile while one is set."""
     from gen_worker_amd import _native
 
     lib = _native.load()
@@ -72,6 +72,7 @@ def test_w8a8_tile_choice():
     assert tile(0, 3072, 3072) == -1 and tile(16, 0, 128) == -1
     assert tile(4608, 9216, 3072) == 1 and tile(4096, 4096, 4096) == 1 and tile(4608, 3072, 3072) == 1
     assert tile(16384, 9216, 3072) == 1
+    assert tile(1024, 9216, 3072) == 1  # 144 tiles in one round against three rounds of 576
     assert tile(256, 9216, 3072) == 0 and tile(1024, 3072, 3072) == 0
     assert tile(4608, 9216, 3136) == 0 and tile(4608, 9216, 1 << 23) == 0
     prev = lib.gwa_w8a8_gemm_force_tile(0)
