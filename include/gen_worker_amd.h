@@ -361,7 +361,7 @@ int gwa_w8a8_quant(const void* x, int64_t ldx, int8_t* q, float* sa, const float
  *   y[m,n] = (sum_k qa[m,k] qw[n,k]) * sa[m or 0] * sw[n] + bias[n]
  *   qa int8 [M, K]; qw int8 [N, K]; sa fp32 [M] or [1]; sw fp32 [N]
  *   bias of bias_dtype [N] or NULL; out [M, N] of out_dtype (bf16/f16)
- * K % 64 == 0, N % 16 == 0. */
+ * K % 64 == 0, N % 16 == 0, N < 2^21. */
 int gwa_w8a8_gemm(const int8_t* qa, const int8_t* qw, const float* sa, int64_t sa_numel, const float* sw,
                   const void* bias, int bias_dtype, void* out, int out_dtype,
                   int64_t M, int64_t N, int64_t K, void* stream);
@@ -375,7 +375,7 @@ enum { GWA_W8A8_TILE_128x128 = 0, GWA_W8A8_TILE_256x256 = 1 };
 int gwa_w8a8_gemm_tile(int64_t M, int64_t N, int64_t K);
 
 /* Test and tuning hook: every later gwa_w8a8_gemm uses this tile (-1
- * restores the choice above; K % 128 != 0, K >= 2^23 or N >= 2^21 always takes
+ * restores the choice above; K % 128 != 0 or K >= 2^23 always takes
  * 128 x 128). Process-wide; returns the previous setting. */
 int gwa_w8a8_gemm_force_tile(int tile);
 
