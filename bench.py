@@ -151,10 +151,11 @@ def summarize_traffic(d: Path) -> int:
 
 def dit_step_pair(steps: int, warmup: int, modulation: str = "w4a4") -> dict:
     """Config 4: one Flux-dev-shaped denoiser forward (batch 1, 4096 image + 512 text tokens, 19 + 38
-    blocks), every linear W4A4 rank 32 in the process's qualified lane (``modulation="awq"``: the one-token
-    adaLN modulation linears AWQ W4A16, as an svdq checkpoint stores them) vs the same model with bf16
-    nn.Linear GEMMs; bf16 SDPA in both. Each model's forward is captured once in a HIP graph and replayed
-    ``steps`` times."""
+    blocks), every linear W4A4 rank 32 on the int4 lane (``modulation="awq"``: the one-token adaLN modulation
+    linears AWQ W4A16, as an svdq checkpoint stores them) vs the same model with bf16 nn.Linear GEMMs; bf16
+    SDPA in both. The W4A4 model is pinned to the int4 lane (the path being measured); the arming gate's own
+    decision on this box is reported beside it as ``gate_lane``. Each model's forward is captured once in a
+    HIP graph and replayed ``steps`` times."""
     import gc
 
     import torch
@@ -164,9 +165,12 @@ def dit_step_pair(steps: int, warmup: int, modulation: str = "w4a4") -> dict:
     cfg = FluxDiTConfig()
     args_in = inputs(cfg)
     res = {"cfg": cfg}
+    from gen_worker_amd.qualify import resolve_lane
+
+    res["gate_lane"] = resolve_lane()
     for kind in ("w4a4", "bf16"):
         log(f"bench: building the {kind} DiT")
-        model = FluxDiT(kind, cfg, modulation=modulation)
+        model = FluxDiT(kind, cfg, modulation=modulation, lane="int4" if kind == "w4a4" else None)
         res[kind + "_lane"] = model.lane
         torch.cuda.synchronize()
         log(f"bench: timing the {kind} DiT step ({steps} graph replays, {model.lane} lane)")
@@ -201,7 +205,8 @@ def bench_dit(args) -> int:
                       "txt_tokens": cfg.txt_tokens, "rank": cfg.rank, "attention": "bf16 SDPA",
                       "modulation": ("W4A4 (one token)" if args.modulation == "w4a4"
                                      else "AWQ W4A16 g64 (one token)"),
-                      "lane": res["w4a4_lane"], "timing": "forward captured in one HIP graph, replayed"},
+                      "lane": res["w4a4_lane"], "gate_lane": res["gate_lane"],
+                      "timing": "forward captured in one HIP graph, replayed"},
            "bf16_gemm_ms": round(res["bf16"], 3), "speedup_vs_bf16": round(res["bf16"] / res["w4a4"], 4),
            "block_linear_int_ops": ops_, "outputs_finite": {"w4a4": res["w4a4_finite"], "bf16": res["bf16_finite"]}}
     print(json.dumps(out), flush=True)
@@ -706,11 +711,12 @@ def main() -> int:
         "cpu_baseline": cpu,
     }
     if args.dit_steps > 0:
-        # the metric's second half: the config-4 DiT step, W4A4 (qualified lane) against bf16 GEMMs
+        # the metric's second half: the config-4 DiT step, W4A4 (int4 lane) against bf16 GEMMs
         torch.cuda.empty_cache()
         res = dit_step_pair(args.dit_steps, 1, args.modulation)
         out.update({"dit_step_ms": round(res["w4a4"], 3), "dit_bf16_step_ms": round(res["bf16"], 3),
                     "dit_speedup_vs_bf16": round(res["bf16"] / res["w4a4"], 4), "dit_lane": res["w4a4_lane"],
+                    "dit_gate_lane": res["gate_lane"],
                     "dit_modulation": args.modulation,
                     "dit_outputs_finite": res["w4a4_finite"] and res["bf16_finite"]})
     print(json.dumps(out), flush=True)
