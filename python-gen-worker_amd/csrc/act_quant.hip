@@ -214,10 +214,10 @@ __global__ __launch_bounds__(512) void svdq_quant_int4_kernel(
 // 16, lane / 16) holds row r, columns 32c .. 32c+31 of the stage: half of
 // group c / 2, so a group's absmax is one max over the lane's 32 values and
 // one exchange with lane ^ 16.
-//  * Every wave issues all of its x loads (CH tasks x 4 x 16 bytes per lane)
-//    at the start, after the workgroup's copies of the stages' proj_down
-//    operands (direct-to-LDS) and smoothing factors; nothing else waits on
-//    HBM.
+//  * Every wave issues its first task's x loads (4 x 16 bytes per lane) at
+//    the start, before the workgroup's copies of the stages' proj_down
+//    operands (direct-to-LDS) and smoothing factors, and each next task's
+//    when the previous one starts.
 //  * The smoothing reciprocals RN(1/s) of the stages are formed once per
 //    workgroup in LDS (a non-normal reciprocal flags the stage for the
 //    division path).
@@ -270,6 +270,19 @@ __global__ __launch_bounds__(Q6_THREADS) void svdq_quant_fp6_kernel(
   const int grow = row0 + r;
   const bool row_ok = grow < M;
 
+  // 0. x, 4 x 16 bytes per lane per task (rows past M / stages past K read 0): task 0's loads first, then
+  //    task t + 1's when task t starts. (Requesting every task's up front, HBM served all waves' requests
+  //    interleaved and each wave's first task arrived late: 1.9 us slower at config 1.)
+  const rsrc_t xbuf = make_rsrc(x, (uint32_t)(((int64_t)(M - 1) * ldx + K) * 2));
+  v4i xv[CH][4];
+  auto load_task = [&](int t) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int col = (st0 + t) * 128 + 32 * c + 8 * j;
+      xv[t][j] = buf_load16(xbuf, (row_ok && st0 + t < S) ? (uint32_t)(((int64_t)grow * ldx + col) * 2) : kOOB);
+    }
+  };
+  load_task(0);
   // 1. the stages' proj_down operands, direct to LDS: CH * RB * 4 runs of 1 KB, dealt round-robin (every
   //    wave issues the same number). The offset goes in the VGPR operand, the one the hardware range-checks:
   //    the runs of stages past K read zeros.
@@ -292,18 +305,8 @@ __global__ __launch_bounds__(Q6_THREADS) void svdq_quant_fp6_kernel(
   const int scol = st0 * 128 + 2 * tid;
   const bool s_role = smooth && 2 * tid < CH * 128;
   const uint32_t sv = s_role ? buf_load4(smbuf, scol < K ? (uint32_t)(scol * 2) : kOOB) : 0u;
-  // 3. x: all CH tasks, 4 x 16 bytes per lane each (rows past M / stages past K read 0)
-  const rsrc_t xbuf = make_rsrc(x, (uint32_t)(((int64_t)(M - 1) * ldx + K) * 2));
-  v4i xv[CH][4];
-#pragma unroll
-  for (int t = 0; t < CH; ++t)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int col = (st0 + t) * 128 + 32 * c + 8 * j;
-      xv[t][j] = buf_load16(xbuf, (row_ok && st0 + t < S) ? (uint32_t)(((int64_t)grow * ldx + col) * 2) : kOOB);
-    }
-  // 4. reciprocals (the copies and the factors are complete once at most CH * 4 loads remain)
-  wait_vm_lgkm0_q<CH * 4>();
+  // 3. reciprocals, once everything in flight has landed (task 0's x included)
+  wait_vm_lgkm0_q<0>();
   if (s_role) {
     const float s0 = bf16_lo(sv), s1 = bf16_hi(sv);
     float* rcp = (float*)(lds + RCP_OFF);
@@ -328,6 +331,7 @@ __global__ __launch_bounds__(Q6_THREADS) void svdq_quant_fp6_kernel(
 
 #pragma unroll
   for (int t = 0; t < CH; ++t) {
+    if (t + 1 < CH) load_task(t + 1);
     const int st = st0 + t;
     if (st >= S) break;  // workgroup-uniform
     // ---- xs = RN_bf16(x / smooth) as floats, and the lane's absmax

@@ -232,8 +232,11 @@ __device__ __forceinline__ void quant32(const float* v, uint32_t mu, bool valid,
     }
   }
   // v_cvt_scalef32_2xpk16_bf6_f32: element 2i from the first source's i, 2i+1 from the second's, divided
-  // by the scale (1: exact for the integers -8 .. 8)
-  pk = __builtin_amdgcn_cvt_scalef32_2xpk16_bf6_f32(qa, qb, 1.0f);
+  // by the scale (1: exact for the integers -8 .. 8). Written as asm with an early-clobber result: the
+  // builtin let the compiler give the 6 result registers a partial overlap with the 32 source registers
+  // (v[2:7] <- v[0:15], v[16:31]), and the instruction then read a source it had already overwritten
+  // (element 4 of a lane's 32 came out as a non-integer e3m2 code).
+  asm("v_cvt_scalef32_2xpk16_bf6_f32 %0, %1, %2, 1.0" : "=&v"(pk) : "v"(qa), "v"(qb));
 }
 
 }  // namespace g64
