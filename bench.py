@@ -25,11 +25,13 @@ measured with rocprofv3 FETCH_SIZE / WRITE_SIZE, scaled by the same
 counters' reading for a copy of known size (profiles/w4a4_gemm_c1_traffic.json,
 written by ``--summarize-traffic``).
 ``cpu_baseline`` times the reference's CPU serving lane (dense fold + one
-bf16 Linear) on a bounded sample of the same workload. The metric's second
-half, the config-4 DiT step (every linear W4A4 in the process's qualified
-lane, against the same model with bf16 GEMMs, each forward one HIP graph
-replayed ``--dit-steps`` times), goes into the same line as ``dit_step_ms``
-and ``dit_bf16_step_ms``. Prints ONE JSON line on stdout; progress goes to
+bf16 Linear) on a bounded sample of the same workload, and under
+``other_configs`` the CPU path of config 0 (W8A8, M=256) and of config 3's
+QKV linear at M=256 and 1024. The metric's second half, the config-4 DiT step
+(every linear W4A4 on the int4 lane, against the same model with bf16 GEMMs,
+each forward one HIP graph replayed ``--dit-steps`` times), goes into the same
+line as ``dit_step_ms`` and ``dit_bf16_step_ms``, with the arming gate's own
+decision on the box as ``dit_gate_lane``. Prints ONE JSON line on stdout; progress goes to
 stderr.
 
 ``--only`` runs one piece eagerly ``--iters`` times (after 3 warmups) and
@@ -321,6 +323,40 @@ def bench_qkv(args) -> int:
            "rows": rows}
     print(json.dumps(out), flush=True)
     return 0
+
+
+def cpu_other_configs(torch, synthetic, threads: int) -> list:
+    """The CPU path of the other configs BASELINE lists at CPU-runnable sizes: config 0 (W8A8, M=256,
+    K=N=3072: the reference's dequant lane and the W8A8 torch chain) and config 3's QKV linear at M=256 and
+    1024 (the W4A4 fallback lane), each the median of 10 after 3 warmups on this host's cores."""
+    import numpy as np
+
+    from gen_worker_amd.svdq import w4a4_int_ops
+    from oracle import cpu_baseline
+
+    b = lambda t: t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)  # noqa: E731
+    out = []
+    c0 = synthetic.C0
+    L8 = synthetic.w8a8_layer(c0["n"], c0["k"])
+    x0 = synthetic.activation(c0["m"], c0["k"], outlier_frac=c0["outlier_frac"], outlier_scale=c0["outlier_scale"])
+    r = cpu_baseline.time_w8a8_linear_cpu(b(x0), L8.qweight.numpy(), L8.weight_scale.numpy(), L8.bias.numpy(),
+                                          threads=threads)
+    ops0 = w4a4_int_ops(c0["m"], c0["n"], c0["k"])
+    out.append({"config": f"c0 W8A8 M={c0['m']} K=N={c0['k']}", "value": round(ops0 / r["dequant_s"] / 1e12, 4),
+                "unit": "TOPS", "sample": (f"dequant lane (bf16 nn.Linear on the dequantized weight) "
+                                           f"{r['dequant_s'] * 1e3:.2f} ms; W8A8 torch chain "
+                                           f"{r['chain_s'] * 1e3:.2f} ms")})
+    c3 = synthetic.C3
+    L3 = synthetic.w4a4_layer(c3["n"], c3["k"], c3["rank"])
+    for m in (256, 1024):
+        x3 = synthetic.activation(m, c3["k"], outlier_frac=c3["outlier_frac"], outlier_scale=c3["outlier_scale"])
+        r = cpu_baseline.time_w4a4_linear_cpu(b(x3), b(L3.smooth), L3.qweight.numpy(), L3.wscales.numpy(),
+                                              b(L3.proj_down), b(L3.proj_up), b(L3.bias), threads=threads)
+        out.append({"config": f"c3 QKV M={m} K={c3['k']} N={c3['n']}",
+                    "value": round(w4a4_int_ops(m, c3["n"], c3["k"]) / r["fallback_s"] / 1e12, 4), "unit": "TOPS",
+                    "sample": (f"fallback lane {r['fallback_s'] * 1e3:.2f} ms; oracle chain "
+                               f"{r['chain_s'] * 1e3:.1f} ms")})
+    return out
 
 
 def bench_w8a8(args) -> int:
@@ -682,6 +718,7 @@ def main() -> int:
                           f"svdq_native.py:200-221) on {rows} of {m} config-1 rows, K=N={k}: median of 10 = "
                           f"{res['fallback_s'] * 1e3:.2f} ms; oracle chain (int4 act-quant -> dequant -> fp32 "
                           f"matmul) {res['chain_s'] * 1e3:.1f} ms; torch threads={res['threads']}")}
+        cpu["other_configs"] = cpu_other_configs(torch, synthetic, res["threads"])
 
     out = {
         "metric": METRIC,

@@ -65,3 +65,32 @@ def time_w4a4_linear_cpu(x_bits: np.ndarray, smooth_bits, qw, sw, down_bits, up_
     t_fb = _median_s(fallback, iters=iters)
     t_chain = _median_s(chain, warmup=1, iters=max(3, iters // 3))
     return {"fallback_s": t_fb, "chain_s": t_chain, "threads": threads}
+
+
+def time_w8a8_linear_cpu(x_bits: np.ndarray, qw: np.ndarray, sw: np.ndarray, bias: np.ndarray | None,
+                         threads: int | None = None, iters: int = 10) -> dict:
+    """Config 0 on the CPU: the reference's W8A8 dequant lane (the weight dequantized once to bf16, then one
+    bf16 ``nn.Linear``: the ``bf16-resident`` mode of ``models/w8a8.py:455-548``) and the W8A8 torch chain
+    (per-token int8 activation quant, then the int-valued product in fp32 times the two scales, plus bias)."""
+    threads = threads or os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    wd = torch.from_numpy((qw.astype(np.float32) * sw.astype(np.float32).reshape(-1, 1))).to(torch.bfloat16)
+    bt = torch.from_numpy(bias.astype(np.float32)) if bias is not None else None
+    xt = torch.from_numpy(O.bf16_bits_to_f32(x_bits)).to(torch.bfloat16)
+    qwt = torch.from_numpy(qw.astype(np.float32))
+    swt = torch.from_numpy(sw.astype(np.float32).reshape(1, -1))
+
+    def dequant_lane():
+        return torch.nn.functional.linear(xt, wd, None if bt is None else bt.to(torch.bfloat16))
+
+    def chain():
+        x32 = xt.float()
+        sa = (x32.abs().amax(dim=1, keepdim=True) / 127.0).clamp(min=1e-12)
+        q = (x32 / sa).round().clamp(-127, 127)
+        y = (q @ qwt.t()) * sa * swt
+        return y + bt if bt is not None else y
+
+    t_dq = _median_s(dequant_lane, iters=iters)
+    t_chain = _median_s(chain, iters=iters)
+    return {"dequant_s": t_dq, "chain_s": t_chain, "threads": threads}
+
