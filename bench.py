@@ -688,6 +688,7 @@ def main() -> int:
     value_tops = int_ops / (step_ms * 1e-3) / 1e12
     gemm_tops = int_ops / (gemm_ms * 1e-3) / 1e12
     qbytes = act_quant_bytes(m, k, r, fp6=True)
+    qmin = act_quant_bytes(m, k, r, fp6=False)
     quant_gbs = qbytes / (quant_ms * 1e-3) / 1e9
     log(f"bench: step {step_ms * 1e3:.1f} us (eager {eager_ms * 1e3:.1f} us)  quant {quant_ms * 1e3:.1f} us "
         f"({quant_gbs:.0f} GB/s)  gemm {gemm_ms * 1e3:.1f} us ({gemm_tops:.0f} TOPS, "
@@ -744,7 +745,10 @@ def main() -> int:
         "eager_ms_per_step": round(eager_ms, 5),
         "act_quant": {"kernel": "svdq_quant_fp6_kernel + la_reduce_kernel", "avg_launch_us": round(quant_ms * 1e3, 2),
                       "algorithmic_bytes": qbytes, "achieved_GBps": round(quant_gbs, 1),
-                      "frac_hbm_peak": round(quant_gbs / HBM_PEAK_GBS, 4)},
+                      "frac_hbm_peak": round(quant_gbs / HBM_PEAK_GBS, 4),
+                      # the int4 contract's minimum (nibble codes + fp16 scales + bf16 la): SURVEY's 36.33 MB
+                      "min_bytes_int4_contract": qmin,
+                      "achieved_GBps_vs_int4_min": round(qmin / (quant_ms * 1e-3) / 1e9, 1)},
         "cpu_baseline": cpu,
     }
     if args.dit_steps > 0:
