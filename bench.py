@@ -746,7 +746,7 @@ def main() -> int:
         "act_quant": {"kernel": "svdq_quant_fp6_kernel + la_reduce_kernel", "avg_launch_us": round(quant_ms * 1e3, 2),
                       "algorithmic_bytes": qbytes, "achieved_GBps": round(quant_gbs, 1),
                       "frac_hbm_peak": round(quant_gbs / HBM_PEAK_GBS, 4),
-                      # the int4 contract's minimum (nibble codes + fp16 scales + bf16 la): SURVEY's 36.33 MB
+                      # the int4 contract's minimum (nibble codes + fp16 scales + bf16 la): 36.33 MB at config 1
                       "min_bytes_int4_contract": qmin,
                       "achieved_GBps_vs_int4_min": round(qmin / (quant_ms * 1e-3) / 1e9, 1)},
         "cpu_baseline": cpu,
