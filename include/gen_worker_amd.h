@@ -450,6 +450,34 @@ int gwa_nvfp4_scale_bias(void* y, const float* s2, const float* ws2, const void*
 int gwa_transpose_2d(const void* src, void* dst, int64_t rows, int64_t cols,
                      int64_t elem_size, void* stream);
 
+/* ---- Block glue of the benchmark's Flux-shaped DiT (config 4) ----------------
+ * No counterpart among the reference's entry points: the reference's DiT is
+ * diffusers' FluxTransformerBlock / FluxSingleTransformerBlock, which computes
+ * these with torch ops between its (quantized) linears. Each is one pass with
+ * the torch expression's bf16 roundings; all tensors bf16, rows with strides. */
+
+/* q and k of one token range -> RMSNorm over head_dim (sum of squares in fp32,
+ * rsqrt(mean + eps), rounded to bf16, times the bf16 weight wq / wk [128])
+ * -> rotary embedding on interleaved (even, odd) pairs with the bf16 tables
+ * cos_t / sin_t [table_rows, 64] at positions pos0 + row; v (xv, optional)
+ * copied to ov. Inputs [rows, heads * 128] at row stride ldx (e.g. column
+ * slices of a fused qkv output), outputs at row stride ldo. head_dim == 128. */
+int gwa_dit_qk_norm_rope(const void* xq, const void* xk, const void* xv, int64_t ldx, const void* wq,
+                         const void* wk, const void* cos_t, const void* sin_t, int64_t pos0, int64_t table_rows,
+                         void* oq, void* ok, void* ov, int64_t ldo, int64_t rows, int64_t heads, int64_t head_dim,
+                         float eps, void* stream);
+
+/* out = RN(RN(RN(LayerNorm(x)) * RN(1 + scale)) + shift): LayerNorm without
+ * affine over cols (fp32 mean and biased variance), scale / shift bf16
+ * [cols]; cols a multiple of 512, <= 4096; 16-byte aligned rows. */
+int gwa_dit_adaln_modulate(const void* x, int64_t ldx, const void* scale, const void* shift, void* out,
+                           int64_t ldo, int64_t rows, int64_t cols, float eps, void* stream);
+
+/* out = RN(x + RN(gate * y)), gate bf16 [cols] broadcast over rows; out may
+ * be x. cols % 8 == 0, 16-byte aligned rows. */
+int gwa_dit_gate_residual(const void* x, int64_t ldx, const void* y, int64_t ldy, const void* gate, void* out,
+                          int64_t ldo, int64_t rows, int64_t cols, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -38,6 +38,7 @@ class NativeError(RuntimeError):
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
 _int = ctypes.c_int
+_flt = ctypes.c_float
 
 # name -> argtypes (all return int status unless listed in _RESTYPES)
 _SIGNATURES: dict[str, tuple] = {
@@ -78,6 +79,10 @@ _SIGNATURES: dict[str, tuple] = {
     "gwa_w8a8_gemm_tile": (_i64, _i64, _i64),
     "gwa_w8a8_gemm_force_tile": (_int,),
     "gwa_awq_w4a16_mm": (_vp, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp),
+    "gwa_dit_qk_norm_rope": (_vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _i64,
+                             _i64, _i64, _flt, _vp),
+    "gwa_dit_adaln_modulate": (_vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _flt, _vp),
+    "gwa_dit_gate_residual": (_vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _vp),
     "gwa_awq_w4a16_dequant": (_vp, _vp, _vp, _vp, _i64, _i64, _vp),
     "gwa_transpose_2d": (_vp, _vp, _i64, _i64, _i64, _vp),
     "gwa_nvfp4_blocked_scale_numel": (_i64, _i64),

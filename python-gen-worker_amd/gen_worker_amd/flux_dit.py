@@ -144,6 +144,8 @@ def modulation_factory(kind: str, device, rank: int = 32, lane: str = "int4",
     raise ValueError(f"linear kind {kind!r} not in ('w4a4', 'bf16')")
 
 
+# torch statements of the block glue; the blocks run the fused kernels below (csrc/dit_block.hip), which
+# round every step as these expressions do
 def _rms(x: Tensor, w: Tensor, eps: float = 1e-6) -> Tensor:
     xf = x.float()
     return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)).to(x.dtype) * w
@@ -157,6 +159,82 @@ def _rope(x: Tensor, cos: Tensor, sin: Tensor) -> Tensor:
     """Rotary embedding on interleaved (even, odd) pairs: x [S, H, D], cos / sin [S, 1, D/2]."""
     xe, xo = x[..., 0::2], x[..., 1::2]
     return torch.stack((xe * cos - xo * sin, xe * sin + xo * cos), dim=-1).flatten(-2)
+
+
+def _check_rows(name: str, t: Tensor, cols: int) -> None:
+    if t.dtype != torch.bfloat16 or not t.is_cuda:
+        raise ValueError(f"{name}: bf16 CUDA tensor expected, got {t.dtype} on {t.device}")
+    if t.dim() != 2 or t.shape[1] != cols or t.stride(1) != 1:
+        raise ValueError(f"{name}: [rows, {cols}] with unit column stride expected, got {tuple(t.shape)} "
+                         f"strides {t.stride()}")
+
+
+def _vector(name: str, t: Tensor, cols: int) -> Tensor:
+    v = t.reshape(-1)
+    if v.numel() != cols or v.dtype != torch.bfloat16 or (cols > 1 and v.stride(0) != 1):
+        raise ValueError(f"{name}: {cols} contiguous bf16 values expected, got {tuple(t.shape)} {t.dtype}")
+    return v
+
+
+def adaln_modulate(x: Tensor, scale: Tensor, shift: Tensor, eps: float = 1e-6) -> Tensor:
+    """``_ln(x) * (1 + scale) + shift`` in one pass (``gwa_dit_adaln_modulate``): x bf16 [rows, C] (row
+    stride allowed), scale / shift C bf16 values (e.g. chunks of a modulation output)."""
+    from . import _native
+
+    c = x.shape[-1]
+    _check_rows("adaln_modulate x", x, c)
+    sc, sh = _vector("adaln_modulate scale", scale, c), _vector("adaln_modulate shift", shift, c)
+    out = torch.empty(x.shape, device=x.device, dtype=torch.bfloat16)
+    _native.call("gwa_dit_adaln_modulate", _native.ptr(x), x.stride(0), _native.ptr(sc), _native.ptr(sh),
+                 _native.ptr(out), c, x.shape[0], c, eps, _native.stream_of(x))
+    return out
+
+
+def gate_residual(x: Tensor, y: Tensor, gate: Tensor) -> Tensor:
+    """``x + gate * y`` in one pass (``gwa_dit_gate_residual``): x, y bf16 [rows, C], gate C bf16 values
+    broadcast over rows."""
+    from . import _native
+
+    c = x.shape[-1]
+    _check_rows("gate_residual x", x, c)
+    _check_rows("gate_residual y", y, c)
+    if y.shape[0] != x.shape[0]:
+        raise ValueError(f"gate_residual: x has {x.shape[0]} rows, y {y.shape[0]}")
+    g = _vector("gate_residual gate", gate, c)
+    out = torch.empty(x.shape, device=x.device, dtype=torch.bfloat16)
+    _native.call("gwa_dit_gate_residual", _native.ptr(x), x.stride(0), _native.ptr(y), y.stride(0), _native.ptr(g),
+                 _native.ptr(out), c, x.shape[0], c, _native.stream_of(x))
+    return out
+
+
+def qk_norm_rope(q: Tensor, k: Tensor, wq: Tensor, wk: Tensor, cos: Tensor, sin: Tensor, pos0: int,
+                 out_q: Tensor, out_k: Tensor, v: Optional[Tensor] = None, out_v: Optional[Tensor] = None,
+                 eps: float = 1e-6) -> None:
+    """``_rope(_rms(q, wq), cos, sin)`` and the same for k, in one pass (``gwa_dit_qk_norm_rope``), written
+    into out_q / out_k [rows, heads, 128] (row slices of a joint sequence's buffers); v, if given, is copied to
+    out_v. q, k (, v): [rows, heads * 128] views sharing one row stride (column slices of a fused qkv output);
+    the rotary tables cos / sin [positions, 1, 64] are read at positions pos0 + row."""
+    from . import _native
+
+    rows, heads, d = out_q.shape
+    hd = heads * d
+    for name, t in (("q", q), ("k", k)) + ((("v", v),) if v is not None else ()):
+        _check_rows(f"qk_norm_rope {name}", t, hd)
+        if t.shape[0] != rows or t.stride(0) != q.stride(0):
+            raise ValueError(f"qk_norm_rope {name}: {rows} rows at q's row stride expected")
+    outs = (out_q, out_k) + ((out_v,) if out_v is not None else ())
+    for o in outs:
+        if o.shape != out_q.shape or o.stride() != out_q.stride() or o.stride(1) != d or o.stride(2) != 1:
+            raise ValueError("qk_norm_rope: outputs must be [rows, heads, head_dim] with rows at one stride")
+    if (v is None) != (out_v is None):
+        raise ValueError("qk_norm_rope: v and out_v go together")
+    if cos.shape != sin.shape or not cos.is_contiguous() or not sin.is_contiguous() or cos.shape[-1] * 2 != d:
+        raise ValueError("qk_norm_rope: cos / sin must be contiguous [positions, 1, head_dim / 2] tables")
+    wq, wk = _vector("qk_norm_rope wq", wq, d), _vector("qk_norm_rope wk", wk, d)
+    _native.call("gwa_dit_qk_norm_rope", _native.ptr(q), _native.ptr(k), _native.ptr(v), q.stride(0),
+                 _native.ptr(wq), _native.ptr(wk), _native.ptr(cos), _native.ptr(sin), pos0, cos.shape[0],
+                 _native.ptr(out_q), _native.ptr(out_k), _native.ptr(out_v), out_q.stride(0), rows, heads, d, eps,
+                 _native.stream_of(out_q))
 
 
 def _attention(q: Tensor, k: Tensor, v: Tensor) -> Tensor:
@@ -196,20 +274,23 @@ class DualBlock(nn.Module):
         cfg = self.cfg
         sh1, sc1, g1, sh2, sc2, g2 = self.mod_img(temb).chunk(6, dim=-1)
         tsh1, tsc1, tg1, tsh2, tsc2, tg2 = self.mod_txt(temb).chunk(6, dim=-1)
-        ni = _ln(img) * (1 + sc1) + sh1
-        nt = _ln(txt) * (1 + tsc1) + tsh1
-        hq = (-1, cfg.heads, cfg.head_dim)
-        qi, ki, vi = self.qkv_img(ni).chunk(3, dim=-1)
-        qt, kt, vt = self.qkv_txt(nt).chunk(3, dim=-1)
-        q = torch.cat((_rms(qt.reshape(hq), self.qn_txt), _rms(qi.reshape(hq), self.qn_img)))
-        k = torch.cat((_rms(kt.reshape(hq), self.kn_txt), _rms(ki.reshape(hq), self.kn_img)))
-        v = torch.cat((vt.reshape(hq), vi.reshape(hq)))
-        a = _attention(_rope(q, cos, sin), _rope(k, cos, sin), v)
-        at, ai = a[: txt.shape[0]], a[txt.shape[0]:]
-        img = img + g1 * self.o_img(ai.contiguous())
-        txt = txt + tg1 * self.o_txt(at.contiguous())
-        img = img + g2 * _mlp(self.fc1_img, self.fc2_img, _ln(img) * (1 + sc2) + sh2, self.fused)
-        txt = txt + tg2 * _mlp(self.fc1_txt, self.fc2_txt, _ln(txt) * (1 + tsc2) + tsh2, self.fused)
+        c, st = cfg.hidden, txt.shape[0]
+        qkv_i = self.qkv_img(adaln_modulate(img, sc1, sh1))
+        qkv_t = self.qkv_txt(adaln_modulate(txt, tsc1, tsh1))
+        # q, k, v of the joint [text; image] sequence, written in place by the norm + rotary kernel
+        q, k, v = (torch.empty(st + img.shape[0], cfg.heads, cfg.head_dim, device=img.device, dtype=img.dtype)
+                   for _ in range(3))
+        for src, qn, kn, rows in ((qkv_t, self.qn_txt, self.kn_txt, slice(0, st)),
+                                  (qkv_i, self.qn_img, self.kn_img, slice(st, None))):
+            qk_norm_rope(src[:, :c], src[:, c:2 * c], qn, kn, cos, sin, rows.start, q[rows], k[rows],
+                         v=src[:, 2 * c:], out_v=v[rows])
+        a = _attention(q, k, v)
+        at, ai = a[:st], a[st:]
+        img = gate_residual(img, self.o_img(ai.contiguous()), g1)
+        txt = gate_residual(txt, self.o_txt(at.contiguous()), tg1)
+        img = gate_residual(img, _mlp(self.fc1_img, self.fc2_img, adaln_modulate(img, sc2, sh2), self.fused), g2)
+        txt = gate_residual(txt, _mlp(self.fc1_txt, self.fc2_txt, adaln_modulate(txt, tsc2, tsh2), self.fused),
+                            tg2)
         return img, txt
 
 
@@ -230,16 +311,17 @@ class SingleBlock(nn.Module):
     def forward(self, x: Tensor, temb: Tensor, cos: Tensor, sin: Tensor) -> Tensor:
         cfg = self.cfg
         sh, sc, g = self.mod(temb).chunk(3, dim=-1)
-        n = _ln(x) * (1 + sc) + sh
-        hq = (-1, cfg.heads, cfg.head_dim)
-        q, k, v = self.qkv(n).chunk(3, dim=-1)
-        a = _attention(_rope(_rms(q.reshape(hq), self.qn), cos, sin), _rope(_rms(k.reshape(hq), self.kn), cos, sin),
-                       v.reshape(hq))
+        n = adaln_modulate(x, sc, sh)
+        c = cfg.hidden
+        qkv = self.qkv(n)
+        q, k = (torch.empty(x.shape[0], cfg.heads, cfg.head_dim, device=x.device, dtype=x.dtype) for _ in range(2))
+        qk_norm_rope(qkv[:, :c], qkv[:, c:2 * c], self.qn, self.kn, cos, sin, 0, q, k)
+        a = _attention(q, k, qkv[:, 2 * c:].reshape(-1, cfg.heads, cfg.head_dim))
         if self.fused:
             from .svdq import svdq_concat_forward
 
-            return x + g * svdq_concat_forward(self.proj_out, a, self.mlp, n)
-        return x + g * self.proj_out(torch.cat((a, self.mlp(n)), dim=-1))
+            return gate_residual(x, svdq_concat_forward(self.proj_out, a, self.mlp, n), g)
+        return gate_residual(x, self.proj_out(torch.cat((a, self.mlp(n)), dim=-1)), g)
 
 
 class FluxDiT(nn.Module):
@@ -286,7 +368,7 @@ class FluxDiT(nn.Module):
             x = blk(x, t, self.cos, self.sin)
         img = x[self.cfg.txt_tokens:]
         scale, shift = self.norm_out(t).chunk(2, dim=-1)
-        return self.proj_out((_ln(img) * (1 + scale) + shift).contiguous())
+        return self.proj_out(adaln_modulate(img, scale, shift))
 
 
 def inputs(cfg: FluxDiTConfig = FluxDiTConfig(), device="cuda", seed: int = 7) -> tuple[Tensor, Tensor, Tensor]:
@@ -341,4 +423,5 @@ def time_step_ms(model: nn.Module, args: tuple[Tensor, ...], steps: int = 5, war
         return e0.elapsed_time(e1) / steps
 
 
-__all__ = ["FluxDiT", "FluxDiTConfig", "block_int_ops", "inputs", "linear_factory", "time_step_ms"]
+__all__ = ["FluxDiT", "FluxDiTConfig", "adaln_modulate", "block_int_ops", "gate_residual", "inputs",
+           "linear_factory", "qk_norm_rope", "time_step_ms"]

@@ -363,3 +363,23 @@ def test_w8a8_module_modes_on_cpu():
     with pytest.raises(W8a8Error, match="one scalar"):
         build_int8_linear(qweight=L.qweight, weight_scale=L.weight_scale, bias=None, device="cpu",
                           input_scale=torch.ones(2))
+
+
+def test_dit_glue_refuses_bad_shapes_before_any_launch():
+    """The DiT block glue entry points validate on the host (no device touched)."""
+    from gen_worker_amd import _native
+
+    lib = _native.load()
+    rc = lib.gwa_dit_qk_norm_rope(None, None, None, 64 * 2, None, None, None, None, 0, 8, None, None, None,
+                                  64 * 2, 4, 2, 64, 1e-6, None)
+    assert rc == 1 and "head_dim" in lib.gwa_last_error().decode()
+    rc = lib.gwa_dit_qk_norm_rope(None, None, None, 256, None, None, None, None, 6, 8, None, None, None, 256, 4,
+                                  2, 128, 1e-6, None)
+    assert rc == 1 and "outside" in lib.gwa_last_error().decode()
+    rc = lib.gwa_dit_adaln_modulate(None, 640, None, None, None, 640, 4, 640, 1e-6, None)
+    assert rc == 1 and "multiple of 512" in lib.gwa_last_error().decode()
+    rc = lib.gwa_dit_gate_residual(None, 12, None, 12, None, None, 12, 4, 12, None)
+    assert rc == 1 and "multiple of 8" in lib.gwa_last_error().decode()
+    # empty problems are no-ops
+    assert lib.gwa_dit_adaln_modulate(None, 512, None, None, None, 512, 0, 512, 1e-6, None) == 0
+    assert lib.gwa_dit_gate_residual(None, 8, None, 8, None, None, 8, 0, 8, None) == 0
