@@ -326,6 +326,36 @@ int gwa_svdq_w4a4_linear_fp6_noalloc(const void* x, int64_t ldx, const void* smo
 /* GWA_NOALLOC_SCRATCH_BYTES, as the built library sees it. */
 int64_t gwa_svdq_w4a4_linear_fp6_noalloc_scratch_bytes(void);
 
+/* One whole SVDQuant W4A4 linear for a few tokens: the forward of
+ * _SvdqFusedLinear (models/svdq_fused.py:516-527) at the token counts of the
+ * DiT's adaLN modulation linears (one token per image), where the GEMM tiles
+ * would spend 32-128 rows of work on each real one. Streams the int4 weight
+ * in the reference's layout (the module's `weight` uint8 [N, K/2], two's-
+ * complement nibbles, low nibble = even input; `weight_scale` fp16 [N, K/64])
+ * once; kernel 1 (gwa_svdq_quant_fp6) supplies la's partial slots when rank >
+ * 0, and the GEMV quantizes the rows itself with kernel 1's quantizer (codes
+ * and scales bit-identical). Same group order and epilogue as the GEMM
+ * (acc = fma(P_g, sx_g * sw_g, acc), * s2 * second, + la . up, + bias,
+ * optional GELU-tanh); only the low-rank sum rounds differently.
+ *   x / smooth / s2 / proj_down_op6 / proj_up / second / bias / out /
+ *   out_dtype / epilogue_flags as gwa_svdq_w4a4_linear_fp6
+ *   qw uint8 [N, K/2] (16-byte aligned rows), sw fp16 [N, K/64]
+ *   workspace >= gwa_svdq_w4a4_linear_gemv_workspace(M, K, rank) bytes,
+ *   256-byte aligned, nothing in it needs initialising
+ * 1 <= M <= gwa_svdq_w4a4_gemv_max_m(K, rank), K % 128 == 0, N % 16 == 0. */
+int gwa_svdq_w4a4_linear_gemv(const void* x, int64_t ldx, const void* smooth, const float* s2,
+                              const void* proj_down_op6, int64_t rank, const uint8_t* qw, const void* sw,
+                              const float* second, int64_t second_numel, const void* proj_up, const void* bias,
+                              void* out, int out_dtype, int epilogue_flags, int64_t M, int64_t N, int64_t K,
+                              void* workspace, int64_t workspace_bytes, void* stream);
+
+/* The most tokens gwa_svdq_w4a4_linear_gemv takes at this K and rank (up to
+ * 8; 0 if K % 128 != 0, K > 8192 or the rank is unsupported). */
+int gwa_svdq_w4a4_gemv_max_m(int64_t K, int64_t rank);
+
+/* Workspace bytes of gwa_svdq_w4a4_linear_gemv (0 for an unsupported shape). */
+int64_t gwa_svdq_w4a4_linear_gemv_workspace(int64_t M, int64_t K, int64_t rank);
+
 /* Standalone epilogue: out = y0 * (s2 * second) + la @ up^T + bias (bf16 out).
  * cozy_gen_worker::svdq_epilogue_lora, models/svdq_fused.py:315-377.
  *   y0 bf16 [M, N]; la bf16 [M, rank]; up bf16 [N, rank]; bias bf16 [N] or NULL */

@@ -61,6 +61,10 @@ _SIGNATURES: dict[str, tuple] = {
     "gwa_svdq_w4a4_linear_fp6_noalloc": (_vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _int,
                                          _int, _i64, _i64, _i64, _vp),
     "gwa_svdq_w4a4_linear_fp6_noalloc_scratch_bytes": (),
+    "gwa_svdq_w4a4_linear_gemv": (_vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _int, _int,
+                                  _i64, _i64, _i64, _vp, _i64, _vp),
+    "gwa_svdq_w4a4_gemv_max_m": (_i64, _i64),
+    "gwa_svdq_w4a4_linear_gemv_workspace": (_i64, _i64, _i64),
     "gwa_svdq_gemm_w4a4_fp6_next": (_vp, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _int,
                                     _vp, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _vp),
     "gwa_svdq_quant_fp6": (_vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _i64, _vp),
@@ -95,7 +99,8 @@ _RESTYPES = {"gwa_build_info": ctypes.c_char_p, "gwa_last_error": ctypes.c_char_
              "gwa_svdq_quant_fp6_partials": ctypes.c_int64, "gwa_svdq_gemm_w4a4_fp6_next_partials": ctypes.c_int64,
              "gwa_nvfp4_blocked_scale_numel": ctypes.c_int64, "gwa_svdq_w4a4_linear_fp6_workspace": ctypes.c_int64,
              "gwa_svdq_w4a4_linear_fp6_noalloc_scratch_bytes": ctypes.c_int64,
-             "gwa_svdq_quant_fp6_la_workspace": ctypes.c_int64}
+             "gwa_svdq_quant_fp6_la_workspace": ctypes.c_int64,
+             "gwa_svdq_w4a4_linear_gemv_workspace": ctypes.c_int64}
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
 

@@ -559,6 +559,77 @@ def _(x2, smooth, s2, proj_down_op6, weight_fp6, second, proj_up, bias, out_dtyp
     return x2.new_empty(int(x2.shape[0]), int(weight_fp6.shape[1]), dtype=out_dtype)
 
 
+def gemv_max_m(k: int, rank: int) -> int:
+    """The most tokens the small-M path (``svdq_forward_gemv``) takes at K inputs and this rank (0: none)."""
+    return int(nat.load().gwa_svdq_w4a4_gemv_max_m(k, rank))
+
+
+@torch.library.custom_op("cozy_gen_worker::svdq_forward_gemv", mutates_args=())
+def svdq_forward_gemv(x2: Tensor, smooth: Optional[Tensor], s2: Optional[Tensor], proj_down_op6: Optional[Tensor],
+                      weight: Tensor, weight_scale: Tensor, second: Optional[Tensor], proj_up: Optional[Tensor],
+                      bias: Optional[Tensor], out_dtype: torch.dtype, gelu: bool) -> Tensor:
+    """The whole linear for a few tokens (``_SvdqFusedLinear.forward``, ``models/svdq_fused.py:516-527``, at
+    M <= ``gemv_max_m``): the int4 weight [N, K/2] and its fp16 scales streamed once by a GEMV that quantizes
+    the rows with kernel 1's quantizer (bit-identical codes and scales) and sums kernel 1's la partial slots;
+    the group order and epilogue of the GEMM lane (only the low-rank sum rounds differently)."""
+    name = "svdq_forward_gemv"
+    if x2.dim() != 2:
+        raise SvdqOpError(f"{name}: x2 must be 2-D, got {tuple(x2.shape)}")
+    s2 = _scalar_f32(name, s2)
+    if second is not None and second.dtype != torch.float32:
+        second = second.float().contiguous()
+    _check_dtype(name, x2, torch.bfloat16, what="x2")
+    _check_dtype(name, smooth, torch.bfloat16, what="smooth")
+    _check_dtype(name, proj_down_op6, torch.bfloat16, what="proj_down_op6")
+    _check_dtype(name, weight, torch.uint8, what="weight")
+    _check_dtype(name, weight_scale, torch.float16, what="weight_scale")
+    _check_dtype(name, proj_up, torch.bfloat16, what="proj_up")
+    _check_dtype(name, bias, torch.bfloat16, what="bias")
+    if out_dtype not in (torch.bfloat16, torch.float16):
+        raise SvdqOpError(f"{name}: out_dtype {out_dtype} not bf16/fp16")
+    if x2.stride(1) != 1 or x2.stride(0) % 8:
+        x2 = x2.contiguous()
+    _check_cuda(name, smooth=smooth, s2=s2, proj_down_op6=proj_down_op6, weight=weight, weight_scale=weight_scale,
+                second=second, proj_up=proj_up, bias=bias)
+    if not x2.is_cuda:
+        raise SvdqOpError(f"{name}: x2 is on {x2.device}; the int4/int8 path runs on the GPU only")
+    m, k = int(x2.shape[0]), int(x2.shape[1])
+    if weight.dim() != 2 or int(weight.shape[1]) * 2 != k or not weight.is_contiguous():
+        raise SvdqOpError(f"{name}: weight must be contiguous [N, K/2 = {k // 2}], got {tuple(weight.shape)}")
+    n = int(weight.shape[0])
+    if tuple(weight_scale.shape) != (n, k // 64) or not weight_scale.is_contiguous():
+        raise SvdqOpError(f"{name}: weight_scale must be contiguous [N={n}, K/64={k // 64}], got "
+                          f"{tuple(weight_scale.shape)}")
+    if smooth is not None and smooth.numel() != k:
+        raise SvdqOpError(f"{name}: smooth has {smooth.numel()} values for K={k}")
+    if (proj_down_op6 is None) != (proj_up is None):
+        raise SvdqOpError(f"{name}: proj_down_op6 and proj_up must both be given or both be None")
+    rank = 0
+    if proj_up is not None:
+        rank = int(proj_up.shape[1])
+        if tuple(proj_up.shape) != (n, rank) or tuple(proj_down_op6.shape) != (k, rank):
+            raise SvdqOpError(f"{name}: proj_up {tuple(proj_up.shape)} / proj_down_op6 {tuple(proj_down_op6.shape)} "
+                              f"do not match [N={n}, r] / [K={k}, r]")
+    if bias is not None and bias.numel() != n:
+        raise SvdqOpError(f"{name}: bias has {bias.numel()} values for N={n}")
+    out = torch.empty(m, n, dtype=out_dtype, device=x2.device)
+    if m == 0:
+        return out
+    ws = torch.empty(max(int(nat.load().gwa_svdq_w4a4_linear_gemv_workspace(m, k, rank)), 256), dtype=torch.uint8,
+                     device=x2.device)
+    nat.call("gwa_svdq_w4a4_linear_gemv", nat.ptr(x2), int(x2.stride(0)), nat.ptr(smooth), nat.ptr(s2),
+             nat.ptr(proj_down_op6), rank, nat.ptr(weight), nat.ptr(weight_scale), nat.ptr(second),
+             0 if second is None else int(second.numel()), nat.ptr(proj_up), nat.ptr(bias), nat.ptr(out),
+             _dt_code(out_dtype), nat.EPI_GELU_TANH if gelu else 0, m, n, k, nat.ptr(ws), int(ws.numel()),
+             nat.stream_of(x2))
+    return out
+
+
+@svdq_forward_gemv.register_fake
+def _(x2, smooth, s2, proj_down_op6, weight, weight_scale, second, proj_up, bias, out_dtype, gelu):
+    return x2.new_empty(int(x2.shape[0]), int(weight.shape[0]), dtype=out_dtype)
+
+
 def _next_records(name: str, q6: Tensor, m: int, k: int, stage_offset: int) -> int:
     """Checks a record buffer [S, m, 104] that receives stages [stage_offset, stage_offset + k/128); returns the
     byte address of the first of them."""

@@ -172,6 +172,8 @@ class SvdqW4A4Linear(nn.Module):
         self.register_buffer("_one", torch.ones((), dtype=torch.float32, device=dev), persistent=False)
         # resident fast-lane operand records (derived from ``weight`` / ``weight_scale`` by refresh_derived)
         self.register_buffer("weight_fp6", None, persistent=False)
+        # token counts up to this run the small-M GEMV on ``weight`` itself (set with the fp6 records)
+        self._gemv_max_m = 0
 
     def refresh_derived(self) -> None:
         """Recompute the derived buffers after ``weight`` / ``proj_down`` change (GPU only): ``proj_down``
@@ -184,8 +186,10 @@ class SvdqW4A4Linear(nn.Module):
             self.proj_down_op6 = (torch.ops.cozy_gen_worker.svdq_prep_proj_down_fp6(self.proj_down)
                                   if on_gpu and fp6 else None)
         self.weight_fp6 = None
+        self._gemv_max_m = 0
         if fp6:
             self.weight_fp6 = torch.ops.cozy_gen_worker.svdq_pack_weight_fp6(self.weight, self.weight_scale)
+            self._gemv_max_m = ops.gemv_max_m(self.in_features, self.rank)
 
     def _apply(self, fn: Any, recurse: bool = True) -> "SvdqW4A4Linear":
         """Module moves and casts (``.to()``, ``.cuda()``, ``.cpu()``) copy buffers without the 1 KB of readable
@@ -238,6 +242,13 @@ class SvdqW4A4Linear(nn.Module):
         out_dtype = self.out_dtype or torch.bfloat16
         self._ensure_derived()
         gelu = self.activation == "gelu_tanh"
+        m = int(x2.shape[0])
+        if self.weight_fp6 is not None and 0 < m <= self._gemv_max_m:
+            # a few tokens (the DiT's modulation linears): the int4 weight streamed once by the GEMV
+            y = torch.ops.cozy_gen_worker.svdq_forward_gemv(
+                x2, self.smooth_factor, None, self.proj_down_op6 if self.rank else None, self.weight,
+                self.weight_scale, self.second, self.proj_up, self.bias, out_dtype, gelu)
+            return y.reshape(*shape[:-1], self.out_features)
         if self.weight_fp6 is not None:
             y = torch.ops.cozy_gen_worker.svdq_forward_fp6(
                 x2, self.smooth_factor, None, self.proj_down_op6 if self.rank else None, self.weight_fp6, self.second,
