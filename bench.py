@@ -154,8 +154,8 @@ def summarize_traffic(d: Path) -> int:
 def dit_step_pair(steps: int, warmup: int, modulation: str = "w4a4") -> dict:
     """Config 4: one Flux-dev-shaped denoiser forward (batch 1, 4096 image + 512 text tokens, 19 + 38
     blocks), every linear W4A4 rank 32 on the int4 lane (``modulation="awq"``: the one-token adaLN modulation
-    linears AWQ W4A16, as an svdq checkpoint stores them) vs the same model with bf16 nn.Linear GEMMs; bf16
-    SDPA in both. The W4A4 model is pinned to the int4 lane (the path being measured); the arming gate's own
+    linears AWQ W4A16, as an svdq checkpoint stores them) vs the same model with bf16 nn.Linear GEMMs; the
+    same attention kernel and block glue in both. The W4A4 model is pinned to the int4 lane (the path being measured); the arming gate's own
     decision on this box is reported beside it as ``gate_lane``. Each model's forward is captured once in a
     HIP graph and replayed ``steps`` times."""
     import gc
@@ -204,7 +204,7 @@ def bench_dit(args) -> int:
            "higher_is_better": False, "dtype": "int4", "data": "synthetic",
            "config": {"workload": "flux_dit_c4", "hidden": cfg.hidden, "heads": cfg.heads, "mlp": cfg.mlp,
                       "dual_blocks": cfg.n_dual, "single_blocks": cfg.n_single, "img_tokens": cfg.img_tokens,
-                      "txt_tokens": cfg.txt_tokens, "rank": cfg.rank, "attention": "bf16 SDPA",
+                      "txt_tokens": cfg.txt_tokens, "rank": cfg.rank, "attention": "bf16 flash attention (gwa_dit_attention)",
                       "modulation": ("W4A4 (one token)" if args.modulation == "w4a4"
                                      else "AWQ W4A16 g64 (one token)"),
                       "lane": res["w4a4_lane"], "gate_lane": res["gate_lane"],

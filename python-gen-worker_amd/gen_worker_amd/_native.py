@@ -87,6 +87,7 @@ _SIGNATURES: dict[str, tuple] = {
                              _i64, _i64, _flt, _vp),
     "gwa_dit_adaln_modulate": (_vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _flt, _vp),
     "gwa_dit_gate_residual": (_vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _vp),
+    "gwa_dit_attention": (_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _flt, _vp),
     "gwa_awq_w4a16_dequant": (_vp, _vp, _vp, _vp, _i64, _i64, _vp),
     "gwa_transpose_2d": (_vp, _vp, _i64, _i64, _i64, _vp),
     "gwa_nvfp4_blocked_scale_numel": (_i64, _i64),

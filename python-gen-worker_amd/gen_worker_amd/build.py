@@ -24,7 +24,7 @@ ARCH = "gfx950"
 
 SOURCES = ("gwa_runtime.hip", "act_quant.hip", "w4a4_gemm.hip", "w4a4_gemm_fp6.hip", "w4a4_gemm_fp6_pipe.hip",
            "w4a4_linear.hip", "w8a8_gemm.hip", "awq_w4a16.hip", "nvfp4.hip", "dit_block.hip",
-           "w4a4_gemv.hip")
+           "w4a4_gemv.hip", "dit_attention.hip")
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",

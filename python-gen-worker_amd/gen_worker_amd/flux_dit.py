@@ -22,9 +22,12 @@ Every linear is built by a factory, so the same model runs as:
     or ``lane=`` to pin it): in the dense lane each is served as its folded
     bf16 Linear, as the reference's swap does;
   * ``"bf16"``: every linear a bf16 ``nn.Linear`` (the bf16 GEMM path).
-Attention is bf16 ``scaled_dot_product_attention`` in both. Weights are
-random-init on the device from seeded generators; values are chosen only to
-keep activations finite and O(1) through the 57 blocks.
+Both models share the rest of the block: the fused glue kernels below (q/k
+RMSNorm + rotary, adaLN modulation, gated residual) and the attention kernel
+(``attention``: bf16 flash attention, the role of diffusers' SDPA call; the
+torch statement ``_sdpa`` is kept for the tests). Weights are random-init on
+the device from seeded generators; values are chosen only to keep activations
+finite and O(1) through the 57 blocks.
 """
 
 from __future__ import annotations
@@ -237,12 +240,35 @@ def qk_norm_rope(q: Tensor, k: Tensor, wq: Tensor, wk: Tensor, cos: Tensor, sin:
                  _native.stream_of(out_q))
 
 
-def _attention(q: Tensor, k: Tensor, v: Tensor) -> Tensor:
-    """[S, H, D] bf16 -> [S, H*D] via SDPA on [1, H, S, D]."""
+def _sdpa(q: Tensor, k: Tensor, v: Tensor) -> Tensor:
+    """torch's statement of the block attention: [S, H, D] bf16 -> [S, H*D] via SDPA on [1, H, S, D]."""
     s, h, d = q.shape
     o = F.scaled_dot_product_attention(q.transpose(0, 1).unsqueeze(0), k.transpose(0, 1).unsqueeze(0),
                                        v.transpose(0, 1).unsqueeze(0))
     return o.squeeze(0).transpose(0, 1).reshape(s, h * d)
+
+
+def attention(q: Tensor, k: Tensor, v: Tensor) -> Tensor:
+    """Joint self-attention of a block (``gwa_dit_attention``): q, k, v bf16 [S, H, 128] with unit head and
+    element strides (token strides free: v may be a column slice of a fused qkv output) -> [S, H * 128]."""
+    from . import _native
+
+    s, h, d = q.shape
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        if (t.dtype != torch.bfloat16 or not t.is_cuda or t.dim() != 3 or tuple(t.shape[1:]) != (h, d)
+                or t.stride(2) != 1 or t.stride(1) != d):
+            raise ValueError(f"attention {name}: bf16 CUDA [tokens, {h}, {d}] with unit head / element strides "
+                             f"expected, got {tuple(t.shape)} strides {t.stride()} {t.dtype}")
+    if k.shape[0] != v.shape[0]:
+        raise ValueError(f"attention: {k.shape[0]} keys, {v.shape[0]} values")
+    out = torch.empty(s, h * d, device=q.device, dtype=torch.bfloat16)
+    _native.call("gwa_dit_attention", _native.ptr(q), q.stride(0), _native.ptr(k), k.stride(0), _native.ptr(v),
+                 v.stride(0), _native.ptr(out), h * d, s, k.shape[0], h, d, 1.0 / math.sqrt(d),
+                 _native.stream_of(q))
+    return out
+
+
+_attention = attention
 
 
 def _mlp(fc1: nn.Module, fc2: nn.Module, x: Tensor, fused: bool) -> Tensor:
