@@ -1,7 +1,7 @@
 """Benchmark of the SVDQuant W4A4 linear hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-    python bench.py --only {step,gemm,quant,copy,awq,w8a8,w8a8_gemm} [--iters N] (profiling driver)
+    python bench.py --only {step,gemm,quant,copy,awq,w8a8,w8a8_gemm,dit} [--iters N] (profiling driver)
     python bench.py --workload {mlp,qkv,dit,mod,nvfp4,w8a8}  (configs 2-4, modulation layers, nvfp4 lane,
                                                               the int8 GEMM sweep)
 
@@ -553,6 +553,30 @@ def only_awq(args) -> int:
     return 0
 
 
+def only_dit(args) -> int:
+    """``--only dit``: the config-4 W4A4 DiT (int4 lane) forward eagerly ``--iters`` times after 2 warmups,
+    for rocprofv3 (each forward's kernels; the model's construction runs before them)."""
+    import torch
+
+    import gen_worker_amd  # noqa: F401
+    from gen_worker_amd import _native
+    from gen_worker_amd.flux_dit import FluxDiT, FluxDiTConfig, inputs
+
+    _native.load()
+    cfg = FluxDiTConfig()
+    model = FluxDiT("w4a4", cfg, modulation=args.modulation, lane="int4")
+    x = inputs(cfg)
+    with torch.no_grad():
+        for _ in range(2):
+            model(*x)
+        torch.cuda.synchronize()
+        for i in range(args.iters):
+            model(*x)
+            torch.cuda.synchronize()
+            log(f"bench: dit forward {i}")
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -560,7 +584,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-rows", type=int, default=512, help="rows of the bounded CPU sample")
-    ap.add_argument("--only", choices=("step", "gemm", "quant", "copy", "awq", "w8a8", "w8a8_gemm"), default=None)
+    ap.add_argument("--only", choices=("step", "gemm", "quant", "copy", "awq", "w8a8", "w8a8_gemm", "dit"),
+                    default=None)
     ap.add_argument("--iters", type=int, default=5)
     ap.add_argument("--tile", type=int, default=-1,
                     help="with --only gemm/step: force the fp6 GEMM's output tile (GWA_FP6_TILE_*; -1: the model's); "
@@ -585,6 +610,8 @@ def main() -> int:
         return summarize_traffic(Path(args.summarize_traffic))
     if args.only == "awq":
         return only_awq(args)
+    if args.only == "dit":
+        return only_dit(args)
     if args.workload != "c1":
         if args.gpus != 1:
             print("bench.py measures one GPU only", file=sys.stderr)
