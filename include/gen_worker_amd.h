@@ -197,7 +197,7 @@ int64_t gwa_svdq_gemm_w4a4_fp6_next_partials(int64_t M, int64_t N);
  * reference's Triton GEMM autotunes its tile (models/svdq_fused.py:157-178). */
 enum {
   GWA_FP6_TILE_256x256 = 0, GWA_FP6_TILE_256x128 = 1, GWA_FP6_TILE_128x128 = 2, GWA_FP6_TILE_192x256 = 3,
-  GWA_FP6_TILE_288x192 = 4, GWA_FP6_TILE_256x192 = 5
+  GWA_FP6_TILE_288x192 = 4, GWA_FP6_TILE_256x192 = 5, GWA_FP6_TILE_64x128 = 6
 };
 int gwa_svdq_gemm_w4a4_fp6_tile(int64_t M, int64_t N);
 

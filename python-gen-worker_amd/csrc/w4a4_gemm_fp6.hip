@@ -62,10 +62,13 @@ namespace {
 // Tile configurations: TN = 128 (64 x 64 wave tiles, registers for the
 // software pipeline, four stage buffers) or TN = 256 (64 x 128 wave tiles,
 // each staged byte feeds twice the outputs, three stage buffers, blocks run
-// back to back).
+// back to back); the 64 x 128 tile has one 32 x 32 block per wave and three
+// stage buffers (61 KB), so two workgroups share a CU: small grids (M = 256)
+// spread over twice the workgroups of the 128 x 128 tile.
 template <int TM, int TN>
 struct Cfg {
-  static constexpr int WBN = 2;
+  static constexpr bool SMALL = TM == 64;
+  static constexpr int WBN = SMALL ? 1 : 2;
   static constexpr int WAVES_N = TN / (32 * WBN);
   static constexpr int WAVES_M = NWAVES / WAVES_N;
   static constexpr int WBM = TM / (32 * WAVES_M);
@@ -74,7 +77,7 @@ struct Cfg {
   static constexpr int LDS_X = (TM * REC + 1023) / 1024 * 1024, OFF_W = LDS_X, LDS_W = TN * REC;
   static constexpr int STAGE = LDS_X + LDS_W;
   static constexpr int NB0 = (kLdsBytes - 2 * TN * 4) / STAGE;
-  static constexpr int NBUF = NB0 > 4 ? 4 : NB0;   // stage buffers; DMA runs NBUF - 1 stages ahead
+  static constexpr int NBUF = SMALL ? 3 : NB0 > 4 ? 4 : NB0;  // stage buffers; DMA runs NBUF - 1 stages ahead
   static constexpr int RUNS = STAGE / 1024;        // 1 KiB DMA runs (64 lanes x 16 B) per stage
   static constexpr int DMA_X = LDS_X / 1024;
   static constexpr int SLOTS = (RUNS + NWAVES - 1) / NWAVES;  // per wave and stage
@@ -85,7 +88,7 @@ struct Cfg {
 };
 
 template <int TM, int TN, int RB, bool GELU, bool OUT_F16, bool NQ>
-__global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_kernel(
+__global__ __launch_bounds__(NTHREADS, (TM == 64 ? 4 : 1)) void w4a4_gemm_fp6_kernel(
     const uint8_t* __restrict__ qa, const uint8_t* __restrict__ qw, const float* __restrict__ s2p,
     const float* __restrict__ second, int second_per_channel, const void* __restrict__ la, int la_f32,
     const uint16_t* __restrict__ up, const uint16_t* __restrict__ bias, uint16_t* __restrict__ out, int M, int N,
@@ -720,7 +723,7 @@ namespace {
 // (w4a4_gemm_fp6_pipe.hip)
 enum Fp6Tile {
   kTile256x256 = 0, kTile256x128 = 1, kTile128x128 = 2, kTile192x256 = 3, kTile288x192 = 4, kTile256x192 = 5,
-  kTileCount = 6
+  kTile64x128 = 6, kTileCount = 7
 };
 bool fp6_tile_pipelined(int tile) { return tile == kTile288x192 || tile == kTile256x192; }
 
@@ -738,6 +741,8 @@ void launch_fp6_rb(int tile, dim3 grid, hipStream_t s, const GwaFp6Args& a, cons
     launch_fp6_tile<192, 256, RB, GL, F16, false>(grid, s, a, nx);
   else if (NQ || tile == kTile256x128)
     launch_fp6_tile<256, 128, RB, GL, F16, NQ>(grid, s, a, nx);
+  else if (tile == kTile64x128)
+    launch_fp6_tile<64, 128, RB, GL, F16, false>(grid, s, a, nx);
   else
     launch_fp6_tile<128, 128, RB, GL, F16, false>(grid, s, a, nx);
 }
@@ -757,20 +762,23 @@ void launch_fp6_flags(int tile, bool gelu, bool f16, bool nq, dim3 grid, hipStre
   }
 }
 
-// One workgroup per CU (the stage buffers fill the LDS), so a grid runs in rounds of kCus tiles. A grid takes
-// the tile shape with the least estimated time: rounds x the tile's MACs x its time per MAC relative to the
-// 256 x 256 tile (one round of each at M=256, N=9216, K=3072: 51.4, 31.9, 23.0 us for 36 256 x 256, 72
-// 256 x 128 and 144 128 x 128 tiles; at M=1024: 54.3 and 44.0 us for 144 256 x 256 and 216 192 x 256
-// tiles; one round of the 288 x 192 and 256 x 192 tiles at K=3072: 54.3 and 43.9 us against 54.9 and 54.6 us
-// for the 256 x 256 tile). The next-layer epilogue needs the 256-row, 256- or 128-column tiles.
+// One workgroup per CU (the stage buffers fill the LDS; the 64 x 128 tile fits twice), so a grid runs in
+// rounds of kCus tiles. A grid takes the tile shape with the least estimated time: rounds x the tile's MACs x
+// its time per MAC relative to the 256 x 256 tile (one round of each at M=256, N=9216, K=3072: 51.4, 31.9,
+// 23.0 us for 36 256 x 256, 72 256 x 128 and 144 128 x 128 tiles; at M=1024: 54.3 and 44.0 us for 144
+// 256 x 256 and 216 192 x 256 tiles; one round of the 288 x 192 and 256 x 192 tiles at K=3072: 54.3 and
+// 43.9 us against 54.9 and 54.6 us for the 256 x 256 tile; 64 x 128: 15.5 us alone on a CU, 23.0 us with two
+// to a CU). The next-layer epilogue needs the 256-row, 256- or 128-column tiles.
 constexpr int kCus = 256;
 struct Fp6Shape {
   int tile, tm, tn;
-  double per_mac;
+  double per_mac;         // one workgroup per CU
+  double per_mac_shared;  // two workgroups on a CU (0: the tile fills a CU's LDS)
 };
-constexpr Fp6Shape kFp6Shapes[kTileCount] = {{kTile256x256, 256, 256, 1.0},  {kTile256x128, 256, 128, 1.24},
-                                             {kTile128x128, 128, 128, 1.80}, {kTile192x256, 192, 256, 1.08},
-                                             {kTile288x192, 288, 192, 1.17}, {kTile256x192, 256, 192, 1.07}};
+constexpr Fp6Shape kFp6Shapes[kTileCount] = {
+    {kTile256x256, 256, 256, 1.0, 0},  {kTile256x128, 256, 128, 1.24, 0}, {kTile128x128, 128, 128, 1.80, 0},
+    {kTile192x256, 192, 256, 1.08, 0}, {kTile288x192, 288, 192, 1.17, 0}, {kTile256x192, 256, 192, 1.07, 0},
+    {kTile64x128, 64, 128, 2.26, 3.35}};
 std::atomic<int> g_force_tile{-1};  // test / tuning hook (gwa_svdq_gemm_w4a4_fp6_force_tile)
 
 bool fp6_tile_allowed(int tile, bool nq) { return !nq || tile == kTile256x256 || tile == kTile256x128; }
@@ -783,7 +791,10 @@ int fp6_tile(int64_t M, int64_t N, bool nq) {
   for (const Fp6Shape& sh : kFp6Shapes) {
     if (!fp6_tile_allowed(sh.tile, nq)) continue;
     const int64_t tiles = ((M + sh.tm - 1) / sh.tm) * ((N + sh.tn - 1) / sh.tn);
-    const double t = (double)((tiles + kCus - 1) / kCus) * sh.tm * sh.tn * sh.per_mac;
+    // a tile that fits twice on a CU runs alone while the grid fits the CUs, two to a CU beyond that
+    const double t = sh.per_mac_shared == 0.0 || tiles <= kCus
+                         ? (double)((tiles + kCus - 1) / kCus) * sh.tm * sh.tn * sh.per_mac
+                         : (double)((tiles + 2 * kCus - 1) / (2 * kCus)) * sh.tm * sh.tn * sh.per_mac_shared;
     if (sh.tile == kTile256x256 || t < best_t * 0.999) {
       best = sh.tile;
       best_t = t;

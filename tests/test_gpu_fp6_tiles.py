@@ -18,7 +18,7 @@ from oracle import svdq_oracle as O
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
-TILES = {0: (256, 256), 1: (256, 128), 2: (128, 128), 3: (192, 256), 4: (288, 192), 5: (256, 192)}
+TILES = {0: (256, 256), 1: (256, 128), 2: (128, 128), 3: (192, 256), 4: (288, 192), 5: (256, 192), 6: (64, 128)}
 
 
 @pytest.fixture(scope="module", autouse=True)

@@ -44,7 +44,8 @@ def test_library_is_a_gfx950_code_object():
 
 def test_fp6_tile_model_choices():
     """The tile model (host code only): 288-row tiles for 4608-token layers (one tile per CU at N=3072),
-    256 x 192 for 4096 tokens, small tiles for short inputs, the forced tile while one is set."""
+    256 x 192 for 4096 tokens, 256 x 128 at 512 tokens and wide outputs, the 64 x 128 tile (two to a CU) for
+    short inputs, the forced tile while one is set."""
     from gen_worker_amd import _native
 
     lib = _native.load()
@@ -52,7 +53,10 @@ def test_fp6_tile_model_choices():
     assert tile(0, 3072) == -1 and tile(16, 0) == -1
     assert tile(4608, 3072) == 4 and tile(4608, 9216) == 4
     assert tile(4096, 3072) == 5
-    assert tile(1024, 3072) == 2
+    assert tile(512, 9216) == 1 and tile(512, 12288) == 1
+    # 96 / 192 / 384 64 x 128 tiles against 48 / 96 / 192 128 x 128 ones (15.5 vs 21.8 us measured at 256)
+    assert tile(256, 3072) == 6 and tile(512, 3072) == 6 and tile(1024, 3072) == 6
+    assert tile(256, 9216) == 6 and tile(256, 12288) == 6
     prev = lib.gwa_svdq_gemm_w4a4_fp6_force_tile(1)
     try:
         assert tile(4608, 3072) == 1
