@@ -4,41 +4,53 @@
 // FluxAttnProcessor calls; here the vendor kernel ran at ~0.49 PFLOP/s).
 //
 // Work split: a 256-thread workgroup owns 128 queries of one head (4 waves x 32 queries) and walks the keys
-// in tiles of 64. Per tile, K [64 keys][128] and V transposed [128][64 keys] are staged in LDS (double
-// buffered; the next tile's global loads are issued before the current tile's MFMAs and written to the other
-// buffers after them, one barrier per tile). Each wave computes, with bf16 MFMA 32x32x16 and fp32
-// accumulation:
+// in tiles of 64. K and V tiles ([64 keys][128], as stored) are copied global -> LDS by direct-to-LDS
+// buffer loads (no staging registers, no LDS writes), double buffered: tile t+1's copies are issued before
+// tile t's MFMAs, one wait and one barrier per tile. The 16-byte chunks of a row are XOR-swizzled by the
+// row at copy time (each lane fetches the chunk that belongs at its LDS slot), so the reads below are free
+// of bank conflicts. Each wave computes, with bf16 MFMA 32x32x16 and fp32 accumulation:
 //   S^T = K_tile q^T            (keys x queries: a lane holds one query and 16 keys of each 32-key half)
 //   p   = exp2(S * c - m)       (c = log2(e) / sqrt(128), m the query's running max: the two lane halves
 //                                exchange their maxima; O is rescaled only in tiles where some lane's max
 //                                moved; the row sums stay per lane until the end)
 //   O^T = O^T * exp2(m_old - m) + V^T p^T   (head_dim x queries: a lane holds one query's 64 outputs)
-// The key order inside a 16-key MFMA step is the one S^T's output layout leaves p in, and V^T is read in the
-// same order, so p goes from the S MFMA to the O MFMA without leaving registers. Output o = O / l in bf16,
-// written as rows [query][head][128] (the layout the next linear reads).
-#include "gwa_common.h"
+// The V^T operand comes straight from the row-major V tile through ds_read_b64_tr_b16: in each 16-lane group
+// lane i receives element e of the 8-byte read of lane 4e + i/4, column i % 4, so lanes that point at 4 keys
+// x 16 head-dim columns hand each lane 4 keys of one column. The key order inside a 16-key MFMA step is the
+// one S^T's output layout leaves p in, so p goes from the S MFMA to the O MFMA without leaving registers.
+// Output o = O / l in bf16, written as rows [query][head][128] (the layout the next linear reads).
+#include "fp6_gemm_common.h"
 
 namespace {
 
 constexpr int AT_D = 128, AT_BM = 128, AT_BN = 64, AT_THREADS = 256;
-constexpr int AT_KROW = AT_D * 2 + 16;                 // K tile row bytes (272: conflict-free 16-byte reads)
-constexpr int AT_VROW = AT_BN * 2 + 16;                // V^T tile row bytes (144: conflict-free 16-byte reads)
-constexpr int AT_KBYTES = AT_BN * AT_KROW;             // 17408
-constexpr int AT_VBYTES = AT_D * AT_VROW;              // 18432
-constexpr int AT_STAGE = AT_KBYTES + AT_VBYTES;
-constexpr int AT_LDS = 2 * AT_STAGE;                   // 71680
+constexpr int AT_ROW = AT_D * 2;                       // tile row bytes (256), chunks swizzled, no padding
+constexpr int AT_TILE = AT_BN * AT_ROW;                // 16 KB per K or V tile
+constexpr int AT_STAGE = 2 * AT_TILE;                  // K then V
+constexpr int AT_LDS = 2 * AT_STAGE;                   // 64 KB
 
 typedef float v16f_ __attribute__((ext_vector_type(16)));
-constexpr float kLazy = 0.0f;   // log2 headroom of the running max before it moves (0: the exact running max)
+typedef short v4s_ __attribute__((ext_vector_type(4)));
+typedef short v2s_ __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ uint32_t pack_bf16_pair(float a, float b) { return pack_bf16x2_rn(a, b); }
+
+// 16-byte chunk slot of chunk ch in tile row r: K rows XOR the row's low 4 bits (16-byte reads by 16 rows
+// hit distinct banks), V rows XOR an even value (the two chunks of a 32-byte run stay adjacent for the
+// transposing 8-byte reads, which take 4 rows x 32 bytes per 16-lane group)
+__device__ __forceinline__ int k_slot(int ch, int r) { return ch ^ (r & 15); }
+__device__ __forceinline__ int v_slot(int ch, int r) { return ch ^ (2 * (r & 7)); }
+
+__device__ __forceinline__ v4s_ lds_read_tr(const uint8_t* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s_*)(uintptr_t)p);
+}
 
 __global__ __launch_bounds__(AT_THREADS, 2) void dit_attention_kernel(
     const uint16_t* __restrict__ q, int64_t ldq, const uint16_t* __restrict__ k, int64_t ldk,
     const uint16_t* __restrict__ v, int64_t ldv, uint16_t* __restrict__ o, int64_t ldo, int S, int Skv,
     float c_log2) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[AT_LDS];
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[AT_LDS];
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int j = lane & 31, h = lane >> 5;              // MFMA column (query / key / head-dim row) and half
   const int head = blockIdx.y;
   const int q0 = blockIdx.x * AT_BM + wave * 32;
@@ -53,93 +65,72 @@ __global__ __launch_bounds__(AT_THREADS, 2) void dit_attention_kernel(
     for (int cd = 0; cd < 8; ++cd) qop[cd] = q_ok ? *(const v4i*)(qp + 16 * cd) : (v4i){0, 0, 0, 0};
   }
 
-  // staging of one key tile: K rows (tid: 4 chunks of 16 bytes of [64 keys][128]), V^T (a lane takes two
-  // keys 2p, 2p+1 and two 8-column chunks, writes key-pair dwords into V^T rows). Buffer loads: each lane's
-  // offsets are fixed, the tile's rows come in through the scalar offset.
-  const rsrc_t kbuf = make_rsrc(k, (uint32_t)(((int64_t)(Skv - 1) * ldk + gridDim.y * AT_D) * 2));
-  const rsrc_t vbuf = make_rsrc(v, (uint32_t)(((int64_t)(Skv - 1) * ldv + gridDim.y * AT_D) * 2));
-  v4i kreg[4], vreg[4];
-  const int vp = lane & 31;                            // key pair of this lane
+  // copies: 16 runs of 1 KB (4 rows) per K tile and per V tile, runs wave, wave + 4, ... of each; lane l of a
+  // run lands at LDS slot l % 16 of row 4 run + l / 16 and fetches the chunk that belongs there
+  const v4i kbuf = raw_rsrc(k, (uint32_t)(((int64_t)(Skv - 1) * ldk + gridDim.y * AT_D) * 2));
+  const v4i vbuf = raw_rsrc(v, (uint32_t)(((int64_t)(Skv - 1) * ldv + gridDim.y * AT_D) * 2));
   uint32_t koff[4], voff[4];
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
-    const int c = u * AT_THREADS + tid;                // K chunk: key c / 16, columns 8 (c % 16) ..
-    koff[u] = (uint32_t)(((c >> 4) * ldk + head * AT_D + 8 * (c & 15)) * 2);
-    // V: key 2vp + (u & 1), 8-column chunk 4 wave + h + 2 (u >> 1)
-    voff[u] = (uint32_t)(((2 * vp + (u & 1)) * ldv + head * AT_D + 8 * (4 * wave + h + 2 * (u >> 1))) * 2);
+    const int run = wave + 4 * u, row = 4 * run + (lane >> 4), slot = lane & 15;
+    koff[u] = (uint32_t)((row * ldk + head * AT_D + 8 * k_slot(slot, row)) * 2);
+    voff[u] = (uint32_t)((row * ldv + head * AT_D + 8 * v_slot(slot, row)) * 2);
   }
-  auto load_k = [&](int t) __attribute__((always_inline)) {
-    const uint32_t ks = (uint32_t)((int64_t)t * AT_BN * ldk * 2);
-#pragma unroll
-    for (int u = 0; u < 4; ++u) kreg[u] = __builtin_amdgcn_raw_buffer_load_b128(kbuf, koff[u], ks, 0);
-  };
-  auto load_v = [&](int t) __attribute__((always_inline)) {
-    const uint32_t vs = (uint32_t)((int64_t)t * AT_BN * ldv * 2);
-#pragma unroll
-    for (int u = 0; u < 4; ++u) vreg[u] = __builtin_amdgcn_raw_buffer_load_b128(vbuf, voff[u], vs, 0);
-  };
-  // V^T key positions: bits 2 and 3 of a key's index in the tile swapped, so the 8 keys of a lane's 16-key
-  // MFMA step (16c + 4h + 0..3 and 16c + 8 + 4h + 0..3) sit at 16c + 8h + 0..7: one 16-byte read
-  const uint32_t vpos = (uint32_t)(((2 * vp) & ~12) | (((2 * vp) & 4) << 1) | (((2 * vp) & 8) >> 1)) * 2;
-  // LDS: K buffers 0, 1, then V^T buffers 0, 1
-  auto kbuf_at = [&](int b) __attribute__((always_inline)) { return lds + b * AT_KBYTES; };
-  auto vbuf_at = [&](int b) __attribute__((always_inline)) { return lds + 2 * AT_KBYTES + b * AT_VBYTES; };
-  auto store_k = [&](int b) __attribute__((always_inline)) {
-    uint8_t* kb = kbuf_at(b);
+  auto issue = [&](int t, int b) __attribute__((always_inline)) {
+    uint8_t* kb = lds + b * AT_STAGE;
+    const uint32_t ks = (uint32_t)((int64_t)t * AT_BN * ldk * 2), vs = (uint32_t)((int64_t)t * AT_BN * ldv * 2);
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const int c = u * AT_THREADS + tid;
-      *(v4i*)(kb + (c >> 4) * AT_KROW + 16 * (c & 15)) = kreg[u];
+      const int run = wave + 4 * u;
+      dma16(kbuf, (uint32_t)(uintptr_t)(kb + run * 1024), koff[u], ks);
+      dma16(vbuf, (uint32_t)(uintptr_t)(kb + AT_TILE + run * 1024), voff[u], vs);
     }
   };
-  auto store_v = [&](int b) __attribute__((always_inline)) {
-    uint8_t* vb = vbuf_at(b);
+
+  // read offsets, loop-invariant: K rows 32 sb + j, chunks 2 cd + h; V^T operand (d block db, 16-key step c):
+  // lane p = lane % 16 of group g = lane / 16 (half hh = g / 2, column half dh = g % 2) points at key
+  // 16 c + 4 hh + p / 4 (+ 8 for the second read), columns 32 db + 16 dh + 4 (p % 4) .. + 4
+  uint32_t kro[2][8];
 #pragma unroll
-    for (int cc = 0; cc < 2; ++cc) {
-      const v4i a = vreg[2 * cc], bb = vreg[2 * cc + 1];  // keys 2vp, 2vp + 1 of columns 8 (4 wave + h + 2 cc) ..
+  for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t lo = __builtin_amdgcn_perm((uint32_t)bb[e], (uint32_t)a[e], 0x05040100u);  // column 2e
-        const uint32_t hi = __builtin_amdgcn_perm((uint32_t)bb[e], (uint32_t)a[e], 0x07060302u);  // column 2e+1
-        const int col = 8 * (4 * wave + h + 2 * cc) + 2 * e;
-        *(uint32_t*)(vb + col * AT_VROW + vpos) = lo;
-        *(uint32_t*)(vb + (col + 1) * AT_VROW + vpos) = hi;
+    for (int cd = 0; cd < 8; ++cd) {
+      const int row = 32 * sb + j;
+      kro[sb][cd] = (uint32_t)(row * AT_ROW + 16 * k_slot(2 * cd + h, row));
+    }
+  const int pg = lane & 15, hh = lane >> 5, dh = (lane >> 4) & 1;
+  uint32_t vro[4][4][2];
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int hb = 0; hb < 2; ++hb) {
+        const int row = 16 * c + 8 * hb + 4 * hh + (pg >> 2);
+        const int col = 32 * db + 16 * dh + 4 * (pg & 3);          // bf16 column; 8-byte piece of a chunk
+        vro[c][db][hb] = (uint32_t)(AT_TILE + row * AT_ROW + 16 * v_slot(col >> 3, row) + 2 * (col & 7));
       }
-    }
-  };
-  // S^T of one key tile (the two 32-key halves' MFMA chains interleaved)
-  auto s_tile = [&](int b, v16f_* s) __attribute__((always_inline)) {
-    s[0] = (v16f_){};
-    s[1] = (v16f_){};
-    const uint8_t* kr = kbuf_at(b) + j * AT_KROW + 16 * h;
-#pragma unroll
-    for (int cd = 0; cd < 8; ++cd)
-#pragma unroll
-      for (int sb = 0; sb < 2; ++sb)
-        s[sb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*(const v8bf*)(kr + 32 * sb * AT_KROW + 32 * cd),
-                                                        __builtin_bit_cast(v8bf, qop[cd]), s[sb], 0, 0, 0);
-  };
 
   v16f_ oacc[4];
 #pragma unroll
   for (int db = 0; db < 4; ++db) oacc[db] = (v16f_){};
   float m_run = -INFINITY, l_run = 0.0f;
 
-  // Iteration t: tile t+1's global loads go out first, tile t's S, softmax and p v run on the LDS copies,
-  // then tile t+1 is written into the other buffers (last read in iteration t-1) and one barrier follows.
   const int ntiles = Skv / AT_BN;
-  load_k(0);
-  load_v(0);
-  store_k(0);
-  store_v(0);
-  __syncthreads();
+  issue(0, 0);
+  wait_vm_lgkm0<0>();
+  barrier_lds();
   for (int t = 0; t < ntiles; ++t) {
-    if (t + 1 < ntiles) {
-      load_k(t + 1);
-      load_v(t + 1);
-    }
-    v16f_ sc[2];
-    s_tile(t & 1, sc);
+    const uint8_t* kb = lds + (t & 1) * AT_STAGE;
+    if (t + 1 < ntiles) issue(t + 1, (t + 1) & 1);
+    // S^T for the two 32-key halves of the tile (the two chains interleaved)
+    v16f_ sc[2] = {(v16f_){}, (v16f_){}};
+#pragma unroll
+    for (int cd = 0; cd < 8; ++cd)
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb)
+        sc[sb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*(const v8bf*)(kb + kro[sb][cd]),
+                                                         __builtin_bit_cast(v8bf, qop[cd]), sc[sb], 0, 0, 0);
     // online softmax of tile t (scaled domain: x = s * c_log2); max of the lane's 32 scores as a tree
     float m8[8];
 #pragma unroll
@@ -149,10 +140,8 @@ __global__ __launch_bounds__(AT_THREADS, 2) void dit_attention_kernel(
 #pragma unroll
       for (int i = 0; i < w; ++i) m8[i] = fmaxf(m8[i], m8[i + w]);
     const float mx = fmaxf(m8[0], __shfl_xor(m8[0], 32));
-    // the running max moves when a score exceeds it by more than kLazy (log2 units; p <= 2^kLazy otherwise,
-    // and O and l share the reference, so o = O / l does not depend on it); O is rescaled only then
     const float x_max = mx * c_log2;
-    const bool bump = x_max > m_run + kLazy;
+    const bool bump = x_max > m_run;
     const float m_new = bump ? x_max : m_run;
     const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 on the first tile (m_run = -inf)
     m_run = m_new;
@@ -174,21 +163,20 @@ __global__ __launch_bounds__(AT_THREADS, 2) void dit_attention_kernel(
 #pragma unroll
       for (int db = 0; db < 4; ++db) oacc[db] *= alpha;
     }
-    // O^T += V^T p^T: V^T row d = 32 db + j, positions 16 c + 8 h .. + 8 (keys 16 c + 4 h .. + 4 and
-    // 16 c + 8 + 4 h .. + 4)
+    // O^T += V^T p^T, the V^T operand by two transposing reads (keys 16 c + 4 hh .. + 4 and + 8)
 #pragma unroll
-    for (int db = 0; db < 4; ++db) {
-      const uint8_t* vr = vbuf_at(t & 1) + (32 * db + j) * AT_VROW + 16 * h;
+    for (int db = 0; db < 4; ++db)
 #pragma unroll
-      for (int c = 0; c < 4; ++c)
-        oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*(const v8bf*)(vr + 32 * c),
-                                                           __builtin_bit_cast(v8bf, pop[c]), oacc[db], 0, 0, 0);
-    }
-    if (t + 1 < ntiles) {
-      store_k((t + 1) & 1);
-      store_v((t + 1) & 1);
-    }
-    __syncthreads();
+      for (int c = 0; c < 4; ++c) {
+        const v4s_ a0 = lds_read_tr(kb + vro[c][db][0]), a1 = lds_read_tr(kb + vro[c][db][1]);
+        const v8bf av = __builtin_bit_cast(v8bf, (v4i){__builtin_bit_cast(int, (v2s_){a0[0], a0[1]}),
+                                                      __builtin_bit_cast(int, (v2s_){a0[2], a0[3]}),
+                                                      __builtin_bit_cast(int, (v2s_){a1[0], a1[1]}),
+                                                      __builtin_bit_cast(int, (v2s_){a1[2], a1[3]})});
+        oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(v8bf, pop[c]), oacc[db], 0, 0, 0);
+      }
+    wait_vm_lgkm0<0>();  // this wave's copies of tile t + 1 have landed
+    barrier_lds();       // everyone's have; everyone is done reading tile t's buffer
   }
   // o = O / l (the two lane halves hold the row sum's two halves)
   const float l_tot = l_run + __shfl_xor(l_run, 32);
