@@ -514,7 +514,7 @@ int gwa_dit_gate_residual(const void* x, int64_t ldx, const void* y, int64_t ldy
  * v[t][h], fp32 accumulation, bf16 q / k / v / o as rows [token][head][128]
  * with token strides ldq / ldk / ldv / ldo (elements). One pass over the keys
  * with an online softmax; p is rounded to bf16 for the p v product.
- * head_dim == 128, Skv % 64 == 0, q / k / v 16-byte aligned. */
+ * head_dim == 128, Skv >= 1, q / k / v 16-byte aligned. */
 int gwa_dit_attention(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv, void* o,
                       int64_t ldo, int64_t S, int64_t Skv, int64_t heads, int64_t head_dim, float scale,
                       void* stream);

@@ -76,14 +76,22 @@ __global__ __launch_bounds__(AT_THREADS, 2) void dit_attention_kernel(
     koff[u] = (uint32_t)((row * ldk + head * AT_D + 8 * k_slot(slot, row)) * 2);
     voff[u] = (uint32_t)((row * ldv + head * AT_D + 8 * v_slot(slot, row)) * 2);
   }
-  auto issue = [&](int t, int b) __attribute__((always_inline)) {
+  // tile t into stage buffer b; a last tile with rv < 64 keys repeats its last key in the rows past it (their
+  // scores are masked to -inf below, so they weigh 0)
+  auto issue = [&](int t, int b, int rv) __attribute__((always_inline)) {
     uint8_t* kb = lds + b * AT_STAGE;
     const uint32_t ks = (uint32_t)((int64_t)t * AT_BN * ldk * 2), vs = (uint32_t)((int64_t)t * AT_BN * ldv * 2);
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int run = wave + 4 * u;
-      dma16(kbuf, (uint32_t)(uintptr_t)(kb + run * 1024), koff[u], ks);
-      dma16(vbuf, (uint32_t)(uintptr_t)(kb + AT_TILE + run * 1024), voff[u], vs);
+      uint32_t ko = koff[u], vo = voff[u];
+      if (rv < AT_BN) {  // workgroup-uniform: the last, partial tile
+        const int row = 4 * run + (lane >> 4), slot = lane & 15, src = min(row, rv - 1);
+        ko = (uint32_t)((src * ldk + head * AT_D + 8 * k_slot(slot, row)) * 2);
+        vo = (uint32_t)((src * ldv + head * AT_D + 8 * v_slot(slot, row)) * 2);
+      }
+      dma16(kbuf, (uint32_t)(uintptr_t)(kb + run * 1024), ko, ks);
+      dma16(vbuf, (uint32_t)(uintptr_t)(kb + AT_TILE + run * 1024), vo, vs);
     }
   };
 
@@ -116,13 +124,14 @@ __global__ __launch_bounds__(AT_THREADS, 2) void dit_attention_kernel(
   for (int db = 0; db < 4; ++db) oacc[db] = (v16f_){};
   float m_run = -INFINITY, l_run = 0.0f;
 
-  const int ntiles = Skv / AT_BN;
-  issue(0, 0);
+  const int ntiles = (Skv + AT_BN - 1) / AT_BN;
+  const int rv_last = Skv - (ntiles - 1) * AT_BN;      // keys in the last tile (1 .. 64)
+  issue(0, 0, ntiles == 1 ? rv_last : AT_BN);
   wait_vm_lgkm0<0>();
   barrier_lds();
   for (int t = 0; t < ntiles; ++t) {
     const uint8_t* kb = lds + (t & 1) * AT_STAGE;
-    if (t + 1 < ntiles) issue(t + 1, (t + 1) & 1);
+    if (t + 1 < ntiles) issue(t + 1, (t + 1) & 1, t + 2 == ntiles ? rv_last : AT_BN);
     // S^T for the two 32-key halves of the tile (the two chains interleaved)
     v16f_ sc[2] = {(v16f_){}, (v16f_){}};
 #pragma unroll
@@ -131,6 +140,13 @@ __global__ __launch_bounds__(AT_THREADS, 2) void dit_attention_kernel(
       for (int sb = 0; sb < 2; ++sb)
         sc[sb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*(const v8bf*)(kb + kro[sb][cd]),
                                                          __builtin_bit_cast(v8bf, qop[cd]), sc[sb], 0, 0, 0);
+    if (t + 1 == ntiles && rv_last < AT_BN) {  // keys past Skv: score -inf (lane's key 32 sb + 8 a + 4 h + r)
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (32 * sb + 8 * (i >> 2) + 4 * h + (i & 3) >= rv_last) sc[sb][i] = -INFINITY;
+    }
     // online softmax of tile t (scaled domain: x = s * c_log2); max of the lane's 32 scores as a tree
     float m8[8];
 #pragma unroll
@@ -202,9 +218,8 @@ extern "C" int gwa_dit_attention(const void* q, int64_t ldq, const void* k, int6
                                  int64_t head_dim, float scale, void* stream) {
   const char* what = "dit_attention";
   GWA_REQUIRE(head_dim == AT_D, "%s: head_dim %lld (only 128 is built)", what, (long long)head_dim);
-  GWA_REQUIRE(S >= 0 && Skv > 0 && Skv % AT_BN == 0 && heads > 0 && heads < 65536,
-              "%s: S=%lld, Skv=%lld (a positive multiple of %d), heads=%lld", what, (long long)S, (long long)Skv,
-              AT_BN, (long long)heads);
+  GWA_REQUIRE(S >= 0 && Skv > 0 && heads > 0 && heads < 65536, "%s: S=%lld, Skv=%lld, heads=%lld", what,
+              (long long)S, (long long)Skv, (long long)heads);
   GWA_REQUIRE(ldq >= heads * AT_D && ldk >= heads * AT_D && ldv >= heads * AT_D && ldo >= heads * AT_D &&
                   ldq % 8 == 0 && ldk % 8 == 0 && ldv % 8 == 0 && ldo % 4 == 0,
               "%s: token strides must be >= heads * 128 (multiples of 8, ldo of 4)", what);

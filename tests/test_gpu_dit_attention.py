@@ -5,7 +5,7 @@ probabilities (or their products) to bf16 on the way into p v, so the kernel mus
 factor of SDPA's error, element by element and on average. Shapes: the full-size DiT's joint sequence
 (4608 tokens, 24 heads; four heads against the reference), the small DiT's (256 tokens), a query count
 that is not a multiple of the 128-query tile, and v as a column slice of a fused qkv output (token
-stride 3 * hidden)."""
+stride 3 * hidden), key counts that end in a partial 64-key tile (the rows past the last key are masked)."""
 
 from __future__ import annotations
 
@@ -51,7 +51,8 @@ def _inputs(s, skv, heads, seed, fused_v=False):
 
 @pytest.mark.parametrize("s,skv,heads,check,fused_v", [(4608, 4608, 24, (0, 7, 13, 23), True),
                                                        (256, 256, 4, (0, 1, 2, 3), False),
-                                                       (200, 320, 3, (0, 1, 2), False)])
+                                                       (200, 320, 3, (0, 1, 2), False),
+                                                       (130, 257, 2, (0, 1), False), (64, 40, 2, (0, 1), True)])
 def test_attention_matches_fp32_reference(s, skv, heads, check, fused_v):
     from gen_worker_amd.flux_dit import _sdpa, attention
 
@@ -103,7 +104,10 @@ def test_attention_refuses_bad_layouts():
     from gen_worker_amd.flux_dit import attention
 
     q, k, v = _inputs(64, 96, 2, seed=1)
-    with pytest.raises(_native.NativeError, match="multiple of 64"):
-        attention(q, k, v)                              # 96 keys: not whole 64-key tiles
+    with pytest.raises(ValueError, match="keys"):
+        attention(q, k, v[:90])                         # 96 keys, 90 values
     with pytest.raises(ValueError, match="unit head"):
         attention(q.transpose(0, 1).contiguous().transpose(0, 1), k, v)
+    lib = _native.load()
+    rc = lib.gwa_dit_attention(None, 128, None, 128, None, 128, None, 128, 4, 4, 1, 64, 0.1, None)
+    assert rc == 1 and "head_dim" in lib.gwa_last_error().decode()
