@@ -214,10 +214,17 @@ __global__ __launch_bounds__(512) void svdq_quant_int4_kernel(
 // 16, lane / 16) holds row r, columns 32c .. 32c+31 of the stage: half of
 // group c / 2, so a group's absmax is one max over the lane's 32 values and
 // one exchange with lane ^ 16.
-//  * Every wave issues its first task's x loads (4 x 16 bytes per lane) at
-//    the start, before the workgroup's copies of the stages' proj_down
-//    operands (direct-to-LDS) and smoothing factors, and each next task's
-//    when the previous one starts.
+//  * x goes global -> LDS by direct copies, one task ahead, into a two-task
+//    ring per wave: each copy moves four whole 256-byte row segments (16
+//    bytes per lane), so every request reads whole cache lines; the
+//    quantizer's lane layout (16 bytes of one row per lane and k-step) is
+//    then read from LDS, the chunk order of each row XOR-swizzled by the row
+//    so those reads are free of bank conflicts. (Loading that layout straight
+//    from global memory touches 64 lines per request, a quarter of each: the
+//    read ran at 5.5 TB/s against 8.5 for whole lines in a probe of the
+//    same shape.)
+//  * Each workgroup copies the stages' proj_down operands and smoothing
+//    factors to LDS before its first task's x, and waits for those only.
 //  * The smoothing reciprocals RN(1/s) of the stages are formed once per
 //    workgroup in LDS (a non-normal reciprocal flags the stage for the
 //    division path).
@@ -259,30 +266,46 @@ __global__ __launch_bounds__(Q6_THREADS) void svdq_quant_fp6_kernel(
   constexpr int RBX = RB > 0 ? RB : 1;
   constexpr int PDO_STAGE = RB * 4096;                       // bytes of proj_down operands per stage
   constexpr int RCP_OFF = CH * PDO_STAGE;                    // [CH][128] reciprocals, [CH][128] factors
-  constexpr int FLAG_OFF = RCP_OFF + CH * 128 * 4 * 2;       // [CH] division-path flags
-  __shared__ __attribute__((aligned(16))) uint8_t lds[FLAG_OFF + CH * 4];
+  constexpr int SMR_OFF = RCP_OFF + CH * 128 * 4 * 2;        // [CH * 128] the factors as copied (bf16)
+  constexpr int FLAG_OFF = SMR_OFF + 1024;                   // [CH] division-path flags
+  constexpr int X_OFF = (FLAG_OFF + CH * 4 + 1023) / 1024 * 1024;
+  constexpr int X_TASK = 4096;                               // a task's x: 16 rows x 256 bytes
+  static_assert(CH * 128 * 2 <= 1024, "smoothing factors of a chunk");
+  __shared__ __attribute__((aligned(16))) uint8_t lds[X_OFF + Q6_WAVES * 2 * X_TASK];
 
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int S = K >> 7;
   const int st0 = blockIdx.y * CH;
+  const int ntask = min(CH, S - st0);  // workgroup-uniform, >= 1
   const int r = lane & 15, c = lane >> 4;
   const int row0 = blockIdx.x * Q6_ROWS + 16 * wave;
   const int grow = row0 + r;
   const bool row_ok = grow < M;
 
-  // 0. x, 4 x 16 bytes per lane per task (rows past M / stages past K read 0): task 0's loads first, then
-  //    task t + 1's when task t starts. (Requesting every task's up front, HBM served all waves' requests
-  //    interleaved and each wave's first task arrived late: 1.9 us slower at config 1.)
-  const rsrc_t xbuf = make_rsrc(x, (uint32_t)(((int64_t)(M - 1) * ldx + K) * 2));
-  v4i xv[CH][4];
-  auto load_task = [&](int t) __attribute__((always_inline)) {
+  // x: a task's 16 rows x 256 bytes go global -> LDS by four direct copies per wave (16 bytes per lane, four
+  // whole rows per copy: every copy reads whole cache lines), into a two-task ring per wave. Slot s of the
+  // task's row q holds the row's 16-byte chunk s ^ q, so the quantizer's reads (row r, chunk 4c + j: sixteen
+  // rows at one chunk index per 16 lanes) fall in sixteen distinct bank groups.
+  const v4i xr4 = raw_rsrc4(x, (uint32_t)(((int64_t)(M - 1) * ldx + K) * 2));
+  uint8_t* const xring = lds + X_OFF + wave * (2 * X_TASK);
+  auto issue_x = [&](int t) __attribute__((always_inline)) {
+    const int col = (st0 + t) * 128;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int col = (st0 + t) * 128 + 32 * c + 8 * j;
-      xv[t][j] = buf_load16(xbuf, (row_ok && st0 + t < S) ? (uint32_t)(((int64_t)grow * ldx + col) * 2) : kOOB);
+      const int q = 4 * j + (lane >> 4), sl = lane & 15;
+      const uint32_t off =
+          row0 + q < M ? (uint32_t)(((int64_t)(row0 + q) * ldx + col + 8 * (sl ^ q)) * 2) : kOOB;
+      dma16_lds(xr4, (uint32_t)(uintptr_t)(xring + (t & 1) * X_TASK + j * 1024), off, 0u);
     }
   };
-  load_task(0);
+  // 0. the chunk's smoothing factors (one copy, wave 0), then the stages' proj_down operands, then task 0's x:
+  //    everything but task 0's x is waited for before the reciprocals
+  if (smooth && wave == 0) {
+    const v4i sm4 = raw_rsrc4(smooth, (uint32_t)(K * 2));
+    const int col = st0 * 128 + 8 * lane;
+    dma16_lds(sm4, (uint32_t)(uintptr_t)(lds + SMR_OFF), lane < CH * 16 && col < K ? (uint32_t)(col * 2) : kOOB,
+              0u);
+  }
   // 1. the stages' proj_down operands, direct to LDS: CH * RB * 4 runs of 1 KB, dealt round-robin (every
   //    wave issues the same number). The offset goes in the VGPR operand, the one the hardware range-checks:
   //    the runs of stages past K read zeros.
@@ -299,14 +322,14 @@ __global__ __launch_bounds__(Q6_THREADS) void svdq_quant_fp6_kernel(
                 in_chunk < valid ? (uint32_t)st0 * PDO_STAGE + in_chunk : kOOB, 0u);
     }
   }
-  // 2. smoothing factors: thread t holds columns 2t, 2t + 1 of the chunk (CH * 128 columns)
-  const rsrc_t smbuf = make_rsrc(smooth, smooth ? (uint32_t)(K * 2) : 0u);
+  issue_x(0);
+  wait_vm_lgkm0_q<4>();  // all but task 0's four copies
+  __syncthreads();
+  // 2. reciprocals of the factors: thread t holds columns 2t, 2t + 1 of the chunk (CH * 128 columns)
   static_assert(CH * 128 <= 2 * Q6_THREADS, "smoothing columns per thread");
   const int scol = st0 * 128 + 2 * tid;
   const bool s_role = smooth && 2 * tid < CH * 128;
-  const uint32_t sv = s_role ? buf_load4(smbuf, scol < K ? (uint32_t)(scol * 2) : kOOB) : 0u;
-  // 3. reciprocals, once everything in flight has landed (task 0's x included)
-  wait_vm_lgkm0_q<0>();
+  const uint32_t sv = s_role ? *(const uint32_t*)(lds + SMR_OFF + 4 * tid) : 0u;
   if (s_role) {
     const float s0 = bf16_lo(sv), s1 = bf16_hi(sv);
     float* rcp = (float*)(lds + RCP_OFF);
@@ -331,17 +354,31 @@ __global__ __launch_bounds__(Q6_THREADS) void svdq_quant_fp6_kernel(
 
 #pragma unroll
   for (int t = 0; t < CH; ++t) {
-    if (t + 1 < CH) load_task(t + 1);
+    if (t >= ntask) break;  // workgroup-uniform
     const int st = st0 + t;
-    if (st >= S) break;  // workgroup-uniform
+    const bool more = t + 1 < ntask;
+    if (more) issue_x(t + 1);
+    // task t's copies have landed once at most the newer memory operations are in flight: task t - 1's three
+    // record stores and task t + 1's four copies (vector memory operations complete in issue order)
+    if (t == 0) {
+      if (more) wait_vm_lgkm0_q<4>();
+      else wait_vm_lgkm0_q<0>();
+    } else {
+      if (more) wait_vm_lgkm0_q<7>();
+      else wait_vm_lgkm0_q<3>();
+    }
+    asm volatile("" ::: "memory");  // the LDS reads below stay after the wait
+    v4i xv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) xv[j] = *(const v4i*)(xring + (t & 1) * X_TASK + r * 256 + 16 * ((4 * c + j) ^ r));
     // ---- xs = RN_bf16(x / smooth) as floats, and the lane's absmax
     float v[32];
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        v[8 * j + 2 * e] = bf16_lo((uint32_t)xv[t][j][e]);
-        v[8 * j + 2 * e + 1] = bf16_hi((uint32_t)xv[t][j][e]);
+        v[8 * j + 2 * e] = bf16_lo((uint32_t)xv[j][e]);
+        v[8 * j + 2 * e + 1] = bf16_hi((uint32_t)xv[j][e]);
       }
     if (smooth) {
       // the stage's flag is workgroup-uniform: one scalar branch, not one per element
@@ -371,7 +408,7 @@ __global__ __launch_bounds__(Q6_THREADS) void svdq_quant_fp6_kernel(
       for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb)
-          acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, xv[t][j]),
+          acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, xv[j]),
                                                             *(const v8bf*)(pb + (j * RB + rb) * 1024), acc[rb],
                                                             0, 0, 0);
     }
