@@ -63,6 +63,60 @@ __global__ __launch_bounds__(64 * QK_WAVES) void qk_norm_rope_kernel(
   if (xv) *(uint32_t*)(ov + oi) = uv;
 }
 
+// Wide form (16-byte aligned rows): one wave per token and 4 heads, 16 lanes per head, lane holding 8
+// consecutive values (4 rotary pairs); the sum of squares is the lane's 4 pair sums, then a butterfly over the
+// head's 16 lanes. 16-byte loads and stores, a quarter of the waves and shuffles of the form above.
+__device__ __forceinline__ float head_sum16(float v) {
+#pragma unroll
+  for (int o = 8; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+__device__ __forceinline__ v4i norm_rope8(v4i u, v4i w, uint2 cs, uint2 sn, float eps) {
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float e = bf16_lo((uint32_t)u[i]), o = bf16_hi((uint32_t)u[i]);
+    ss += e * e + o * o;
+  }
+  const float r = rsqrtf(head_sum16(ss) * (1.0f / 128.0f) + eps);
+  v4i out;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float e = bf16_lo((uint32_t)u[i]), o = bf16_hi((uint32_t)u[i]);
+    const uint32_t cw = i < 2 ? cs.x : cs.y, sw = i < 2 ? sn.x : sn.y;
+    const float c = (i & 1) ? bf16_hi(cw) : bf16_lo(cw), s = (i & 1) ? bf16_hi(sw) : bf16_lo(sw);
+    const float ye = bf16r(bf16r(e * r) * bf16_lo((uint32_t)w[i]));
+    const float yo = bf16r(bf16r(o * r) * bf16_hi((uint32_t)w[i]));
+    const float oe = bf16r(bf16r(ye * c) - bf16r(yo * s));
+    const float oo = bf16r(bf16r(ye * s) + bf16r(yo * c));
+    out[i] = (int)((uint32_t)f32_to_bf16(oe) | ((uint32_t)f32_to_bf16(oo) << 16));
+  }
+  return out;
+}
+
+__global__ __launch_bounds__(64 * QK_WAVES) void qk_norm_rope_wide_kernel(
+    const uint16_t* __restrict__ xq, const uint16_t* __restrict__ xk, const uint16_t* __restrict__ xv, int64_t ldx,
+    const uint16_t* __restrict__ wq, const uint16_t* __restrict__ wk, const uint16_t* __restrict__ cos_t,
+    const uint16_t* __restrict__ sin_t, int64_t pos0, uint16_t* __restrict__ oq, uint16_t* __restrict__ ok,
+    uint16_t* __restrict__ ov, int64_t ldo, int64_t items, int heads, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t item = (int64_t)blockIdx.x * QK_WAVES + (threadIdx.x >> 6);
+  if (item >= items) return;  // wave-uniform
+  const int hgroups = (heads + 3) >> 2;
+  const int64_t row = item / hgroups;
+  const int h = (int)(item - row * hgroups) * 4 + (lane >> 4), e8 = 8 * (lane & 15);
+  if (h >= heads) return;  // a whole 16-lane group: its butterfly stays inside the group
+  const int64_t xi = row * ldx + h * 128 + e8, oi = row * ldo + h * 128 + e8;
+  const int64_t ti = (pos0 + row) * 64 + (e8 >> 1);
+  const v4i uq = *(const v4i*)(xq + xi), uk = *(const v4i*)(xk + xi);
+  const uint2 cs = *(const uint2*)(cos_t + ti), sn = *(const uint2*)(sin_t + ti);
+  const v4i gq = *(const v4i*)(wq + e8), gk = *(const v4i*)(wk + e8);
+  if (xv) *(v4i*)(ov + oi) = *(const v4i*)(xv + xi);
+  *(v4i*)(oq + oi) = norm_rope8(uq, gq, cs, sn, eps);
+  *(v4i*)(ok + oi) = norm_rope8(uk, gk, cs, sn, eps);
+}
+
 // ---------------------------------------------------------------------------------------------------------
 // adaLN modulate. One wave per row of C = 512 * NCH columns; lane l holds columns 512 j + 8 l .. + 8.
 // ---------------------------------------------------------------------------------------------------------
@@ -169,10 +223,14 @@ extern "C" int gwa_dit_qk_norm_rope(const void* xq, const void* xk, const void* 
   GWA_REQUIRE(GWA_ALIGNED(xq, 4) && GWA_ALIGNED(xk, 4) && GWA_ALIGNED(xv, 4) && GWA_ALIGNED(wq, 4) &&
                   GWA_ALIGNED(wk, 4) && GWA_ALIGNED(oq, 4) && GWA_ALIGNED(ok, 4) && GWA_ALIGNED(ov, 4),
               "%s: tensors must be 4-byte aligned", what);
-  const int64_t items = rows * heads;
+  const bool wide = GWA_ALIGNED(xq, 16) && GWA_ALIGNED(xk, 16) && GWA_ALIGNED(xv, 16) && GWA_ALIGNED(wq, 16) &&
+                    GWA_ALIGNED(wk, 16) && GWA_ALIGNED(oq, 16) && GWA_ALIGNED(ok, 16) && GWA_ALIGNED(ov, 16) &&
+                    GWA_ALIGNED(cos_t, 8) && GWA_ALIGNED(sin_t, 8) && ldx % 8 == 0 && ldo % 8 == 0;
+  const int64_t items = rows * (wide ? (heads + 3) / 4 : heads);
   const int64_t blocks = (items + QK_WAVES - 1) / QK_WAVES;
   GWA_REQUIRE(blocks < (1ll << 31), "%s: grid too large", what);
-  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((unsigned)blocks), dim3(64 * QK_WAVES), 0, (hipStream_t)stream,
+  hipLaunchKernelGGL(wide ? qk_norm_rope_wide_kernel : qk_norm_rope_kernel, dim3((unsigned)blocks),
+                     dim3(64 * QK_WAVES), 0, (hipStream_t)stream,
                      (const uint16_t*)xq, (const uint16_t*)xk, (const uint16_t*)xv, ldx, (const uint16_t*)wq,
                      (const uint16_t*)wk, (const uint16_t*)cos_t, (const uint16_t*)sin_t, pos0, (uint16_t*)oq,
                      (uint16_t*)ok, (uint16_t*)ov, ldo, items, (int)heads, eps);

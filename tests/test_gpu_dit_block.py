@@ -79,13 +79,16 @@ def test_adaln_modulate(rows, cols):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("rows,heads,pos0", [(4096, 24, 512), (512, 24, 0), (67, 4, 3)])
-def test_qk_norm_rope(rows, heads, pos0):
+@pytest.mark.parametrize("rows,heads,pos0,off", [(4096, 24, 512, 0), (512, 24, 0, 0), (67, 4, 3, 0),
+                                                (33, 6, 1, 0), (29, 6, 2, 2)])
+def test_qk_norm_rope(rows, heads, pos0, off):
+    """Aligned rows take the wide kernel (4 heads per wave; 6 heads: a half-empty second group); off = 2
+    (rows 4-byte aligned only) the one-head-per-wave kernel."""
     from gen_worker_amd.flux_dit import _rms, _rope, qk_norm_rope
 
     d, c = 128, heads * 128
     g = torch.Generator(device=DEV).manual_seed(rows * heads + pos0)
-    qkv = (torch.randn(rows, 3 * c, generator=g, device=DEV) * 2).to(torch.bfloat16)
+    qkv = (torch.randn(rows, 3 * c + off, generator=g, device=DEV) * 2).to(torch.bfloat16)[:, off:]
     qkv[:, 7] *= 40
     wq = (1 + 0.1 * torch.randn(d, generator=g, device=DEV)).to(torch.bfloat16)
     wk = (1 + 0.1 * torch.randn(d, generator=g, device=DEV)).to(torch.bfloat16)
