@@ -290,6 +290,7 @@ class DualBlock(nn.Module):
         self.o_img, self.o_txt = make(c, c, seed + 4), make(c, c, seed + 5)
         self.fc1_img, self.fc1_txt = make(c, cfg.mlp, seed + 6, gelu=True), make(c, cfg.mlp, seed + 7, gelu=True)
         self.fc2_img, self.fc2_txt = make(cfg.mlp, c, seed + 8), make(cfg.mlp, c, seed + 9)
+        self.side: Optional[torch.cuda.Stream] = None  # set by FluxDiT(..., streams=2)
         ones = torch.ones(cfg.head_dim, device=device, dtype=torch.bfloat16)
         self.register_buffer("qn_img", ones.clone())
         self.register_buffer("kn_img", ones.clone())
@@ -297,6 +298,8 @@ class DualBlock(nn.Module):
         self.register_buffer("kn_txt", ones.clone())
 
     def forward(self, img: Tensor, txt: Tensor, temb: Tensor, cos: Tensor, sin: Tensor) -> tuple[Tensor, Tensor]:
+        if self.side is not None:
+            return self._forward_two_streams(img, txt, temb, cos, sin)
         cfg = self.cfg
         sh1, sc1, g1, sh2, sc2, g2 = self.mod_img(temb).chunk(6, dim=-1)
         tsh1, tsc1, tg1, tsh2, tsc2, tg2 = self.mod_txt(temb).chunk(6, dim=-1)
@@ -318,6 +321,42 @@ class DualBlock(nn.Module):
         txt = gate_residual(txt, _mlp(self.fc1_txt, self.fc2_txt, adaln_modulate(txt, tsc2, tsh2), self.fused),
                             tg2)
         return img, txt
+
+    def _forward_two_streams(self, img: Tensor, txt: Tensor, temb: Tensor, cos: Tensor,
+                             sin: Tensor) -> tuple[Tensor, Tensor]:
+        """The same kernels on the same inputs, the text stream's (512 tokens: grids that leave CUs idle) on a
+        second HIP stream, joined for the attention and at the end."""
+        cfg, side = self.cfg, self.side
+        main = torch.cuda.current_stream(img.device)
+        c, st = cfg.hidden, txt.shape[0]
+        side.wait_stream(main)
+        with torch.cuda.stream(side):
+            tsh1, tsc1, tg1, tsh2, tsc2, tg2 = self.mod_txt(temb).chunk(6, dim=-1)
+            qkv_t = self.qkv_txt(adaln_modulate(txt, tsc1, tsh1))
+        sh1, sc1, g1, sh2, sc2, g2 = self.mod_img(temb).chunk(6, dim=-1)
+        qkv_i = self.qkv_img(adaln_modulate(img, sc1, sh1))
+        q, k, v = (torch.empty(st + img.shape[0], cfg.heads, cfg.head_dim, device=img.device, dtype=img.dtype)
+                   for _ in range(3))
+        side.wait_stream(main)  # q, k, v allocated before the text rows are written on the side stream
+        with torch.cuda.stream(side):
+            qk_norm_rope(qkv_t[:, :c], qkv_t[:, c:2 * c], self.qn_txt, self.kn_txt, cos, sin, 0, q[:st], k[:st],
+                         v=qkv_t[:, 2 * c:], out_v=v[:st])
+        qk_norm_rope(qkv_i[:, :c], qkv_i[:, c:2 * c], self.qn_img, self.kn_img, cos, sin, st, q[st:], k[st:],
+                     v=qkv_i[:, 2 * c:], out_v=v[st:])
+        main.wait_stream(side)
+        a = _attention(q, k, v)
+        at, ai = a[:st], a[st:]
+        side.wait_stream(main)
+        with torch.cuda.stream(side):
+            t2 = gate_residual(txt, self.o_txt(at.contiguous()), tg1)
+            t2 = gate_residual(t2, _mlp(self.fc1_txt, self.fc2_txt, adaln_modulate(t2, tsc2, tsh2), self.fused),
+                               tg2)
+        img = gate_residual(img, self.o_img(ai.contiguous()), g1)
+        img = gate_residual(img, _mlp(self.fc1_img, self.fc2_img, adaln_modulate(img, sc2, sh2), self.fused), g2)
+        # joined before any tensor of this block is freed: the allocator's per-stream pools stay ordered (a
+        # block freed here is reused only after this join, or by the stream that allocated it)
+        main.wait_stream(side)
+        return img, t2
 
 
 class SingleBlock(nn.Module):
@@ -354,7 +393,7 @@ class FluxDiT(nn.Module):
     """The config-4 denoiser; ``forward(latents [4096, 64], text [512, 4096], temb [1, 3072]) -> [4096, 64]``."""
 
     def __init__(self, kind: str, cfg: FluxDiTConfig = FluxDiTConfig(), device="cuda", seed: int = 1000,
-                 lane: Optional[str] = None, modulation: str = "w4a4") -> None:
+                 lane: Optional[str] = None, modulation: str = "w4a4", streams: int = 1) -> None:
         super().__init__()
         if kind == "w4a4":
             from .qualify import resolve_lane
@@ -373,6 +412,12 @@ class FluxDiT(nn.Module):
                                   for i in range(cfg.n_dual))
         self.single = nn.ModuleList(SingleBlock(cfg, make, seed + 400 + 10 * i, device, fused, make_mod)
                                     for i in range(cfg.n_single))
+        if streams == 2:  # the dual blocks' text stream on a second HIP stream (default priority)
+            side = torch.cuda.Stream(device=device)
+            for blk in self.dual:
+                blk.side = side
+        elif streams != 1:
+            raise ValueError(f"streams must be 1 or 2, got {streams}")
         self.norm_out = make(c, 2 * c, seed + 2)
         self.proj_out = make(c, cfg.in_channels, seed + 3)
         # rotary tables for the 4608 joint positions ([text; image]), theta 10000

@@ -67,6 +67,28 @@ def test_full_size_dit_forward():
         torch.cuda.synchronize()
     del g, yg
 
+    # the dual blocks' text stream on a second HIP stream (the bench's configuration): the same kernels on the
+    # same inputs, so the same bits, eager and graph-replayed
+    side = torch.cuda.Stream()
+    for blk in m4.dual:
+        blk.side = side
+    with torch.no_grad():
+        y3 = m4(*args)
+    torch.cuda.synchronize()
+    assert torch.equal(y3, y1), "two-stream forward differs from one stream"
+    g = torch.cuda.CUDAGraph()
+    with torch.no_grad(), torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            yg = m4(*args)
+    torch.cuda.synchronize()
+    for _ in range(2):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(yg, y1), "two-stream graph replay differs"
+    for blk in m4.dual:
+        blk.side = None
+    del g, yg, y3
+
     md = FluxDiT("w4a4", cfg, device=DEV, lane="dense")
     assert md.lane == "dense" and not any(isinstance(m, SvdqW4A4Linear) for m in md.modules())
     with torch.no_grad():
