@@ -369,6 +369,7 @@ class SingleBlock(nn.Module):
         self.qkv = make(c, 3 * c, seed + 1)
         self.mlp = make(c, cfg.mlp, seed + 2, gelu=True)
         self.proj_out = make(c + cfg.mlp, c, seed + 3)
+        self.side: Optional[torch.cuda.Stream] = None  # set by FluxDiT(..., streams=2)
         ones = torch.ones(cfg.head_dim, device=device, dtype=torch.bfloat16)
         self.register_buffer("qn", ones.clone())
         self.register_buffer("kn", ones.clone())
@@ -378,10 +379,31 @@ class SingleBlock(nn.Module):
         sh, sc, g = self.mod(temb).chunk(3, dim=-1)
         n = adaln_modulate(x, sc, sh)
         c = cfg.hidden
+        side = self.side
+        if side is not None:
+            # the MLP branch (it needs only n) on the second stream while the attention branch runs here;
+            # joined before proj_out reads both
+            main = torch.cuda.current_stream(x.device)
+            if self.fused:
+                from .svdq import SvdqConcat
+
+                cc = SvdqConcat(self.proj_out, self.mlp, n, c)  # buffers allocated on this stream first
+                side.wait_stream(main)
+                with torch.cuda.stream(side):
+                    cc.produce()
+            else:
+                side.wait_stream(main)
+                with torch.cuda.stream(side):
+                    h = self.mlp(n)
         qkv = self.qkv(n)
         q, k = (torch.empty(x.shape[0], cfg.heads, cfg.head_dim, device=x.device, dtype=x.dtype) for _ in range(2))
         qk_norm_rope(qkv[:, :c], qkv[:, c:2 * c], self.qn, self.kn, cos, sin, 0, q, k)
         a = _attention(q, k, qkv[:, 2 * c:].reshape(-1, cfg.heads, cfg.head_dim))
+        if side is not None:
+            if self.fused:
+                return gate_residual(x, cc.finish(a, before_reduce=lambda: main.wait_stream(side)), g)
+            main.wait_stream(side)
+            return gate_residual(x, self.proj_out(torch.cat((a, h), dim=-1)), g)
         if self.fused:
             from .svdq import svdq_concat_forward
 
@@ -412,9 +434,9 @@ class FluxDiT(nn.Module):
                                   for i in range(cfg.n_dual))
         self.single = nn.ModuleList(SingleBlock(cfg, make, seed + 400 + 10 * i, device, fused, make_mod)
                                     for i in range(cfg.n_single))
-        if streams == 2:  # the dual blocks' text stream on a second HIP stream (default priority)
-            side = torch.cuda.Stream(device=device)
-            for blk in self.dual:
+        if streams == 2:  # a second HIP stream (default priority): the dual blocks' text stream, the single
+            side = torch.cuda.Stream(device=device)  # blocks' MLP branch
+            for blk in list(self.dual) + list(self.single):
                 blk.side = side
         elif streams != 1:
             raise ValueError(f"streams must be 1 or 2, got {streams}")

@@ -318,32 +318,60 @@ def svdq_concat_forward(consumer: SvdqW4A4Linear, x_a: Tensor, producer: SvdqW4A
     ka = int(x_a.shape[-1])
     if not _fusable(producer, consumer, ka):
         return consumer(torch.cat((x_a, producer(x_b)), dim=-1))
-    cg = torch.ops.cozy_gen_worker
-    shape = x_a.shape
-    xa2 = x_a.reshape(-1, ka)
-    if xa2.dtype != torch.bfloat16:
-        raise SvdqFusedError(f"svdq_concat_forward expects bf16 activations, got {xa2.dtype}")
-    xa2 = xa2.contiguous()
-    xb2 = producer._input2d(x_b)
-    m = int(xa2.shape[0])
-    if int(xb2.shape[0]) != m:
-        raise SvdqFusedError(f"svdq_concat_forward: {m} rows in x_a, {int(xb2.shape[0])} in x_b")
-    q6n = ops.records_empty(consumer.in_features // ops.FP6_STAGE, m, xa2.device)
-    part = None
-    pa = 0
-    if consumer.rank:
-        pa = ops.la_partials_quant(m, ka, consumer.rank)
-        pb = ops.la_partials_next(m, producer.out_features)
-        part = torch.empty(pa + pb, m, consumer.rank, dtype=torch.float32, device=xa2.device)
-    sm_a, pdo_a = _next_operands(consumer, 0, ka)
-    cg.svdq_quant_fp6_into(xa2, sm_a, pdo_a, q6n, part)
-    q6, la = cg.svdq_quant_fp6(xb2, producer.smooth_factor, None, producer.proj_down_op6)
-    sm_b, pdo_b = _next_operands(consumer, ka, consumer.in_features)
-    cg.svdq_w4a4_linear_fp6_next(q6, producer.weight_fp6, None, producer.second, la if producer.rank else None,
-                                 producer.proj_up, producer.bias, producer.activation == "gelu_tanh", sm_b, pdo_b,
-                                 q6n, part[pa:] if part is not None else None, ka // ops.FP6_STAGE, False)
-    y = consumer.forward_records(q6n, cg.svdq_la_reduce(part) if part is not None else None)
-    return y.reshape(*shape[:-1], consumer.out_features)
+    st = SvdqConcat(consumer, producer, x_b, ka)
+    st.produce()
+    return st.finish(x_a)
+
+
+class SvdqConcat:
+    """``svdq_concat_forward`` in two halves, so a caller can run the producer's half (``produce``: its input
+    quantization and its GEMM, whose epilogue writes the consumer's records and partial slots past ``ka``) on
+    another stream while x_a is still being computed; ``finish(x_a)`` writes x_a's records and slots (kernel 1),
+    reduces the slots and runs the consumer. The two halves write disjoint records and slots, so their order
+    does not change a bit. The buffers are allocated on the stream that constructs this."""
+
+    def __init__(self, consumer: SvdqW4A4Linear, producer: SvdqW4A4Linear, x_b: Tensor, ka: int) -> None:
+        if not _fusable(producer, consumer, ka):
+            raise SvdqFusedError("SvdqConcat: outside the fused contract (x_a's width a multiple of 128, fp6 lane)")
+        self.consumer, self.producer, self.ka = consumer, producer, ka
+        self.xb2 = producer._input2d(x_b)
+        m = self.m = int(self.xb2.shape[0])
+        self.q6n = ops.records_empty(consumer.in_features // ops.FP6_STAGE, m, self.xb2.device)
+        self.part, self.pa = None, 0
+        if consumer.rank:
+            self.pa = ops.la_partials_quant(m, ka, consumer.rank)
+            pb = ops.la_partials_next(m, producer.out_features)
+            self.part = torch.empty(self.pa + pb, m, consumer.rank, dtype=torch.float32, device=self.xb2.device)
+
+    def produce(self) -> None:
+        cg = torch.ops.cozy_gen_worker
+        consumer, producer, ka = self.consumer, self.producer, self.ka
+        q6, la = cg.svdq_quant_fp6(self.xb2, producer.smooth_factor, None, producer.proj_down_op6)
+        sm_b, pdo_b = _next_operands(consumer, ka, consumer.in_features)
+        cg.svdq_w4a4_linear_fp6_next(q6, producer.weight_fp6, None, producer.second,
+                                     la if producer.rank else None, producer.proj_up, producer.bias,
+                                     producer.activation == "gelu_tanh", sm_b, pdo_b, self.q6n,
+                                     self.part[self.pa:] if self.part is not None else None, ka // ops.FP6_STAGE,
+                                     False)
+
+    def finish(self, x_a: Tensor, before_reduce=None) -> Tensor:
+        """``before_reduce`` (if given) runs after x_a's records are written and before the slots are summed:
+        the point where a caller joins the stream that ran ``produce``."""
+        cg = torch.ops.cozy_gen_worker
+        consumer, ka = self.consumer, self.ka
+        shape = x_a.shape
+        xa2 = x_a.reshape(-1, ka)
+        if xa2.dtype != torch.bfloat16:
+            raise SvdqFusedError(f"svdq_concat_forward expects bf16 activations, got {xa2.dtype}")
+        xa2 = xa2.contiguous()
+        if int(xa2.shape[0]) != self.m:
+            raise SvdqFusedError(f"svdq_concat_forward: {int(xa2.shape[0])} rows in x_a, {self.m} in x_b")
+        sm_a, pdo_a = _next_operands(consumer, 0, ka)
+        cg.svdq_quant_fp6_into(xa2, sm_a, pdo_a, self.q6n, self.part)
+        if before_reduce is not None:
+            before_reduce()
+        y = consumer.forward_records(self.q6n, cg.svdq_la_reduce(self.part) if self.part is not None else None)
+        return y.reshape(*shape[:-1], consumer.out_features)
 
 
 def build_svdq_w4a4_linear(*, qweight: Tensor, wscales: Tensor, smooth: Optional[Tensor],

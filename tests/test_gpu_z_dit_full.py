@@ -67,10 +67,10 @@ def test_full_size_dit_forward():
         torch.cuda.synchronize()
     del g, yg
 
-    # the dual blocks' text stream on a second HIP stream (the bench's configuration): the same kernels on the
-    # same inputs, so the same bits, eager and graph-replayed
+    # the dual blocks' text stream and the single blocks' MLP branch on a second HIP stream (the bench's
+    # configuration): the same kernels on the same inputs, so the same bits, eager and graph-replayed
     side = torch.cuda.Stream()
-    for blk in m4.dual:
+    for blk in list(m4.dual) + list(m4.single):
         blk.side = side
     with torch.no_grad():
         y3 = m4(*args)
@@ -85,7 +85,7 @@ def test_full_size_dit_forward():
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(yg, y1), "two-stream graph replay differs"
-    for blk in m4.dual:
+    for blk in list(m4.dual) + list(m4.single):
         blk.side = None
     del g, yg, y3
 
