@@ -343,12 +343,15 @@ class DualBlock(nn.Module):
                          v=qkv_t[:, 2 * c:], out_v=v[:st])
         qk_norm_rope(qkv_i[:, :c], qkv_i[:, c:2 * c], self.qn_img, self.kn_img, cos, sin, st, q[st:], k[st:],
                      v=qkv_i[:, 2 * c:], out_v=v[st:])
+        # the joint attention as two launches over the same keys: the text queries' on the side stream (its
+        # 96 workgroups finish in the first round, so the text stream's next kernels can take the CUs the
+        # image queries' last round leaves idle), the image queries' here; each query's result is the same
         main.wait_stream(side)
-        a = _attention(q, k, v)
-        at, ai = a[:st], a[st:]
         side.wait_stream(main)
+        ai = _attention(q[st:], k, v)
         with torch.cuda.stream(side):
-            t2 = gate_residual(txt, self.o_txt(at.contiguous()), tg1)
+            at = _attention(q[:st], k, v)
+            t2 = gate_residual(txt, self.o_txt(at), tg1)
             t2 = gate_residual(t2, _mlp(self.fc1_txt, self.fc2_txt, adaln_modulate(t2, tsc2, tsh2), self.fused),
                                tg2)
         img = gate_residual(img, self.o_img(ai.contiguous()), g1)
