@@ -279,6 +279,18 @@ def _mlp(fc1: nn.Module, fc2: nn.Module, x: Tensor, fused: bool) -> Tensor:
     return fc2(fc1(x))
 
 
+def _take_modulation(blk: nn.Module, compute: Callable[[], tuple]) -> tuple:
+    """The block's modulation outputs: precomputed on another stream (``pre_mod`` = (outputs, event): this stream
+    waits for the event), or computed here."""
+    pre = blk.pre_mod
+    if pre is None:
+        return compute()
+    outs, ev = pre
+    blk.pre_mod = None
+    torch.cuda.current_stream(outs[0].device).wait_event(ev)
+    return outs
+
+
 class DualBlock(nn.Module):
     def __init__(self, cfg: FluxDiTConfig, make, seed: int, device, fused: bool = False, make_mod=None) -> None:
         super().__init__()
@@ -291,6 +303,7 @@ class DualBlock(nn.Module):
         self.fc1_img, self.fc1_txt = make(c, cfg.mlp, seed + 6, gelu=True), make(c, cfg.mlp, seed + 7, gelu=True)
         self.fc2_img, self.fc2_txt = make(cfg.mlp, c, seed + 8), make(cfg.mlp, c, seed + 9)
         self.side: Optional[torch.cuda.Stream] = None  # set by FluxDiT(..., streams=2)
+        self.pre_mod = None  # modulation outputs computed ahead on another stream, and their event
         ones = torch.ones(cfg.head_dim, device=device, dtype=torch.bfloat16)
         self.register_buffer("qn_img", ones.clone())
         self.register_buffer("kn_img", ones.clone())
@@ -301,8 +314,9 @@ class DualBlock(nn.Module):
         if self.side is not None:
             return self._forward_two_streams(img, txt, temb, cos, sin)
         cfg = self.cfg
-        sh1, sc1, g1, sh2, sc2, g2 = self.mod_img(temb).chunk(6, dim=-1)
-        tsh1, tsc1, tg1, tsh2, tsc2, tg2 = self.mod_txt(temb).chunk(6, dim=-1)
+        mi, mt = _take_modulation(self, lambda: (self.mod_img(temb), self.mod_txt(temb)))
+        sh1, sc1, g1, sh2, sc2, g2 = mi.chunk(6, dim=-1)
+        tsh1, tsc1, tg1, tsh2, tsc2, tg2 = mt.chunk(6, dim=-1)
         c, st = cfg.hidden, txt.shape[0]
         qkv_i = self.qkv_img(adaln_modulate(img, sc1, sh1))
         qkv_t = self.qkv_txt(adaln_modulate(txt, tsc1, tsh1))
@@ -329,11 +343,18 @@ class DualBlock(nn.Module):
         cfg, side = self.cfg, self.side
         main = torch.cuda.current_stream(img.device)
         c, st = cfg.hidden, txt.shape[0]
+        pre = self.pre_mod is not None
+        if pre:
+            mi, mt = _take_modulation(self, None)
         side.wait_stream(main)
         with torch.cuda.stream(side):
-            tsh1, tsc1, tg1, tsh2, tsc2, tg2 = self.mod_txt(temb).chunk(6, dim=-1)
+            if not pre:
+                mt = self.mod_txt(temb)
+            tsh1, tsc1, tg1, tsh2, tsc2, tg2 = mt.chunk(6, dim=-1)
             qkv_t = self.qkv_txt(adaln_modulate(txt, tsc1, tsh1))
-        sh1, sc1, g1, sh2, sc2, g2 = self.mod_img(temb).chunk(6, dim=-1)
+        if not pre:
+            mi = self.mod_img(temb)
+        sh1, sc1, g1, sh2, sc2, g2 = mi.chunk(6, dim=-1)
         qkv_i = self.qkv_img(adaln_modulate(img, sc1, sh1))
         q, k, v = (torch.empty(st + img.shape[0], cfg.heads, cfg.head_dim, device=img.device, dtype=img.dtype)
                    for _ in range(3))
@@ -373,13 +394,15 @@ class SingleBlock(nn.Module):
         self.mlp = make(c, cfg.mlp, seed + 2, gelu=True)
         self.proj_out = make(c + cfg.mlp, c, seed + 3)
         self.side: Optional[torch.cuda.Stream] = None  # set by FluxDiT(..., streams=2)
+        self.pre_mod = None
         ones = torch.ones(cfg.head_dim, device=device, dtype=torch.bfloat16)
         self.register_buffer("qn", ones.clone())
         self.register_buffer("kn", ones.clone())
 
     def forward(self, x: Tensor, temb: Tensor, cos: Tensor, sin: Tensor) -> Tensor:
         cfg = self.cfg
-        sh, sc, g = self.mod(temb).chunk(3, dim=-1)
+        (m3,) = _take_modulation(self, lambda: (self.mod(temb),))
+        sh, sc, g = m3.chunk(3, dim=-1)
         n = adaln_modulate(x, sc, sh)
         c = cfg.hidden
         side = self.side
@@ -437,10 +460,14 @@ class FluxDiT(nn.Module):
                                   for i in range(cfg.n_dual))
         self.single = nn.ModuleList(SingleBlock(cfg, make, seed + 400 + 10 * i, device, fused, make_mod)
                                     for i in range(cfg.n_single))
+        self.mod_stream: Optional[torch.cuda.Stream] = None
         if streams == 2:  # a second HIP stream (default priority): the dual blocks' text stream, the single
             side = torch.cuda.Stream(device=device)  # blocks' MLP branch
             for blk in list(self.dual) + list(self.single):
                 blk.side = side
+            # and a third for the modulation linears (they read only the timestep embedding): all of them are
+            # queued there at the start, each block waiting for its own
+            self.mod_stream = torch.cuda.Stream(device=device)
         elif streams != 1:
             raise ValueError(f"streams must be 1 or 2, got {streams}")
         self.norm_out = make(c, 2 * c, seed + 2)
@@ -455,6 +482,22 @@ class FluxDiT(nn.Module):
 
     def forward(self, latents: Tensor, text: Tensor, temb: Tensor) -> Tensor:
         t = F.silu(temb)
+        ms = self.mod_stream
+        if ms is not None:
+            main = torch.cuda.current_stream(t.device)
+            ms.wait_stream(main)
+            with torch.cuda.stream(ms):
+                for blk in self.dual:
+                    outs = (blk.mod_img(t), blk.mod_txt(t))
+                    ev = torch.cuda.Event()
+                    ev.record(ms)
+                    blk.pre_mod = (outs, ev)
+                for blk in self.single:
+                    outs = (blk.mod(t),)
+                    ev = torch.cuda.Event()
+                    ev.record(ms)
+                    blk.pre_mod = (outs, ev)
+                nmod = self.norm_out(t)
         img = self.x_embedder(latents)
         txt = self.context_embedder(text)
         for blk in self.dual:
@@ -463,7 +506,11 @@ class FluxDiT(nn.Module):
         for blk in self.single:
             x = blk(x, t, self.cos, self.sin)
         img = x[self.cfg.txt_tokens:]
-        scale, shift = self.norm_out(t).chunk(2, dim=-1)
+        if ms is not None:
+            main.wait_stream(ms)  # the last modulation; every tensor the stream wrote is consumed after this
+            scale, shift = nmod.chunk(2, dim=-1)
+        else:
+            scale, shift = self.norm_out(t).chunk(2, dim=-1)
         return self.proj_out(adaln_modulate(img, scale, shift))
 
 

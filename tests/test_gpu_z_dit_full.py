@@ -67,11 +67,13 @@ def test_full_size_dit_forward():
         torch.cuda.synchronize()
     del g, yg
 
-    # the dual blocks' text stream and the single blocks' MLP branch on a second HIP stream (the bench's
-    # configuration): the same kernels on the same inputs, so the same bits, eager and graph-replayed
+    # the dual blocks' text stream and the single blocks' MLP branch on a second HIP stream, the modulation
+    # linears on a third (the bench's configuration): the same kernels on the same inputs, so the same bits,
+    # eager and graph-replayed
     side = torch.cuda.Stream()
     for blk in list(m4.dual) + list(m4.single):
         blk.side = side
+    m4.mod_stream = torch.cuda.Stream()  # and the modulation linears queued ahead on a third stream
     with torch.no_grad():
         y3 = m4(*args)
     torch.cuda.synchronize()
@@ -87,6 +89,7 @@ def test_full_size_dit_forward():
         assert torch.equal(yg, y1), "two-stream graph replay differs"
     for blk in list(m4.dual) + list(m4.single):
         blk.side = None
+    m4.mod_stream = None
     del g, yg, y3
 
     md = FluxDiT("w4a4", cfg, device=DEV, lane="dense")
