@@ -194,6 +194,21 @@ def test_fake_impls_trace_shapes():
         assert y.shape == (77, 128) and y.dtype == torch.float16
 
 
+def test_concat_halves_refuse_outside_the_fused_contract():
+    """SvdqConcat (the two halves of the single block's proj_out-over-[attention, MLP] forward) takes only the
+    fp6 lane's fused contract: modules off the GPU, or widths that do not meet, are refused before any launch."""
+    from gen_worker_amd import SvdqFusedError, SvdqW4A4Linear
+    from gen_worker_amd.svdq import SvdqConcat
+
+    mlp = SvdqW4A4Linear(256, 512, rank=32, bias=True, activation="gelu_tanh")
+    proj = SvdqW4A4Linear(256 + 512, 256, rank=32, bias=True)
+    n = torch.zeros(4, 256, dtype=torch.bfloat16)
+    with pytest.raises(SvdqFusedError, match="fused contract"):
+        SvdqConcat(proj, mlp, n, 256)          # CPU modules: not the fp6 lane
+    with pytest.raises(SvdqFusedError, match="fused contract"):
+        SvdqConcat(proj, mlp, n, 128)          # 128 + 512 != 768
+
+
 def test_module_contract_refusals():
     from gen_worker_amd import SvdqFusedError, SvdqW4A4Linear, W8a8Error, Int8ScaledLinear
 
