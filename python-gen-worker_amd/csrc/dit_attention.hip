@@ -3,7 +3,7 @@
 // (the flash-attention recurrence), in place of torch's scaled_dot_product_attention (which diffusers'
 // FluxAttnProcessor calls; here the vendor kernel ran at ~0.49 PFLOP/s).
 //
-// Work split: a 256-thread workgroup owns 128 queries of one head (4 waves x 32 queries) and walks the keys
+// Work split: a 512-thread workgroup owns 256 queries of one head (8 waves x 32 queries) and walks the keys
 // in tiles of 64. K and V tiles ([64 keys][128], as stored) are copied global -> LDS by direct-to-LDS
 // buffer loads (no staging registers, no LDS writes), double buffered: tile t+1's copies are issued before
 // tile t's MFMAs, one wait and one barrier per tile. The 16-byte chunks of a row are XOR-swizzled by the
@@ -23,7 +23,10 @@
 
 namespace {
 
-constexpr int AT_D = 128, AT_BM = 128, AT_BN = 64, AT_THREADS = 256;
+// 8 waves per workgroup (one workgroup per CU): each K / V tile copy serves 256 queries (4 waves: 128, two
+// workgroups per CU, 319 -> 303 us at 4608 tokens x 24 heads)
+constexpr int AT_D = 128, AT_BN = 64, AT_NW = 8, AT_BM = 32 * AT_NW, AT_THREADS = 64 * AT_NW;
+constexpr int AT_RUNS = 16 / AT_NW;  // 1 KB copy runs per wave, per K and per V tile
 constexpr int AT_ROW = AT_D * 2;                       // tile row bytes (256), chunks swizzled, no padding
 constexpr int AT_TILE = AT_BN * AT_ROW;                // 16 KB per K or V tile
 constexpr int AT_STAGE = 2 * AT_TILE;                  // K then V
@@ -45,7 +48,7 @@ __device__ __forceinline__ v4s_ lds_read_tr(const uint8_t* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s_*)(uintptr_t)p);
 }
 
-__global__ __launch_bounds__(AT_THREADS, 2) void dit_attention_kernel(
+__global__ __launch_bounds__(AT_THREADS, 8 / AT_NW) void dit_attention_kernel(
     const uint16_t* __restrict__ q, int64_t ldq, const uint16_t* __restrict__ k, int64_t ldk,
     const uint16_t* __restrict__ v, int64_t ldv, uint16_t* __restrict__ o, int64_t ldo, int S, int Skv,
     float c_log2) {
@@ -65,14 +68,14 @@ __global__ __launch_bounds__(AT_THREADS, 2) void dit_attention_kernel(
     for (int cd = 0; cd < 8; ++cd) qop[cd] = q_ok ? *(const v4i*)(qp + 16 * cd) : (v4i){0, 0, 0, 0};
   }
 
-  // copies: 16 runs of 1 KB (4 rows) per K tile and per V tile, runs wave, wave + 4, ... of each; lane l of a
+  // copies: 16 runs of 1 KB (4 rows) per K tile and per V tile, runs wave, wave + 8 of each; lane l of a
   // run lands at LDS slot l % 16 of row 4 run + l / 16 and fetches the chunk that belongs there
   const v4i kbuf = raw_rsrc(k, (uint32_t)(((int64_t)(Skv - 1) * ldk + gridDim.y * AT_D) * 2));
   const v4i vbuf = raw_rsrc(v, (uint32_t)(((int64_t)(Skv - 1) * ldv + gridDim.y * AT_D) * 2));
-  uint32_t koff[4], voff[4];
+  uint32_t koff[AT_RUNS], voff[AT_RUNS];
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int run = wave + 4 * u, row = 4 * run + (lane >> 4), slot = lane & 15;
+  for (int u = 0; u < AT_RUNS; ++u) {
+    const int run = wave + AT_NW * u, row = 4 * run + (lane >> 4), slot = lane & 15;
     koff[u] = (uint32_t)((row * ldk + head * AT_D + 8 * k_slot(slot, row)) * 2);
     voff[u] = (uint32_t)((row * ldv + head * AT_D + 8 * v_slot(slot, row)) * 2);
   }
@@ -82,8 +85,8 @@ __global__ __launch_bounds__(AT_THREADS, 2) void dit_attention_kernel(
     uint8_t* kb = lds + b * AT_STAGE;
     const uint32_t ks = (uint32_t)((int64_t)t * AT_BN * ldk * 2), vs = (uint32_t)((int64_t)t * AT_BN * ldv * 2);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int run = wave + 4 * u;
+    for (int u = 0; u < AT_RUNS; ++u) {
+      const int run = wave + AT_NW * u;
       uint32_t ko = koff[u], vo = voff[u];
       if (rv < AT_BN) {  // workgroup-uniform: the last, partial tile
         const int row = 4 * run + (lane >> 4), slot = lane & 15, src = min(row, rv - 1);
