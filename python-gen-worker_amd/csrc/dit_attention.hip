@@ -4,7 +4,7 @@
 // FluxAttnProcessor calls; here the vendor kernel ran at ~0.49 PFLOP/s).
 //
 // Work split: a 512-thread workgroup owns 256 queries of one head (8 waves x 32 queries) and walks the keys
-// in tiles of 64. K and V tiles ([64 keys][128], as stored) are copied global -> LDS by direct-to-LDS
+// in tiles of 128. K and V tiles ([128 keys][128], as stored) are copied global -> LDS by direct-to-LDS
 // buffer loads (no staging registers, no LDS writes), double buffered: tile t+1's copies are issued before
 // tile t's MFMAs, one wait and one barrier per tile. The 16-byte chunks of a row are XOR-swizzled by the
 // row at copy time (each lane fetches the chunk that belongs at its LDS slot), so the reads below are free
@@ -24,13 +24,15 @@
 namespace {
 
 // 8 waves per workgroup (one workgroup per CU): each K / V tile copy serves 256 queries (4 waves: 128, two
-// workgroups per CU, 319 -> 303 us at 4608 tokens x 24 heads)
-constexpr int AT_D = 128, AT_BN = 64, AT_NW = 8, AT_BM = 32 * AT_NW, AT_THREADS = 64 * AT_NW;
-constexpr int AT_RUNS = 16 / AT_NW;  // 1 KB copy runs per wave, per K and per V tile
+// workgroups per CU, 319 -> 303 us at 4608 tokens x 24 heads); 128-key tiles halve the waits and barriers
+// per key (64-key tiles: 303 -> 298 us)
+constexpr int AT_D = 128, AT_BN = 128, AT_NW = 8, AT_BM = 32 * AT_NW, AT_THREADS = 64 * AT_NW;
+constexpr int AT_NSB = AT_BN / 32, AT_NC = AT_BN / 16;  // 32-key halves and 16-key MFMA steps of a tile
+constexpr int AT_RUNS = AT_BN / 4 / AT_NW;  // 1 KB copy runs (4 rows) per wave, per K and per V tile
 constexpr int AT_ROW = AT_D * 2;                       // tile row bytes (256), chunks swizzled, no padding
-constexpr int AT_TILE = AT_BN * AT_ROW;                // 16 KB per K or V tile
+constexpr int AT_TILE = AT_BN * AT_ROW;                // 32 KB per K or V tile
 constexpr int AT_STAGE = 2 * AT_TILE;                  // K then V
-constexpr int AT_LDS = 2 * AT_STAGE;                   // 64 KB
+constexpr int AT_LDS = 2 * AT_STAGE;                   // 128 KB
 
 typedef float v16f_ __attribute__((ext_vector_type(16)));
 typedef short v4s_ __attribute__((ext_vector_type(4)));
@@ -68,7 +70,7 @@ __global__ __launch_bounds__(AT_THREADS, 8 / AT_NW) void dit_attention_kernel(
     for (int cd = 0; cd < 8; ++cd) qop[cd] = q_ok ? *(const v4i*)(qp + 16 * cd) : (v4i){0, 0, 0, 0};
   }
 
-  // copies: 16 runs of 1 KB (4 rows) per K tile and per V tile, runs wave, wave + 8 of each; lane l of a
+  // copies: 32 runs of 1 KB (4 rows) per K tile and per V tile, runs wave + 8 u of each; lane l of a
   // run lands at LDS slot l % 16 of row 4 run + l / 16 and fetches the chunk that belongs there
   const v4i kbuf = raw_rsrc(k, (uint32_t)(((int64_t)(Skv - 1) * ldk + gridDim.y * AT_D) * 2));
   const v4i vbuf = raw_rsrc(v, (uint32_t)(((int64_t)(Skv - 1) * ldv + gridDim.y * AT_D) * 2));
@@ -79,7 +81,7 @@ __global__ __launch_bounds__(AT_THREADS, 8 / AT_NW) void dit_attention_kernel(
     koff[u] = (uint32_t)((row * ldk + head * AT_D + 8 * k_slot(slot, row)) * 2);
     voff[u] = (uint32_t)((row * ldv + head * AT_D + 8 * v_slot(slot, row)) * 2);
   }
-  // tile t into stage buffer b; a last tile with rv < 64 keys repeats its last key in the rows past it (their
+  // tile t into stage buffer b; a last tile with rv < 128 keys repeats its last key in the rows past it (their
   // scores are masked to -inf below, so they weigh 0)
   auto issue = [&](int t, int b, int rv) __attribute__((always_inline)) {
     uint8_t* kb = lds + b * AT_STAGE;
@@ -101,26 +103,19 @@ __global__ __launch_bounds__(AT_THREADS, 8 / AT_NW) void dit_attention_kernel(
   // read offsets, loop-invariant: K rows 32 sb + j, chunks 2 cd + h; V^T operand (d block db, 16-key step c):
   // lane p = lane % 16 of group g = lane / 16 (half hh = g / 2, column half dh = g % 2) points at key
   // 16 c + 4 hh + p / 4 (+ 8 for the second read), columns 32 db + 16 dh + 4 (p % 4) .. + 4
-  uint32_t kro[2][8];
+  // (the swizzles depend on a row's low 4 / 3 bits only, so the 32-key half sb and the 16-key step c are
+  // constant offsets)
+  uint32_t kro[8];
 #pragma unroll
-  for (int sb = 0; sb < 2; ++sb)
-#pragma unroll
-    for (int cd = 0; cd < 8; ++cd) {
-      const int row = 32 * sb + j;
-      kro[sb][cd] = (uint32_t)(row * AT_ROW + 16 * k_slot(2 * cd + h, row));
-    }
+  for (int cd = 0; cd < 8; ++cd) kro[cd] = (uint32_t)(j * AT_ROW + 16 * k_slot(2 * cd + h, j));
   const int pg = lane & 15, hh = lane >> 5, dh = (lane >> 4) & 1;
-  uint32_t vro[4][4][2];
+  uint32_t vbase[4];
 #pragma unroll
-  for (int c = 0; c < 4; ++c)
-#pragma unroll
-    for (int db = 0; db < 4; ++db)
-#pragma unroll
-      for (int hb = 0; hb < 2; ++hb) {
-        const int row = 16 * c + 8 * hb + 4 * hh + (pg >> 2);
-        const int col = 32 * db + 16 * dh + 4 * (pg & 3);          // bf16 column; 8-byte piece of a chunk
-        vro[c][db][hb] = (uint32_t)(AT_TILE + row * AT_ROW + 16 * v_slot(col >> 3, row) + 2 * (col & 7));
-      }
+  for (int db = 0; db < 4; ++db) {
+    const int row = 4 * hh + (pg >> 2);
+    const int col = 32 * db + 16 * dh + 4 * (pg & 3);              // bf16 column; 8-byte piece of a chunk
+    vbase[db] = (uint32_t)(AT_TILE + row * AT_ROW + 16 * v_slot(col >> 3, row) + 2 * (col & 7));
+  }
 
   v16f_ oacc[4];
 #pragma unroll
@@ -128,32 +123,38 @@ __global__ __launch_bounds__(AT_THREADS, 8 / AT_NW) void dit_attention_kernel(
   float m_run = -INFINITY, l_run = 0.0f;
 
   const int ntiles = (Skv + AT_BN - 1) / AT_BN;
-  const int rv_last = Skv - (ntiles - 1) * AT_BN;      // keys in the last tile (1 .. 64)
+  const int rv_last = Skv - (ntiles - 1) * AT_BN;      // keys in the last tile (1 .. AT_BN)
   issue(0, 0, ntiles == 1 ? rv_last : AT_BN);
   wait_vm_lgkm0<0>();
   barrier_lds();
   for (int t = 0; t < ntiles; ++t) {
     const uint8_t* kb = lds + (t & 1) * AT_STAGE;
     if (t + 1 < ntiles) issue(t + 1, (t + 1) & 1, t + 2 == ntiles ? rv_last : AT_BN);
-    // S^T for the two 32-key halves of the tile (the two chains interleaved)
-    v16f_ sc[2] = {(v16f_){}, (v16f_){}};
+    // S^T for the 32-key halves of the tile (their chains interleaved)
+    v16f_ sc[AT_NSB];
+#pragma unroll
+    for (int sb = 0; sb < AT_NSB; ++sb) sc[sb] = (v16f_){};
 #pragma unroll
     for (int cd = 0; cd < 8; ++cd)
 #pragma unroll
-      for (int sb = 0; sb < 2; ++sb)
-        sc[sb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*(const v8bf*)(kb + kro[sb][cd]),
+      for (int sb = 0; sb < AT_NSB; ++sb)
+        sc[sb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*(const v8bf*)(kb + sb * 32 * AT_ROW + kro[cd]),
                                                          __builtin_bit_cast(v8bf, qop[cd]), sc[sb], 0, 0, 0);
     if (t + 1 == ntiles && rv_last < AT_BN) {  // keys past Skv: score -inf (lane's key 32 sb + 8 a + 4 h + r)
 #pragma unroll
-      for (int sb = 0; sb < 2; ++sb)
+      for (int sb = 0; sb < AT_NSB; ++sb)
 #pragma unroll
         for (int i = 0; i < 16; ++i)
           if (32 * sb + 8 * (i >> 2) + 4 * h + (i & 3) >= rv_last) sc[sb][i] = -INFINITY;
     }
-    // online softmax of tile t (scaled domain: x = s * c_log2); max of the lane's 32 scores as a tree
+    // online softmax of tile t (scaled domain: x = s * c_log2); max of the lane's scores as a tree
     float m8[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) m8[i] = fmaxf(fmaxf(sc[0][i], sc[0][i + 8]), fmaxf(sc[1][i], sc[1][i + 8]));
+    for (int i = 0; i < 8; ++i) {
+      m8[i] = fmaxf(sc[0][i], sc[0][i + 8]);
+#pragma unroll
+      for (int sb = 1; sb < AT_NSB; ++sb) m8[i] = fmaxf(m8[i], fmaxf(sc[sb][i], sc[sb][i + 8]));
+    }
 #pragma unroll
     for (int w = 4; w >= 1; w >>= 1)
 #pragma unroll
@@ -164,10 +165,10 @@ __global__ __launch_bounds__(AT_THREADS, 8 / AT_NW) void dit_attention_kernel(
     const float m_new = bump ? x_max : m_run;
     const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 on the first tile (m_run = -inf)
     m_run = m_new;
-    float ps[4];                                         // four partial row sums (short dependent chains)
-    v4i pop[4];                                          // p^T operands of the four 16-key steps
+    float ps[AT_NC];                                     // partial row sums (short dependent chains)
+    v4i pop[AT_NC];                                      // p^T operands of the 16-key steps
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
+    for (int c = 0; c < AT_NC; ++c) {
       const int sb = c >> 1, r0 = 8 * (c & 1);
       float p[8];
 #pragma unroll
@@ -176,7 +177,11 @@ __global__ __launch_bounds__(AT_THREADS, 8 / AT_NW) void dit_attention_kernel(
       pop[c] = (v4i){(int)pack_bf16_pair(p[0], p[1]), (int)pack_bf16_pair(p[2], p[3]),
                      (int)pack_bf16_pair(p[4], p[5]), (int)pack_bf16_pair(p[6], p[7])};
     }
-    const float psum = (ps[0] + ps[1]) + (ps[2] + ps[3]);
+#pragma unroll
+    for (int w = AT_NC / 2; w >= 1; w >>= 1)
+#pragma unroll
+      for (int i = 0; i < w; ++i) ps[i] += ps[i + w];
+    const float psum = ps[0];
     l_run = __builtin_fmaf(l_run, alpha, psum);
     if (__builtin_amdgcn_ballot_w64(bump) != 0) {  // wave-uniform: alpha == 1 in lanes that did not move
 #pragma unroll
@@ -186,8 +191,9 @@ __global__ __launch_bounds__(AT_THREADS, 8 / AT_NW) void dit_attention_kernel(
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const v4s_ a0 = lds_read_tr(kb + vro[c][db][0]), a1 = lds_read_tr(kb + vro[c][db][1]);
+      for (int c = 0; c < AT_NC; ++c) {
+        const v4s_ a0 = lds_read_tr(kb + vbase[db] + 16 * c * AT_ROW);
+        const v4s_ a1 = lds_read_tr(kb + vbase[db] + (16 * c + 8) * AT_ROW);
         const v8bf av = __builtin_bit_cast(v8bf, (v4i){__builtin_bit_cast(int, (v2s_){a0[0], a0[1]}),
                                                       __builtin_bit_cast(int, (v2s_){a0[2], a0[3]}),
                                                       __builtin_bit_cast(int, (v2s_){a1[0], a1[1]}),

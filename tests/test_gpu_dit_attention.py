@@ -52,7 +52,8 @@ def _inputs(s, skv, heads, seed, fused_v=False):
 @pytest.mark.parametrize("s,skv,heads,check,fused_v", [(4608, 4608, 24, (0, 7, 13, 23), True),
                                                        (256, 256, 4, (0, 1, 2, 3), False),
                                                        (200, 320, 3, (0, 1, 2), False),
-                                                       (130, 257, 2, (0, 1), False), (64, 40, 2, (0, 1), True)])
+                                                       (130, 257, 2, (0, 1), False), (96, 200, 2, (0, 1), False),
+                                                       (64, 40, 2, (0, 1), True)])
 def test_attention_matches_fp32_reference(s, skv, heads, check, fused_v):
     from gen_worker_amd.flux_dit import _sdpa, attention
 
