@@ -556,7 +556,8 @@ def only_awq(args) -> int:
 
 def only_dit(args) -> int:
     """``--only dit``: the config-4 W4A4 DiT (int4 lane) forward eagerly ``--iters`` times after 2 warmups,
-    for rocprofv3 (each forward's kernels; the model's construction runs before them)."""
+    for rocprofv3 (each forward's kernels; the model's construction runs before them). ``--streams 1`` runs
+    every kernel on one stream, so each kernel's trace duration is its own (with 2 they share the CUs)."""
     import torch
 
     import gen_worker_amd  # noqa: F401
@@ -565,7 +566,7 @@ def only_dit(args) -> int:
 
     _native.load()
     cfg = FluxDiTConfig()
-    model = FluxDiT("w4a4", cfg, modulation=args.modulation, lane="int4", streams=2)
+    model = FluxDiT("w4a4", cfg, modulation=args.modulation, lane="int4", streams=args.streams)
     x = inputs(cfg)
     with torch.no_grad():
         for _ in range(2):
@@ -588,6 +589,9 @@ def main() -> int:
     ap.add_argument("--only", choices=("step", "gemm", "quant", "copy", "awq", "w8a8", "w8a8_gemm", "dit"),
                     default=None)
     ap.add_argument("--iters", type=int, default=5)
+    ap.add_argument("--streams", type=int, choices=(1, 2), default=2,
+                    help="with --only dit: 1 runs the forward on one HIP stream (per-kernel profiles), 2 overlaps "
+                         "the text stream, the single blocks' MLP branch and the modulation linears (the bench's)")
     ap.add_argument("--tile", type=int, default=-1,
                     help="with --only gemm/step: force the fp6 GEMM's output tile (GWA_FP6_TILE_*; -1: the model's); "
                          "with --only w8a8_gemm: the int8 GEMM's (GWA_W8A8_TILE_*)")
