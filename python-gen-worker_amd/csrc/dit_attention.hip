@@ -19,6 +19,8 @@
 // x 16 head-dim columns hand each lane 4 keys of one column. The key order inside a 16-key MFMA step is the
 // one S^T's output layout leaves p in, so p goes from the S MFMA to the O MFMA without leaving registers.
 // Output o = O / l in bf16, written as rows [query][head][128] (the layout the next linear reads).
+#include <type_traits>
+
 #include "fp6_gemm_common.h"
 
 namespace {
@@ -127,7 +129,12 @@ __global__ __launch_bounds__(AT_THREADS, 8 / AT_NW) void dit_attention_kernel(
   issue(0, 0, ntiles == 1 ? rv_last : AT_BN);
   wait_vm_lgkm0<0>();
   barrier_lds();
-  for (int t = 0; t < ntiles; ++t) {
+  // one tile step; LAST (the partial last tile only) masks the keys past Skv. Taking that tile out of the
+  // loop keeps the mask out of the full tiles' code: with the uniform test inside the loop the compiler
+  // hoisted the 64 per-lane key compares, spilled their masks to VGPR lanes and selected every score in
+  // every tile (126 extra VALU instructions per tile).
+  auto step = [&](int t, auto last_c) __attribute__((always_inline)) {
+    constexpr bool LAST = decltype(last_c)::value;
     const uint8_t* kb = lds + (t & 1) * AT_STAGE;
     if (t + 1 < ntiles) issue(t + 1, (t + 1) & 1, t + 2 == ntiles ? rv_last : AT_BN);
     // S^T for the 32-key halves of the tile (their chains interleaved)
@@ -140,7 +147,7 @@ __global__ __launch_bounds__(AT_THREADS, 8 / AT_NW) void dit_attention_kernel(
       for (int sb = 0; sb < AT_NSB; ++sb)
         sc[sb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*(const v8bf*)(kb + sb * 32 * AT_ROW + kro[cd]),
                                                          __builtin_bit_cast(v8bf, qop[cd]), sc[sb], 0, 0, 0);
-    if (t + 1 == ntiles && rv_last < AT_BN) {  // keys past Skv: score -inf (lane's key 32 sb + 8 a + 4 h + r)
+    if (LAST) {  // keys past Skv: score -inf (lane's key 32 sb + 8 a + 4 h + r)
 #pragma unroll
       for (int sb = 0; sb < AT_NSB; ++sb)
 #pragma unroll
@@ -202,7 +209,10 @@ __global__ __launch_bounds__(AT_THREADS, 8 / AT_NW) void dit_attention_kernel(
       }
     wait_vm_lgkm0<0>();  // this wave's copies of tile t + 1 have landed
     barrier_lds();       // everyone's have; everyone is done reading tile t's buffer
-  }
+  };
+  const int nfull = rv_last < AT_BN ? ntiles - 1 : ntiles;
+  for (int t = 0; t < nfull; ++t) step(t, std::false_type{});
+  if (nfull < ntiles) step(nfull, std::true_type{});
   // o = O / l (the two lane halves hold the row sum's two halves)
   const float l_tot = l_run + __shfl_xor(l_run, 32);
   const float inv = 1.0f / l_tot;
