@@ -158,9 +158,12 @@ __global__ __launch_bounds__(AT_THREADS, 8 / AT_NW) void dit_attention_kernel(
     float m8[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      m8[i] = fmaxf(sc[0][i], sc[0][i + 8]);
+      // first level as med3(a, b, 3e38) = max(a, b) for scores below 3e38: fmaxf on raw MFMA results first
+      // quiets each input (one v_max x, x per score: 101 max instructions per tile, now 52), med3's results
+      // count as quieted, so the levels above need none (a +inf bound is folded back into fmaxf)
+      m8[i] = __builtin_amdgcn_fmed3f(sc[0][i], sc[0][i + 8], 3.0e38f);
 #pragma unroll
-      for (int sb = 1; sb < AT_NSB; ++sb) m8[i] = fmaxf(m8[i], fmaxf(sc[sb][i], sc[sb][i + 8]));
+      for (int sb = 1; sb < AT_NSB; ++sb) m8[i] = fmaxf(m8[i], __builtin_amdgcn_fmed3f(sc[sb][i], sc[sb][i + 8], 3.0e38f));
     }
 #pragma unroll
     for (int w = 4; w >= 1; w >>= 1)
