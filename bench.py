@@ -58,6 +58,12 @@ HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, 8 TB/s
 COPY_BYTES = 64 << 20        # calibration copy for the traffic counters
 
 
+ATTENTION_DESC = {"sdpa": "torch bf16 scaled_dot_product_attention (flash / memory-efficient kernels only)",
+                  "flash": "bf16 flash attention (gwa_dit_attention)"}
+STREAMS_DESC = ("both models: dual blocks' text stream and single blocks' MLP branch on a second HIP stream, the "
+                "modulation linears queued on a third")
+
+
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
@@ -151,13 +157,14 @@ def summarize_traffic(d: Path) -> int:
     return 0
 
 
-def dit_step_pair(steps: int, warmup: int, modulation: str = "w4a4") -> dict:
+def dit_step_pair(steps: int, warmup: int, modulation: str = "w4a4", attention: str = "sdpa") -> dict:
     """Config 4: one Flux-dev-shaped denoiser forward (batch 1, 4096 image + 512 text tokens, 19 + 38
     blocks), every linear W4A4 rank 32 on the int4 lane (``modulation="awq"``: the one-token adaLN modulation
     linears AWQ W4A16, as an svdq checkpoint stores them) vs the same model with bf16 nn.Linear GEMMs; the
-    same attention kernel and block glue in both. The W4A4 model is pinned to the int4 lane (the path being measured); the arming gate's own
-    decision on this box is reported beside it as ``gate_lane``. Each model's forward is captured once in a
-    HIP graph and replayed ``steps`` times."""
+    same attention (``"sdpa"``: torch's bf16 SDPA, as config 4 states; ``"flash"``: gwa_dit_attention), block
+    glue and stream overlap in both. The W4A4 model is pinned to the int4 lane (the path being measured); the
+    arming gate's own decision on this box is reported beside it as ``gate_lane``. Each model's forward is
+    captured once in a HIP graph and replayed ``steps`` times."""
     import gc
 
     import torch
@@ -171,8 +178,9 @@ def dit_step_pair(steps: int, warmup: int, modulation: str = "w4a4") -> dict:
 
     res["gate_lane"] = resolve_lane()
     for kind in ("w4a4", "bf16"):
-        log(f"bench: building the {kind} DiT")
-        model = FluxDiT(kind, cfg, modulation=modulation, lane="int4" if kind == "w4a4" else None, streams=2)
+        log(f"bench: building the {kind} DiT ({attention} attention)")
+        model = FluxDiT(kind, cfg, modulation=modulation, lane="int4" if kind == "w4a4" else None, streams=2,
+                        attention=attention)
         res[kind + "_lane"] = model.lane
         torch.cuda.synchronize()
         log(f"bench: timing the {kind} DiT step ({steps} graph replays, {model.lane} lane)")
@@ -196,7 +204,7 @@ def bench_dit(args) -> int:
 
     _native.load()
     torch.cuda.set_device(0)
-    res = dit_step_pair(args.steps, args.warmup, args.modulation)
+    res = dit_step_pair(args.steps, args.warmup, args.modulation, args.attention)
     cfg = res["cfg"]
     ops_ = block_int_ops(cfg)
     out = {"metric": "DiT step ms (Flux-dev-shaped, batch 1, 4096+512 tokens, 19+38 blocks)",
@@ -204,12 +212,11 @@ def bench_dit(args) -> int:
            "higher_is_better": False, "dtype": "int4", "data": "synthetic",
            "config": {"workload": "flux_dit_c4", "hidden": cfg.hidden, "heads": cfg.heads, "mlp": cfg.mlp,
                       "dual_blocks": cfg.n_dual, "single_blocks": cfg.n_single, "img_tokens": cfg.img_tokens,
-                      "txt_tokens": cfg.txt_tokens, "rank": cfg.rank, "attention": "bf16 flash attention (gwa_dit_attention)",
+                      "txt_tokens": cfg.txt_tokens, "rank": cfg.rank, "attention": ATTENTION_DESC[args.attention],
                       "modulation": ("W4A4 (one token)" if args.modulation == "w4a4"
                                      else "AWQ W4A16 g64 (one token)"),
                       "lane": res["w4a4_lane"], "gate_lane": res["gate_lane"],
-                      "streams": "dual blocks' text stream on a second HIP stream (both models)",
-                      "timing": "forward captured in one HIP graph, replayed"},
+                      "streams": STREAMS_DESC, "timing": "forward captured in one HIP graph, replayed"},
            "bf16_gemm_ms": round(res["bf16"], 3), "speedup_vs_bf16": round(res["bf16"] / res["w4a4"], 4),
            "block_linear_int_ops": ops_, "outputs_finite": {"w4a4": res["w4a4_finite"], "bf16": res["bf16_finite"]}}
     print(json.dumps(out), flush=True)
@@ -566,7 +573,8 @@ def only_dit(args) -> int:
 
     _native.load()
     cfg = FluxDiTConfig()
-    model = FluxDiT("w4a4", cfg, modulation=args.modulation, lane="int4", streams=args.streams)
+    model = FluxDiT("w4a4", cfg, modulation=args.modulation, lane="int4", streams=args.streams,
+                    attention=args.attention)
     x = inputs(cfg)
     with torch.no_grad():
         for _ in range(2):
@@ -605,6 +613,9 @@ def main() -> int:
     ap.add_argument("--modulation", choices=("w4a4", "awq"), default="w4a4",
                     help="the DiT's one-token adaLN modulation linears: W4A4 like every other linear (config 4 "
                          "as stated), or AWQ W4A16 as an svdq checkpoint stores them")
+    ap.add_argument("--attention", choices=("sdpa", "flash"), default="sdpa",
+                    help="the DiT's attention: torch's bf16 SDPA (config 4 as stated) or gwa_dit_attention; the "
+                         "default (c1) line reports SDPA as dit_* and the flash kernel as dit_*_flash_attention")
     ap.add_argument("--dit-steps", type=int, default=3,
                     help="graph replays of each DiT forward in the default (c1) line; 0 skips the DiT half")
     ap.add_argument("--summarize-traffic", metavar="DIR", default=None,
@@ -786,12 +797,19 @@ def main() -> int:
     if args.dit_steps > 0:
         # the metric's second half: the config-4 DiT step, W4A4 (int4 lane) against bf16 GEMMs
         torch.cuda.empty_cache()
-        res = dit_step_pair(args.dit_steps, 1, args.modulation)
+        res = dit_step_pair(args.dit_steps, 1, args.modulation, "sdpa")
         out.update({"dit_step_ms": round(res["w4a4"], 3), "dit_bf16_step_ms": round(res["bf16"], 3),
                     "dit_speedup_vs_bf16": round(res["bf16"] / res["w4a4"], 4), "dit_lane": res["w4a4_lane"],
                     "dit_gate_lane": res["gate_lane"],
-                    "dit_modulation": args.modulation,
+                    "dit_modulation": args.modulation, "dit_attention": ATTENTION_DESC["sdpa"],
+                    "dit_streams": STREAMS_DESC,
                     "dit_outputs_finite": res["w4a4_finite"] and res["bf16_finite"]})
+        # the same pair with this package's flash-attention kernel in both models (not config 4 as stated)
+        torch.cuda.empty_cache()
+        rf = dit_step_pair(args.dit_steps, 1, args.modulation, "flash")
+        out.update({"dit_step_ms_flash_attention": round(rf["w4a4"], 3),
+                    "dit_bf16_step_ms_flash_attention": round(rf["bf16"], 3),
+                    "dit_speedup_vs_bf16_flash_attention": round(rf["bf16"] / rf["w4a4"], 4)})
     print(json.dumps(out), flush=True)
     return 0
 

@@ -57,6 +57,15 @@ enum {
  * row stride. */
 enum { GWA_FP6_REC = 104 };
 
+/* Readable bytes the fp6 GEMMs need past the last record of each record
+ * buffer they read (qa6, qw6): they copy records into LDS in 1 KB runs with
+ * scalar offsets the hardware does not range-check, and the run holding a
+ * tile's last real row may reach this far past it. Every entry point that
+ * takes a record pointer also takes its readable byte count (from the
+ * pointer to the end of its storage) and refuses a buffer shorter than the
+ * records plus this slack with GWA_ERR_INVALID. */
+enum { GWA_FP6_RECORD_SLACK = 1024 };
+
 /* Library version and build description ("archs=gfx950 hip=..."). Mirrors
  * cozy_kernels::build_info, csrc/cozy_kernels/ops.cpp:23-27. */
 int gwa_version(void);
@@ -134,21 +143,24 @@ int gwa_svdq_group_psums(const uint8_t* qa, const uint8_t* qw, int32_t* out,
  * in [-8, 7].
  *   qw   uint8 [N, K/2] logical two's-complement codes (in)
  *   sw   fp16 [N, K/64] group scales (in)
- *   qw6  uint8 [K/128, N, 104] records (out); K % 128 == 0. Allocate 1024
- *        bytes of slack after it (gwa_svdq_gemm_w4a4_fp6 reads up to 1 KB past). */
+ *   qw6  uint8 [K/128, N, 104] records (out); K % 128 == 0. Allocate
+ *        GWA_FP6_RECORD_SLACK bytes of slack after it (the GEMMs read up to 1 KB
+ *        past and refuse a shorter buffer). */
 int gwa_svdq_pack_weight_fp6(const uint8_t* qw, const void* sw, uint8_t* qw6, int64_t N, int64_t K, void* stream);
 
 /* Kernel 2, fp6 path: the contract of gwa_svdq_gemm_w4a4 (replacing
  * _gemm_w4a4 + svdq_epilogue_lora, models/w4a4.py:173-180 and
  * models/svdq_fused.py:315-377) on fp6 operand records: qa6 [K/128, M, 104]
  * from gwa_svdq_quant_fp6, qw6 [K/128, N, 104] from gwa_svdq_pack_weight_fp6
- * (the records carry sa and sw). The storage of qa6 and of qw6 must stay
- * readable for 1024 bytes past its last record (operand records are copied
- * in 1 KB runs; the run holding a tile's last real row may reach past it).
+ * (the records carry sa and sw). qa6_bytes / qw6_bytes are the readable
+ * bytes from each pointer to the end of its storage: at least the records
+ * ((K/128) * M * 104, (K/128) * N * 104) plus GWA_FP6_RECORD_SLACK, else
+ * GWA_ERR_INVALID before any launch (operand records are copied in 1 KB runs;
+ * the run holding a tile's last real row may reach past them).
  * One exact fp6 MFMA per K-group and 32x32 block. la is bf16 [M, rank], or fp32 with GWA_EPI_LA_F32 in
  * epilogue_flags (rounded to bf16 in the epilogue). K % 128 == 0,
  * N % 16 == 0. */
-int gwa_svdq_gemm_w4a4_fp6(const uint8_t* qa6, const uint8_t* qw6,
+int gwa_svdq_gemm_w4a4_fp6(const uint8_t* qa6, int64_t qa6_bytes, const uint8_t* qw6, int64_t qw6_bytes,
                            const float* s2, const float* second, int64_t second_numel,
                            const void* la, const void* up, int64_t rank, const void* bias,
                            void* out, int out_dtype, int epilogue_flags,
@@ -179,8 +191,9 @@ int gwa_svdq_gemm_w4a4_fp6(const uint8_t* qa6, const uint8_t* qw6,
  *   next_proj_down_op the next layer's proj_down rows for these N inputs in
  *            gwa_svdq_prep_proj_down_fp6 order, next_rank in {0,16,32,64,128}
  * Single-level (the next layer's s2 = 1). Output dtype bf16; la may be fp32
- * (GWA_EPI_LA_F32). N % 128 == 0, K % 128 == 0. */
-int gwa_svdq_gemm_w4a4_fp6_next(const uint8_t* qa6, const uint8_t* qw6,
+ * (GWA_EPI_LA_F32). qa6_bytes / qw6_bytes as gwa_svdq_gemm_w4a4_fp6 checks
+ * them. N % 128 == 0, K % 128 == 0. */
+int gwa_svdq_gemm_w4a4_fp6_next(const uint8_t* qa6, int64_t qa6_bytes, const uint8_t* qw6, int64_t qw6_bytes,
                                 const float* s2, const float* second, int64_t second_numel,
                                 const void* la, const void* up, int64_t rank, const void* bias,
                                 void* out, int epilogue_flags,
@@ -262,9 +275,11 @@ int gwa_svdq_la_reduce(const float* part, int64_t P, int64_t M, int64_t rank, vo
 int gwa_svdq_prep_proj_down_fp6(const void* proj_down, void* out, int64_t K, int64_t rank, void* stream);
 
 /* Debug: exact int32 per-group partial sums (layout of gwa_svdq_group_psums)
- * through the fp6 GEMM's MFMA on fp6 operand records. No reference counterpart. */
-int gwa_svdq_group_psums_fp6(const uint8_t* qa6, const uint8_t* qw6, int32_t* out,
-                             int64_t M, int64_t N, int64_t K, void* stream);
+ * through the fp6 GEMM's MFMA on fp6 operand records. No reference
+ * counterpart. This kernel reads records through range-checked lane offsets:
+ * qa6_bytes / qw6_bytes must cover the records, no slack. */
+int gwa_svdq_group_psums_fp6(const uint8_t* qa6, int64_t qa6_bytes, const uint8_t* qw6, int64_t qw6_bytes,
+                             int32_t* out, int64_t M, int64_t N, int64_t K, void* stream);
 
 /* One whole SVDQuant W4A4 linear on the fp6 lane: the forward of the
  * reference's fused module, _SvdqFusedLinear.forward
@@ -276,8 +291,10 @@ int gwa_svdq_group_psums_fp6(const uint8_t* qa6, const uint8_t* qw6, int32_t* ou
  *            s2 fp32 device scalar or NULL (= 1.0)
  *   proj_down_op6  gwa_svdq_prep_proj_down_fp6 order, or NULL (rank 0);
  *            proj_up bf16 [N, rank] (NULL iff proj_down_op6 is NULL)
- *   qw6      the weight's fp6 records (gwa_svdq_pack_weight_fp6, with 1 KB of
- *            readable slack after them)
+ *   qw6      the weight's fp6 records (gwa_svdq_pack_weight_fp6) and
+ *            qw6_bytes, its readable bytes: >= (K/128) * N * 104 +
+ *            GWA_FP6_RECORD_SLACK (the activation records live in the
+ *            workspace, slack included)
  *   second / bias / out / out_dtype as gwa_svdq_gemm_w4a4_fp6; epilogue_flags
  *            GWA_EPI_GELU_TANH or 0
  *   workspace  device memory of workspace_bytes >=
@@ -287,7 +304,7 @@ int gwa_svdq_group_psums_fp6(const uint8_t* qa6, const uint8_t* qw6, int32_t* ou
  *            reused by another call until this call's work on `stream` ends.
  * K % 128 == 0, N % 16 == 0. */
 int gwa_svdq_w4a4_linear_fp6(const void* x, int64_t ldx, const void* smooth, const float* s2,
-                             const void* proj_down_op6, int64_t rank, const uint8_t* qw6,
+                             const void* proj_down_op6, int64_t rank, const uint8_t* qw6, int64_t qw6_bytes,
                              const float* second, int64_t second_numel, const void* proj_up,
                              const void* bias, void* out, int out_dtype, int epilogue_flags,
                              int64_t M, int64_t N, int64_t K, void* workspace, int64_t workspace_bytes,
@@ -318,7 +335,7 @@ enum { GWA_NOALLOC_SCRATCH_MIB = 128 };
  * with the stream's device current. Same arguments and results as
  * gwa_svdq_w4a4_linear_fp6. */
 int gwa_svdq_w4a4_linear_fp6_noalloc(const void* x, int64_t ldx, const void* smooth, const float* s2,
-                                     const void* proj_down_op6, int64_t rank, const uint8_t* qw6,
+                                     const void* proj_down_op6, int64_t rank, const uint8_t* qw6, int64_t qw6_bytes,
                                      const float* second, int64_t second_numel, const void* proj_up,
                                      const void* bias, void* out, int out_dtype, int epilogue_flags,
                                      int64_t M, int64_t N, int64_t K, void* stream);

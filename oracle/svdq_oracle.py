@@ -334,11 +334,23 @@ def int8_gemm(qa: np.ndarray, qw: np.ndarray) -> np.ndarray:
 
 def w8a8_linear(x_bits: np.ndarray, qw: np.ndarray, sw: np.ndarray,
                 bias: np.ndarray | None, pertensor: bool = False,
-                static: float | None = None) -> np.ndarray:
-    """``_scaled_mm(xq, W^T, scale_a=sa, scale_b=sw^T, bias)`` (``models/w8a8.py:374-378``; the pertensor
-    branch ``:366-372`` applies the same scales) in float64, activation quant as :func:`quantize_act_int8`."""
+                static: float | None = None, ref_roundings: bool = False) -> np.ndarray:
+    """``_scaled_mm(xq, W^T, scale_a=sa, scale_b=sw^T, bias)`` (``models/w8a8.py:374-378``) in float64,
+    activation quant as :func:`quantize_act_int8`. The pertensor branch (``:366-372``) is the same product
+    with every scale applied exactly, unless ``ref_roundings``: then it takes the reference's three bf16
+    roundings, ``y0 = bf16(acc * sa)`` (``_scaled_mm`` with unit ``scale_b``, bf16 out), ``y1 = bf16(y0 *
+    bf16(sw))`` (the weight scale cast to the output dtype), ``y = bf16(y1 + bias)`` (a bf16 bias), returned
+    as float64 values of those bf16 numbers."""
     qa, sa = quantize_act_int8(x_bits, pertensor, static)
     acc = int8_gemm(qa, qw).astype(np.float64)
+    if ref_roundings and pertensor:
+        y0 = round_bf16((acc * sa.astype(np.float64)).astype(np.float32))
+        sw16 = round_bf16(sw.astype(np.float32).reshape(1, -1))
+        y = round_bf16((y0.astype(np.float64) * sw16.astype(np.float64)).astype(np.float32))
+        if bias is not None:
+            b16 = round_bf16(np.asarray(bias, dtype=np.float32).reshape(1, -1))
+            y = round_bf16((y.astype(np.float64) + b16.astype(np.float64)).astype(np.float32))
+        return y.astype(np.float64)
     y = acc * sa.astype(np.float64) * sw.astype(np.float64).reshape(1, -1)
     if bias is not None:
         y = y + np.asarray(bias, dtype=np.float64).reshape(1, -1)

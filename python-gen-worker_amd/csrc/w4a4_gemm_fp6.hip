@@ -700,14 +700,20 @@ extern "C" int gwa_svdq_pack_weight_fp6(const uint8_t* qw, const void* sw, uint8
   return gwa_check_launch("svdq_pack_weight_fp6");
 }
 
-extern "C" int gwa_svdq_group_psums_fp6(const uint8_t* qa6, const uint8_t* qw6, int32_t* out, int64_t M, int64_t N,
-                                        int64_t K, void* stream) {
+extern "C" int gwa_svdq_group_psums_fp6(const uint8_t* qa6, int64_t qa6_bytes, const uint8_t* qw6,
+                                        int64_t qw6_bytes, int32_t* out, int64_t M, int64_t N, int64_t K,
+                                        void* stream) {
   GWA_REQUIRE(M >= 0 && N >= 0 && K > 0 && K % 128 == 0, "svdq_group_psums_fp6: bad shape (K %% 128 == 0)");
   GWA_REQUIRE(M < (1ll << 31) && N < (1ll << 30) && K < (1ll << 30) && M * N * (K / 64) * 4 < (1ll << 31) &&
                   M * (K / 128) * REC < (1ll << 31) && N * (K / 128) * REC < (1ll << 31),
               "svdq_group_psums_fp6: shape too large (buffers must stay below 2 GiB)");
   GWA_REQUIRE((N + 31) / 32 < 65536, "svdq_group_psums_fp6: N too large");
   if (M == 0 || N == 0) return GWA_OK;
+  // this kernel reads each lane's record bytes through range-checked lane offsets: the records, no slack
+  GWA_REQUIRE(qa6_bytes >= (K / 128) * M * REC && qw6_bytes >= (K / 128) * N * REC,
+              "svdq_group_psums_fp6: record buffers of %lld / %lld bytes, the shape needs %lld / %lld",
+              (long long)qa6_bytes, (long long)qw6_bytes, (long long)((K / 128) * M * REC),
+              (long long)((K / 128) * N * REC));
   GWA_REQUIRE(qa6 && qw6 && out, "svdq_group_psums_fp6: null pointer");
   GWA_REQUIRE(GWA_ALIGNED(qa6, 8) && GWA_ALIGNED(qw6, 8) && GWA_ALIGNED(out, 4),
               "svdq_group_psums_fp6: misaligned pointer");
@@ -806,10 +812,10 @@ int fp6_tile_m(int tile) { return kFp6Shapes[tile].tm; }
 int fp6_tile_n(int tile) { return kFp6Shapes[tile].tn; }
 
 // shared argument checks and launch of both GEMM entry points (nx.q6 != NULL: the NQ epilogue)
-int gemm_fp6(const char* what, const uint8_t* qa6, const uint8_t* qw6, const float* s2, const float* second,
-             int64_t second_numel, const void* la, const void* up, int64_t rank, const void* bias, void* out,
-             int out_dtype, int epilogue_flags, int64_t M, int64_t N, int64_t K, const NextLayer& nx,
-             void* stream) {
+int gemm_fp6(const char* what, const uint8_t* qa6, int64_t qa6_bytes, const uint8_t* qw6, int64_t qw6_bytes,
+             const float* s2, const float* second, int64_t second_numel, const void* la, const void* up, int64_t rank,
+             const void* bias, void* out, int out_dtype, int epilogue_flags, int64_t M, int64_t N, int64_t K,
+             const NextLayer& nx, void* stream) {
   GWA_REQUIRE(M >= 0 && N > 0 && K > 0, "%s: bad shape M=%lld N=%lld K=%lld", what, (long long)M, (long long)N,
               (long long)K);
   GWA_REQUIRE(K % 128 == 0, "%s: K=%lld is not a multiple of 128", what, (long long)K);
@@ -832,6 +838,16 @@ int gemm_fp6(const char* what, const uint8_t* qa6, const uint8_t* qw6, const flo
   if (M == 0) return GWA_OK;
   const bool nq = nx.q6 != nullptr;
   GWA_REQUIRE(qa6 && qw6 && (out || nq), "%s: null pointer", what);
+  // the copies move records in 1 KB runs with unchecked scalar offsets: the run holding a tile's last real
+  // row may read up to GWA_FP6_RECORD_SLACK bytes past the last record
+  GWA_REQUIRE(qa6_bytes >= nst * M * REC + GWA_FP6_RECORD_SLACK,
+              "%s: qa6 has %lld readable bytes, [%lld, %lld, %d] records need %lld plus %d of slack", what,
+              (long long)qa6_bytes, (long long)nst, (long long)M, REC, (long long)(nst * M * REC),
+              GWA_FP6_RECORD_SLACK);
+  GWA_REQUIRE(qw6_bytes >= nst * N * REC + GWA_FP6_RECORD_SLACK,
+              "%s: qw6 has %lld readable bytes, [%lld, %lld, %d] records need %lld plus %d of slack", what,
+              (long long)qw6_bytes, (long long)nst, (long long)N, REC, (long long)(nst * N * REC),
+              GWA_FP6_RECORD_SLACK);
   GWA_REQUIRE(GWA_ALIGNED(qa6, 16) && GWA_ALIGNED(qw6, 16) && GWA_ALIGNED(la, 16) && GWA_ALIGNED(up, 16) &&
                   GWA_ALIGNED(out, 8) && GWA_ALIGNED(bias, 2) && GWA_ALIGNED(second, 4) && GWA_ALIGNED(s2, 4),
               "%s: misaligned pointer", what);
@@ -864,17 +880,19 @@ int gemm_fp6(const char* what, const uint8_t* qa6, const uint8_t* qw6, const flo
 
 }  // namespace
 
-extern "C" int gwa_svdq_gemm_w4a4_fp6(const uint8_t* qa6, const uint8_t* qw6, const float* s2, const float* second,
-                                      int64_t second_numel, const void* la, const void* up, int64_t rank,
-                                      const void* bias, void* out, int out_dtype, int epilogue_flags, int64_t M,
-                                      int64_t N, int64_t K, void* stream) {
+extern "C" int gwa_svdq_gemm_w4a4_fp6(const uint8_t* qa6, int64_t qa6_bytes, const uint8_t* qw6,
+                                      int64_t qw6_bytes, const float* s2, const float* second, int64_t second_numel,
+                                      const void* la, const void* up, int64_t rank, const void* bias, void* out,
+                                      int out_dtype, int epilogue_flags, int64_t M, int64_t N, int64_t K,
+                                      void* stream) {
   const NextLayer none{nullptr, nullptr, 0, nullptr, nullptr};
-  return gemm_fp6("svdq_gemm_w4a4_fp6", qa6, qw6, s2, second, second_numel, la, up, rank, bias, out, out_dtype,
-                  epilogue_flags, M, N, K, none, stream);
+  return gemm_fp6("svdq_gemm_w4a4_fp6", qa6, qa6_bytes, qw6, qw6_bytes, s2, second, second_numel, la, up, rank, bias,
+                  out, out_dtype, epilogue_flags, M, N, K, none, stream);
 }
 
-extern "C" int gwa_svdq_gemm_w4a4_fp6_next(const uint8_t* qa6, const uint8_t* qw6, const float* s2,
-                                           const float* second, int64_t second_numel, const void* la, const void* up,
+extern "C" int gwa_svdq_gemm_w4a4_fp6_next(const uint8_t* qa6, int64_t qa6_bytes, const uint8_t* qw6,
+                                           int64_t qw6_bytes, const float* s2, const float* second,
+                                           int64_t second_numel, const void* la, const void* up,
                                            int64_t rank, const void* bias, void* out, int epilogue_flags,
                                            const void* next_smooth, const void* next_proj_down_op, int64_t next_rank,
                                            uint8_t* next_q6, float* next_la_part, int64_t M, int64_t N, int64_t K,
@@ -894,8 +912,8 @@ extern "C" int gwa_svdq_gemm_w4a4_fp6_next(const uint8_t* qa6, const uint8_t* qw
               "%s: next_smooth and next_proj_down_op must be 16-byte, next_q6 8-byte aligned", what);
   const NextLayer nx{(const uint16_t*)next_smooth, (const uint16_t*)next_proj_down_op, (int)(NR / 16), next_q6,
                      next_la_part};
-  return gemm_fp6(what, qa6, qw6, s2, second, second_numel, la, up, rank, bias, out, GWA_DT_BF16, epilogue_flags, M,
-                  N, K, nx, stream);
+  return gemm_fp6(what, qa6, qa6_bytes, qw6, qw6_bytes, s2, second, second_numel, la, up, rank, bias, out,
+                  GWA_DT_BF16, epilogue_flags, M, N, K, nx, stream);
 }
 
 extern "C" int gwa_svdq_gemm_w4a4_fp6_tile(int64_t M, int64_t N) {

@@ -16,7 +16,7 @@
 namespace {
 
 constexpr int64_t kAlign = 256;
-constexpr int64_t kRecordSlack = 1024;  // the GEMM copies records in 1 KB runs and may read this far past them
+constexpr int64_t kRecordSlack = GWA_FP6_RECORD_SLACK;  // the GEMM may read this far past the records
 
 int64_t align_up(int64_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
@@ -34,8 +34,16 @@ Scratch scratch_layout(int64_t M, int64_t K, int64_t R) {
   return s;
 }
 
+// the weight records' readable bytes, checked before anything is enqueued (the GEMM checks them again)
+int check_weight_records(const char* what, const uint8_t* qw6, int64_t qw6_bytes, int64_t N, int64_t K) {
+  GWA_REQUIRE(qw6 != nullptr && qw6_bytes >= (K / 128) * N * GWA_FP6_REC + kRecordSlack,
+              "%s: qw6 has %lld readable bytes, the weight's records need %lld plus %d of slack", what,
+              (long long)qw6_bytes, (long long)((K / 128) * N * GWA_FP6_REC), GWA_FP6_RECORD_SLACK);
+  return GWA_OK;
+}
+
 int linear_fp6_run(const char* what, const void* x, int64_t ldx, const void* smooth, const float* s2,
-                   const void* proj_down_op6, int64_t rank, const uint8_t* qw6, const float* second,
+                   const void* proj_down_op6, int64_t rank, const uint8_t* qw6, int64_t qw6_bytes, const float* second,
                    int64_t second_numel, const void* proj_up, const void* bias, void* out, int out_dtype,
                    int epilogue_flags, int64_t M, int64_t N, int64_t K, uint8_t* ws, int64_t ws_bytes, void* stream) {
   GWA_REQUIRE(M >= 0 && N > 0 && K > 0 && K % 128 == 0, "%s: bad shape M=%lld N=%lld K=%lld (K %% 128 == 0)", what,
@@ -49,6 +57,8 @@ int linear_fp6_run(const char* what, const void* x, int64_t ldx, const void* smo
               (long long)R);
   GWA_REQUIRE(M < (1ll << 31) && K < (1ll << 24), "%s: shape too large", what);
   if (M == 0) return GWA_OK;
+  const int wrc = check_weight_records(what, qw6, qw6_bytes, N, K);  // before kernel 1 is enqueued
+  if (wrc != GWA_OK) return wrc;
   const Scratch s = scratch_layout(M, K, R);
   GWA_REQUIRE(ws != nullptr && ws_bytes >= s.total, "%s: workspace of %lld bytes, this shape needs %lld", what,
               (long long)ws_bytes, (long long)s.total);
@@ -58,8 +68,9 @@ int linear_fp6_run(const char* what, const void* x, int64_t ldx, const void* smo
                                            s.partial_bytes, M, K, stream)
                    : gwa_svdq_quant_fp6(x, ldx, smooth, s2, nullptr, 0, ws, nullptr, M, K, stream);
   if (rc != GWA_OK) return rc;
-  return gwa_svdq_gemm_w4a4_fp6(ws, qw6, s2, second, second_numel, la, R ? proj_up : nullptr, R, bias, out, out_dtype,
-                                epilogue_flags, M, N, K, stream);
+  // the records' region of the workspace holds the slack the GEMM reads past them
+  return gwa_svdq_gemm_w4a4_fp6(ws, s.partials, qw6, qw6_bytes, s2, second, second_numel, la, R ? proj_up : nullptr,
+                                R, bias, out, out_dtype, epilogue_flags, M, N, K, stream);
 }
 
 }  // namespace
@@ -103,7 +114,7 @@ int current_scratch(const char* what, uint8_t** out) {
 
 extern "C" int gwa_svdq_w4a4_linear_fp6_noalloc(const void* x, int64_t ldx, const void* smooth, const float* s2,
                                                 const void* proj_down_op6, int64_t rank, const uint8_t* qw6,
-                                                const float* second, int64_t second_numel, const void* proj_up,
+                                                int64_t qw6_bytes, const float* second, int64_t second_numel, const void* proj_up,
                                                 const void* bias, void* out, int out_dtype, int epilogue_flags,
                                                 int64_t M, int64_t N, int64_t K, void* stream) {
   const char* what = "svdq_w4a4_linear_fp6_noalloc";
@@ -113,12 +124,16 @@ extern "C" int gwa_svdq_w4a4_linear_fp6_noalloc(const void* x, int64_t ldx, cons
               "(use gwa_svdq_w4a4_linear_fp6 with a workspace, or split the rows)",
               what, (long long)M, (long long)K, (long long)rank, (long long)need, (long long)kScratchBytes);
   uint8_t* ws = nullptr;
+  if (M > 0 && N > 0 && K > 0 && K % 128 == 0) {
+    const int wrc = check_weight_records(what, qw6, qw6_bytes, N, K);  // before the scratch lookup's HIP calls
+    if (wrc != GWA_OK) return wrc;
+  }
   if (M > 0) {
     const int rc = current_scratch(what, &ws);
     if (rc != GWA_OK) return rc;
   }
-  return linear_fp6_run(what, x, ldx, smooth, s2, proj_down_op6, rank, qw6, second, second_numel, proj_up, bias, out,
-                        out_dtype, epilogue_flags, M, N, K, ws, kScratchBytes, stream);
+  return linear_fp6_run(what, x, ldx, smooth, s2, proj_down_op6, rank, qw6, qw6_bytes, second, second_numel, proj_up,
+                        bias, out, out_dtype, epilogue_flags, M, N, K, ws, kScratchBytes, stream);
 }
 
 extern "C" int64_t gwa_svdq_w4a4_linear_fp6_noalloc_scratch_bytes(void) { return kScratchBytes; }
@@ -131,11 +146,11 @@ extern "C" int64_t gwa_svdq_w4a4_linear_fp6_workspace(int64_t M, int64_t K, int6
 
 extern "C" int gwa_svdq_w4a4_linear_fp6(const void* x, int64_t ldx, const void* smooth, const float* s2,
                                         const void* proj_down_op6, int64_t rank, const uint8_t* qw6,
-                                        const float* second, int64_t second_numel, const void* proj_up,
+                                        int64_t qw6_bytes, const float* second, int64_t second_numel, const void* proj_up,
                                         const void* bias, void* out, int out_dtype, int epilogue_flags, int64_t M,
                                         int64_t N, int64_t K, void* workspace, int64_t workspace_bytes,
                                         void* stream) {
-  return linear_fp6_run("svdq_w4a4_linear_fp6", x, ldx, smooth, s2, proj_down_op6, rank, qw6, second,
+  return linear_fp6_run("svdq_w4a4_linear_fp6", x, ldx, smooth, s2, proj_down_op6, rank, qw6, qw6_bytes, second,
                         second_numel, proj_up, bias, out, out_dtype, epilogue_flags, M, N, K, (uint8_t*)workspace,
                         workspace_bytes, stream);
 }

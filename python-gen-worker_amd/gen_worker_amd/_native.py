@@ -52,20 +52,20 @@ _SIGNATURES: dict[str, tuple] = {
                            _i64, _i64, _i64, _vp),
     "gwa_svdq_group_psums": (_vp, _vp, _vp, _i64, _i64, _i64, _vp),
     "gwa_svdq_pack_weight_fp6": (_vp, _vp, _vp, _i64, _i64, _vp),
-    "gwa_svdq_gemm_w4a4_fp6": (_vp, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _int, _int,
+    "gwa_svdq_gemm_w4a4_fp6": (_vp, _i64, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _int, _int,
                                _i64, _i64, _i64, _vp),
-    "gwa_svdq_group_psums_fp6": (_vp, _vp, _vp, _i64, _i64, _i64, _vp),
-    "gwa_svdq_w4a4_linear_fp6": (_vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _int, _int,
+    "gwa_svdq_group_psums_fp6": (_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _vp),
+    "gwa_svdq_w4a4_linear_fp6": (_vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _int, _int,
                                  _i64, _i64, _i64, _vp, _i64, _vp),
     "gwa_svdq_w4a4_linear_fp6_workspace": (_i64, _i64, _i64),
-    "gwa_svdq_w4a4_linear_fp6_noalloc": (_vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _int,
-                                         _int, _i64, _i64, _i64, _vp),
+    "gwa_svdq_w4a4_linear_fp6_noalloc": (_vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp,
+                                         _int, _int, _i64, _i64, _i64, _vp),
     "gwa_svdq_w4a4_linear_fp6_noalloc_scratch_bytes": (),
     "gwa_svdq_w4a4_linear_gemv": (_vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _int, _int,
                                   _i64, _i64, _i64, _vp, _i64, _vp),
     "gwa_svdq_w4a4_gemv_max_m": (_i64, _i64),
     "gwa_svdq_w4a4_linear_gemv_workspace": (_i64, _i64, _i64),
-    "gwa_svdq_gemm_w4a4_fp6_next": (_vp, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _int,
+    "gwa_svdq_gemm_w4a4_fp6_next": (_vp, _i64, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _int,
                                     _vp, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _vp),
     "gwa_svdq_quant_fp6": (_vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _i64, _vp),
     "gwa_svdq_prep_proj_down_fp6": (_vp, _vp, _i64, _i64, _vp),

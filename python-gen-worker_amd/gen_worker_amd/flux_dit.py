@@ -23,11 +23,13 @@ Every linear is built by a factory, so the same model runs as:
     bf16 Linear, as the reference's swap does;
   * ``"bf16"``: every linear a bf16 ``nn.Linear`` (the bf16 GEMM path).
 Both models share the rest of the block: the fused glue kernels below (q/k
-RMSNorm + rotary, adaLN modulation, gated residual) and the attention kernel
-(``attention``: bf16 flash attention, the role of diffusers' SDPA call; the
-torch statement ``_sdpa`` is kept for the tests). Weights are random-init on
-the device from seeded generators; values are chosen only to keep activations
-finite and O(1) through the 57 blocks.
+RMSNorm + rotary, adaLN modulation, gated residual) and the attention, chosen
+per model: ``attention="sdpa"`` (the default) is diffusers' call, torch's bf16
+scaled_dot_product_attention restricted to its flash / memory-efficient
+kernels; ``attention="flash"`` is this package's bf16 flash-attention kernel
+(``gwa_dit_attention``). Weights are random-init on the device from seeded
+generators; values are chosen only to keep activations finite and O(1)
+through the 57 blocks.
 """
 
 from __future__ import annotations
@@ -241,11 +243,22 @@ def qk_norm_rope(q: Tensor, k: Tensor, wq: Tensor, wk: Tensor, cos: Tensor, sin:
 
 
 def _sdpa(q: Tensor, k: Tensor, v: Tensor) -> Tensor:
-    """torch's statement of the block attention: [S, H, D] bf16 -> [S, H*D] via SDPA on [1, H, S, D]."""
+    """torch's statement of the block attention: [S, H, D] bf16 -> [S, H*D] via SDPA on [1, H, S, D] (any
+    backend torch picks)."""
     s, h, d = q.shape
     o = F.scaled_dot_product_attention(q.transpose(0, 1).unsqueeze(0), k.transpose(0, 1).unsqueeze(0),
                                        v.transpose(0, 1).unsqueeze(0))
     return o.squeeze(0).transpose(0, 1).reshape(s, h * d)
+
+
+def sdpa_attention(q: Tensor, k: Tensor, v: Tensor) -> Tensor:
+    """The block attention as diffusers calls it (``F.scaled_dot_product_attention`` on [1, H, S, D] bf16),
+    restricted to torch's flash and memory-efficient kernels: the math fallback (batched bf16 products on
+    transposed views) is never taken; a shape those kernels refuse raises instead."""
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+        return _sdpa(q, k, v)
 
 
 def attention(q: Tensor, k: Tensor, v: Tensor) -> Tensor:
@@ -268,7 +281,7 @@ def attention(q: Tensor, k: Tensor, v: Tensor) -> Tensor:
     return out
 
 
-_attention = attention
+ATTENTION = {"sdpa": sdpa_attention, "flash": attention}
 
 
 def _mlp(fc1: nn.Module, fc2: nn.Module, x: Tensor, fused: bool) -> Tensor:
@@ -303,6 +316,7 @@ class DualBlock(nn.Module):
         self.fc1_img, self.fc1_txt = make(c, cfg.mlp, seed + 6, gelu=True), make(c, cfg.mlp, seed + 7, gelu=True)
         self.fc2_img, self.fc2_txt = make(cfg.mlp, c, seed + 8), make(cfg.mlp, c, seed + 9)
         self.side: Optional[torch.cuda.Stream] = None  # set by FluxDiT(..., streams=2)
+        self.attn: Callable[[Tensor, Tensor, Tensor], Tensor] = sdpa_attention  # set by FluxDiT(..., attention=)
         self.pre_mod = None  # modulation outputs computed ahead on another stream, and their event
         ones = torch.ones(cfg.head_dim, device=device, dtype=torch.bfloat16)
         self.register_buffer("qn_img", ones.clone())
@@ -327,7 +341,7 @@ class DualBlock(nn.Module):
                                   (qkv_i, self.qn_img, self.kn_img, slice(st, None))):
             qk_norm_rope(src[:, :c], src[:, c:2 * c], qn, kn, cos, sin, rows.start, q[rows], k[rows],
                          v=src[:, 2 * c:], out_v=v[rows])
-        a = _attention(q, k, v)
+        a = self.attn(q, k, v)
         at, ai = a[:st], a[st:]
         img = gate_residual(img, self.o_img(ai.contiguous()), g1)
         txt = gate_residual(txt, self.o_txt(at.contiguous()), tg1)
@@ -369,9 +383,9 @@ class DualBlock(nn.Module):
         # image queries' last round leaves idle), the image queries' here; each query's result is the same
         main.wait_stream(side)
         side.wait_stream(main)
-        ai = _attention(q[st:], k, v)
+        ai = self.attn(q[st:], k, v)
         with torch.cuda.stream(side):
-            at = _attention(q[:st], k, v)
+            at = self.attn(q[:st], k, v)
             t2 = gate_residual(txt, self.o_txt(at), tg1)
             t2 = gate_residual(t2, _mlp(self.fc1_txt, self.fc2_txt, adaln_modulate(t2, tsc2, tsh2), self.fused),
                                tg2)
@@ -394,6 +408,7 @@ class SingleBlock(nn.Module):
         self.mlp = make(c, cfg.mlp, seed + 2, gelu=True)
         self.proj_out = make(c + cfg.mlp, c, seed + 3)
         self.side: Optional[torch.cuda.Stream] = None  # set by FluxDiT(..., streams=2)
+        self.attn: Callable[[Tensor, Tensor, Tensor], Tensor] = sdpa_attention  # set by FluxDiT(..., attention=)
         self.pre_mod = None
         ones = torch.ones(cfg.head_dim, device=device, dtype=torch.bfloat16)
         self.register_buffer("qn", ones.clone())
@@ -424,7 +439,7 @@ class SingleBlock(nn.Module):
         qkv = self.qkv(n)
         q, k = (torch.empty(x.shape[0], cfg.heads, cfg.head_dim, device=x.device, dtype=x.dtype) for _ in range(2))
         qk_norm_rope(qkv[:, :c], qkv[:, c:2 * c], self.qn, self.kn, cos, sin, 0, q, k)
-        a = _attention(q, k, qkv[:, 2 * c:].reshape(-1, cfg.heads, cfg.head_dim))
+        a = self.attn(q, k, qkv[:, 2 * c:].reshape(-1, cfg.heads, cfg.head_dim))
         if side is not None:
             if self.fused:
                 return gate_residual(x, cc.finish(a, before_reduce=lambda: main.wait_stream(side)), g)
@@ -438,11 +453,16 @@ class SingleBlock(nn.Module):
 
 
 class FluxDiT(nn.Module):
-    """The config-4 denoiser; ``forward(latents [4096, 64], text [512, 4096], temb [1, 3072]) -> [4096, 64]``."""
+    """The config-4 denoiser; ``forward(latents [4096, 64], text [512, 4096], temb [1, 3072]) -> [4096, 64]``.
+    ``attention``: ``"sdpa"`` (torch's SDPA, as config 4 states) or ``"flash"`` (``gwa_dit_attention``)."""
 
     def __init__(self, kind: str, cfg: FluxDiTConfig = FluxDiTConfig(), device="cuda", seed: int = 1000,
-                 lane: Optional[str] = None, modulation: str = "w4a4", streams: int = 1) -> None:
+                 lane: Optional[str] = None, modulation: str = "w4a4", streams: int = 1,
+                 attention: str = "sdpa") -> None:
         super().__init__()
+        if attention not in ATTENTION:
+            raise ValueError(f"attention must be one of {sorted(ATTENTION)}, got {attention!r}")
+        self.attention = attention
         if kind == "w4a4":
             from .qualify import resolve_lane
 
@@ -460,6 +480,8 @@ class FluxDiT(nn.Module):
                                   for i in range(cfg.n_dual))
         self.single = nn.ModuleList(SingleBlock(cfg, make, seed + 400 + 10 * i, device, fused, make_mod)
                                     for i in range(cfg.n_single))
+        for blk in list(self.dual) + list(self.single):
+            blk.attn = ATTENTION[attention]
         self.mod_stream: Optional[torch.cuda.Stream] = None
         if streams == 2:  # a second HIP stream (default priority): the dual blocks' text stream, the single
             side = torch.cuda.Stream(device=device)  # blocks' MLP branch
@@ -566,5 +588,5 @@ def time_step_ms(model: nn.Module, args: tuple[Tensor, ...], steps: int = 5, war
         return e0.elapsed_time(e1) / steps
 
 
-__all__ = ["FluxDiT", "FluxDiTConfig", "adaln_modulate", "block_int_ops", "gate_residual", "inputs",
-           "linear_factory", "qk_norm_rope", "time_step_ms"]
+__all__ = ["ATTENTION", "FluxDiT", "FluxDiTConfig", "adaln_modulate", "attention", "block_int_ops", "gate_residual",
+           "inputs", "linear_factory", "qk_norm_rope", "sdpa_attention", "time_step_ms"]

@@ -180,6 +180,24 @@ class _ShardReader:
                 if f"{layer}{s}" in self.where}
 
 
+def _layer_bias(layer: str, target: str, tensors: Dict[str, Tensor], old: Any) -> Optional[Tensor]:
+    """The layer's bias: the checkpoint's ``L.bias`` when the module has a bias, else the module's own when it
+    is materialized. A checkpoint bias on a module without one, or a module bias that neither provides, raises
+    (the reference builds the module with ``bias=old.bias is not None`` and its ``load_state_dict`` reports
+    both as unexpected / missing keys, ``models/w4a4.py:488-493``)."""
+    ckpt = tensors.get(f"{layer}.bias")
+    mod_bias = getattr(old, "bias", None)
+    if mod_bias is None:
+        if ckpt is not None:
+            raise Nvfp4CheckpointError(f"checkpoint has {layer}.bias but module {target!r} has no bias")
+        return None
+    if ckpt is not None:
+        return ckpt
+    if mod_bias.is_meta:
+        raise Nvfp4CheckpointError(f"module {target!r} has a bias the checkpoint does not provide")
+    return mod_bias.detach()
+
+
 def _check_lane(lane: str) -> str:
     if lane not in LANES:
         raise ValueError(f"lane {lane!r} is not one of {LANES}")
@@ -191,7 +209,8 @@ def swap_nvfp4_linears(model: nn.Module, art: Nvfp4Artifact, *, key_map: Optiona
                        compute_dtype: torch.dtype = torch.bfloat16) -> dict:
     """Swap the artifact's quantized layers in an already-built ``model`` (``swap_w4a4_linears``): each plain,
     aligned ``nn.Linear`` becomes an ``Nvfp4Linear``; any other keeps its module with the dequantized weight
-    assigned. The bias is the checkpoint's ``L.bias`` when it has one, else the module's. ``key_map`` maps an
+    assigned. The bias is the checkpoint's ``L.bias`` when it has one, else the module's (``_layer_bias``: a
+    bias only one side has raises). ``key_map`` maps an
     artifact layer name to the model's module path. Returns {"quantized", "swapped", "dequantized":
     {reason: count}}; a shape mismatch raises."""
     _check_lane(lane)
@@ -208,9 +227,7 @@ def swap_nvfp4_linears(model: nn.Module, art: Nvfp4Artifact, *, key_map: Optiona
             raise Nvfp4CheckpointError(f"layer {layer!r} is [{out_f}, {in_f}] in the checkpoint, module {target!r} "
                                        f"is {list(mod_shape)}")
         why = _swap_reason(old, out_f, in_f, lane)
-        bias = tensors.get(f"{layer}.bias")
-        if bias is None and getattr(old, "bias", None) is not None and not old.bias.is_meta:
-            bias = old.bias.detach()
+        bias = _layer_bias(layer, target, tensors, old)
         if why is None:
             new = build_nvfp4_linear(w, tensors[f"{layer}.weight_scale"], tensors[f"{layer}.weight_scale_2"],
                                      bias=bias, input_scale=tensors.get(f"{layer}.input_scale"),
@@ -220,9 +237,7 @@ def swap_nvfp4_linears(model: nn.Module, art: Nvfp4Artifact, *, key_map: Optiona
         else:
             dense = _dense_weight(tensors, layer, compute_dtype).to(device)
             old.weight = nn.Parameter(dense, requires_grad=False)
-            if getattr(old, "bias", None) is not None:
-                if bias is None:
-                    raise Nvfp4CheckpointError(f"module {target!r} has a bias the checkpoint does not provide")
+            if bias is not None:
                 old.bias = nn.Parameter(bias.to(device=device, dtype=compute_dtype), requires_grad=False)
             counts["dequantized"][why] = counts["dequantized"].get(why, 0) + 1
     partial = {k: v for k, v in counts["dequantized"].items() if k != "dense_lane"}

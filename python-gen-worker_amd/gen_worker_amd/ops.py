@@ -211,6 +211,12 @@ def record_slack_bytes(rec: Tensor) -> int:
     return rec.untyped_storage().nbytes() - end
 
 
+def readable_bytes(t: Tensor) -> int:
+    """Bytes of ``t``'s storage from its first element to the storage's end: the byte count the C-ABI's record
+    entry points take beside each record pointer (they check the records plus the slack against it)."""
+    return t.untyped_storage().nbytes() - t.storage_offset() * t.element_size()
+
+
 def _check_record_slack(name: str, rec: Tensor, what: str) -> None:
     """The fp6 GEMM copies operand records in 1 KB runs with unchecked scalar offsets: the run holding a tile's
     last real row may read up to RECORD_SLACK bytes past the last record, so a record tensor handed to it must own
@@ -473,8 +479,8 @@ def _fp6_impl(qa6: Tensor, weight_fp6: Tensor, s2: Optional[Tensor], second: Opt
     _check_record_slack(name, weight_fp6, "weight_fp6")
     rank, sec_n = _epilogue_operands(name, m, n, la, up, bias, second)
     out = torch.empty(m, n, dtype=out_dtype, device=qa6.device)
-    nat.call("gwa_svdq_gemm_w4a4_fp6", nat.ptr(qa6), nat.ptr(weight_fp6), nat.ptr(s2), nat.ptr(second),
-             sec_n, nat.ptr(la), nat.ptr(up), rank, nat.ptr(bias), nat.ptr(out), _dt_code(out_dtype),
+    nat.call("gwa_svdq_gemm_w4a4_fp6", nat.ptr(qa6), readable_bytes(qa6), nat.ptr(weight_fp6),
+             readable_bytes(weight_fp6), nat.ptr(s2), nat.ptr(second), sec_n, nat.ptr(la), nat.ptr(up), rank, nat.ptr(bias), nat.ptr(out), _dt_code(out_dtype),
              _epi_flags(gelu, la), m, n, k, nat.stream_of(qa6))
     return out
 
@@ -547,7 +553,7 @@ def svdq_forward_fp6(x2: Tensor, smooth: Optional[Tensor], s2: Optional[Tensor],
         return out
     ws = torch.empty(linear_fp6_workspace_bytes(m, k, rank), dtype=torch.uint8, device=x2.device)
     nat.call("gwa_svdq_w4a4_linear_fp6", nat.ptr(x2), int(x2.stride(0)), nat.ptr(smooth), nat.ptr(s2),
-             nat.ptr(proj_down_op6), rank, nat.ptr(weight_fp6), nat.ptr(second),
+             nat.ptr(proj_down_op6), rank, nat.ptr(weight_fp6), readable_bytes(weight_fp6), nat.ptr(second),
              0 if second is None else int(second.numel()), nat.ptr(proj_up), nat.ptr(bias), nat.ptr(out),
              _dt_code(out_dtype), nat.EPI_GELU_TANH if gelu else 0, m, n, k, nat.ptr(ws), int(ws.numel()),
              nat.stream_of(x2))
@@ -682,8 +688,8 @@ def svdq_w4a4_linear_fp6_next(qa6: Tensor, weight_fp6: Tensor, s2: Optional[Tens
     q6_addr = _next_records(name, next_q6, m, n, stage_offset)
     nrank = _la_part_check(name, next_la_part, next_proj_down_op, m, n, la_partials_next(m, n))
     out = torch.empty(m, n if write_out else 0, dtype=torch.bfloat16, device=qa6.device)
-    nat.call("gwa_svdq_gemm_w4a4_fp6_next", nat.ptr(qa6), nat.ptr(weight_fp6), nat.ptr(s2), nat.ptr(second),
-             sec_n, nat.ptr(la), nat.ptr(up), rank, nat.ptr(bias), nat.ptr(out) if write_out else None,
+    nat.call("gwa_svdq_gemm_w4a4_fp6_next", nat.ptr(qa6), readable_bytes(qa6), nat.ptr(weight_fp6),
+             readable_bytes(weight_fp6), nat.ptr(s2), nat.ptr(second), sec_n, nat.ptr(la), nat.ptr(up), rank, nat.ptr(bias), nat.ptr(out) if write_out else None,
              _epi_flags(gelu, la), nat.ptr(next_smooth), nat.ptr(next_proj_down_op), nrank, q6_addr,
              nat.ptr(next_la_part), m, n, k, nat.stream_of(qa6))
     return out
@@ -747,8 +753,9 @@ def svdq_group_psums_fp6(qa6: Tensor, weight_fp6: Tensor) -> Tensor:
     if kw != k:
         raise SvdqOpError(f"{name}: activation K={k} and weight K={kw} differ")
     out = torch.empty(m, n, k // GROUP, dtype=torch.int32, device=qa6.device)
-    nat.call("gwa_svdq_group_psums_fp6", nat.ptr(qa6.contiguous()), nat.ptr(weight_fp6.contiguous()), nat.ptr(out),
-             m, n, k, nat.stream_of(qa6))
+    qa6, weight_fp6 = qa6.contiguous(), weight_fp6.contiguous()
+    nat.call("gwa_svdq_group_psums_fp6", nat.ptr(qa6), readable_bytes(qa6), nat.ptr(weight_fp6),
+             readable_bytes(weight_fp6), nat.ptr(out), m, n, k, nat.stream_of(qa6))
     return out
 
 

@@ -18,6 +18,13 @@ and degrades to a dequantized lane when one fails:
   after 3 warmups at M = N = K = 4096, at least 1.10x faster than the bf16
   matmul (each timed call here a graph replay of 10 back-to-back calls).
 * ``w4a4_gemm_mode`` (``models/w4a4.py:262-286``): the lane, chosen once.
+* ``w8a8_gemm_mode`` (``models/w8a8.py:137-247``): the W8A8 GEMM branch,
+  "rowwise" then "pertensor", each armed only by a probe and the same 1.10x
+  bar at 4096^3, else "" and the dequant lane; chosen once.
+
+Timing protocol: the gates decide on graph replays of back-to-back calls
+(``_median_ms``); the reference times single eager calls, and that ratio is
+recorded beside the decision (``_median_ms_eager``).
 
 Here the lanes are ``"int4"`` (the HIP kernels: ``SvdqW4A4Linear``) and
 ``"dense"`` (``fold_to_dense``: one bf16 ``nn.Linear`` per layer on the same
@@ -221,14 +228,36 @@ def gemm_numerics_ok() -> Optional[str]:
     return None
 
 
+def _median_ms_eager(fn: Any) -> float:
+    """The reference's protocol as written (``models/w4a4.py:216-232``): median ms of ``BENCH_ITERS`` single
+    eager calls, each bracketed by two events and a synchronize, after ``BENCH_WARMUP`` untimed calls. The
+    events also bracket the op's host dispatch (Python custom op + ctypes for the int4 side, torch's C++
+    dispatch for the matmul) and the clock's climb out of each idle gap."""
+    for _ in range(BENCH_WARMUP):
+        fn()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(BENCH_ITERS):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        fn()
+        e1.record()
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1))
+    times.sort()
+    return times[len(times) // 2]
+
+
 def _median_ms(fn: Any) -> float:
-    """Median ms of ``BENCH_ITERS`` timed calls after ``BENCH_WARMUP`` untimed ones (``models/w4a4.py:216-232``).
-    Each timed call is one replay of a HIP graph holding ``BENCH_CALLS_PER_REPLAY`` back-to-back calls of
-    ``fn``, divided by that count, so the events bracket the op's GPU work only: the int4 op's host side
-    (Python custom op + ctypes, ~20-30 us) and torch's C++ matmul dispatch would otherwise enter the two sides
-    unequally, and a lone ~0.07-0.1 ms kernel per replay also carries the replay's launch latency and the
+    """The protocol the gates decide on: median ms of ``BENCH_ITERS`` timed calls after ``BENCH_WARMUP``
+    untimed ones, each timed call one replay of a HIP graph holding ``BENCH_CALLS_PER_REPLAY`` back-to-back
+    calls of ``fn``, divided by that count, so the events bracket the op's GPU work only: the int4 op's host
+    side (Python custom op + ctypes, ~20-30 us) and torch's C++ matmul dispatch would otherwise enter the two
+    sides unequally, and a lone ~0.07-0.1 ms kernel per replay also carries the replay's launch latency and the
     clock's climb out of the idle gap before it (measured: 0.092 / 0.099 ms for one call per replay against
-    0.072 / 0.09 ms back to back, which pulled the ratio to the 1.10x line)."""
+    0.072 / 0.09 ms back to back, which pulled the ratio to the 1.10x line). This assumes the serving loop
+    queues its launches (graphs or back-to-back eager calls); ``_median_ms_eager`` is the reference's
+    single-call protocol, recorded beside it."""
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
@@ -255,10 +284,12 @@ def _median_ms(fn: Any) -> float:
     return times[len(times) // 2]
 
 
-def gemm_speedup() -> tuple[float, float, float]:
+def gemm_speedup(protocol: str = "graph") -> tuple[float, float, float]:
     """``_gemm_profitable`` (``models/w4a4.py:235-259``): (int4 GEMM ms, bf16 matmul ms, speedup) at
     M = N = K = 4096; the int4 side is the fp6-lane GEMM with its epilogue on ready activation records, as the
-    reference times its fp4 GEMM on ready operands."""
+    reference times its fp4 GEMM on ready operands. ``protocol``: "graph" (``_median_ms``, the decision) or
+    "eager" (``_median_ms_eager``, the reference's single calls)."""
+    timer = {"graph": _median_ms, "eager": _median_ms_eager}[protocol]
     ops = torch.ops.cozy_gen_worker
     d = BENCH_DIM
     g = torch.Generator(device="cuda").manual_seed(3)
@@ -268,9 +299,8 @@ def gemm_speedup() -> tuple[float, float, float]:
     sw = torch.ones(d, d // GROUP, device="cuda", dtype=torch.float16)
     w6 = ops.svdq_pack_weight_fp6(qw, sw)
     q6, _ = ops.svdq_quant_fp6(x, None, None, None)
-    int4_ms = _median_ms(lambda: ops.svdq_w4a4_linear_fp6(q6, w6, None, None, None, None, None, torch.bfloat16,
-                                                         False))
-    bf16_ms = _median_ms(lambda: x @ w.t())
+    int4_ms = timer(lambda: ops.svdq_w4a4_linear_fp6(q6, w6, None, None, None, None, None, torch.bfloat16, False))
+    bf16_ms = timer(lambda: x @ w.t())
     return int4_ms, bf16_ms, bf16_ms / max(int4_ms, 1e-9)
 
 
@@ -278,9 +308,13 @@ def gemm_speedup() -> tuple[float, float, float]:
 class Qualification:
     lane: str                       # "int4", "dense" or "unavailable"
     reasons: list[str] = field(default_factory=list)
-    int4_ms: Optional[float] = None
+    int4_ms: Optional[float] = None     # the decision's protocol: graph replays of back-to-back calls
     bf16_ms: Optional[float] = None
     speedup: Optional[float] = None
+    # the reference's protocol (single eager calls), recorded beside the decision, not deciding it
+    int4_ms_eager: Optional[float] = None
+    bf16_ms_eager: Optional[float] = None
+    speedup_eager: Optional[float] = None
 
 
 def qualify() -> Qualification:
@@ -293,18 +327,20 @@ def qualify() -> Qualification:
             why = gate()
             if why is not None:
                 reasons.append(why)
-        int4_ms, bf16_ms, speedup = gemm_speedup()
+        int4_ms, bf16_ms, speedup = gemm_speedup("graph")
+        int4_e, bf16_e, speedup_e = gemm_speedup("eager")
         if speedup < BENCH_MIN_SPEEDUP:
             reasons.append(f"int4 GEMM {int4_ms:.3f} ms vs bf16 {bf16_ms:.3f} ms: speedup {speedup:.2f}x "
                            f"< {BENCH_MIN_SPEEDUP:.2f}x")
     except Exception as exc:  # noqa: BLE001 — a failing probe degrades the lane, as in the reference
         return Qualification("dense", [f"qualification raised {exc!r}"])
-    q = Qualification("int4" if not reasons else "dense", reasons, int4_ms, bf16_ms, speedup)
+    q = Qualification("int4" if not reasons else "dense", reasons, int4_ms, bf16_ms, speedup, int4_e, bf16_e,
+                      speedup_e)
     if reasons:
         logger.warning("gen_worker_amd: int4 lane not armed (%s); dense lane", "; ".join(reasons))
     else:
-        logger.info("gen_worker_amd: int4 lane armed (GEMM %.3f ms vs bf16 %.3f ms, %.2fx)", int4_ms, bf16_ms,
-                    speedup)
+        logger.info("gen_worker_amd: int4 lane armed (GEMM %.3f ms vs bf16 %.3f ms, %.2fx; single eager calls "
+                    "%.3f vs %.3f ms, %.2fx)", int4_ms, bf16_ms, speedup, int4_e, bf16_e, speedup_e)
     return q
 
 
@@ -346,9 +382,123 @@ def serving_linear(mod: Any, lane: Optional[str] = None) -> Any:
     return dense
 
 
+# ---------------------------------------------------------------------------
+# W8A8: the GEMM branch, chosen once per process (models/w8a8.py:137-256)
+# ---------------------------------------------------------------------------
+
+W8A8_MODES = ("rowwise", "pertensor")     # candidate order of the reference on its newest parts (:210-211)
+W8A8_PROBE = (128, 256, 128)              # (m, k, n): the int8 kernel's contract (K % 64, N % 16)
+
+
+def w8a8_probe(mode: str) -> Optional[str]:
+    """``_gemm_call_ok`` (``models/w8a8.py:146-159``), with the numerics the int4 gate holds its GEMM to: the
+    int8 GEMM in ``mode`` (per-token activation scales, or one per tensor) on the quantizer's codes, within
+    relative Frobenius error 2e-2 of the dequantize-then-matmul product. None when it runs and agrees."""
+    if mode not in W8A8_MODES:
+        raise ValueError(f"W8A8 mode {mode!r} is not one of {W8A8_MODES}")
+    ops = torch.ops.cozy_gen_worker
+    m, k, n = W8A8_PROBE
+    g = torch.Generator(device="cuda").manual_seed(4)
+    x = torch.randn(m, k, generator=g, device="cuda").to(torch.bfloat16)
+    w = torch.randn(n, k, generator=g, device="cuda") * 0.02
+    sw = (w.abs().amax(dim=1) / 127.0).clamp(min=1e-12)
+    qw = (w / sw[:, None]).round().clamp(-127, 127).to(torch.int8)
+    bias = (torch.randn(n, generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    qa, sa = ops.w8a8_quant(x, mode == "pertensor", None)
+    if (sa.numel() == 1) != (mode == "pertensor"):
+        return f"w8a8 {mode}: activation scale has {sa.numel()} values"
+    y = ops.w8a8_scaled_mm(qa, qw, sa, sw, bias, torch.bfloat16)
+    ref = (qa.float() * sa.float().reshape(-1, 1)) @ (qw.float() * sw[:, None]).t() + bias.float()
+    rel = _rel(y, ref)
+    if not rel < GEMM_REL_TOL:
+        return f"w8a8 {mode}: rel err {rel:.4f} at {m}x{k}x{n}"
+    return None
+
+
+def w8a8_gemm_speedup(mode: str, protocol: str = "graph") -> tuple[float, float, float]:
+    """``_bench_gemm_pair`` / ``_gemm_profitable`` (``models/w8a8.py:183-216``): (int8 GEMM ms, bf16 matmul ms,
+    speedup) at M = N = K = 4096 on ready int8 operands; the per-tensor branch with one activation scale (its
+    per-channel weight scale rides in the same epilogue, where the reference adds a bf16 multiply)."""
+    timer = {"graph": _median_ms, "eager": _median_ms_eager}[protocol]
+    ops = torch.ops.cozy_gen_worker
+    d = BENCH_DIM
+    g = torch.Generator(device="cuda").manual_seed(5)
+    x = torch.randn(d, d, generator=g, device="cuda").to(torch.bfloat16)
+    w = torch.randn(d, d, generator=g, device="cuda").to(torch.bfloat16)
+    qa = torch.randint(-127, 128, (d, d), generator=g, device="cuda", dtype=torch.int8)
+    qw = torch.randint(-127, 128, (d, d), generator=g, device="cuda", dtype=torch.int8)
+    sa = torch.full((d if mode == "rowwise" else 1,), 1e-3, device="cuda")
+    sw = torch.full((d,), 1e-2, device="cuda")
+    int8_ms = timer(lambda: ops.w8a8_scaled_mm(qa, qw, sa, sw, None, torch.bfloat16))
+    bf16_ms = timer(lambda: x @ w.t())
+    return int8_ms, bf16_ms, bf16_ms / max(int8_ms, 1e-9)
+
+
+@dataclass
+class W8a8Qualification:
+    mode: str                       # "rowwise", "pertensor", or "" (the dequant lane)
+    reasons: list[str] = field(default_factory=list)
+    timings: dict = field(default_factory=dict)   # mode -> {"graph": (int8, bf16, x), "eager": (...)}
+
+
+def qualify_w8a8() -> W8a8Qualification:
+    """Try each branch in order (``_choose_gemm_mode``, ``models/w8a8.py:210-232``): the first whose probe
+    passes and whose GEMM beats bf16 by ``BENCH_MIN_SPEEDUP`` at 4096^3 is the process's mode; none: "" (the
+    dequant lane, logged as a degrade). Without the library or a GPU: ""."""
+    if not extension_available():
+        return W8a8Qualification("", ["the HIP library or a GPU is missing (no CPU path for the int8 GEMM)"])
+    reasons: list[str] = []
+    timings: dict = {}
+    for mode in W8A8_MODES:
+        try:
+            why = w8a8_probe(mode)
+            if why is not None:
+                reasons.append(why)
+                continue
+            graph = w8a8_gemm_speedup(mode, "graph")
+            timings[mode] = {"graph": graph, "eager": w8a8_gemm_speedup(mode, "eager")}
+            if graph[2] >= BENCH_MIN_SPEEDUP:
+                logger.info("gen_worker_amd: W8A8 %s branch armed (int8 %.3f ms vs bf16 %.3f ms, %.2fx)", mode,
+                            *graph)
+                return W8a8Qualification(mode, reasons, timings)
+            reasons.append(f"w8a8 {mode}: int8 GEMM {graph[0]:.3f} ms vs bf16 {graph[1]:.3f} ms: speedup "
+                           f"{graph[2]:.2f}x < {BENCH_MIN_SPEEDUP:.2f}x")
+        except Exception as exc:  # noqa: BLE001 — a failing probe or bench moves to the next branch
+            reasons.append(f"w8a8 {mode} raised {exc!r}")
+    logger.warning("gen_worker_amd: no W8A8 GEMM branch qualified (%s); dequant lane", "; ".join(reasons))
+    return W8a8Qualification("", reasons, timings)
+
+
+@functools.lru_cache(maxsize=1)
+def w8a8_qualification() -> W8a8Qualification:
+    """The once-per-process result (``w8a8_gemm_mode``, ``models/w8a8.py:235-247``)."""
+    return qualify_w8a8()
+
+
+def w8a8_gemm_mode() -> str:
+    """"rowwise", "pertensor", or "" for the dequant lane."""
+    return w8a8_qualification().mode
+
+
+W8A8_LANES = W8A8_MODES + ("dequant",)
+
+
+def resolve_w8a8_mode(mode: Optional[str] = None) -> str:
+    """``mode`` when given ("rowwise", "pertensor" or "dequant"), else the process's qualified branch, with ""
+    resolved to "dequant" (the reference serves the dequantized weight and never refuses,
+    ``models/w8a8.py:465-466``)."""
+    if mode is None:
+        return w8a8_gemm_mode() or "dequant"
+    if mode not in W8A8_LANES:
+        raise ValueError(f"W8A8 mode {mode!r} is not one of {W8A8_LANES}")
+    return mode
+
+
 __all__ = [
     "EPILOGUE_REL_TOL", "GEMM_REL_TOL", "IDENTITY_PROBES", "Qualification", "SELF_CHECK_PROBES",
     "decode_fp6_records_torch", "extension_available", "fused_self_check", "gemm_numerics_ok", "gemm_speedup",
     "LANES", "pack_int4_torch", "qualification", "qualify", "quantize_act_torch", "quantizer_bit_identical",
     "resolve_lane", "serving_linear", "w4a4_lane",
+    "W8A8_LANES", "W8A8_MODES", "W8a8Qualification", "qualify_w8a8", "resolve_w8a8_mode", "w8a8_gemm_mode",
+    "w8a8_gemm_speedup", "w8a8_probe", "w8a8_qualification",
 ]

@@ -29,7 +29,8 @@ logger = logging.getLogger(__name__)
 
 SVDQ_METHOD = "svdquant"
 DENOISER_DIRS = ("transformer", "unet", "transformer_2", "dit")   # snapshot folders that hold a denoiser
-HEADER_LIMIT = 128 << 20   # a larger declared header is treated as unreadable, never allocated
+HEADER_LIMIT = 100 << 20   # the reference's MAX_HEADER_BYTES (models/safetensors_header.py:11): a larger
+# declared header is treated as unreadable, never allocated
 
 
 class SvdqArtifactError(RuntimeError):
@@ -157,7 +158,7 @@ def load_svdq_artifact(model_path: Path | str, model: Any, *, device: Any = "cud
                 art.file.name, art.lowrank_quant or "bf16")
     counts = load_svdq_int4_checkpoint(art.file, model, model_class=art.denoiser_class,
                                        adanorm_splits=adanorm_splits, device=device, lane=lane,
-                                       lowrank_quant=art.lowrank_quant)
+                                       lowrank_quant=art.lowrank_quant or "bf16")
     counts["artifact"] = art
     return counts
 

@@ -297,10 +297,12 @@ def _decode_lowrank(down: Tensor, up: Tensor, tensors: dict[str, Tensor], n: int
 
 
 def decode_int4_linear(tensors: dict[str, Tensor], out_features: int, in_features: int, *,
-                       lowrank_quant: Optional[str] = None) -> DecodedInt4Linear:
+                       lowrank_quant: Optional[str] = "bf16") -> DecodedInt4Linear:
     """One int4 svdq linear's stored tensors -> :class:`DecodedInt4Linear` (``decode_linear``,
     ``models/svdq_layout.py:366-434``, with int4 group-64 arithmetic); ``lowrank_quant`` is the artifact's
-    declared low-rank scheme (None: whatever the factors' dtype says)."""
+    declared low-rank scheme: "bf16" when the artifact declares none (the reference's default,
+    ``models/svdq_native.py:376``), so quantized factors that were not declared are refused; None accepts
+    whatever the factors' dtype says."""
     missing = [k for k in ("qweight", "wscales") if k not in tensors]
     if missing:
         raise SvdqLayoutError(f"not an svdq W4A4 linear (missing {missing})")
@@ -521,7 +523,7 @@ def _group_by_prefix(names) -> dict[str, list[str]]:
 
 def load_svdq_int4_checkpoint(path, model: nn.Module, *, model_class: str = "",
                               adanorm_splits: Optional[Dict[str, int]] = None, device: Any = "cuda",
-                              lane: Optional[str] = None, lowrank_quant: Optional[str] = None) -> dict:
+                              lane: Optional[str] = None, lowrank_quant: Optional[str] = "bf16") -> dict:
     """Read an int4 svdq safetensors file into ``model`` (a skeleton whose module names match the
     checkpoint's): int4 linears swapped for ``SvdqW4A4Linear`` (fused projections split), AWQ modulation
     linears for ``AwqPackedLinear``, every other tensor copied into the parameter / buffer of that name."""

@@ -129,5 +129,39 @@ def quantize_linear_w8a8(linear: nn.Linear, *, compute_dtype: Any = torch.bfloat
     return build_int8_linear(qweight=q, weight_scale=s, bias=b, compute_dtype=compute_dtype, device=device)
 
 
-__all__ = ["GEMM_MODES", "Int8ScaledLinear", "W8a8Error", "build_int8_linear", "quantize_linear_w8a8",
-           "quantize_weight_int8"]
+def dequantized_linear(*, qweight: Tensor, weight_scale: Tensor, bias: Optional[Tensor],
+                       compute_dtype: Any = torch.bfloat16, device: Any = "cuda") -> nn.Linear:
+    """The dequant lane's module: one ``nn.Linear`` holding ``qweight * weight_scale`` in ``compute_dtype``
+    (``models/w8a8.py:484-488``: the weight's memory saving is given up, its numbers are kept)."""
+    n, k = int(qweight.shape[0]), int(qweight.shape[1])
+    s = weight_scale.detach().float().reshape(-1)
+    if s.numel() not in (1, n):
+        raise W8a8Error(f"weight_scale has {s.numel()} values for {n} output channels")
+    w = qweight.detach().float() * s.reshape(-1, 1).to(qweight.device)
+    lin = nn.Linear(k, n, bias=bias is not None, device="meta")
+    lin.weight = nn.Parameter(w.to(device=device, dtype=compute_dtype), requires_grad=False)
+    if bias is not None:
+        lin.bias = nn.Parameter(bias.detach().reshape(-1).to(device=device, dtype=compute_dtype),
+                                requires_grad=False)
+    return lin
+
+
+def serving_w8a8_linear(*, qweight: Tensor, weight_scale: Tensor, bias: Optional[Tensor],
+                        compute_dtype: Any = torch.bfloat16, device: Any = "cuda",
+                        input_scale: Optional[Tensor] = None, mode: Optional[str] = None) -> nn.Module:
+    """The module to serve for one W8A8 layer: an ``Int8ScaledLinear`` in ``mode`` ("rowwise" or
+    "pertensor"; default: the branch this process qualified, ``qualify.w8a8_gemm_mode``, chosen once), or in
+    the dequant lane (``mode="dequant"``, or no branch qualified) the dequantized ``nn.Linear``: the
+    reference's loader rule (``models/w8a8.py:462-466``, ``:478-488``)."""
+    from .qualify import resolve_w8a8_mode
+
+    mode = resolve_w8a8_mode(mode)
+    if mode == "dequant":
+        return dequantized_linear(qweight=qweight, weight_scale=weight_scale, bias=bias,
+                                  compute_dtype=compute_dtype, device=device)
+    return build_int8_linear(qweight=qweight, weight_scale=weight_scale, bias=bias, compute_dtype=compute_dtype,
+                             device=device, input_scale=input_scale, gemm_mode=mode)
+
+
+__all__ = ["GEMM_MODES", "Int8ScaledLinear", "W8a8Error", "build_int8_linear", "dequantized_linear",
+           "quantize_linear_w8a8", "quantize_weight_int8", "serving_w8a8_linear"]

@@ -36,6 +36,10 @@ def check_output(y: torch.Tensor, ref: np.ndarray, *, what: str = "") -> dict:
         "mean_rel": O.mean_rel_err(yf, ref),
         "rel_fro": float(np.linalg.norm(yf - ref) / max(np.linalg.norm(ref), 1e-30)) if ref.size else 0.0,
     }
+    # the plain max-abs error is printed beside the relaxed bound (bf16 outputs above ~5 carry a half-ulp
+    # rounding larger than 2e-2 by themselves)
+    print(f"{what}: max_abs {stats['max_abs']:.3e} (beyond the output rounding {excess:.3e}), mean_rel "
+          f"{stats['mean_rel']:.3e}, rel_fro {stats['rel_fro']:.3e}")
     assert np.isfinite(yf).all(), f"{what}: non-finite output"
     assert excess <= MAX_ABS, f"{what}: {stats}"
     assert stats["mean_rel"] <= MEAN_REL, f"{what}: {stats}"

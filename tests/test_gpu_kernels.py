@@ -689,8 +689,9 @@ def test_flux_dit_lanes_agree():
 
 def test_qualification_gates():
     """The arming protocol on the device: every numerics gate passes, the profitability gate (the int4 GEMM
-    against the bf16 matmul at 4096^3, >= 1.10x, ``models/w4a4.py:210-259``) decides the lane by its own rule,
-    and on MI355X it arms the int4 lane (1.21x measured: 0.086 ms against 0.104 ms, back-to-back calls)."""
+    against the bf16 matmul at 4096^3, >= 1.10x, ``models/w4a4.py:210-259``) decides the lane by its own rule
+    (on MI355X it has armed the int4 lane: 1.21x measured, 0.086 ms against 0.104 ms, back-to-back calls; a
+    box where the ratio falls under the bar degrades to the dense lane, which this test accepts)."""
     from gen_worker_amd import qualify
 
     assert qualify.extension_available()
@@ -702,7 +703,7 @@ def test_qualification_gates():
     assert q.speedup is not None and q.speedup > 0
     assert q.lane == ("int4" if q.speedup >= qualify.BENCH_MIN_SPEEDUP else "dense"), q
     assert (q.lane == "int4") == (not q.reasons), q
-    assert q.lane == "int4" and qualify.resolve_lane() == "int4", q
+    assert qualify.resolve_lane() == q.lane, q  # the lane is decided once per process and then reused
     # the record decoder of the gates agrees with the test helper's
     x = torch.randn(77, 384, device=DEV).to(torch.bfloat16)
     q6, _ = torch.ops.cozy_gen_worker.svdq_quant_fp6(x, None, None, None)

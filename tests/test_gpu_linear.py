@@ -91,7 +91,8 @@ def test_linear_entry_point_workspace_contract():
     ws = torch.empty(need + 256, dtype=torch.uint8, device=DEV)
     out = torch.empty(m, n, dtype=torch.bfloat16, device=DEV)
     args = lambda w, nbytes: (nat.ptr(x), k, nat.ptr(mod.smooth_factor), None, nat.ptr(mod.proj_down_op6), r,  # noqa: E731
-                              nat.ptr(mod.weight_fp6), nat.ptr(mod.second), 1, nat.ptr(mod.proj_up),
+                              nat.ptr(mod.weight_fp6), ops.readable_bytes(mod.weight_fp6), nat.ptr(mod.second), 1,
+                              nat.ptr(mod.proj_up),
                               nat.ptr(mod.bias), nat.ptr(out), nat.DT_BF16, 0, m, n, k, w, nbytes,
                               nat.stream_of(x))
     nat.call("gwa_svdq_w4a4_linear_fp6", *args(ws.data_ptr(), need))

@@ -7,6 +7,8 @@ the whole forward: finite output of the right shape, two eager forwards bit-iden
 deterministic: fixed-order la sums, no atomics in any accumulation), a HIP-graph replay bit-identical to
 eager, and agreement with the same weights run on the dense lane (each layer folded to one bf16 Linear)
 within the drift that int4 activation quantization compounds over 57 blocks (cosine 0.999 measured).
+Those checks run with this package's attention kernel; the model with torch's SDPA (config 4 as stated, the
+bench's default DiT line) is held to a finite output, a graph replay equal to eager and agreement with it.
 """
 
 from __future__ import annotations
@@ -39,7 +41,7 @@ def test_full_size_dit_forward():
 
     cfg = FluxDiTConfig()
     args = inputs(cfg)
-    m4 = FluxDiT("w4a4", cfg, device=DEV, lane="int4")
+    m4 = FluxDiT("w4a4", cfg, device=DEV, lane="int4", attention="flash")
     assert m4.lane == "int4"
     assert sum(isinstance(m, SvdqW4A4Linear) for m in m4.modules()) > 4 * (cfg.n_dual + cfg.n_single)
     with torch.no_grad():
@@ -92,7 +94,7 @@ def test_full_size_dit_forward():
     m4.mod_stream = None
     del g, yg, y3
 
-    md = FluxDiT("w4a4", cfg, device=DEV, lane="dense")
+    md = FluxDiT("w4a4", cfg, device=DEV, lane="dense", attention="flash")
     assert md.lane == "dense" and not any(isinstance(m, SvdqW4A4Linear) for m in md.modules())
     with torch.no_grad():
         yd = md(*args)
@@ -100,4 +102,42 @@ def test_full_size_dit_forward():
     cos = _cos(y1, yd)
     print(f"full-size DiT: cosine(int4 lane, dense lane) = {cos:.4f}")
     assert bool(torch.isfinite(yd).all())
+    assert cos > 0.99, cos
+
+
+def test_full_size_dit_forward_sdpa():
+    """Config 4 as stated: the same int4-lane model with torch's bf16 SDPA in every block (flash /
+    memory-efficient kernels only). Finite, a HIP-graph replay equal to the eager forward, and within the
+    attention kernels' difference of the model run with gwa_dit_attention."""
+    from gen_worker_amd.flux_dit import ATTENTION, FluxDiT, FluxDiTConfig, inputs
+
+    cfg = FluxDiTConfig()
+    args = inputs(cfg)
+    ms = FluxDiT("w4a4", cfg, device=DEV, lane="int4", attention="sdpa", streams=2)
+    with torch.no_grad():
+        y1 = ms(*args)
+    torch.cuda.synchronize()
+    assert tuple(y1.shape) == (cfg.img_tokens, cfg.in_channels) and bool(torch.isfinite(y1).all())
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.no_grad(), torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            yg = ms(*args)
+    torch.cuda.synchronize()
+    for _ in range(2):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(yg, y1), "SDPA model: graph replay differs from eager"
+        with torch.no_grad():
+            ms(*args)
+        torch.cuda.synchronize()
+    del g, yg
+    for blk in list(ms.dual) + list(ms.single):
+        blk.attn = ATTENTION["flash"]
+    with torch.no_grad():
+        yf = ms(*args)
+    torch.cuda.synchronize()
+    cos = _cos(y1, yf)
+    print(f"full-size DiT: cosine(SDPA, gwa_dit_attention) = {cos:.5f}")
     assert cos > 0.99, cos

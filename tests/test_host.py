@@ -112,14 +112,15 @@ def test_invalid_arguments_are_refused_before_any_launch():
     assert lib.gwa_svdq_gemm_w4a4_fp6_next_partials(4608, 12288) == 48
     assert lib.gwa_svdq_gemm_w4a4_fp6_next_partials(256, 3072) == 24
     assert lib.gwa_svdq_quant_fp6_partials(4608, 3072, 0) == 0
-    rc = lib.gwa_svdq_gemm_w4a4_fp6(None, None, None, None, 0, None, None, 0, None, None, 0, 0, 8, 64, 192, None)
+    rc = lib.gwa_svdq_gemm_w4a4_fp6(None, 0, None, 0, None, None, 0, None, None, 0, None, None, 0, 0, 8, 64, 192,
+                                    None)
     assert rc == 1 and "multiple of 128" in lib.gwa_last_error().decode()
     # the next-layer epilogue needs whole 128-column stages and a record buffer
-    rc = lib.gwa_svdq_gemm_w4a4_fp6_next(None, None, None, None, 0, None, None, 0, None, None, 0, None, None, 0,
-                                         None, None, 8, 192, 128, None)
+    rc = lib.gwa_svdq_gemm_w4a4_fp6_next(None, 0, None, 0, None, None, 0, None, None, 0, None, None, 0, None, None,
+                                         0, None, None, 8, 192, 128, None)
     assert rc == 1 and "multiple of 128" in lib.gwa_last_error().decode()
-    rc = lib.gwa_svdq_gemm_w4a4_fp6_next(None, None, None, None, 0, None, None, 0, None, None, 0, None, None, 0,
-                                         None, None, 8, 256, 128, None)
+    rc = lib.gwa_svdq_gemm_w4a4_fp6_next(None, 0, None, 0, None, None, 0, None, None, 0, None, None, 0, None, None,
+                                         0, None, None, 8, 256, 128, None)
     assert rc == 1 and "next_q6" in lib.gwa_last_error().decode()
     rc = lib.gwa_svdq_prep_proj_down(None, None, 64, 24, None)
     assert rc == 1 and "rank" in lib.gwa_last_error().decode()
@@ -133,6 +134,42 @@ def test_invalid_arguments_are_refused_before_any_launch():
     # empty problems are no-ops
     assert lib.gwa_svdq_quant_int4(None, 64, None, None, None, 0, 0, None, None, None, 0, 64, None) == 0
     assert lib.gwa_probe_add_one(None, None, 0, None) == 0
+
+
+def test_record_buffer_sizes_are_checked_at_the_c_abi():
+    """Every C entry point that reads fp6 records takes each record pointer's readable byte count and refuses a
+    buffer shorter than the records plus GWA_FP6_RECORD_SLACK (the GEMMs' 1 KB copy runs may read that far past
+    the last record) with GWA_ERR_INVALID before anything is enqueued; the psums kernel reads through
+    range-checked lane offsets and needs the records only. The pointers below are never dereferenced: every
+    call is refused on its sizes before any HIP call."""
+    from gen_worker_amd import _native as nat
+
+    lib = nat.load()
+    fake = ctypes.c_void_p(1 << 20)   # aligned, non-null; never touched
+    m, n, k = 288, 192, 384
+    qa_need, qw_need, slack = (k // 128) * m * nat.FP6_REC, (k // 128) * n * nat.FP6_REC, 1024
+    for fn in ("gwa_svdq_gemm_w4a4_fp6", "gwa_svdq_gemm_w4a4_fp6_next"):
+        def call(qa_b, qw_b):
+            if fn == "gwa_svdq_gemm_w4a4_fp6":
+                return lib.gwa_svdq_gemm_w4a4_fp6(fake, qa_b, fake, qw_b, None, None, 0, None, None, 0, None, fake,
+                                                  0, 0, m, n, k, None)
+            return lib.gwa_svdq_gemm_w4a4_fp6_next(fake, qa_b, fake, qw_b, None, None, 0, None, None, 0, None, fake,
+                                                   0, None, None, 0, fake, None, m, 256, k, None)
+        nn_ = n if fn == "gwa_svdq_gemm_w4a4_fp6" else 256
+        qwn = (k // 128) * nn_ * nat.FP6_REC
+        assert call(qa_need + slack - 1, qwn + slack) == 1
+        assert "qa6 has" in lib.gwa_last_error().decode() and "slack" in lib.gwa_last_error().decode()
+        assert call(qa_need + slack, qwn + slack - 1) == 1
+        assert "qw6 has" in lib.gwa_last_error().decode()
+    rc = lib.gwa_svdq_group_psums_fp6(fake, qa_need - 1, fake, qw_need, fake, m, n, k, None)
+    assert rc == 1 and "record buffers" in lib.gwa_last_error().decode()
+    rc = lib.gwa_svdq_group_psums_fp6(fake, qa_need, fake, qw_need - 1, fake, m, n, k, None)
+    assert rc == 1 and "record buffers" in lib.gwa_last_error().decode()
+    for fn in ("gwa_svdq_w4a4_linear_fp6", "gwa_svdq_w4a4_linear_fp6_noalloc"):
+        tail = (fake, 1 << 30, None) if fn == "gwa_svdq_w4a4_linear_fp6" else (None,)
+        rc = getattr(lib, fn)(fake, k, None, None, None, 0, fake, qw_need + slack - 1, None, 0, None, None, fake, 0,
+                              0, m, n, k, *tail)
+        assert rc == 1 and "qw6 has" in lib.gwa_last_error().decode(), lib.gwa_last_error()
 
 
 def test_native_error_is_raised_with_message():

@@ -150,6 +150,19 @@ def test_key_map_and_refusals(tmp_path):
         load_nvfp4_denoiser([path], small, key_map=strip, device="cpu", lane="dense")
     with pytest.raises(ValueError, match="lane"):
         load_nvfp4_denoiser([path], _meta_skeleton(), key_map=strip, device="cpu", lane="fp4")
+    # bias presence must agree (the reference's load_state_dict reports either side's extra bias), in the
+    # swap branch (lane nvfp4: refused before any module is built) and the dequantized one
+    from safetensors.torch import save_file
+
+    no_b0 = tmp_path / "no_lin0_bias.safetensors"
+    save_file({k: v for k, v in sd.items() if k != "transformer.lin0.bias"}, str(no_b0))
+    for lane in ("nvfp4", "dense"):   # lin0 is the first layer swapped: nothing is built before the check
+        nobias = _meta_skeleton()
+        nobias.lin0 = nn.Linear(64, 32, bias=False, device="meta")     # the checkpoint has lin0.bias
+        with pytest.raises(Nvfp4CheckpointError, match="no bias"):
+            load_nvfp4_denoiser([path], nobias, key_map=strip, device="cpu", lane=lane)
+        with pytest.raises(Nvfp4CheckpointError, match="does not provide"):   # module bias, none stored
+            load_nvfp4_denoiser([no_b0], _meta_skeleton(), key_map=strip, device="cpu", lane=lane)
 
 
 @pytest.mark.gpu

@@ -40,6 +40,12 @@ def test_metadata_reader(tmp_path):
     huge = tmp_path / "huge.safetensors"
     huge.write_bytes(struct.pack("<Q", 1 << 40) + b"{}")      # a declared header far past the limit: not read
     assert A.read_safetensors_metadata(huge) == {}
+    # the bound is the reference's MAX_HEADER_BYTES (models/safetensors_header.py:11); one byte past it is
+    # refused before any read
+    assert A.HEADER_LIMIT == 100 * 1024 * 1024
+    over = tmp_path / "over.safetensors"
+    over.write_bytes(struct.pack("<Q", A.HEADER_LIMIT + 1) + b'{"__metadata__": {"a": "b"}}')
+    assert A.read_safetensors_metadata(over) == {}
     assert A.read_safetensors_metadata(tmp_path / "missing.safetensors") == {}
 
 
@@ -155,14 +161,18 @@ def test_decode_quantized_lowrank_branch(scheme):
     dec = C.decode_int4_linear(stored, 256, 384, lowrank_quant=scheme)
     assert dec.rank == 32 and torch.equal(dec.proj_down, down) and torch.equal(dec.proj_up, up)
     assert np.array_equal(dec.codes.numpy(), logical["codes"])
-    assert torch.equal(C.decode_int4_linear(stored, 256, 384).proj_down, down)   # undeclared: by dtype
+    # undeclared means bf16 (the reference's default): quantized factors are refused; None decodes by dtype
+    with pytest.raises(C.SvdqLayoutError, match="declares"):
+        C.decode_int4_linear(stored, 256, 384)
+    assert torch.equal(C.decode_int4_linear(stored, 256, 384, lowrank_quant=None).proj_down, down)
     other = "int8" if scheme != "int8" else "fp8_e4m3"
     with pytest.raises(C.SvdqLayoutError, match="declares"):
         C.decode_int4_linear(stored, 256, 384, lowrank_quant=other)
     with pytest.raises(C.SvdqLayoutError, match="proj_up_scale"):
-        C.decode_int4_linear({k_: v for k_, v in stored.items() if k_ != "proj_up_scale"}, 256, 384)
+        C.decode_int4_linear({k_: v for k_, v in stored.items() if k_ != "proj_up_scale"}, 256, 384,
+                             lowrank_quant=scheme)
     with pytest.raises(C.SvdqLayoutError, match="one scheme"):
-        C.decode_int4_linear(dict(stored, proj_up=up), 256, 384)
+        C.decode_int4_linear(dict(stored, proj_up=up), 256, 384, lowrank_quant=scheme)
     _, plain = synthetic_int4_layer(256, 384, 32, 9)
     with pytest.raises(C.SvdqLayoutError, match="not stored quantized"):
         C.decode_int4_linear(dict(plain, proj_down_scale=stored["proj_down_scale"]), 256, 384)

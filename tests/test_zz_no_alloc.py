@@ -42,10 +42,12 @@ def _module(n, k, r, seed):
 
 def _args(mod, x, out, gelu=False):
     from gen_worker_amd import _native as nat
+    from gen_worker_amd import ops
 
     m, k = int(x.shape[0]), int(x.shape[1])
     return (nat.ptr(x), k, nat.ptr(mod.smooth_factor), None, nat.ptr(mod.proj_down_op6) if mod.rank else None,
-            mod.rank, nat.ptr(mod.weight_fp6), nat.ptr(mod.second), int(mod.second.numel()),
+            mod.rank, nat.ptr(mod.weight_fp6), ops.readable_bytes(mod.weight_fp6), nat.ptr(mod.second),
+            int(mod.second.numel()),
             nat.ptr(mod.proj_up) if mod.rank else None, nat.ptr(mod.bias), nat.ptr(out), nat.DT_BF16,
             nat.EPI_GELU_TANH if gelu else 0, m, mod.out_features, k)
 
@@ -114,9 +116,9 @@ def test_no_alloc_refuses_shapes_beyond_its_scratch():
         lo, hi = (mid, hi) if ops.linear_fp6_workspace_bytes(mid, 3072, 32) <= cap else (lo, mid)
     too_big = hi
     dummy = 256   # never dereferenced: the size check comes first
-    rc = lib.gwa_svdq_w4a4_linear_fp6_noalloc(dummy, 3072, None, None, dummy, 32, dummy, None, 0, dummy, None, dummy,
-                                              nat.DT_BF16, 0, too_big, 3072, 3072, None)
+    rc = lib.gwa_svdq_w4a4_linear_fp6_noalloc(dummy, 3072, None, None, dummy, 32, dummy, 1 << 30, None, 0, dummy, None,
+                                              dummy, nat.DT_BF16, 0, too_big, 3072, 3072, None)
     assert rc == 1 and "static scratch holds" in lib.gwa_last_error().decode()
-    rc = lib.gwa_svdq_w4a4_linear_fp6_noalloc(None, 3072, None, None, None, 0, None, None, 0, None, None, None,
+    rc = lib.gwa_svdq_w4a4_linear_fp6_noalloc(None, 3072, None, None, None, 0, None, 0, None, 0, None, None, None,
                                               nat.DT_BF16, 0, 0, 3072, 3072, None)
     assert rc == 0   # M = 0: nothing to do
