@@ -90,17 +90,48 @@ def test_w4a4_qkv(m, odt, w4a4_layer):
 
 
 @pytest.mark.parametrize("m", [256, 1024, 4608, 16384])
-def test_w8a8_qkv(m, w8a8_layer):
+@pytest.mark.parametrize("odt", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("mode", ["rowwise", "pertensor"])
+def test_w8a8_qkv(m, odt, mode, w8a8_layer):
     from gen_worker_amd.w8a8 import build_int8_linear
 
     L = w8a8_layer
-    mod = build_int8_linear(qweight=L.qweight, weight_scale=L.weight_scale, bias=L.bias, device=DEV)
+    mod = build_int8_linear(qweight=L.qweight, weight_scale=L.weight_scale, bias=L.bias, compute_dtype=odt,
+                            device=DEV, gemm_mode=mode)
     x = _act(m).to(DEV)
     y = mod(x)
     y2 = mod(x)
     torch.cuda.synchronize()
-    assert tuple(y.shape) == (m, N) and torch.isfinite(y).all()
+    assert y.dtype == odt and tuple(y.shape) == (m, N) and torch.isfinite(y).all()
     assert torch.equal(y.view(torch.int16), y2.view(torch.int16)), "not deterministic"
-    rows = _rows(m)
-    ref = O.w8a8_linear(bits16(x[rows]), L.qweight.numpy(), L.weight_scale.numpy(), L.bias.numpy())
-    check_output(y[rows], ref, what=f"W8A8 QKV M={m}")
+    if mode == "pertensor":
+        # one activation scale for the whole call: the oracle needs every row's absmax, then checks a sample
+        xs = bits16(x)
+        amax = float(np.abs(O.bf16_bits_to_f32(xs)).max())
+        static = max(np.float32(amax) / np.float32(O.INT8_QMAX), np.float32(O.INT8_SCALE_MIN))
+        rows = _rows(m)
+        ref = O.w8a8_linear(xs[rows], L.qweight.numpy(), L.weight_scale.numpy(), L.bias.numpy(), pertensor=True,
+                            static=float(static))
+    else:
+        rows = _rows(m)
+        ref = O.w8a8_linear(bits16(x[rows]), L.qweight.numpy(), L.weight_scale.numpy(), L.bias.numpy())
+    check_output(y[rows], ref, what=f"W8A8 QKV M={m} {odt} {mode}")
+
+
+def test_w8a8_gate_on_the_device():
+    """The W8A8 branch gate (``models/w8a8.py:137-256``) on MI355X: both branches' probes pass, their 4096^3
+    timings under both protocols are recorded for every branch it tried, and the mode follows its rule (the
+    first branch at >= 1.10x over bf16, else the dequant lane)."""
+    from gen_worker_amd import qualify
+
+    for mode in qualify.W8A8_MODES:
+        assert qualify.w8a8_probe(mode) is None, mode
+    q = qualify.qualify_w8a8()
+    print("w8a8 qualification", q)
+    tried = list(q.timings)
+    assert tried and tried[0] == "rowwise"
+    for mode, t in q.timings.items():
+        assert set(t) == {"graph", "eager"} and all(v[0] > 0 and v[1] > 0 for v in t.values())
+    first_ok = next((m_ for m_ in qualify.W8A8_MODES if m_ in q.timings
+                     and q.timings[m_]["graph"][2] >= qualify.BENCH_MIN_SPEEDUP), "")
+    assert q.mode == first_ok, q
