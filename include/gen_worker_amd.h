@@ -51,7 +51,8 @@ enum {
  *   bytes [0, 96)   the stage's two groups as e3m2 codes: element t of group j
  *                   at bits [6t, 6t+6) of bytes [48j, 48j+48) (little-endian)
  *   bytes [96, 100) the two groups' fp16 scales
- *   bytes [100,104) unused
+ *   bytes [100,104) zero (written by every producer: the GEMMs read bytes
+ *                   [96, 104) as one (scales, 0) operand pair)
  * (every int4 code -8..7 is an exact e3m2 value). A tile's stage of operand
  * rows is one contiguous run, and its LDS image keeps a bank-conflict-free
  * row stride. */

@@ -592,7 +592,8 @@ __global__ __launch_bounds__(NTHREADS, (TM == 64 ? 4 : 1)) void w4a4_gemm_fp6_ke
     const rsrc_t qb = make_rsrc(nx.q6, (uint32_t)((int64_t)(N >> 7) * M * REC));
     const int nstage = col >> 7;
     const uint32_t in_rec = (uint32_t)(48 * ((cch32 >> 1) & 1) + 24 * (cch32 & 1));
-    const uint32_t sc_off = (cch32 & 1) ? kOOB : (uint32_t)(96 + 2 * ((cch32 >> 1) & 1));
+    // the scales at 96 + 2 g from the even lanes, zeros into the unused bytes 100..103 from the odd ones
+    const uint32_t sc_off = (uint32_t)(96 + 2 * ((cch32 >> 1) & 1) + 4 * (cch32 & 1));
 #pragma unroll 1
     for (int r0 = 0; r0 < TM; r0 += RPP32) {
       const int row = r0 + crow32;
@@ -616,7 +617,7 @@ __global__ __launch_bounds__(NTHREADS, (TM == 64 ? 4 : 1)) void w4a4_gemm_fp6_ke
       const uint32_t rec = (uint32_t)(((int64_t)nstage * M + m0 + row) * REC);
       buf_store16((v4i){(int)pk[0], (int)pk[1], (int)pk[2], (int)pk[3]}, qb, valid ? rec + in_rec : kOOB);
       buf_store8(make_uint2(pk[4], pk[5]), qb, valid ? rec + in_rec + 16u : kOOB);
-      buf_store2(sh, qb, (valid && sc_off != kOOB) ? rec + sc_off : kOOB);
+      buf_store2((cch32 & 1) ? (uint16_t)0 : sh, qb, valid ? rec + sc_off : kOOB);
     }
   }
 }

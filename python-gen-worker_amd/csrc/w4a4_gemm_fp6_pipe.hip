@@ -178,8 +178,14 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_pipe_kernel(
   // operand registers: activation operands (block rows) and their stage scales, weight operands (block columns)
   // and theirs (lanes 32..63 hold zero weight scales: K slots 4..7 of the S MFMA)
   v8i xo[NA], wo[NB];
-  uint2 xsel[NA][GS];  // (activation row's scale of group g in its half, 0): the S MFMA's B operand per group
-  uint2 ws[NB];        // (the stage's two weight group scales, 0): the S MFMA's A operand
+  // (activation row's scale of group g in its half, 0): the S MFMA's B operand per group; (the stage's two
+  // weight group scales, 0): its A operand. The .y halves (K slots 2..3, zero) are set here and never
+  // written again: the reads below refresh .x only, and the scheduling pins pass the registers through.
+  uint2 xsel[NA][GS], ws[NB];
+#pragma unroll
+  for (int a = 0; a < NA; ++a) xsel[a][0] = xsel[a][1] = make_uint2(0u, 0u);
+#pragma unroll
+  for (int b = 0; b < NB; ++b) ws[b] = make_uint2(0u, 0u);
   auto row_of = [&](int a) __attribute__((always_inline)) { return a < 2 ? 64 * wm + 32 * a : 256; };
   auto col_of = [&](int b) __attribute__((always_inline)) {
     const int c = rot + b;
