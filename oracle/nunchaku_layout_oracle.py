@@ -24,7 +24,14 @@ product's tensor reshapes:
   ((((((cp * RP + rp) * 8 + nl) * 4 + kl) * 2 + ns) * 2 + ks) * 2 + kr)
   (``models/svdq_layout.py:27-31``); for proj_down i_n runs over the rank
   and i_k over the input, for proj_up i_n over the output and i_k over the
-  rank.
+  rank;
+* fp4 micro-scales (``pack_micro_scale``, the reference test's restatement at
+  ``tests/test_svdq_official_layout_pgw770.py:47-63``, decoded by
+  ``models/svdq_layout.py:110-125``): scale [n, NB] (one e4m3 per 16 inputs),
+  row n = 128 t + 32 a + 8 b + c and block = 4 q + j, goes to flat position
+  ((((t * Q + q) * 8 + c) * 4 + b) * 4 + a) * 4 + j of the stored [NB, n]
+  grid (Q = NB / 4), the (4, 4, 8) row split with the lane index c
+  outermost.
 """
 
 from __future__ import annotations
@@ -80,3 +87,18 @@ def pack_lowrank(weight: np.ndarray, *, down: bool) -> np.ndarray:
             f = (((((cp * rp_n + rp) * 8 + nl) * 4 + kl) * 2 + ns) * 2 + ks) * 2 + kr
             flat[f] = weight[row, col]
     return flat.reshape(c_n, r_n)
+
+
+def pack_micro_scale(scales: np.ndarray) -> np.ndarray:
+    """e4m3 scale bytes [n, NB] -> the stored grid [NB, n]."""
+    n, nb = scales.shape
+    q_n = nb // 4
+    flat = np.zeros(n * nb, dtype=scales.dtype)
+    for row in range(n):
+        t, r = divmod(row, 128)
+        a, r = divmod(r, 32)
+        b, c = divmod(r, 8)
+        for blk in range(nb):
+            q, j = divmod(blk, 4)
+            flat[((((t * q_n + q) * 8 + c) * 4 + b) * 4 + a) * 4 + j] = scales[row, blk]
+    return flat.reshape(nb, n)

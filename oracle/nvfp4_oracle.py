@@ -20,7 +20,13 @@ reference's torch ops on fp32 tensors):
   zero-block rule ``bs[bs == 0] = 1.0``;
 * ``nvfp4_linear`` = ``_W4A4Linear.forward`` (``models/w4a4.py:336-352``):
   the fp4 product summed in float64 and rounded to bf16 (torch._scaled_mm
-  with a bf16 out_dtype), times bf16(s2 * weight_scale_2), plus the bf16 bias.
+  with a bf16 out_dtype), times bf16(s2 * weight_scale_2), plus the bf16 bias;
+* ``svdq_fp4_linear`` = the svdq fp4 module's forward (``_SvdqLinear.forward``,
+  ``models/svdq_native.py:140-156``): the activation divided by the smoothing
+  factors (bf16), the dynamic scale s2 = max|xs| / (6 * 448), the fp4 product
+  rounded to bf16, times bf16(s2 * second) (second per output channel or per
+  tensor), plus the low-rank branch on the RAW activation
+  bf16(bf16(x @ down) @ up^T), plus the bias, each sum rounded to bf16.
 """
 
 from __future__ import annotations
@@ -167,4 +173,25 @@ def nvfp4_linear(x: np.ndarray, s2: float, wq: np.ndarray, ws_flat: np.ndarray, 
     y = bf16_round(y * bf16_round(np.float32(s2) * np.float32(ws2)))
     if bias is not None:
         y = bf16_round(y + np.asarray(bias, np.float32))
+    return y.astype(np.float64)
+
+
+def svdq_fp4_linear(x: np.ndarray, smooth, wq: np.ndarray, ws_flat: np.ndarray, second, down=None, up=None,
+                    bias=None, s2=None) -> np.ndarray:
+    """bf16-valued float32 x [M, K]; smooth [K] or None; packed codes wq [N, K/2]; flat e4m3 scale bytes
+    ws_flat [N, K/16]; second [N] or [1]; down [K, r] and up [N, r] or None; bias [N] or None; s2 the call's
+    dynamic scale (computed from x when None; a row sample passes the full call's) -> float64 [M, N]."""
+    x = np.asarray(x, np.float32)
+    xs = x if smooth is None else bf16_round(x / np.asarray(smooth, np.float32).reshape(1, -1))
+    s2 = dynamic_s2(xs) if s2 is None else np.float32(s2)
+    xq, xsc = quantize_activation(xs, s2)
+    acc = dequantize(xq, xsc).astype(np.float64) @ dequantize(wq, ws_flat).astype(np.float64).T
+    y = bf16_round(acc.astype(np.float32))
+    y = bf16_round(y * bf16_round(np.float32(s2) * np.asarray(second, np.float32).reshape(1, -1)))
+    if down is not None:
+        t = bf16_round((x.astype(np.float64) @ np.asarray(down, np.float64)).astype(np.float32))
+        lr = bf16_round((t.astype(np.float64) @ np.asarray(up, np.float64).T).astype(np.float32))
+        y = bf16_round(y + lr)
+    if bias is not None:
+        y = bf16_round(y + np.asarray(bias, np.float32).reshape(1, -1))
     return y.astype(np.float64)

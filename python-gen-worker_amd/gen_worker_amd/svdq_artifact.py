@@ -6,14 +6,15 @@ The reference tags a nunchaku single-file checkpoint by its safetensors
 ``model_class`` named ``Nunchaku…``, the weight precision from
 ``quantization_config.weight.dtype`` (fp4 / int4) and the rank; it looks in
 the denoiser component folders first, then at the snapshot root, and refuses
-what it cannot serve with typed errors. This build serves the int4 packaging
-natively (the reference's refusal, ``models/svdq.py:30-37``) and refuses the
-nvfp4 (fp4) svdq packaging, whose block-16 e4m3 micro-scales and fragment
-layout this build does not decode.
+what it cannot serve with typed errors. This build serves both packagings:
+int4 natively on the int4-g64 kernels (where the reference refuses,
+``models/svdq.py:30-37``) and fp4 (block-16 e4m3 micro-scales,
+``svdq_fp4``) folded to bf16 or, in the blockwise mode, with the reference's
+fp4 numerics.
 
-``load_svdq_artifact`` is the routing: detect, check, then load the int4 file
-into a caller-built module skeleton with the process's qualified lane
-(``svdq_checkpoint.load_svdq_int4_checkpoint``).
+``load_svdq_artifact`` is the routing: detect, check, then load the file into
+a caller-built module skeleton with the process's qualified lane
+(``svdq_checkpoint.load_svdq_checkpoint``).
 """
 
 from __future__ import annotations
@@ -129,13 +130,11 @@ def detect_svdq_artifact(model_path: Path | str) -> Optional[SvdqArtifact]:
 
 
 def check_svdq_servable(art: SvdqArtifact) -> None:
-    """Raise the typed refusal for an artifact this build cannot serve (nothing for the int4 packaging)."""
-    if art.precision != "int4":
-        raise SvdqPrecisionUnsupported(
-            f"{art.file} is svdq-{art.precision}: this build decodes the int4 group-64 svdq packaging (served on "
-            f"the int4 lane, or folded to bf16 in the dense lane); the fp4 packaging's block-16 e4m3 "
-            f"micro-scales have no decoder here (the nvfp4 lane serves modelopt nvfp4 linears, a different "
-            f"file layout)")
+    """Raise the typed refusal for an artifact this build cannot serve (nothing for the int4 and fp4
+    packagings with a known low-rank scheme)."""
+    if art.precision not in ("int4", "fp4"):
+        raise SvdqPrecisionUnsupported(f"{art.file} is svdq-{art.precision}: this build decodes the int4 group-64 "
+                                       f"and the fp4 block-16 svdq packagings")
     from .svdq_checkpoint import LOWRANK_SCHEMES
 
     if art.lowrank_quant not in (None, "bf16") and art.lowrank_quant not in LOWRANK_SCHEMES:
@@ -144,10 +143,11 @@ def check_svdq_servable(art: SvdqArtifact) -> None:
 
 
 def load_svdq_artifact(model_path: Path | str, model: Any, *, device: Any = "cuda", lane: Optional[str] = None,
-                       adanorm_splits: Optional[Dict[str, int]] = None) -> dict:
+                       adanorm_splits: Optional[Dict[str, int]] = None, fp4_mode: Optional[str] = None) -> dict:
     """Detect the snapshot's svdq checkpoint, refuse what this build cannot serve, and load it into ``model``
-    (a module skeleton whose names match the checkpoint's). Returns the loader's counts plus the artifact."""
-    from .svdq_checkpoint import load_svdq_int4_checkpoint
+    (a module skeleton whose names match the checkpoint's): int4 linears by ``lane``, fp4 linears by
+    ``fp4_mode`` ("dense" by default, "blockwise"). Returns the loader's counts plus the artifact."""
+    from .svdq_checkpoint import load_svdq_checkpoint
 
     art = detect_svdq_artifact(model_path)
     if art is None:
@@ -156,9 +156,9 @@ def load_svdq_artifact(model_path: Path | str, model: Any, *, device: Any = "cud
     check_svdq_servable(art)
     logger.info("svdq: %s %s rank %d (%s), low-rank branch %s", art.precision, art.model_class, art.rank,
                 art.file.name, art.lowrank_quant or "bf16")
-    counts = load_svdq_int4_checkpoint(art.file, model, model_class=art.denoiser_class,
-                                       adanorm_splits=adanorm_splits, device=device, lane=lane,
-                                       lowrank_quant=art.lowrank_quant or "bf16")
+    counts = load_svdq_checkpoint(art.file, model, model_class=art.denoiser_class, adanorm_splits=adanorm_splits,
+                                  device=device, lane=lane, lowrank_quant=art.lowrank_quant or "bf16",
+                                  fp4_mode=fp4_mode, precision=art.precision)
     counts["artifact"] = art
     return counts
 

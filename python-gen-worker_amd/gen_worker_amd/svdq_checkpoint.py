@@ -33,9 +33,11 @@ splits nunchaku's fused projections (``to_qkv`` -> ``to_q``/``to_k``/``to_v``,
 folded dense Linear in the dense lane and where the kernel contract does not
 hold). AWQ W4A16 modulation layers go through
 ``swap_awq_linears`` with the exporter's adaLN split count
-(``models/svdq_native.py:324-338``). ``load_svdq_int4_checkpoint`` reads a
+(``models/svdq_native.py:324-338``). ``load_svdq_checkpoint`` reads a
 safetensors file into a caller-built module skeleton (the reference builds
-the stock diffusers class, which this environment does not ship).
+the stock diffusers class, which this environment does not ship). The fp4
+packaging the reference serves (e4m3 micro-scales per 16 inputs) decodes
+through ``svdq_fp4`` into the same logical domain and the same swap.
 
 The interleaves are formats fixed by the checkpoints; the functions here
 compute them independently (the oracle restates the forward packers with
@@ -355,7 +357,12 @@ def split_decoded(dec: DecodedInt4Linear, sections: Sequence[int]) -> tuple[Deco
 
 
 def dequantize_decoded(dec: DecodedInt4Linear) -> Tensor:
-    """fp32 [out, in] = signed code * scale (* second): the 4-bit branch's weight."""
+    """fp32 [out, in] = signed code * scale (* second): the 4-bit branch's weight (an fp4 linear: e2m1 code *
+    e4m3 micro-scale * second)."""
+    from .svdq_fp4 import DecodedFp4Linear, dequantize_fp4_decoded
+
+    if isinstance(dec, DecodedFp4Linear):
+        return dequantize_fp4_decoded(dec)
     c = dec.codes.to(torch.int16)
     c = torch.where(c >= 8, c - 16, c).float()
     w = (c.reshape(dec.out_features, -1, GROUP) * dec.scales.float().unsqueeze(-1)).reshape(dec.out_features, -1)
@@ -382,12 +389,18 @@ def fold_decoded(dec: DecodedInt4Linear, *, compute_dtype=torch.bfloat16, device
     return lin
 
 
-def build_module(dec: DecodedInt4Linear, *, device: Any = "cuda", lane: Optional[str] = None) -> nn.Module:
+def build_module(dec: DecodedInt4Linear, *, device: Any = "cuda", lane: Optional[str] = None,
+                 fp4_mode: Optional[str] = None) -> nn.Module:
     """The device module for one decoded linear: ``SvdqW4A4Linear`` in the int4 lane when the kernel contract
     holds, else the folded dense Linear. ``lane`` None takes the process's qualified lane
-    (``qualify.resolve_lane``; the reference decides its mode once, ``models/svdq_native.py:283-286``)."""
+    (``qualify.resolve_lane``; the reference decides its mode once, ``models/svdq_native.py:283-286``). An fp4
+    linear goes by ``fp4_mode`` (``svdq_fp4.build_fp4_module``)."""
     from .qualify import resolve_lane
     from .svdq import build_svdq_w4a4_linear, fused_shape_supported
+    from .svdq_fp4 import DecodedFp4Linear, build_fp4_module
+
+    if isinstance(dec, DecodedFp4Linear):
+        return build_fp4_module(dec, device=device, mode=fp4_mode)
 
     if resolve_lane(lane) != "int4" or not fused_shape_supported(dec.out_features, dec.in_features, dec.rank):
         return fold_decoded(dec, device=device)
@@ -448,13 +461,15 @@ def plan_targets(model: nn.Module, prefix: str) -> tuple[tuple[str, int], ...]:
 
 
 def swap_svdq_linears(model: nn.Module, decoded: Dict[str, DecodedInt4Linear], *, device: Any = "cuda",
-                      lane: Optional[str] = None) -> dict:
-    """Install the checkpoint's int4 linears in ``model`` (the role of the reference's ``swap_svdq_linears``,
+                      lane: Optional[str] = None, fp4_mode: Optional[str] = None) -> dict:
+    """Install the checkpoint's svdq linears in ``model`` (the role of the reference's ``swap_svdq_linears``,
     ``models/svdq_native.py:270-321``): fused projections are split in the decoded domain, every piece must
-    match the shape of the Linear it replaces, and each becomes ``SvdqW4A4Linear`` in the int4 lane (the
-    process's qualified lane unless ``lane`` says otherwise) or a folded dense Linear. Returns counts and the
-    lane used."""
+    match the shape of the Linear it replaces, and each int4 piece becomes ``SvdqW4A4Linear`` in the int4 lane
+    (the process's qualified lane unless ``lane`` says otherwise) or a folded dense Linear; each fp4 piece
+    becomes ``SvdqFp4Linear`` in the blockwise ``fp4_mode`` or a folded Linear. Returns counts and the modes
+    used."""
     from .qualify import resolve_lane
+    from .svdq_fp4 import SvdqFp4Linear, resolve_fp4_mode
 
     index = _linear_index(model)
     name = type(model).__name__
@@ -469,14 +484,17 @@ def swap_svdq_linears(model: nn.Module, decoded: Dict[str, DecodedInt4Linear], *
                                       f"{piece.in_features}], the model's nn.Linear is [{t.out_features}, "
                                       f"{t.in_features}]")
             plan.append((t, piece))
-    chosen = resolve_lane(lane)
-    counts: dict = {"prefixes": len(decoded), "linears": len(plan), "int4": 0, "dense": 0, "lane": chosen}
+    chosen, fp4_chosen = resolve_lane(lane), resolve_fp4_mode(fp4_mode)
+    counts: dict = {"prefixes": len(decoded), "linears": len(plan), "int4": 0, "blockwise": 0, "dense": 0,
+                    "lane": chosen, "fp4_mode": fp4_chosen}
     for t, piece in plan:
-        new = build_module(piece, device=device, lane=chosen)
-        counts["dense" if isinstance(new, nn.Linear) else "int4"] += 1
+        new = build_module(piece, device=device, lane=chosen, fp4_mode=fp4_chosen)
+        kind = "dense" if isinstance(new, nn.Linear) else "blockwise" if isinstance(new, SvdqFp4Linear) else "int4"
+        counts[kind] += 1
         _replace(model, t.path, new)
-    logger.info("svdq int4 swap (%s lane): %d checkpoint linears -> %d modules (%d int4, %d dense)", chosen,
-                counts["prefixes"], counts["linears"], counts["int4"], counts["dense"])
+    logger.info("svdq swap (int4 lane %s, fp4 mode %s): %d checkpoint linears -> %d modules (%d int4, %d fp4 "
+                "blockwise, %d dense)", chosen, fp4_chosen, counts["prefixes"], counts["linears"], counts["int4"],
+                counts["blockwise"], counts["dense"])
     return counts
 
 
@@ -521,17 +539,22 @@ def _group_by_prefix(names) -> dict[str, list[str]]:
     return groups
 
 
-def load_svdq_int4_checkpoint(path, model: nn.Module, *, model_class: str = "",
-                              adanorm_splits: Optional[Dict[str, int]] = None, device: Any = "cuda",
-                              lane: Optional[str] = None, lowrank_quant: Optional[str] = "bf16") -> dict:
-    """Read an int4 svdq safetensors file into ``model`` (a skeleton whose module names match the
-    checkpoint's): int4 linears swapped for ``SvdqW4A4Linear`` (fused projections split), AWQ modulation
-    linears for ``AwqPackedLinear``, every other tensor copied into the parameter / buffer of that name."""
+def load_svdq_checkpoint(path, model: nn.Module, *, model_class: str = "",
+                         adanorm_splits: Optional[Dict[str, int]] = None, device: Any = "cuda",
+                         lane: Optional[str] = None, lowrank_quant: Optional[str] = "bf16",
+                         fp4_mode: Optional[str] = None, precision: Optional[str] = None) -> dict:
+    """Read an svdq safetensors file into ``model`` (a skeleton whose module names match the checkpoint's;
+    ``load_svdq_native_denoiser``, ``models/svdq_native.py:366-467``): int4 linears swapped for
+    ``SvdqW4A4Linear`` and fp4 linears for ``SvdqFp4Linear`` (or folded Linears, per lane / mode; fused
+    projections split), AWQ modulation linears for ``AwqPackedLinear``, every other tensor copied into the
+    parameter / buffer of that name. ``precision`` ("int4" / "fp4"), when given, is the artifact's declared
+    weight precision, and every linear must be stored in it."""
     from safetensors import safe_open
 
     from .awq import is_awq_linear
+    from .svdq_fp4 import decode_fp4_linear, is_fp4_svdq_linear
 
-    counts = {"int4_prefixes": 0, "awq": 0, "plain": 0}
+    counts = {"int4_prefixes": 0, "fp4_prefixes": 0, "awq": 0, "plain": 0}
     decoded: Dict[str, DecodedInt4Linear] = {}
     awq_layers: Dict[str, dict] = {}
     plain: Dict[str, Tensor] = {}
@@ -542,15 +565,21 @@ def load_svdq_int4_checkpoint(path, model: nn.Module, *, model_class: str = "",
                 awq_layers[prefix] = tensors
             elif "qweight" in tensors:
                 targets = _resolve_targets(_linear_index(model), prefix, type(model).__name__)
-                decoded[prefix] = decode_int4_linear(tensors, sum(t.out_features for t in targets),
-                                                     targets[0].in_features, lowrank_quant=lowrank_quant)
+                stored = "fp4" if is_fp4_svdq_linear(tensors) else "int4"
+                if precision is not None and stored != precision:
+                    raise SvdqLayoutError(f"{prefix!r} is stored as svdq-{stored} in an artifact that declares "
+                                          f"svdq-{precision}")
+                decode = decode_fp4_linear if stored == "fp4" else decode_int4_linear
+                decoded[prefix] = decode(tensors, sum(t.out_features for t in targets), targets[0].in_features,
+                                         lowrank_quant=lowrank_quant)
             else:
                 for leaf, t in tensors.items():
                     plain[f"{prefix}.{leaf}" if prefix else leaf] = t
     counts["awq"] = swap_awq_linears(model, awq_layers, model_class=model_class, adanorm_splits=adanorm_splits,
                                      device=device)
-    counts.update(swap_svdq_linears(model, decoded, device=device, lane=lane))
-    counts["int4_prefixes"] = len(decoded)
+    counts.update(swap_svdq_linears(model, decoded, device=device, lane=lane, fp4_mode=fp4_mode))
+    counts["fp4_prefixes"] = sum(1 for d in decoded.values() if not isinstance(d, DecodedInt4Linear))
+    counts["int4_prefixes"] = len(decoded) - counts["fp4_prefixes"]
     state = dict(model.named_parameters())
     state.update(dict(model.named_buffers()))
     with torch.no_grad():
@@ -574,10 +603,14 @@ def load_svdq_int4_checkpoint(path, model: nn.Module, *, model_class: str = "",
     return counts
 
 
+load_svdq_int4_checkpoint = load_svdq_checkpoint   # the name callers of the int4-only loader use
+
+
 __all__ = [
     "DecodedInt4Linear", "LOWRANK_QUANT_KEY", "LOWRANK_SCHEMES", "SvdqLayoutError", "SwapTarget",
     "adanorm_splits_for", "dequantize_lowrank_factor", "quantize_lowrank_factor", "build_module", "decode_int4_linear",
-    "dequantize_decoded", "fold_decoded", "is_int4_svdq_linear", "load_svdq_int4_checkpoint", "pack_group_scales",
+    "dequantize_decoded", "fold_decoded", "is_int4_svdq_linear", "load_svdq_checkpoint", "load_svdq_int4_checkpoint",
+    "pack_group_scales",
     "pack_lowrank", "pack_qweight", "pack_vector", "plan_targets", "split_decoded", "swap_awq_linears",
     "swap_svdq_linears", "unpack_group_scales", "unpack_lowrank", "unpack_qweight", "unpack_vector",
 ]

@@ -87,6 +87,59 @@ def w8a8_layer(n: int, k: int, *, bias: bool = True, std: float = 0.02, seed_off
     return W8A8Layer(w, q, s, b)
 
 
+@dataclass
+class SvdqFp4Layer:
+    """One synthetic linear in nunchaku's svdq fp4 packaging: ``stored`` holds the file's tensors, ``w`` the
+    fp32 [N, K] weight they approximate and ``bias`` the bf16 bias."""
+    stored: dict
+    w: Tensor
+    bias: Optional[Tensor]
+
+
+def svdq_fp4_layer(n: int, k: int, rank: int, *, per_channel: bool = True, smooth: bool = True,
+                   bias: bool = True, std: float = 0.02, seed_offset: int = 0) -> SvdqFp4Layer:
+    """An exporter's output for the weight W = (R + up @ down) / s: residual R ~ N(0, std) [N, K], low-rank
+    factors up ~ N(0, std) [N, rank] and down ~ N(0, rank^-1/2) [rank, K] (bf16; the branch is as large as the
+    residual, as SVDQuant's is), smoothing s. The file stores proj_down = down / s (the exporter bakes the
+    smoothing in), the second scale bf16(max|R| / (6 * 448)) per row or per tensor, e4m3 block scales
+    clamp(max|R_block| / (6 * second), 2^-9, 448) and the e2m1 codes of R / (scale * second), every tensor
+    packed as the file stores it; ``w`` is W in fp32."""
+    from .nvfp4 import _cast_e2m1
+    from .svdq_checkpoint import pack_lowrank, pack_qweight, pack_vector
+    from .svdq_fp4 import BLOCK, pack_micro_scales
+
+    so = seed_offset
+    resid = normal((n, k), std, SEED_W + so)
+    s = smooth_factor(k, SEED_SMOOTH + so) if smooth else torch.ones(k, dtype=torch.bfloat16)
+    w = resid.clone()
+    stored: dict = {}
+    if rank:
+        down = normal((rank, k), rank ** -0.5, SEED_L1 + so, torch.bfloat16)
+        up = normal((n, rank), std, SEED_L2 + so, torch.bfloat16)
+        w = w + up.float() @ down.float()
+        stored["proj_down"] = pack_lowrank((down.float() / s.float().reshape(1, -1)).to(torch.bfloat16).t()
+                                           .contiguous(), down=True)
+        stored["proj_up"] = pack_lowrank(up, down=False)
+    w = w / s.float().reshape(1, -1)
+    amax = resid.abs().amax(dim=1, keepdim=True) if per_channel else resid.abs().amax().reshape(1, 1)
+    second = (amax / (6.0 * 448.0)).clamp(min=1e-8).to(torch.bfloat16).float()
+    blocks = resid.reshape(n, k // BLOCK, BLOCK)
+    bs = (blocks.abs().amax(dim=-1) / (6.0 * second)).clamp(2.0 ** -9, 448.0).to(torch.float8_e4m3fn)
+    codes = _cast_e2m1((blocks / (bs.float().unsqueeze(-1) * second.unsqueeze(-1))).reshape(n, k))
+    stored["qweight"] = pack_qweight(codes)
+    stored["wscales"] = pack_micro_scales(bs)
+    if per_channel:
+        stored["wcscales"] = pack_vector(second.reshape(-1).to(torch.bfloat16), n)
+    else:
+        stored["wtscale"] = second.reshape(1).to(torch.bfloat16)
+    if smooth:
+        stored["smooth_factor"] = pack_vector(s, k)
+    b = normal((n,), std, SEED_BIAS + so, torch.bfloat16) if bias else None
+    if b is not None:
+        stored["bias"] = pack_vector(b, n)
+    return SvdqFp4Layer(stored, w, b)
+
+
 # BASELINE configs
 C0 = dict(m=256, k=3072, n=3072, outlier_frac=0.01, outlier_scale=20.0)
 C1 = dict(m=4608, k=3072, n=3072, rank=32, outlier_frac=0.005, outlier_scale=30.0)

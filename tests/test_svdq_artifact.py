@@ -95,8 +95,10 @@ def test_servability(tmp_path):
     base = dict(component="", file=tmp_path / "x.safetensors", model_class="NunchakuX", rank=32)
     A.check_svdq_servable(A.SvdqArtifact(precision="int4", lowrank_quant=None, **base))
     A.check_svdq_servable(A.SvdqArtifact(precision="int4", lowrank_quant="fp8_e4m3", **base))
-    with pytest.raises(A.SvdqPrecisionUnsupported, match="svdq-fp4"):
-        A.check_svdq_servable(A.SvdqArtifact(precision="fp4", lowrank_quant=None, **base))
+    A.check_svdq_servable(A.SvdqArtifact(precision="fp4", lowrank_quant=None, **base))
+    A.check_svdq_servable(A.SvdqArtifact(precision="fp4", lowrank_quant="int8", **base))
+    with pytest.raises(A.SvdqPrecisionUnsupported, match="svdq-int2"):
+        A.check_svdq_servable(A.SvdqArtifact(precision="int2", lowrank_quant=None, **base))
     with pytest.raises(A.SvdqArtifactError, match="lowrank_quant"):
         A.check_svdq_servable(A.SvdqArtifact(precision="int4", lowrank_quant="int4", **base))
     with pytest.raises(A.SvdqArtifactError, match="no svdq checkpoint"):

@@ -239,7 +239,8 @@ def test_swap_follows_the_dense_lane(monkeypatch):
     model = _skeleton(d)
     decoded = _decoded_qkv_and_out(d)
     counts = C.swap_svdq_linears(model, decoded, device="cpu")
-    assert counts == {"prefixes": 2, "linears": 4, "int4": 0, "dense": 4, "lane": "dense"}
+    assert counts == {"prefixes": 2, "linears": 4, "int4": 0, "blockwise": 0, "dense": 4, "lane": "dense",
+                      "fp4_mode": "dense"}
     assert len(calls) == 1
     attn = model.blocks[0].attn
     for mod in (attn.to_q, attn.to_k, attn.to_v, attn.to_out[0]):
