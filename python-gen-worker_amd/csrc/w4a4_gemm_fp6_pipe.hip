@@ -178,22 +178,23 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_pipe_kernel(
   // operand registers: activation operands (block rows) and their stage scales, weight operands (block columns)
   // and theirs (lanes 32..63 hold zero weight scales: K slots 4..7 of the S MFMA)
   v8i xo[NA], wo[NB];
-  // (activation row's scale of group g in its half, 0): the S MFMA's B operand per group; (the stage's two
-  // weight group scales, 0): its A operand. The .y halves (K slots 2..3, zero) are set here and never
-  // written again: the reads below refresh .x only, and the scheduling pins pass the registers through.
-  uint2 xsel[NA][GS], ws[NB];
+  // The records' scale dwords as read: an activation row's two group scales (masked to group g's half when a
+  // step forms the S MFMA's B operand, so the LDS read is waited for there, groups later, not right after the
+  // read) and the stage's two weight group scales (the A operand; lanes 32..63 read the record's four zero
+  // bytes instead: K slots 4..7 of the weight side are zero).
+  uint32_t xsc[NA], wsc[NB];
 #pragma unroll
-  for (int a = 0; a < NA; ++a) xsel[a][0] = xsel[a][1] = make_uint2(0u, 0u);
+  for (int a = 0; a < NA; ++a) xsc[a] = 0u;
 #pragma unroll
-  for (int b = 0; b < NB; ++b) ws[b] = make_uint2(0u, 0u);
+  for (int b = 0; b < NB; ++b) wsc[b] = 0u;
   auto row_of = [&](int a) __attribute__((always_inline)) { return a < 2 ? 64 * wm + 32 * a : 256; };
   auto col_of = [&](int b) __attribute__((always_inline)) {
     const int c = rot + b;
     return 96 * wn + 32 * (c < 3 ? c : c - 3);
   };
   // this lane's operand rows (+ its 24-byte half of a group) in buffer 0; buffer u adds u * LDS_X / u * LDS_W.
-  // A scale read at base + OFF_SC gives lanes 32..63 bytes of the next record: they are masked to zero (the S
-  // MFMA's K slots 4..7 are zero on the weight side and must be finite on the activation side).
+  // An activation scale read at base + OFF_SC gives lanes 32..63 bytes of the next record: the masks zero them
+  // (the S MFMA's K slots 4..7 must be finite on the activation side).
   int xaddr[NA], waddr[NB];
 #pragma unroll
   for (int a = 0; a < NA; ++a) xaddr[a] = (row_of(a) + r32) * REC + 24 * h;
@@ -208,12 +209,11 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_pipe_kernel(
     wo[b] = lds_operand(g_lds + waddr[b] + u * LDS_W + gi * GB);
   };
   auto read_xs = [&](int u, int a) __attribute__((always_inline)) {
-    const uint32_t v = *(const uint32_t*)(g_lds + xaddr[a] + u * LDS_X + OFF_SC);
-    xsel[a][0].x = v & gmask0;
-    xsel[a][1].x = v & gmask1;
+    xsc[a] = *(const uint32_t*)(g_lds + xaddr[a] + u * LDS_X + OFF_SC);
   };
+  const int wsoff = OFF_SC - 20 * h;  // lanes 32..63: record bytes [100, 104), zero by the record format
   auto read_ws = [&](int u, int b) __attribute__((always_inline)) {
-    ws[b].x = *(const uint32_t*)(g_lds + waddr[b] + u * LDS_W + OFF_SC) & hmask;
+    wsc[b] = *(const uint32_t*)(g_lds + waddr[b] + wsoff + u * LDS_W);
   };
 
   uint8_t* const spare_x = g_lds + (nst % NBUF) * LDS_X;
@@ -237,9 +237,9 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_pipe_kernel(
   // and MFMAs of neighbouring steps).
   auto step = [&](int p, int gi) __attribute__((always_inline)) {
     const int a = O::A[p], b = O::B[p];
-    asm volatile("" : "+v"(xsel[a][gi]), "+v"(xo[a]), "+v"(wo[b]), "+v"(ws[b]));
-    const v4h swop = __builtin_bit_cast(v4h, ws[b]);
-    const v4h sel = __builtin_bit_cast(v4h, xsel[a][gi]);
+    asm volatile("" : "+v"(xsc[a]), "+v"(xo[a]), "+v"(wo[b]), "+v"(wsc[b]));
+    const v4h swop = __builtin_bit_cast(v4h, make_uint2(wsc[b], 0u));
+    const v4h sel = __builtin_bit_cast(v4h, make_uint2(xsc[a] & (gi ? gmask1 : gmask0), 0u));
     if constexpr (C::PIPE) {
       const int prev = p == 0 ? NBLK - 1 : p - 1;
       __builtin_amdgcn_sched_barrier(0);
@@ -269,9 +269,10 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_pipe_kernel(
   // stage's buffer (group 1's codes), group 1 from the next buffer (the next stage's group 0 codes and the
   // stage's scales) after the stage's sync, which comes right before the first such read.
   auto stage = [&](int st, int cur, int nxt) __attribute__((always_inline)) {
-#pragma unroll
+    // fully unrolled (plain unroll pragmas leave the block loop rolled once the masks form in the steps)
+#pragma clang loop unroll(full)
     for (int gi = 0; gi < GS; ++gi) {
-#pragma unroll
+#pragma clang loop unroll(full)
       for (int p = 0; p < NBLK; ++p) {
         step(p, gi);
         if (gi == 1 && p == O::first_refill()) sync(st, cur);
