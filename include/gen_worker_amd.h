@@ -77,6 +77,20 @@ const char* gwa_build_info(void);
  * csrc/cozy_kernels/probe.cu:15-16,25. */
 const char* gwa_last_error(void);
 
+/* Debug build only (libgen_worker_amd_debug.so, compiled with GWA_DEBUG; no
+ * reference counterpart: the survey's debug build with bounds checks). Its
+ * kernels check the global accesses no hardware range check covers or whose
+ * silent drop would hide a mistake — the fp6 GEMMs' 1 KB record copies at
+ * scalar offsets (records + GWA_FP6_RECORD_SLACK), kernel 1's record stores,
+ * the GEMMs' output stores, the W8A8 copies' K offsets — and a failed check
+ * redirects or drops that access and is recorded. This call synchronizes the
+ * device, then returns the OR of the sites' bits (bit s = site s of
+ * GwaDbgSite in csrc/gwa_common.h: 0/1 activation/weight record copy, 2 fp6
+ * output, 3 kernel-1 record, 4 W8A8 copy, 5 W8A8 output) and the first
+ * failure (site << 56 | workgroup << 32 | byte offset); clear != 0 resets
+ * them. The release library returns GWA_ERR_INVALID. */
+int gwa_debug_violations(uint32_t* bits, uint64_t* first, int clear);
+
 /* out[i] = in[i] + 1 for float32 [n]. The extension probe
  * cozy_kernels::probe_add_one, csrc/cozy_kernels/probe.cu:9-27; used by the
  * load-and-probe gate of models/native_kernels.py:120-143. */

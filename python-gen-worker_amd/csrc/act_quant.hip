@@ -398,10 +398,14 @@ __global__ __launch_bounds__(Q6_THREADS) void svdq_quant_fp6_kernel(
     // ---- record (stage st, row grow): bytes [24c, 24c + 24) hold this half-group; 96 + 2 g the scale, and
     // the odd lanes zero the record's unused bytes 100..103 (the GEMM reads bytes 96..103 as one operand pair)
     const uint32_t rec = (uint32_t)(((int64_t)st * M + grow) * GWA_FP6_REC);
-    buf_store16((v4i){(int)pk[0], (int)pk[1], (int)pk[2], (int)pk[3]}, qbuf, row_ok ? rec + 24u * c : kOOB);
-    buf_store8(make_uint2(pk[4], pk[5]), qbuf, row_ok ? rec + 24u * c + 16u : kOOB);
+    // the record lies inside the [S, M, 104] buffer (a row past M stores nothing)
+    const bool rec_ok = GWA_DCHECK(!row_ok || (int64_t)rec + GWA_FP6_REC <= (int64_t)S * M * GWA_FP6_REC,
+                                   kDbgQuantRec, rec);
+    buf_store16((v4i){(int)pk[0], (int)pk[1], (int)pk[2], (int)pk[3]}, qbuf,
+                row_ok && rec_ok ? rec + 24u * c : kOOB);
+    buf_store8(make_uint2(pk[4], pk[5]), qbuf, row_ok && rec_ok ? rec + 24u * c + 16u : kOOB);
     buf_store2((c & 1) ? (uint16_t)0 : sh, qbuf,
-               row_ok ? rec + 96u + (uint32_t)(c & 2) + 4u * (uint32_t)(c & 1) : kOOB);
+               row_ok && rec_ok ? rec + 96u + (uint32_t)(c & 2) + 4u * (uint32_t)(c & 1) : kOOB);
 
     // ---- la += x[rows, stage] @ proj_down[stage, :]
     if constexpr (RB > 0) {

@@ -138,6 +138,56 @@ __device__ __forceinline__ void buf_store2(uint16_t v, rsrc_t r, uint32_t off) {
 constexpr uint32_t kOOB = 0x80000000u;  // an offset past every buffer this library builds (all < 2 GiB)
 
 // ---------------------------------------------------------------------------
+// Debug build (GWA_DEBUG): bounds checks on the global accesses whose range no hardware check covers or
+// whose silent drop would hide a mistake (direct-to-LDS copies at scalar offsets; record and output
+// stores at computed offsets). A failed check sets its site's bit in this translation unit's violation word,
+// keeps the first failure's site, workgroup and offset, and the access is redirected or skipped: nothing
+// traps and no access leaves its buffer. gwa_debug_violations (gwa_runtime.hip) ORs every translation
+// unit's word. Release builds compile the checks to nothing.
+// ---------------------------------------------------------------------------
+enum GwaDbgSite {
+  kDbgFp6CopyA = 0,   // fp6 GEMM: an activation-record copy run past its buffer + slack
+  kDbgFp6CopyW = 1,   // fp6 GEMM: a weight-record copy run past its buffer + slack
+  kDbgFp6Out = 2,     // fp6 GEMM: an output store past the [M, N] output
+  kDbgQuantRec = 3,   // kernel 1: a record store past the record buffer
+  kDbgW8Copy = 4,     // W8A8 GEMM: a copy run past the operand rows' K bytes
+  kDbgW8Out = 5,      // W8A8 GEMM: an output store past the [M, N] output
+};
+#ifdef GWA_DEBUG
+int gwa_dbg_register(int (*reader)(uint32_t* bits, uint64_t* first, int clear));
+namespace {
+__device__ uint32_t g_gwa_dbg_bits;   // bit s: site s failed
+__device__ uint64_t g_gwa_dbg_first;  // site << 56 | workgroup << 32 | offset of the first failure seen
+int gwa_dbg_read_tu(uint32_t* bits, uint64_t* first, int clear) {
+  uint32_t b = 0;
+  uint64_t f = 0;
+  if (hipMemcpyFromSymbol(&b, HIP_SYMBOL(g_gwa_dbg_bits), sizeof b) != hipSuccess) return GWA_ERR_HIP;
+  if (hipMemcpyFromSymbol(&f, HIP_SYMBOL(g_gwa_dbg_first), sizeof f) != hipSuccess) return GWA_ERR_HIP;
+  *bits |= b;
+  if (*first == 0) *first = f;
+  if (clear) {
+    const uint32_t zb = 0;
+    const uint64_t zf = 0;
+    if (hipMemcpyToSymbol(HIP_SYMBOL(g_gwa_dbg_bits), &zb, sizeof zb) != hipSuccess) return GWA_ERR_HIP;
+    if (hipMemcpyToSymbol(HIP_SYMBOL(g_gwa_dbg_first), &zf, sizeof zf) != hipSuccess) return GWA_ERR_HIP;
+  }
+  return GWA_OK;
+}
+[[maybe_unused]] const int g_gwa_dbg_registered = gwa_dbg_register(gwa_dbg_read_tu);
+}  // namespace
+__device__ __forceinline__ bool gwa_dcheck(bool ok, int site, uint32_t off) {
+  if (!ok) {
+    const uint64_t rec = ((uint64_t)site << 56) | ((uint64_t)(blockIdx.x & 0xFFFFFFu) << 32) | off;
+    if (atomicOr(&g_gwa_dbg_bits, 1u << site) == 0u) atomicCAS((unsigned long long*)&g_gwa_dbg_first, 0ull, rec);
+  }
+  return ok;
+}
+#define GWA_DCHECK(ok, site, off) gwa_dcheck((ok), (site), (uint32_t)(off))
+#else
+#define GWA_DCHECK(ok, site, off) true
+#endif
+
+// ---------------------------------------------------------------------------
 // GEMM tile order
 // ---------------------------------------------------------------------------
 constexpr int kXcds = 8;  // MI355X: workgroup i runs on XCD i % 8

@@ -38,6 +38,43 @@ extern "C" const char* gwa_build_info(void) {
 extern "C" const char* gwa_last_error(void) { return g_last_error; }
 
 // ---------------------------------------------------------------------------
+// debug build: every translation unit's violation word (gwa_common.h)
+// ---------------------------------------------------------------------------
+#ifdef GWA_DEBUG
+namespace {
+constexpr int kDbgMaxTus = 32;
+int (*g_dbg_readers[kDbgMaxTus])(uint32_t*, uint64_t*, int);
+int g_dbg_count = 0;
+}  // namespace
+
+// called from static initialisers (one per translation unit, before any entry point runs)
+int gwa_dbg_register(int (*reader)(uint32_t*, uint64_t*, int)) {
+  if (g_dbg_count < kDbgMaxTus) g_dbg_readers[g_dbg_count++] = reader;
+  return g_dbg_count;
+}
+#endif
+
+extern "C" int gwa_debug_violations(uint32_t* bits, uint64_t* first, int clear) {
+#ifdef GWA_DEBUG
+  GWA_REQUIRE(bits && first, "debug_violations: null pointer");
+  *bits = 0;
+  *first = 0;
+  hipError_t e = hipDeviceSynchronize();
+  if (e != hipSuccess) return gwa_set_error(GWA_ERR_HIP, "debug_violations: %s", hipGetErrorString(e));
+  for (int i = 0; i < g_dbg_count; ++i) {
+    const int rc = g_dbg_readers[i](bits, first, clear);
+    if (rc != GWA_OK) return gwa_set_error(rc, "debug_violations: reading a violation word failed");
+  }
+  return GWA_OK;
+#else
+  (void)bits;
+  (void)first;
+  (void)clear;
+  return gwa_set_error(GWA_ERR_INVALID, "debug_violations: not a debug build (compile with GWA_DEBUG)");
+#endif
+}
+
+// ---------------------------------------------------------------------------
 // probe: out = in + 1
 // ---------------------------------------------------------------------------
 __global__ void gwa_add_one_kernel(const float* __restrict__ in, float* __restrict__ out, int64_t n) {

@@ -124,6 +124,8 @@ __global__ __launch_bounds__(NTHREADS, (TM == 64 ? 4 : 1)) void w4a4_gemm_fp6_ke
   // which in the last stage is the 1 KB of slack every record buffer carries.
   const uint32_t dvo = 16u * (uint32_t)lane;
   const uint32_t x_valid = (uint32_t)(M - m0) * REC, w_valid = (uint32_t)(N - n0) * REC;
+  [[maybe_unused]] const uint32_t x_bytes = (uint32_t)((int64_t)nst * M * REC);
+  [[maybe_unused]] const uint32_t w_bytes = (uint32_t)((int64_t)nst * N * REC);
   auto issue = [&](uint8_t* stage, int st) __attribute__((always_inline)) {
     const uint32_t xs = (uint32_t)(((int64_t)st * M + m0) * REC);
     const uint32_t ws = (uint32_t)(((int64_t)st * N + n0) * REC);
@@ -135,7 +137,9 @@ __global__ __launch_bounds__(NTHREADS, (TM == 64 ? 4 : 1)) void w4a4_gemm_fp6_ke
       // a run that starts past the tile's last real row re-reads the stage's first run (its rows' results are
       // never stored); a run that straddles it reads up to 1 KB past it: the record buffers' slack
       const uint32_t r0 = (uint32_t)((isx ? q : q - C::DMA_X) * 1024);
-      const uint32_t soff = (isx ? xs : ws) + (r0 < (isx ? x_valid : w_valid) ? r0 : 0u);
+      uint32_t soff = (isx ? xs : ws) + (r0 < (isx ? x_valid : w_valid) ? r0 : 0u);
+      // the run [soff, soff + 1 KB) stays within the records plus their 1 KB slack
+      if (!GWA_DCHECK(soff <= (isx ? x_bytes : w_bytes), isx ? kDbgFp6CopyA : kDbgFp6CopyW, soff)) soff = isx ? xs : ws;
       dma16(isx ? xbuf : wbuf, (uint32_t)(uintptr_t)(stage + q * 1024), dvo, soff);
     }
   };
@@ -555,8 +559,9 @@ __global__ __launch_bounds__(NTHREADS, (TM == 64 ? 4 : 1)) void w4a4_gemm_fp6_ke
       const int row = r0 + crow;
       const uint2 lo = *(const uint2*)(ob + row * OSTR + cch * 16);
       const uint2 hi = *(const uint2*)(ob + row * OSTR + cch * 16 + 8);
-      const uint32_t off =
+      uint32_t off =
           (col_ok && m0 + row < M) ? (uint32_t)(((int64_t)(m0 + row) * N + n0 + 8 * cch) * 2) : kOOB;
+      if (!GWA_DCHECK(off == kOOB || (int64_t)off + 16 <= (int64_t)M * N * 2, kDbgFp6Out, off)) off = kOOB;
       buf_store16((v4i){(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y}, obuf, off);
     }
   }

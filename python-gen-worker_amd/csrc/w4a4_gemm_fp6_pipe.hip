@@ -114,6 +114,8 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_pipe_kernel(
   // rows do not fill whole KB) reads up to 1 KB past it: the record buffers' slack.
   const uint32_t dvo = 16u * (uint32_t)lane;
   const uint32_t x_valid = (uint32_t)(M - m0) * REC, w_valid = (uint32_t)(N - n0) * REC;
+  [[maybe_unused]] const uint32_t x_bytes = (uint32_t)((int64_t)nst * M * REC);
+  [[maybe_unused]] const uint32_t w_bytes = (uint32_t)((int64_t)nst * N * REC);
   auto issue = [&](int u, int st) __attribute__((always_inline)) {
     const uint32_t xs_ = (uint32_t)(((int64_t)st * M + m0) * REC);
     const uint32_t ws_ = (uint32_t)(((int64_t)st * N + n0) * REC);
@@ -123,7 +125,10 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_pipe_kernel(
       q = q < C::RUNS ? q : C::RUNS - 1;
       const bool isx = q < C::DMA_X;
       const uint32_t r0 = (uint32_t)((isx ? q : q - C::DMA_X) * 1024);
-      const uint32_t soff = (isx ? xs_ : ws_) + (r0 < (isx ? x_valid : w_valid) ? r0 : 0u);
+      uint32_t soff = (isx ? xs_ : ws_) + (r0 < (isx ? x_valid : w_valid) ? r0 : 0u);
+      // the run [soff, soff + 1 KB) stays within the records plus their 1 KB slack
+      if (!GWA_DCHECK(soff <= (isx ? x_bytes : w_bytes), isx ? kDbgFp6CopyA : kDbgFp6CopyW, soff))
+        soff = isx ? xs_ : ws_;
       uint8_t* dst = isx ? g_lds + u * LDS_X + q * 1024 : g_lds + OFF_W + u * LDS_W + (q - C::DMA_X) * 1024;
       dma16(isx ? xbuf : wbuf, (uint32_t)(uintptr_t)dst, dvo, soff);
     }
@@ -428,8 +433,9 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_pipe_kernel(
     const int row = i / CPR, cch = i - row * CPR;
     const uint2 lo = *(const uint2*)(ob + row * OSTR + cch * 16);
     const uint2 hi = *(const uint2*)(ob + row * OSTR + cch * 16 + 8);
-    const uint32_t off = (n0 + 8 * cch < N && m0 + row < M) ? (uint32_t)(((int64_t)(m0 + row) * N + n0 + 8 * cch) * 2)
-                                                            : kOOB;
+    uint32_t off = (n0 + 8 * cch < N && m0 + row < M) ? (uint32_t)(((int64_t)(m0 + row) * N + n0 + 8 * cch) * 2)
+                                                      : kOOB;
+    if (!GWA_DCHECK(off == kOOB || (int64_t)off + 16 <= (int64_t)M * N * 2, kDbgFp6Out, off)) off = kOOB;
     buf_store16((v4i){(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y}, obuf, off);
   }
 }

@@ -153,7 +153,9 @@ __global__ __launch_bounds__(256) void w8a8_gemm_kernel(const int8_t* __restrict
     const int row = i / CPR, c = i % CPR;
     const uint2 lo = *(const uint2*)(ob + row * OSTR + c * 16);
     const uint2 hi = *(const uint2*)(ob + row * OSTR + c * 16 + 8);
-    const uint32_t off = row < rows && 8 * c < cols ? (uint32_t)((row * N + 8 * c) * 2) : kOOB;
+    uint32_t off = row < rows && 8 * c < cols ? (uint32_t)((row * N + 8 * c) * 2) : kOOB;
+    if (!GWA_DCHECK(off == kOOB || (int64_t)off + 16 <= (int64_t)((rows - 1) * N + cols) * 2, kDbgW8Out, off))
+      off = kOOB;
     buf_store16((v4i){(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y}, obuf, off);
   }
 }
@@ -232,9 +234,12 @@ __global__ __launch_bounds__(NTHREADS, 1) void w8a8_gemm_lds_kernel(const int8_t
     ldst[j] = (uint32_t)(uintptr_t)(g_lds + (isx ? 0 : L_REG) + (q % L_RUNS) * 1024);
   }
   auto issue = [&](int u, int st) __attribute__((always_inline)) {
+    // the stage's K bytes lie inside every operand row (the lane offsets are range-checked by the hardware,
+    // the stage's scalar offset is not)
+    const uint32_t soff = GWA_DCHECK((st + 1) * L_KS <= K, kDbgW8Copy, st * L_KS) ? (uint32_t)(st * L_KS) : 0u;
 #pragma unroll
     for (int j = 0; j < L_SLOTS; ++j)
-      dma16(j < L_SLOTS / 2 ? xbuf : wbuf, ldst[j] + (uint32_t)(u * L_STAGE), voff[j], (uint32_t)(st * L_KS));
+      dma16(j < L_SLOTS / 2 ? xbuf : wbuf, ldst[j] + (uint32_t)(u * L_STAGE), voff[j], soff);
   };
 
   v16i acc[4][2];
@@ -359,7 +364,9 @@ __global__ __launch_bounds__(NTHREADS, 1) void w8a8_gemm_lds_kernel(const int8_t
     const int row = i / CPR, c = i % CPR;
     const uint2 lo = *(const uint2*)(ob + row * L_OSTR + c * 16);
     const uint2 hi = *(const uint2*)(ob + row * L_OSTR + c * 16 + 8);
-    const uint32_t off = row < rows && 8 * c < cols ? (uint32_t)((row * N + 8 * c) * 2) : kOOB;
+    uint32_t off = row < rows && 8 * c < cols ? (uint32_t)((row * N + 8 * c) * 2) : kOOB;
+    if (!GWA_DCHECK(off == kOOB || (int64_t)off + 16 <= (int64_t)((rows - 1) * N + cols) * 2, kDbgW8Out, off))
+      off = kOOB;
     buf_store16((v4i){(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y}, obuf, off);
   }
 }

@@ -72,6 +72,7 @@ _SIGNATURES: dict[str, tuple] = {
     "gwa_svdq_quant_fp6_partials": (_i64, _i64, _i64),
     "gwa_svdq_quant_fp6_la": (_vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _vp),
     "gwa_svdq_quant_fp6_la_workspace": (_i64, _i64, _i64),
+    "gwa_debug_violations": (ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(ctypes.c_uint64), _int),
     "gwa_svdq_gemm_w4a4_fp6_next_partials": (_i64, _i64),
     "gwa_svdq_gemm_w4a4_fp6_tile": (_i64, _i64),
     "gwa_svdq_gemm_w4a4_fp6_force_tile": (_int,),
@@ -114,6 +115,32 @@ def library_path() -> Path:
     if override:
         return Path(override)
     return Path(__file__).resolve().parent / LIB_NAME
+
+
+DEBUG_LIB_NAME = "libgen_worker_amd_debug.so"
+
+
+def debug_library_path() -> Path:
+    """The GWA_DEBUG build of the same sources (device-side bounds checks; ``gwa_debug_violations`` reads
+    them), built beside the library by ``build()``."""
+    return Path(__file__).resolve().parent / DEBUG_LIB_NAME
+
+
+def load_debug() -> ctypes.CDLL:
+    """Load the debug build as a second, independent library (its own kernels and state); raises
+    :class:`NativeUnavailable` when it is not built."""
+    path = debug_library_path()
+    if not path.exists():
+        raise NativeUnavailable(f"{path} does not exist: `python -m gen_worker_amd.build` builds it")
+    import torch  # noqa: F401  (the HIP runtime torch loaded)
+    lib = ctypes.CDLL(str(path))
+    for name, argtypes in _SIGNATURES.items():
+        fn = getattr(lib, name, None)
+        if fn is None:
+            raise NativeUnavailable(f"{path} does not export {name}")
+        fn.argtypes = list(argtypes)
+        fn.restype = _RESTYPES.get(name, ctypes.c_int)
+    return lib
 
 
 def load() -> ctypes.CDLL:

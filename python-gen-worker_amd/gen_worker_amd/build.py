@@ -20,6 +20,8 @@ INCLUDE = PKG_DIR.parent.parent / "include"
 BUILD_DIR = PKG_DIR.parent / "_build"
 LIB_NAME = "libgen_worker_amd.so"
 LIB_PATH = PKG_DIR / LIB_NAME
+DEBUG_LIB_NAME = "libgen_worker_amd_debug.so"
+DEBUG_LIB_PATH = PKG_DIR / DEBUG_LIB_NAME
 ARCH = "gfx950"
 
 SOURCES = ("gwa_runtime.hip", "act_quant.hip", "w4a4_gemm.hip", "w4a4_gemm_fp6.hip", "w4a4_gemm_fp6_pipe.hip",
@@ -52,29 +54,41 @@ def _compile(src: Path, obj: Path, extra: list[str]) -> None:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stderr[-6000:]}")
 
 
-def build(verbose: bool = False, jobs: int | None = None) -> Path:
-    """Compile every HIP source for gfx950 and link the shared library; returns its path."""
-    BUILD_DIR.mkdir(parents=True, exist_ok=True)
-    desc = f'-DGWA_BUILD_DESC="archs={ARCH}"'
-    objs = []
-    jobs = jobs or min(len(SOURCES), max(1, (os.cpu_count() or 2) // 2))
-    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        futs = []
-        for s in SOURCES:
-            obj = BUILD_DIR / (Path(s).stem + ".o")
-            objs.append(obj)
-            futs.append(ex.submit(_compile, CSRC / s, obj, [desc]))
-        for f in futs:
-            f.result()
-    tmp = LIB_PATH.with_suffix(".so.tmp")
+def _build_one(debug: bool, ex: cf.Executor) -> Path:
+    """Compile every source (GWA_DEBUG: the bounds-checked debug build) and link; returns the library path."""
+    out_dir = BUILD_DIR / ("debug" if debug else "release")
+    out_dir.mkdir(parents=True, exist_ok=True)
+    lib_path = DEBUG_LIB_PATH if debug else LIB_PATH
+    extra = [f'-DGWA_BUILD_DESC="archs={ARCH}{" debug" if debug else ""}"'] + (["-DGWA_DEBUG=1"] if debug else [])
+    objs = [out_dir / (Path(s).stem + ".o") for s in SOURCES]
+    for f in [ex.submit(_compile, CSRC / s, o, extra) for s, o in zip(SOURCES, objs)]:
+        f.result()
+    tmp = lib_path.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr[-4000:]}")
-    os.replace(tmp, LIB_PATH)
+    os.replace(tmp, lib_path)
+    return lib_path
+
+
+def build(verbose: bool = False, jobs: int | None = None, debug: bool = True) -> Path:
+    """Compile every HIP source for gfx950 and link the shared library; returns its path. With ``debug`` the
+    same sources are also built with GWA_DEBUG (device-side bounds checks that record violations, read with
+    ``gwa_debug_violations``) into ``libgen_worker_amd_debug.so``."""
+    jobs = jobs or max(1, (os.cpu_count() or 2) - 1)
+    # the two builds wait on compile jobs of a pool of their own, so neither can starve the other
+    with cf.ThreadPoolExecutor(max_workers=jobs) as cex, cf.ThreadPoolExecutor(max_workers=2) as bex:
+        rel = bex.submit(_build_one, False, cex)
+        dbg = bex.submit(_build_one, True, cex) if debug else None
+        path = rel.result()
+        if dbg is not None:
+            dpath = dbg.result()
+            if verbose:
+                print(f"built {dpath}", file=sys.stderr)
     if verbose:
-        print(f"built {LIB_PATH}", file=sys.stderr)
-    return LIB_PATH
+        print(f"built {path}", file=sys.stderr)
+    return path
 
 
 if __name__ == "__main__":

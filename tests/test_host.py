@@ -35,6 +35,25 @@ def test_library_exports_every_header_symbol():
     assert "gfx950" in _native.build_info()
 
 
+def test_debug_build_exports_the_header_and_the_release_build_refuses_its_query():
+    """The GWA_DEBUG build of the same sources exports the same header; only it answers
+    gwa_debug_violations (the release library refuses before touching a device)."""
+    import ctypes as C
+
+    from gen_worker_amd import _native
+
+    lib = _native.load()
+    bits, first = C.c_uint32(7), C.c_uint64(7)
+    assert lib.gwa_debug_violations(C.byref(bits), C.byref(first), 0) == 1
+    assert "not a debug build" in lib.gwa_last_error().decode()
+    if not _native.debug_library_path().exists():
+        pytest.skip("the debug library is not built (`python -m gen_worker_amd.build` builds it)")
+    dbg = _native.load_debug()
+    for s in _header_symbols():
+        assert hasattr(dbg, s), s
+    assert "debug" in dbg.gwa_build_info().decode()
+
+
 def test_library_is_a_gfx950_code_object():
     from gen_worker_amd import _native
 
