@@ -636,6 +636,95 @@ def _(x2, smooth, s2, proj_down_op6, weight, weight_scale, second, proj_up, bias
     return x2.new_empty(int(x2.shape[0]), int(weight.shape[0]), dtype=out_dtype)
 
 
+def eager_call_ok(x2: Tensor) -> bool:
+    """Whether a module forward may call a bound linear (``BoundLinearFp6``) instead of the registered op: a plain
+    CUDA tensor, eager mode (not under torch.compile, no Python dispatch or torch-function mode active, which the
+    op would pass through) and no autograd graph to record (the op has no autograd formula)."""
+    return (type(x2) is Tensor and x2.is_cuda and not torch.compiler.is_compiling()
+            and not (x2.requires_grad and torch.is_grad_enabled())
+            and not torch._C._is_torch_function_mode_enabled()
+            and torch._C._len_torch_dispatch_stack() == 0)
+
+
+class BoundLinearFp6:
+    """One fp6-lane linear's resident operands bound for eager calls: the same library entry points and
+    arguments as ``svdq_forward_fp6`` (and ``svdq_forward_gemv`` up to ``gemv_max_m`` tokens), so the output is
+    the op's bit for bit, without the dispatcher's and the per-call operand checks' host time. The operands are
+    checked once, by running both ops on a 0-row activation; a call then checks only the activation (dtype,
+    device, width; rows with an unaligned stride are copied, as the op does), allocates the output and the
+    workspace and enqueues on the current stream. The pointers are those of the tensors at binding: the owner
+    rebinds when any of them changes (``key``), and the binding holds them (``held``)."""
+
+    __slots__ = ("key", "held", "device", "k", "n", "rank", "out_dtype", "gemv_max_m", "_lin", "_gemv",
+                 "_lin_args", "_gemv_args", "_tail", "_ws_lin", "_ws_gemv", "_ws", "_dev_index")
+
+    def __init__(self, *, key: tuple, held: tuple, smooth: Optional[Tensor], proj_down_op6: Optional[Tensor],
+                 weight: Tensor,
+                 weight_scale: Tensor, weight_fp6: Tensor, second: Optional[Tensor], proj_up: Optional[Tensor],
+                 bias: Optional[Tensor], out_dtype: torch.dtype, gelu: bool, gemv_max_m: int) -> None:
+        n, k = _fp6_records_k("BoundLinearFp6", weight_fp6, "weight_fp6")
+        x0 = torch.empty(0, k, dtype=torch.bfloat16, device=weight_fp6.device)
+        svdq_forward_fp6(x0, smooth, None, proj_down_op6, weight_fp6, second, proj_up, bias, out_dtype, gelu)
+        if gemv_max_m > 0:
+            svdq_forward_gemv(x0, smooth, None, proj_down_op6, weight, weight_scale, second, proj_up, bias, out_dtype,
+                              gelu)
+        if second is not None and second.dtype != torch.float32:
+            raise SvdqOpError("BoundLinearFp6: second must be float32 (the op would convert it per call)")
+        lib = nat.load()
+        self.key = key
+        self.held = held  # the bound pointers' tensors stay allocated while the binding exists
+        self.device = weight_fp6.device
+        self._dev_index = self.device.index if self.device.index is not None else torch.cuda.current_device()
+        self.k, self.n = k, n
+        self.rank = int(proj_up.shape[1]) if proj_up is not None else 0
+        self.out_dtype = out_dtype
+        self.gemv_max_m = int(gemv_max_m)
+        self._lin = lib.gwa_svdq_w4a4_linear_fp6
+        self._gemv = lib.gwa_svdq_w4a4_linear_gemv
+        self._ws_lin = lib.gwa_svdq_w4a4_linear_fp6_workspace
+        self._ws_gemv = lib.gwa_svdq_w4a4_linear_gemv_workspace
+        self._ws: dict = {}
+        sn = 0 if second is None else int(second.numel())
+        # the arguments between the activation's (pointer, row stride) and the output pointer
+        self._lin_args = (nat.ptr(smooth), None, nat.ptr(proj_down_op6), self.rank, weight_fp6.data_ptr(),
+                          readable_bytes(weight_fp6), nat.ptr(second), sn, nat.ptr(proj_up), nat.ptr(bias))
+        self._gemv_args = (nat.ptr(smooth), None, nat.ptr(proj_down_op6), self.rank, weight.data_ptr(),
+                           weight_scale.data_ptr(), nat.ptr(second), sn, nat.ptr(proj_up), nat.ptr(bias))
+        self._tail = (_dt_code(out_dtype), nat.EPI_GELU_TANH if gelu else 0)
+
+    def workspace_bytes(self, m: int, gemv: bool) -> int:
+        ws = self._ws.get((m, gemv))
+        if ws is None:
+            ws = (max(int(self._ws_gemv(m, self.k, self.rank)), 256) if gemv
+                  else int(self._ws_lin(m, self.k, self.rank)))
+            if len(self._ws) < 256:
+                self._ws[(m, gemv)] = ws
+        return ws
+
+    def __call__(self, x2: Tensor) -> Optional[Tensor]:
+        """The linear of bf16 activations [M, K] on this device; None when ``x2`` does not fit the binding (the
+        caller then takes the op, which raises the contract error)."""
+        if x2.dtype != torch.bfloat16 or x2.dim() != 2 or x2.shape[1] != self.k or x2.device != self.device:
+            return None
+        if x2.stride(1) != 1 or x2.stride(0) % 8:
+            x2 = x2.contiguous()
+        m = int(x2.shape[0])
+        out = torch.empty((m, self.n), dtype=self.out_dtype, device=self.device)
+        if m == 0:
+            return out
+        gemv = m <= self.gemv_max_m
+        wsn = self.workspace_bytes(m, gemv)
+        ws = torch.empty(wsn, dtype=torch.uint8, device=self.device)
+        stream = torch._C._cuda_getCurrentRawStream(self._dev_index)
+        fn = self._gemv if gemv else self._lin
+        rc = fn(x2.data_ptr(), x2.stride(0), *(self._gemv_args if gemv else self._lin_args), out.data_ptr(),
+                *self._tail, m, self.n, self.k, ws.data_ptr(), wsn, stream)
+        if rc != 0:
+            name = "gwa_svdq_w4a4_linear_gemv" if gemv else "gwa_svdq_w4a4_linear_fp6"
+            raise nat.NativeError(f"{name} failed (code {rc}): {nat.load().gwa_last_error().decode(errors='replace')}")
+        return out
+
+
 def _next_records(name: str, q6: Tensor, m: int, k: int, stage_offset: int) -> int:
     """Checks a record buffer [S, m, 104] that receives stages [stage_offset, stage_offset + k/128); returns the
     byte address of the first of them."""

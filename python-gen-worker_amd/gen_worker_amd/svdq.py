@@ -174,6 +174,8 @@ class SvdqW4A4Linear(nn.Module):
         self.register_buffer("weight_fp6", None, persistent=False)
         # token counts up to this run the small-M GEMV on ``weight`` itself (set with the fp6 records)
         self._gemv_max_m = 0
+        # the fp6 lane's operands bound for eager calls (ops.BoundLinearFp6), rebuilt when any of them changes
+        self._bound: Optional[ops.BoundLinearFp6] = None
 
     def refresh_derived(self) -> None:
         """Recompute the derived buffers after ``weight`` / ``proj_down`` change (GPU only): ``proj_down``
@@ -187,6 +189,7 @@ class SvdqW4A4Linear(nn.Module):
                                   if on_gpu and fp6 else None)
         self.weight_fp6 = None
         self._gemv_max_m = 0
+        self._bound = None
         if fp6:
             self.weight_fp6 = torch.ops.cozy_gen_worker.svdq_pack_weight_fp6(self.weight, self.weight_scale)
             self._gemv_max_m = ops.gemv_max_m(self.in_features, self.rank)
@@ -198,6 +201,7 @@ class SvdqW4A4Linear(nn.Module):
         forward."""
         super()._apply(fn, recurse)
         self.weight_fp6 = None
+        self._bound = None
         if self.rank:
             self.proj_down_op = None
             self.proj_down_op6 = None
@@ -243,6 +247,10 @@ class SvdqW4A4Linear(nn.Module):
         self._ensure_derived()
         gelu = self.activation == "gelu_tanh"
         m = int(x2.shape[0])
+        if self.weight_fp6 is not None and ops.eager_call_ok(x2):
+            y = self._eager(x2, out_dtype, gelu)
+            if y is not None:
+                return y.reshape(*shape[:-1], self.out_features)
         if self.weight_fp6 is not None and 0 < m <= self._gemv_max_m:
             # a few tokens (the DiT's modulation linears): the int4 weight streamed once by the GEMV
             y = torch.ops.cozy_gen_worker.svdq_forward_gemv(
@@ -263,6 +271,23 @@ class SvdqW4A4Linear(nn.Module):
             qa, sa, self.weight, self.weight_scale, None, self.second, la, self.proj_up,
             self.bias, out_dtype, gelu)
         return y.reshape(*shape[:-1], self.out_features)
+
+    def _eager(self, x2: Tensor, out_dtype: torch.dtype, gelu: bool) -> Optional[Tensor]:
+        """The fp6 lane's forward through the bound call (the ops' entry points and arguments, no dispatcher);
+        None when ``x2`` does not fit it. The binding holds the operand tensors it was made from and is remade
+        when any operand attribute names another tensor or storage, or the output dtype, activation or GEMV
+        bound changes."""
+        pdo6 = self.proj_down_op6 if self.rank else None
+        up = self.proj_up if self.rank else None
+        ts = (self.weight_fp6, self.weight, self.weight_scale, self.smooth_factor, pdo6, self.second, up, self.bias)
+        key = (tuple(None if t is None else (id(t), t.data_ptr()) for t in ts), out_dtype, gelu, self._gemv_max_m)
+        b = self._bound
+        if b is None or b.key != key:
+            b = self._bound = ops.BoundLinearFp6(
+                key=key, held=ts, smooth=self.smooth_factor, proj_down_op6=pdo6, weight=self.weight,
+                weight_scale=self.weight_scale, weight_fp6=self.weight_fp6, second=self.second, proj_up=up,
+                bias=self.bias, out_dtype=out_dtype, gelu=gelu, gemv_max_m=self._gemv_max_m)
+        return b(x2)
 
     def extra_repr(self) -> str:
         return (f"in_features={self.in_features}, out_features={self.out_features}, rank={self.rank}, "
