@@ -1050,6 +1050,60 @@ def _(qa, weight, sa, weight_scale, bias, out_dtype):
     return qa.new_empty(int(qa.shape[0]), int(weight.shape[0]), dtype=out_dtype)
 
 
+class BoundLinearW8a8:
+    """A W8A8 linear's resident operands bound for eager calls: ``w8a8_quant`` then ``w8a8_scaled_mm`` as the
+    ops enqueue them (same entry points and arguments, so the same output bit for bit) without the dispatcher
+    and the per-call operand checks. The operands are checked once by both ops on a 0-row activation; a call
+    checks the activation (bf16, contiguous [M, K] on this device) and allocates the codes, the activation
+    scales and the output. The owner rebinds when an operand changes (``key``); the binding holds the tensors
+    whose pointers it uses (``held``)."""
+
+    __slots__ = ("key", "held", "device", "k", "n", "pertensor", "dynamic_pt", "out_dtype", "_quant", "_gemm",
+                 "_q_args", "_g_args", "_dev_index")
+
+    def __init__(self, *, key: tuple, held: tuple, weight: Tensor, weight_scale: Tensor, bias: Optional[Tensor],
+                 static: Optional[Tensor], pertensor: bool, out_dtype: torch.dtype) -> None:
+        n, k = int(weight.shape[0]), int(weight.shape[1])
+        x0 = torch.empty(0, k, dtype=torch.bfloat16, device=weight.device)
+        q0, sa0 = w8a8_quant(x0, pertensor, static)
+        w8a8_scaled_mm(q0, weight, sa0, weight_scale, bias, out_dtype)
+        lib = nat.load()
+        self.key, self.held = key, held
+        self.device = weight.device
+        self._dev_index = self.device.index if self.device.index is not None else torch.cuda.current_device()
+        self.k, self.n = k, n
+        self.pertensor = bool(pertensor)
+        self.dynamic_pt = self.pertensor and static is None   # the per-tensor amax needs a one-word workspace
+        self.out_dtype = out_dtype
+        self._quant = lib.gwa_w8a8_quant
+        self._gemm = lib.gwa_w8a8_gemm
+        self._q_args = (nat.ptr(static), int(self.pertensor))
+        self._g_args = (weight.data_ptr(), weight_scale.data_ptr(), nat.ptr(bias),
+                        _dt_code(bias.dtype) if bias is not None else 0)
+
+    def __call__(self, x2: Tensor) -> Optional[Tensor]:
+        """The linear of bf16 activations [M, K]; None when ``x2`` does not fit the binding (the caller then
+        takes the ops, which raise the contract error)."""
+        if (x2.dtype != torch.bfloat16 or x2.dim() != 2 or x2.shape[1] != self.k or x2.device != self.device
+                or not x2.is_contiguous()):
+            return None
+        m, k, dev = int(x2.shape[0]), self.k, self.device
+        q = torch.empty((m, k), dtype=torch.int8, device=dev)
+        sa = torch.empty((1 if self.pertensor else m, 1), dtype=torch.float32, device=dev)
+        ws = torch.empty(1, dtype=torch.int32, device=dev) if self.dynamic_pt else None
+        out = torch.empty((m, self.n), dtype=self.out_dtype, device=dev)
+        stream = torch._C._cuda_getCurrentRawStream(self._dev_index)
+        rc = self._quant(x2.data_ptr(), k, q.data_ptr(), sa.data_ptr(), *self._q_args, nat.ptr(ws), m, k, stream)
+        if rc == 0:
+            w, s, b, bdt = self._g_args
+            rc = self._gemm(q.data_ptr(), w, sa.data_ptr(), sa.numel(), s, b, bdt, out.data_ptr(),
+                            _dt_code(self.out_dtype), m, self.n, k, stream)
+        if rc != 0:
+            raise nat.NativeError(f"W8A8 linear failed (code {rc}): "
+                                  f"{nat.load().gwa_last_error().decode(errors='replace')}")
+        return out
+
+
 # ---------------------------------------------------------------------------
 # AWQ W4A16 (the adaLN modulation layers)
 # ---------------------------------------------------------------------------

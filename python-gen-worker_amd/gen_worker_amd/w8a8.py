@@ -78,6 +78,8 @@ class Int8ScaledLinear(nn.Module):
             self.bias = None
         self.register_buffer("lora_a", None, persistent=False)
         self.register_buffer("lora_b", None, persistent=False)
+        # the operands bound for eager calls (ops.BoundLinearW8a8), rebuilt when any of them changes
+        self._bound: Optional[ops.BoundLinearW8a8] = None
 
     def _lora_addend(self, x2: Tensor) -> Tensor:
         return (x2 @ self.lora_a.t()) @ self.lora_b.t()
@@ -88,12 +90,33 @@ class Int8ScaledLinear(nn.Module):
         if x2.dtype != torch.bfloat16:
             raise W8a8Error(f"Int8ScaledLinear expects bf16 activations, got {x2.dtype}")
         x2 = x2.contiguous()
-        xq, sa = torch.ops.cozy_gen_worker.w8a8_quant(x2, self.gemm_mode == "pertensor", self.input_scale)
-        y = torch.ops.cozy_gen_worker.w8a8_scaled_mm(xq, self.weight, sa, self.weight_scale, self.bias,
-                                                     self.compute_dtype)
+        y = self._eager(x2) if ops.eager_call_ok(x2) else None
+        if y is None:
+            xq, sa = torch.ops.cozy_gen_worker.w8a8_quant(x2, self.gemm_mode == "pertensor", self.input_scale)
+            y = torch.ops.cozy_gen_worker.w8a8_scaled_mm(xq, self.weight, sa, self.weight_scale, self.bias,
+                                                         self.compute_dtype)
         if self.lora_a is not None:
             y = y + self._lora_addend(x2)
         return y.reshape(*shape[:-1], self.out_features)
+
+    def _eager(self, x2: Tensor) -> Optional[Tensor]:
+        """The quant and the GEMM through the bound call (the ops' entry points and arguments, no dispatcher);
+        None when ``x2`` does not fit it. The binding holds the operand tensors it was made from and is remade
+        when an operand attribute names another tensor or storage, or the mode or output dtype changes."""
+        ts = (self.weight, self.weight_scale, self.bias, self.input_scale)
+        key = (tuple(None if t is None else (id(t), t.data_ptr()) for t in ts), self.gemm_mode, self.compute_dtype)
+        b = self._bound
+        if b is None or b.key != key:
+            b = self._bound = ops.BoundLinearW8a8(
+                key=key, held=ts, weight=self.weight, weight_scale=self.weight_scale, bias=self.bias,
+                static=self.input_scale, pertensor=self.gemm_mode == "pertensor", out_dtype=self.compute_dtype)
+        return b(x2)
+
+    def _apply(self, fn: Any, recurse: bool = True) -> "Int8ScaledLinear":
+        """Module moves and casts drop the eager binding (it is remade from the moved buffers)."""
+        super()._apply(fn, recurse)
+        self._bound = None
+        return self
 
     def extra_repr(self) -> str:
         return (f"in_features={self.in_features}, out_features={self.out_features}, "

@@ -1,4 +1,4 @@
-"""The fp6-lane module's eager forward through its bound call (ops.BoundLinearFp6) against the registered ops.
+"""The modules' eager forwards through their bound calls (ops.BoundLinearFp6, ops.BoundLinearW8a8) against the ops.
 
 ``SvdqW4A4Linear.forward`` in eager mode calls the library entry points of ``svdq_forward_fp6`` /
 ``svdq_forward_gemv`` directly with the operands bound once. These tests hold it to the ops bit for bit over
@@ -15,7 +15,7 @@ from torch.utils._python_dispatch import TorchDispatchMode
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
-K, N = 640, 384
+K, N = 640, 384   # K % 128 == 0 (the fp6 lane), N % 16 == 0
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -146,3 +146,55 @@ def test_dispatch_mode_takes_the_op():
         y = mod(x)
     assert any("svdq_forward_fp6" in o for o in mode.ops), mode.ops
     assert torch.equal(y.view(torch.int16), ref.view(torch.int16))
+
+
+def _w8_module(mode, static, bias_dtype, out_dtype):
+    from gen_worker_amd import synthetic
+    from gen_worker_amd.w8a8 import build_int8_linear
+
+    L = synthetic.w8a8_layer(N, K, bias=bias_dtype is not None, seed_offset=5)
+    b = L.bias.to(bias_dtype) if bias_dtype is not None else None
+    s = torch.tensor([[0.04]]) if static else None
+    return build_int8_linear(qweight=L.qweight, weight_scale=L.weight_scale, bias=b, compute_dtype=out_dtype,
+                             device=DEV, input_scale=s, gemm_mode=mode)
+
+
+def _w8_op(mod, x):
+    cg = torch.ops.cozy_gen_worker
+    q, sa = cg.w8a8_quant(x, mod.gemm_mode == "pertensor", mod.input_scale)
+    return cg.w8a8_scaled_mm(q, mod.weight, sa, mod.weight_scale, mod.bias, mod.compute_dtype)
+
+
+@pytest.mark.parametrize("mode,static,bias_dtype,out_dtype", [
+    ("rowwise", False, torch.float32, torch.bfloat16),
+    ("rowwise", True, torch.bfloat16, torch.float16),
+    ("pertensor", False, None, torch.bfloat16),
+    ("pertensor", True, torch.float16, torch.float16),
+])
+def test_w8a8_bound_forward_equals_the_ops(mode, static, bias_dtype, out_dtype):
+    mod = _w8_module(mode, static, bias_dtype, out_dtype)
+    for m in (0, 1, 77, 300):
+        x = _act(m, seed=11)
+        y = mod(x)
+        assert mod._bound is not None, "the eager forward did not take the bound call"
+        ref = _w8_op(mod, x)
+        torch.cuda.synchronize()
+        assert y.dtype == out_dtype and tuple(y.shape) == (m, N)
+        assert torch.equal(y.view(torch.int16), ref.view(torch.int16)), f"m={m}: bound call differs from the ops"
+
+
+def test_w8a8_bound_call_rebinds_on_changes():
+    mod = _w8_module("rowwise", False, torch.float32, torch.bfloat16)
+    x = _act(150, seed=11)
+    mod(x)
+    b0 = mod._bound
+    mod.gemm_mode = "pertensor"
+    y = mod(x)
+    assert mod._bound is not b0
+    assert torch.equal(y.view(torch.int16), _w8_op(mod, x).view(torch.int16))
+    with torch.no_grad():
+        mod.weight_scale.data = mod.weight_scale.data * 0.5
+    y2 = mod(x)
+    assert torch.equal(y2.view(torch.int16), _w8_op(mod, x).view(torch.int16))
+    mod.to(DEV)
+    assert mod._bound is None
