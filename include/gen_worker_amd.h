@@ -55,7 +55,11 @@ enum {
  *                   [96, 104) as one (scales, 0) operand pair)
  * (every int4 code -8..7 is an exact e3m2 value). A tile's stage of operand
  * rows is one contiguous run, and its LDS image keeps a bank-conflict-free
- * row stride. */
+ * row stride. The records cover S = ceil(K/128) stages ([K/128, rows, 104]
+ * below means [S, rows, 104]): with K % 128 == 64 the last stage is a half
+ * stage whose second group holds zero codes (scale 0 from
+ * gwa_svdq_pack_weight_fp6, kernel 1's all-zero-group scale from
+ * gwa_svdq_quant_fp6), so it adds nothing to a GEMM. */
 enum { GWA_FP6_REC = 104 };
 
 /* Readable bytes the fp6 GEMMs need past the last record of each record
@@ -138,7 +142,7 @@ int gwa_svdq_prep_proj_down(const void* proj_down, void* out, int64_t K, int64_t
  *   out    [M, N] of out_dtype (GWA_DT_BF16 or GWA_DT_F16)
  * K % 64 == 0, N % 16 == 0. This is the general path (int8 MFMA on the logical
  * two's-complement weights, any code in [-8, 7]); gwa_svdq_gemm_w4a4_fp6 is
- * the fast path (K % 128 == 0) on fp6 operand records. */
+ * the fast path (K % 64 == 0) on fp6 operand records. */
 int gwa_svdq_gemm_w4a4(const uint8_t* qa, const void* sa, const uint8_t* qw, const void* sw,
                        const float* s2, const float* second, int64_t second_numel,
                        const void* la, const void* up, int64_t rank, const void* bias,
@@ -158,7 +162,7 @@ int gwa_svdq_group_psums(const uint8_t* qa, const uint8_t* qw, int32_t* out,
  * in [-8, 7].
  *   qw   uint8 [N, K/2] logical two's-complement codes (in)
  *   sw   fp16 [N, K/64] group scales (in)
- *   qw6  uint8 [K/128, N, 104] records (out); K % 128 == 0. Allocate
+ *   qw6  uint8 [K/128, N, 104] records (out); K % 64 == 0. Allocate
  *        GWA_FP6_RECORD_SLACK bytes of slack after it (the GEMMs read up to 1 KB
  *        past and refuse a shorter buffer). */
 int gwa_svdq_pack_weight_fp6(const uint8_t* qw, const void* sw, uint8_t* qw6, int64_t N, int64_t K, void* stream);
@@ -173,7 +177,7 @@ int gwa_svdq_pack_weight_fp6(const uint8_t* qw, const void* sw, uint8_t* qw6, in
  * GWA_ERR_INVALID before any launch (operand records are copied in 1 KB runs;
  * the run holding a tile's last real row may reach past them).
  * One exact fp6 MFMA per K-group and 32x32 block. la is bf16 [M, rank], or fp32 with GWA_EPI_LA_F32 in
- * epilogue_flags (rounded to bf16 in the epilogue). K % 128 == 0,
+ * epilogue_flags (rounded to bf16 in the epilogue). K % 64 == 0,
  * N % 16 == 0. */
 int gwa_svdq_gemm_w4a4_fp6(const uint8_t* qa6, int64_t qa6_bytes, const uint8_t* qw6, int64_t qw6_bytes,
                            const float* s2, const float* second, int64_t second_numel,
@@ -207,7 +211,7 @@ int gwa_svdq_gemm_w4a4_fp6(const uint8_t* qa6, int64_t qa6_bytes, const uint8_t*
  *            gwa_svdq_prep_proj_down_fp6 order, next_rank in {0,16,32,64,128}
  * Single-level (the next layer's s2 = 1). Output dtype bf16; la may be fp32
  * (GWA_EPI_LA_F32). qa6_bytes / qw6_bytes as gwa_svdq_gemm_w4a4_fp6 checks
- * them. N % 128 == 0, K % 128 == 0. */
+ * them. N % 128 == 0, K % 64 == 0. */
 int gwa_svdq_gemm_w4a4_fp6_next(const uint8_t* qa6, int64_t qa6_bytes, const uint8_t* qw6, int64_t qw6_bytes,
                                 const float* s2, const float* second, int64_t second_numel,
                                 const void* la, const void* up, int64_t rank, const void* bias,
@@ -240,7 +244,8 @@ int gwa_svdq_gemm_w4a4_fp6_force_tile(int tile);
  * the low-rank product as fp32 partial sums (replaces
  * cozy_gen_worker::svdq_quant, models/svdq_fused.py:293-306, plus
  * `la = x2 @ proj_down`, :524):
- *   x          bf16 [M, K] rows with stride ldx (elements), K % 128 == 0
+ *   x          bf16 [M, K] rows with stride ldx (elements), K % 64 == 0 (a
+ *              half stage reads no column past K)
  *   smooth     bf16 [K] or NULL;  s2 fp32 device scalar or NULL (= 1.0)
  *   proj_down_op6  proj_down in this kernel's operand order
  *              (gwa_svdq_prep_proj_down_fp6) or NULL; rank in {0,16,32,64,128}
@@ -284,8 +289,9 @@ int gwa_svdq_la_reduce(const float* part, int64_t P, int64_t M, int64_t rank, vo
 
 /* proj_down bf16 [K, rank] -> the operand order of gwa_svdq_quant_fp6 and of
  * the next-layer epilogue of gwa_svdq_gemm_w4a4_fp6_next (done once per
- * weight; no reference counterpart). K % 128 == 0.
- *   out  bf16 [K * rank] (16-byte aligned): stage-major, element
+ * weight; no reference counterpart). K % 64 == 0.
+ *   out  bf16 [ceil(K/128) * 128 * rank] (16-byte aligned; a half stage's rows
+ *        past K are zeros): stage-major, element
  *        (((s*4 + j)*(rank/16) + b)*64 + l)*8 + e = proj_down[128s + 32(l/16) + 8j + e][16b + l%16] */
 int gwa_svdq_prep_proj_down_fp6(const void* proj_down, void* out, int64_t K, int64_t rank, void* stream);
 
@@ -317,7 +323,7 @@ int gwa_svdq_group_psums_fp6(const uint8_t* qa6, int64_t qa6_bytes, const uint8_
  *            the activation records (+ slack), the la partial slots and the
  *            bf16 la. Nothing in it needs to be initialised; it must not be
  *            reused by another call until this call's work on `stream` ends.
- * K % 128 == 0, N % 16 == 0. */
+ * K % 64 == 0, N % 16 == 0. */
 int gwa_svdq_w4a4_linear_fp6(const void* x, int64_t ldx, const void* smooth, const float* s2,
                              const void* proj_down_op6, int64_t rank, const uint8_t* qw6, int64_t qw6_bytes,
                              const float* second, int64_t second_numel, const void* proj_up,

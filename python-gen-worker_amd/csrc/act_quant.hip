@@ -274,7 +274,7 @@ __global__ __launch_bounds__(Q6_THREADS) void svdq_quant_fp6_kernel(
   __shared__ __attribute__((aligned(16))) uint8_t lds[X_OFF + Q6_WAVES * 2 * X_TASK];
 
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-  const int S = K >> 7;
+  const int S = (K + 127) >> 7;  // K % 128 == 64: the last stage's second group lies past K (read as zeros)
   const int st0 = blockIdx.y * CH;
   const int ntask = min(CH, S - st0);  // workgroup-uniform, >= 1
   const int r = lane & 15, c = lane >> 4;
@@ -293,8 +293,8 @@ __global__ __launch_bounds__(Q6_THREADS) void svdq_quant_fp6_kernel(
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int q = 4 * j + (lane >> 4), sl = lane & 15;
-      const uint32_t off =
-          row0 + q < M ? (uint32_t)(((int64_t)(row0 + q) * ldx + col + 8 * (sl ^ q)) * 2) : kOOB;
+      const int cc = col + 8 * (sl ^ q);  // columns past K (a half stage) land as zeros
+      const uint32_t off = row0 + q < M && cc < K ? (uint32_t)(((int64_t)(row0 + q) * ldx + cc) * 2) : kOOB;
       dma16_lds(xr4, (uint32_t)(uintptr_t)(xring + (t & 1) * X_TASK + j * 1024), off, 0u);
     }
   };
@@ -331,7 +331,8 @@ __global__ __launch_bounds__(Q6_THREADS) void svdq_quant_fp6_kernel(
   const bool s_role = smooth && 2 * tid < CH * 128;
   const uint32_t sv = s_role ? *(const uint32_t*)(lds + SMR_OFF + 4 * tid) : 0u;
   if (s_role) {
-    const float s0 = bf16_lo(sv), s1 = bf16_hi(sv);
+    // columns past K (K % 64 == 0: both or neither of the pair) take factor 1: their x is zero
+    const float s0 = scol < K ? bf16_lo(sv) : 1.0f, s1 = scol < K ? bf16_hi(sv) : 1.0f;
     float* rcp = (float*)(lds + RCP_OFF);
     const int i = 2 * tid;
     rcp[i] = 1.0f / s0;
@@ -463,7 +464,7 @@ __global__ __launch_bounds__(256) void prep_proj_down_fp6_kernel(const uint16_t*
                                                                  uint16_t* __restrict__ out, int K, int R) {
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int RB = R / 16;
-  if (idx >= (int64_t)(K / 128) * 4 * RB * 64) return;
+  if (idx >= (int64_t)((K + 127) / 128) * 4 * RB * 64) return;
   const int lane = (int)(idx % 64);
   const int rb = (int)((idx / 64) % RB);
   const int j = (int)((idx / (64 * RB)) % 4);
@@ -472,7 +473,7 @@ __global__ __launch_bounds__(256) void prep_proj_down_fp6_kernel(const uint16_t*
   const int k0 = st * 128 + 32 * (lane >> 4) + 8 * j;
   uint16_t v[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) v[e] = pd[(int64_t)(k0 + e) * R + col];
+  for (int e = 0; e < 8; ++e) v[e] = k0 + e < K ? pd[(int64_t)(k0 + e) * R + col] : (uint16_t)0;  // a half stage's rows past K: zero
   uint4 o;
   o.x = (uint32_t)v[0] | ((uint32_t)v[1] << 16);
   o.y = (uint32_t)v[2] | ((uint32_t)v[3] << 16);
@@ -599,13 +600,13 @@ __global__ __launch_bounds__(256) void svdq_epilogue_kernel(const uint16_t* __re
 
 extern "C" int gwa_svdq_prep_proj_down_fp6(const void* proj_down, void* out, int64_t K, int64_t rank,
                                            void* stream) {
-  GWA_REQUIRE(K > 0 && K % 128 == 0 && K < (1ll << 24), "svdq_prep_proj_down_fp6: K=%lld is not a multiple of 128",
+  GWA_REQUIRE(K > 0 && K % 64 == 0 && K < (1ll << 24), "svdq_prep_proj_down_fp6: K=%lld is not a multiple of 64",
               (long long)K);
   GWA_REQUIRE(rank == 16 || rank == 32 || rank == 64 || rank == 128,
               "svdq_prep_proj_down_fp6: rank %lld not in {16,32,64,128}", (long long)rank);
   GWA_REQUIRE(proj_down && out, "svdq_prep_proj_down_fp6: null pointer");
   GWA_REQUIRE(GWA_ALIGNED(proj_down, 2) && GWA_ALIGNED(out, 16), "svdq_prep_proj_down_fp6: out must be 16-byte aligned");
-  const int64_t total = (K / 128) * 4 * (rank / 16) * 64;
+  const int64_t total = ((K + 127) / 128) * 4 * (rank / 16) * 64;
   hipLaunchKernelGGL(prep_proj_down_fp6_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
                      (hipStream_t)stream, (const uint16_t*)proj_down, (uint16_t*)out, (int)K, (int)rank);
   return gwa_check_launch("svdq_prep_proj_down_fp6");
@@ -614,15 +615,15 @@ extern "C" int gwa_svdq_prep_proj_down_fp6(const void* proj_down, void* out, int
 // stages per workgroup of svdq_quant_fp6_kernel: as many as keep >= 256 workgroups (a workgroup's loads all
 // go out at once), with the proj_down operands of a workgroup's stages within 32 KB of LDS
 static int quant_fp6_stages_per_group(int64_t M, int64_t K, int64_t R) {
-  const int64_t S = K / 128, groups = (M + Q6_ROWS - 1) / Q6_ROWS;
+  const int64_t S = (K + 127) / 128, groups = (M + Q6_ROWS - 1) / Q6_ROWS;
   int ch = 4;
   while (ch > 1 && (groups * ((S + ch - 1) / ch) < 256 || ch * (R / 16) > 8)) ch /= 2;
   return ch;
 }
 
 extern "C" int64_t gwa_svdq_quant_fp6_partials(int64_t M, int64_t K, int64_t rank) {
-  if (M <= 0 || K <= 0 || K % 128 || rank <= 0) return 0;
-  const int64_t S = K / 128;
+  if (M <= 0 || K <= 0 || K % 64 || rank <= 0) return 0;
+  const int64_t S = (K + 127) / 128;
   const int ch = quant_fp6_stages_per_group(M, K, rank);
   return (S + ch - 1) / ch;
 }
@@ -640,7 +641,7 @@ extern "C" int gwa_svdq_la_reduce(const float* part, int64_t P, int64_t M, int64
 }
 
 extern "C" int64_t gwa_svdq_quant_fp6_la_workspace(int64_t M, int64_t K, int64_t rank) {
-  if (M <= 0 || K <= 0 || K % 128 || rank <= 0 || K >= (1ll << 24)) return 0;
+  if (M <= 0 || K <= 0 || K % 64 || rank <= 0 || K >= (1ll << 24)) return 0;
   return gwa_svdq_quant_fp6_partials(M, K, rank) * M * rank * 4;
 }
 
@@ -648,7 +649,7 @@ extern "C" int gwa_svdq_quant_fp6(const void* x, int64_t ldx, const void* smooth
                                   const void* proj_down_op6, int64_t rank, uint8_t* q6, float* la_part, int64_t M,
                                   int64_t K, void* stream) {
   const char* what = "svdq_quant_fp6";
-  GWA_REQUIRE(M >= 0 && K > 0 && K % 128 == 0, "%s: K=%lld is not a multiple of 128", what, (long long)K);
+  GWA_REQUIRE(M >= 0 && K > 0 && K % 64 == 0, "%s: K=%lld is not a multiple of 64", what, (long long)K);
   GWA_REQUIRE(ldx >= K && ldx % 8 == 0, "%s: row stride %lld must be >= K and a multiple of 8", what,
               (long long)ldx);
   GWA_REQUIRE((proj_down_op6 == nullptr) == (la_part == nullptr),
@@ -656,8 +657,9 @@ extern "C" int gwa_svdq_quant_fp6(const void* x, int64_t ldx, const void* smooth
   const int64_t R = proj_down_op6 ? rank : 0;
   GWA_REQUIRE(R == 0 || R == 16 || R == 32 || R == 64 || R == 128, "%s: rank %lld not in {0,16,32,64,128}", what,
               (long long)R);
+  const int64_t S = (K + 127) / 128;  // K % 128 == 64: a half stage, its second group zero codes
   GWA_REQUIRE(M < (1ll << 31) && K < (1ll << 24) && M * ldx * 2 < (1ll << 31) &&
-                  M * (K / 128) * GWA_FP6_REC < (1ll << 31) && (K / 128) * R * 256 < (1ll << 31),
+                  M * S * GWA_FP6_REC < (1ll << 31) && S * R * 256 < (1ll << 31),
               "%s: x and q6 must stay below 2 GiB (buffer addressing)", what);
   if (M == 0) return GWA_OK;
   GWA_REQUIRE(x && q6, "%s: null pointer", what);
@@ -665,7 +667,7 @@ extern "C" int gwa_svdq_quant_fp6(const void* x, int64_t ldx, const void* smooth
                   GWA_ALIGNED(la_part, 4) && GWA_ALIGNED(s2, 4),
               "%s: x and proj_down_op6 must be 16-byte, q6 8-byte aligned", what);
   const int rb = (int)(R / 16);
-  const int64_t S = K / 128, groups = (M + Q6_ROWS - 1) / Q6_ROWS;
+  const int64_t groups = (M + Q6_ROWS - 1) / Q6_ROWS;
   const int ch = quant_fp6_stages_per_group(M, K, R);
   const dim3 grid((unsigned)groups, (unsigned)((S + ch - 1) / ch)), block(Q6_THREADS);
   GWA_REQUIRE(groups < (1ll << 31) && grid.y < 65536u, "%s: grid too large", what);
@@ -700,7 +702,7 @@ extern "C" int gwa_svdq_quant_fp6_la(const void* x, int64_t ldx, const void* smo
                                      const void* proj_down_op6, int64_t rank, uint8_t* q6, void* la, float* la_ws,
                                      int64_t la_ws_bytes, int64_t M, int64_t K, void* stream) {
   const char* what = "svdq_quant_fp6_la";
-  GWA_REQUIRE(M >= 0 && K > 0 && K % 128 == 0, "%s: K=%lld is not a multiple of 128", what, (long long)K);
+  GWA_REQUIRE(M >= 0 && K > 0 && K % 64 == 0, "%s: K=%lld is not a multiple of 64", what, (long long)K);
   GWA_REQUIRE(rank == 16 || rank == 32 || rank == 64 || rank == 128, "%s: rank %lld not in {16,32,64,128}", what,
               (long long)rank);
   GWA_REQUIRE(M < (1ll << 31) && K < (1ll << 24), "%s: shape too large", what);

@@ -662,16 +662,17 @@ __global__ __launch_bounds__(64) void w4a4_psums_fp6_kernel(const uint8_t* __res
 __global__ __launch_bounds__(256) void pack_weight_fp6_kernel(const uint8_t* __restrict__ qw,
                                                               const uint16_t* __restrict__ sw,
                                                               uint8_t* __restrict__ qw6, int N, int K) {
-  const int G = K >> 6;
+  const int G = K >> 6, GP = 2 * ((K + 127) >> 7);  // groups, and groups of the records (a half stage: G + 1)
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= (int64_t)N * G * 2) return;
-  const int64_t row = i / (2 * G);
-  const int rem = (int)(i - row * 2 * G), g = rem >> 1, hh = rem & 1;
-  const uint32_t* src = (const uint32_t*)(qw + row * (K / 2) + g * 32 + hh * 16);
+  if (i >= (int64_t)N * GP * 2) return;
+  const int64_t row = i / (2 * GP);
+  const int rem = (int)(i - row * 2 * GP), g = rem >> 1, hh = rem & 1;
+  const bool pad = g >= G;  // the half stage's second group: zero codes, zero scale
+  const uint32_t* src = (const uint32_t*)(qw + row * (K / 2) + (pad ? 0 : g * 32 + hh * 16));
   uint64_t pc[4];
 #pragma unroll
   for (int d = 0; d < 4; ++d) {
-    const uint32_t w = src[d];
+    const uint32_t w = pad ? 0u : src[d];
     const uint32_t ev = w & 0x0F0F0F0Fu, od = (w >> 4) & 0x0F0F0F0Fu;  // codes 8d + 0,2,4,6 / 8d + 1,3,5,7
     const uint32_t c0 = __builtin_amdgcn_perm(od, ev, 0x05010400u);    // codes 8d + 0..3, one per byte
     const uint32_t c1 = __builtin_amdgcn_perm(od, ev, 0x07030602u);    // codes 8d + 4..7
@@ -686,7 +687,7 @@ __global__ __launch_bounds__(256) void pack_weight_fp6_kernel(const uint8_t* __r
   dst[4] = (uint32_t)((pc[2] >> 32) | (pc[3] << 16));
   dst[5] = (uint32_t)(pc[3] >> 16);
   if (hh == 0) {
-    *(uint16_t*)(rec + OFF_SC + (g & 1) * 2) = sw[row * G + g];
+    *(uint16_t*)(rec + OFF_SC + (g & 1) * 2) = pad ? (uint16_t)0 : sw[row * G + g];
     if ((g & 1) == 0) *(uint32_t*)(rec + OFF_SC + 4) = 0u;
   }
 }
@@ -695,12 +696,12 @@ __global__ __launch_bounds__(256) void pack_weight_fp6_kernel(const uint8_t* __r
 
 extern "C" int gwa_svdq_pack_weight_fp6(const uint8_t* qw, const void* sw, uint8_t* qw6, int64_t N, int64_t K,
                                         void* stream) {
-  GWA_REQUIRE(N > 0 && K > 0 && K % 128 == 0, "svdq_pack_weight_fp6: bad shape N=%lld K=%lld (K %% 128 == 0)",
+  GWA_REQUIRE(N > 0 && K > 0 && K % 64 == 0, "svdq_pack_weight_fp6: bad shape N=%lld K=%lld (K %% 64 == 0)",
               (long long)N, (long long)K);
   GWA_REQUIRE(N * (K / 64) * 2 < (1ll << 40) && K < (1ll << 30), "svdq_pack_weight_fp6: shape too large");
   GWA_REQUIRE(qw && sw && qw6, "svdq_pack_weight_fp6: null pointer");
   GWA_REQUIRE(GWA_ALIGNED(qw, 4) && GWA_ALIGNED(qw6, 8) && GWA_ALIGNED(sw, 2), "svdq_pack_weight_fp6: misaligned pointer");
-  const int64_t threads = N * (K / 64) * 2;
+  const int64_t threads = N * ((K + 127) / 128) * 2 * 2;  // (row, group of the records, half)
   hipLaunchKernelGGL(pack_weight_fp6_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
                      (hipStream_t)stream, qw, (const uint16_t*)sw, qw6, (int)N, (int)K);
   return gwa_check_launch("svdq_pack_weight_fp6");
@@ -824,7 +825,7 @@ int gemm_fp6(const char* what, const uint8_t* qa6, int64_t qa6_bytes, const uint
              const NextLayer& nx, void* stream) {
   GWA_REQUIRE(M >= 0 && N > 0 && K > 0, "%s: bad shape M=%lld N=%lld K=%lld", what, (long long)M, (long long)N,
               (long long)K);
-  GWA_REQUIRE(K % 128 == 0, "%s: K=%lld is not a multiple of 128", what, (long long)K);
+  GWA_REQUIRE(K % 64 == 0, "%s: K=%lld is not a multiple of 64", what, (long long)K);
   GWA_REQUIRE(N % 16 == 0, "%s: N=%lld is not a multiple of 16", what, (long long)N);
   GWA_REQUIRE(out_dtype == GWA_DT_BF16 || out_dtype == GWA_DT_F16, "%s: out_dtype %d", what, out_dtype);
   GWA_REQUIRE((la == nullptr) == (up == nullptr), "%s: la and up must both be given or both NULL", what);
@@ -836,7 +837,9 @@ int gemm_fp6(const char* what, const uint8_t* qa6, int64_t qa6_bytes, const uint
   GWA_REQUIRE((epilogue_flags & ~(GWA_EPI_GELU_TANH | GWA_EPI_LA_F32)) == 0, "%s: unknown epilogue flags 0x%x",
               what, epilogue_flags);
   const int la_f32 = (epilogue_flags & GWA_EPI_LA_F32) ? 1 : 0;
-  const int64_t nst = K / 128;
+  // K % 128 == 64: the records' last stage is a half stage whose second group holds zero codes (P = 0), so
+  // the kernels run over the padded K
+  const int64_t nst = (K + 127) / 128, Kp = nst * 128;
   // the DMA offsets of a tile's last run stay below 2^31 + 2^16
   GWA_REQUIRE(nst * (M + 288) * REC < (1ll << 31) && nst * (N + 256) * REC < (1ll << 31) && M * N * 2 < (1ll << 31) &&
                   M * R * 4 < (1ll << 31) && (N / 128) * M * REC < (1ll << 31),
@@ -864,7 +867,7 @@ int gemm_fp6(const char* what, const uint8_t* qa6, int64_t qa6_bytes, const uint
   const int64_t per_xcd = (tiles + kXcds - 1) / kXcds;
   const dim3 grid((unsigned)(per_xcd * kXcds));
   const GwaFp6Args a{qa6, qw6, s2, second, (int)(second_numel > 1), la, la_f32, (const uint16_t*)up,
-                  (const uint16_t*)bias, (uint16_t*)out, (int)M, (int)N, (int)K};
+                  (const uint16_t*)bias, (uint16_t*)out, (int)M, (int)N, (int)Kp};
   const bool gelu = epilogue_flags & GWA_EPI_GELU_TANH;
   const bool f16 = out_dtype == GWA_DT_F16;
   hipStream_t s = (hipStream_t)stream;

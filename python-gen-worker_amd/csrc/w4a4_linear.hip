@@ -28,7 +28,7 @@ struct Scratch {
 Scratch scratch_layout(int64_t M, int64_t K, int64_t R) {
   Scratch s;
   s.partial_bytes = R ? gwa_svdq_quant_fp6_la_workspace(M, K, R) : 0;
-  s.partials = align_up(M * (K / 128) * GWA_FP6_REC + kRecordSlack);
+  s.partials = align_up(M * ((K + 127) / 128) * GWA_FP6_REC + kRecordSlack);
   s.la = align_up(s.partials + s.partial_bytes);
   s.total = align_up(s.la + M * R * 2);
   return s;
@@ -36,9 +36,10 @@ Scratch scratch_layout(int64_t M, int64_t K, int64_t R) {
 
 // the weight records' readable bytes, checked before anything is enqueued (the GEMM checks them again)
 int check_weight_records(const char* what, const uint8_t* qw6, int64_t qw6_bytes, int64_t N, int64_t K) {
-  GWA_REQUIRE(qw6 != nullptr && qw6_bytes >= (K / 128) * N * GWA_FP6_REC + kRecordSlack,
+  const int64_t S = (K + 127) / 128;  // K % 128 == 64: a half stage
+  GWA_REQUIRE(qw6 != nullptr && qw6_bytes >= S * N * GWA_FP6_REC + kRecordSlack,
               "%s: qw6 has %lld readable bytes, the weight's records need %lld plus %d of slack", what,
-              (long long)qw6_bytes, (long long)((K / 128) * N * GWA_FP6_REC), GWA_FP6_RECORD_SLACK);
+              (long long)qw6_bytes, (long long)(S * N * GWA_FP6_REC), GWA_FP6_RECORD_SLACK);
   return GWA_OK;
 }
 
@@ -46,7 +47,7 @@ int linear_fp6_run(const char* what, const void* x, int64_t ldx, const void* smo
                    const void* proj_down_op6, int64_t rank, const uint8_t* qw6, int64_t qw6_bytes, const float* second,
                    int64_t second_numel, const void* proj_up, const void* bias, void* out, int out_dtype,
                    int epilogue_flags, int64_t M, int64_t N, int64_t K, uint8_t* ws, int64_t ws_bytes, void* stream) {
-  GWA_REQUIRE(M >= 0 && N > 0 && K > 0 && K % 128 == 0, "%s: bad shape M=%lld N=%lld K=%lld (K %% 128 == 0)", what,
+  GWA_REQUIRE(M >= 0 && N > 0 && K > 0 && K % 64 == 0, "%s: bad shape M=%lld N=%lld K=%lld (K %% 64 == 0)", what,
               (long long)M, (long long)N, (long long)K);
   GWA_REQUIRE((proj_down_op6 == nullptr) == (proj_up == nullptr),
               "%s: proj_down_op6 and proj_up must both be given or both be NULL", what);
@@ -124,7 +125,7 @@ extern "C" int gwa_svdq_w4a4_linear_fp6_noalloc(const void* x, int64_t ldx, cons
               "(use gwa_svdq_w4a4_linear_fp6 with a workspace, or split the rows)",
               what, (long long)M, (long long)K, (long long)rank, (long long)need, (long long)kScratchBytes);
   uint8_t* ws = nullptr;
-  if (M > 0 && N > 0 && K > 0 && K % 128 == 0) {
+  if (M > 0 && N > 0 && K > 0 && K % 64 == 0) {
     const int wrc = check_weight_records(what, qw6, qw6_bytes, N, K);  // before the scratch lookup's HIP calls
     if (wrc != GWA_OK) return wrc;
   }
@@ -139,7 +140,7 @@ extern "C" int gwa_svdq_w4a4_linear_fp6_noalloc(const void* x, int64_t ldx, cons
 extern "C" int64_t gwa_svdq_w4a4_linear_fp6_noalloc_scratch_bytes(void) { return kScratchBytes; }
 
 extern "C" int64_t gwa_svdq_w4a4_linear_fp6_workspace(int64_t M, int64_t K, int64_t rank) {
-  if (M <= 0 || K <= 0 || K % 128 || M >= (1ll << 31) || K >= (1ll << 24)) return 0;
+  if (M <= 0 || K <= 0 || K % 64 || M >= (1ll << 31) || K >= (1ll << 24)) return 0;
   if (rank != 0 && rank != 16 && rank != 32 && rank != 64 && rank != 128) return 0;
   return scratch_layout(M, K, rank).total;
 }

@@ -63,6 +63,12 @@ GROUP = 64
 FP6_STAGE = 128   # K elements per fp6 operand record
 
 
+def fp6_stages(k: int) -> int:
+    """Stages of fp6 records for K inputs (K % 64 == 0): with K % 128 == 64 the last is a half stage whose
+    second group holds zero codes."""
+    return (int(k) + FP6_STAGE - 1) // FP6_STAGE
+
+
 class SvdqOpError(ValueError):
     """Typed contract violation at the op boundary (never a silent fallback)."""
 
@@ -251,8 +257,9 @@ def _la_part_check(name: str, la_part: Optional[Tensor], proj_down_op6: Optional
     if la_part.dim() != 3 or int(la_part.shape[1]) != m or int(la_part.shape[0]) < slots:
         raise SvdqOpError(f"{name}: la_part must be [>= {slots}, {m}, rank], got {tuple(la_part.shape)}")
     r = int(la_part.shape[2])
-    if proj_down_op6.dim() != 2 or int(proj_down_op6.shape[1]) != r or int(proj_down_op6.shape[0]) < k:
-        raise SvdqOpError(f"{name}: proj_down_op6 must be [>= {k}, {r}] rows in operand order, got "
+    kp = fp6_stages(k) * FP6_STAGE
+    if proj_down_op6.dim() != 2 or int(proj_down_op6.shape[1]) != r or int(proj_down_op6.shape[0]) < kp:
+        raise SvdqOpError(f"{name}: proj_down_op6 must be [>= {kp}, {r}] rows in operand order, got "
                           f"{tuple(proj_down_op6.shape)}")
     return r
 
@@ -268,8 +275,11 @@ def _fp6_quant_into(name: str, x2: Tensor, smooth: Optional[Tensor], s2: Optiona
     s2 = _scalar_f32(name, s2)
     _check_cuda(name, x2=x2, smooth=smooth, s2=s2, proj_down_op6=proj_down_op6, q6=q6, la_part=la_part)
     m, k = int(x2.shape[0]), int(x2.shape[1])
-    if k % FP6_STAGE:
-        raise SvdqOpError(f"{name}: the fp6 records need K % {FP6_STAGE} == 0, got K={k}")
+    if k % GROUP:
+        raise SvdqOpError(f"{name}: the fp6 records need K % {GROUP} == 0, got K={k}")
+    if k % FP6_STAGE and fp6_stages(k) != int(q6.shape[0]):
+        raise SvdqOpError(f"{name}: K={k} ends in a half stage, which must be the records' last "
+                          f"({int(q6.shape[0])} stages)")
     if smooth is not None and smooth.numel() != k:
         raise SvdqOpError(f"{name}: smooth has {smooth.numel()} values for K={k}")
     q6_addr = _next_records(name, q6, m, k, 0)
@@ -307,21 +317,22 @@ def _(la_part):
 @torch.library.custom_op("cozy_gen_worker::svdq_prep_proj_down_fp6", mutates_args=())
 def svdq_prep_proj_down_fp6(proj_down: Tensor) -> Tensor:
     """proj_down [K, rank] bf16 -> the operand order of the fp6-lane act-quant kernel and of the next-layer
-    epilogue ([K, rank], stage-major; K % 128 == 0). Done once per weight."""
+    epilogue ([K', rank], stage-major, K' = K rounded up to whole 128-row stages: a half stage's rows past K are
+    zeros; K % 64 == 0). Done once per weight."""
     name = "svdq_prep_proj_down_fp6"
     _check_dtype(name, proj_down, torch.bfloat16, what="proj_down")
     _check_cuda(name, proj_down=proj_down)
     if proj_down.dim() != 2:
         raise SvdqOpError(f"{name}: proj_down must be [K, rank], got {tuple(proj_down.shape)}")
     k, r = int(proj_down.shape[0]), int(proj_down.shape[1])
-    out = torch.empty(k, r, dtype=torch.bfloat16, device=proj_down.device)
+    out = torch.empty(fp6_stages(k) * FP6_STAGE, r, dtype=torch.bfloat16, device=proj_down.device)
     nat.call("gwa_svdq_prep_proj_down_fp6", nat.ptr(proj_down), nat.ptr(out), k, r, nat.stream_of(proj_down))
     return out
 
 
 @svdq_prep_proj_down_fp6.register_fake
 def _(proj_down):
-    return proj_down.new_empty(int(proj_down.shape[0]), int(proj_down.shape[1]))
+    return proj_down.new_empty(fp6_stages(int(proj_down.shape[0])) * FP6_STAGE, int(proj_down.shape[1]))
 
 
 @torch.library.custom_op("cozy_gen_worker::svdq_quant_fp6", mutates_args=())
@@ -332,7 +343,7 @@ def svdq_quant_fp6(x2: Tensor, smooth: Optional[Tensor], s2: Optional[Tensor],
     (fp32 partial sums over K ranges, reduced in a fixed order, rounded to bf16); la is [M, 0] when
     ``proj_down_op6`` (``svdq_prep_proj_down_fp6``) is None."""
     m, k = int(x2.shape[0]), int(x2.shape[-1])
-    q6 = records_empty(k // FP6_STAGE, m, x2.device)
+    q6 = records_empty(fp6_stages(k), m, x2.device)
     r = int(proj_down_op6.shape[1]) if proj_down_op6 is not None else 0
     if not r:
         _fp6_quant_into("svdq_quant_fp6", x2, smooth, s2, None, q6, None)
@@ -345,13 +356,13 @@ def svdq_quant_fp6(x2: Tensor, smooth: Optional[Tensor], s2: Optional[Tensor],
     _check_dtype(name, proj_down_op6, torch.bfloat16, what="proj_down_op6")
     s2 = _scalar_f32(name, s2)
     _check_cuda(name, x2=x2, smooth=smooth, s2=s2, proj_down_op6=proj_down_op6)
-    if k % FP6_STAGE:
-        raise SvdqOpError(f"{name}: the fp6 records need K % {FP6_STAGE} == 0, got K={k}")
+    if k % GROUP:
+        raise SvdqOpError(f"{name}: the fp6 records need K % {GROUP} == 0, got K={k}")
     if smooth is not None and smooth.numel() != k:
         raise SvdqOpError(f"{name}: smooth has {smooth.numel()} values for K={k}")
-    if proj_down_op6.dim() != 2 or int(proj_down_op6.shape[0]) < k:
-        raise SvdqOpError(f"{name}: proj_down_op6 must be [>= {k}, rank] rows in operand order, got "
-                          f"{tuple(proj_down_op6.shape)}")
+    if proj_down_op6.dim() != 2 or int(proj_down_op6.shape[0]) < fp6_stages(k) * FP6_STAGE:
+        raise SvdqOpError(f"{name}: proj_down_op6 must be [>= {fp6_stages(k) * FP6_STAGE}, rank] rows in operand "
+                          f"order, got {tuple(proj_down_op6.shape)}")
     if x2.stride(1) != 1:
         x2 = x2.contiguous()
     la = torch.empty(m, r, dtype=torch.bfloat16, device=x2.device)
@@ -366,7 +377,7 @@ def svdq_quant_fp6(x2: Tensor, smooth: Optional[Tensor], s2: Optional[Tensor],
 def _(x2, smooth, s2, proj_down_op6):
     m, k = int(x2.shape[0]), int(x2.shape[1])
     r = int(proj_down_op6.shape[1]) if proj_down_op6 is not None else 0
-    return (x2.new_empty(k // FP6_STAGE, m, nat.FP6_REC, dtype=torch.uint8),
+    return (x2.new_empty(fp6_stages(k), m, nat.FP6_REC, dtype=torch.uint8),
             x2.new_empty(m, r, dtype=torch.bfloat16))
 
 
@@ -532,9 +543,12 @@ def svdq_forward_fp6(x2: Tensor, smooth: Optional[Tensor], s2: Optional[Tensor],
     if not x2.is_cuda:
         raise SvdqOpError(f"{name}: x2 is on {x2.device}; the int4/int8 path runs on the GPU only")
     m, k = int(x2.shape[0]), int(x2.shape[1])
+    if k % GROUP:
+        raise SvdqOpError(f"{name}: the fp6 lane needs K % {GROUP} == 0, got K={k}")
+    kp = fp6_stages(k) * FP6_STAGE  # K % 128 == 64: the records end in a half stage
     n, kw = _fp6_records_k(name, weight_fp6, "weight_fp6")
-    if kw != k:
-        raise SvdqOpError(f"{name}: x2 has K={k}, weight_fp6 K={kw}")
+    if kw != kp:
+        raise SvdqOpError(f"{name}: x2 has K={k} ({kp // FP6_STAGE} stages), weight_fp6 {kw // FP6_STAGE} stages")
     if smooth is not None and smooth.numel() != k:
         raise SvdqOpError(f"{name}: smooth has {smooth.numel()} values for K={k}")
     _check_record_slack(name, weight_fp6, "weight_fp6")
@@ -543,9 +557,9 @@ def svdq_forward_fp6(x2: Tensor, smooth: Optional[Tensor], s2: Optional[Tensor],
     rank = 0
     if proj_up is not None:
         rank = int(proj_up.shape[1])
-        if tuple(proj_up.shape) != (n, rank) or tuple(proj_down_op6.shape) != (k, rank):
+        if tuple(proj_up.shape) != (n, rank) or tuple(proj_down_op6.shape) != (kp, rank):
             raise SvdqOpError(f"{name}: proj_up {tuple(proj_up.shape)} / proj_down_op6 {tuple(proj_down_op6.shape)} "
-                              f"do not match [N={n}, r] / [K={k}, r]")
+                              f"do not match [N={n}, r] / [K'={kp}, r]")
     if bias is not None and bias.numel() != n:
         raise SvdqOpError(f"{name}: bias has {bias.numel()} values for N={n}")
     out = torch.empty(m, n, dtype=out_dtype, device=x2.device)
@@ -658,11 +672,11 @@ class BoundLinearFp6:
     __slots__ = ("key", "held", "device", "k", "n", "rank", "out_dtype", "gemv_max_m", "_lin", "_gemv",
                  "_lin_args", "_gemv_args", "_tail", "_ws_lin", "_ws_gemv", "_ws", "_dev_index")
 
-    def __init__(self, *, key: tuple, held: tuple, smooth: Optional[Tensor], proj_down_op6: Optional[Tensor],
+    def __init__(self, *, key: tuple, held: tuple, k: int, smooth: Optional[Tensor], proj_down_op6: Optional[Tensor],
                  weight: Tensor,
                  weight_scale: Tensor, weight_fp6: Tensor, second: Optional[Tensor], proj_up: Optional[Tensor],
                  bias: Optional[Tensor], out_dtype: torch.dtype, gelu: bool, gemv_max_m: int) -> None:
-        n, k = _fp6_records_k("BoundLinearFp6", weight_fp6, "weight_fp6")
+        n = _fp6_records_k("BoundLinearFp6", weight_fp6, "weight_fp6")[0]
         x0 = torch.empty(0, k, dtype=torch.bfloat16, device=weight_fp6.device)
         svdq_forward_fp6(x0, smooth, None, proj_down_op6, weight_fp6, second, proj_up, bias, out_dtype, gelu)
         if gemv_max_m > 0:
@@ -808,18 +822,18 @@ def _(x2, smooth, proj_down_op6, q6, la_part):
 @torch.library.custom_op("cozy_gen_worker::svdq_pack_weight_fp6", mutates_args=())
 def svdq_pack_weight_fp6(weight: Tensor, wscales: Tensor) -> Tensor:
     """Logical int4 weights [N, K/2] + fp16 group scales [N, K/64] -> fp6 operand records
-    [K/128, N, 104] (any code in [-8, 7])."""
+    [ceil(K/128), N, 104] (any code in [-8, 7]; K % 128 == 64 ends in a half stage: zero codes and scale)."""
     name = "svdq_pack_weight_fp6"
     _check_dtype(name, weight, torch.uint8, what="weight")
     _check_dtype(name, wscales, torch.float16, what="wscales")
     _check_cuda(name, weight=weight, wscales=wscales)
     n, kh = int(weight.shape[0]), int(weight.shape[1])
     k = 2 * kh
-    if k % FP6_STAGE:
-        raise SvdqOpError(f"{name}: K={k} is not a multiple of {FP6_STAGE}")
+    if k % GROUP:
+        raise SvdqOpError(f"{name}: K={k} is not a multiple of {GROUP}")
     if tuple(wscales.shape) != (n, k // GROUP):
         raise SvdqOpError(f"{name}: wscales {tuple(wscales.shape)} do not match [N={n}, K/64={k // GROUP}]")
-    out = records_empty(k // FP6_STAGE, n, weight.device)
+    out = records_empty(fp6_stages(k), n, weight.device)
     nat.call("gwa_svdq_pack_weight_fp6", nat.ptr(weight.contiguous()), nat.ptr(wscales.contiguous()), nat.ptr(out),
              n, k, nat.stream_of(weight))
     return out
@@ -827,7 +841,7 @@ def svdq_pack_weight_fp6(weight: Tensor, wscales: Tensor) -> Tensor:
 
 @svdq_pack_weight_fp6.register_fake
 def _(weight, wscales):
-    return weight.new_empty(int(weight.shape[1]) * 2 // FP6_STAGE, int(weight.shape[0]), nat.FP6_REC)
+    return weight.new_empty(fp6_stages(int(weight.shape[1]) * 2), int(weight.shape[0]), nat.FP6_REC)
 
 
 @torch.library.custom_op("cozy_gen_worker::svdq_group_psums_fp6", mutates_args=())
@@ -911,8 +925,9 @@ def svdq_gemm_w4a4_lora(qa: Tensor, sa: Tensor, wq_kn: Tensor, ws: Tensor, s2: T
                         lora_act: Tensor, up: Tensor, bias: Optional[Tensor]) -> Tensor:
     """The reference schema (``models/svdq_fused.py:379-389``): int4 nibble activations ``qa`` [M, K/2] with
     fp16 scales ``sa`` [M, K/64], the K-major weight ``wq_kn`` [K/2, N] with ``ws`` [N, K/64], bf16 out.
-    With K % 128 == 0 it runs the fp6 lane: the activations repacked as fp6 records each call, the weight's
-    records built once per weight tensor (``reference_gemm_weight_cache``); otherwise the general lane."""
+    It runs the fp6 lane: the activations repacked as fp6 records each call, the weight's records built once
+    per weight tensor (``reference_gemm_weight_cache``); operands outside that lane's contract (or M == 0) go
+    to the general lane, which raises the contract error."""
     name = "svdq_gemm_w4a4_lora"
     _check_cuda(name, wq_kn=wq_kn, qa=qa, sa=sa, ws=ws)
     _check_dtype(name, wq_kn, torch.uint8, what="wq_kn")
@@ -922,7 +937,7 @@ def svdq_gemm_w4a4_lora(qa: Tensor, sa: Tensor, wq_kn: Tensor, ws: Tensor, s2: T
     kh, n = int(wq_kn.shape[0]), int(wq_kn.shape[1])
     m, k = int(qa.shape[0]), 2 * kh
     r = int(up.shape[1]) if up is not None else 0
-    if (k % FP6_STAGE == 0 and r in (0, 16, 32, 64, 128) and n % 16 == 0 and m > 0
+    if (k % GROUP == 0 and r in (0, 16, 32, 64, 128) and n % 16 == 0 and m > 0
             and tuple(qa.shape) == (m, kh) and tuple(sa.shape) == (m, k // GROUP) and tuple(ws.shape) == (n, k // GROUP)):
         w6 = _REF_WEIGHT_FP6.get(wq_kn, ws)
         q6 = svdq_pack_weight_fp6(qa, sa)

@@ -7,10 +7,12 @@ same buffer names (``weight``, ``weight_scale``, ``second``,
 structure (``:516-527``: quantize -> W4A4 GEMM -> low-rank + bias epilogue),
 but two launches instead of four: kernel 1 fuses the smoothing, the act-quant
 and ``x2 @ proj_down``; kernel 2 fuses the GEMM with the whole epilogue.
-With ``in_features % 128 == 0`` (the fp6 lane) kernel 1 writes its codes and
-scales as fp6 operand records and the GEMM runs on gfx950's fp6 MFMA against
-weights prepacked into the same records (``weight_fp6``); other shapes use
-the int4 codes and the int8-MFMA GEMM.
+On the GPU (the fp6 lane) kernel 1 writes its codes and scales as fp6
+operand records and the GEMM runs on gfx950's fp6 MFMA against weights
+prepacked into the same records (``weight_fp6``); an ``in_features`` with
+``in_features % 128 == 64`` ends in a half stage whose second group holds zero
+codes. The general lane (int4 codes, int8-MFMA GEMM) stays available through
+its ops.
 
 Buffer formats (the int4 lane's own layout):
   weight        uint8 [out, in/2]   two's-complement int4 codes, low nibble = even k
@@ -179,9 +181,9 @@ class SvdqW4A4Linear(nn.Module):
 
     def refresh_derived(self) -> None:
         """Recompute the derived buffers after ``weight`` / ``proj_down`` change (GPU only): ``proj_down``
-        in kernel 1's operand order, and the weights as fp6 operand records (``in_features % 128 == 0``;
-        other shapes keep the general int8 path)."""
-        fp6 = self.weight.is_cuda and self.in_features % ops.FP6_STAGE == 0
+        in kernel 1's operand order, and the weights as fp6 operand records (``in_features % 128 == 64`` ends
+        in a half stage of zero codes)."""
+        fp6 = self.weight.is_cuda and self.in_features % GROUP == 0
         if self.rank:
             on_gpu = self.proj_down.is_cuda
             self.proj_down_op = torch.ops.cozy_gen_worker.svdq_prep_proj_down(self.proj_down) if on_gpu else None
@@ -219,7 +221,7 @@ class SvdqW4A4Linear(nn.Module):
         return "fp6" if self.weight_fp6 is not None else "general"
 
     def _ensure_derived(self) -> None:
-        fp6 = self.weight.is_cuda and self.in_features % ops.FP6_STAGE == 0
+        fp6 = self.weight.is_cuda and self.in_features % GROUP == 0
         if ((self.rank and (self.proj_down_op is None or (fp6 and self.proj_down_op6 is None)))
                 or (self.weight_fp6 is None and fp6)):
             self.refresh_derived()
@@ -231,11 +233,11 @@ class SvdqW4A4Linear(nn.Module):
         return x2.contiguous()
 
     def forward_records(self, q6: Tensor, la: Optional[Tensor], out_dtype: Optional[torch.dtype] = None) -> Tensor:
-        """The fp6-lane GEMM on ready input records [K/128, M, 104] and la [M, rank] (bf16, or fp32); returns
-        [M, out_features]."""
+        """The fp6-lane GEMM on ready input records [ceil(K/128), M, 104] and la [M, rank] (bf16, or fp32);
+        returns [M, out_features]."""
         self._ensure_derived()
         if self.weight_fp6 is None:
-            raise SvdqFusedError("forward_records needs the fp6 lane (in_features % 128 == 0, weights on the GPU)")
+            raise SvdqFusedError("forward_records needs the fp6 lane (weights on the GPU)")
         return torch.ops.cozy_gen_worker.svdq_w4a4_linear_fp6(
             q6, self.weight_fp6, None, self.second, la if self.rank else None, self.proj_up, self.bias,
             out_dtype or self.out_dtype or torch.bfloat16, self.activation == "gelu_tanh")
@@ -284,7 +286,7 @@ class SvdqW4A4Linear(nn.Module):
         b = self._bound
         if b is None or b.key != key:
             b = self._bound = ops.BoundLinearFp6(
-                key=key, held=ts, smooth=self.smooth_factor, proj_down_op6=pdo6, weight=self.weight,
+                key=key, held=ts, k=self.in_features, smooth=self.smooth_factor, proj_down_op6=pdo6, weight=self.weight,
                 weight_scale=self.weight_scale, weight_fp6=self.weight_fp6, second=self.second, proj_up=up,
                 bias=self.bias, out_dtype=out_dtype, gelu=gelu, gemv_max_m=self._gemv_max_m)
         return b(x2)

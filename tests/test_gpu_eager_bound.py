@@ -90,6 +90,25 @@ def test_bound_forward_equals_the_ops(rank, bias, activation, out_dtype, per_cha
         assert torch.equal(mod(xv).view(torch.int16), _op(mod, xv.contiguous()).view(torch.int16))
 
 
+def test_bound_forward_half_stage():
+    """in_features % 128 == 64 (the records end in a half stage; no GEMV): the bound call equals the op."""
+    from gen_worker_amd import synthetic
+    from gen_worker_amd.svdq import build_svdq_w4a4_linear
+
+    k = 320
+    L = synthetic.w4a4_layer(N, k, 32, seed_offset=9)
+    mod = build_svdq_w4a4_linear(qweight=L.qweight, wscales=L.wscales, smooth=L.smooth, proj_down=L.proj_down,
+                                 proj_up=L.proj_up, bias=L.bias, device=DEV)
+    assert mod.lane == "fp6" and mod._gemv_max_m == 0 and int(mod.weight_fp6.shape[0]) == 3
+    for m in (0, 1, 77, 300):
+        x = synthetic.activation(m, k, outlier_frac=0.005, outlier_scale=30.0, seed=13 + m).to(DEV)
+        y = mod(x)
+        assert mod._bound is not None
+        ref = _op(mod, x)
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int16), ref.view(torch.int16)), f"m={m}"
+
+
 def test_bound_call_rebinds_on_changes():
     mod = _module(32, True)
     x = _act(200)

@@ -79,6 +79,14 @@ def _run_quant(x_bits, smooth_bits, down_bits, s2=None, fmt="int4"):
         torch.cuda.synchronize()
         codes, sbits = decode_fp6_records(q6.cpu().numpy())
         assert codes.min() >= -8 and codes.max() <= 7
+        k = int(x.shape[1])
+        if codes.shape[1] > k:
+            # K % 128 == 64: the half stage's second group is an all-zero group (zero codes, the oracle's
+            # scale of a zero group)
+            zq, zs = O.quantize_act_int4(O.f32_to_bf16_bits(np.zeros((1, 64), np.float32)))
+            assert codes.shape[1] == k + 64 and not codes[:, k:].any()
+            assert np.all(sbits[:, k // 64] == zs.view(np.uint16)[0, 0])
+            codes, sbits = codes[:, :k], sbits[:, :k // 64]
         return O.pack_int4(codes), sbits, (la if down_bits is not None else None)
     if down_bits is not None:
         pdo = torch.ops.cozy_gen_worker.svdq_prep_proj_down(_dev16(down_bits))
@@ -121,9 +129,9 @@ _QUANT_SHAPES = [
 ]
 
 
-# the fp6 records hold 128-column stages: that format needs K % 128 == 0
+# the fp6 records hold 128-column stages: K % 128 == 64 ends in a half stage (K = 64, 192, 320)
 @pytest.mark.parametrize("m,k,rank,smooth,fmt", [(*c, "int4") for c in _QUANT_SHAPES] +
-                         [(*c, "fp6") for c in _QUANT_SHAPES if c[1] % 128 == 0])
+                         [(*c, "fp6") for c in _QUANT_SHAPES])
 def test_quant_seeded_bit_exact(m, k, rank, smooth, fmt):
     x = _rand_act(m, k, seed=m * 7 + k)
     g = np.random.default_rng(k)
@@ -311,6 +319,16 @@ def test_pack_weight_fp6_layout():
     got_codes, got_scales = decode_fp6_records(w6.cpu().numpy())
     assert np.array_equal(got_codes, codes)
     assert np.array_equal(got_scales, sw.view(np.uint16))
+    # K = 320: the third stage is a half stage whose second group holds zero codes and a zero scale, and every
+    # record's four unused bytes are zero
+    w6h = torch.ops.cozy_gen_worker.svdq_pack_weight_fp6(torch.from_numpy(O.pack_int4(codes[:, :320])).to(DEV),
+                                                        torch.from_numpy(sw[:, :5].copy()).to(DEV))
+    assert tuple(w6h.shape) == (3, 40, 104)
+    rec = w6h.cpu().numpy()
+    hc, hs = decode_fp6_records(rec)
+    assert np.array_equal(hc[:, :320], codes[:, :320]) and not hc[:, 320:].any()
+    assert np.array_equal(hs[:, :5], sw[:, :5].view(np.uint16)) and not hs[:, 5:].any()
+    assert not rec[:, :, 100:].any()
 
 
 def _fp6_rows(q):
@@ -335,6 +353,8 @@ def test_psums_fp6_bit_exact(m, n, k):
 @pytest.mark.parametrize("m,n,k,rank", [
     (1, 16, 128, 0), (77, 128, 512, 32), (256, 3072, 3072, 32), (333, 272, 640, 128), (130, 144, 256, 16),
     (64, 256, 12288, 64), (300, 128, 15360, 32), (513, 400, 1152, 32), (4097, 48, 768, 16), (600, 528, 384, 32),
+    # K % 128 == 64: the records end in a half stage (K = 64 is Flux's x_embedder)
+    (4096, 3072, 64, 32), (45, 96, 192, 16), (333, 272, 320, 128), (577, 656, 2112, 32), (2, 64, 64, 0),
 ])
 def test_w4a4_fp6_seeded(m, n, k, rank):
     y, ref = _w4a4_case(m, n, k, rank, seed=m * 13 + n + k, fp6=True)
@@ -375,12 +395,12 @@ def test_w4a4_fp6_epilogue_variants():
 
 
 def test_module_lanes_agree():
-    """in_features % 128 == 0 takes the fp6 lane (any code, -8 included), other shapes the general lane;
-    both match the oracle."""
+    """Every in_features % 64 == 0 takes the fp6 lane (any code, -8 included), K % 128 == 64 with a half
+    stage (K = 64: Flux's x_embedder); each matches the oracle, and the general int8-MFMA lane's ops agree."""
     from gen_worker_amd import synthetic
     from gen_worker_amd.svdq import build_svdq_w4a4_linear
 
-    for k, want in ((512, "fp6"), (320, "general")):
+    for k, want in ((512, "fp6"), (320, "fp6"), (64, "fp6"), (192, "fp6")):
         L = synthetic.w4a4_layer(256, k, 32)
         qw = L.qweight.clone()
         qw[0, 0] = (qw[0, 0] & 0xF0) | 0x8     # one -8 code
@@ -391,7 +411,12 @@ def test_module_lanes_agree():
         y = mod(x.to(DEV))
         ref = O.w4a4_linear(bits16(x), bits16(L.smooth), qw.numpy(), L.wscales.numpy(), bits16(L.proj_down),
                             bits16(L.proj_up), bits16(L.bias))
-        check_output(y, ref, what=mod.lane)
+        check_output(y, ref, what=f"{mod.lane} K={k}")
+        cg = torch.ops.cozy_gen_worker
+        qa, sa, la = cg.svdq_quant_lora(x.to(DEV), mod.smooth_factor, None, mod.proj_down_op)
+        yg = cg.svdq_w4a4_linear(qa, sa, mod.weight, mod.weight_scale, None, mod.second, la, mod.proj_up, mod.bias,
+                                 torch.bfloat16, False)
+        check_output(yg, ref, what=f"general lane K={k}")
 
 
 def test_w4a4_module_config1_full_size():
@@ -434,8 +459,8 @@ def _ref_schema_oracle(x, qw, sw, up, la, b, second):
                                      (4608, 3072, 3072, 32)])
 def test_reference_schema_gemm(m, n, k, r):
     """cozy_gen_worker::svdq_gemm_w4a4_lora keeps the reference schema (nibble activations, K-major wq_kn):
-    against the oracle, and with K % 128 == 0 on the fp6 lane, bit-identical to svdq_w4a4_linear_fp6 on the
-    same operands (the general lane serves K % 128 != 0)."""
+    against the oracle, and on the fp6 lane (K % 128 == 64: a half stage) bit-identical to svdq_w4a4_linear_fp6
+    on the same operands."""
     x, qw, sw, up, la, b, second = _ref_schema_case(m, n, k, r, seed=m + k)
     cg = torch.ops.cozy_gen_worker
     qa, sa = cg.svdq_quant(_dev16(x), None, torch.ones((), device=DEV), False)
@@ -447,11 +472,11 @@ def test_reference_schema_gemm(m, n, k, r):
     rows = np.unique(np.r_[0:min(m, 64), m - min(m, 64):m])
     check_output(y[rows], _ref_schema_oracle(x[rows], qw, sw, up, la[rows], b, second),
                  what=f"svdq_gemm_w4a4_lora {m}x{n}x{k}")
-    if k % 128 == 0:
-        w6 = cg.svdq_pack_weight_fp6(torch.from_numpy(qw).to(DEV), swd)
-        q6 = cg.svdq_pack_weight_fp6(qa, sa)
-        y6 = cg.svdq_w4a4_linear_fp6(q6, w6, s2, sec, _dev16(la), _dev16(up), _dev16(b), torch.bfloat16, False)
-        assert torch.equal(y.view(torch.int16), y6.view(torch.int16))
+    w6 = cg.svdq_pack_weight_fp6(torch.from_numpy(qw).to(DEV), swd)
+    q6 = cg.svdq_pack_weight_fp6(qa, sa)
+    assert int(w6.shape[0]) == (k + 127) // 128
+    y6 = cg.svdq_w4a4_linear_fp6(q6, w6, s2, sec, _dev16(la), _dev16(up), _dev16(b), torch.bfloat16, False)
+    assert torch.equal(y.view(torch.int16), y6.view(torch.int16))
 
 
 def test_reference_schema_weight_cache():

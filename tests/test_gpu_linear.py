@@ -55,6 +55,8 @@ def _two_op(mod, x, out_dtype, gelu):
     (300, 384, 768, 0, True, torch.float16),
     (513, 640, 1024, 64, True, torch.bfloat16),
     (4608, 3072, 3072, 32, False, torch.bfloat16),
+    (4096, 3072, 64, 32, False, torch.bfloat16),    # K % 128 == 64: half stages (Flux's x_embedder)
+    (129, 272, 320, 16, True, torch.float16),
 ])
 def test_forward_fp6_equals_two_op_path(m, n, k, r, gelu, odt):
     from gen_worker_amd import synthetic

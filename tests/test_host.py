@@ -119,10 +119,14 @@ def test_invalid_arguments_are_refused_before_any_launch():
     assert rc == 1 and "out_format" in lib.gwa_last_error().decode()
     rc = lib.gwa_svdq_quant_int4(None, 192, None, None, None, 0, 1, None, None, None, 4, 192, None)
     assert rc == 1 and "gwa_svdq_quant_fp6" in lib.gwa_last_error().decode()
+    # the fp6 records take any K % 64 == 0 (K % 128 == 64 ends in a half stage)
+    rc = lib.gwa_svdq_quant_fp6(None, 160, None, None, None, 0, None, None, 4, 160, None)
+    assert rc == 1 and "multiple of 64" in lib.gwa_last_error().decode()
     rc = lib.gwa_svdq_quant_fp6(None, 192, None, None, None, 0, None, None, 4, 192, None)
-    assert rc == 1 and "multiple of 128" in lib.gwa_last_error().decode()
-    rc = lib.gwa_svdq_prep_proj_down_fp6(None, None, 192, 32, None)
-    assert rc == 1 and "multiple of 128" in lib.gwa_last_error().decode()
+    assert rc == 1 and "null pointer" in lib.gwa_last_error().decode()
+    rc = lib.gwa_svdq_prep_proj_down_fp6(None, None, 160, 32, None)
+    assert rc == 1 and "multiple of 64" in lib.gwa_last_error().decode()
+    assert lib.gwa_svdq_quant_fp6_partials(77, 320, 32) == 3 and lib.gwa_svdq_quant_fp6_partials(77, 160, 32) == 0
     rc = lib.gwa_svdq_la_reduce(None, 0, 4, 32, None, None)
     assert rc == 1 and "bad shape" in lib.gwa_last_error().decode()
     # partial-slot counts: kernel 1 splits K=3072 of 4608 rows over 6 ranges; the 256-wide GEMM tiles of
@@ -131,9 +135,14 @@ def test_invalid_arguments_are_refused_before_any_launch():
     assert lib.gwa_svdq_gemm_w4a4_fp6_next_partials(4608, 12288) == 48
     assert lib.gwa_svdq_gemm_w4a4_fp6_next_partials(256, 3072) == 24
     assert lib.gwa_svdq_quant_fp6_partials(4608, 3072, 0) == 0
-    rc = lib.gwa_svdq_gemm_w4a4_fp6(None, 0, None, 0, None, None, 0, None, None, 0, None, None, 0, 0, 8, 64, 192,
+    rc = lib.gwa_svdq_gemm_w4a4_fp6(None, 0, None, 0, None, None, 0, None, None, 0, None, None, 0, 0, 8, 64, 160,
                                     None)
-    assert rc == 1 and "multiple of 128" in lib.gwa_last_error().decode()
+    assert rc == 1 and "multiple of 64" in lib.gwa_last_error().decode()
+    # K = 192: two stages (the second a half stage), so the records and their slack are 2 * 8 * 104 + 1024 bytes
+    rc = lib.gwa_svdq_gemm_w4a4_fp6(None, 2 * 8 * 104, None, 0, None, None, 0, None, None, 0, None, None, 0, 0, 8,
+                                    64, 192, None)
+    assert rc == 1 and "null pointer" in lib.gwa_last_error().decode()
+    assert lib.gwa_svdq_w4a4_linear_fp6_workspace(8, 192, 32) > 0 == lib.gwa_svdq_w4a4_linear_fp6_workspace(8, 160, 32)
     # the next-layer epilogue needs whole 128-column stages and a record buffer
     rc = lib.gwa_svdq_gemm_w4a4_fp6_next(None, 0, None, 0, None, None, 0, None, None, 0, None, None, 0, None, None,
                                          0, None, None, 8, 192, 128, None)
@@ -228,6 +237,14 @@ def test_fake_impls_trace_shapes():
         w6 = torch.ops.cozy_gen_worker.svdq_pack_weight_fp6(torch.empty(128, 192, dtype=torch.uint8),
                                                            torch.empty(128, 6, dtype=torch.float16))
         assert w6.shape == (3, 128, 104)
+        # K = 320 (K % 128 == 64): records of 3 stages, the last a half stage; proj_down rows padded to 384
+        xh = torch.empty(77, 320, dtype=torch.bfloat16)
+        pdoh = torch.ops.cozy_gen_worker.svdq_prep_proj_down_fp6(torch.empty(320, 32, dtype=torch.bfloat16))
+        qh, lah = torch.ops.cozy_gen_worker.svdq_quant_fp6(xh, None, None, pdoh)
+        wh = torch.ops.cozy_gen_worker.svdq_pack_weight_fp6(torch.empty(128, 160, dtype=torch.uint8),
+                                                           torch.empty(128, 5, dtype=torch.float16))
+        assert pdoh.shape == (384, 32) and qh.shape == (3, 77, 104) and lah.shape == (77, 32)
+        assert wh.shape == (3, 128, 104)
         y6 = torch.ops.cozy_gen_worker.svdq_w4a4_linear_fp6(q6, w6, None, None, None, None, None, torch.bfloat16,
                                                             False)
         assert y6.shape == (77, 128) and y6.dtype == torch.bfloat16
