@@ -92,11 +92,52 @@ __device__ __forceinline__ v16f group_mfma_fp6(v8i a, v8i b) {
                                                          kUnitE8M0);
 }
 
-// one lane's 32 codes of a group half: 24 bytes, three 8-byte LDS reads
+// one lane's 32 codes of a group half: 24 bytes, three 8-byte LDS reads. An e3m2 operand of the scaled MFMA is
+// six dwords (the instruction reads v[a:a+5] of the 8-register operand), so the last two are left undefined:
+// materialising zeros there cost a v_mov per dword per read in the loop.
 __device__ __forceinline__ v8i lds_operand(const uint8_t* p) {
-  const uint2 a = *(const uint2*)(p), b = *(const uint2*)(p + 8), c = *(const uint2*)(p + 16);
-  const v8i v = (v8i){(int)a.x, (int)a.y, (int)b.x, (int)b.y, (int)c.x, (int)c.y, 0, 0};
-  return v;
+  typedef int v2i_ __attribute__((ext_vector_type(2)));
+  const v2i_ a = *(const v2i_*)(p), b = *(const v2i_*)(p + 8), c = *(const v2i_*)(p + 16);
+  const v4i ab = __builtin_shufflevector(a, b, 0, 1, 2, 3);
+  const v4i cc = __builtin_shufflevector(c, c, 0, 1, -1, -1);
+  return __builtin_shufflevector(ab, cc, 0, 1, 2, 3, 4, 5, -1, -1);
+}
+
+// A tile's per-column epilogue constants s2 * second[n] and bias[n]. The raw words are loaded by thread n - n0
+// before the first operand copies are issued (branch-free: an absent operand's buffer has no records and reads
+// as zero), stay in three registers through the K loop and are first used when the epilogue writes them to
+// LDS, so no wait for them precedes the copies.
+struct EpiConsts {
+  uint32_t s2, sec;
+  uint16_t b;
+  bool ok;
+};
+__device__ __forceinline__ EpiConsts epi_consts_load(const float* s2p, const float* second, int second_per_channel,
+                                                     const uint16_t* bias, int n0, int tid, int tn, int N) {
+  const int n = n0 + tid;
+  EpiConsts c;
+  c.ok = tid < tn && n < N;
+  const uint32_t sec_bytes = second ? (uint32_t)((second_per_channel ? N : 1) * 4) : 0u;
+  c.s2 = __builtin_amdgcn_raw_buffer_load_b32(make_rsrc(s2p, s2p ? 4u : 0u), c.ok ? 0u : kOOB, 0, 0);
+  c.sec = __builtin_amdgcn_raw_buffer_load_b32(make_rsrc(second, sec_bytes),
+                                               c.ok ? (uint32_t)((second_per_channel ? n : 0) * 4) : kOOB, 0, 0);
+  c.b = __builtin_amdgcn_raw_buffer_load_b16(make_rsrc(bias, bias ? (uint32_t)(N * 2) : 0u),
+                                             c.ok ? (uint32_t)(n * 2) : kOOB, 0, 0);
+  return c;
+}
+// the constants into g_epi[0, tn) (multiplier) and g_epi[tn, 2 tn) (bias); zeros for columns past N
+__device__ __forceinline__ void epi_consts_store(const EpiConsts& c, const float* s2p, const float* second,
+                                                 const uint16_t* bias, float* g_epi, int tid, int tn) {
+  if (tid < tn) {
+    float mult = 0.0f, bv = 0.0f;
+    if (c.ok) {
+      mult = s2p ? __uint_as_float(c.s2) : 1.0f;
+      if (second) mult *= __uint_as_float(c.sec);
+      if (bias) bv = bf16_to_f32(c.b);
+    }
+    g_epi[tid] = mult;
+    g_epi[tn + tid] = bv;
+  }
 }
 
 __device__ __forceinline__ v8i buf_operand(rsrc_t r, uint32_t off) {

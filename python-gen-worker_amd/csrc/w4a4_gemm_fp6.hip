@@ -329,19 +329,9 @@ __global__ __launch_bounds__(NTHREADS, (TM == 64 ? 4 : 1)) void w4a4_gemm_fp6_ke
     }
   };
 
-  // the tile's per-column epilogue constants: s2 * second[n] and bias[n]
-  if (tid < TN) {
-    const int n = n0 + tid;
-    float mult = 0.0f, bv = 0.0f;
-    if (n < N) {
-      mult = s2p ? *s2p : 1.0f;
-      if (second) mult *= second[second_per_channel ? n : 0];
-      if (bias) bv = bf16_to_f32(bias[n]);
-    }
-    g_epi[tid] = mult;
-    g_epi[TN + tid] = bv;
-  }
-  __syncthreads();  // the epilogue constants' loads are complete before any copy is in flight
+  // the epilogue constants' loads go out first; they are older than every copy, so the stage waits below cover
+  // them too
+  const EpiConsts epc = epi_consts_load(s2p, second, second_per_channel, bias, n0, tid, TN, N);
   // stages 0 .. NBUF - 1 in flight; stage 0 complete; its first group's operands and scales into registers
 #pragma unroll
   for (int u = 0; u < NBUF; ++u)
@@ -368,6 +358,7 @@ __global__ __launch_bounds__(NTHREADS, (TM == 64 ? 4 : 1)) void w4a4_gemm_fp6_ke
     fma_half(kLast, 0);
     fma_half(kLast, 1);
   }
+  epi_consts_store(epc, s2p, second, bias, g_epi, tid, TN);
   wait_vm_lgkm0<0>();  // the low-rank copies (and the reads past the last stage) complete
   barrier_lds();
 
