@@ -178,11 +178,30 @@ class SvdqW4A4Linear(nn.Module):
         self._gemv_max_m = 0
         # the fp6 lane's operands bound for eager calls (ops.BoundLinearFp6), rebuilt when any of them changes
         self._bound: Optional[ops.BoundLinearFp6] = None
+        # identity and version counter of each buffer the derived ones were computed from (_primary_versions)
+        self._derived_from: Optional[tuple] = None
+
+    def _primary_versions(self) -> tuple:
+        """(id, version counter) of ``weight``, ``weight_scale`` and ``proj_down``, the buffers the derived ones
+        are computed from: an in-place update (``mod.weight.copy_(...)``) bumps the counter and a reassignment
+        changes the id, and either makes the next forward rebuild the derived buffers. A tensor made under
+        ``torch.inference_mode`` keeps no counter (its in-place updates need an explicit ``refresh_derived``)."""
+        out = []
+        for t in (self.weight, self.weight_scale, self.proj_down):
+            if t is None:
+                out.append(None)
+                continue
+            try:
+                out.append((id(t), t._version))
+            except RuntimeError:
+                out.append((id(t), None))
+        return tuple(out)
 
     def refresh_derived(self) -> None:
-        """Recompute the derived buffers after ``weight`` / ``proj_down`` change (GPU only): ``proj_down``
-        in kernel 1's operand order, and the weights as fp6 operand records (``in_features % 128 == 64`` ends
-        in a half stage of zero codes)."""
+        """Recompute the derived buffers from ``weight`` / ``weight_scale`` / ``proj_down`` (GPU only):
+        ``proj_down`` in kernel 1's operand order, and the weights as fp6 operand records (``in_features % 128
+        == 64`` ends in a half stage of zero codes). The forward calls it by itself when those buffers changed
+        since the last call (``_primary_versions``)."""
         fp6 = self.weight.is_cuda and self.in_features % GROUP == 0
         if self.rank:
             on_gpu = self.proj_down.is_cuda
@@ -195,6 +214,7 @@ class SvdqW4A4Linear(nn.Module):
         if fp6:
             self.weight_fp6 = torch.ops.cozy_gen_worker.svdq_pack_weight_fp6(self.weight, self.weight_scale)
             self._gemv_max_m = ops.gemv_max_m(self.in_features, self.rank)
+        self._derived_from = self._primary_versions()
 
     def _apply(self, fn: Any, recurse: bool = True) -> "SvdqW4A4Linear":
         """Module moves and casts (``.to()``, ``.cuda()``, ``.cpu()``) copy buffers without the 1 KB of readable
@@ -223,7 +243,7 @@ class SvdqW4A4Linear(nn.Module):
     def _ensure_derived(self) -> None:
         fp6 = self.weight.is_cuda and self.in_features % GROUP == 0
         if ((self.rank and (self.proj_down_op is None or (fp6 and self.proj_down_op6 is None)))
-                or (self.weight_fp6 is None and fp6)):
+                or (self.weight_fp6 is None and fp6) or self._derived_from != self._primary_versions()):
             self.refresh_derived()
 
     def _input2d(self, x: Tensor) -> Tensor:

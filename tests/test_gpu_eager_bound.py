@@ -146,6 +146,23 @@ def test_bound_call_rebinds_on_changes():
     assert torch.equal(mod(x).view(torch.int16), _op(mod, x).view(torch.int16))
 
 
+def test_in_place_weight_updates_rebuild_the_derived_buffers():
+    """Every buffer of a module overwritten in place with another module's values (same storages): the next
+    forward rebuilds the fp6 weight records and proj_down's operand orders, and equals the other module bit for
+    bit on the fp6 lane and on the small-M GEMV."""
+    mod, other = _module(32, True, seed=3), _module(32, True, seed=11)
+    xs = [_act(200), _act(3)]
+    assert mod._gemv_max_m >= 3
+    before = [mod(x) for x in xs]
+    with torch.no_grad():
+        for name in ("weight", "weight_scale", "smooth_factor", "proj_down", "proj_up", "bias"):
+            getattr(mod, name).copy_(getattr(other, name))
+    for x, y0 in zip(xs, before):
+        y = mod(x)
+        assert not torch.equal(y, y0)
+        assert torch.equal(y.view(torch.int16), other(x).view(torch.int16)), f"M={x.shape[0]}"
+
+
 class _Passthrough(TorchDispatchMode):
     def __init__(self):
         super().__init__()

@@ -282,6 +282,40 @@ def test_concat_halves_refuse_outside_the_fused_contract():
         SvdqConcat(proj, mlp, n, 128)          # 128 + 512 != 768
 
 
+def test_module_tracks_in_place_updates_of_its_primary_buffers():
+    """The derived buffers are rebuilt on the next forward after ``weight`` / ``weight_scale`` / ``proj_down``
+    change in place (version counter) or are reassigned (identity); nothing else triggers a rebuild, and tensors
+    made under inference mode (no version counter) are tracked by identity without raising."""
+    from gen_worker_amd import SvdqW4A4Linear
+
+    m = SvdqW4A4Linear(128, 128, rank=0, bias=False, device="cpu")
+    calls = []
+    orig = m.refresh_derived
+    m.refresh_derived = lambda: (calls.append(1), orig())[1]
+    m._ensure_derived()
+    m._ensure_derived()
+    assert len(calls) == 1, "an unchanged module rebuilt its derived buffers"
+    with torch.no_grad():
+        m.weight.add_(1)
+    m._ensure_derived()
+    assert len(calls) == 2, "an in-place weight update was missed"
+    with torch.no_grad():
+        m.weight_scale.mul_(2)
+    m._ensure_derived()
+    assert len(calls) == 3, "an in-place weight_scale update was missed"
+    m.weight = torch.zeros_like(m.weight)
+    m._ensure_derived()
+    m._ensure_derived()
+    assert len(calls) == 4, "a reassigned weight was missed (or rebuilt twice)"
+    m.second.fill_(3.0)  # read by the kernels directly, nothing derived from it
+    m._ensure_derived()
+    assert len(calls) == 4
+    with torch.inference_mode():
+        mi = SvdqW4A4Linear(128, 128, rank=16, bias=False, device="cpu")
+        v = mi._primary_versions()
+    assert all(e is not None and e[1] is None for e in v), v
+
+
 def test_module_contract_refusals():
     from gen_worker_amd import SvdqFusedError, SvdqW4A4Linear, W8a8Error, Int8ScaledLinear
 
