@@ -181,15 +181,17 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_pipe_kernel(
   };
 
   // operand registers: activation operands (block rows) and their stage scales, weight operands (block columns)
-  // and theirs (lanes 32..63 hold zero weight scales: K slots 4..7 of the S MFMA)
+  // and theirs
   v8i xo[NA], wo[NB];
-  // The records' scale dwords as read: an activation row's two group scales (masked to group g's half when a
-  // step forms the S MFMA's B operand, so the LDS read is waited for there, groups later, not right after the
-  // read) and the stage's two weight group scales (the A operand; lanes 32..63 read the record's four zero
-  // bytes instead: K slots 4..7 of the weight side are zero).
-  uint32_t xsc[NA], wsc[NB];
+  // The S MFMA's operands. B (activation side, every lane): the row record's eight bytes 96..103 as read,
+  // {sx_g0, sx_g1, 0, 0} as f16 K slots (lanes 32..63 read their row's record too: finite scales in slots 4..7).
+  // A (weight side): the stage's two weight group scales as read (lanes 32..63 read the record's four zero
+  // bytes instead), masked to group g's slot once per run of blocks that share the weight operand (the other
+  // group's slot and K slots 2..3 zero; lanes 32..63 zero), so S = sw_g * sx_g exactly.
+  uint2 xs8[NA];
+  uint32_t wsc[NB];
 #pragma unroll
-  for (int a = 0; a < NA; ++a) xsc[a] = 0u;
+  for (int a = 0; a < NA; ++a) xs8[a] = make_uint2(0u, 0u);
 #pragma unroll
   for (int b = 0; b < NB; ++b) wsc[b] = 0u;
   auto row_of = [&](int a) __attribute__((always_inline)) { return a < 2 ? 64 * wm + 32 * a : 256; };
@@ -197,9 +199,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_pipe_kernel(
     const int c = rot + b;
     return 96 * wn + 32 * (c < 3 ? c : c - 3);
   };
-  // this lane's operand rows (+ its 24-byte half of a group) in buffer 0; buffer u adds u * LDS_X / u * LDS_W.
-  // An activation scale read at base + OFF_SC gives lanes 32..63 bytes of the next record: the masks zero them
-  // (the S MFMA's K slots 4..7 must be finite on the activation side).
+  // this lane's operand rows (+ its 24-byte half of a group) in buffer 0; buffer u adds u * LDS_X / u * LDS_W
   int xaddr[NA], waddr[NB];
 #pragma unroll
   for (int a = 0; a < NA; ++a) xaddr[a] = (row_of(a) + r32) * REC + 24 * h;
@@ -214,7 +214,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_pipe_kernel(
     wo[b] = lds_operand(g_lds + waddr[b] + u * LDS_W + gi * GB);
   };
   auto read_xs = [&](int u, int a) __attribute__((always_inline)) {
-    xsc[a] = *(const uint32_t*)(g_lds + xaddr[a] + u * LDS_X + OFF_SC);
+    xs8[a] = *(const uint2*)(g_lds + xaddr[a] - 24 * h + u * LDS_X + OFF_SC);  // the row's bytes 96..103
   };
   const int wsoff = OFF_SC - 20 * h;  // lanes 32..63: record bytes [100, 104), zero by the record format
   auto read_ws = [&](int u, int b) __attribute__((always_inline)) {
@@ -240,11 +240,13 @@ __global__ __launch_bounds__(NTHREADS, 1) void w4a4_gemm_fp6_pipe_kernel(
   // The step's MFMA inputs pass through an empty asm, so the (pure) MFMAs cannot be hoisted out of their step;
   // full scheduling fences keep the step's parts in this order (the compiler would otherwise regroup the fmas
   // and MFMAs of neighbouring steps).
+  uint2 swp = make_uint2(0u, 0u);  // the S MFMA's A operand for the current run of blocks
   auto step = [&](int p, int gi) __attribute__((always_inline)) {
     const int a = O::A[p], b = O::B[p];
-    asm volatile("" : "+v"(xsc[a]), "+v"(xo[a]), "+v"(wo[b]), "+v"(wsc[b]));
-    const v4h swop = __builtin_bit_cast(v4h, make_uint2(wsc[b], 0u));
-    const v4h sel = __builtin_bit_cast(v4h, make_uint2(xsc[a] & (gi ? gmask1 : gmask0), 0u));
+    asm volatile("" : "+v"(xs8[a]), "+v"(xo[a]), "+v"(wo[b]), "+v"(wsc[b]));
+    if (p == 0 || O::B[p - 1] != b) swp = make_uint2(wsc[b] & (gi ? gmask1 : gmask0), 0u);
+    const v4h swop = __builtin_bit_cast(v4h, swp);
+    const v4h sel = __builtin_bit_cast(v4h, xs8[a]);
     if constexpr (C::PIPE) {
       const int prev = p == 0 ? NBLK - 1 : p - 1;
       __builtin_amdgcn_sched_barrier(0);
