@@ -31,8 +31,11 @@ QKV linear at M=256 and 1024. The metric's second half, the config-4 DiT step
 (every linear W4A4 on the int4 lane, against the same model with bf16 GEMMs,
 each forward one HIP graph replayed ``--dit-steps`` times), goes into the same
 line as ``dit_step_ms`` and ``dit_bf16_step_ms``, with the arming gate's own
-decision on the box as ``dit_gate_lane``. Prints ONE JSON line on stdout; progress goes to
-stderr.
+decision on the box as ``dit_gate_lane``. It runs first, as ``--workload dit``
+in a child process started before this process touches the GPU: its own
+allocator and memory state, and a failure there leaves the config-1 line
+standing (``dit_error`` instead of the dit_* figures). Prints ONE JSON line on
+stdout; progress goes to stderr.
 
 ``--only`` runs one piece eagerly ``--iters`` times (after 3 warmups) and
 prints nothing on stdout: it is the command the committed rocprofv3
@@ -76,14 +79,13 @@ def graph_time_ms(torch, fn, reps: int, warm_calls: int = 0) -> float:
     synchronized on both sides and timed with events on the stream the graph runs on. Before it the graph is
     replayed untimed for at least ``warm_calls`` calls and at least WARM_MS of load (page-in, and the clock
     ramp: right after an idle gap the first ~20 ms of replays run up to 15 % slower than steady state)."""
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.stream(s):
-        with torch.cuda.graph(g, stream=s):
-            for _ in range(reps):
-                fn()
-    torch.cuda.synchronize()
+    from gen_worker_amd.flux_dit import capture_graph
+
+    def body() -> None:
+        for _ in range(reps):
+            fn()  # each call's outputs are released before the next one, as in eager use
+
+    g = capture_graph(body)[0]
     cur = torch.cuda.current_stream()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
@@ -221,6 +223,30 @@ def bench_dit(args) -> int:
            "block_linear_int_ops": ops_, "outputs_finite": {"w4a4": res["w4a4_finite"], "bf16": res["bf16_finite"]}}
     print(json.dumps(out), flush=True)
     return 0
+
+
+def run_dit_child(args) -> dict:
+    """The default line's DiT half: ``--workload dit`` (torch SDPA attention, config 4 as stated) with
+    ``--dit-steps`` graph replays per model, in a child process whose progress goes to this stderr. Returns
+    the line's dit_* keys, or ``dit_error`` when the child fails or prints no line."""
+    import subprocess
+
+    cmd = [sys.executable, "-u", str(Path(__file__).resolve()), "--workload", "dit", "--steps", str(args.dit_steps),
+           "--warmup", "1", "--modulation", args.modulation, "--attention", "sdpa"]
+    log("bench: the config-4 DiT pair in a child process (" + " ".join(cmd[3:]) + ")")
+    try:
+        res = subprocess.run(cmd, stdout=subprocess.PIPE, text=True, timeout=900)
+    except subprocess.TimeoutExpired:
+        return {"dit_error": "the DiT child process ran past 900 s"}
+    lines = [ln for ln in res.stdout.splitlines() if ln.startswith("{")]
+    if res.returncode != 0 or not lines:
+        return {"dit_error": f"the DiT child process exited with code {res.returncode}"}
+    d = json.loads(lines[-1])
+    return {"dit_step_ms": d["value"], "dit_bf16_step_ms": d["bf16_gemm_ms"],
+            "dit_speedup_vs_bf16": d["speedup_vs_bf16"], "dit_lane": d["config"]["lane"],
+            "dit_gate_lane": d["config"]["gate_lane"], "dit_modulation": args.modulation,
+            "dit_attention": ATTENTION_DESC["sdpa"], "dit_streams": STREAMS_DESC,
+            "dit_outputs_finite": bool(d["outputs_finite"]["w4a4"] and d["outputs_finite"]["bf16"])}
 
 
 def _w4a4_module(torch, L, dev, activation=None, out_dtype=None):
@@ -614,8 +640,8 @@ def main() -> int:
                     help="the DiT's one-token adaLN modulation linears: W4A4 like every other linear (config 4 "
                          "as stated), or AWQ W4A16 as an svdq checkpoint stores them")
     ap.add_argument("--attention", choices=("sdpa", "flash"), default="sdpa",
-                    help="the DiT's attention: torch's bf16 SDPA (config 4 as stated) or gwa_dit_attention; the "
-                         "default (c1) line reports SDPA as dit_* and the flash kernel as dit_*_flash_attention")
+                    help="the DiT's attention with --workload dit / --only dit: torch's bf16 SDPA (config 4 as "
+                         "stated, the default line's dit_* figures) or gwa_dit_attention")
     ap.add_argument("--dit-steps", type=int, default=3,
                     help="graph replays of each DiT forward in the default (c1) line; 0 skips the DiT half")
     ap.add_argument("--summarize-traffic", metavar="DIR", default=None,
@@ -639,6 +665,10 @@ def main() -> int:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}): this build's path is a single-GPU "
               f"kernel pair; multi-GPU sharding is design-only.", file=sys.stderr)
         return 2
+
+    # the metric's second half (the config-4 DiT pair) first, in a child process started before this process
+    # touches the GPU; it has ended before the config-1 timing starts
+    dit = run_dit_child(args) if args.only is None and args.dit_steps > 0 else None
 
     import torch
 
@@ -794,22 +824,8 @@ def main() -> int:
                       "achieved_GBps_vs_int4_min": round(qmin / (quant_ms * 1e-3) / 1e9, 1)},
         "cpu_baseline": cpu,
     }
-    if args.dit_steps > 0:
-        # the metric's second half: the config-4 DiT step, W4A4 (int4 lane) against bf16 GEMMs
-        torch.cuda.empty_cache()
-        res = dit_step_pair(args.dit_steps, 1, args.modulation, "sdpa")
-        out.update({"dit_step_ms": round(res["w4a4"], 3), "dit_bf16_step_ms": round(res["bf16"], 3),
-                    "dit_speedup_vs_bf16": round(res["bf16"] / res["w4a4"], 4), "dit_lane": res["w4a4_lane"],
-                    "dit_gate_lane": res["gate_lane"],
-                    "dit_modulation": args.modulation, "dit_attention": ATTENTION_DESC["sdpa"],
-                    "dit_streams": STREAMS_DESC,
-                    "dit_outputs_finite": res["w4a4_finite"] and res["bf16_finite"]})
-        # the same pair with this package's flash-attention kernel in both models (not config 4 as stated)
-        torch.cuda.empty_cache()
-        rf = dit_step_pair(args.dit_steps, 1, args.modulation, "flash")
-        out.update({"dit_step_ms_flash_attention": round(rf["w4a4"], 3),
-                    "dit_bf16_step_ms_flash_attention": round(rf["bf16"], 3),
-                    "dit_speedup_vs_bf16_flash_attention": round(rf["bf16"] / rf["w4a4"], 4)})
+    if dit is not None:
+        out.update(dit)
     print(json.dumps(out), flush=True)
     return 0
 
