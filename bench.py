@@ -79,7 +79,7 @@ def graph_time_ms(torch, fn, reps: int, warm_calls: int = 0) -> float:
     synchronized on both sides and timed with events on the stream the graph runs on. Before it the graph is
     replayed untimed for at least ``warm_calls`` calls and at least WARM_MS of load (page-in, and the clock
     ramp: right after an idle gap the first ~20 ms of replays run up to 15 % slower than steady state)."""
-    from gen_worker_amd.flux_dit import capture_graph
+    from gen_worker_amd.graphs import capture_graph
 
     def body() -> None:
         for _ in range(reps):

@@ -34,15 +34,16 @@ through the 57 blocks.
 
 from __future__ import annotations
 
-import gc
 import math
 from dataclasses import dataclass
-from typing import Any, Callable, Optional
+from typing import Callable, Optional
 
 import torch
 import torch.nn as nn
 import torch.nn.functional as F
 from torch import Tensor
+
+from .graphs import capture_graph
 
 
 @dataclass(frozen=True)
@@ -555,28 +556,6 @@ def block_int_ops(cfg: FluxDiTConfig = FluxDiTConfig()) -> int:
     return cfg.n_dual * dual + cfg.n_single * single
 
 
-def capture_graph(fn: Callable[[], Any]) -> tuple["torch.cuda.CUDAGraph", Any]:
-    """``fn()`` captured into a new HIP graph on a fresh stream that first waits for the current one; returns
-    (graph, fn's result), synchronized. Garbage is collected before the capture and Python's cyclic collector
-    stays off during it, so no tensor held by a dead reference cycle is released while the graph is captured
-    (torch's capture no longer collects first)."""
-    gc.collect()
-    was_enabled = gc.isenabled()
-    gc.disable()
-    try:
-        s = torch.cuda.Stream()
-        s.wait_stream(torch.cuda.current_stream())
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.stream(s):
-            with torch.cuda.graph(g, stream=s):
-                out = fn()
-        torch.cuda.synchronize()
-    finally:
-        if was_enabled:
-            gc.enable()
-    return g, out
-
-
 def time_step_ms(model: nn.Module, args: tuple[Tensor, ...], steps: int = 5, warmup: int = 2,
                  graph: bool = True) -> float:
     """Mean ms per forward, replaying ``steps`` forwards captured in one HIP graph (or eager)."""
@@ -605,5 +584,5 @@ def time_step_ms(model: nn.Module, args: tuple[Tensor, ...], steps: int = 5, war
         return e0.elapsed_time(e1) / steps
 
 
-__all__ = ["ATTENTION", "FluxDiT", "FluxDiTConfig", "adaln_modulate", "attention", "block_int_ops", "capture_graph",
-           "gate_residual", "inputs", "linear_factory", "qk_norm_rope", "sdpa_attention", "time_step_ms"]
+__all__ = ["ATTENTION", "FluxDiT", "FluxDiTConfig", "adaln_modulate", "attention", "block_int_ops", "gate_residual",
+           "inputs", "linear_factory", "qk_norm_rope", "sdpa_attention", "time_step_ms"]

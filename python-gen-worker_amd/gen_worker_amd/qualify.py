@@ -258,17 +258,19 @@ def _median_ms(fn: Any) -> float:
     0.072 / 0.09 ms back to back, which pulled the ratio to the 1.10x line). This assumes the serving loop
     queues its launches (graphs or back-to-back eager calls); ``_median_ms_eager`` is the reference's
     single-call protocol, recorded beside it."""
+    from .graphs import capture_graph
+
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
         fn()                      # allocations of the op's outputs happen outside the capture
     torch.cuda.current_stream().wait_stream(s)
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.stream(s):
-        with torch.cuda.graph(graph, stream=s):
-            for _ in range(BENCH_CALLS_PER_REPLAY):
-                fn()
-    torch.cuda.synchronize()
+
+    def calls() -> None:
+        for _ in range(BENCH_CALLS_PER_REPLAY):
+            fn()
+
+    graph = capture_graph(calls, stream=s)[0]
     for _ in range(BENCH_WARMUP):
         graph.replay()
     torch.cuda.synchronize()

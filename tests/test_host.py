@@ -282,6 +282,44 @@ def test_concat_halves_refuse_outside_the_fused_contract():
         SvdqConcat(proj, mlp, n, 128)          # 128 + 512 != 768
 
 
+def test_capture_graph_keeps_the_cyclic_collector_off_only_while_capturing(monkeypatch):
+    """graphs.capture_graph collects garbage first, runs the capture with Python's cyclic collector off, and
+    restores it afterwards, also when the captured function raises (CUDA calls stubbed)."""
+    import contextlib
+    import gc
+
+    from gen_worker_amd import graphs
+
+    class _Stream:
+        def wait_stream(self, other):
+            pass
+
+    seen = []
+    monkeypatch.setattr(torch.cuda, "Stream", lambda *a, **k: _Stream())
+    monkeypatch.setattr(torch.cuda, "current_stream", lambda *a, **k: _Stream())
+    monkeypatch.setattr(torch.cuda, "CUDAGraph", lambda *a, **k: object())
+    monkeypatch.setattr(torch.cuda, "stream", lambda s: contextlib.nullcontext())
+    monkeypatch.setattr(torch.cuda, "graph", lambda g, stream=None: contextlib.nullcontext())
+    monkeypatch.setattr(torch.cuda, "synchronize", lambda *a, **k: None)
+    assert gc.isenabled()
+    g, out = graphs.capture_graph(lambda: seen.append(gc.isenabled()) or 7)
+    assert out == 7 and seen == [False] and gc.isenabled()
+
+    def boom():
+        seen.append(gc.isenabled())
+        raise RuntimeError("capture failed")
+
+    with pytest.raises(RuntimeError, match="capture failed"):
+        graphs.capture_graph(boom)
+    assert seen == [False, False] and gc.isenabled()
+    gc.disable()
+    try:  # a caller that runs with the collector off keeps it off
+        graphs.capture_graph(lambda: None)
+        assert not gc.isenabled()
+    finally:
+        gc.enable()
+
+
 def test_module_tracks_in_place_updates_of_its_primary_buffers():
     """The derived buffers are rebuilt on the next forward after ``weight`` / ``weight_scale`` / ``proj_down``
     change in place (version counter) or are reassigned (identity); nothing else triggers a rebuild, and tensors
