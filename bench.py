@@ -241,12 +241,15 @@ def run_dit_child(args) -> dict:
     lines = [ln for ln in res.stdout.splitlines() if ln.startswith("{")]
     if res.returncode != 0 or not lines:
         return {"dit_error": f"the DiT child process exited with code {res.returncode}"}
-    d = json.loads(lines[-1])
-    return {"dit_step_ms": d["value"], "dit_bf16_step_ms": d["bf16_gemm_ms"],
-            "dit_speedup_vs_bf16": d["speedup_vs_bf16"], "dit_lane": d["config"]["lane"],
-            "dit_gate_lane": d["config"]["gate_lane"], "dit_modulation": args.modulation,
-            "dit_attention": ATTENTION_DESC["sdpa"], "dit_streams": STREAMS_DESC,
-            "dit_outputs_finite": bool(d["outputs_finite"]["w4a4"] and d["outputs_finite"]["bf16"])}
+    try:
+        d = json.loads(lines[-1])
+        return {"dit_step_ms": d["value"], "dit_bf16_step_ms": d["bf16_gemm_ms"],
+                "dit_speedup_vs_bf16": d["speedup_vs_bf16"], "dit_lane": d["config"]["lane"],
+                "dit_gate_lane": d["config"]["gate_lane"], "dit_modulation": args.modulation,
+                "dit_attention": ATTENTION_DESC["sdpa"], "dit_streams": STREAMS_DESC,
+                "dit_outputs_finite": bool(d["outputs_finite"]["w4a4"] and d["outputs_finite"]["bf16"])}
+    except (ValueError, KeyError, TypeError) as e:
+        return {"dit_error": f"the DiT child process printed an unreadable line ({type(e).__name__}: {e})"}
 
 
 def _w4a4_module(torch, L, dev, activation=None, out_dtype=None):

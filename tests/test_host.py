@@ -547,3 +547,41 @@ def test_dit_glue_refuses_bad_shapes_before_any_launch():
     # empty problems are no-ops
     assert lib.gwa_dit_adaln_modulate(None, 512, None, None, None, 512, 0, 512, 1e-6, None) == 0
     assert lib.gwa_dit_gate_residual(None, 8, None, 8, None, None, 8, 0, 8, None) == 0
+
+
+def test_bench_dit_child_results_and_failures_map_to_the_line(monkeypatch):
+    """bench.run_dit_child: the child's --workload dit line becomes the default line's dit_* keys; a child
+    that fails, prints an unreadable line or runs too long leaves only dit_error (the config-1 figures stand)."""
+    import argparse
+    import importlib.util
+    import json
+    import subprocess
+    import types
+
+    spec = importlib.util.spec_from_file_location("bench_under_test", Path(__file__).resolve().parents[1] / "bench.py")
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    args = argparse.Namespace(dit_steps=3, modulation="w4a4")
+    good = {"value": 72.5, "bf16_gemm_ms": 96.0, "speedup_vs_bf16": 1.3241,
+            "config": {"lane": "int4", "gate_lane": "int4"}, "outputs_finite": {"w4a4": True, "bf16": True}}
+    calls = []
+
+    def fake(stdout, rc=0, exc=None):
+        def run(cmd, **kw):
+            calls.append(cmd)
+            if exc is not None:
+                raise exc
+            return types.SimpleNamespace(returncode=rc, stdout=stdout)
+        return run
+
+    monkeypatch.setattr(subprocess, "run", fake("progress\n" + json.dumps(good) + "\n"))
+    out = bench.run_dit_child(args)
+    assert out["dit_step_ms"] == 72.5 and out["dit_bf16_step_ms"] == 96.0 and out["dit_lane"] == "int4"
+    assert out["dit_outputs_finite"] is True and "dit_error" not in out
+    assert calls[-1][2:] == [str(Path(bench.__file__).resolve()), "--workload", "dit", "--steps", "3", "--warmup",
+                             "1", "--modulation", "w4a4", "--attention", "sdpa"]
+    for run in (fake(json.dumps(good), rc=134), fake("no line"), fake('{"value": 1.0}'), fake("{not json"),
+                fake("", exc=subprocess.TimeoutExpired(cmd="x", timeout=900))):
+        monkeypatch.setattr(subprocess, "run", run)
+        out = bench.run_dit_child(args)
+        assert set(out) == {"dit_error"}, out
