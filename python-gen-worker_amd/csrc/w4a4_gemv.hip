@@ -66,24 +66,10 @@ __global__ __launch_bounds__(GV_THREADS) void svdq_gemv_w4a4_kernel(
   const int tid = threadIdx.x, G = K >> 6, n0 = blockIdx.x * GV_ROWS;
   const int items = GV_ROWS * G;
 
-  // 0. this workgroup's weight bytes and scales, first (they are the stream; everything else is L2-resident)
-  v4i wv[GV_MAX_ITEMS][2];
-  uint16_t swv[GV_MAX_ITEMS];
-#pragma unroll
-  for (int it = 0; it < GV_MAX_ITEMS; ++it) {
-    const int item = it * GV_THREADS + tid;
-    if (item < items) {
-      const int r = item / G, g = item - r * G;
-      const uint8_t* wp = qw + (int64_t)(n0 + r) * (K / 2) + g * 32;
-      wv[it][0] = *(const v4i*)wp;
-      wv[it][1] = *(const v4i*)(wp + 16);
-      swv[it] = sw[(int64_t)(n0 + r) * G + g];
-    }
-  }
-
-  // 1. the rest of what this workgroup reads, issued before any of it is used (one memory round trip): the
-  //    rows to quantize and their smoothing factors (the first QPRE rounds of quantizer lanes) and the first
-  //    LPRE la partial slots of this thread's la value
+  // 0. the small, cache-resident reads first (vector loads complete in issue order, so step 2 waits only for
+  //    these, and the quantization runs while the weight stream below is in flight): the rows to quantize
+  //    and their smoothing factors (the first QPRE rounds of quantizer lanes) and the first LPRE la partial
+  //    slots of this thread's la value
   constexpr int QPRE = 2, LPRE = 32;
   const int lanes_per_row = K / 8, qlanes = M * lanes_per_row;
   v4i xpre[QPRE], spre[QPRE];
@@ -103,9 +89,26 @@ __global__ __launch_bounds__(GV_THREADS) void svdq_gemv_w4a4_kernel(
 #pragma unroll
     for (int p = 0; p < LPRE; ++p) lpre[p] = (tid < MR && p < P) ? la_part[p * MR + tid] : 0.0f;
   }
+  const float s2 = s2p ? *s2p : 1.0f;
+
+  // 1. this workgroup's weight bytes and scales (the stream; first needed in step 3)
+  v4i wv[GV_MAX_ITEMS][2];
+  // the scales as 32-bit values: each load gets a register of its own (held as 16-bit values, they went
+  // through one temporary register, and every item's loads waited for the previous item's scale)
+  uint32_t swv[GV_MAX_ITEMS];
+  // Branch-free: an item index past the workgroup's items re-reads its last item (one broadcast line, never
+  // used), so every load goes out in one batch with nothing to merge.
+#pragma unroll
+  for (int it = 0; it < GV_MAX_ITEMS; ++it) {
+    const int item = min(it * GV_THREADS + tid, items - 1);
+    const int r = item / G, g = item - r * G;
+    const uint8_t* wp = qw + (int64_t)(n0 + r) * (K / 2) + g * 32;
+    wv[it][0] = *(const v4i*)wp;
+    wv[it][1] = *(const v4i*)(wp + 16);
+    swv[it] = sw[(int64_t)(n0 + r) * G + g];
+  }
 
   // 2. activation codes and scales (kernel 1's quantizer; a group = 8 consecutive lanes, 8 elements each)
-  const float s2 = s2p ? *s2p : 1.0f;
   const bool s2_one = s2 == 1.0f;
   for (int base = 0, q = 0; base < qlanes; base += GV_THREADS, ++q) {  // uniform trip count: quant8 is wave-collective
     const int li = base + tid;
@@ -173,7 +176,7 @@ __global__ __launch_bounds__(GV_THREADS) void svdq_gemv_w4a4_kernel(
     const int item = it * GV_THREADS + tid;
     if (item < items) {
       const int r = item / G, g = item - r * G;
-      swl[r * G + g] = f16_bits_to_f32(swv[it]);
+      swl[r * G + g] = f16_bits_to_f32((uint16_t)swv[it]);
       for (int m = 0; m < M; ++m) {
         const uint32_t* a = codes + m * lanes_per_row + g * 8;
         int d = 0;
