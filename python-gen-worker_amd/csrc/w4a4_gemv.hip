@@ -29,19 +29,38 @@ namespace {
 // a workgroup owns ROWS = 16 or 32 weight rows; items (row, group) per thread <= GV_MAX_ITEMS
 constexpr int GV_THREADS = 256, GV_MAX_M = 8, GV_MAX_ITEMS = 8;
 
-// dynamic LDS layout (bytes), all float / u32 arrays
+// Dynamic LDS layout (bytes), all float / u32 arrays. Strides are odd numbers of dwords where lanes read
+// across them: a group's 8 code dwords sit cs = 9 apart (step 3: lanes on consecutive groups), a row's
+// per-group values gp = G + 1 apart (step 4: lanes on consecutive rows), so those reads hit distinct banks
+// (at the plain strides of 8 and G = 48 dwords they were 8-way conflicts). A shape whose padded layout would
+// pass 64 KB keeps the plain strides (cs = 8, gp = G); host and kernel derive the same layout.
 struct GvLds {
-  int codes, sx, la, sw, p, total;
+  int codes, sx, la, sw, p, total, cs, gp;
+  __host__ __device__ void place(int M, int G, int R, int ROWS) {
+    codes = 0;                     // u32 [M][G][cs]
+    sx = codes + M * G * cs * 4;   // f32 [M][G]
+    la = sx + M * G * 4;           // f32 [M][R]
+    sw = la + M * R * 4;           // f32 [ROWS][gp]
+    p = sw + ROWS * gp * 4;        // f32 [M][ROWS][gp]
+    total = p + M * ROWS * gp * 4;
+  }
   __host__ __device__ GvLds(int M, int K, int R, int ROWS) {
     const int G = K / 64;
-    codes = 0;                              // u32 [M][K/8]
-    sx = codes + M * (K / 8) * 4;           // f32 [M][G]
-    la = sx + M * G * 4;                    // f32 [M][R]
-    sw = la + M * R * 4;                    // f32 [ROWS][G]
-    p = sw + ROWS * G * 4;                  // f32 [M][ROWS][G]
-    total = p + M * ROWS * G * 4;
+    cs = 9;
+    gp = G + 1;
+    place(M, G, R, ROWS);
+    if (total > 64 * 1024) {
+      cs = 8;
+      gp = G;
+      place(M, G, R, ROWS);
+    }
   }
 };
+// The footprint the token limit and the row count are chosen by: the plain layout's.
+__host__ __device__ inline int gv_budget_bytes(int M, int K, int R, int ROWS) {
+  const int G = K / 64;
+  return M * (K / 8) * 4 + M * G * 4 + M * R * 4 + ROWS * G * 4 + M * ROWS * G * 4;
+}
 
 // nb[0] = codes of elements 0..3 (one nibble per byte), nb[1] = elements 4..7 -> 8 nibbles, element i at 4i
 __device__ __forceinline__ uint32_t pack_nibbles8(const uint32_t nb[2]) {
@@ -147,7 +166,7 @@ __global__ __launch_bounds__(GV_THREADS) void svdq_gemv_w4a4_kernel(
     uint16_t sh;
     g64::quant8(w, valid, s2_one, s2, nb, sh);
     if (valid) {
-      codes[m * lanes_per_row + e8] = pack_nibbles8(nb);
+      codes[(m * G + (e8 >> 3)) * L.cs + (e8 & 7)] = pack_nibbles8(nb);
       if ((e8 & 7) == 0) sxl[m * G + (e8 >> 3)] = f16_bits_to_f32(sh);
     }
   }
@@ -176,16 +195,16 @@ __global__ __launch_bounds__(GV_THREADS) void svdq_gemv_w4a4_kernel(
     const int item = it * GV_THREADS + tid;
     if (item < items) {
       const int r = item / G, g = item - r * G;
-      swl[r * G + g] = f16_bits_to_f32((uint16_t)swv[it]);
+      swl[r * L.gp + g] = f16_bits_to_f32((uint16_t)swv[it]);
       for (int m = 0; m < M; ++m) {
-        const uint32_t* a = codes + m * lanes_per_row + g * 8;
+        const uint32_t* a = codes + (m * G + g) * L.cs;
         int d = 0;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           d = __builtin_amdgcn_sdot8((int)a[j], wv[it][0][j], d, false);
           d = __builtin_amdgcn_sdot8((int)a[4 + j], wv[it][1][j], d, false);
         }
-        pl[(m * GV_ROWS + r) * G + g] = (float)d;
+        pl[(m * GV_ROWS + r) * L.gp + g] = (float)d;
       }
     }
   }
@@ -194,9 +213,9 @@ __global__ __launch_bounds__(GV_THREADS) void svdq_gemv_w4a4_kernel(
   // 4. per (token, row): the group chain in the GEMM's order, then the epilogue
   if (tid < M * GV_ROWS) {
     const int m = tid / GV_ROWS, r = tid - m * GV_ROWS, n = n0 + r;
-    const float* pp = pl + (m * GV_ROWS + r) * G;
+    const float* pp = pl + (m * GV_ROWS + r) * L.gp;
     const float* sxm = sxl + m * G;
-    const float* swr = swl + r * G;
+    const float* swr = swl + r * L.gp;
     float acc = 0.0f;
 #pragma unroll 8
     for (int g = 0; g < G; ++g) acc = __builtin_fmaf(pp[g], sxm[g] * swr[g], acc);  // LDS reads batched by 8
@@ -234,7 +253,7 @@ extern "C" int gwa_svdq_w4a4_gemv_max_m(int64_t K, int64_t rank) {
   if (K <= 0 || K % 128 || K > 64 * GV_MAX_ITEMS * GV_THREADS / 16) return 0;
   if (!(rank == 0 || rank == 16 || rank == 32 || rank == 64 || rank == 128)) return 0;
   int m = GV_MAX_M;
-  while (m > 0 && GvLds((int)m, (int)K, (int)rank, 16).total > 64 * 1024) --m;
+  while (m > 0 && gv_budget_bytes((int)m, (int)K, (int)rank, 16) > 64 * 1024) --m;
   return m;
 }
 
@@ -293,7 +312,7 @@ extern "C" int gwa_svdq_w4a4_linear_gemv(const void* x, int64_t ldx, const void*
   // items and LDS allow, else 16
   const int G = (int)(K / 64);
   const bool rows32 = G * 32 <= GV_MAX_ITEMS * GV_THREADS && N % 32 == 0 &&
-                      GvLds((int)M, (int)K, (int)R, 32).total <= 64 * 1024;
+                      gv_budget_bytes((int)M, (int)K, (int)R, 32) <= 64 * 1024;
   const int rows = rows32 ? 32 : 16;
   const GvLds L((int)M, (int)K, (int)R, rows);
   const dim3 grid((unsigned)(N / rows)), block(GV_THREADS);

@@ -116,6 +116,19 @@ def test_rank0_bit_identical_to_gemm_lane(m):
         assert bool(((y16.float() - g16.float()).abs()[d] <= 2.0 ** -10 * g16.float().abs()[d]).all())
 
 
+def test_plain_lds_layout_bit_identical_to_gemm_lane():
+    """K = 6144 with 6 tokens and rank 0: the padded LDS layout would pass 64 KB, so the kernel keeps the plain
+    strides (8 and G dwords); the result is the fp6 GEMM lane's bit for bit, as with the padded layout."""
+    from gen_worker_amd import ops
+
+    assert ops.gemv_max_m(6144, 0) >= 6
+    L, mod = _layer(64, 6144, 0, per_channel=True, gelu=False, smooth=True, seed=61)
+    x = _x(6, 6144, seed=61)
+    y = _gemv(mod, x)
+    assert torch.equal(y, _gemm(mod, x))
+    check_output(y, _oracle(L, mod, x), what="gemv plain layout 6x64x6144 r0")
+
+
 @pytest.mark.parametrize("m,k,n,rank", [(4, 8192, 160, 32), (1, 128, 16, 16), (7, 1024, 48, 64),
                                         (2, 3072, 272, 128)])
 def test_shapes_match_oracle(m, k, n, rank):
